@@ -1,0 +1,204 @@
+"""Benchmark of the LTV combined-QKV filter path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+
+Workload (the d12 training shape): x bf16
+[32, 1024, 768] ~ N(0, 1); c.weight [2322, 768] fp32 ~ N(0, 1/768) (value rows
+and the 18 gate rows, r = 128); logit_bias = 0; init_param ~ N(0, 1/768);
+upstream dq, dk, dv ~ N(0, 1).  Synthetic data, random-init weights.
+
+One step = one pass of the hot path through the drop-in filter module:
+forward (bf16 MFMA projection into the head-major layout, gated EWMA scan) and
+backward (reverse scan, projection dX and dW) via autograd.  Inputs are resident
+in HBM before the timed region.  ``value`` = tokens / s = B*T*K / elapsed.
+
+Printed as one JSON line, with
+  roofline     -- the dominant kernel's algorithmic bytes (or FLOPs) per launch
+                  over its average duration (HIP events on the launch stream
+                  across the timed steps), against MI355X's published peak;
+  kernels      -- the same figure for every kernel of the path;
+  cpu_baseline -- the CPU oracle (oracle/ltv_oracle.py, a restatement of the
+                  reference's sequential PyTorch path) timed on a bounded
+                  sample of the same workload on the host cores.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "nanochat-filter_amd"))
+
+# published MI355X peaks
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+
+B, T, C = 32, 1024, 768
+NH = NKVH = 6
+D, R = 128, 128
+DA = D // R
+H = NH + 2 * NKVH
+F = H * (D + DA)
+S_IO = 2  # bf16
+
+
+def algorithmic_work():
+    """Per-launch algorithmic bytes / FLOPs (formulas of BASELINE.md section 2)."""
+    scan_fwd = B * T * (F + H * D) * S_IO + B * H * D * S_IO + 4 * H * DA
+    scan_bwd = B * T * (2 * F + H * D) * S_IO + 2 * B * H * D * S_IO + 4 * H * DA
+    gemm = 2 * B * T * C * F
+    return {
+        "scan_fwd": ("hbm", scan_fwd),
+        "scan_bwd": ("hbm", scan_bwd),
+        "qkv_project_fwd": ("mfma", gemm),
+        "qkv_project_bwd": ("mfma", 2 * gemm),
+        "pack_weight": ("hbm", F * C * 4 + 2368 * C * 2),
+    }
+
+
+def cpu_baseline(seconds_target: float = 10.0):
+    """Time the oracle's forward+backward on a sample of the workload."""
+    import numpy as np
+    from threadpoolctl import threadpool_limits
+
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import ltv_oracle as O
+
+    cores = len(os.sched_getaffinity(0))
+    Bs = 1  # one sequence of the 32 at full T and C
+    rng = np.random.default_rng(0)
+    x = rng.standard_normal((Bs, T, C), dtype=np.float32)
+    w = (rng.standard_normal((F, C)) / np.sqrt(C)).astype(np.float32)
+    ini = (rng.standard_normal((Bs, H, D)) / np.sqrt(C)).astype(np.float32)
+    bias = np.zeros((H, DA), np.float32)
+    dq = rng.standard_normal((Bs, T, NH, D), dtype=np.float32)
+    dk = rng.standard_normal((Bs, T, NKVH, D), dtype=np.float32)
+    dv = rng.standard_normal((Bs, T, NKVH, D), dtype=np.float32)
+    reps = 0
+    t0 = time.perf_counter()
+    with threadpool_limits(limits=cores):
+        while True:
+            q, k, v, comb, saved = O.filter_forward(x, w, ini, bias, NH, NKVH, DA, R, "f32")
+            O.filter_backward(x, w, ini, bias, comb, saved, dq, dk, dv, NH, NKVH, DA, R, "f32")
+            reps += 1
+            el = time.perf_counter() - t0
+            if el >= seconds_target:
+                break
+    return {
+        "value": round(Bs * T * reps / el, 1),
+        "unit": "tokens/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": f"{reps} x fwd+bwd of {Bs} sequence(s) of the workload "
+                  f"(T={T}, C={C}, F={F}), fp32 numpy, {el:.1f} s",
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported in this build "
+              "(the path shards over B with no exchange but the weight-gradient reduction; "
+              "only the single-GPU figure is reported)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from nanochat_amd import _native as N
+    from nanochat_amd.ltv.ltv_filter import LtvInitValues
+    from nanochat_amd.ltv_cuda_fused_concat_head_major_register_cast_blelloch_scan_qkv_filter import (
+        LtvCudaFusedConcatHeadMajorRegisterCastBlellochScanQkvFilter as Filter,
+    )
+
+    dev = torch.device("cuda:0")
+    torch.manual_seed(0)
+    f = Filter(NH, NKVH, D, R)
+    with torch.no_grad():
+        f.c.weight.normal_(0.0, C ** -0.5)
+        f.logit_bias.zero_()
+        f.init_param.normal_(0.0, C ** -0.5)
+    f = f.to(dev)
+    g = torch.Generator(device=dev).manual_seed(0)
+    x = torch.randn(B, T, C, generator=g, device=dev).to(torch.bfloat16).requires_grad_(True)
+    dq = torch.randn(B, T, NH, D, generator=g, device=dev).to(torch.bfloat16)
+    dk = torch.randn(B, T, NKVH, D, generator=g, device=dev).to(torch.bfloat16)
+    dv = torch.randn(B, T, NKVH, D, generator=g, device=dev).to(torch.bfloat16)
+    none = LtvInitValues()
+
+    def step():
+        f.zero_grad(set_to_none=True)
+        x.grad = None
+        q, k, v = f(x, none)
+        torch.autograd.backward([q, k, v], [dq, dk, dv])
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    with N.KernelRecorder() as rec:
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            step()
+        torch.cuda.synchronize()
+        elapsed = time.perf_counter() - t0
+
+    durs = rec.durations_ms()
+    work = algorithmic_work()
+    kernels = {}
+    for name, ms in durs.items():
+        bound, amount = work[name]
+        avg = sum(ms) / len(ms)
+        if bound == "hbm":
+            ach, peak, unit = amount / (avg * 1e-3) / 1e9, HBM_PEAK_GBS, "GB/s"
+        else:
+            ach, peak, unit = amount / (avg * 1e-3) / 1e12, BF16_PEAK_TFLOPS, "TFLOP/s"
+        kernels[name] = {"bound": bound, "avg_us": round(avg * 1e3, 2), "launches": len(ms),
+                         "achieved": round(ach, 1), "peak": peak, "unit": unit,
+                         "frac": round(ach / peak, 4), "work_per_launch": amount}
+    dominant = max(kernels, key=lambda k: kernels[k]["avg_us"] * kernels[k]["launches"])
+    dk_ = kernels[dominant]
+    roofline = {"kernel": dominant, "bound": dk_["bound"], "achieved": dk_["achieved"],
+                "peak": dk_["peak"], "unit": dk_["unit"], "frac": dk_["frac"], "traffic": None}
+    scan_time = kernels.get("scan_fwd", {}).get("avg_us", 0) + kernels.get("scan_bwd", {}).get("avg_us", 0)
+    scan_bytes = work["scan_fwd"][1] + work["scan_bwd"][1]
+    scan_gbs = scan_bytes / (scan_time * 1e-6) / 1e9 if scan_time else None
+
+    ms_per_step = elapsed * 1e3 / args.steps
+    out = {
+        "metric": "QKV+EWMA scan fwd+bwd tokens/s and scan HBM GB/s (%peak) at B32 T1024 C768",
+        "value": round(B * T * args.steps / elapsed, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "configs[2]: d12 fused QKV projection + EWMA scan, fwd+bwd",
+                   "B": B, "T": T, "C": C, "n_head": NH, "n_kv_head": NKVH, "head_dim": D,
+                   "r": R, "F": F, "parallelism": "single GPU"},
+        "scan_gbs": round(scan_gbs, 1) if scan_gbs else None,
+        "scan_frac_hbm": round(scan_gbs / HBM_PEAK_GBS, 4) if scan_gbs else None,
+        "roofline": roofline,
+        "kernels": kernels,
+    }
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

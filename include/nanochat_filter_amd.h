@@ -1,0 +1,196 @@
+/*
+ * nanochat_filter_amd.h -- C ABI of the MI355X (gfx950) LTV combined-QKV
+ * filter path: the fused QKV projection and the gated EWMA scan, forward and
+ * backward.
+ *
+ * Conventions for every entry point:
+ *   - All tensor arguments are raw device pointers plus element strides
+ *     (int64, in elements of the tensor's own dtype).  Shapes are plain ints.
+ *   - `dtype` selects the I/O element type: LTV_DTYPE_F32 or LTV_DTYPE_BF16
+ *     (bf16 as raw 16-bit patterns).  State and arithmetic are always fp32;
+ *     `logit_bias` / `grad_logit_bias` are always fp32.
+ *   - `stream` is a hipStream_t (NULL = default stream).  Every call only
+ *     enqueues work on that stream; none synchronises the host.
+ *   - Outputs are caller-allocated; the library never allocates device memory.
+ *     Temporary device memory is passed in as `workspace` (size from the
+ *     matching *_workspace_size query).
+ *   - Return value: LTV_OK, or an LTV_ERR_* code with a message available from
+ *     ltv_last_error() (per host thread).
+ *
+ * Reference interfaces replaced (paths relative to aioaneid/nanochat-filter):
+ *   pybind11 module `cpp_ewma_cuda` (cpp_ewma/src/bindings.cpp) functions
+ *   ltv_fused_concat_head_major_register_cast_blelloch_scan_cuda_{forward,backward}
+ *   and fused_linear_transpose{,_backward}, which the torch.library ops in
+ *   nanochat/ops/ltv_cuda_fused_concat_head_major_register_cast_blelloch_scan.py
+ *   and nanochat/ops/fused_linear_transpose.py call.
+ */
+#ifndef NANOCHAT_FILTER_AMD_H
+#define NANOCHAT_FILTER_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LTV_DTYPE_F32 0
+#define LTV_DTYPE_BF16 1
+
+#define LTV_OK 0
+#define LTV_ERR_INVALID_ARG 1
+#define LTV_ERR_UNSUPPORTED 2
+#define LTV_ERR_HIP 3
+#define LTV_ERR_WORKSPACE 4
+
+/* Version of this ABI (bumped on any signature change). */
+int ltv_abi_version(void);
+
+/* Message of the last failing call on this host thread ("" if none). */
+const char* ltv_last_error(void);
+
+/* ------------------------------------------------------------------------
+ * Gated EWMA scan, reference layout.
+ *
+ * combined : (B, T, F) with F = H*(D+Da), H = NH + 2*NKVH, D = Da*r, any
+ *            strides; per-head features [values D | logits Da]
+ * inits    : (B, H, D), any strides
+ * logit_bias: (H, Da) fp32, contiguous
+ * out_q    : (B, NH, T, D), out_k / out_v : (B, NKVH, T, D), any strides
+ *
+ * Replaces ltv_fused_concat_head_major_register_cast_blelloch_scan_cuda_forward
+ * (cpp_ewma/src/ltv_fused_concat_head_major_register_cast_blelloch_scan_cuda_forward.cu:532-552,
+ *  called from nanochat/ops/ltv_cuda_fused_concat_head_major_register_cast_blelloch_scan.py:35-71).
+ * The reference's tuning arguments (scan/r threads, r items) are launch
+ * shapes of its CUDA kernel and have no counterpart here.
+ * ---------------------------------------------------------------------- */
+int ltv_hm_scan_forward(int dtype, const void* combined, const int64_t combined_strides[3],
+                        const void* inits, const int64_t inits_strides[3],
+                        const float* logit_bias, void* out_q, const int64_t out_q_strides[4],
+                        void* out_k, const int64_t out_k_strides[4], void* out_v,
+                        const int64_t out_v_strides[4], int B, int T, int NH, int NKVH, int Da,
+                        int r, int use_sigmoid, void* stream);
+
+/* Workspace bytes needed by ltv_hm_scan_backward / ltv_hm_scan_backward_split. */
+size_t ltv_hm_scan_backward_workspace_size(int dtype, int B, int T, int NH, int NKVH, int Da,
+                                           int r);
+
+/* ------------------------------------------------------------------------
+ * Backward of ltv_hm_scan_forward.
+ *
+ * hq/hk/hv       : the forward outputs (any strides)
+ * grad_hq/hk/hv  : upstream gradients, shaped like the outputs (any strides)
+ * grad_combined  : (B, T, F), any strides (fully overwritten)
+ * grad_inits     : (B, H, D), any strides (overwritten)
+ * grad_logit_bias: (H, Da) fp32 contiguous (overwritten, not accumulated)
+ *
+ * Replaces ltv_fused_concat_head_major_register_cast_blelloch_scan_cuda_backward
+ * (cpp_ewma/src/ltv_fused_concat_head_major_register_cast_blelloch_scan_cuda_backward.cu:882-976,
+ *  called from nanochat/ops/ltv_cuda_fused_concat_head_major_register_cast_blelloch_scan.py:145-193).
+ * The reference zero-fills grad_logit_bias and atomically accumulates; this
+ * entry point writes it once, deterministically.
+ * ---------------------------------------------------------------------- */
+int ltv_hm_scan_backward(int dtype, const void* combined, const int64_t combined_strides[3],
+                         const void* inits, const int64_t inits_strides[3],
+                         const float* logit_bias, const void* hq, const int64_t hq_strides[4],
+                         const void* hk, const int64_t hk_strides[4], const void* hv,
+                         const int64_t hv_strides[4], const void* grad_hq,
+                         const int64_t grad_hq_strides[4], const void* grad_hk,
+                         const int64_t grad_hk_strides[4], const void* grad_hv,
+                         const int64_t grad_hv_strides[4], void* grad_combined,
+                         const int64_t grad_combined_strides[3], void* grad_inits,
+                         const int64_t grad_inits_strides[3], float* grad_logit_bias,
+                         void* workspace, size_t workspace_bytes, int B, int T, int NH, int NKVH,
+                         int Da, int r, int use_sigmoid, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Same scan with the value and logit slots given as two separate 4-D views
+ * (b, h, t, channel) instead of one interleaved (B, T, F) tensor.  This is
+ * the form the projection below writes (values and logits in one row-major
+ * (B*T, Fp) buffer, see ltv_qkv_project_forward) and is what the filter
+ * module's fast path uses.  Same math and buffer contracts as above.
+ * Counterpart in the reference: the same scan entry points (the reference has
+ * only the interleaved layout).
+ * ---------------------------------------------------------------------- */
+int ltv_hm_scan_forward_split(int dtype, const void* values, const int64_t values_strides[4],
+                              const void* logits, const int64_t logits_strides[4],
+                              const void* inits, const int64_t inits_strides[3],
+                              const float* logit_bias, void* out_q,
+                              const int64_t out_q_strides[4], void* out_k,
+                              const int64_t out_k_strides[4], void* out_v,
+                              const int64_t out_v_strides[4], int B, int T, int NH, int NKVH,
+                              int Da, int r, int use_sigmoid, void* stream);
+
+int ltv_hm_scan_backward_split(
+    int dtype, const void* values, const int64_t values_strides[4], const void* logits,
+    const int64_t logits_strides[4], const void* inits, const int64_t inits_strides[3],
+    const float* logit_bias, const void* hq, const int64_t hq_strides[4], const void* hk,
+    const int64_t hk_strides[4], const void* hv, const int64_t hv_strides[4],
+    const void* grad_hq, const int64_t grad_hq_strides[4], const void* grad_hk,
+    const int64_t grad_hk_strides[4], const void* grad_hv, const int64_t grad_hv_strides[4],
+    void* grad_values, const int64_t grad_values_strides[4], void* grad_logits,
+    const int64_t grad_logits_strides[4], void* grad_inits, const int64_t grad_inits_strides[3],
+    float* grad_logit_bias, void* workspace, size_t workspace_bytes, int B, int T, int NH,
+    int NKVH, int Da, int r, int use_sigmoid, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Projection, reference layout: out[b] (F x T) = weight (F x K) . x[b]^T
+ *
+ * x (B, T, K), weight (F, K), out (B, F, T): all contiguous, all `dtype`.
+ * Replaces fused_linear_transpose (cpp_ewma/src/fused_linear_transpose_forward.cu:23-58,
+ * called from nanochat/ops/fused_linear_transpose.py:20-40).
+ * ---------------------------------------------------------------------- */
+int ltv_linear_transpose_forward(int dtype, const void* x, const void* weight, void* out, int B,
+                                 int T, int K, int F, void* stream);
+
+/* Backward: grad_x (B, T, K) = grad_out^T-mapped . weight,
+ * grad_weight (F, K) = sum_b grad_out[b] . x[b]  (both overwritten, in
+ * `dtype`, fp32 accumulation).
+ * grad_out is (B, F, T) contiguous, or its (B, T, F)-contiguous transpose
+ * when grad_out_is_btf != 0 (the two layouts the reference accepts,
+ * nanochat/ops/fused_linear_transpose.py:76-84).
+ * Replaces fused_linear_transpose_backward
+ * (cpp_ewma/src/fused_linear_transpose_backward.cu:22-132). */
+int ltv_linear_transpose_backward(int dtype, const void* x, const void* weight,
+                                  const void* grad_out, int grad_out_is_btf, void* grad_x,
+                                  void* grad_weight, int B, int T, int K, int F, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Fused QKV projection for the filter module (bf16 MFMA, fp32 accumulate).
+ *
+ * The parameter c.weight is (F, C) with per-head interleaved rows
+ * [h0 values (D) | h0 logits (Da) | h1 values | ...]
+ * (nanochat/ltv_combined_head_major_qkv_filter.py:11-66).
+ *
+ * ltv_qkv_pack_weight: weight (F, C) fp32 or bf16 contiguous ->
+ *   wpack (Fp, C) bf16: rows [all values, head-major | all logits | zeros]
+ * with Fp = ltv_qkv_packed_width(H, D, Da) (a multiple of 64).
+ *
+ * ltv_qkv_project_forward: x (M = B*T, C) bf16 contiguous ->
+ *   combined (M, Fp) bf16 row-major: column h*D + d holds head h's value
+ *   channel d, column H*D + h*Da + j its logit j, remaining columns zero.
+ *
+ * ltv_qkv_project_backward: grad_combined (M, Fp) bf16 (same layout; padding
+ *   columns are ignored) ->
+ *   grad_x (M, C) bf16 and grad_weight (F, C) fp32 in the parameter's
+ *   interleaved row order (both overwritten).
+ * Counterpart in the reference: fused_linear_transpose forward/backward as used
+ * by nanochat/ltv_cuda_fused_concat_head_major_register_cast_blelloch_scan_qkv_filter.py:35-41
+ * (there the output is (B, F, T) and the scan reads it through a transposed view).
+ * ---------------------------------------------------------------------- */
+int ltv_qkv_packed_width(int H, int D, int Da);
+int ltv_qkv_pack_weight(int weight_dtype, const void* weight, void* wpack, int H, int D,
+                        int Da, int C, void* stream);
+int ltv_qkv_project_forward(const void* x, const void* wpack, void* combined, int M, int C,
+                            int Fp, void* stream);
+size_t ltv_qkv_project_backward_workspace_size(int M, int C, int H, int D, int Da);
+int ltv_qkv_project_backward(const void* x, const void* wpack, const void* grad_combined,
+                             void* grad_x, float* grad_weight, void* workspace,
+                             size_t workspace_bytes, int M, int C, int H, int D, int Da,
+                             void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NANOCHAT_FILTER_AMD_H */

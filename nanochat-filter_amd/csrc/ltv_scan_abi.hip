@@ -1,0 +1,301 @@
+// C-ABI entry points of the scan: argument checks, layout views and launch-shape
+// selection.  Kernels live in ltv_scan_fwd.hip / ltv_scan_bwd.hip.
+#include "ltv_scan_kernels.hpp"
+
+namespace ltv {
+namespace {
+
+struct HostView4 {
+  const void* p;
+  int64_t s[4];
+};
+
+inline View4 to_dev(const HostView4& v) {
+  View4 o;
+  o.p = v.p;
+  for (int i = 0; i < 4; ++i) o.s[i] = v.s[i];
+  return o;
+}
+
+// A view can be read/written as 16-byte vectors along the channel axis.
+inline bool vec_ok(const void* p, const int64_t* s, int nd_outer, int V) {
+  if (!aligned16(p)) return false;
+  if (s[nd_outer] != 1) return false;
+  for (int i = 0; i < nd_outer; ++i)
+    if (s[i] % V != 0) return false;
+  return true;
+}
+
+int check_shape(int dtype, int B, int T, int NH, int NKVH, int Da, int r) {
+  LTV_REQUIRE(dtype == LTV_DTYPE_F32 || dtype == LTV_DTYPE_BF16, LTV_ERR_INVALID_ARG,
+              "dtype must be LTV_DTYPE_F32 or LTV_DTYPE_BF16, got %d", dtype);
+  LTV_REQUIRE(B >= 0 && T >= 0 && NH >= 0 && NKVH >= 0, LTV_ERR_INVALID_ARG,
+              "negative size (B=%d T=%d NH=%d NKVH=%d)", B, T, NH, NKVH);
+  LTV_REQUIRE(Da >= 1 && r >= 1, LTV_ERR_INVALID_ARG, "Da and r must be >= 1 (Da=%d r=%d)", Da,
+              r);
+  const int V = dtype == LTV_DTYPE_BF16 ? 8 : 4;
+  const int D = Da * r;
+  LTV_REQUIRE(D <= 64 * V, LTV_ERR_UNSUPPORTED,
+              "head_dim D=%d exceeds the supported maximum %d for this dtype", D, 64 * V);
+  return LTV_OK;
+}
+
+// The backward's in-register group reduction handles r % V == 0 with r / V a
+// power of two, and r dividing V; anything else goes to the channel kernel.
+inline bool bwd_main_ok(int r, int V) {
+  if (r % V == 0) return is_pow2(r / V);
+  return V % r == 0;
+}
+
+int scan_forward_impl(int dtype, const HostView4& u, const HostView4& lg, const HostView4& init,
+                      const float* bias, void* const outp[3], const int64_t* const outs[3], int B,
+                      int T, int NH, int NKVH, int Da, int r, int use_sigmoid, hipStream_t st) {
+  int rc = check_shape(dtype, B, T, NH, NKVH, Da, r);
+  if (rc) return rc;
+  const int H = NH + 2 * NKVH;
+  const int D = Da * r;
+  if (B == 0 || T == 0 || H == 0) return LTV_OK;
+  LTV_REQUIRE(bias != nullptr && u.p && lg.p && init.p, LTV_ERR_INVALID_ARG,
+              "null tensor pointer");
+  const int V = dtype == LTV_DTYPE_BF16 ? 8 : 4;
+  const int cl_full = next_pow2((D + V - 1) / V);
+  // Forward: slabs of at most 8 channel lanes (64 bf16 / 32 fp32 channels)
+  // give more workgroups per head; channels are independent in the forward.
+  const int CL = cl_full < 8 ? cl_full : 8;
+  const int nslab = (D + CL * V - 1) / (CL * V);
+
+  FwdArgs a;
+  a.sh = ScanShape{B, T, NH, NKVH, Da, r, D, H, nslab, use_sigmoid};
+  a.u = to_dev(u);
+  a.lg = to_dev(lg);
+  a.init = to_dev(init);
+  a.bias = bias;
+  bool vec = (D % V == 0) && vec_ok(u.p, u.s, 3, V) && vec_ok(init.p, init.s, 3, V);
+  for (int i = 0; i < 3; ++i) {
+    a.out.p[i] = outp[i];
+    for (int k = 0; k < 4; ++k) a.out.s[i][k] = outs[i][k];
+    const int nh = i == 0 ? NH : NKVH;
+    if (nh > 0) {
+      LTV_REQUIRE(outp[i] != nullptr, LTV_ERR_INVALID_ARG, "null output pointer");
+      vec = vec && vec_ok(outp[i], outs[i], 3, V);
+    }
+  }
+  const bool lanegate = (r % V) == 0;
+  const int64_t grid = (int64_t)B * H * nslab;
+  LTV_REQUIRE(grid < (1ll << 31), LTV_ERR_UNSUPPORTED, "grid too large");
+  return scan_launch_fwd(dtype == LTV_DTYPE_BF16, a, CL, (int)grid, vec, lanegate, st);
+}
+
+size_t bwd_workspace_bytes(int dtype, int B, int T, int NH, int NKVH, int Da, int r) {
+  const int H = NH + 2 * NKVH;
+  const int V = dtype == LTV_DTYPE_BF16 ? 8 : 4;
+  size_t bytes = (size_t)B * H * Da * sizeof(float);
+  bytes = (bytes + 255) & ~(size_t)255;
+  if (!bwd_main_ok(r, V)) bytes += (size_t)B * H * T * Da * r * sizeof(float);
+  return bytes;
+}
+
+int scan_backward_impl(int dtype, const HostView4& u, const HostView4& lg, const HostView4& init,
+                       const float* bias, const void* const hp[3], const int64_t* const hs[3],
+                       const void* const gp[3], const int64_t* const gs[3], const HostView4& du,
+                       const HostView4& dlg, const HostView4& dinit, float* dbias, void* ws,
+                       size_t ws_bytes, int B, int T, int NH, int NKVH, int Da, int r,
+                       int use_sigmoid, hipStream_t st) {
+  int rc = check_shape(dtype, B, T, NH, NKVH, Da, r);
+  if (rc) return rc;
+  const int H = NH + 2 * NKVH;
+  const int D = Da * r;
+  if (H == 0) return LTV_OK;
+  LTV_REQUIRE(dbias != nullptr, LTV_ERR_INVALID_ARG, "null grad_logit_bias");
+  if (B == 0 || T == 0) {
+    // nothing flows back: zero grad_logit_bias (inits receive no gradient terms
+    // either; with T == 0 the caller's grad_inits are left as allocated zeros)
+    LTV_HIP_CHECK(hipMemsetAsync(dbias, 0, sizeof(float) * H * Da, st));
+    return LTV_OK;
+  }
+  const size_t need = bwd_workspace_bytes(dtype, B, T, NH, NKVH, Da, r);
+  LTV_REQUIRE(ws != nullptr && ws_bytes >= need, LTV_ERR_WORKSPACE,
+              "workspace too small: need %zu bytes, got %zu", need, ws_bytes);
+  const int V = dtype == LTV_DTYPE_BF16 ? 8 : 4;
+
+  BwdArgs a;
+  a.sh = ScanShape{B, T, NH, NKVH, Da, r, D, H, 1, use_sigmoid};
+  a.u = to_dev(u);
+  a.lg = to_dev(lg);
+  a.init = to_dev(init);
+  a.bias = bias;
+  bool vec = (D % V == 0) && vec_ok(u.p, u.s, 3, V) && vec_ok(init.p, init.s, 3, V) &&
+             vec_ok(du.p, du.s, 3, V) && vec_ok(dinit.p, dinit.s, 3, V);
+  for (int i = 0; i < 3; ++i) {
+    a.h.p[i] = const_cast<void*>(hp[i]);
+    a.gy.p[i] = const_cast<void*>(gp[i]);
+    for (int k = 0; k < 4; ++k) {
+      a.h.s[i][k] = hs[i][k];
+      a.gy.s[i][k] = gs[i][k];
+    }
+    const int nh = i == 0 ? NH : NKVH;
+    if (nh > 0) {
+      LTV_REQUIRE(hp[i] && gp[i], LTV_ERR_INVALID_ARG, "null saved output or gradient pointer");
+      vec = vec && vec_ok(hp[i], hs[i], 3, V) && vec_ok(gp[i], gs[i], 3, V);
+    }
+  }
+  a.du.p[0] = const_cast<void*>(du.p);
+  a.du.p[1] = a.du.p[2] = nullptr;
+  for (int k = 0; k < 4; ++k) a.du.s[0][k] = a.du.s[1][k] = a.du.s[2][k] = du.s[k];
+  a.dlg = to_dev(dlg);
+  a.dinit = to_dev(dinit);
+  a.dbias_partial = reinterpret_cast<float*>(ws);
+
+  const int64_t grid = (int64_t)B * H;
+  LTV_REQUIRE(grid < (1ll << 31), LTV_ERR_UNSUPPORTED, "grid too large");
+  if (bwd_main_ok(r, V)) {
+    const int CL = next_pow2((D + V - 1) / V);
+    const bool lanegate = (r % V) == 0;
+    rc = scan_launch_bwd(dtype == LTV_DTYPE_BF16, a, CL, (int)grid, vec, lanegate, st);
+    if (rc) return rc;
+  } else {
+    size_t off = ((size_t)B * H * Da * sizeof(float) + 255) & ~(size_t)255;
+    float* dalpha = reinterpret_cast<float*>(reinterpret_cast<char*>(ws) + off);
+    rc = scan_launch_bwd_channel(dtype == LTV_DTYPE_BF16, a, dalpha, st);
+    if (rc) return rc;
+  }
+  const int HDa = H * Da;
+  return scan_launch_dbias_reduce(reinterpret_cast<const float*>(ws), dbias, B, HDa, st);
+}
+
+// (B, T, F) interleaved tensor -> value / logit 4-D views
+inline HostView4 values_view(const void* p, const int64_t* cs, int D, int Da) {
+  HostView4 v;
+  v.p = p;
+  v.s[0] = cs[0];
+  v.s[1] = (int64_t)(D + Da) * cs[2];
+  v.s[2] = cs[1];
+  v.s[3] = cs[2];
+  return v;
+}
+
+inline HostView4 logits_view(const void* p, const int64_t* cs, int D, int Da, int esize) {
+  HostView4 v = values_view(p, cs, D, Da);
+  v.p = reinterpret_cast<const char*>(p) + (int64_t)D * cs[2] * esize;
+  return v;
+}
+
+inline HostView4 view3(const void* p, const int64_t* s) {
+  HostView4 v;
+  v.p = p;
+  v.s[0] = s[0];
+  v.s[1] = s[1];
+  v.s[2] = 0;
+  v.s[3] = s[2];
+  return v;
+}
+
+inline HostView4 view4(const void* p, const int64_t* s) {
+  HostView4 v;
+  v.p = p;
+  for (int i = 0; i < 4; ++i) v.s[i] = s[i];
+  return v;
+}
+
+}  // namespace
+}  // namespace ltv
+
+using namespace ltv;
+
+extern "C" int ltv_hm_scan_forward(int dtype, const void* combined,
+                                   const int64_t combined_strides[3], const void* inits,
+                                   const int64_t inits_strides[3], const float* logit_bias,
+                                   void* out_q, const int64_t out_q_strides[4], void* out_k,
+                                   const int64_t out_k_strides[4], void* out_v,
+                                   const int64_t out_v_strides[4], int B, int T, int NH, int NKVH,
+                                   int Da, int r, int use_sigmoid, void* stream) {
+  LTV_REQUIRE(combined_strides && inits_strides && out_q_strides && out_k_strides &&
+                  out_v_strides,
+              LTV_ERR_INVALID_ARG, "null stride array");
+  const int D = Da * r;
+  const int es = dtype == LTV_DTYPE_BF16 ? 2 : 4;
+  void* outp[3] = {out_q, out_k, out_v};
+  const int64_t* outs[3] = {out_q_strides, out_k_strides, out_v_strides};
+  return scan_forward_impl(dtype, values_view(combined, combined_strides, D, Da),
+                           logits_view(combined, combined_strides, D, Da, es),
+                           view3(inits, inits_strides), logit_bias, outp, outs, B, T, NH, NKVH,
+                           Da, r, use_sigmoid, (hipStream_t)stream);
+}
+
+extern "C" int ltv_hm_scan_forward_split(
+    int dtype, const void* values, const int64_t values_strides[4], const void* logits,
+    const int64_t logits_strides[4], const void* inits, const int64_t inits_strides[3],
+    const float* logit_bias, void* out_q, const int64_t out_q_strides[4], void* out_k,
+    const int64_t out_k_strides[4], void* out_v, const int64_t out_v_strides[4], int B, int T,
+    int NH, int NKVH, int Da, int r, int use_sigmoid, void* stream) {
+  LTV_REQUIRE(values_strides && logits_strides && inits_strides && out_q_strides &&
+                  out_k_strides && out_v_strides,
+              LTV_ERR_INVALID_ARG, "null stride array");
+  void* outp[3] = {out_q, out_k, out_v};
+  const int64_t* outs[3] = {out_q_strides, out_k_strides, out_v_strides};
+  return scan_forward_impl(dtype, view4(values, values_strides), view4(logits, logits_strides),
+                           view3(inits, inits_strides), logit_bias, outp, outs, B, T, NH, NKVH,
+                           Da, r, use_sigmoid, (hipStream_t)stream);
+}
+
+extern "C" size_t ltv_hm_scan_backward_workspace_size(int dtype, int B, int T, int NH, int NKVH,
+                                                      int Da, int r) {
+  return bwd_workspace_bytes(dtype, B, T, NH, NKVH, Da, r);
+}
+
+extern "C" int ltv_hm_scan_backward(
+    int dtype, const void* combined, const int64_t combined_strides[3], const void* inits,
+    const int64_t inits_strides[3], const float* logit_bias, const void* hq,
+    const int64_t hq_strides[4], const void* hk, const int64_t hk_strides[4], const void* hv,
+    const int64_t hv_strides[4], const void* grad_hq, const int64_t grad_hq_strides[4],
+    const void* grad_hk, const int64_t grad_hk_strides[4], const void* grad_hv,
+    const int64_t grad_hv_strides[4], void* grad_combined, const int64_t grad_combined_strides[3],
+    void* grad_inits, const int64_t grad_inits_strides[3], float* grad_logit_bias,
+    void* workspace, size_t workspace_bytes, int B, int T, int NH, int NKVH, int Da, int r,
+    int use_sigmoid, void* stream) {
+  LTV_REQUIRE(combined_strides && inits_strides && hq_strides && hk_strides && hv_strides &&
+                  grad_hq_strides && grad_hk_strides && grad_hv_strides &&
+                  grad_combined_strides && grad_inits_strides,
+              LTV_ERR_INVALID_ARG, "null stride array");
+  const int D = Da * r;
+  const int es = dtype == LTV_DTYPE_BF16 ? 2 : 4;
+  const void* hp[3] = {hq, hk, hv};
+  const int64_t* hs[3] = {hq_strides, hk_strides, hv_strides};
+  const void* gp[3] = {grad_hq, grad_hk, grad_hv};
+  const int64_t* gs[3] = {grad_hq_strides, grad_hk_strides, grad_hv_strides};
+  return scan_backward_impl(
+      dtype, values_view(combined, combined_strides, D, Da),
+      logits_view(combined, combined_strides, D, Da, es), view3(inits, inits_strides),
+      logit_bias, hp, hs, gp, gs, values_view(grad_combined, grad_combined_strides, D, Da),
+      logits_view(grad_combined, grad_combined_strides, D, Da, es),
+      view3(grad_inits, grad_inits_strides), grad_logit_bias, workspace, workspace_bytes, B, T,
+      NH, NKVH, Da, r, use_sigmoid, (hipStream_t)stream);
+}
+
+extern "C" int ltv_hm_scan_backward_split(
+    int dtype, const void* values, const int64_t values_strides[4], const void* logits,
+    const int64_t logits_strides[4], const void* inits, const int64_t inits_strides[3],
+    const float* logit_bias, const void* hq, const int64_t hq_strides[4], const void* hk,
+    const int64_t hk_strides[4], const void* hv, const int64_t hv_strides[4],
+    const void* grad_hq, const int64_t grad_hq_strides[4], const void* grad_hk,
+    const int64_t grad_hk_strides[4], const void* grad_hv, const int64_t grad_hv_strides[4],
+    void* grad_values, const int64_t grad_values_strides[4], void* grad_logits,
+    const int64_t grad_logits_strides[4], void* grad_inits, const int64_t grad_inits_strides[3],
+    float* grad_logit_bias, void* workspace, size_t workspace_bytes, int B, int T, int NH,
+    int NKVH, int Da, int r, int use_sigmoid, void* stream) {
+  LTV_REQUIRE(values_strides && logits_strides && inits_strides && hq_strides && hk_strides &&
+                  hv_strides && grad_hq_strides && grad_hk_strides && grad_hv_strides &&
+                  grad_values_strides && grad_logits_strides && grad_inits_strides,
+              LTV_ERR_INVALID_ARG, "null stride array");
+  const void* hp[3] = {hq, hk, hv};
+  const int64_t* hs[3] = {hq_strides, hk_strides, hv_strides};
+  const void* gp[3] = {grad_hq, grad_hk, grad_hv};
+  const int64_t* gs[3] = {grad_hq_strides, grad_hk_strides, grad_hv_strides};
+  return scan_backward_impl(dtype, view4(values, values_strides), view4(logits, logits_strides),
+                            view3(inits, inits_strides), logit_bias, hp, hs, gp, gs,
+                            view4(grad_values, grad_values_strides),
+                            view4(grad_logits, grad_logits_strides),
+                            view3(grad_inits, grad_inits_strides), grad_logit_bias, workspace,
+                            workspace_bytes, B, T, NH, NKVH, Da, r, use_sigmoid,
+                            (hipStream_t)stream);
+}

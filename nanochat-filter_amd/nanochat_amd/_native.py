@@ -1,0 +1,210 @@
+"""ctypes binding of ``libnanochat_filter_amd.so`` (the C ABI in
+``include/nanochat_filter_amd.h``).
+
+There is exactly one compute path: the HIP library.  If it is missing or fails
+to load, every op raises -- nothing falls back to a CPU or PyTorch
+implementation.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+import torch
+
+LIB_NAME = "libnanochat_filter_amd.so"
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
+
+DTYPE_F32 = 0
+DTYPE_BF16 = 1
+
+ERR_NAMES = {1: "LTV_ERR_INVALID_ARG", 2: "LTV_ERR_UNSUPPORTED", 3: "LTV_ERR_HIP",
+             4: "LTV_ERR_WORKSPACE"}
+
+_c_int = ctypes.c_int
+_c_vp = ctypes.c_void_p
+_c_sz = ctypes.c_size_t
+_c_i64p = ctypes.POINTER(ctypes.c_int64)
+
+# name -> (restype, argtypes); kept in the order of include/nanochat_filter_amd.h
+SIGNATURES = {
+    "ltv_abi_version": (_c_int, []),
+    "ltv_last_error": (ctypes.c_char_p, []),
+    "ltv_hm_scan_forward": (
+        _c_int,
+        [_c_int, _c_vp, _c_i64p, _c_vp, _c_i64p, _c_vp, _c_vp, _c_i64p, _c_vp, _c_i64p, _c_vp,
+         _c_i64p, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_vp],
+    ),
+    "ltv_hm_scan_backward_workspace_size": (
+        _c_sz, [_c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int]),
+    "ltv_hm_scan_backward": (
+        _c_int,
+        [_c_int, _c_vp, _c_i64p, _c_vp, _c_i64p, _c_vp,
+         _c_vp, _c_i64p, _c_vp, _c_i64p, _c_vp, _c_i64p,
+         _c_vp, _c_i64p, _c_vp, _c_i64p, _c_vp, _c_i64p,
+         _c_vp, _c_i64p, _c_vp, _c_i64p, _c_vp,
+         _c_vp, _c_sz, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_vp],
+    ),
+    "ltv_hm_scan_forward_split": (
+        _c_int,
+        [_c_int, _c_vp, _c_i64p, _c_vp, _c_i64p, _c_vp, _c_i64p, _c_vp, _c_vp, _c_i64p, _c_vp,
+         _c_i64p, _c_vp, _c_i64p, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_vp],
+    ),
+    "ltv_hm_scan_backward_split": (
+        _c_int,
+        [_c_int, _c_vp, _c_i64p, _c_vp, _c_i64p, _c_vp, _c_i64p, _c_vp,
+         _c_vp, _c_i64p, _c_vp, _c_i64p, _c_vp, _c_i64p,
+         _c_vp, _c_i64p, _c_vp, _c_i64p, _c_vp, _c_i64p,
+         _c_vp, _c_i64p, _c_vp, _c_i64p, _c_vp, _c_i64p, _c_vp,
+         _c_vp, _c_sz, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_vp],
+    ),
+    "ltv_linear_transpose_forward": (
+        _c_int, [_c_int, _c_vp, _c_vp, _c_vp, _c_int, _c_int, _c_int, _c_int, _c_vp]),
+    "ltv_linear_transpose_backward": (
+        _c_int,
+        [_c_int, _c_vp, _c_vp, _c_vp, _c_int, _c_vp, _c_vp, _c_int, _c_int, _c_int, _c_int,
+         _c_vp],
+    ),
+    "ltv_qkv_packed_width": (_c_int, [_c_int, _c_int, _c_int]),
+    "ltv_qkv_pack_weight": (
+        _c_int, [_c_int, _c_vp, _c_vp, _c_int, _c_int, _c_int, _c_int, _c_vp]),
+    "ltv_qkv_project_forward": (
+        _c_int, [_c_vp, _c_vp, _c_vp, _c_int, _c_int, _c_int, _c_vp]),
+    "ltv_qkv_project_backward_workspace_size": (
+        _c_sz, [_c_int, _c_int, _c_int, _c_int, _c_int]),
+    "ltv_qkv_project_backward": (
+        _c_int,
+        [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_sz, _c_int, _c_int, _c_int, _c_int,
+         _c_int, _c_vp],
+    ),
+}
+
+_lib = None
+_lib_error: Exception | None = None
+_lock = threading.Lock()
+
+
+def load(path: str | None = None) -> ctypes.CDLL:
+    """Load the library once; raise a RuntimeError naming the cause if it cannot be."""
+    global _lib, _lib_error
+    with _lock:
+        if _lib is not None:
+            return _lib
+        p = path or LIB_PATH
+        if not os.path.exists(p):
+            _lib_error = RuntimeError(
+                f"{LIB_NAME} not found at {p}: build it with "
+                "`python nanochat-filter_amd/build_lib.py` (or __graft_entry__.build())"
+            )
+            raise _lib_error
+        lib = ctypes.CDLL(p)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = lib
+        return lib
+
+
+def lib() -> ctypes.CDLL:
+    return _lib if _lib is not None else load()
+
+
+def last_error() -> str:
+    return lib().ltv_last_error().decode("utf-8", "replace")
+
+
+def check(rc: int, what: str) -> None:
+    if rc != 0:
+        raise RuntimeError(f"{what} failed ({ERR_NAMES.get(rc, rc)}): {last_error()}")
+
+
+# ---------------------------------------------------------------------------
+# argument helpers
+# ---------------------------------------------------------------------------
+def strides(t: torch.Tensor, n: int | None = None):
+    s = list(t.stride())
+    if n is not None:
+        assert len(s) == n, (t.shape, n)
+    return (ctypes.c_int64 * len(s))(*s)
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def dtype_code(dt: torch.dtype) -> int:
+    if dt == torch.float32:
+        return DTYPE_F32
+    if dt == torch.bfloat16:
+        return DTYPE_BF16
+    raise TypeError(f"LTV kernels support float32 and bfloat16 tensors, got {dt}")
+
+
+def stream_of(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def require_device(*tensors: torch.Tensor) -> None:
+    for t in tensors:
+        if t is not None and t.device.type != "cuda":
+            raise RuntimeError(
+                f"LTV HIP kernels need GPU tensors, got a tensor on {t.device}")
+
+
+# ---------------------------------------------------------------------------
+# optional per-call timing: HIP events recorded on the launch stream around
+# each library call while a recorder is active (used by bench.py)
+# ---------------------------------------------------------------------------
+class KernelRecorder:
+    """Collects (name, start_event, end_event) for every instrumented call made
+    while it is active.  Events are recorded on torch's current stream, which is
+    the stream every op launches on."""
+
+    def __init__(self):
+        self.spans: list[tuple[str, torch.cuda.Event, torch.cuda.Event]] = []
+
+    def __enter__(self):
+        global _recorder
+        _recorder = self
+        return self
+
+    def __exit__(self, *exc):
+        global _recorder
+        _recorder = None
+        return False
+
+    def durations_ms(self) -> dict[str, list[float]]:
+        out: dict[str, list[float]] = {}
+        for name, a, b in self.spans:
+            out.setdefault(name, []).append(a.elapsed_time(b))
+        return out
+
+
+_recorder: KernelRecorder | None = None
+
+
+class span:
+    """``with span("scan_fwd"): lib.call(...)`` -- no-op unless recording."""
+
+    __slots__ = ("name", "ev")
+
+    def __init__(self, name: str):
+        self.name = name
+        self.ev = None
+
+    def __enter__(self):
+        if _recorder is not None:
+            a = torch.cuda.Event(enable_timing=True)
+            a.record()
+            self.ev = a
+        return self
+
+    def __exit__(self, *exc):
+        if self.ev is not None and _recorder is not None:
+            b = torch.cuda.Event(enable_timing=True)
+            b.record()
+            _recorder.spans.append((self.name, self.ev, b))
+        return False

@@ -1,0 +1,95 @@
+"""The drop-in LTV combined-QKV filter, running on the gfx950 HIP library.
+
+Same class name, constructor, parameters and ``forward(x, previous_values) ->
+(q, k, v)`` contract as the reference's
+``nanochat/ltv_cuda_fused_concat_head_major_register_cast_blelloch_scan_qkv_filter.py:21-73``:
+q is (B, T, n_head, D) and k, v are (B, T, n_kv_head, D), each a transposed view
+of a contiguous (B, H, T, D) buffer.
+
+dtype policy (reference ``:24-49``): the filter computes in float32 when autocast
+asks for float32, otherwise in the dtype of ``x``.
+  * bf16: the fast path -- ``nanochat_amd::qkv_project`` (bf16 MFMA with fp32
+    accumulation, the fp32 master weight cast to bf16 on the fly) writes values
+    and logits straight into the layout ``nanochat_amd::hm_scan`` reads.
+  * fp32: the reference-layout ops ``fused_linear_transpose`` (B, F, T) and the
+    ``nanochat_cuda`` scan op read through the transposed (B, T, F) view,
+    exactly the reference's dataflow.
+"""
+
+import torch
+
+import nanochat_amd.ops  # noqa: F401  (registers the ops)
+from nanochat_amd.ltv.ltv_filter import LtvInitValues
+from nanochat_amd.ltv_combined_head_major_qkv_filter import LtvCombinedHeadMajorQkvFilter
+from nanochat_amd.ltv_fused_concat_register_cast_scan_util import (
+    CUDA_SUPPORTS_NATIVE_BF16,
+    resolve_inits_original_dtype,
+    _SCAN_THREADS_FORWARD,
+    _R_THREADS_FORWARD,
+    _R_ITEMS_FORWARD,
+    _SCAN_THREADS_BACKWARD,
+    _R_THREADS_BACKWARD,
+    _R_ITEMS_BACKWARD,
+)
+from nanochat_amd.ops.ltv_cuda_ops import (
+    fused_linear_transpose,
+    ltv_cuda_fused_concat_head_major_register_cast_blelloch_scan,
+)
+
+
+class LtvCudaFusedConcatHeadMajorRegisterCastBlellochScanQkvFilter(
+    LtvCombinedHeadMajorQkvFilter
+):
+    def forward(self, x, previous_values: LtvInitValues):
+        B, _, _ = x.size()
+        autocast_dtype = torch.get_autocast_dtype("cuda")
+        run_ltv_in_fp32 = (
+            autocast_dtype == torch.float32 if CUDA_SUPPORTS_NATIVE_BF16 else True
+        )
+        compute_dtype = torch.float32 if run_ltv_in_fp32 else x.dtype
+        inits = resolve_inits_original_dtype(B, self.init_param, previous_values)
+        if compute_dtype == torch.bfloat16:
+            return self._forward_bf16(x, inits)
+        if compute_dtype != torch.float32:
+            raise TypeError(f"LTV filter computes in bfloat16 or float32, not {compute_dtype}")
+        return self._forward_fp32(x, inits)
+
+    def _forward_bf16(self, x, inits):
+        H, D, Da = self.total_active_heads, self.head_dim, self.num_alpha_groups
+        combined, _ = torch.ops.nanochat_amd.qkv_project(
+            x.to(torch.bfloat16).contiguous(), self.c.weight, H, D, Da
+        )
+        hq, hk, hv = torch.ops.nanochat_amd.hm_scan(
+            combined,
+            inits.to(dtype=torch.bfloat16).contiguous(),
+            self.logit_bias.float().contiguous(),
+            self.n_head,
+            self.n_kv_head,
+            Da,
+            self.r,
+            True,
+        )
+        return hq.transpose(1, 2), hk.transpose(1, 2), hv.transpose(1, 2)
+
+    def _forward_fp32(self, x, inits):
+        out_buf = fused_linear_transpose(x.float().contiguous(), self.c.weight.float().contiguous())
+        kernel_combined = out_buf.transpose(1, 2)  # (B, T, F) view, strides (F*T, 1, T)
+        hq, hk, hv = ltv_cuda_fused_concat_head_major_register_cast_blelloch_scan(
+            kernel_combined,
+            inits.to(dtype=kernel_combined.dtype).contiguous(),
+            self.logit_bias.float().contiguous(),
+            self.n_head,
+            self.n_kv_head,
+            self.num_alpha_groups,
+            self.r,
+            _SCAN_THREADS_FORWARD,
+            _R_THREADS_FORWARD,
+            _R_ITEMS_FORWARD,
+            _SCAN_THREADS_BACKWARD,
+            _R_THREADS_BACKWARD,
+            _R_ITEMS_BACKWARD,
+            True,  # use_sigmoid
+        )
+        if x.dtype != torch.float32:
+            hq, hk, hv = hq.to(x.dtype), hk.to(x.dtype), hv.to(x.dtype)
+        return hq.transpose(1, 2), hk.transpose(1, 2), hv.transpose(1, 2)

@@ -1,0 +1,105 @@
+"""Shared helpers for the LTV parity tests.
+
+The integer generators, the stride-layout enumeration and the tolerance rule
+follow the reference's own test utilities
+(tests/ltv_scan_test_utils.py:59-136 of aioaneid/nanochat-filter): values
+((9b + 7t + 3h + d) % 5) - 2, gate logits (b + t + h + j) % 2, inits
+((13b + 3h + d) % 7) - 3, logit bias ((h + 2j) % 3) - 1 with the sigmoid and 0
+without it.  Without the sigmoid the gates are 0 or 1 and every result is a
+small integer, so kernel and oracle must agree exactly.
+"""
+
+from __future__ import annotations
+
+import itertools
+
+import numpy as np
+import torch
+
+import ltv_oracle as O
+
+
+def stride_layouts(shape):
+    """Every axis order x gap factor in {1, 2} per axis (reference :66-77)."""
+    layouts = set()
+    ndim = len(shape)
+    for order in itertools.permutations(range(ndim)):
+        for gaps in itertools.product((1, 2), repeat=ndim):
+            stride = [0] * ndim
+            running = 1
+            for axis, gap in zip(order, gaps):
+                stride[axis] = running * gap
+                running = stride[axis] * shape[axis]
+            layouts.add(tuple(stride))
+    return sorted(layouts)
+
+
+def storage_size(shape, stride):
+    return 1 + sum((n - 1) * s for n, s in zip(shape, stride))
+
+
+def int_combined(B, T, NH, NKVH, Da, r):
+    H = NH + 2 * NKVH
+    D = Da * r
+    b, t, h, e = np.meshgrid(np.arange(B), np.arange(T), np.arange(H), np.arange(D + Da),
+                             indexing="ij")
+    vals = ((9 * b + 7 * t + 3 * h + e) % 5) - 2
+    gates = (b + t + h + (e - D)) % 2
+    c = np.where(e < D, vals, gates).astype(np.float32)
+    return c.reshape(B, T, H * (D + Da))
+
+
+def int_inits(B, NH, NKVH, Da, r):
+    H = NH + 2 * NKVH
+    D = Da * r
+    b, h, d = np.meshgrid(np.arange(B), np.arange(H), np.arange(D), indexing="ij")
+    return (((13 * b + 3 * h + d) % 7) - 3).astype(np.float32)
+
+
+def int_logit_bias(NH, NKVH, Da, sigmoid):
+    H = NH + 2 * NKVH
+    h, j = np.meshgrid(np.arange(H), np.arange(Da), indexing="ij")
+    if not sigmoid:
+        return np.zeros((H, Da), np.float32)
+    return (((h + 2 * j) % 3) - 1).astype(np.float32)
+
+
+def to_torch(a: np.ndarray, dtype: torch.dtype, device="cpu") -> torch.Tensor:
+    t = torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32))
+    return t.to(dtype).to(device)
+
+
+def strided_copy(a: np.ndarray, stride, dtype, device) -> torch.Tensor:
+    """Device tensor with the values of ``a`` and the given element strides."""
+    base = torch.zeros(storage_size(a.shape, stride), dtype=dtype, device=device)
+    view = torch.as_strided(base, size=a.shape, stride=stride)
+    view.copy_(to_torch(a, dtype, device))
+    return view
+
+
+def np_of(t: torch.Tensor) -> np.ndarray:
+    return t.detach().float().cpu().numpy()
+
+
+def io_name(dtype: torch.dtype) -> str:
+    return "bf16" if dtype == torch.bfloat16 else "f32"
+
+
+# tolerances: fp32 1e-4, bf16 I/O with fp32 state 2e-2
+TOL = {torch.float32: 1e-4, torch.bfloat16: 2e-2}
+
+
+def assert_close(actual, expected, tol, label=""):
+    """|a - e| <= tol * (|e| + max(1, max|e|)) elementwise; tol = 0 means exact."""
+    a = np.asarray(actual, np.float64)
+    e = np.asarray(expected, np.float64)
+    assert a.shape == e.shape, (label, a.shape, e.shape)
+    if tol == 0:
+        bad = a != e
+    else:
+        scale = max(1.0, float(np.abs(e).max()) if e.size else 1.0)
+        bad = np.abs(a - e) > tol * (np.abs(e) + scale)
+    if bad.any():
+        idx = np.argwhere(bad)[:5]
+        msg = ", ".join(f"{tuple(i)}: got {a[tuple(i)]} want {e[tuple(i)]}" for i in idx)
+        raise AssertionError(f"{label}: {int(bad.sum())}/{bad.size} mismatches (tol={tol}): {msg}")

@@ -1,0 +1,74 @@
+"""CPU checks of the C-ABI library: it loads, exports every function declared in
+include/nanochat_filter_amd.h, and the ctypes binding covers exactly those.
+No compute calls (there is no GPU here)."""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "nanochat_filter_amd.h")
+
+
+def declared_functions():
+    src = open(HEADER).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    names = re.findall(r"^\s*(?:const\s+)?[A-Za-z_][A-Za-z0-9_]*\s*\*?\s*(ltv_[a-z0-9_]+)\s*\(",
+                       src, flags=re.M)
+    return sorted(set(names))
+
+
+def test_header_declares_entry_points():
+    names = declared_functions()
+    for must in ("ltv_hm_scan_forward", "ltv_hm_scan_backward", "ltv_qkv_project_forward",
+                 "ltv_qkv_project_backward", "ltv_linear_transpose_forward",
+                 "ltv_linear_transpose_backward"):
+        assert must in names
+
+
+def test_library_exports_every_declared_symbol():
+    from nanochat_amd import _native as N
+    if not os.path.exists(N.LIB_PATH):
+        pytest.skip("library not built (run __graft_entry__.build())")
+    lib = ctypes.CDLL(N.LIB_PATH)
+    missing = [n for n in declared_functions() if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_ctypes_binding_matches_header():
+    from nanochat_amd import _native as N
+    assert sorted(N.SIGNATURES) == declared_functions()
+
+
+def test_abi_version_and_host_only_queries():
+    from nanochat_amd import _native as N
+    if not os.path.exists(N.LIB_PATH):
+        pytest.skip("library not built")
+    lib = N.load()
+    assert lib.ltv_abi_version() == 1
+    # d12: 18 heads x (128 + 1) = 2322 -> padded to a multiple of 64
+    assert lib.ltv_qkv_packed_width(18, 128, 1) == 2368
+    assert lib.ltv_hm_scan_backward_workspace_size(1, 32, 1024, 6, 6, 1, 128) >= 32 * 18 * 4
+    assert lib.ltv_qkv_project_backward_workspace_size(32768, 768, 18, 128, 1) > 0
+    # argument errors are reported without touching a device
+    rc = lib.ltv_qkv_project_forward(None, None, None, 16, 12, 64, None)
+    assert rc == 2 and "multiples of 8" in N.last_error()
+
+
+def test_ops_import_without_gpu():
+    import torch
+    import nanochat_amd.ops  # noqa: F401
+    assert hasattr(torch.ops.nanochat_cuda,
+                   "ltv_fused_concat_head_major_register_cast_blelloch_scan_cuda_op")
+    assert hasattr(torch.ops.nanochat_amd, "hm_scan")
+
+
+def test_product_path_refuses_cpu_tensors():
+    import torch
+    import nanochat_amd.ops  # noqa: F401
+    x = torch.zeros(1, 2, 8, dtype=torch.bfloat16)
+    w = torch.zeros(2 * (8 + 1) * 3, 8)
+    with pytest.raises(Exception):
+        torch.ops.nanochat_amd.qkv_project(x, w, 6, 8, 1)

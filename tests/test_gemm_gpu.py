@@ -1,0 +1,103 @@
+"""GPU parity of the projection.
+
+* the reference-layout op ``fused_linear_transpose`` against torch.matmul in
+  fp32 on the shapes of the reference's tests/test_fused_linear_transpose.py:32-86
+  (fp32 tolerance 1e-4, bf16 5e-2 as there);
+* the fast path ``nanochat_amd::qkv_project`` (bf16 MFMA) against a float64
+  product of the same bf16-rounded operands, forward and backward, including the
+  head-major split layout it writes.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from ltv_test_utils import assert_close, np_of
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _ops():
+    import nanochat_amd.ops  # noqa: F401
+    return torch.ops
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("B,T,K,F", [(1, 16, 32, 128), (4, 128, 128, 256),
+                                     (4, 1024, 1024, 3096), (2, 31, 63, 127)])
+def test_fused_linear_transpose(dtype, B, T, K, F):
+    ops = _ops()
+    g = torch.Generator().manual_seed(B * T + K + F)
+    x = (torch.randn(B, T, K, generator=g) / K ** 0.5).to(dtype).to(DEV).requires_grad_(True)
+    w = (torch.randn(F, K, generator=g) / K ** 0.5).to(dtype).to(DEV).requires_grad_(True)
+    xr = x.detach().float().requires_grad_(True)
+    wr = w.detach().float().requires_grad_(True)
+    ref = torch.matmul(wr, xr.transpose(-1, -2))  # plain torch fp32 reference
+    go = torch.randn(ref.shape, generator=g).to(DEV)
+    ref.backward(go)
+    out = ops.nanochat_cuda.fused_linear_transpose_cuda_op(x, w)
+    assert out.shape == (B, F, T) and out.is_contiguous() and out.dtype == dtype
+    out.backward(go.to(dtype))
+    tol = 5e-2 if dtype == torch.bfloat16 else 1e-4
+    assert_close(np_of(out), np_of(ref), tol, "out")
+    assert_close(np_of(x.grad), np_of(xr.grad), tol, "grad_x")
+    assert_close(np_of(w.grad), np_of(wr.grad), tol, "grad_weight")
+
+
+def test_fused_linear_transpose_accepts_btf_grad():
+    ops = _ops()
+    B, T, K, F = 2, 40, 24, 56
+    x = torch.randn(B, T, K, device=DEV)
+    w = torch.randn(F, K, device=DEV)
+    go_btf = torch.randn(B, T, F, device=DEV)
+    gx = torch.zeros_like(x)
+    gw = torch.zeros_like(w)
+    ops.nanochat_cuda.fused_linear_transpose_backward_kernel(x, w, go_btf.transpose(1, 2), gx, gw)
+    go = go_btf.transpose(1, 2).double().cpu()
+    assert_close(np_of(gx), (go.transpose(1, 2) @ w.double().cpu()).numpy(), 1e-4, "gx")
+    assert_close(np_of(gw), torch.einsum("bft,btk->fk", go, x.double().cpu()).numpy(), 1e-4, "gw")
+
+
+def _bf(t):
+    return t.to(torch.bfloat16).double()
+
+
+@pytest.mark.parametrize("B,T,C,NH,NKVH,D,Da", [
+    (2, 256, 768, 6, 6, 128, 1),   # d12 widths
+    (1, 100, 64, 1, 1, 16, 2),     # ragged M, small heads
+    (3, 33, 128, 2, 1, 64, 64),    # per-channel gates (r = 1)
+])
+def test_qkv_project_fast_path(B, T, C, NH, NKVH, D, Da):
+    ops = _ops()
+    H = NH + 2 * NKVH
+    F = H * (D + Da)
+    g = torch.Generator().manual_seed(T + C)
+    x = torch.randn(B, T, C, generator=g).to(torch.bfloat16)
+    w = torch.randn(F, C, generator=g) / C ** 0.5  # fp32 master, cast to bf16 by the op
+    xd = x.to(DEV).requires_grad_(True)
+    wd = w.to(DEV).requires_grad_(True)
+    comb, wpack = ops.nanochat_amd.qkv_project(xd, wd, H, D, Da)
+    Fp = comb.shape[2]
+    assert Fp % 64 == 0 and Fp >= F and comb.dtype == torch.bfloat16
+
+    ref = _bf(x) @ _bf(w).T  # (B, T, F) in the interleaved order, float64
+    ref4 = ref.view(B, T, H, D + Da)
+    want = torch.zeros(B, T, Fp, dtype=torch.float64)
+    want[..., : H * D] = ref4[..., :D].reshape(B, T, H * D)
+    want[..., H * D: H * D + H * Da] = ref4[..., D:].reshape(B, T, H * Da)
+    assert_close(np_of(comb), want.numpy(), 2e-2, "combined")
+
+    gc = torch.randn(B, T, Fp, generator=g).to(torch.bfloat16)
+    gc[..., H * (D + Da):] = float("nan")  # padding columns must be ignored
+    comb.backward(gc.to(DEV))
+    gc_i = torch.cat([gc[..., : H * D].view(B, T, H, D), gc[..., H * D: H * (D + Da)].view(B, T, H, Da)],
+                     dim=-1).reshape(B, T, F).double()
+    want_gx = gc_i @ _bf(w)
+    want_gw = torch.einsum("btf,btc->fc", gc_i, _bf(x))
+    assert torch.isfinite(xd.grad).all() and torch.isfinite(wd.grad).all()
+    assert wd.grad.dtype == torch.float32
+    assert_close(np_of(xd.grad), want_gx.numpy(), 2e-2, "grad_x")
+    assert_close(np_of(wd.grad), want_gw.numpy(), 2e-2, "grad_weight")
