@@ -25,6 +25,14 @@ __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
   return u >> 16;
 }
 
+// Two fp32 -> packed bf16 pair (lo in bits 0..15), round-to-nearest-even, on
+// the gfx950 conversion unit (v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint32_t cvt_pk_bf16(float lo, float hi) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  bf16x2_t v = {(__bf16)lo, (__bf16)hi};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
 template <typename TIO>
 struct io_traits;
 
@@ -78,13 +86,13 @@ __device__ __forceinline__ uint4 pack16(const float (&v)[8], bf16_t) {
 
 // ---------------------------------------------------------------------------
 // Gate: alpha = 1 / (1 + e^{-x}).  e^{-x} = 2^{-x log2 e} on the hardware
-// exp2 unit (v_exp_f32); the reciprocal is IEEE division.  For x -> +inf the
-// exponent underflows to 0 (alpha = 1); for x -> -inf it overflows to +inf
-// (alpha = 0).
+// exp2 unit (v_exp_f32) and the reciprocal on v_rcp_f32 (1 ulp).  For
+// x -> +inf the exponent underflows to 0 (alpha = 1); for x -> -inf it
+// overflows to +inf and the reciprocal gives 0 (alpha = 0).
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ float sigmoid_f32(float x) {
   const float e = __builtin_amdgcn_exp2f(-x * 1.4426950408889634f);
-  return 1.0f / (1.0f + e);
+  return __builtin_amdgcn_rcpf(1.0f + e);
 }
 
 __device__ __forceinline__ float gate_alpha(float logit_plus_bias, bool use_sigmoid) {

@@ -1,8 +1,66 @@
-// C-ABI entry points of the scan: argument checks, layout views and launch-shape
-// selection.  Kernels live in ltv_scan_fwd.hip / ltv_scan_bwd.hip.
-#include "ltv_scan_kernels.hpp"
+// C-ABI entry points of the scan: argument checks, layout views, gate-mode and
+// launch-shape selection.  The main kernels are built in ltv_scan_{fwd,bwd}_*.hip.
+#include <stdio.h>
+#include <stdlib.h>
+
+#include "ltv_scan_launch.hpp"
 
 namespace ltv {
+
+// dbias[h, j] = sum_b partial[b, h, j], fixed order.
+__global__ void dbias_reduce_kernel(const float* __restrict__ partial, float* __restrict__ dbias,
+                                    int B, int HDa) {
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < HDa; i += gridDim.x * blockDim.x) {
+    float acc = 0.0f;
+    for (int b = 0; b < B; ++b) acc += partial[(int64_t)b * HDa + i];
+    dbias[i] = acc;
+  }
+}
+
+int scan_launch_fwd(bool bf16, const FwdArgs& a, ScanCfg cfg, int grid, bool vec, int gm,
+                    hipStream_t st) {
+  return bf16 ? scan_fwd_launch_bf16(a, cfg, grid, vec, gm, st)
+              : scan_fwd_launch_f32(a, cfg, grid, vec, gm, st);
+}
+
+int scan_launch_bwd(bool bf16, const BwdArgs& a, ScanCfg cfg, int grid, bool vec, int gm,
+                    hipStream_t st) {
+  return bf16 ? scan_bwd_launch_bf16(a, cfg, grid, vec, gm, st)
+              : scan_bwd_launch_f32(a, cfg, grid, vec, gm, st);
+}
+
+int scan_launch_bwd_channel(bool bf16, const BwdArgs& a, float* dalpha, hipStream_t st) {
+  const ScanShape& S = a.sh;
+  const int64_t n = (int64_t)S.B * S.H * S.D;
+  const int threads = 256;
+  const int blocks = (int)((n + threads - 1) / threads);
+  const int64_t ng = (int64_t)S.B * S.H * S.Da;
+  const int gblocks = (int)((ng + threads - 1) / threads);
+  if (bf16) {
+    hipLaunchKernelGGL(scan_bwd_channel_kernel<bf16_t>, dim3(blocks), dim3(threads), 0, st, a,
+                       dalpha);
+    LTV_LAUNCH_CHECK();
+    hipLaunchKernelGGL(scan_bwd_group_reduce_kernel<bf16_t>, dim3(gblocks), dim3(threads), 0,
+                       st, a, dalpha);
+  } else {
+    hipLaunchKernelGGL(scan_bwd_channel_kernel<float>, dim3(blocks), dim3(threads), 0, st, a,
+                       dalpha);
+    LTV_LAUNCH_CHECK();
+    hipLaunchKernelGGL(scan_bwd_group_reduce_kernel<float>, dim3(gblocks), dim3(threads), 0, st,
+                       a, dalpha);
+  }
+  LTV_LAUNCH_CHECK();
+  return LTV_OK;
+}
+
+int scan_launch_dbias_reduce(const float* partial, float* dbias, int B, int HDa,
+                             hipStream_t st) {
+  hipLaunchKernelGGL(dbias_reduce_kernel, dim3((HDa + 255) / 256), dim3(256), 0, st, partial,
+                     dbias, B, HDa);
+  LTV_LAUNCH_CHECK();
+  return LTV_OK;
+}
+
 namespace {
 
 struct HostView4 {
@@ -26,6 +84,27 @@ inline bool vec_ok(const void* p, const int64_t* s, int nd_outer, int V) {
   return true;
 }
 
+// Launch-shape overrides, read once: LTV_SCAN_FWD_CFG="CL,L,NW" (CL = channel
+// lanes per wavefront, L = steps per lane, NW = wavefronts per workgroup) and
+// LTV_SCAN_BWD_CFG="L,NW" (the backward always spans the whole head).
+struct ScanTuning {
+  int fwd_cl = 0, fwd_l = 0, fwd_nw = 0;
+  int bwd_l = 0, bwd_nw = 0;
+  ScanTuning() {
+    if (const char* e = getenv("LTV_SCAN_FWD_CFG")) {
+      if (sscanf(e, "%d,%d,%d", &fwd_cl, &fwd_l, &fwd_nw) != 3) fwd_cl = fwd_l = fwd_nw = 0;
+    }
+    if (const char* e = getenv("LTV_SCAN_BWD_CFG")) {
+      if (sscanf(e, "%d,%d", &bwd_l, &bwd_nw) != 2) bwd_l = bwd_nw = 0;
+    }
+  }
+};
+
+const ScanTuning& tuning() {
+  static const ScanTuning t;
+  return t;
+}
+
 int check_shape(int dtype, int B, int T, int NH, int NKVH, int Da, int r) {
   LTV_REQUIRE(dtype == LTV_DTYPE_F32 || dtype == LTV_DTYPE_BF16, LTV_ERR_INVALID_ARG,
               "dtype must be LTV_DTYPE_F32 or LTV_DTYPE_BF16, got %d", dtype);
@@ -40,11 +119,18 @@ int check_shape(int dtype, int B, int T, int NH, int NKVH, int Da, int r) {
   return LTV_OK;
 }
 
-// The backward's in-register group reduction handles r % V == 0 with r / V a
-// power of two, and r dividing V; anything else goes to the channel kernel.
-inline bool bwd_main_ok(int r, int V) {
-  if (r % V == 0) return is_pow2(r / V);
-  return V % r == 0;
+// The main backward kernel reduces dalpha over gate groups that fill whole
+// lanes (r % V == 0, at most kMaxLaneGroups groups per head) or that fit in one
+// lane (V % r == 0); anything else goes to the per-channel kernel.
+inline int bwd_gate_mode(int r, int Da, int V) {
+  if (r % V == 0) return Da <= kMaxLaneGroups ? GATE_LANE : -1;
+  if (V % r == 0) return GATE_CHAN;
+  return -1;
+}
+
+// r == 1 with channel-contiguous, 16-byte addressable logits: vector gate loads.
+inline bool chanvec_ok(int r, int D, int V, const HostView4& lg) {
+  return r == 1 && D % V == 0 && vec_ok(lg.p, lg.s, 3, V);
 }
 
 int scan_forward_impl(int dtype, const HostView4& u, const HostView4& lg, const HostView4& init,
@@ -59,13 +145,8 @@ int scan_forward_impl(int dtype, const HostView4& u, const HostView4& lg, const 
               "null tensor pointer");
   const int V = dtype == LTV_DTYPE_BF16 ? 8 : 4;
   const int cl_full = next_pow2((D + V - 1) / V);
-  // Forward: slabs of at most 8 channel lanes (64 bf16 / 32 fp32 channels)
-  // give more workgroups per head; channels are independent in the forward.
-  const int CL = cl_full < 8 ? cl_full : 8;
-  const int nslab = (D + CL * V - 1) / (CL * V);
 
   FwdArgs a;
-  a.sh = ScanShape{B, T, NH, NKVH, Da, r, D, H, nslab, use_sigmoid};
   a.u = to_dev(u);
   a.lg = to_dev(lg);
   a.init = to_dev(init);
@@ -80,10 +161,22 @@ int scan_forward_impl(int dtype, const HostView4& u, const HostView4& lg, const 
       vec = vec && vec_ok(outp[i], outs[i], 3, V);
     }
   }
-  const bool lanegate = (r % V) == 0;
+  int gm = GATE_CHAN;
+  if (r % V == 0) gm = GATE_LANE;
+  else if (vec && chanvec_ok(r, D, V, lg)) gm = GATE_CHANVEC;
+
+  // Channels are independent in the forward: slabs of up to 8 channel lanes
+  // (64 bf16 / 32 fp32 channels), 4 steps per lane, 4 wavefronts.  Measured on
+  // MI355X at d12 this is the fastest built shape: the whole grid is resident
+  // at once and each load instruction covers 8 rows of 128 bytes.
+  ScanCfg cfg{cl_full < 8 ? cl_full : 8, 4, 4};
+  const ScanTuning& tu = tuning();
+  if (vec && tu.fwd_cl > 0) cfg = ScanCfg{tu.fwd_cl < cl_full ? tu.fwd_cl : cl_full, tu.fwd_l, tu.fwd_nw};
+  const int nslab = (D + cfg.CL * V - 1) / (cfg.CL * V);
+  a.sh = ScanShape{B, T, NH, NKVH, Da, r, D, H, nslab, use_sigmoid};
   const int64_t grid = (int64_t)B * H * nslab;
   LTV_REQUIRE(grid < (1ll << 31), LTV_ERR_UNSUPPORTED, "grid too large");
-  return scan_launch_fwd(dtype == LTV_DTYPE_BF16, a, CL, (int)grid, vec, lanegate, st);
+  return scan_launch_fwd(dtype == LTV_DTYPE_BF16, a, cfg, (int)grid, vec, gm, st);
 }
 
 size_t bwd_workspace_bytes(int dtype, int B, int T, int NH, int NKVH, int Da, int r) {
@@ -91,7 +184,7 @@ size_t bwd_workspace_bytes(int dtype, int B, int T, int NH, int NKVH, int Da, in
   const int V = dtype == LTV_DTYPE_BF16 ? 8 : 4;
   size_t bytes = (size_t)B * H * Da * sizeof(float);
   bytes = (bytes + 255) & ~(size_t)255;
-  if (!bwd_main_ok(r, V)) bytes += (size_t)B * H * T * Da * r * sizeof(float);
+  if (bwd_gate_mode(r, Da, V) < 0) bytes += (size_t)B * H * T * Da * r * sizeof(float);
   return bytes;
 }
 
@@ -139,19 +232,25 @@ int scan_backward_impl(int dtype, const HostView4& u, const HostView4& lg, const
       vec = vec && vec_ok(hp[i], hs[i], 3, V) && vec_ok(gp[i], gs[i], 3, V);
     }
   }
-  a.du.p[0] = const_cast<void*>(du.p);
-  a.du.p[1] = a.du.p[2] = nullptr;
-  for (int k = 0; k < 4; ++k) a.du.s[0][k] = a.du.s[1][k] = a.du.s[2][k] = du.s[k];
+  a.du = to_dev(du);
   a.dlg = to_dev(dlg);
   a.dinit = to_dev(dinit);
   a.dbias_partial = reinterpret_cast<float*>(ws);
 
   const int64_t grid = (int64_t)B * H;
   LTV_REQUIRE(grid < (1ll << 31), LTV_ERR_UNSUPPORTED, "grid too large");
-  if (bwd_main_ok(r, V)) {
-    const int CL = next_pow2((D + V - 1) / V);
-    const bool lanegate = (r % V) == 0;
-    rc = scan_launch_bwd(dtype == LTV_DTYPE_BF16, a, CL, (int)grid, vec, lanegate, st);
+  int gm = bwd_gate_mode(r, Da, V);
+  if (gm == GATE_CHAN && vec && chanvec_ok(r, D, V, lg) && chanvec_ok(r, D, V, dlg))
+    gm = GATE_CHANVEC;
+  if (gm >= 0) {
+    // whole head per workgroup; 4 steps per lane keeps 3 wavefronts per SIMD
+    ScanCfg cfg{next_pow2((D + V - 1) / V), 4, 4};
+    const ScanTuning& tu = tuning();
+    if (vec && tu.bwd_l > 0) {
+      cfg.L = tu.bwd_l;
+      cfg.NW = tu.bwd_nw;
+    }
+    rc = scan_launch_bwd(dtype == LTV_DTYPE_BF16, a, cfg, (int)grid, vec, gm, st);
     if (rc) return rc;
   } else {
     size_t off = ((size_t)B * H * Da * sizeof(float) + 255) & ~(size_t)255;

@@ -1,0 +1,9 @@
+// Scan backward kernels for bf16 I/O.
+#include "ltv_scan_launch.hpp"
+
+namespace ltv {
+int scan_bwd_launch_bf16(const BwdArgs& a, ScanCfg c, int grid, bool vec, int gm,
+                        hipStream_t st) {
+  return scan_bwd_launch_t<bf16_t>(a, c, grid, vec, gm, st);
+}
+}  // namespace ltv

@@ -1,0 +1,9 @@
+// Scan backward kernels for fp32 I/O.
+#include "ltv_scan_launch.hpp"
+
+namespace ltv {
+int scan_bwd_launch_f32(const BwdArgs& a, ScanCfg c, int grid, bool vec, int gm,
+                        hipStream_t st) {
+  return scan_bwd_launch_t<float>(a, c, grid, vec, gm, st);
+}
+}  // namespace ltv

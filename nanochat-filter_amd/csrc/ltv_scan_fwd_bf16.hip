@@ -1,0 +1,9 @@
+// Scan forward kernels for bf16 I/O.
+#include "ltv_scan_launch.hpp"
+
+namespace ltv {
+int scan_fwd_launch_bf16(const FwdArgs& a, ScanCfg c, int grid, bool vec, int gm,
+                        hipStream_t st) {
+  return scan_fwd_launch_t<bf16_t>(a, c, grid, vec, gm, st);
+}
+}  // namespace ltv

@@ -5,29 +5,35 @@
 //   h_t     = (1 - alpha_t) * h_{t-1} + alpha_t * u_t,   h_{-1} = inits
 // as in nanochat/ops/ltv_reference_ops.py:83-124 and the CUDA kernels
 // cpp_ewma/src/ltv_fused_concat_head_major_register_cast_blelloch_scan_cuda_{forward,backward}.cu.
+// Each step is evaluated as h + alpha * (u - h) (one subtract, one FMA).
 //
-// Work decomposition (all of T for one (b, head, channel slab) per workgroup):
-//   * a lane owns V = 16 / sizeof(io) consecutive channels ("a vector") and a
-//     run of L consecutive time steps; the V x L block lives in registers;
-//   * a 64-lane wavefront is CL channel lanes x TG = 64 / CL time groups, with
-//     lane = cl * TG + tg, so the TG time groups of one channel vector are
-//     adjacent lanes;
-//   * NW wavefronts split time further; one pass ("tile") covers
-//     TW = NW * TG * L steps and the workgroup walks T tile by tile, carrying
-//     the fp32 state across tiles in registers.
-// Each tile is a three-level affine scan of (a, x) pairs, (a1,x1) then (a2,x2)
-// = (a1 a2, a2 x1 + x2):
-//   1. per lane: sequential fold of its L steps (registers);
-//   2. per wavefront: inclusive scan over the TG time-group lanes (shuffles);
-//   3. per workgroup: wavefront aggregates through LDS (one barrier per tile),
+// Work decomposition (a workgroup owns all of T for one (b, head, channel slab)):
+//   * a lane owns V = 16 / sizeof(io) consecutive channels (one 16-byte vector)
+//     and a run of L consecutive time steps; the L vectors stay packed in
+//     registers in the I/O format and are widened to fp32 when used;
+//   * a 64-lane wavefront is CL channel lanes x TG = 64 / CL time groups, lane =
+//     cl * TG + tg, so the TG time groups of one channel vector are adjacent lanes
+//     of one 16-lane DPP row (when TG <= 16);
+//   * NW wavefronts split time further; one tile covers TW = NW * TG * L steps and
+//     the workgroup walks T tile by tile, carrying the fp32 state in registers.
+// A tile is a three-level affine scan of (A, X) pairs, (A1,X1) then (A2,X2) =
+// (A1 A2, A2 X1 + X2):
+//   1. per lane: sequential fold of its L steps;
+//   2. per wavefront: inclusive scan over the TG time-group lanes (DPP row shifts);
+//   3. per workgroup: wavefront totals through LDS (one barrier per tile),
 //      composed in wavefront order onto the running carry.
-// The lane then re-runs its L steps sequentially from its exact carry-in and
-// writes the outputs, so values are read from HBM once and written once.
+// The lane then re-runs its L steps from its exact carry-in and stores, so every
+// element is read from HBM once and written once.
 //
-// The backward runs the same structure in reverse time over
+// The backward walks the tiles in reverse.  Per tile it first recomputes the
+// forward states h_{t-1} from the saved output row just before the tile (the
+// same three-level scan), rounds them to the I/O dtype (the state the reference
+// backward reads back, ltv_reference_ops.py:7-34), then runs the reverse scan
 //   g_t = gy_t + (1 - alpha_{t+1}) g_{t+1},   g_T = 0
-// and emits du, dlogit, dinit and a per-workgroup dbias partial (reduced by a
-// second, single-workgroup kernel in a fixed order: no atomics, deterministic).
+// and emits du = alpha g, dalpha = (u - h_{t-1}) g reduced over each gate group,
+// dlogit = alpha (1 - alpha) dalpha, dinit = (1 - alpha_0) g_0 and a per-(b, h)
+// dbias partial.  All reductions run in a fixed order (LDS, no atomics), so the
+// results are bitwise reproducible.
 
 #pragma once
 
@@ -45,21 +51,21 @@ struct View4 {
 };
 
 struct OutHeads {
-  void* p[3];      // q, k, v
+  void* p[3];       // q, k, v
   int64_t s[3][4];  // element strides (b, h_local, t, d)
 };
 
 struct ScanShape {
   int B, T, NH, NKVH, Da, r, D, H;
-  int nslab;      // channel slabs per head
+  int nslab;  // channel slabs per head (forward only)
   int use_sigmoid;
 };
 
 struct FwdArgs {
   ScanShape sh;
-  View4 u;       // values   (B, H, T, D)
-  View4 lg;      // logits   (B, H, T, Da)
-  View4 init;    // inits    (B, H, D) -- s[2] unused
+  View4 u;     // values   (B, H, T, D)
+  View4 lg;    // logits   (B, H, T, Da)
+  View4 init;  // inits    (B, H, D) -- s[2] unused
   const float* bias;  // (H, Da) contiguous fp32
   OutHeads out;
 };
@@ -70,16 +76,22 @@ struct BwdArgs {
   View4 lg;
   View4 init;
   const float* bias;
-  OutHeads h;      // saved forward outputs
-  OutHeads gy;     // upstream gradients
-  OutHeads du;     // gradient of the value slots (3 "heads" share one view: p[0])
-  View4 dlg;       // gradient of the logit slots
-  View4 dinit;     // (B, H, D)
+  OutHeads h;     // saved forward outputs
+  OutHeads gy;    // upstream gradients
+  View4 du;       // gradient of the value slots (B, H, T, D)
+  View4 dlg;      // gradient of the logit slots (B, H, T, Da)
+  View4 dinit;    // (B, H, D)
   float* dbias_partial;  // (B, H, Da) fp32 workspace
 };
 
-__device__ __forceinline__ void head_select(const OutHeads& o, int h, int NH, int NKVH,
-                                            int& which, int& hl) {
+// How a lane finds the gate of each of its V channels.
+enum GateMode {
+  GATE_LANE = 0,     // r % V == 0: one gate for the whole lane
+  GATE_CHAN = 1,     // per-channel gate j = c / r, scalar logit loads
+  GATE_CHANVEC = 2,  // r == 1 with channel-contiguous logits: one 16-byte logit load
+};
+
+__device__ __forceinline__ void head_select(int h, int NH, int NKVH, int& which, int& hl) {
   if (h < NH) {
     which = 0;
     hl = h;
@@ -92,44 +104,229 @@ __device__ __forceinline__ void head_select(const OutHeads& o, int h, int NH, in
   }
 }
 
-// Lane-local load / store of V channels at (b, h, t, c0..c0+V-1) of a strided view.
-template <typename TIO, bool VEC>
-__device__ __forceinline__ void load_vec(const TIO* base, int64_t sc, int nvalid,
-                                         float (&o)[io_traits<TIO>::kVec]) {
-  constexpr int V = io_traits<TIO>::kVec;
-  if (VEC) {
-    uint4 q = *reinterpret_cast<const uint4*>(base);
-    unpack16(q, o, TIO());
-  } else {
-#pragma unroll
-    for (int v = 0; v < V; ++v) o[v] = (v < nvalid) ? io_traits<TIO>::load(base + v * sc) : 0.0f;
+// ---------------------------------------------------------------------------
+// Packed 16-byte vectors of I/O elements
+// ---------------------------------------------------------------------------
+template <typename TIO>
+struct Pack;
+
+template <>
+struct Pack<bf16_t> {
+  static constexpr int V = 8;
+  __device__ static __forceinline__ float get(const uint4& q, int v) {
+    const uint32_t w = v < 2 ? q.x : v < 4 ? q.y : v < 6 ? q.z : q.w;
+    return __uint_as_float((v & 1) ? (w & 0xffff0000u) : (w << 16));
   }
+  __device__ static __forceinline__ uint32_t raw(const bf16_t* p) { return *p; }
+  __device__ static __forceinline__ void put_raw(uint32_t (&w)[4], int v, uint32_t bits) {
+    w[v >> 1] |= bits << (16 * (v & 1));
+  }
+  __device__ static __forceinline__ uint4 pack(const float (&x)[8]) {
+    return make_uint4(cvt_pk_bf16(x[0], x[1]), cvt_pk_bf16(x[2], x[3]),
+                      cvt_pk_bf16(x[4], x[5]), cvt_pk_bf16(x[6], x[7]));
+  }
+  __device__ static __forceinline__ void store1(bf16_t* p, float x) {
+    *p = (bf16_t)(cvt_pk_bf16(x, 0.0f) & 0xffffu);
+  }
+  __device__ static __forceinline__ float load1(const bf16_t* p) {
+    return __uint_as_float((uint32_t)*p << 16);
+  }
+};
+
+template <>
+struct Pack<float> {
+  static constexpr int V = 4;
+  __device__ static __forceinline__ float get(const uint4& q, int v) {
+    return __uint_as_float(v == 0 ? q.x : v == 1 ? q.y : v == 2 ? q.z : q.w);
+  }
+  __device__ static __forceinline__ uint32_t raw(const float* p) { return __float_as_uint(*p); }
+  __device__ static __forceinline__ void put_raw(uint32_t (&w)[4], int v, uint32_t bits) {
+    w[v] = bits;
+  }
+  __device__ static __forceinline__ uint4 pack(const float (&x)[4]) {
+    return make_uint4(__float_as_uint(x[0]), __float_as_uint(x[1]), __float_as_uint(x[2]),
+                      __float_as_uint(x[3]));
+  }
+  __device__ static __forceinline__ void store1(float* p, float x) { *p = x; }
+  __device__ static __forceinline__ float load1(const float* p) { return *p; }
+};
+
+// V channels at base, base + sc, ... (channels >= nvalid read as zero).
+template <typename TIO, bool VEC>
+__device__ __forceinline__ uint4 ld_vec(const TIO* base, int64_t sc, int nvalid) {
+  if (VEC) return *reinterpret_cast<const uint4*>(base);
+  constexpr int V = Pack<TIO>::V;
+  uint32_t w[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int v = 0; v < V; ++v)
+    if (v < nvalid) Pack<TIO>::put_raw(w, v, Pack<TIO>::raw(base + v * sc));
+  return make_uint4(w[0], w[1], w[2], w[3]);
 }
 
 template <typename TIO, bool VEC>
-__device__ __forceinline__ void store_vec(TIO* base, int64_t sc, int nvalid,
-                                          const float (&x)[io_traits<TIO>::kVec]) {
-  constexpr int V = io_traits<TIO>::kVec;
+__device__ __forceinline__ void st_vec(TIO* base, int64_t sc, int nvalid,
+                                       const float (&x)[Pack<TIO>::V]) {
   if (VEC) {
-    *reinterpret_cast<uint4*>(base) = pack16(x, TIO());
+    *reinterpret_cast<uint4*>(base) = Pack<TIO>::pack(x);
   } else {
 #pragma unroll
-    for (int v = 0; v < V; ++v)
-      if (v < nvalid) io_traits<TIO>::store(base + v * sc, x[v]);
+    for (int v = 0; v < Pack<TIO>::V; ++v)
+      if (v < nvalid) Pack<TIO>::store1(base + v * sc, x[v]);
   }
 }
+
+// Makes the compiler treat the packed vectors as rewritten, so it widens them
+// again where they are next used instead of keeping L x V fp32 copies alive
+// across the scan levels (widening is one shift or mask per element).
+template <int N>
+__device__ __forceinline__ void reload_barrier(uint4 (&q)[N]) {
+#pragma unroll
+  for (int s = 0; s < N; ++s)
+    asm volatile("" : "+v"(q[s].x), "+v"(q[s].y), "+v"(q[s].z), "+v"(q[s].w));
+}
+
+// ---------------------------------------------------------------------------
+// Shifts inside segments of TG adjacent lanes.  For TG <= 16 the segment lies in
+// one 16-lane row and a DPP row shift is exact for every lane the caller keeps
+// (tg >= off, resp. tg + off < TG); wider segments go through ds_bpermute.
+// ---------------------------------------------------------------------------
+template <int TG, int OFF>
+__device__ __forceinline__ float shift_up(float x) {
+  if constexpr (TG <= 16) {
+    return __int_as_float(
+        __builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x110 + OFF, 0xf, 0xf, false));
+  } else {
+    return __shfl_up(x, OFF, TG);
+  }
+}
+
+template <int TG, int OFF>
+__device__ __forceinline__ float shift_down(float x) {
+  if constexpr (TG <= 16) {
+    return __int_as_float(
+        __builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x100 + OFF, 0xf, 0xf, false));
+  } else {
+    return __shfl_down(x, OFF, TG);
+  }
+}
+
+// Inclusive then exclusive prefix (time order) of (A, X) pairs over the TG lanes.
+template <int TG, int NA, int V, int GI_LANE>
+struct SegScan {
+  template <int OFF>
+  __device__ static __forceinline__ void up_level(int tg, float (&A)[NA], float (&X)[V]) {
+    if constexpr (OFF < TG) {
+      float Ap[NA], Xp[V];
+#pragma unroll
+      for (int i = 0; i < NA; ++i) Ap[i] = shift_up<TG, OFF>(A[i]);
+#pragma unroll
+      for (int v = 0; v < V; ++v) Xp[v] = shift_up<TG, OFF>(X[v]);
+      if (tg >= OFF) {
+#pragma unroll
+        for (int v = 0; v < V; ++v) X[v] = fmaf(A[GI_LANE ? 0 : v], Xp[v], X[v]);
+#pragma unroll
+        for (int i = 0; i < NA; ++i) A[i] *= Ap[i];
+      }
+      up_level<OFF * 2>(tg, A, X);
+    }
+  }
+  template <int OFF>
+  __device__ static __forceinline__ void down_level(int tg, float (&A)[NA], float (&X)[V]) {
+    if constexpr (OFF < TG) {
+      float An[NA], Xn[V];
+#pragma unroll
+      for (int i = 0; i < NA; ++i) An[i] = shift_down<TG, OFF>(A[i]);
+#pragma unroll
+      for (int v = 0; v < V; ++v) Xn[v] = shift_down<TG, OFF>(X[v]);
+      if (tg + OFF < TG) {
+#pragma unroll
+        for (int v = 0; v < V; ++v) X[v] = fmaf(A[GI_LANE ? 0 : v], Xn[v], X[v]);
+#pragma unroll
+        for (int i = 0; i < NA; ++i) A[i] *= An[i];
+      }
+      down_level<OFF * 2>(tg, A, X);
+    }
+  }
+};
+
+// ---------------------------------------------------------------------------
+// Per-lane gate setup
+// ---------------------------------------------------------------------------
+template <int GM, int V>
+struct GateIdx {
+  static constexpr int NA = GM == GATE_LANE ? 1 : V;
+  int64_t off[NA];  // element offset of each gate's logit along the channel axis
+  float bias[NA];
+  __device__ __forceinline__ void init(const float* bias_h, int c0, int nvalid, int D, int r,
+                                       int64_t sc) {
+#pragma unroll
+    for (int i = 0; i < NA; ++i) {
+      const int c = min(c0 + (GM == GATE_LANE ? 0 : i), D - 1);
+      const int j = nvalid > 0 ? c / r : 0;
+      off[i] = (int64_t)j * sc;
+      bias[i] = bias_h[j];
+    }
+  }
+};
+
+// Raw logits of NS steps as loaded from memory: GATE_LANE keeps one value per
+// step, the per-channel modes one packed 16-byte vector per step (the V
+// channels' logits, gathered for GATE_CHAN).
+template <typename TIO, int GM, int NS>
+struct LogitRaw {
+  static constexpr int V = Pack<TIO>::V;
+  float one[GM == GATE_LANE ? NS : 1];
+  uint4 vec[GM == GATE_LANE ? 1 : NS];
+
+  __device__ __forceinline__ void load(const TIO* lp_t0, int64_t lst, const GateIdx<GM, V>& gi,
+                                       int t0, int T, bool active, int nvalid) {
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      const bool ok = active && (t0 + s) < T;
+      const TIO* p = lp_t0 + (int64_t)s * lst;
+      if (GM == GATE_LANE) {
+        one[s] = ok ? Pack<TIO>::load1(p + gi.off[0]) : 0.0f;
+      } else if (GM == GATE_CHANVEC) {
+        vec[s] = ok ? *reinterpret_cast<const uint4*>(p) : make_uint4(0u, 0u, 0u, 0u);
+      } else {
+        uint32_t w[4] = {0u, 0u, 0u, 0u};
+        if (ok) {
+#pragma unroll
+          for (int v = 0; v < V; ++v)
+            if (v < nvalid) Pack<TIO>::put_raw(w, v, Pack<TIO>::raw(p + gi.off[v]));
+        }
+        vec[s] = make_uint4(w[0], w[1], w[2], w[3]);
+      }
+    }
+  }
+
+  // alpha per step and gate; padded steps get alpha = 0 (the identity step)
+  template <int NA>
+  __device__ __forceinline__ void gates(const GateIdx<GM, V>& gi, int t0, int T, bool active,
+                                        bool use_sig, float (&al)[NS][NA]) const {
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      const bool ok = active && (t0 + s) < T;
+#pragma unroll
+      for (int i = 0; i < NA; ++i) {
+        const float raw = GM == GATE_LANE ? one[s] : Pack<TIO>::get(vec[s], i);
+        al[s][i] = ok ? gate_alpha(raw + gi.bias[i], use_sig) : 0.0f;
+      }
+    }
+  }
+};
 
 // ---------------------------------------------------------------------------
 // Forward
 // ---------------------------------------------------------------------------
-// LANEGATE: every lane's V channels share one gate (r % V == 0); otherwise each
-// channel reads its own gate j = c / r.
-template <typename TIO, int CL, int L, int NW, bool VEC, bool LANEGATE>
+template <typename TIO, int CL, int L, int NW, bool VEC, int GM>
 __global__ void __launch_bounds__(NW * 64)
 scan_fwd_kernel(const FwdArgs args) {
-  constexpr int V = io_traits<TIO>::kVec;
+  constexpr int V = Pack<TIO>::V;
   constexpr int TG = 64 / CL;
-  constexpr int NA = LANEGATE ? 1 : V;  // decay factors per lane
+  constexpr int NA = GM == GATE_LANE ? 1 : V;
+  constexpr int TW = NW * TG * L;
+  constexpr bool GL = GM == GATE_LANE;
   const ScanShape& S = args.sh;
 
   const int lane = threadIdx.x & 63;
@@ -144,11 +341,11 @@ scan_fwd_kernel(const FwdArgs args) {
   const int b = bid / S.H;
 
   const int c0 = (slab * CL + cl) * V;
-  const int nvalid = min(V, S.D - c0);  // may be <= 0 for padding lanes
-  const bool lane_active = nvalid > 0;
+  const int nvalid = min(V, S.D - c0);
+  const bool active = nvalid > 0;
 
   int which, hl;
-  head_select(args.out, h, S.NH, S.NKVH, which, hl);
+  head_select(h, S.NH, S.NKVH, which, hl);
   TIO* outp = reinterpret_cast<TIO*>(args.out.p[which]);
   const int64_t* os = args.out.s[which];
   outp += (int64_t)b * os[0] + (int64_t)hl * os[1] + (int64_t)c0 * os[3];
@@ -157,70 +354,55 @@ scan_fwd_kernel(const FwdArgs args) {
                   (int64_t)h * args.u.s[1] + (int64_t)c0 * args.u.s[3];
   const TIO* lp = reinterpret_cast<const TIO*>(args.lg.p) + (int64_t)b * args.lg.s[0] +
                   (int64_t)h * args.lg.s[1];
+  if (GM == GATE_CHANVEC) lp += (int64_t)c0;  // r == 1: gate j == channel
 
-  // gate index and bias per decay factor
-  int gj[NA];
-  float gbias[NA];
-#pragma unroll
-  for (int i = 0; i < NA; ++i) {
-    int c = c0 + (LANEGATE ? 0 : i);
-    int j = lane_active ? min(c, S.D - 1) / S.r : 0;
-    gj[i] = j;
-    gbias[i] = args.bias[h * S.Da + j];
-  }
+  GateIdx<GM, V> gi;
+  gi.init(args.bias + h * S.Da, c0, nvalid, S.D, S.r, args.lg.s[3]);
 
-  // running state (exact carry at the start of the current tile)
   float carry[V];
   {
     const TIO* ip = reinterpret_cast<const TIO*>(args.init.p) + (int64_t)b * args.init.s[0] +
                     (int64_t)h * args.init.s[1] + (int64_t)c0 * args.init.s[3];
-    if (lane_active)
-      load_vec<TIO, VEC>(ip, args.init.s[3], nvalid, carry);
-    else
+    uint4 q = make_uint4(0u, 0u, 0u, 0u);
+    if (active) q = ld_vec<TIO, VEC>(ip, args.init.s[3], nvalid);
 #pragma unroll
-      for (int v = 0; v < V; ++v) carry[v] = 0.0f;
+    for (int v = 0; v < V; ++v) carry[v] = Pack<TIO>::get(q, v);
   }
 
   __shared__ float lds_a[2][NW][CL][NA];
-  __shared__ float lds_x[2][NW][CL][V];
+  __shared__ float4 lds_x[2][NW][CL][V / 4];
 
-  constexpr int TW = NW * TG * L;
   const int ntiles = (S.T + TW - 1) / TW;
   const bool use_sig = S.use_sigmoid != 0;
+  const int64_t ust = args.u.s[2], usc = args.u.s[3], lst = args.lg.s[2];
+
+  // the next tile's packed values and raw logits are loaded while the current
+  // tile is scanned, so every wavefront keeps loads in flight
+  const int tl0 = (w * TG + tg) * L;
+  uint4 nu[L];
+  LogitRaw<TIO, GM, L> nl;
+  auto load_tile = [&](int it) {
+    const int t0 = it * TW + tl0;
+#pragma unroll
+    for (int s = 0; s < L; ++s) {
+      const bool ok = active && (t0 + s) < S.T;
+      nu[s] = ok ? ld_vec<TIO, VEC>(up + (int64_t)(t0 + s) * ust, usc, nvalid)
+                 : make_uint4(0u, 0u, 0u, 0u);
+    }
+    nl.load(lp + (int64_t)t0 * lst, lst, gi, t0, S.T, active, nvalid);
+  };
+  load_tile(0);
 
   for (int it = 0; it < ntiles; ++it) {
-    const int t0 = it * TW + (w * TG + tg) * L;
-
-    // ---- loads (all L steps issued before any use)
-    float uv[L][V];
+    const int t0 = it * TW + tl0;
+    uint4 uq[L];
+#pragma unroll
+    for (int s = 0; s < L; ++s) uq[s] = nu[s];
     float al[L][NA];
-#pragma unroll
-    for (int s = 0; s < L; ++s) {
-      const int t = t0 + s;
-      const bool ok = lane_active && t < S.T;
-      if (ok) {
-        load_vec<TIO, VEC>(up + (int64_t)t * args.u.s[2], args.u.s[3], nvalid, uv[s]);
-#pragma unroll
-        for (int i = 0; i < NA; ++i)
-          al[s][i] = io_traits<TIO>::load(lp + (int64_t)t * args.lg.s[2] +
-                                          (int64_t)gj[i] * args.lg.s[3]);
-      } else {
-#pragma unroll
-        for (int v = 0; v < V; ++v) uv[s][v] = 0.0f;
-#pragma unroll
-        for (int i = 0; i < NA; ++i) al[s][i] = 0.0f;
-      }
-    }
-    // ---- gates; padded steps become the identity (alpha = 0 -> a = 1, x = 0)
-#pragma unroll
-    for (int s = 0; s < L; ++s) {
-      const bool ok = lane_active && (t0 + s) < S.T;
-#pragma unroll
-      for (int i = 0; i < NA; ++i)
-        al[s][i] = ok ? gate_alpha(al[s][i] + gbias[i], use_sig) : 0.0f;
-    }
+    nl.gates(gi, t0, S.T, active, use_sig, al);
+    if (it + 1 < ntiles) load_tile(it + 1);
 
-    // ---- level 1: lane-local fold
+    // level 1: lane-local fold (padded steps have alpha = 0: the identity)
     float A[NA], X[V];
 #pragma unroll
     for (int i = 0; i < NA; ++i) A[i] = 1.0f;
@@ -230,95 +412,72 @@ scan_fwd_kernel(const FwdArgs args) {
     for (int s = 0; s < L; ++s) {
 #pragma unroll
       for (int v = 0; v < V; ++v) {
-        const float a = al[s][LANEGATE ? 0 : v];
-        X[v] = (1.0f - a) * X[v] + a * uv[s][v];
+        const float a = al[s][GL ? 0 : v];
+        X[v] = fmaf(a, Pack<TIO>::get(uq[s], v) - X[v], X[v]);
       }
 #pragma unroll
-      for (int i = 0; i < NA; ++i) A[i] *= (1.0f - al[s][i]);
+      for (int i = 0; i < NA; ++i) A[i] = fmaf(-A[i], al[s][i], A[i]);
     }
 
-    // ---- level 2: inclusive scan over the TG time-group lanes
-#pragma unroll
-    for (int off = 1; off < TG; off <<= 1) {
-      float Ap[NA], Xp[V];
-#pragma unroll
-      for (int i = 0; i < NA; ++i) Ap[i] = __shfl_up(A[i], off, TG);
-#pragma unroll
-      for (int v = 0; v < V; ++v) Xp[v] = __shfl_up(X[v], off, TG);
-      if (tg >= off) {
-#pragma unroll
-        for (int v = 0; v < V; ++v) X[v] = A[LANEGATE ? 0 : v] * Xp[v] + X[v];
-#pragma unroll
-        for (int i = 0; i < NA; ++i) A[i] *= Ap[i];
-      }
-    }
-    // exclusive prefix of this lane inside its wavefront
+    // level 2: inclusive scan over the time-group lanes, then the exclusive prefix
+    SegScan<TG, NA, V, GL>::template up_level<1>(tg, A, X);
     float Ae[NA], Xe[V];
 #pragma unroll
     for (int i = 0; i < NA; ++i) {
-      float t = __shfl_up(A[i], 1, TG);
-      Ae[i] = (tg == 0) ? 1.0f : t;
+      const float t = shift_up<TG, 1>(A[i]);
+      Ae[i] = tg == 0 ? 1.0f : t;
     }
 #pragma unroll
     for (int v = 0; v < V; ++v) {
-      float t = __shfl_up(X[v], 1, TG);
-      Xe[v] = (tg == 0) ? 0.0f : t;
+      const float t = shift_up<TG, 1>(X[v]);
+      Xe[v] = tg == 0 ? 0.0f : t;
     }
 
-    // ---- level 3: wavefront aggregates through LDS
-    float hin[V];
-    if (NW > 1) {
-      const int buf = it & 1;
-      if (tg == TG - 1) {
+    // level 3: wavefront totals through LDS, composed onto the running carry
+    const int buf = it & 1;
+    if (tg == TG - 1) {
 #pragma unroll
-        for (int i = 0; i < NA; ++i) lds_a[buf][w][cl][i] = A[i];
+      for (int i = 0; i < NA; ++i) lds_a[buf][w][cl][i] = A[i];
 #pragma unroll
-        for (int v = 0; v < V; ++v) lds_x[buf][w][cl][v] = X[v];
+      for (int q = 0; q < V / 4; ++q)
+        lds_x[buf][w][cl][q] = make_float4(X[4 * q], X[4 * q + 1], X[4 * q + 2], X[4 * q + 3]);
+    }
+    __syncthreads();
+    float hw[V];
+#pragma unroll
+    for (int v = 0; v < V; ++v) hw[v] = carry[v];
+#pragma unroll
+    for (int ww = 0; ww < NW; ++ww) {
+      if (ww == w) {
+#pragma unroll
+        for (int v = 0; v < V; ++v) hw[v] = carry[v];
       }
-      __syncthreads();
-      // carry into this wavefront, then on to the end of the tile
-      float cw[V];
+      float Aw[NA];
 #pragma unroll
-      for (int v = 0; v < V; ++v) cw[v] = carry[v];
+      for (int i = 0; i < NA; ++i) Aw[i] = lds_a[buf][ww][cl][i];
 #pragma unroll
-      for (int ww = 0; ww < NW; ++ww) {
-        if (ww == w) {
-#pragma unroll
-          for (int v = 0; v < V; ++v) hin[v] = cw[v];
-        }
-#pragma unroll
-        for (int v = 0; v < V; ++v)
-          cw[v] = lds_a[buf][ww][cl][LANEGATE ? 0 : v] * cw[v] + lds_x[buf][ww][cl][v];
-      }
-#pragma unroll
-      for (int v = 0; v < V; ++v) carry[v] = cw[v];
-    } else {
-      float Aw[NA], Xw[V];
-#pragma unroll
-      for (int i = 0; i < NA; ++i) Aw[i] = __shfl(A[i], TG - 1, TG);
-#pragma unroll
-      for (int v = 0; v < V; ++v) Xw[v] = __shfl(X[v], TG - 1, TG);
-#pragma unroll
-      for (int v = 0; v < V; ++v) {
-        hin[v] = carry[v];
-        carry[v] = Aw[LANEGATE ? 0 : v] * carry[v] + Xw[v];
+      for (int q = 0; q < V / 4; ++q) {
+        const float4 x4 = lds_x[buf][ww][cl][q];
+        carry[4 * q + 0] = fmaf(Aw[GL ? 0 : 4 * q + 0], carry[4 * q + 0], x4.x);
+        carry[4 * q + 1] = fmaf(Aw[GL ? 0 : 4 * q + 1], carry[4 * q + 1], x4.y);
+        carry[4 * q + 2] = fmaf(Aw[GL ? 0 : 4 * q + 2], carry[4 * q + 2], x4.z);
+        carry[4 * q + 3] = fmaf(Aw[GL ? 0 : 4 * q + 3], carry[4 * q + 3], x4.w);
       }
     }
-#pragma unroll
-    for (int v = 0; v < V; ++v) hin[v] = Ae[LANEGATE ? 0 : v] * hin[v] + Xe[v];
 
-    // ---- re-run the lane's steps from the exact carry-in and store
+    // re-run the lane's steps from its exact carry-in and store
+    reload_barrier(uq);
+    float hv[V];
+#pragma unroll
+    for (int v = 0; v < V; ++v) hv[v] = fmaf(Ae[GL ? 0 : v], hw[v], Xe[v]);
 #pragma unroll
     for (int s = 0; s < L; ++s) {
-      float hv[V];
 #pragma unroll
       for (int v = 0; v < V; ++v) {
-        const float a = al[s][LANEGATE ? 0 : v];
-        hin[v] = (1.0f - a) * hin[v] + a * uv[s][v];
-        hv[v] = hin[v];
+        const float a = al[s][GL ? 0 : v];
+        hv[v] = fmaf(a, Pack<TIO>::get(uq[s], v) - hv[v], hv[v]);
       }
-      const int t = t0 + s;
-      if (lane_active && t < S.T) store_vec<TIO, VEC>(outp + (int64_t)t * os[2], os[3], nvalid, hv);
+      if (active && (t0 + s) < S.T) st_vec<TIO, VEC>(outp + (int64_t)(t0 + s) * os[2], os[3], nvalid, hv);
     }
   }
 }
@@ -326,15 +485,21 @@ scan_fwd_kernel(const FwdArgs args) {
 // ---------------------------------------------------------------------------
 // Backward
 // ---------------------------------------------------------------------------
-// GROUP_LANES (runtime, power of two): number of channel lanes that share one
-// gate when LANEGATE (= r / V); 1 otherwise.  When !LANEGATE, r divides V and
-// each lane owns V / r complete gate groups.
-template <typename TIO, int CL, int L, int NW, bool VEC, bool LANEGATE>
+// GATE_LANE: r % V == 0; the gate group spans r / V adjacent channel lanes and
+//   dalpha is summed across them through LDS; at most kMaxLaneGroups groups.
+// GATE_CHAN / GATE_CHANVEC: V % r == 0; each lane holds V / r whole groups.
+constexpr int kMaxLaneGroups = 16;
+
+template <typename TIO, int CL, int L, int NW, bool VEC, int GM>
 __global__ void __launch_bounds__(NW * 64)
 scan_bwd_kernel(const BwdArgs args) {
-  constexpr int V = io_traits<TIO>::kVec;
+  constexpr int V = Pack<TIO>::V;
   constexpr int TG = 64 / CL;
-  constexpr int NA = LANEGATE ? 1 : V;
+  constexpr int NA = GM == GATE_LANE ? 1 : V;
+  constexpr int TW = NW * TG * L;
+  constexpr int NT = NW * 64;
+  constexpr bool GL = GM == GATE_LANE;
+  constexpr int MAXG = GL ? (CL < kMaxLaneGroups ? CL : kMaxLaneGroups) : V;
   const ScanShape& S = args.sh;
 
   const int lane = threadIdx.x & 63;
@@ -342,300 +507,368 @@ scan_bwd_kernel(const BwdArgs args) {
   const int cl = lane / TG;
   const int tg = lane % TG;
 
-  int bid = blockIdx.x;  // nslab == 1 for the backward: the workgroup owns the head
-  const int h = bid % S.H;
-  const int b = bid / S.H;
+  const int h = blockIdx.x % S.H;  // one workgroup per (b, head): every gate group inside
+  const int b = blockIdx.x / S.H;
 
   const int c0 = cl * V;
   const int nvalid = min(V, S.D - c0);
-  const bool lane_active = nvalid > 0;
-  const int group_lanes = LANEGATE ? (S.r / V) : 1;   // lanes per gate group
-  const int groups_per_lane = LANEGATE ? 1 : (V / S.r);
+  const bool active = nvalid > 0;
 
   int which, hl;
-  head_select(args.h, h, S.NH, S.NKVH, which, hl);
-  const TIO* hp = reinterpret_cast<const TIO*>(args.h.p[which]);
+  head_select(h, S.NH, S.NKVH, which, hl);
   const int64_t* hs = args.h.s[which];
-  hp += (int64_t)b * hs[0] + (int64_t)hl * hs[1] + (int64_t)c0 * hs[3];
-  const TIO* gp = reinterpret_cast<const TIO*>(args.gy.p[which]);
+  const TIO* hp = reinterpret_cast<const TIO*>(args.h.p[which]) + (int64_t)b * hs[0] +
+                  (int64_t)hl * hs[1] + (int64_t)c0 * hs[3];
   const int64_t* gs = args.gy.s[which];
-  gp += (int64_t)b * gs[0] + (int64_t)hl * gs[1] + (int64_t)c0 * gs[3];
-
+  const TIO* gp = reinterpret_cast<const TIO*>(args.gy.p[which]) + (int64_t)b * gs[0] +
+                  (int64_t)hl * gs[1] + (int64_t)c0 * gs[3];
   const TIO* up = reinterpret_cast<const TIO*>(args.u.p) + (int64_t)b * args.u.s[0] +
                   (int64_t)h * args.u.s[1] + (int64_t)c0 * args.u.s[3];
-  TIO* dup = reinterpret_cast<TIO*>(args.du.p[0]) + (int64_t)b * args.du.s[0][0] +
-             (int64_t)h * args.du.s[0][1] + (int64_t)c0 * args.du.s[0][3];
-  const int64_t dus_t = args.du.s[0][2], dus_c = args.du.s[0][3];
+  TIO* dup = reinterpret_cast<TIO*>(const_cast<void*>(args.du.p)) + (int64_t)b * args.du.s[0] +
+             (int64_t)h * args.du.s[1] + (int64_t)c0 * args.du.s[3];
   const TIO* lp = reinterpret_cast<const TIO*>(args.lg.p) + (int64_t)b * args.lg.s[0] +
                   (int64_t)h * args.lg.s[1];
   TIO* dlp = reinterpret_cast<TIO*>(const_cast<void*>(args.dlg.p)) + (int64_t)b * args.dlg.s[0] +
              (int64_t)h * args.dlg.s[1];
+  if (GM == GATE_CHANVEC) lp += (int64_t)c0;
   const TIO* ip = reinterpret_cast<const TIO*>(args.init.p) + (int64_t)b * args.init.s[0] +
                   (int64_t)h * args.init.s[1] + (int64_t)c0 * args.init.s[3];
-  TIO* dip = reinterpret_cast<TIO*>(const_cast<void*>(args.dinit.p)) + (int64_t)b * args.dinit.s[0] +
-             (int64_t)h * args.dinit.s[1] + (int64_t)c0 * args.dinit.s[3];
+  TIO* dip = reinterpret_cast<TIO*>(const_cast<void*>(args.dinit.p)) +
+             (int64_t)b * args.dinit.s[0] + (int64_t)h * args.dinit.s[1] +
+             (int64_t)c0 * args.dinit.s[3];
 
-  int gj[NA];
-  float gbias[NA];
-#pragma unroll
-  for (int i = 0; i < NA; ++i) {
-    int c = c0 + (LANEGATE ? 0 : i);
-    int j = lane_active ? min(c, S.D - 1) / S.r : 0;
-    gj[i] = j;
-    gbias[i] = args.bias[h * S.Da + j];
-  }
-  // this lane writes dlogit for group i when it leads it
-  const bool leader = LANEGATE ? ((cl % group_lanes) == 0) : true;
+  GateIdx<GM, V> gi;
+  gi.init(args.bias + h * S.Da, c0, nvalid, S.D, S.r, args.lg.s[3]);
 
-  float carry[V];  // g at the first step after the current tile (g_T = 0)
-#pragma unroll
-  for (int v = 0; v < V; ++v) carry[v] = 0.0f;
-  float dbias_acc[NA];
-#pragma unroll
-  for (int i = 0; i < NA; ++i) dbias_acc[i] = 0.0f;
-
-  __shared__ float lds_a[2][NW][CL][NA];
-  __shared__ float lds_x[2][NW][CL][V];
-  __shared__ float lds_db[NW * TG][CL][NA];
-
-  constexpr int TW = NW * TG * L;
-  const int ntiles = (S.T + TW - 1) / TW;
+  const int64_t ust = args.u.s[2], usc = args.u.s[3], lst = args.lg.s[2];
+  const int64_t dlst = args.dlg.s[2], dlsc = args.dlg.s[3];
   const bool use_sig = S.use_sigmoid != 0;
+  const int gl_lanes = GL ? S.r / V : 1;           // lanes per gate group (GATE_LANE)
 
+  __shared__ float lds_fa[NW][CL][NA];
+  __shared__ float4 lds_fx[NW][CL][V / 4];
+  __shared__ float lds_ba[NW][CL][NA];
+  __shared__ float4 lds_bx[NW][CL][V / 4];
+  // GATE_LANE: per-(step, lane) dalpha partials and per-(step, group) gate slopes
+  __shared__ float lds_p[GL ? TW : 1][GL ? CL : 1];
+  __shared__ float lds_sl[GL ? TW : 1][GL ? MAXG : 1];
+  __shared__ float lds_red[NT][MAXG];
+
+  float gcarry[V];  // g at the first step after the current tile
+#pragma unroll
+  for (int v = 0; v < V; ++v) gcarry[v] = 0.0f;
+  // dbias accumulators: GATE_CHAN* keeps one per channel slot in registers;
+  // GATE_LANE accumulates per group j in this thread's own row of lds_red.
+  float dacc[GL ? 1 : V];
+#pragma unroll
+  for (int k = 0; k < (GL ? 1 : V); ++k) dacc[k] = 0.0f;
+  if (GL) {
+#pragma unroll
+    for (int k = 0; k < MAXG; ++k) lds_red[threadIdx.x][k] = 0.0f;
+  }
+
+  const int ntiles = (S.T + TW - 1) / TW;
   for (int it = ntiles - 1; it >= 0; --it) {
-    const int t0 = it * TW + (w * TG + tg) * L;
+    const int T0 = it * TW;
+    const int t0 = T0 + (w * TG + tg) * L;
 
-    float gyv[L][V];
-    float uv[L][V];
-    float hpv[L][V];
-    float al[L + 1][NA];
+    uint4 uq[L], gq[L];
 #pragma unroll
     for (int s = 0; s < L; ++s) {
-      const int t = t0 + s;
-      const bool ok = lane_active && t < S.T;
-      if (ok) {
-        load_vec<TIO, VEC>(gp + (int64_t)t * gs[2], gs[3], nvalid, gyv[s]);
-        load_vec<TIO, VEC>(up + (int64_t)t * args.u.s[2], args.u.s[3], nvalid, uv[s]);
-        if (t == 0)
-          load_vec<TIO, VEC>(ip, args.init.s[3], nvalid, hpv[s]);
-        else
-          load_vec<TIO, VEC>(hp + (int64_t)(t - 1) * hs[2], hs[3], nvalid, hpv[s]);
-      } else {
+      const bool ok = active && (t0 + s) < S.T;
+      uq[s] = ok ? ld_vec<TIO, VEC>(up + (int64_t)(t0 + s) * ust, usc, nvalid)
+                 : make_uint4(0u, 0u, 0u, 0u);
+      gq[s] = ok ? ld_vec<TIO, VEC>(gp + (int64_t)(t0 + s) * gs[2], gs[3], nvalid)
+                 : make_uint4(0u, 0u, 0u, 0u);
+    }
+    // state entering the tile: the saved output at T0 - 1, or the inits
+    float hc[V];
+    {
+      uint4 q = make_uint4(0u, 0u, 0u, 0u);
+      if (active) {
+        q = T0 == 0 ? ld_vec<TIO, VEC>(ip, args.init.s[3], nvalid)
+                    : ld_vec<TIO, VEC>(hp + (int64_t)(T0 - 1) * hs[2], hs[3], nvalid);
+      }
+#pragma unroll
+      for (int v = 0; v < V; ++v) hc[v] = Pack<TIO>::get(q, v);
+    }
+    float al[L + 1][NA];
+    {
+      LogitRaw<TIO, GM, L + 1> lr;
+      lr.load(lp + (int64_t)t0 * lst, lst, gi, t0, S.T, active, nvalid);
+      lr.gates(gi, t0, S.T, active, use_sig, al);
+    }
+
+    // ---- forward recompute of h_{t-1} inside the tile
+    uint4 hq[L];  // h_{t-1} for each step, rounded to the I/O dtype
+    {
+      float A[NA], X[V];
+#pragma unroll
+      for (int i = 0; i < NA; ++i) A[i] = 1.0f;
+#pragma unroll
+      for (int v = 0; v < V; ++v) X[v] = 0.0f;
+#pragma unroll
+      for (int s = 0; s < L; ++s) {
 #pragma unroll
         for (int v = 0; v < V; ++v) {
-          gyv[s][v] = 0.0f;
-          uv[s][v] = 0.0f;
-          hpv[s][v] = 0.0f;
+          const float a = al[s][GL ? 0 : v];
+          X[v] = fmaf(a, Pack<TIO>::get(uq[s], v) - X[v], X[v]);
         }
-      }
-    }
 #pragma unroll
-    for (int s = 0; s <= L; ++s) {
-      const int t = t0 + s;
-      const bool ok = lane_active && t < S.T;
+        for (int i = 0; i < NA; ++i) A[i] = fmaf(-A[i], al[s][i], A[i]);
+      }
+      SegScan<TG, NA, V, GL>::template up_level<1>(tg, A, X);
+      float Ae[NA], Xe[V];
 #pragma unroll
       for (int i = 0; i < NA; ++i) {
-        float raw = ok ? io_traits<TIO>::load(lp + (int64_t)t * args.lg.s[2] +
-                                              (int64_t)gj[i] * args.lg.s[3])
-                       : 0.0f;
-        al[s][i] = ok ? gate_alpha(raw + gbias[i], use_sig) : 0.0f;
-      }
-    }
-    // decay factor that carries g_{t+1} into g_t: a_{t+1} = 1 - alpha_{t+1};
-    // zero past the end of the sequence (g_T = 0) and for padded steps.
-    // level 1: lane-local reverse fold, (A, G): g_{t0} = A g_{t0+L} + G
-    float A[NA], G[V];
-#pragma unroll
-    for (int i = 0; i < NA; ++i) A[i] = 1.0f;
-#pragma unroll
-    for (int v = 0; v < V; ++v) G[v] = 0.0f;
-#pragma unroll
-    for (int s = L - 1; s >= 0; --s) {
-      const bool ok = lane_active && (t0 + s) < S.T;
-      const bool has_next = (t0 + s + 1) < S.T;
-#pragma unroll
-      for (int i = 0; i < NA; ++i) {
-        const float an = (ok && has_next) ? (1.0f - al[s + 1][i]) : (ok ? 0.0f : 1.0f);
-        // padded steps are the identity (A, G unchanged)
-        if (ok) A[i] *= an;
+        const float t = shift_up<TG, 1>(A[i]);
+        Ae[i] = tg == 0 ? 1.0f : t;
       }
 #pragma unroll
       for (int v = 0; v < V; ++v) {
-        const float an = has_next ? (1.0f - al[s + 1][LANEGATE ? 0 : v]) : 0.0f;
-        if (ok) G[v] = gyv[s][v] + an * G[v];
+        const float t = shift_up<TG, 1>(X[v]);
+        Xe[v] = tg == 0 ? 0.0f : t;
+      }
+      if (tg == TG - 1) {
+#pragma unroll
+        for (int i = 0; i < NA; ++i) lds_fa[w][cl][i] = A[i];
+#pragma unroll
+        for (int q = 0; q < V / 4; ++q)
+          lds_fx[w][cl][q] = make_float4(X[4 * q], X[4 * q + 1], X[4 * q + 2], X[4 * q + 3]);
+      }
+      __syncthreads();  // (1)
+      for (int ww = 0; ww < w; ++ww) {
+        float Aw[NA];
+#pragma unroll
+        for (int i = 0; i < NA; ++i) Aw[i] = lds_fa[ww][cl][i];
+#pragma unroll
+        for (int q = 0; q < V / 4; ++q) {
+          const float4 x4 = lds_fx[ww][cl][q];
+          hc[4 * q + 0] = fmaf(Aw[GL ? 0 : 4 * q + 0], hc[4 * q + 0], x4.x);
+          hc[4 * q + 1] = fmaf(Aw[GL ? 0 : 4 * q + 1], hc[4 * q + 1], x4.y);
+          hc[4 * q + 2] = fmaf(Aw[GL ? 0 : 4 * q + 2], hc[4 * q + 2], x4.z);
+          hc[4 * q + 3] = fmaf(Aw[GL ? 0 : 4 * q + 3], hc[4 * q + 3], x4.w);
+        }
+      }
+      reload_barrier(uq);
+      float hv[V];
+#pragma unroll
+      for (int v = 0; v < V; ++v) hv[v] = fmaf(Ae[GL ? 0 : v], hc[v], Xe[v]);
+#pragma unroll
+      for (int s = 0; s < L; ++s) {
+        hq[s] = Pack<TIO>::pack(hv);
+        if (s + 1 < L) {
+#pragma unroll
+          for (int v = 0; v < V; ++v) {
+            const float a = al[s][GL ? 0 : v];
+            hv[v] = fmaf(a, Pack<TIO>::get(uq[s], v) - hv[v], hv[v]);
+          }
+        }
       }
     }
 
-    // level 2: inclusive suffix scan over the TG time-group lanes
-#pragma unroll
-    for (int off = 1; off < TG; off <<= 1) {
-      float An[NA], Gn[V];
-#pragma unroll
-      for (int i = 0; i < NA; ++i) An[i] = __shfl_down(A[i], off, TG);
-#pragma unroll
-      for (int v = 0; v < V; ++v) Gn[v] = __shfl_down(G[v], off, TG);
-      if (tg + off < TG) {
-#pragma unroll
-        for (int v = 0; v < V; ++v) G[v] = A[LANEGATE ? 0 : v] * Gn[v] + G[v];
-#pragma unroll
-        for (int i = 0; i < NA; ++i) A[i] *= An[i];
-      }
-    }
-    float Ae[NA], Ge[V];  // exclusive suffix (lanes after this one)
-#pragma unroll
-    for (int i = 0; i < NA; ++i) {
-      float t = __shfl_down(A[i], 1, TG);
-      Ae[i] = (tg == TG - 1) ? 1.0f : t;
-    }
-#pragma unroll
-    for (int v = 0; v < V; ++v) {
-      float t = __shfl_down(G[v], 1, TG);
-      Ge[v] = (tg == TG - 1) ? 0.0f : t;
-    }
-
-    // level 3: wavefront aggregates, composed from the last wavefront back
+    // ---- reverse scan: g_t = gy_t + (1 - alpha_{t+1}) g_{t+1}
+    // decay carrying g_{t+1} into g_t; zero for the last step of the sequence
     float gin[V];
-    if (NW > 1) {
-      const int buf = it & 1;
+    {
+      float A[NA], G[V];
+#pragma unroll
+      for (int i = 0; i < NA; ++i) A[i] = 1.0f;
+#pragma unroll
+      for (int v = 0; v < V; ++v) G[v] = 0.0f;
+#pragma unroll
+      for (int s = L - 1; s >= 0; --s) {
+        const int t = t0 + s;
+        if (active && t < S.T) {
+          const bool nxt = t + 1 < S.T;
+#pragma unroll
+          for (int v = 0; v < V; ++v) {
+            const float an = nxt ? 1.0f - al[s + 1][GL ? 0 : v] : 0.0f;
+            G[v] = fmaf(an, G[v], Pack<TIO>::get(gq[s], v));
+          }
+#pragma unroll
+          for (int i = 0; i < NA; ++i) A[i] *= nxt ? 1.0f - al[s + 1][i] : 0.0f;
+        }
+      }
+      SegScan<TG, NA, V, GL>::template down_level<1>(tg, A, G);
+      float Ae[NA], Ge[V];
+#pragma unroll
+      for (int i = 0; i < NA; ++i) {
+        const float t = shift_down<TG, 1>(A[i]);
+        Ae[i] = tg == TG - 1 ? 1.0f : t;
+      }
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        const float t = shift_down<TG, 1>(G[v]);
+        Ge[v] = tg == TG - 1 ? 0.0f : t;
+      }
       if (tg == 0) {
 #pragma unroll
-        for (int i = 0; i < NA; ++i) lds_a[buf][w][cl][i] = A[i];
+        for (int i = 0; i < NA; ++i) lds_ba[w][cl][i] = A[i];
 #pragma unroll
-        for (int v = 0; v < V; ++v) lds_x[buf][w][cl][v] = G[v];
+        for (int q = 0; q < V / 4; ++q)
+          lds_bx[w][cl][q] = make_float4(G[4 * q], G[4 * q + 1], G[4 * q + 2], G[4 * q + 3]);
       }
-      __syncthreads();
-      float cw[V];
+      __syncthreads();  // (2)
+      float gw[V];
 #pragma unroll
-      for (int v = 0; v < V; ++v) cw[v] = carry[v];
+      for (int v = 0; v < V; ++v) gw[v] = gcarry[v];
 #pragma unroll
       for (int ww = NW - 1; ww >= 0; --ww) {
         if (ww == w) {
 #pragma unroll
-          for (int v = 0; v < V; ++v) gin[v] = cw[v];
+          for (int v = 0; v < V; ++v) gw[v] = gcarry[v];
         }
+        float Aw[NA];
 #pragma unroll
-        for (int v = 0; v < V; ++v)
-          cw[v] = lds_a[buf][ww][cl][LANEGATE ? 0 : v] * cw[v] + lds_x[buf][ww][cl][v];
+        for (int i = 0; i < NA; ++i) Aw[i] = lds_ba[ww][cl][i];
+#pragma unroll
+        for (int q = 0; q < V / 4; ++q) {
+          const float4 x4 = lds_bx[ww][cl][q];
+          gcarry[4 * q + 0] = fmaf(Aw[GL ? 0 : 4 * q + 0], gcarry[4 * q + 0], x4.x);
+          gcarry[4 * q + 1] = fmaf(Aw[GL ? 0 : 4 * q + 1], gcarry[4 * q + 1], x4.y);
+          gcarry[4 * q + 2] = fmaf(Aw[GL ? 0 : 4 * q + 2], gcarry[4 * q + 2], x4.z);
+          gcarry[4 * q + 3] = fmaf(Aw[GL ? 0 : 4 * q + 3], gcarry[4 * q + 3], x4.w);
+        }
       }
 #pragma unroll
-      for (int v = 0; v < V; ++v) carry[v] = cw[v];
-    } else {
-      float Aw[NA], Gw[V];
-#pragma unroll
-      for (int i = 0; i < NA; ++i) Aw[i] = __shfl(A[i], 0, TG);
-#pragma unroll
-      for (int v = 0; v < V; ++v) Gw[v] = __shfl(G[v], 0, TG);
-#pragma unroll
-      for (int v = 0; v < V; ++v) {
-        gin[v] = carry[v];
-        carry[v] = Aw[LANEGATE ? 0 : v] * carry[v] + Gw[v];
-      }
+      for (int v = 0; v < V; ++v) gin[v] = fmaf(Ae[GL ? 0 : v], gw[v], Ge[v]);
     }
-#pragma unroll
-    for (int v = 0; v < V; ++v) gin[v] = Ae[LANEGATE ? 0 : v] * gin[v] + Ge[v];
 
-    // re-run the lane's steps backwards from the exact carry-in
-    float dl[L][NA];
+    // ---- re-run backwards: du, dinit and the gate-group dalpha sums
+    reload_barrier(uq);
+    reload_barrier(gq);
+      float pl[L];  // GATE_LANE: this lane's dalpha partial per step
 #pragma unroll
     for (int s = L - 1; s >= 0; --s) {
       const int t = t0 + s;
-      const bool ok = lane_active && t < S.T;
-      const bool has_next = (t + 1) < S.T;
-      float duv[V], dav[V];
+      const bool ok = active && t < S.T;
+      const bool nxt = t + 1 < S.T;
+      float gv[V], duv[V], dav[V];
 #pragma unroll
       for (int v = 0; v < V; ++v) {
-        const int gi = LANEGATE ? 0 : v;
-        const float an = has_next ? (1.0f - al[s + 1][gi]) : 0.0f;
-        const float g = gyv[s][v] + an * gin[v];
-        gin[v] = ok ? g : gin[v];
-        const float alpha = al[s][gi];
-        duv[v] = alpha * g;
-        dav[v] = (uv[s][v] - hpv[s][v]) * g;
+        const int ia = GL ? 0 : v;
+        const float an = nxt ? 1.0f - al[s + 1][ia] : 0.0f;
+        gv[v] = ok ? fmaf(an, gin[v], Pack<TIO>::get(gq[s], v)) : gin[v];
+        gin[v] = gv[v];
+        duv[v] = al[s][ia] * gv[v];
+        dav[v] = (Pack<TIO>::get(uq[s], v) - Pack<TIO>::get(hq[s], v)) * gv[v];
       }
       if (ok) {
-        store_vec<TIO, VEC>(dup + (int64_t)t * dus_t, dus_c, nvalid, duv);
+        st_vec<TIO, VEC>(dup + (int64_t)t * args.du.s[2], args.du.s[3], nvalid, duv);
         if (t == 0) {
           float di[V];
 #pragma unroll
-          for (int v = 0; v < V; ++v) di[v] = (1.0f - al[s][LANEGATE ? 0 : v]) * gin[v];
-          store_vec<TIO, VEC>(dip, args.dinit.s[3], nvalid, di);
+          for (int v = 0; v < V; ++v) di[v] = (1.0f - al[s][GL ? 0 : v]) * gv[v];
+          st_vec<TIO, VEC>(dip, args.dinit.s[3], nvalid, di);
         }
       }
-      // per-group partial sums of dalpha over this lane's channels
-      if (LANEGATE) {
+      if (GL) {
         float p = 0.0f;
 #pragma unroll
-        for (int v = 0; v < V; ++v) p += (v < nvalid) ? dav[v] : 0.0f;
-        dl[s][0] = ok ? p : 0.0f;
+        for (int v = 0; v < V; ++v) p += v < nvalid ? dav[v] : 0.0f;
+        pl[s] = ok ? p : 0.0f;
       } else {
+        // whole groups of r channels (r | V, a power of two) inside the lane:
+        // butterfly sums leave every channel holding its group's total; the
+        // group's first channel stores the dlogit
 #pragma unroll
-        for (int i = 0; i < NA; ++i) dl[s][i] = 0.0f;
-        // V / r groups of r channels each: group k holds channels k*r .. k*r+r-1
-        for (int k = 0; k < groups_per_lane; ++k) {
-          float p = 0.0f;
-          for (int q = 0; q < S.r; ++q) {
-            const int v = k * S.r + q;
+        for (int m = 1; m < V; m <<= 1) {
+          if (m < S.r) {
+            float tsum[V];
 #pragma unroll
-            for (int vv = 0; vv < V; ++vv)
-              if (vv == v) p += (vv < nvalid) ? dav[vv] : 0.0f;
+            for (int v = 0; v < V; ++v) tsum[v] = dav[v] + dav[v ^ m];
+#pragma unroll
+            for (int v = 0; v < V; ++v) dav[v] = tsum[v];
           }
+        }
+        if (ok) {
+          float dl[V];
 #pragma unroll
-          for (int i = 0; i < NA; ++i)
-            if (i == k) dl[s][i] = ok ? p : 0.0f;
+          for (int v = 0; v < V; ++v) {
+            const float a = al[s][v];
+            dl[v] = use_sig ? dav[v] * (a * (1.0f - a)) : dav[v];
+          }
+          if (GM == GATE_CHANVEC) {
+            // r == 1: the V dlogits of this lane are contiguous
+            st_vec<TIO, true>(dlp + (int64_t)t * dlst + c0, 1, V, dl);
+#pragma unroll
+            for (int v = 0; v < V; ++v) dacc[v] += dl[v];
+          } else {
+#pragma unroll
+            for (int v = 0; v < V; ++v) {
+              if ((v & (S.r - 1)) == 0 && v < nvalid) {
+                dacc[v] += dl[v];
+                Pack<TIO>::store1(dlp + (int64_t)t * dlst + (int64_t)((c0 + v) / S.r) * dlsc,
+                                  dl[v]);
+              }
+            }
+          }
         }
       }
     }
-    // cross-lane reduction for groups that span lanes (butterfly over the
-    // channel-lane bits inside the group: bitwise identical in every lane)
-    if (LANEGATE) {
-      for (int m = 1; m < group_lanes; m <<= 1) {
+
+    if (GL) {
+      // ---- dlogit[t, j] = slope * sum of the group's lane partials (fixed order)
+      const int tl0 = (w * TG + tg) * L;
 #pragma unroll
-        for (int s = 0; s < L; ++s) dl[s][0] += __shfl_xor(dl[s][0], m * TG);
+      for (int s = 0; s < L; ++s) lds_p[tl0 + s][cl] = pl[s];
+      if (active && (cl % gl_lanes) == 0 && cl / gl_lanes < MAXG) {
+#pragma unroll
+        for (int s = 0; s < L; ++s) {
+          const float a = al[s][0];
+          lds_sl[tl0 + s][cl / gl_lanes] = use_sig ? a * (1.0f - a) : 1.0f;
+        }
       }
-    }
-    // finish: sigmoid multiplier, store dlogit, accumulate dbias
+      __syncthreads();  // (3)
+      for (int tl = threadIdx.x; tl < TW; tl += NT) {
+        const int t = T0 + tl;
+        if (t < S.T) {
 #pragma unroll
-    for (int s = 0; s < L; ++s) {
-      const int t = t0 + s;
-      const bool ok = lane_active && t < S.T;
-#pragma unroll
-      for (int i = 0; i < NA; ++i) {
-        // a group exists when its first channel is a real channel of the head
-        if (LANEGATE || (i < groups_per_lane && c0 + i * S.r < S.D)) {
-          const int gi = LANEGATE ? 0 : i * S.r;  // decay slot of the group's first channel
-          const float alpha = al[s][gi];
-          const float d = use_sig ? dl[s][i] * (alpha * (1.0f - alpha)) : dl[s][i];
-          if (ok && leader) {
-            const int j = gj[gi];
-            io_traits<TIO>::store(dlp + (int64_t)t * args.dlg.s[2] + (int64_t)j * args.dlg.s[3], d);
-            dbias_acc[i] += d;
+          for (int j = 0; j < MAXG; ++j) {
+            if (j < S.Da) {
+              float p = 0.0f;
+              for (int q = 0; q < gl_lanes; ++q) p += lds_p[tl][j * gl_lanes + q];
+              const float d = p * lds_sl[tl][j];
+              lds_red[threadIdx.x][j] += d;
+              Pack<TIO>::store1(dlp + (int64_t)t * dlst + (int64_t)j * dlsc, d);
+            }
           }
         }
       }
     }
   }
 
-  // dbias partial for (b, h): sum the leaders' accumulators in a fixed order
-  const int tgw = w * TG + tg;
+  // ---- dbias partial for (b, h): fixed-order sum of the accumulators
+  if (!GL) {
 #pragma unroll
-  for (int i = 0; i < NA; ++i) lds_db[tgw][cl][i] = (lane_active && leader) ? dbias_acc[i] : 0.0f;
+    for (int k = 0; k < V; ++k) lds_red[threadIdx.x][k] = dacc[k];
+  }
   __syncthreads();
-  for (int j = threadIdx.x; j < S.Da; j += NW * 64) {
-    // gate j is led by channel lane (j * r) / V, decay slot (j * r) % V
-    const int c = j * S.r;
-    const int lcl = c / V;
-    const int slot = LANEGATE ? 0 : (c % V) / S.r;
+  for (int j = threadIdx.x; j < S.Da; j += NT) {
     float acc = 0.0f;
-    for (int q = 0; q < NW * TG; ++q) acc += lds_db[q][lcl][slot];
+    if (GL) {
+      // threads tl < min(TW, NT) hold group j in slot j
+      const int nth = TW < NT ? TW : NT;
+      for (int q = 0; q < nth; ++q) acc += lds_red[q][j];
+    } else {
+      // group j is led by channel c = j r: lane cl = c / V, slot c % V, in every
+      // time lane (w, tg) of the workgroup
+      const int c = j * S.r;
+      const int lcl = c / V, k = c % V;
+      for (int ww = 0; ww < NW; ++ww)
+        for (int q = 0; q < TG; ++q) acc += lds_red[ww * 64 + lcl * TG + q][k];
+    }
     args.dbias_partial[((int64_t)b * S.H + h) * S.Da + j] = acc;
   }
 }
 
 // ---------------------------------------------------------------------------
-// Generic backward for gate groups the main kernel cannot reduce in lanes
-// (r neither divides V nor is V times a power of two).  One thread per
-// (b, h, channel) walks T backwards; the per-channel dalpha terms go to an fp32
-// workspace and a second kernel reduces each group in channel order.
+// Generic backward for gate groups that neither fill whole lanes nor fit inside
+// one (r neither a multiple nor a divisor of V, or too many groups per head).
+// One thread per (b, h, channel) walks T backwards; the per-channel dalpha terms
+// go to an fp32 workspace and a second kernel reduces each group in channel
+// order.
 // ---------------------------------------------------------------------------
 template <typename TIO>
 __global__ void scan_bwd_channel_kernel(const BwdArgs args, float* __restrict__ dalpha_ws) {
@@ -646,15 +879,16 @@ __global__ void scan_bwd_channel_kernel(const BwdArgs args, float* __restrict__ 
   const int h = (int)((idx / S.D) % S.H);
   const int b = (int)(idx / ((int64_t)S.D * S.H));
   int which, hl;
-  head_select(args.h, h, S.NH, S.NKVH, which, hl);
+  head_select(h, S.NH, S.NKVH, which, hl);
   const TIO* hp = reinterpret_cast<const TIO*>(args.h.p[which]) + (int64_t)b * args.h.s[which][0] +
                   (int64_t)hl * args.h.s[which][1] + (int64_t)c * args.h.s[which][3];
-  const TIO* gp = reinterpret_cast<const TIO*>(args.gy.p[which]) + (int64_t)b * args.gy.s[which][0] +
-                  (int64_t)hl * args.gy.s[which][1] + (int64_t)c * args.gy.s[which][3];
+  const TIO* gp = reinterpret_cast<const TIO*>(args.gy.p[which]) +
+                  (int64_t)b * args.gy.s[which][0] + (int64_t)hl * args.gy.s[which][1] +
+                  (int64_t)c * args.gy.s[which][3];
   const TIO* up = reinterpret_cast<const TIO*>(args.u.p) + (int64_t)b * args.u.s[0] +
                   (int64_t)h * args.u.s[1] + (int64_t)c * args.u.s[3];
-  TIO* dup = reinterpret_cast<TIO*>(args.du.p[0]) + (int64_t)b * args.du.s[0][0] +
-             (int64_t)h * args.du.s[0][1] + (int64_t)c * args.du.s[0][3];
+  TIO* dup = reinterpret_cast<TIO*>(const_cast<void*>(args.du.p)) + (int64_t)b * args.du.s[0] +
+             (int64_t)h * args.du.s[1] + (int64_t)c * args.du.s[3];
   const int j = c / S.r;
   const TIO* lp = reinterpret_cast<const TIO*>(args.lg.p) + (int64_t)b * args.lg.s[0] +
                   (int64_t)h * args.lg.s[1] + (int64_t)j * args.lg.s[3];
@@ -662,30 +896,32 @@ __global__ void scan_bwd_channel_kernel(const BwdArgs args, float* __restrict__ 
   const bool use_sig = S.use_sigmoid != 0;
   float g = 0.0f, a_next = 0.0f;
   for (int t = S.T - 1; t >= 0; --t) {
-    const float alpha = gate_alpha(io_traits<TIO>::load(lp + (int64_t)t * args.lg.s[2]) + bias, use_sig);
-    g = io_traits<TIO>::load(gp + (int64_t)t * args.gy.s[which][2]) + a_next * g;
-    io_traits<TIO>::store(dup + (int64_t)t * args.du.s[0][2], alpha * g);
+    const float alpha = gate_alpha(Pack<TIO>::load1(lp + (int64_t)t * args.lg.s[2]) + bias, use_sig);
+    g = fmaf(a_next, g, Pack<TIO>::load1(gp + (int64_t)t * args.gy.s[which][2]));
+    Pack<TIO>::store1(dup + (int64_t)t * args.du.s[2], alpha * g);
     float hprev;
     if (t == 0) {
       const TIO* ip = reinterpret_cast<const TIO*>(args.init.p) + (int64_t)b * args.init.s[0] +
                       (int64_t)h * args.init.s[1] + (int64_t)c * args.init.s[3];
-      hprev = io_traits<TIO>::load(ip);
-      TIO* dip = reinterpret_cast<TIO*>(const_cast<void*>(args.dinit.p)) + (int64_t)b * args.dinit.s[0] +
-                 (int64_t)h * args.dinit.s[1] + (int64_t)c * args.dinit.s[3];
-      io_traits<TIO>::store(dip, (1.0f - alpha) * g);
+      hprev = Pack<TIO>::load1(ip);
+      TIO* dip = reinterpret_cast<TIO*>(const_cast<void*>(args.dinit.p)) +
+                 (int64_t)b * args.dinit.s[0] + (int64_t)h * args.dinit.s[1] +
+                 (int64_t)c * args.dinit.s[3];
+      Pack<TIO>::store1(dip, (1.0f - alpha) * g);
     } else {
-      hprev = io_traits<TIO>::load(hp + (int64_t)(t - 1) * args.h.s[which][2]);
+      hprev = Pack<TIO>::load1(hp + (int64_t)(t - 1) * args.h.s[which][2]);
     }
-    const float da = (io_traits<TIO>::load(up + (int64_t)t * args.u.s[2]) - hprev) * g;
+    const float da = (Pack<TIO>::load1(up + (int64_t)t * args.u.s[2]) - hprev) * g;
     dalpha_ws[(((int64_t)b * S.H + h) * S.T + t) * S.D + c] = da;
     a_next = 1.0f - alpha;
   }
 }
 
 template <typename TIO>
-__global__ void scan_bwd_group_reduce_kernel(const BwdArgs args, const float* __restrict__ dalpha_ws) {
+__global__ void scan_bwd_group_reduce_kernel(const BwdArgs args,
+                                             const float* __restrict__ dalpha_ws) {
   const ScanShape& S = args.sh;
-  // one thread per (b, h, j) over all t, so dbias partials need no extra pass
+  // one thread per (b, h, j) over all t, so the dbias partial needs no extra pass
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= (int64_t)S.B * S.H * S.Da) return;
   const int j = (int)(idx % S.Da);
@@ -702,25 +938,26 @@ __global__ void scan_bwd_group_reduce_kernel(const BwdArgs args, const float* __
     const float* row = dalpha_ws + (((int64_t)b * S.H + h) * S.T + t) * S.D + (int64_t)j * S.r;
     float p = 0.0f;
     for (int q = 0; q < S.r; ++q) p += row[q];
-    const float alpha = gate_alpha(io_traits<TIO>::load(lp + (int64_t)t * args.lg.s[2]) + bias, use_sig);
+    const float alpha = gate_alpha(Pack<TIO>::load1(lp + (int64_t)t * args.lg.s[2]) + bias, use_sig);
     const float d = use_sig ? p * (alpha * (1.0f - alpha)) : p;
-    io_traits<TIO>::store(dlp + (int64_t)t * args.dlg.s[2], d);
+    Pack<TIO>::store1(dlp + (int64_t)t * args.dlg.s[2], d);
     acc_b += d;
   }
   args.dbias_partial[idx] = acc_b;
 }
 
 // ---------------------------------------------------------------------------
-// Host launchers (ltv_scan_fwd.hip / ltv_scan_bwd.hip)
+// Launch configuration and host launchers (ltv_scan_fwd*.hip / ltv_scan_bwd.hip)
 // ---------------------------------------------------------------------------
-constexpr int kScanL = 8;   // steps per lane per tile
-constexpr int kScanNW = 4;  // wavefronts per workgroup
+struct ScanCfg {
+  int CL, L, NW;
+};
 
-// Forward: grid = B * H * nslab workgroups of kScanNW * 64 threads.
-int scan_launch_fwd(bool bf16, const FwdArgs& a, int CL, int grid, bool vec, bool lanegate,
+// Forward: grid = B * H * nslab workgroups of NW * 64 threads.
+int scan_launch_fwd(bool bf16, const FwdArgs& a, ScanCfg cfg, int grid, bool vec, int gm,
                     hipStream_t st);
-// Backward main kernel: grid = B * H, CL channel lanes cover the whole head.
-int scan_launch_bwd(bool bf16, const BwdArgs& a, int CL, int grid, bool vec, bool lanegate,
+// Backward main kernel: grid = B * H; CL channel lanes cover the whole head.
+int scan_launch_bwd(bool bf16, const BwdArgs& a, ScanCfg cfg, int grid, bool vec, int gm,
                     hipStream_t st);
 // Backward for gate groups outside the main kernel's reduction patterns.
 int scan_launch_bwd_channel(bool bf16, const BwdArgs& a, float* dalpha_ws, hipStream_t st);
@@ -728,4 +965,3 @@ int scan_launch_bwd_channel(bool bf16, const BwdArgs& a, float* dalpha_ws, hipSt
 int scan_launch_dbias_reduce(const float* partial, float* dbias, int B, int HDa, hipStream_t st);
 
 }  // namespace ltv
-

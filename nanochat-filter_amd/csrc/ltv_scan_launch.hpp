@@ -1,0 +1,137 @@
+// Kernel instantiation and dispatch of the scan for one I/O dtype.  Included by
+// ltv_scan_{fwd,bwd}_{bf16,f32}.hip, one translation unit per direction and
+// dtype so the instantiations build in parallel.
+//
+// Launch shapes (CL channel lanes, L steps per lane, NW wavefronts) are template
+// parameters.  Every CL in {1, ..., 64} is built with (L, NW) = (4, 4); for the
+// channel-lane counts the d12 shapes use, a few more (L, NW) pairs are built so
+// the launch shape can be tuned (LTV_SCAN_FWD_CFG / LTV_SCAN_BWD_CFG).
+#pragma once
+
+#include "ltv_scan_kernels.hpp"
+
+namespace ltv {
+namespace detail {
+
+template <int CL, int L, int NW>
+constexpr bool is_base_cfg() {
+  return L == 4 && NW == 4;
+}
+
+template <typename TIO, int CL, int L, int NW>
+bool fwd_dispatch(const FwdArgs& a, int grid, bool vec, int gm, hipStream_t st) {
+  const dim3 blk(NW * 64);
+  if (vec) {
+    switch (gm) {
+      case GATE_LANE:
+        hipLaunchKernelGGL((scan_fwd_kernel<TIO, CL, L, NW, true, GATE_LANE>), dim3(grid), blk, 0, st, a);
+        return true;
+      case GATE_CHAN:
+        hipLaunchKernelGGL((scan_fwd_kernel<TIO, CL, L, NW, true, GATE_CHAN>), dim3(grid), blk, 0, st, a);
+        return true;
+      case GATE_CHANVEC:
+        hipLaunchKernelGGL((scan_fwd_kernel<TIO, CL, L, NW, true, GATE_CHANVEC>), dim3(grid), blk, 0, st, a);
+        return true;
+      default:
+        return false;
+    }
+  }
+  if constexpr (is_base_cfg<CL, L, NW>()) {
+    switch (gm) {
+      case GATE_LANE:
+        hipLaunchKernelGGL((scan_fwd_kernel<TIO, CL, L, NW, false, GATE_LANE>), dim3(grid), blk, 0, st, a);
+        return true;
+      case GATE_CHAN:
+        hipLaunchKernelGGL((scan_fwd_kernel<TIO, CL, L, NW, false, GATE_CHAN>), dim3(grid), blk, 0, st, a);
+        return true;
+      default:
+        return false;
+    }
+  }
+  return false;
+}
+
+template <typename TIO, int CL, int L, int NW>
+bool bwd_dispatch(const BwdArgs& a, int grid, bool vec, int gm, hipStream_t st) {
+  const dim3 blk(NW * 64);
+  if (vec) {
+    switch (gm) {
+      case GATE_LANE:
+        hipLaunchKernelGGL((scan_bwd_kernel<TIO, CL, L, NW, true, GATE_LANE>), dim3(grid), blk, 0, st, a);
+        return true;
+      case GATE_CHAN:
+        hipLaunchKernelGGL((scan_bwd_kernel<TIO, CL, L, NW, true, GATE_CHAN>), dim3(grid), blk, 0, st, a);
+        return true;
+      case GATE_CHANVEC:
+        hipLaunchKernelGGL((scan_bwd_kernel<TIO, CL, L, NW, true, GATE_CHANVEC>), dim3(grid), blk, 0, st, a);
+        return true;
+      default:
+        return false;
+    }
+  }
+  if constexpr (is_base_cfg<CL, L, NW>()) {
+    switch (gm) {
+      case GATE_LANE:
+        hipLaunchKernelGGL((scan_bwd_kernel<TIO, CL, L, NW, false, GATE_LANE>), dim3(grid), blk, 0, st, a);
+        return true;
+      case GATE_CHAN:
+        hipLaunchKernelGGL((scan_bwd_kernel<TIO, CL, L, NW, false, GATE_CHAN>), dim3(grid), blk, 0, st, a);
+        return true;
+      default:
+        return false;
+    }
+  }
+  return false;
+}
+
+}  // namespace detail
+
+// The launch shapes built for each direction: (CL, L, NW).
+#define LTV_SCAN_FWD_CONFIGS(X)                                                        \
+  X(1, 4, 4) X(2, 4, 4) X(4, 4, 4) X(8, 4, 4) X(16, 4, 4) X(32, 4, 4) X(64, 4, 4)      \
+  X(8, 8, 4) X(8, 2, 4) X(8, 4, 2) X(16, 8, 4) X(4, 8, 4)
+#define LTV_SCAN_BWD_CONFIGS(X)                                                        \
+  X(1, 4, 4) X(2, 4, 4) X(4, 4, 4) X(8, 4, 4) X(16, 4, 4) X(32, 4, 4) X(64, 4, 4)      \
+  X(16, 8, 4) X(16, 4, 2) X(16, 2, 4) X(32, 8, 4) X(8, 8, 4)
+
+template <typename TIO>
+int scan_fwd_launch_t(const FwdArgs& a, ScanCfg c, int grid, bool vec, int gm, hipStream_t st) {
+  bool ok = false;
+#define LTV_X(CL_, L_, NW_)                                                   \
+  if (!ok && c.CL == CL_ && c.L == L_ && c.NW == NW_)                         \
+    ok = detail::fwd_dispatch<TIO, CL_, L_, NW_>(a, grid, vec, gm, st);
+  LTV_SCAN_FWD_CONFIGS(LTV_X)
+#undef LTV_X
+  if (!ok) {
+    set_error("scan forward: launch shape CL=%d L=%d NW=%d (vec=%d gate=%d) is not built",
+              c.CL, c.L, c.NW, (int)vec, gm);
+    return LTV_ERR_UNSUPPORTED;
+  }
+  LTV_LAUNCH_CHECK();
+  return LTV_OK;
+}
+
+template <typename TIO>
+int scan_bwd_launch_t(const BwdArgs& a, ScanCfg c, int grid, bool vec, int gm, hipStream_t st) {
+  bool ok = false;
+#define LTV_X(CL_, L_, NW_)                                                   \
+  if (!ok && c.CL == CL_ && c.L == L_ && c.NW == NW_)                         \
+    ok = detail::bwd_dispatch<TIO, CL_, L_, NW_>(a, grid, vec, gm, st);
+  LTV_SCAN_BWD_CONFIGS(LTV_X)
+#undef LTV_X
+  if (!ok) {
+    set_error("scan backward: launch shape CL=%d L=%d NW=%d (vec=%d gate=%d) is not built",
+              c.CL, c.L, c.NW, (int)vec, gm);
+    return LTV_ERR_UNSUPPORTED;
+  }
+  LTV_LAUNCH_CHECK();
+  return LTV_OK;
+}
+
+// Per-dtype entry points (defined in the four translation units).
+int scan_fwd_launch_bf16(const FwdArgs& a, ScanCfg c, int grid, bool vec, int gm, hipStream_t st);
+int scan_fwd_launch_f32(const FwdArgs& a, ScanCfg c, int grid, bool vec, int gm, hipStream_t st);
+int scan_bwd_launch_bf16(const BwdArgs& a, ScanCfg c, int grid, bool vec, int gm, hipStream_t st);
+int scan_bwd_launch_f32(const BwdArgs& a, ScanCfg c, int grid, bool vec, int gm, hipStream_t st);
+
+}  // namespace ltv
