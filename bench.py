@@ -43,6 +43,7 @@ D, R = 128, 128
 DA = D // R
 H = NH + 2 * NKVH
 F = H * (D + DA)
+FP = (F + 127) // 128 * 128  # packed weight rows
 S_IO = 2  # bf16
 
 
@@ -55,8 +56,9 @@ def algorithmic_work():
         "scan_fwd": ("hbm", scan_fwd),
         "scan_bwd": ("hbm", scan_bwd),
         "qkv_project_fwd": ("mfma", gemm),
-        "qkv_project_bwd": ("mfma", 2 * gemm),
-        "pack_weight": ("hbm", F * C * 4 + 2368 * C * 2),
+        "qkv_project_bwd_input": ("mfma", gemm),
+        "qkv_project_bwd_weight": ("mfma", gemm),
+        "pack_weight": ("hbm", F * C * 4 + FP * C * 2),
     }
 
 

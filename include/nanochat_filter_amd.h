@@ -43,7 +43,7 @@ extern "C" {
 #define LTV_ERR_HIP 3
 #define LTV_ERR_WORKSPACE 4
 
-/* Version of this ABI (bumped on any signature change). */
+/* Version of this ABI (bumped on any signature change): 2. */
 int ltv_abi_version(void);
 
 /* Message of the last failing call on this host thread ("" if none). */
@@ -159,35 +159,50 @@ int ltv_linear_transpose_backward(int dtype, const void* x, const void* weight,
  * Fused QKV projection for the filter module (bf16 MFMA, fp32 accumulate).
  *
  * The parameter c.weight is (F, C) with per-head interleaved rows
- * [h0 values (D) | h0 logits (Da) | h1 values | ...]
+ * [h0 values (D) | h0 logits (Da) | h1 values | ...], F = H (D + Da)
  * (nanochat/ltv_combined_head_major_qkv_filter.py:11-66).
  *
+ * ltv_qkv_packed_width(H, D, Da) = Fp: F rounded up to a multiple of 128.
+ * ltv_qkv_logit_width(H, Da)     = Lp: H Da rounded up to a multiple of 8.
+ *
  * ltv_qkv_pack_weight: weight (F, C) fp32 or bf16 contiguous ->
- *   wpack (Fp, C) bf16: rows [all values, head-major | all logits | zeros]
- * with Fp = ltv_qkv_packed_width(H, D, Da) (a multiple of 64).
+ *   wpack (Fp, C) bf16: rows [all values, head-major | all logits | zeros].
  *
- * ltv_qkv_project_forward: x (M = B*T, C) bf16 contiguous ->
- *   combined (M, Fp) bf16 row-major: column h*D + d holds head h's value
- *   channel d, column H*D + h*Da + j its logit j, remaining columns zero.
+ * ltv_qkv_project_forward: x (B T, C) bf16 contiguous ->
+ *   values (B, H, T, D) bf16 contiguous (head-major: what the scan reads) and
+ *   logits (B T, Lp) bf16 contiguous (column h Da + j = logit j of head h;
+ *   columns >= H Da are unspecified).  One kernel launch.
  *
- * ltv_qkv_project_backward: grad_combined (M, Fp) bf16 (same layout; padding
- *   columns are ignored) ->
- *   grad_x (M, C) bf16 and grad_weight (F, C) fp32 in the parameter's
- *   interleaved row order (both overwritten).
+ * ltv_qkv_project_backward: grad_combined (B T, Fp) bf16 row-major with column
+ *   h D + d = gradient of value channel d of head h and column H D + h Da + j =
+ *   gradient of logit j (columns >= F are ignored) ->
+ *   grad_x (B T, C) bf16 and grad_weight (F, C) fp32 in the parameter's
+ *   interleaved row order (both overwritten; deterministic).
  * Counterpart in the reference: fused_linear_transpose forward/backward as used
  * by nanochat/ltv_cuda_fused_concat_head_major_register_cast_blelloch_scan_qkv_filter.py:35-41
  * (there the output is (B, F, T) and the scan reads it through a transposed view).
  * ---------------------------------------------------------------------- */
 int ltv_qkv_packed_width(int H, int D, int Da);
+int ltv_qkv_logit_width(int H, int Da);
 int ltv_qkv_pack_weight(int weight_dtype, const void* weight, void* wpack, int H, int D,
                         int Da, int C, void* stream);
-int ltv_qkv_project_forward(const void* x, const void* wpack, void* combined, int M, int C,
-                            int Fp, void* stream);
+int ltv_qkv_project_forward(const void* x, const void* wpack, void* values, void* logits, int B,
+                            int T, int C, int H, int D, int Da, void* stream);
 size_t ltv_qkv_project_backward_workspace_size(int M, int C, int H, int D, int Da);
 int ltv_qkv_project_backward(const void* x, const void* wpack, const void* grad_combined,
                              void* grad_x, float* grad_weight, void* workspace,
                              size_t workspace_bytes, int M, int C, int H, int D, int Da,
                              void* stream);
+/* The two halves of ltv_qkv_project_backward, as separate calls: grad_x
+ * (one GEMM launch) and grad_weight (split-K GEMM plus a fixed-order reduction;
+ * needs the workspace).  They mirror the grad_x and grad_weight loops of
+ * cpp_ewma/src/fused_linear_transpose_backward.cu:67-94 and :96-131. */
+int ltv_qkv_project_backward_input(const void* x, const void* wpack, const void* grad_combined,
+                                   void* grad_x, int M, int C, int H, int D, int Da,
+                                   void* stream);
+int ltv_qkv_project_backward_weight(const void* x, const void* grad_combined,
+                                    float* grad_weight, void* workspace, size_t workspace_bytes,
+                                    int M, int C, int H, int D, int Da, void* stream);
 
 #ifdef __cplusplus
 }

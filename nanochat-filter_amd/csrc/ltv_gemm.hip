@@ -5,254 +5,25 @@
 // Reference: cpp_ewma/src/fused_linear_transpose_forward.cu:23-58 (one
 // strided-batched GEMM, out[b] = W x[b]^T written (B, F, T)) and
 // cpp_ewma/src/fused_linear_transpose_backward.cu:22-132 (B GEMMs for dX and B
-// accumulating GEMMs for dW).  Here:
-//   forward   C[M, Fp]  = X[M, C] . Wp^T           (A, B both K-contiguous)
-//   backward  dX[M, C]  = dC[M, Fp] . Wp           (B operand N-contiguous)
-//             dW[Fp, C] = dC^T . X  over all M     (both operands reduction-strided),
-//             split over M into fp32 partials and reduced in a fixed order.
-// Wp is the parameter with its rows regrouped [values, head-major | logits | 0].
+// accumulating GEMMs for dW).  Here (M = B T tokens, Wp the parameter with its
+// rows regrouped [values, head-major | logits | zero pad], Fp rows):
+//   forward   values[B, H, T, D] | logits[M, Lp]  =  X[M, C] . Wp^T
+//             one launch; the epilogue writes the scan's head-major layout
+//   backward  dX[M, C]   = dC[M, Fp] . Wp                (Wp read transposed from LDS)
+//             dW^T[C, Fp] = X^T . dC  over all M          (both operands read transposed),
+//             split over M into fp32 partials, reduced in a fixed order into the
+//             parameter's interleaved row order.
 
 #include "ltv_device.hpp"
 #include "ltv_abi_internal.hpp"
+#include "ltv_gemm_mfma.hpp"
+
+#include <stdio.h>
+#include <stdlib.h>
 
 #include <algorithm>
 
 namespace ltv {
-
-typedef __bf16 bf16x8_v __attribute__((ext_vector_type(8)));
-typedef float floatx16_v __attribute__((ext_vector_type(16)));
-
-// ---------------------------------------------------------------------------
-// MFMA GEMM: C[m, n] = sum_k A(m, k) B(n, k)
-//   A_TRANS = false: A(m, k) at A[m * lda + k]   (K-contiguous)
-//   A_TRANS = true : A(m, k) at A[k * lda + m]   (M-contiguous)
-//   B likewise with n.
-// Tile 128 x 128 x 64, 256 threads = 4 wavefronts in 2 x 2, each 64 x 64 made
-// of 2 x 2 v_mfma_f32_32x32x16_bf16.  Operands staged K-contiguous in LDS
-// (M/N-contiguous operands are transposed in registers on the way in),
-// double-buffered with register prefetch: one barrier per K tile.
-// ---------------------------------------------------------------------------
-constexpr int GBM = 128, GBN = 128, GBK = 64;
-constexpr int GPAD = 8;                 // bf16 elements of row padding in LDS
-constexpr int GLDK = GBK + GPAD;        // LDS row pitch (elements)
-
-enum { EPI_BF16 = 0, EPI_F32 = 1 };
-
-struct MfmaArgs {
-  const bf16_t* A;
-  int64_t lda;
-  const bf16_t* B;
-  int64_t ldb;
-  void* C;
-  int64_t ldc;
-  int64_t c_split_stride;  // elements between split-K partial outputs
-  int M, N;
-  int k_begin, k_len;      // this launch's reduction range (per split: k_len)
-  int k_valid;             // A/B elements with k >= k_valid read as zero
-  int m_valid, n_valid;    // stores limited to these
-  int tiles_m, tiles_n;
-};
-
-// 4 (k) x 8 (row) block of bf16 -> 8 rows x 4 k (each uint2)
-__device__ __forceinline__ void transpose4x8(const uint4 (&in)[4], uint2 (&out)[8]) {
-  const uint32_t* w0 = reinterpret_cast<const uint32_t*>(&in[0]);
-  const uint32_t* w1 = reinterpret_cast<const uint32_t*>(&in[1]);
-  const uint32_t* w2 = reinterpret_cast<const uint32_t*>(&in[2]);
-  const uint32_t* w3 = reinterpret_cast<const uint32_t*>(&in[3]);
-#pragma unroll
-  for (int p = 0; p < 4; ++p) {
-    // rows 2p (low halves) and 2p+1 (high halves)
-    out[2 * p].x = __builtin_amdgcn_perm(w1[p], w0[p], 0x05040100u);
-    out[2 * p].y = __builtin_amdgcn_perm(w3[p], w2[p], 0x05040100u);
-    out[2 * p + 1].x = __builtin_amdgcn_perm(w1[p], w0[p], 0x07060302u);
-    out[2 * p + 1].y = __builtin_amdgcn_perm(w3[p], w2[p], 0x07060302u);
-  }
-}
-
-// zero the bf16 elements of a 16-byte chunk whose index k0 + e >= k_valid
-__device__ __forceinline__ uint4 mask_tail(uint4 q, int k0, int k_valid) {
-  if (k0 + 8 <= k_valid) return q;
-  uint32_t* w = reinterpret_cast<uint32_t*>(&q);
-#pragma unroll
-  for (int p = 0; p < 4; ++p) {
-    uint32_t keep = 0;
-    if (k0 + 2 * p < k_valid) keep |= 0x0000ffffu;
-    if (k0 + 2 * p + 1 < k_valid) keep |= 0xffff0000u;
-    w[p] &= keep;
-  }
-  return q;
-}
-
-// Per-thread staging registers for one operand tile.
-struct TileRegs {
-  uint4 q[4];
-};
-
-// K-contiguous operand: 128 rows x 64 k; thread loads rows (tid/8) + 32 i, k chunk (tid%8)*8
-__device__ __forceinline__ void load_tile_k(const bf16_t* P, int64_t ld, int row0, int rows,
-                                            int k0, int k_end, int k_valid, TileRegs& r) {
-  const int tid = threadIdx.x;
-  const int kc = (tid & 7) * 8;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int row = (tid >> 3) + 32 * i;
-    const int gr = row0 + row;
-    const int gk = k0 + kc;
-    uint4 q = make_uint4(0, 0, 0, 0);
-    if (gr < rows && gk < k_end) {
-      q = *reinterpret_cast<const uint4*>(P + (int64_t)gr * ld + gk);
-      q = mask_tail(q, gk, min(k_valid, k_end));
-    }
-    r.q[i] = q;
-  }
-}
-
-__device__ __forceinline__ void store_tile_k(bf16_t* lds, const TileRegs& r) {
-  const int tid = threadIdx.x;
-  const int kc = (tid & 7) * 8;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int row = (tid >> 3) + 32 * i;
-    *reinterpret_cast<uint4*>(lds + row * GLDK + kc) = r.q[i];
-  }
-}
-
-// Row-contiguous operand: element (row, k) at P[k * ld + row]; thread loads k rows
-// (tid/16)*4 .. +4, row chunk (tid%16)*8 .. +8.
-__device__ __forceinline__ void load_tile_t(const bf16_t* P, int64_t ld, int row0, int rows,
-                                            int k0, int k_end, int k_valid, TileRegs& r) {
-  const int tid = threadIdx.x;
-  const int rc = (tid & 15) * 8;
-  const int kg = (tid >> 4) * 4;
-  const int kmax = min(k_end, k_valid);
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int gk = k0 + kg + i;
-    const int gr = row0 + rc;
-    uint4 q = make_uint4(0, 0, 0, 0);
-    if (gk < kmax && gr < rows) q = *reinterpret_cast<const uint4*>(P + (int64_t)gk * ld + gr);
-    r.q[i] = q;
-  }
-}
-
-__device__ __forceinline__ void store_tile_t(bf16_t* lds, const TileRegs& r) {
-  const int tid = threadIdx.x;
-  const int rc = (tid & 15) * 8;
-  const int kg = (tid >> 4) * 4;
-  uint2 o[8];
-  transpose4x8(r.q, o);
-#pragma unroll
-  for (int e = 0; e < 8; ++e) *reinterpret_cast<uint2*>(lds + (rc + e) * GLDK + kg) = o[e];
-}
-
-template <bool A_TRANS, bool B_TRANS, int EPI>
-__global__ void __launch_bounds__(256, 2) gemm_mfma_kernel(const MfmaArgs g) {
-  __shared__ __attribute__((aligned(16))) bf16_t lds_a[2][GBM * GLDK];
-  __shared__ __attribute__((aligned(16))) bf16_t lds_b[2][GBN * GLDK];
-
-  // XCD-aware tile order: hardware hands workgroup i to XCD i % 8; give each
-  // XCD a contiguous run of tiles (all N tiles of an M block in a row) so the
-  // shared A rows stay in that XCD's L2.
-  const int ntiles = g.tiles_m * g.tiles_n;
-  int tile = blockIdx.x;
-  {
-    const int per = (ntiles + 7) / 8;
-    const int xcd = tile % 8, idx = tile / 8;
-    const int cand = xcd * per + idx;
-    // fall back to identity order for the ragged remainder
-    if (ntiles % 8 == 0) tile = cand;
-  }
-  const int tm = tile / g.tiles_n;
-  const int tn = tile % g.tiles_n;
-  const int m0 = tm * GBM, n0 = tn * GBN;
-  const int split = blockIdx.y;
-  const int kb = g.k_begin + split * g.k_len;
-  const int ke = kb + g.k_len;
-
-  const int lane = threadIdx.x & 63;
-  const int wv = threadIdx.x >> 6;
-  const int wm = wv >> 1, wn = wv & 1;
-
-  floatx16_v acc[2][2];
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
-
-  TileRegs ra, rb;
-  auto load = [&](int k0) {
-    if (A_TRANS) load_tile_t(g.A, g.lda, m0, g.M, k0, ke, g.k_valid, ra);
-    else load_tile_k(g.A, g.lda, m0, g.M, k0, ke, g.k_valid, ra);
-    if (B_TRANS) load_tile_t(g.B, g.ldb, n0, g.N, k0, ke, g.k_valid, rb);
-    else load_tile_k(g.B, g.ldb, n0, g.N, k0, ke, g.k_valid, rb);
-  };
-  auto stash = [&](int buf) {
-    if (A_TRANS) store_tile_t(lds_a[buf], ra);
-    else store_tile_k(lds_a[buf], ra);
-    if (B_TRANS) store_tile_t(lds_b[buf], rb);
-    else store_tile_k(lds_b[buf], rb);
-  };
-
-  const int nk = (ke - kb + GBK - 1) / GBK;
-  if (nk > 0) {
-    load(kb);
-    stash(0);
-  }
-  __syncthreads();
-
-  const int frow = lane & 31;
-  const int fk = (lane >> 5) * 8;
-  for (int kt = 0; kt < nk; ++kt) {
-    const int cur = kt & 1;
-    if (kt + 1 < nk) load(kb + (kt + 1) * GBK);
-    const bf16_t* la = lds_a[cur] + (wm * 64 + frow) * GLDK + fk;
-    const bf16_t* lb = lds_b[cur] + (wn * 64 + frow) * GLDK + fk;
-#pragma unroll
-    for (int ks = 0; ks < GBK; ks += 16) {
-      bf16x8_v af[2], bfr[2];
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        uint4 qa = *reinterpret_cast<const uint4*>(la + i * 32 * GLDK + ks);
-        uint4 qb = *reinterpret_cast<const uint4*>(lb + i * 32 * GLDK + ks);
-        af[i] = __builtin_bit_cast(bf16x8_v, qa);
-        bfr[i] = __builtin_bit_cast(bf16x8_v, qb);
-      }
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
-    }
-    if (kt + 1 < nk) stash(cur ^ 1);
-    __syncthreads();
-  }
-
-  // epilogue: lane holds column (lane % 32) of each 32 x 32 block, rows
-  // 8 * (v / 4) + 4 * (lane / 32) + v % 4
-  const int col = lane & 31;
-  const int rbase = (lane >> 5) * 4;
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int n = n0 + wn * 64 + j * 32 + col;
-      if (n >= g.n_valid) continue;
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int m = m0 + wm * 64 + i * 32 + 8 * (v >> 2) + rbase + (v & 3);
-        if (m >= g.m_valid) continue;
-        if (EPI == EPI_BF16) {
-          reinterpret_cast<bf16_t*>(g.C)[(int64_t)m * g.ldc + n] =
-              (bf16_t)f32_to_bf16_bits(acc[i][j][v]);
-        } else {
-          reinterpret_cast<float*>(g.C)[(int64_t)split * g.c_split_stride + (int64_t)m * g.ldc + n] =
-              acc[i][j][v];
-        }
-      }
-    }
-}
 
 // ---------------------------------------------------------------------------
 // Weight packing: parameter rows (per head: D values then Da logits) ->
@@ -395,13 +166,38 @@ int launch_simt(int dtype_in, int dtype_out, const SimtArgs& a, int batches, hip
   return LTV_OK;
 }
 
-template <bool AT, bool BT, int EPI>
-int launch_mfma(const MfmaArgs& a, int splits, hipStream_t st) {
-  dim3 grid(a.tiles_m * a.tiles_n, splits);
-  hipLaunchKernelGGL((gemm_mfma_kernel<AT, BT, EPI>), grid, dim3(256), 0, st, a);
+template <int BI, int BJ, int WGI, int WGJ, int PL, int QL, class Epi>
+int launch_gemm(const GemmArgs& a, const Epi& e, int splits, hipStream_t st) {
+  dim3 grid(a.tiles_i * a.tiles_j, splits);
+  hipLaunchKernelGGL((gemm_bf16_kernel<BI, BJ, WGI, WGJ, PL, QL, Epi>), grid, dim3(WGI * WGJ * 64),
+                     0, st, a, e);
   LTV_LAUNCH_CHECK();
   return LTV_OK;
 }
+
+// Tile variants of the three projection GEMMs, overridable for tuning with
+// LTV_GEMM_CFG="fwd,dx,dw,dw_split_rows" (variant indices, rows per dW split).
+struct GemmTuning {
+  int fwd = 0, dx = 0, dw = 0, dw_split = 4096;
+  GemmTuning() {
+    if (const char* e = getenv("LTV_GEMM_CFG")) {
+      int a = 0, b = 0, c = 0, d = 4096;
+      if (sscanf(e, "%d,%d,%d,%d", &a, &b, &c, &d) == 4 && d > 0 && d % kGemmBK == 0) {
+        fwd = a;
+        dx = b;
+        dw = c;
+        dw_split = d;
+      }
+    }
+  }
+};
+
+const GemmTuning& gemm_tuning() {
+  static const GemmTuning t;
+  return t;
+}
+
+inline int round_up(int x, int m) { return (x + m - 1) / m * m; }
 
 inline int dsize(int dtype) { return dtype == LTV_DTYPE_BF16 ? 2 : 4; }
 
@@ -459,9 +255,10 @@ extern "C" int ltv_linear_transpose_backward(int dtype, const void* x, const voi
 }
 
 extern "C" int ltv_qkv_packed_width(int H, int D, int Da) {
-  const int F = H * D + H * Da;
-  return (F + 63) / 64 * 64;
+  return round_up(H * D + H * Da, 128);
 }
+
+extern "C" int ltv_qkv_logit_width(int H, int Da) { return round_up(H * Da, 8); }
 
 extern "C" int ltv_qkv_pack_weight(int weight_dtype, const void* weight, void* wpack, int H,
                                    int D, int Da, int C, void* stream) {
@@ -485,45 +282,96 @@ extern "C" int ltv_qkv_pack_weight(int weight_dtype, const void* weight, void* w
   return LTV_OK;
 }
 
-extern "C" int ltv_qkv_project_forward(const void* x, const void* wpack, void* combined, int M,
-                                       int C, int Fp, void* stream) {
-  LTV_REQUIRE(M >= 0 && C > 0 && Fp > 0, LTV_ERR_INVALID_ARG, "bad shape");
-  LTV_REQUIRE(C % 8 == 0 && Fp % 8 == 0, LTV_ERR_UNSUPPORTED,
-              "C and Fp must be multiples of 8 (C=%d Fp=%d)", C, Fp);
+extern "C" int ltv_qkv_project_forward(const void* x, const void* wpack, void* values,
+                                       void* logits, int B, int T, int C, int H, int D, int Da,
+                                       void* stream) {
+  LTV_REQUIRE(B >= 0 && T >= 0 && C > 0 && H > 0 && D > 0 && Da > 0, LTV_ERR_INVALID_ARG,
+              "bad shape");
+  LTV_REQUIRE(C % 8 == 0 && D % 4 == 0, LTV_ERR_UNSUPPORTED,
+              "C must be a multiple of 8 and D of 4 (C=%d D=%d)", C, D);
+  const int64_t M64 = (int64_t)B * T;
+  LTV_REQUIRE(M64 < (1ll << 31), LTV_ERR_UNSUPPORTED, "too many tokens");
+  const int M = (int)M64;
   if (M == 0) return LTV_OK;
-  LTV_REQUIRE(x && wpack && combined, LTV_ERR_INVALID_ARG, "null tensor pointer");
-  LTV_REQUIRE(aligned16(x) && aligned16(wpack) && aligned16(combined), LTV_ERR_INVALID_ARG,
-              "x, wpack and combined must be 16-byte aligned");
-  MfmaArgs a;
-  a.A = reinterpret_cast<const bf16_t*>(x); a.lda = C;
-  a.B = reinterpret_cast<const bf16_t*>(wpack); a.ldb = C;
-  a.C = combined; a.ldc = Fp; a.c_split_stride = 0;
-  a.M = M; a.N = Fp; a.k_begin = 0; a.k_len = C; a.k_valid = C;
-  a.m_valid = M; a.n_valid = Fp;
-  a.tiles_m = (M + GBM - 1) / GBM; a.tiles_n = (Fp + GBN - 1) / GBN;
-  return launch_mfma<false, false, EPI_BF16>(a, 1, (hipStream_t)stream);
+  LTV_REQUIRE(x && wpack && values && logits, LTV_ERR_INVALID_ARG, "null tensor pointer");
+  LTV_REQUIRE(aligned16(x) && aligned16(wpack) && aligned16(values) && aligned16(logits),
+              LTV_ERR_INVALID_ARG, "x, wpack, values and logits must be 16-byte aligned");
+  const int Fp = ltv_qkv_packed_width(H, D, Da);
+  GemmArgs a;
+  a.P = GemmOperand{reinterpret_cast<const bf16_t*>(wpack), C, Fp, C};  // (n, k) KC
+  a.Q = GemmOperand{reinterpret_cast<const bf16_t*>(x), C, M, C};       // (m, k) KC
+  a.K = C;
+  a.k_split = round_up(C, kGemmBK);
+  EpiProjectHM e{reinterpret_cast<bf16_t*>(values), reinterpret_cast<bf16_t*>(logits), H, D, T,
+                 ltv_qkv_logit_width(H, Da), H * D + H * Da, M};
+  hipStream_t st = (hipStream_t)stream;
+  if (gemm_tuning().fwd == 1) {
+    a.tiles_i = (Fp + 255) / 256;
+    a.tiles_j = (M + 255) / 256;
+    return launch_gemm<256, 256, 2, 4, OP_KC, OP_KC>(a, e, 1, st);
+  }
+  a.tiles_i = Fp / 128;
+  a.tiles_j = (M + 255) / 256;
+  return launch_gemm<128, 256, 2, 2, OP_KC, OP_KC>(a, e, 1, st);
 }
 
 namespace {
-constexpr int kDwSplitRows = 4096;  // rows of M reduced by one split of the dW GEMM
-inline int dw_splits(int M) { return std::max(1, (M + kDwSplitRows - 1) / kDwSplitRows); }
+inline int dw_splits(int M, int rows) { return std::max(1, (M + rows - 1) / rows); }
+inline int dw_rows(int Fp, int variant) { return variant == 1 ? round_up(Fp, 128) : round_up(Fp, 256); }
 }  // namespace
 
 extern "C" size_t ltv_qkv_project_backward_workspace_size(int M, int C, int H, int D, int Da) {
   const int Fp = ltv_qkv_packed_width(H, D, Da);
-  const int Fr = (Fp + GBM - 1) / GBM * GBM;
-  return (size_t)dw_splits(M) * Fr * C * sizeof(float);
+  const GemmTuning& tu = gemm_tuning();
+  return (size_t)dw_splits(M, tu.dw_split) * dw_rows(Fp, tu.dw) * C * sizeof(float);
 }
 
-extern "C" int ltv_qkv_project_backward(const void* x, const void* wpack,
-                                        const void* grad_combined, void* grad_x,
-                                        float* grad_weight, void* workspace,
-                                        size_t workspace_bytes, int M, int C, int H, int D,
-                                        int Da, void* stream) {
+namespace {
+int project_backward_check(const void* x, const void* wpack, const void* grad_combined, int M,
+                           int C, int H, int D, int Da) {
   LTV_REQUIRE(M >= 0 && C > 0 && H > 0 && D > 0 && Da > 0, LTV_ERR_INVALID_ARG, "bad shape");
   LTV_REQUIRE(C % 8 == 0, LTV_ERR_UNSUPPORTED, "C must be a multiple of 8 (C=%d)", C);
-  LTV_REQUIRE(x && wpack && grad_combined && grad_x && grad_weight, LTV_ERR_INVALID_ARG,
-              "null tensor pointer");
+  LTV_REQUIRE(x && wpack && grad_combined, LTV_ERR_INVALID_ARG, "null tensor pointer");
+  LTV_REQUIRE(aligned16(x) && aligned16(wpack) && aligned16(grad_combined), LTV_ERR_INVALID_ARG,
+              "x, wpack and grad_combined must be 16-byte aligned");
+  return LTV_OK;
+}
+}  // namespace
+
+extern "C" int ltv_qkv_project_backward_input(const void* x, const void* wpack,
+                                              const void* grad_combined, void* grad_x, int M,
+                                              int C, int H, int D, int Da, void* stream) {
+  int rc = project_backward_check(x, wpack, grad_combined, M, C, H, D, Da);
+  if (rc) return rc;
+  LTV_REQUIRE(grad_x && aligned16(grad_x), LTV_ERR_INVALID_ARG, "grad_x null or misaligned");
+  if (M == 0) return LTV_OK;
+  const int Fp = ltv_qkv_packed_width(H, D, Da);
+  const int Fvalid = H * (D + Da);
+  // dX[m, c] = sum_f dC[m, f] Wp[f, c]:  i = c (RC: Wp[f * C + c]), j = m (KC: dC[m * Fp + f]);
+  // the padding columns of dC (f >= Fvalid) are never read
+  GemmArgs a;
+  a.P = GemmOperand{reinterpret_cast<const bf16_t*>(wpack), C, C, Fvalid};
+  a.Q = GemmOperand{reinterpret_cast<const bf16_t*>(grad_combined), Fp, M, Fvalid};
+  a.K = Fp;
+  a.k_split = Fp;
+  EpiRowBF16 e{reinterpret_cast<bf16_t*>(grad_x), C, C, M};
+  a.tiles_j = (M + 255) / 256;
+  hipStream_t st = (hipStream_t)stream;
+  if (gemm_tuning().dx == 1 && C % 256 == 0) {
+    a.tiles_i = C / 256;
+    return launch_gemm<256, 256, 2, 4, OP_RC, OP_KC>(a, e, 1, st);
+  }
+  a.tiles_i = (C + 127) / 128;
+  return launch_gemm<128, 256, 2, 2, OP_RC, OP_KC>(a, e, 1, st);
+}
+
+extern "C" int ltv_qkv_project_backward_weight(const void* x, const void* grad_combined,
+                                               float* grad_weight, void* workspace,
+                                               size_t workspace_bytes, int M, int C, int H,
+                                               int D, int Da, void* stream) {
+  int rc = project_backward_check(x, x, grad_combined, M, C, H, D, Da);
+  if (rc) return rc;
+  LTV_REQUIRE(grad_weight, LTV_ERR_INVALID_ARG, "null grad_weight");
   const int Fp = ltv_qkv_packed_width(H, D, Da);
   const int Fvalid = H * (D + Da);
   hipStream_t st = (hipStream_t)stream;
@@ -534,27 +382,26 @@ extern "C" int ltv_qkv_project_backward(const void* x, const void* wpack,
   const size_t need = ltv_qkv_project_backward_workspace_size(M, C, H, D, Da);
   LTV_REQUIRE(workspace && workspace_bytes >= need, LTV_ERR_WORKSPACE,
               "workspace too small: need %zu bytes, got %zu", need, workspace_bytes);
-  // dX[M, C] = dC[M, Fp] . Wp[Fp, C]: B(n = c, k = f) at Wp[f * C + c] (N-contiguous)
-  MfmaArgs a;
-  a.A = reinterpret_cast<const bf16_t*>(grad_combined); a.lda = Fp;
-  a.B = reinterpret_cast<const bf16_t*>(wpack); a.ldb = C;
-  a.C = grad_x; a.ldc = C; a.c_split_stride = 0;
-  a.M = M; a.N = C; a.k_begin = 0; a.k_len = Fp; a.k_valid = Fvalid;
-  a.m_valid = M; a.n_valid = C;
-  a.tiles_m = (M + GBM - 1) / GBM; a.tiles_n = (C + GBN - 1) / GBN;
-  int rc = launch_mfma<false, true, EPI_BF16>(a, 1, st);
-  if (rc) return rc;
-  // dW partials: P_s[f, c] = sum_{m in split s} dC[m, f] X[m, c]
-  const int S = dw_splits(M);
-  const int Fr = (Fp + GBM - 1) / GBM * GBM;
-  MfmaArgs w;
-  w.A = reinterpret_cast<const bf16_t*>(grad_combined); w.lda = Fp;   // A(f, m) at dC[m*Fp + f]
-  w.B = reinterpret_cast<const bf16_t*>(x); w.ldb = C;                // B(c, m) at X[m*C + c]
-  w.C = workspace; w.ldc = C; w.c_split_stride = (int64_t)Fr * C;
-  w.M = Fvalid; w.N = C; w.k_begin = 0; w.k_len = kDwSplitRows; w.k_valid = M;
-  w.m_valid = Fr; w.n_valid = C;
-  w.tiles_m = Fr / GBM; w.tiles_n = (C + GBN - 1) / GBN;
-  rc = launch_mfma<true, true, EPI_F32>(w, S, st);
+  const GemmTuning& tu = gemm_tuning();
+  // dW^T[c, f] = sum_m X[m, c] dC[m, f]:  i = c (RC: X[m * C + c]), j = f (RC: dC[m * Fp + f]),
+  // the reduction over m split into fp32 partials P_s[f][c]
+  const int S = dw_splits(M, tu.dw_split);
+  const int Fr = dw_rows(Fp, tu.dw);
+  GemmArgs a;
+  a.P = GemmOperand{reinterpret_cast<const bf16_t*>(x), C, C, M};
+  a.Q = GemmOperand{reinterpret_cast<const bf16_t*>(grad_combined), Fp, Fp, M};
+  a.K = M;
+  a.k_split = tu.dw_split;
+  EpiRowF32Split e{reinterpret_cast<float*>(workspace), C, (int64_t)Fr * C, C, Fr};
+  if (tu.dw == 1) {
+    a.tiles_i = (C + 255) / 256;
+    a.tiles_j = Fr / 128;
+    rc = launch_gemm<256, 128, 2, 2, OP_RC, OP_RC>(a, e, S, st);
+  } else {
+    a.tiles_i = (C + 127) / 128;
+    a.tiles_j = Fr / 256;
+    rc = launch_gemm<128, 256, 2, 2, OP_RC, OP_RC>(a, e, S, st);
+  }
   if (rc) return rc;
   const int64_t total = (int64_t)Fvalid * C;
   const int blocks = (int)std::min<int64_t>((total + 255) / 256, 8192);
@@ -563,4 +410,16 @@ extern "C" int ltv_qkv_project_backward(const void* x, const void* wpack,
                      (int64_t)Fr * C, H, D, Da, C);
   LTV_LAUNCH_CHECK();
   return LTV_OK;
+}
+
+extern "C" int ltv_qkv_project_backward(const void* x, const void* wpack,
+                                        const void* grad_combined, void* grad_x,
+                                        float* grad_weight, void* workspace,
+                                        size_t workspace_bytes, int M, int C, int H, int D,
+                                        int Da, void* stream) {
+  int rc = ltv_qkv_project_backward_input(x, wpack, grad_combined, grad_x, M, C, H, D, Da,
+                                          stream);
+  if (rc) return rc;
+  return ltv_qkv_project_backward_weight(x, grad_combined, grad_weight, workspace,
+                                         workspace_bytes, M, C, H, D, Da, stream);
 }

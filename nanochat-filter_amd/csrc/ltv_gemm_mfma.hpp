@@ -1,0 +1,297 @@
+// bf16 MFMA GEMM core for gfx950 (fp32 accumulation).
+//
+//   Out(i, j) = sum_k P(i, k) * Q(j, k)
+//
+// i is the output axis that is contiguous in memory (each lane of a
+// v_mfma_f32_32x32x16_bf16 result holds four consecutive i), j the other one.
+// Each operand is stored either K-contiguous (KC: (row, k) at row * ld + k) or
+// row-contiguous (RC: (row, k) at k * ld + row).  Tiles are staged through LDS
+// in the operand's own orientation; KC fragments are read with ds_read_b128,
+// RC fragments with ds_read_b64_tr_b16, whose lane layout (pinned on MI355X):
+// within each 16-lane group, lane i receives element i % 4 of the 8-byte chunks
+// addressed by lanes i / 4, i / 4 + 4, i / 4 + 8, i / 4 + 12.  Addressing lane s
+// at row kb + s / 4, columns 4 (s % 4) .. + 3 of a [k][row] tile therefore hands
+// lane i the column-i values of rows kb .. kb + 3: an MFMA operand fragment.
+//
+// Block tile BI x BJ x 64, WGI x WGJ wavefronts each owning (BI / WGI) x
+// (BJ / WGJ) as 32 x 32 MFMA blocks.  Two LDS stages and one register stage:
+// global loads run a k-tile ahead of the MFMAs, one barrier per k-tile.
+// blockIdx.y selects a split of the reduction range (split-K).
+#pragma once
+
+#include "ltv_device.hpp"
+
+namespace ltv {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef short i16x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+enum OpLayout { OP_KC = 0, OP_RC = 1 };
+
+struct GemmOperand {
+  const bf16_t* p;
+  int64_t ld;
+  int rows;     // rows >= this read as zero
+  int k_valid;  // k >= this reads as zero
+};
+
+struct GemmArgs {
+  GemmOperand P, Q;
+  int K;        // total reduction length
+  int k_split;  // reduction length per split (multiple of 64)
+  int tiles_i, tiles_j;
+};
+
+constexpr int kGemmBK = 64;
+constexpr int kPadKC = 8;   // bf16 of padding per KC row in LDS (bank spread)
+constexpr int kPadRC = 16;  // bf16 of padding per RC row in LDS
+
+template <int R, int L>
+struct LdsTile {
+  static constexpr int kElems = L == OP_KC ? R * (kGemmBK + kPadKC) : kGemmBK * (R + kPadRC);
+};
+
+// zero the bf16 elements of a 16-byte chunk whose index k0 + e >= k_valid
+__device__ __forceinline__ uint4 mask_k_tail(uint4 q, int k0, int k_valid) {
+  if (k0 + 8 <= k_valid) return q;
+  uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    uint32_t keep = 0;
+    if (k0 + 2 * p < k_valid) keep |= 0x0000ffffu;
+    if (k0 + 2 * p + 1 < k_valid) keep |= 0xffff0000u;
+    w[p] &= keep;
+  }
+  return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+// Global -> registers -> LDS staging of one operand tile (R rows x 64 k).
+template <int R, int L, int NT>
+struct TileStage {
+  static constexpr int CH = R * 8 / NT;  // 16-byte chunks per thread
+  static_assert(CH >= 1 && R * 8 % NT == 0, "tile too small for the thread count");
+  uint4 q[CH];
+
+  __device__ __forceinline__ void load(const GemmOperand& op, int row0, int k0, int k_end) {
+    const int kv = min(k_end, op.k_valid);
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+      const int idx = threadIdx.x + c * NT;
+      uint4 v = make_uint4(0u, 0u, 0u, 0u);
+      if (L == OP_KC) {
+        const int row = idx >> 3, kc = (idx & 7) * 8;
+        const int gr = row0 + row, gk = k0 + kc;
+        if (gr < op.rows && gk < kv)
+          v = mask_k_tail(*reinterpret_cast<const uint4*>(op.p + (int64_t)gr * op.ld + gk), gk, kv);
+      } else {
+        const int kk = idx / (R / 8), rc = (idx % (R / 8)) * 8;
+        const int gk = k0 + kk, gr = row0 + rc;
+        if (gk < kv && gr < op.rows)
+          v = *reinterpret_cast<const uint4*>(op.p + (int64_t)gk * op.ld + gr);
+      }
+      q[c] = v;
+    }
+  }
+
+  __device__ __forceinline__ void store(bf16_t* lds) const {
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+      const int idx = threadIdx.x + c * NT;
+      if (L == OP_KC) {
+        const int row = idx >> 3, kc = (idx & 7) * 8;
+        *reinterpret_cast<uint4*>(lds + row * (kGemmBK + kPadKC) + kc) = q[c];
+      } else {
+        const int kk = idx / (R / 8), rc = (idx % (R / 8)) * 8;
+        *reinterpret_cast<uint4*>(lds + kk * (R + kPadRC) + rc) = q[c];
+      }
+    }
+  }
+};
+
+// MFMA operand fragment (8 consecutive k of one row) for k-step ks.
+template <int R, int L>
+__device__ __forceinline__ bf16x8_t read_frag(const bf16_t* lds, int row_base, int ks, int lane) {
+  if (L == OP_KC) {
+    const bf16_t* p = lds + (row_base + (lane & 31)) * (kGemmBK + kPadKC) + ks * 16 + 8 * (lane >> 5);
+    return __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(p));
+  } else {
+    const int g = lane >> 4, s = lane & 15;
+    const int row = row_base + (g & 1) * 16 + 4 * (s & 3);
+    const int k = ks * 16 + (g >> 1) * 8 + (s >> 2);
+    typedef __attribute__((address_space(3))) i16x4_t lds_i16x4;
+    const bf16_t* p0 = lds + k * (R + kPadRC) + row;
+    const bf16_t* p1 = p0 + 4 * (R + kPadRC);
+    const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)p0);
+    const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)p1);
+    typedef short i16x8_t __attribute__((ext_vector_type(8)));
+    const i16x8_t v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    return __builtin_bit_cast(bf16x8_t, v);
+  }
+}
+
+template <int BI, int BJ, int WGI, int WGJ, int PL, int QL, class Epi>
+__global__ void __launch_bounds__(WGI * WGJ * 64)
+gemm_bf16_kernel(const GemmArgs g, const Epi epi) {
+  constexpr int NT = WGI * WGJ * 64;
+  constexpr int WI = BI / WGI, WJ = BJ / WGJ;
+  constexpr int MI = WI / 32, MJ = WJ / 32;
+  static_assert(MI >= 1 && MJ >= 1 && WI % 32 == 0 && WJ % 32 == 0, "bad wave tile");
+  constexpr int PE = LdsTile<BI, PL>::kElems, QE = LdsTile<BJ, QL>::kElems;
+
+  __shared__ __attribute__((aligned(16))) bf16_t lds_p[2][PE];
+  __shared__ __attribute__((aligned(16))) bf16_t lds_q[2][QE];
+
+  // XCD-aware order: workgroup w runs on XCD w % 8; give each XCD a contiguous
+  // run of tiles, i fastest, so tiles sharing a j block share that XCD's L2.
+  const int ntiles = g.tiles_i * g.tiles_j;
+  int tile = blockIdx.x;
+  if (ntiles % 8 == 0) tile = (tile % 8) * (ntiles / 8) + tile / 8;
+  const int ti = tile % g.tiles_i, tj = tile / g.tiles_i;
+  const int i0 = ti * BI, j0 = tj * BJ;
+  const int kb = blockIdx.y * g.k_split;
+  const int ke = min(kb + g.k_split, g.K);
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int wi = wave % WGI, wj = wave / WGI;
+
+  f32x16_t acc[MI][MJ];
+#pragma unroll
+  for (int a = 0; a < MI; ++a)
+#pragma unroll
+    for (int b = 0; b < MJ; ++b)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[a][b][v] = 0.0f;
+
+  TileStage<BI, PL, NT> sp;
+  TileStage<BJ, QL, NT> sq;
+
+  // One k-tile of MFMAs from LDS; operand fragments double-buffered in
+  // registers (the next k-step's reads are in flight while this step's MFMAs
+  // issue), with a scheduling fence per step so at most two sets are live.
+  auto compute = [&](const bf16_t* lp, const bf16_t* lq) {
+    bf16x8_t pf[2][MI], qf[2][MJ];
+#pragma unroll
+    for (int a = 0; a < MI; ++a) pf[0][a] = read_frag<BI, PL>(lp, wi * WI + a * 32, 0, lane);
+#pragma unroll
+    for (int b = 0; b < MJ; ++b) qf[0][b] = read_frag<BJ, QL>(lq, wj * WJ + b * 32, 0, lane);
+#pragma unroll
+    for (int ks = 0; ks < kGemmBK / 16; ++ks) {
+      const int cur = ks & 1;
+      if (ks + 1 < kGemmBK / 16) {
+#pragma unroll
+        for (int a = 0; a < MI; ++a)
+          pf[cur ^ 1][a] = read_frag<BI, PL>(lp, wi * WI + a * 32, ks + 1, lane);
+#pragma unroll
+        for (int b = 0; b < MJ; ++b)
+          qf[cur ^ 1][b] = read_frag<BJ, QL>(lq, wj * WJ + b * 32, ks + 1, lane);
+      }
+#pragma unroll
+      for (int a = 0; a < MI; ++a)
+#pragma unroll
+        for (int b = 0; b < MJ; ++b)
+          acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pf[cur][a], qf[cur][b], acc[a][b], 0,
+                                                              0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
+  // Two LDS stages, one register stage: tile kt + 1 waits in registers while
+  // tile kt is multiplied, then goes to the other LDS stage.
+  const int nk = (ke - kb + kGemmBK - 1) / kGemmBK;
+  if (nk > 0) {
+    sp.load(g.P, i0, kb, ke);
+    sq.load(g.Q, j0, kb, ke);
+    sp.store(lds_p[0]);
+    sq.store(lds_q[0]);
+    if (nk > 1) {
+      sp.load(g.P, i0, kb + kGemmBK, ke);
+      sq.load(g.Q, j0, kb + kGemmBK, ke);
+    }
+  }
+  __syncthreads();
+  for (int kt = 0; kt < nk; ++kt) {
+    const int cur = kt & 1;
+    compute(lds_p[cur], lds_q[cur]);
+    if (kt + 1 < nk) {
+      sp.store(lds_p[cur ^ 1]);
+      sq.store(lds_q[cur ^ 1]);
+      if (kt + 2 < nk) {
+        sp.load(g.P, i0, kb + (kt + 2) * kGemmBK, ke);
+        sq.load(g.Q, j0, kb + (kt + 2) * kGemmBK, ke);
+      }
+    }
+    __syncthreads();
+  }
+
+  // epilogue: lane holds column j = lane % 32 of each 32 x 32 block and rows
+  // 8 (v / 4) + 4 (lane / 32) + v % 4: four consecutive i per group of 4
+#pragma unroll
+  for (int a = 0; a < MI; ++a)
+#pragma unroll
+    for (int b = 0; b < MJ; ++b) {
+      const int j = j0 + wj * WJ + b * 32 + (lane & 31);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int i = i0 + wi * WI + a * 32 + 8 * q + 4 * (lane >> 5);
+        const float4 v = make_float4(acc[a][b][4 * q], acc[a][b][4 * q + 1], acc[a][b][4 * q + 2],
+                                     acc[a][b][4 * q + 3]);
+        epi.store4(i, j, blockIdx.y, v);
+      }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Epilogues.  store4(i, j, split, v): v = Out(i .. i + 3, j).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint2 pack4_bf16(const float4& v) {
+  return make_uint2(cvt_pk_bf16(v.x, v.y), cvt_pk_bf16(v.z, v.w));
+}
+
+// Row-major bf16 output C[j][i] (i contiguous), rows j < j_valid, i < i_valid
+// (i_valid a multiple of 4).
+struct EpiRowBF16 {
+  bf16_t* c;
+  int64_t ldc;
+  int i_valid, j_valid;
+  __device__ __forceinline__ void store4(int i, int j, int, const float4& v) const {
+    if (i < i_valid && j < j_valid)
+      *reinterpret_cast<uint2*>(c + (int64_t)j * ldc + i) = pack4_bf16(v);
+  }
+};
+
+// Row-major fp32 split-K partials C[split][j][i].
+struct EpiRowF32Split {
+  float* c;
+  int64_t ldc, split_stride;
+  int i_valid, j_valid;
+  __device__ __forceinline__ void store4(int i, int j, int split, const float4& v) const {
+    if (i < i_valid && j < j_valid)
+      *reinterpret_cast<float4*>(c + (int64_t)split * split_stride + (int64_t)j * ldc + i) = v;
+  }
+};
+
+// Projection output, i = packed feature n, j = token m = b T + t:
+//   n <  H D : value channel d = n % D of head h = n / D ->
+//              values[((b H + h) T + t) D + d]           (head-major, bf16)
+//   n >= H D : logit column n - H D ->  logits[m Lp + n - H D] (row-major, bf16)
+// D and Lp are multiples of 4, so four consecutive n stay in one head / row.
+struct EpiProjectHM {
+  bf16_t* values;
+  bf16_t* logits;
+  int H, D, T, Lp, n_logit_end, m_valid;
+  __device__ __forceinline__ void store4(int n, int m, int, const float4& v) const {
+    if (m >= m_valid) return;
+    const int HD = H * D;
+    if (n < HD) {
+      const int h = n / D, d = n - h * D;
+      const int b = m / T, t = m - b * T;
+      *reinterpret_cast<uint2*>(values + (((int64_t)b * H + h) * T + t) * D + d) = pack4_bf16(v);
+    } else if (n < n_logit_end) {
+      *reinterpret_cast<uint2*>(logits + (int64_t)m * Lp + (n - HD)) = pack4_bf16(v);
+    }
+  }
+};
+
+}  // namespace ltv

@@ -68,16 +68,24 @@ SIGNATURES = {
          _c_vp],
     ),
     "ltv_qkv_packed_width": (_c_int, [_c_int, _c_int, _c_int]),
+    "ltv_qkv_logit_width": (_c_int, [_c_int, _c_int]),
     "ltv_qkv_pack_weight": (
         _c_int, [_c_int, _c_vp, _c_vp, _c_int, _c_int, _c_int, _c_int, _c_vp]),
     "ltv_qkv_project_forward": (
-        _c_int, [_c_vp, _c_vp, _c_vp, _c_int, _c_int, _c_int, _c_vp]),
+        _c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
+                 _c_vp]),
     "ltv_qkv_project_backward_workspace_size": (
         _c_sz, [_c_int, _c_int, _c_int, _c_int, _c_int]),
     "ltv_qkv_project_backward": (
         _c_int,
         [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_sz, _c_int, _c_int, _c_int, _c_int,
          _c_int, _c_vp],
+    ),
+    "ltv_qkv_project_backward_input": (
+        _c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_int, _c_int, _c_int, _c_int, _c_int, _c_vp]),
+    "ltv_qkv_project_backward_weight": (
+        _c_int,
+        [_c_vp, _c_vp, _c_vp, _c_vp, _c_sz, _c_int, _c_int, _c_int, _c_int, _c_int, _c_vp],
     ),
 }
 

@@ -8,9 +8,10 @@ of a contiguous (B, H, T, D) buffer.
 
 dtype policy (reference ``:24-49``): the filter computes in float32 when autocast
 asks for float32, otherwise in the dtype of ``x``.
-  * bf16: the fast path -- ``nanochat_amd::qkv_project`` (bf16 MFMA with fp32
-    accumulation, the fp32 master weight cast to bf16 on the fly) writes values
-    and logits straight into the layout ``nanochat_amd::hm_scan`` reads.
+  * bf16: the fast path -- ``nanochat_amd::qkv_filter``: the bf16 MFMA
+    projection (fp32 accumulation, the fp32 master weight cast to bf16 on the
+    fly) writes values and logits straight into the head-major layout the
+    scan streams, forward and backward in two fused ops.
   * fp32: the reference-layout ops ``fused_linear_transpose`` (B, F, T) and the
     ``nanochat_cuda`` scan op read through the transposed (B, T, F) view,
     exactly the reference's dataflow.
@@ -55,19 +56,15 @@ class LtvCudaFusedConcatHeadMajorRegisterCastBlellochScanQkvFilter(
         return self._forward_fp32(x, inits)
 
     def _forward_bf16(self, x, inits):
-        H, D, Da = self.total_active_heads, self.head_dim, self.num_alpha_groups
-        combined, _ = torch.ops.nanochat_amd.qkv_project(
-            x.to(torch.bfloat16).contiguous(), self.c.weight, H, D, Da
-        )
-        hq, hk, hv = torch.ops.nanochat_amd.hm_scan(
-            combined,
+        hq, hk, hv, _, _, _ = torch.ops.nanochat_amd.qkv_filter(
+            x.to(torch.bfloat16).contiguous(),
+            self.c.weight,
             inits.to(dtype=torch.bfloat16).contiguous(),
             self.logit_bias.float().contiguous(),
             self.n_head,
             self.n_kv_head,
-            Da,
+            self.num_alpha_groups,
             self.r,
-            True,
         )
         return hq.transpose(1, 2), hk.transpose(1, 2), hv.transpose(1, 2)
 
@@ -90,6 +87,4 @@ class LtvCudaFusedConcatHeadMajorRegisterCastBlellochScanQkvFilter(
             _R_ITEMS_BACKWARD,
             True,  # use_sigmoid
         )
-        if x.dtype != torch.float32:
-            hq, hk, hv = hq.to(x.dtype), hk.to(x.dtype), hv.to(x.dtype)
         return hq.transpose(1, 2), hk.transpose(1, 2), hv.transpose(1, 2)

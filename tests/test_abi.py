@@ -47,14 +47,18 @@ def test_abi_version_and_host_only_queries():
     if not os.path.exists(N.LIB_PATH):
         pytest.skip("library not built")
     lib = N.load()
-    assert lib.ltv_abi_version() == 1
-    # d12: 18 heads x (128 + 1) = 2322 -> padded to a multiple of 64
-    assert lib.ltv_qkv_packed_width(18, 128, 1) == 2368
+    assert lib.ltv_abi_version() == 2
+    # d12: 18 heads x (128 + 1) = 2322 -> padded to a multiple of 128; 18 logits -> 24
+    assert lib.ltv_qkv_packed_width(18, 128, 1) == 2432
+    assert lib.ltv_qkv_logit_width(18, 1) == 24
     assert lib.ltv_hm_scan_backward_workspace_size(1, 32, 1024, 6, 6, 1, 128) >= 32 * 18 * 4
     assert lib.ltv_qkv_project_backward_workspace_size(32768, 768, 18, 128, 1) > 0
     # argument errors are reported without touching a device
-    rc = lib.ltv_qkv_project_forward(None, None, None, 16, 12, 64, None)
-    assert rc == 2 and "multiples of 8" in N.last_error()
+    rc = lib.ltv_qkv_project_forward(None, None, None, None, 2, 8, 12, 3, 64, 1, None)
+    assert rc == 2 and "multiple of 8" in N.last_error()
+    rc = lib.ltv_hm_scan_forward(7, None, None, None, None, None, None, None, None, None, None,
+                                 None, 1, 1, 1, 1, 1, 1, 1, None)
+    assert rc == 1
 
 
 def test_ops_import_without_gpu():
@@ -62,7 +66,8 @@ def test_ops_import_without_gpu():
     import nanochat_amd.ops  # noqa: F401
     assert hasattr(torch.ops.nanochat_cuda,
                    "ltv_fused_concat_head_major_register_cast_blelloch_scan_cuda_op")
-    assert hasattr(torch.ops.nanochat_amd, "hm_scan")
+    assert hasattr(torch.ops.nanochat_amd, "qkv_filter")
+    assert hasattr(torch.ops.nanochat_amd, "qkv_filter_backward")
 
 
 def test_product_path_refuses_cpu_tensors():
@@ -70,5 +75,7 @@ def test_product_path_refuses_cpu_tensors():
     import nanochat_amd.ops  # noqa: F401
     x = torch.zeros(1, 2, 8, dtype=torch.bfloat16)
     w = torch.zeros(2 * (8 + 1) * 3, 8)
-    with pytest.raises(Exception):
-        torch.ops.nanochat_amd.qkv_project(x, w, 6, 8, 1)
+    inits = torch.zeros(1, 6, 8, dtype=torch.bfloat16)
+    bias = torch.zeros(6, 1)
+    with pytest.raises(RuntimeError, match="GPU tensors"):
+        torch.ops.nanochat_amd.qkv_filter(x, w, inits, bias, 2, 2, 1, 8)

@@ -69,35 +69,56 @@ def _bf(t):
     (2, 256, 768, 6, 6, 128, 1),   # d12 widths
     (1, 100, 64, 1, 1, 16, 2),     # ragged M, small heads
     (3, 33, 128, 2, 1, 64, 64),    # per-channel gates (r = 1)
+    (1, 300, 256, 3, 0, 12, 4),    # head width not a multiple of 8, no kv heads
 ])
 def test_qkv_project_fast_path(B, T, C, NH, NKVH, D, Da):
-    ops = _ops()
+    """bf16 MFMA projection: head-major values and row-major logits forward;
+    grad_x and fp32 grad_weight (parameter row order) backward."""
+    from nanochat_amd.ops import ltv_hm_fast as F_
     H = NH + 2 * NKVH
     F = H * (D + Da)
+    Fp, Lp = F_.packed_width(H, D, Da), F_.logit_width(H, Da)
     g = torch.Generator().manual_seed(T + C)
     x = torch.randn(B, T, C, generator=g).to(torch.bfloat16)
     w = torch.randn(F, C, generator=g) / C ** 0.5  # fp32 master, cast to bf16 by the op
-    xd = x.to(DEV).requires_grad_(True)
-    wd = w.to(DEV).requires_grad_(True)
-    comb, wpack = ops.nanochat_amd.qkv_project(xd, wd, H, D, Da)
-    Fp = comb.shape[2]
-    assert Fp % 64 == 0 and Fp >= F and comb.dtype == torch.bfloat16
+    values, logits, wpack = F_.project(x.to(DEV), w.to(DEV), H, D, Da)
+    assert values.shape == (B, H, T, D) and logits.shape == (B, T, Lp)
 
-    ref = _bf(x) @ _bf(w).T  # (B, T, F) in the interleaved order, float64
-    ref4 = ref.view(B, T, H, D + Da)
-    want = torch.zeros(B, T, Fp, dtype=torch.float64)
-    want[..., : H * D] = ref4[..., :D].reshape(B, T, H * D)
-    want[..., H * D: H * D + H * Da] = ref4[..., D:].reshape(B, T, H * Da)
-    assert_close(np_of(comb), want.numpy(), 2e-2, "combined")
+    ref = (_bf(x) @ _bf(w).T).view(B, T, H, D + Da)  # interleaved order, float64
+    assert_close(np_of(values), ref[..., :D].permute(0, 2, 1, 3).numpy(), 2e-2, "values")
+    assert_close(np_of(logits)[..., : H * Da], ref[..., D:].reshape(B, T, H * Da).numpy(), 2e-2,
+                 "logits")
 
     gc = torch.randn(B, T, Fp, generator=g).to(torch.bfloat16)
-    gc[..., H * (D + Da):] = float("nan")  # padding columns must be ignored
-    comb.backward(gc.to(DEV))
-    gc_i = torch.cat([gc[..., : H * D].view(B, T, H, D), gc[..., H * D: H * (D + Da)].view(B, T, H, Da)],
+    gc[..., F:] = float("nan")  # padding columns must be ignored
+    gx, gw = F_.project_backward(x.to(DEV), wpack, gc.to(DEV), H, D, Da)
+    gc_i = torch.cat([gc[..., : H * D].view(B, T, H, D), gc[..., H * D: F].view(B, T, H, Da)],
                      dim=-1).reshape(B, T, F).double()
     want_gx = gc_i @ _bf(w)
     want_gw = torch.einsum("btf,btc->fc", gc_i, _bf(x))
-    assert torch.isfinite(xd.grad).all() and torch.isfinite(wd.grad).all()
-    assert wd.grad.dtype == torch.float32
-    assert_close(np_of(xd.grad), want_gx.numpy(), 2e-2, "grad_x")
-    assert_close(np_of(wd.grad), want_gw.numpy(), 2e-2, "grad_weight")
+    assert torch.isfinite(gx).all() and torch.isfinite(gw).all()
+    assert gw.dtype == torch.float32
+    assert_close(np_of(gx), want_gx.numpy(), 2e-2, "grad_x")
+    assert_close(np_of(gw), want_gw.numpy(), 2e-2, "grad_weight")
+
+
+@pytest.mark.parametrize("M", [1, 255, 257, 8192 + 64])
+def test_projection_ragged_token_counts(M):
+    """Token counts that leave partial 256-row tiles and partial dW splits."""
+    from nanochat_amd.ops import ltv_hm_fast as F_
+    H, D, Da, C = 3, 128, 1, 256
+    F = H * (D + Da)
+    Fp = F_.packed_width(H, D, Da)
+    g = torch.Generator().manual_seed(M)
+    x = torch.randn(1, M, C, generator=g).to(torch.bfloat16)
+    w = torch.randn(F, C, generator=g) / C ** 0.5
+    values, logits, wpack = F_.project(x.to(DEV), w.to(DEV), H, D, Da)
+    ref = (_bf(x) @ _bf(w).T).view(1, M, H, D + Da)
+    assert_close(np_of(values), ref[..., :D].permute(0, 2, 1, 3).numpy(), 2e-2, "values")
+    gc = torch.randn(1, M, Fp, generator=g).to(torch.bfloat16)
+    gx, gw = F_.project_backward(x.to(DEV), wpack, gc.to(DEV), H, D, Da)
+    gc_i = torch.cat([gc[..., : H * D].view(1, M, H, D), gc[..., H * D: F].view(1, M, H, Da)],
+                     dim=-1).reshape(1, M, F).double()
+    assert_close(np_of(gx), (gc_i @ _bf(w)).numpy(), 2e-2, "grad_x")
+    assert_close(np_of(gw), torch.einsum("btf,btc->fc", gc_i, _bf(x)).numpy(), 2e-2,
+                 "grad_weight")
