@@ -166,19 +166,42 @@ int launch_simt(int dtype_in, int dtype_out, const SimtArgs& a, int batches, hip
   return LTV_OK;
 }
 
+// Compute units of the current device (cached per device).
+int device_cu_count() {
+  static int counts[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (counts[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        n <= 0)
+      n = 256;
+    counts[dev] = n;
+  }
+  return counts[dev];
+}
+
+// Persistent launch: one workgroup per compute unit (the tiles use most of the
+// LDS), or fewer when there are fewer work items.
 template <int BI, int BJ, int WGI, int WGJ, int PL, int QL, class Epi>
-int launch_gemm(const GemmArgs& a, const Epi& e, int splits, hipStream_t st) {
-  dim3 grid(a.tiles_i * a.tiles_j, splits);
-  hipLaunchKernelGGL((gemm_bf16_kernel<BI, BJ, WGI, WGJ, PL, QL, Epi>), grid, dim3(WGI * WGJ * 64),
-                     0, st, a, e);
+int launch_gemm(GemmArgs a, const Epi& e, int splits, hipStream_t st) {
+  a.splits = splits;
+  const int total = a.tiles_i * a.tiles_j * splits;
+  if (total == 0) return LTV_OK;
+  int grid = device_cu_count();
+  if (total < grid) grid = total;
+  hipLaunchKernelGGL((gemm_bf16_kernel<BI, BJ, WGI, WGJ, PL, QL, Epi>), dim3(grid),
+                     dim3(WGI * WGJ * 64), 0, st, a, e);
   LTV_LAUNCH_CHECK();
   return LTV_OK;
 }
 
 // Tile variants of the three projection GEMMs, overridable for tuning with
 // LTV_GEMM_CFG="fwd,dx,dw,dw_split_rows" (variant indices, rows per dW split).
+// Defaults measured on MI355X at d12: 256 x 256 tiles with 8 wavefronts for the
+// forward and dX, 128 x 256 tiles with 8192-row splits for dW.
 struct GemmTuning {
-  int fwd = 0, dx = 0, dw = 0, dw_split = 4096;
+  int fwd = 1, dx = 1, dw = 0, dw_split = 8192;
   GemmTuning() {
     if (const char* e = getenv("LTV_GEMM_CFG")) {
       int a = 0, b = 0, c = 0, d = 4096;

@@ -15,8 +15,9 @@
 //
 // Block tile BI x BJ x 64, WGI x WGJ wavefronts each owning (BI / WGI) x
 // (BJ / WGJ) as 32 x 32 MFMA blocks.  Two LDS stages and one register stage:
-// global loads run a k-tile ahead of the MFMAs, one barrier per k-tile.
-// blockIdx.y selects a split of the reduction range (split-K).
+// global loads run a k-tile ahead of the MFMAs, one barrier per k-tile.  The
+// reduction range can be split (split-K); the kernel is persistent over all
+// (tile, split) work items.
 #pragma once
 
 #include "ltv_device.hpp"
@@ -40,12 +41,16 @@ struct GemmArgs {
   GemmOperand P, Q;
   int K;        // total reduction length
   int k_split;  // reduction length per split (multiple of 64)
+  int splits;   // number of splits of the reduction
   int tiles_i, tiles_j;
 };
 
 constexpr int kGemmBK = 64;
 constexpr int kPadKC = 8;   // bf16 of padding per KC row in LDS (bank spread)
-constexpr int kPadRC = 16;  // bf16 of padding per RC row in LDS
+// bf16 of padding per RC row in LDS: with a 64-byte row offset modulo 256
+// bytes, the four rows one 16-lane group of ds_read_b64_tr_b16 touches land in
+// four disjoint 16-bank windows
+constexpr int kPadRC = 32;
 
 template <int R, int L>
 struct LdsTile {
@@ -130,6 +135,48 @@ __device__ __forceinline__ bf16x8_t read_frag(const bf16_t* lds, int row_base, i
   }
 }
 
+// Position in a workgroup's stream of (output tile, split, k-tile) steps.
+// Workgroup w takes work items w, w + G, w + 2G, ... (G = gridDim.x); when the
+// item count and G are multiples of 8, item u is remapped so that all items of
+// one XCD (w % 8) form a contiguous range, i fastest: tiles that share a j
+// block then share that XCD's L2.
+struct GemmCursor {
+  int k, kt, nk;  // item ordinal of this workgroup, k-tile within the item, k-tiles in it
+  int i0, j0, kb, ke, split;
+  bool valid;
+};
+
+template <int BI, int BJ>
+__device__ __forceinline__ void gemm_decode(const GemmArgs& g, GemmCursor& c) {
+  const int ntiles = g.tiles_i * g.tiles_j;
+  const int total = ntiles * g.splits;
+  int u = blockIdx.x + c.k * gridDim.x;
+  c.valid = u < total;
+  if (!c.valid) return;
+  if (total % 8 == 0 && gridDim.x % 8 == 0) u = (u % 8) * (total / 8) + u / 8;
+  const int split = u / ntiles;
+  const int tile = u - split * ntiles;
+  const int ti = tile % g.tiles_i, tj = tile / g.tiles_i;
+  c.i0 = ti * BI;
+  c.j0 = tj * BJ;
+  c.split = split;
+  c.kb = split * g.k_split;
+  c.ke = min(c.kb + g.k_split, g.K);
+  c.nk = (c.ke - c.kb + kGemmBK - 1) / kGemmBK;
+  c.kt = 0;
+}
+
+template <int BI, int BJ>
+__device__ __forceinline__ void gemm_advance(const GemmArgs& g, GemmCursor& c) {
+  if (++c.kt >= c.nk) {
+    ++c.k;
+    gemm_decode<BI, BJ>(g, c);
+  }
+}
+
+// Persistent: gridDim.x workgroups walk all (tile, split) items as one
+// continuous stream of k-tiles, so the loads of the next tile are in flight
+// while the current tile's epilogue stores drain.  Every item needs >= 1 k-tile.
 template <int BI, int BJ, int WGI, int WGJ, int PL, int QL, class Epi>
 __global__ void __launch_bounds__(WGI * WGJ * 64)
 gemm_bf16_kernel(const GemmArgs g, const Epi epi) {
@@ -141,16 +188,6 @@ gemm_bf16_kernel(const GemmArgs g, const Epi epi) {
 
   __shared__ __attribute__((aligned(16))) bf16_t lds_p[2][PE];
   __shared__ __attribute__((aligned(16))) bf16_t lds_q[2][QE];
-
-  // XCD-aware order: workgroup w runs on XCD w % 8; give each XCD a contiguous
-  // run of tiles, i fastest, so tiles sharing a j block share that XCD's L2.
-  const int ntiles = g.tiles_i * g.tiles_j;
-  int tile = blockIdx.x;
-  if (ntiles % 8 == 0) tile = (tile % 8) * (ntiles / 8) + tile / 8;
-  const int ti = tile % g.tiles_i, tj = tile / g.tiles_i;
-  const int i0 = ti * BI, j0 = tj * BJ;
-  const int kb = blockIdx.y * g.k_split;
-  const int ke = min(kb + g.k_split, g.K);
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -197,49 +234,58 @@ gemm_bf16_kernel(const GemmArgs g, const Epi epi) {
     }
   };
 
-  // Two LDS stages, one register stage: tile kt + 1 waits in registers while
-  // tile kt is multiplied, then goes to the other LDS stage.
-  const int nk = (ke - kb + kGemmBK - 1) / kGemmBK;
-  if (nk > 0) {
-    sp.load(g.P, i0, kb, ke);
-    sq.load(g.Q, j0, kb, ke);
+  auto load = [&](const GemmCursor& c) {
+    const int k0 = c.kb + c.kt * kGemmBK;
+    sp.load(g.P, c.i0, k0, c.ke);
+    sq.load(g.Q, c.j0, k0, c.ke);
+  };
+
+  // Two LDS stages, one register stage: the step after next waits in
+  // registers while the current step is multiplied.
+  GemmCursor lc, cc;
+  lc.k = 0;
+  gemm_decode<BI, BJ>(g, lc);
+  cc = lc;
+  if (lc.valid) {
+    load(lc);
     sp.store(lds_p[0]);
     sq.store(lds_q[0]);
-    if (nk > 1) {
-      sp.load(g.P, i0, kb + kGemmBK, ke);
-      sq.load(g.Q, j0, kb + kGemmBK, ke);
-    }
+    gemm_advance<BI, BJ>(g, lc);
+    if (lc.valid) load(lc);
   }
   __syncthreads();
-  for (int kt = 0; kt < nk; ++kt) {
-    const int cur = kt & 1;
-    compute(lds_p[cur], lds_q[cur]);
-    if (kt + 1 < nk) {
-      sp.store(lds_p[cur ^ 1]);
-      sq.store(lds_q[cur ^ 1]);
-      if (kt + 2 < nk) {
-        sp.load(g.P, i0, kb + (kt + 2) * kGemmBK, ke);
-        sq.load(g.Q, j0, kb + (kt + 2) * kGemmBK, ke);
-      }
+  int stage = 0;
+  while (cc.valid) {
+    compute(lds_p[stage], lds_q[stage]);
+    if (lc.valid) {
+      sp.store(lds_p[stage ^ 1]);
+      sq.store(lds_q[stage ^ 1]);
+      gemm_advance<BI, BJ>(g, lc);
+      if (lc.valid) load(lc);
     }
+    if (cc.kt == cc.nk - 1) {
+      // epilogue: lane holds column j = lane % 32 of each 32 x 32 block and rows
+      // 8 (v / 4) + 4 (lane / 32) + v % 4: four consecutive i per group of 4
+#pragma unroll
+      for (int a = 0; a < MI; ++a)
+#pragma unroll
+        for (int b = 0; b < MJ; ++b) {
+          const int j = cc.j0 + wj * WJ + b * 32 + (lane & 31);
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int i = cc.i0 + wi * WI + a * 32 + 8 * q + 4 * (lane >> 5);
+            const float4 v = make_float4(acc[a][b][4 * q], acc[a][b][4 * q + 1],
+                                         acc[a][b][4 * q + 2], acc[a][b][4 * q + 3]);
+            epi.store4(i, j, cc.split, v);
+          }
+#pragma unroll
+          for (int v = 0; v < 16; ++v) acc[a][b][v] = 0.0f;
+        }
+    }
+    gemm_advance<BI, BJ>(g, cc);
     __syncthreads();
+    stage ^= 1;
   }
-
-  // epilogue: lane holds column j = lane % 32 of each 32 x 32 block and rows
-  // 8 (v / 4) + 4 (lane / 32) + v % 4: four consecutive i per group of 4
-#pragma unroll
-  for (int a = 0; a < MI; ++a)
-#pragma unroll
-    for (int b = 0; b < MJ; ++b) {
-      const int j = j0 + wj * WJ + b * 32 + (lane & 31);
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int i = i0 + wi * WI + a * 32 + 8 * q + 4 * (lane >> 5);
-        const float4 v = make_float4(acc[a][b][4 * q], acc[a][b][4 * q + 1], acc[a][b][4 * q + 2],
-                                     acc[a][b][4 * q + 3]);
-        epi.store4(i, j, blockIdx.y, v);
-      }
-    }
 }
 
 // ---------------------------------------------------------------------------
