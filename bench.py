@@ -33,6 +33,8 @@ import time
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "nanochat-filter_amd"))
 
+COPY_CAL_BYTES = 256 << 20
+
 # published MI355X peaks
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
@@ -107,6 +109,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="after the timed region, run a plain device copy of 256 MiB five times "
+                         "(the known-size reference for rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported in this build "
@@ -153,6 +158,13 @@ def main():
             step()
         torch.cuda.synchronize()
         elapsed = time.perf_counter() - t0
+
+    if args.calibrate_copy:
+        src = torch.empty(COPY_CAL_BYTES, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
 
     durs = rec.durations_ms()
     work = algorithmic_work()

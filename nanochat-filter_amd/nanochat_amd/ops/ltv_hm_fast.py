@@ -232,13 +232,17 @@ def _filter_setup(ctx, inputs, output):
     ctx.save_for_backward(x, wpack, values, logits, inits, logit_bias, q, k, v)
     ctx.args = (NH, NKVH, Da, r)
     ctx.weight_dtype = weight.dtype
+    # values / logits / wpack are internal outputs: no zero gradients for them
+    ctx.set_materialize_grads(False)
 
 
 def _filter_backward(ctx, gq, gk, gv, g_values, g_logits, g_wpack):
     x, wpack, values, logits, inits, logit_bias, q, k, v = ctx.saved_tensors
-    gq = torch.zeros_like(q) if gq is None else gq.contiguous()
-    gk = torch.zeros_like(k) if gk is None else gk.contiguous()
-    gv = torch.zeros_like(v) if gv is None else gv.contiguous()
+    # upstream grads keep their strides (typically the transposed (B, T, H, D)
+    # views): the scan backward reads any layout, 16-byte vectors along D
+    gq = torch.zeros_like(q) if gq is None else gq
+    gk = torch.zeros_like(k) if gk is None else gk
+    gv = torch.zeros_like(v) if gv is None else gv
     gx, gw, gi, gb = torch.ops.nanochat_amd.qkv_filter_backward(
         x, wpack, values, logits, inits, logit_bias, q, k, v, gq, gk, gv, *ctx.args)
     if ctx.weight_dtype != torch.float32:
