@@ -64,6 +64,18 @@ def algorithmic_work():
     }
 
 
+def profiled_traffic(span: str):
+    """HBM bytes per launch of a kernel span, from the committed rocprofv3 FETCH_SIZE /
+    WRITE_SIZE summary of this workload (copy-calibrated); None if not profiled."""
+    path = os.path.join(ROOT, "profiles", "d12_traffic.json")
+    try:
+        with open(path) as fh:
+            d = json.load(fh)
+        return d["bytes_per_launch"].get(span), d["source"]
+    except (OSError, ValueError, KeyError):
+        return None, None
+
+
 def cpu_baseline(seconds_target: float = 10.0):
     """Time the oracle's forward+backward on a sample of the workload."""
     import numpy as np
@@ -181,8 +193,10 @@ def main():
                          "frac": round(ach / peak, 4), "work_per_launch": amount}
     dominant = max(kernels, key=lambda k: kernels[k]["avg_us"] * kernels[k]["launches"])
     dk_ = kernels[dominant]
+    traffic, traffic_src = profiled_traffic(dominant)
     roofline = {"kernel": dominant, "bound": dk_["bound"], "achieved": dk_["achieved"],
-                "peak": dk_["peak"], "unit": dk_["unit"], "frac": dk_["frac"], "traffic": None}
+                "peak": dk_["peak"], "unit": dk_["unit"], "frac": dk_["frac"], "traffic": traffic,
+                "traffic_source": traffic_src}
     scan_time = kernels.get("scan_fwd", {}).get("avg_us", 0) + kernels.get("scan_bwd", {}).get("avg_us", 0)
     scan_bytes = work["scan_fwd"][1] + work["scan_bwd"][1]
     scan_gbs = scan_bytes / (scan_time * 1e-6) / 1e9 if scan_time else None
