@@ -175,7 +175,9 @@ int ltv_linear_transpose_backward(int dtype, const void* x, const void* weight,
  *
  * ltv_qkv_project_backward: grad_combined (B T, Fp) bf16 row-major with column
  *   h D + d = gradient of value channel d of head h and column H D + h Da + j =
- *   gradient of logit j (columns >= F are ignored) ->
+ *   gradient of logit j (columns >= F are scratch: their values are ignored and
+ *   the grad_x computation may overwrite columns F .. round_up(F, 8) - 1 with
+ *   zeros, since it reads grad_combined in 8-column chunks) ->
  *   grad_x (B T, C) bf16 and grad_weight (F, C) fp32 in the parameter's
  *   interleaved row order (both overwritten; deterministic).
  * Counterpart in the reference: fused_linear_transpose forward/backward as used
@@ -189,7 +191,7 @@ int ltv_qkv_pack_weight(int weight_dtype, const void* weight, void* wpack, int H
 int ltv_qkv_project_forward(const void* x, const void* wpack, void* values, void* logits, int B,
                             int T, int C, int H, int D, int Da, void* stream);
 size_t ltv_qkv_project_backward_workspace_size(int M, int C, int H, int D, int Da);
-int ltv_qkv_project_backward(const void* x, const void* wpack, const void* grad_combined,
+int ltv_qkv_project_backward(const void* x, const void* wpack, void* grad_combined,
                              void* grad_x, float* grad_weight, void* workspace,
                              size_t workspace_bytes, int M, int C, int H, int D, int Da,
                              void* stream);
@@ -197,7 +199,7 @@ int ltv_qkv_project_backward(const void* x, const void* wpack, const void* grad_
  * (one GEMM launch) and grad_weight (split-K GEMM plus a fixed-order reduction;
  * needs the workspace).  They mirror the grad_x and grad_weight loops of
  * cpp_ewma/src/fused_linear_transpose_backward.cu:67-94 and :96-131. */
-int ltv_qkv_project_backward_input(const void* x, const void* wpack, const void* grad_combined,
+int ltv_qkv_project_backward_input(const void* x, const void* wpack, void* grad_combined,
                                    void* grad_x, int M, int C, int H, int D, int Da,
                                    void* stream);
 int ltv_qkv_project_backward_weight(const void* x, const void* grad_combined,

@@ -16,7 +16,7 @@
 
 #include "ltv_device.hpp"
 #include "ltv_abi_internal.hpp"
-#include "ltv_gemm_mfma.hpp"
+#include "ltv_gemm_dma.hpp"
 
 #include <stdio.h>
 #include <stdlib.h>
@@ -48,6 +48,15 @@ __global__ void pack_weight_kernel(const TW* __restrict__ w, bf16_t* __restrict_
     }
     wp[i] = (bf16_t)f32_to_bf16_bits(v);
   }
+}
+
+// zero columns [c0, c1) of a row-major bf16 (rows, ld) buffer
+__global__ void zero_cols_kernel(bf16_t* __restrict__ p, int rows, int64_t ld, int c0, int c1) {
+  const int w = c1 - c0;
+  const int64_t total = (int64_t)rows * w;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x)
+    p[(i / w) * ld + c0 + (i % w)] = 0;
 }
 
 // grad_weight[param row, c] = sum_s partial[s][packed row, c]  (fixed order)
@@ -183,8 +192,16 @@ int device_cu_count() {
 
 // Persistent launch: one workgroup per compute unit (the tiles use most of the
 // LDS), or fewer when there are fewer work items.
+// Elements an operand spans: rows x k for K-contiguous (ld = row pitch), k x rows for
+// row-contiguous (ld = k pitch).
+inline int64_t operand_span(const GemmOperand& o, int K, int layout) {
+  return layout == OP_KC ? (int64_t)o.rows * o.ld : (int64_t)K * o.ld;
+}
+
 template <int BI, int BJ, int WGI, int WGJ, int PL, int QL, class Epi>
 int launch_gemm(GemmArgs a, const Epi& e, int splits, hipStream_t st) {
+  LTV_REQUIRE(operand_span(a.P, a.K, PL) < (1ll << 31) && operand_span(a.Q, a.K, QL) < (1ll << 31),
+              LTV_ERR_UNSUPPORTED, "GEMM operand spans 2^31 elements or more");
   a.splits = splits;
   const int total = a.tiles_i * a.tiles_j * splits;
   if (total == 0) return LTV_OK;
@@ -196,20 +213,61 @@ int launch_gemm(GemmArgs a, const Epi& e, int splits, hipStream_t st) {
   return LTV_OK;
 }
 
+// Whether the direct-to-LDS kernel takes these operands: spans within its
+// 32-bit offsets, KC reduction ends at 8-element chunks, RC rows in 8-row chunks.
+inline bool dma_ok(const GemmOperand& op, int64_t K, int layout) {
+  if (operand_span(op, K, layout) > kDmaMaxSpan) return false;
+  if (layout == OP_KC) return op.k_valid % 8 == 0 && op.ld % 8 == 0;
+  return op.rows % 8 == 0 && op.ld % 8 == 0;
+}
+
+// Largest output buffer an epilogue of the direct-to-LDS kernel addresses.
+inline int64_t dma_epi_bytes(const EpiRowBF16& e, int) { return (int64_t)e.j_valid * e.ldc * 2; }
+inline int64_t dma_epi_bytes(const EpiRowF32Split& e, int splits) {
+  return (int64_t)splits * e.split_stride * 4;
+}
+inline int64_t dma_epi_bytes(const EpiProjectHM& e, int) {
+  return std::max((int64_t)e.m_valid * e.H * e.D * 2, (int64_t)e.m_valid * e.Lp * 2);
+}
+
+template <class Epi>
+bool dma_usable(const GemmArgs& a, int PL, int QL, const Epi& e, int splits) {
+  return dma_ok(a.P, a.K, PL) && dma_ok(a.Q, a.K, QL) && dma_epi_bytes(e, splits) <= kDmaMaxBytes;
+}
+
+// Same, with the direct-to-LDS kernel.
+template <int BI, int BJ, int WGI, int WGJ, int PL, int QL, class Epi>
+int launch_gemm_dma(GemmArgs a, const Epi& e, int splits, hipStream_t st) {
+  LTV_REQUIRE(dma_usable(a, PL, QL, e, splits), LTV_ERR_UNSUPPORTED,
+              "operands not supported by the direct-to-LDS GEMM");
+  a.splits = splits;
+  const int total = a.tiles_i * a.tiles_j * splits;
+  if (total == 0) return LTV_OK;
+  int grid = device_cu_count();
+  if (total < grid) grid = total;
+  hipLaunchKernelGGL((gemm_dma_kernel<BI, BJ, WGI, WGJ, PL, QL, Epi>), dim3(grid),
+                     dim3(WGI * WGJ * 64), 0, st, a, e);
+  LTV_LAUNCH_CHECK();
+  return LTV_OK;
+}
+
 // Tile variants of the three projection GEMMs, overridable for tuning with
-// LTV_GEMM_CFG="fwd,dx,dw,dw_split_rows" (variant indices, rows per dW split).
+// LTV_GEMM_CFG="fwd,dx,dw,dw_split_rows[,dma]" (variant indices, rows per dW
+// split, 1 = direct-to-LDS kernels).
 // Defaults measured on MI355X at d12: 256 x 256 tiles with 8 wavefronts for the
 // forward and dX, 128 x 256 tiles with 8192-row splits for dW.
 struct GemmTuning {
-  int fwd = 1, dx = 1, dw = 0, dw_split = 8192;
+  int fwd = 1, dx = 1, dw = 0, dw_split = 4096, dma = 1;
   GemmTuning() {
     if (const char* e = getenv("LTV_GEMM_CFG")) {
-      int a = 0, b = 0, c = 0, d = 4096;
-      if (sscanf(e, "%d,%d,%d,%d", &a, &b, &c, &d) == 4 && d > 0 && d % kGemmBK == 0) {
+      int a = 0, b = 0, c = 0, d = 4096, f = 0;
+      const int n = sscanf(e, "%d,%d,%d,%d,%d", &a, &b, &c, &d, &f);
+      if (n >= 4 && d > 0 && d % kGemmBK == 0) {
         fwd = a;
         dx = b;
         dw = c;
         dw_split = d;
+        dma = n == 5 ? f : 1;
       }
     }
   }
@@ -328,10 +386,20 @@ extern "C" int ltv_qkv_project_forward(const void* x, const void* wpack, void* v
   EpiProjectHM e{reinterpret_cast<bf16_t*>(values), reinterpret_cast<bf16_t*>(logits), H, D, T,
                  ltv_qkv_logit_width(H, Da), H * D + H * Da, M};
   hipStream_t st = (hipStream_t)stream;
+  if (gemm_tuning().dma && dma_usable(a, OP_KC, OP_KC, e, 1)) {
+    a.tiles_i = (Fp + 255) / 256;
+    a.tiles_j = (M + 255) / 256;
+    return launch_gemm_dma<256, 256, 2, 4, OP_KC, OP_KC>(a, e, 1, st);
+  }
   if (gemm_tuning().fwd == 1) {
     a.tiles_i = (Fp + 255) / 256;
     a.tiles_j = (M + 255) / 256;
     return launch_gemm<256, 256, 2, 4, OP_KC, OP_KC>(a, e, 1, st);
+  }
+  if (gemm_tuning().fwd == 2) {
+    a.tiles_i = (Fp + 255) / 256;
+    a.tiles_j = (M + 255) / 256;
+    return launch_gemm<256, 256, 2, 2, OP_KC, OP_KC>(a, e, 1, st);
   }
   a.tiles_i = Fp / 128;
   a.tiles_j = (M + 255) / 256;
@@ -362,7 +430,7 @@ int project_backward_check(const void* x, const void* wpack, const void* grad_co
 }  // namespace
 
 extern "C" int ltv_qkv_project_backward_input(const void* x, const void* wpack,
-                                              const void* grad_combined, void* grad_x, int M,
+                                              void* grad_combined, void* grad_x, int M,
                                               int C, int H, int D, int Da, void* stream) {
   int rc = project_backward_check(x, wpack, grad_combined, M, C, H, D, Da);
   if (rc) return rc;
@@ -380,9 +448,32 @@ extern "C" int ltv_qkv_project_backward_input(const void* x, const void* wpack,
   EpiRowBF16 e{reinterpret_cast<bf16_t*>(grad_x), C, C, M};
   a.tiles_j = (M + 255) / 256;
   hipStream_t st = (hipStream_t)stream;
+  if (gemm_tuning().dma) {
+    // the direct-to-LDS loads fetch dC in 8-column chunks: columns up to the
+    // next multiple of 8 past Fvalid are read, so they are set to zero first
+    const int Fv8 = round_up(Fvalid, 8);
+    GemmArgs ad = a;
+    ad.Q.k_valid = Fv8;
+    if (dma_usable(ad, OP_RC, OP_KC, e, 1)) {
+      if (Fv8 > Fvalid) {
+        const int64_t total = (int64_t)M * (Fv8 - Fvalid);
+        const int blocks = (int)std::min<int64_t>((total + 255) / 256, 4096);
+        hipLaunchKernelGGL(zero_cols_kernel, dim3(blocks), dim3(256), 0, st,
+                           reinterpret_cast<bf16_t*>(grad_combined), M,
+                           (int64_t)Fp, Fvalid, Fv8);
+        LTV_LAUNCH_CHECK();
+      }
+      ad.tiles_i = (C + 255) / 256;
+      return launch_gemm_dma<256, 256, 2, 4, OP_RC, OP_KC>(ad, e, 1, st);
+    }
+  }
   if (gemm_tuning().dx == 1 && C % 256 == 0) {
     a.tiles_i = C / 256;
     return launch_gemm<256, 256, 2, 4, OP_RC, OP_KC>(a, e, 1, st);
+  }
+  if (gemm_tuning().dx == 2 && C % 256 == 0) {
+    a.tiles_i = C / 256;
+    return launch_gemm<256, 256, 2, 2, OP_RC, OP_KC>(a, e, 1, st);
   }
   a.tiles_i = (C + 127) / 128;
   return launch_gemm<128, 256, 2, 2, OP_RC, OP_KC>(a, e, 1, st);
@@ -416,10 +507,18 @@ extern "C" int ltv_qkv_project_backward_weight(const void* x, const void* grad_c
   a.K = M;
   a.k_split = tu.dw_split;
   EpiRowF32Split e{reinterpret_cast<float*>(workspace), C, (int64_t)Fr * C, C, Fr};
-  if (tu.dw == 1) {
+  if (tu.dma && dma_usable(a, OP_RC, OP_RC, e, S)) {
+    a.tiles_i = (C + 255) / 256;
+    a.tiles_j = (Fr + 255) / 256;
+    rc = launch_gemm_dma<256, 256, 2, 4, OP_RC, OP_RC>(a, e, S, st);
+  } else if (tu.dw == 1) {
     a.tiles_i = (C + 255) / 256;
     a.tiles_j = Fr / 128;
     rc = launch_gemm<256, 128, 2, 2, OP_RC, OP_RC>(a, e, S, st);
+  } else if (tu.dw == 2) {
+    a.tiles_i = (C + 255) / 256;
+    a.tiles_j = Fr / 256;
+    rc = launch_gemm<256, 256, 2, 2, OP_RC, OP_RC>(a, e, S, st);
   } else {
     a.tiles_i = (C + 127) / 128;
     a.tiles_j = Fr / 256;
@@ -436,7 +535,7 @@ extern "C" int ltv_qkv_project_backward_weight(const void* x, const void* grad_c
 }
 
 extern "C" int ltv_qkv_project_backward(const void* x, const void* wpack,
-                                        const void* grad_combined, void* grad_x,
+                                        void* grad_combined, void* grad_x,
                                         float* grad_weight, void* workspace,
                                         size_t workspace_bytes, int M, int C, int H, int D,
                                         int Da, void* stream) {

@@ -1,0 +1,456 @@
+// bf16 MFMA GEMM with direct global -> LDS loads (gfx950 buffer_load ... lds).
+//
+//   Out(i, j) = sum_k P(i, k) * Q(j, k)         (same contract as ltv_gemm_mfma.hpp)
+//
+// The operand tiles never pass through VGPRs: each wavefront issues
+// buffer_load_dwordx4 with the LDS bit, which writes its 64 lanes' 16-byte chunks
+// to 1 KB of LDS at the M0 base.  A k-step is kDmaBK = 64 reduction indices, so
+// every row of a KC operand is fetched as one full 128-byte line: the L2 serves
+// about one request per channel per clock whatever its size, and 64-byte
+// requests halve its throughput.  Two stages (2 x 64 KB for a 256 x 256 tile)
+// double-buffer the k-steps: the loads of step s + 1 are issued before the
+// MFMAs of step s and waited for after them, one barrier per step.
+//
+// LDS layouts (no padding; 16-byte chunks XOR-swizzled so both fragment reads
+// are bank-conflict free):
+//   KC tile [R rows][64 k] (128 B rows): chunk c of row r sits at slot
+//       c ^ ((r >> 1) & 7); any 16 consecutive rows then cover 16 distinct
+//       16-byte bank windows for the ds_read_b128 fragment reads.
+//   RC tile [64 k][R rows] (2R-byte rows): row-chunk c of k-row k sits at slot
+//       c ^ (4 (k & 3)); the 4 k-rows one 16-lane group of ds_read_b64_tr_b16
+//       reads then land in 4 disjoint 64-byte windows.
+// The swizzle is applied on the load side by choosing which global chunk each
+// lane fetches (a lane's LDS destination is fixed by its lane index); the
+// lanes that fill one row still fetch one whole 128-byte line.
+//
+// Chunks past an operand's rows or reduction range are not fetched: the lane
+// gets an offset the buffer range check rejects, which writes zeros to LDS.
+// The wait for a stage is an explicit s_waitcnt vmcnt on this wavefront's own
+// loads followed by s_barrier, so every wavefront's loads into the stage have
+// landed before any wavefront reads it.
+#pragma once
+
+#include "ltv_gemm_mfma.hpp"
+
+namespace ltv {
+
+constexpr int kDmaBK = 64;
+
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+
+// Raw buffer resource (stride 0) over [p, p + bytes): gfx9 word 3 = 0x00020000.
+__device__ __forceinline__ i32x4_t make_buffer_rsrc(const void* p, uint32_t bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(p);
+  i32x4_t r;
+  r[0] = (int)(uint32_t)a;
+  r[1] = (int)(uint32_t)((a >> 32) & 0xffffu);
+  r[2] = (int)bytes;
+  r[3] = 0x00020000;
+  return r;
+}
+
+// One wavefront-wide 16-byte-per-lane load into LDS at lds_base (wave-uniform
+// byte address): lane l's chunk goes to lds_base + 16 l.
+__device__ __forceinline__ void dma16(uint32_t lds_base, i32x4_t rsrc, uint32_t voffset,
+                                      uint32_t soffset) {
+  asm volatile(
+      "s_mov_b32 m0, %0\n\t"
+      "s_nop 4\n\t"
+      "buffer_load_dwordx4 %1, %2, %3 offen lds"
+      :
+      : "s"(lds_base), "v"(voffset), "s"(rsrc), "s"(soffset)
+      : "memory", "m0");
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
+}
+
+// s_waitcnt vmcnt(n) for a wave-uniform runtime n in [LO, HI] (binary dispatch
+// to the immediate forms).
+template <int LO, int HI>
+__device__ __forceinline__ void wait_vmcnt_range(int n) {
+  if constexpr (LO == HI) {
+    wait_vmcnt<LO>();
+  } else {
+    constexpr int MID = (LO + HI) / 2;
+    if (n <= MID)
+      wait_vmcnt_range<LO, MID>(n);
+    else
+      wait_vmcnt_range<MID + 1, HI>(n);
+  }
+}
+
+// Wait until at most n of this wavefront's vector memory instructions are
+// outstanding (n above the 6-bit counter's range waits for 63).
+__device__ __forceinline__ void wait_vmcnt_rt(int n) { wait_vmcnt_range<0, 63>(n < 63 ? n : 63); }
+
+typedef unsigned u32x2_t __attribute__((ext_vector_type(2)));
+typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+// One buffer store instruction each (exactly one vmcnt event, whatever the
+// lanes' offsets; lanes with an offset past num_records write nothing).
+__device__ __forceinline__ void buf_store_b64(u32x2_t v, uint32_t voff, i32x4_t rsrc) {
+  asm volatile("buffer_store_dwordx2 %0, %1, %2, 0 offen" : : "v"(v), "v"(voff), "s"(rsrc)
+               : "memory");
+}
+// A store of more than 8 bytes reads its data registers a cycle late: the nop
+// keeps the next VALU write to them from landing first (the compiler inserts
+// such wait states for its own instructions, not around inline asm).
+__device__ __forceinline__ void buf_store_b128(u32x4_t v, uint32_t voff, i32x4_t rsrc) {
+  asm volatile("buffer_store_dwordx4 %0, %1, %2, 0 offen\n\ts_nop 1" : : "v"(v), "v"(voff),
+               "s"(rsrc) : "memory");
+}
+
+__device__ __forceinline__ void lds_fence() { asm volatile("" : : : "memory"); }
+
+template <typename T>
+__device__ __forceinline__ uint32_t lds_addr(const T* p) {
+  return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p;
+}
+
+// Byte offset that the buffer range check rejects (operands are limited to
+// kDmaMaxSpan elements, so num_records <= this offset and offset + 16 does not
+// wrap): such a lane's load writes zeros to LDS.
+constexpr uint32_t kDmaOob = 0x80000000u;
+constexpr int64_t kDmaMaxSpan = 1ll << 30;
+
+// Per-operand DMA plan: which global 8-element chunk each lane fetches for each
+// of its wavefront's instructions in a stage (fixed per work item), plus the
+// resource.  The whole offset is per lane (the scalar offset is 0), and a chunk
+// is fetched only if its rows and reductions indices are all valid:
+//   KC: row < rows and k0 + c8 < kend   (kend a multiple of 8 or the chunk
+//       straddling it reads buffer contents past kend, which must then be 0)
+//   RC: rows a multiple of 8, row0 + c8 < rows and k < kend
+template <int R, int L, int NW>
+struct DmaOperand {
+  static constexpr int kInstr = R * kDmaBK * 2 / 1024;  // 1 KB instructions per stage
+  static constexpr int kPerWave = kInstr / NW;
+  static_assert(kInstr % NW == 0 && kPerWave >= 1, "tile too small for the wavefronts");
+  static_assert(L == OP_KC || R >= 128, "RC tiles need >= 16 chunks per k-row");
+  i32x4_t rsrc;
+  uint32_t base[kPerWave];  // element offset at k0 = 0, or kDmaOob
+  int kk[kPerWave];         // this lane's reduction offset within a k-step
+  uint32_t kstride;         // elements per unit of k
+  int kend;
+
+  __device__ __forceinline__ void setup(const GemmOperand& op, int K, int row0, int ke, int wave,
+                                        int lane) {
+    const int64_t span = L == OP_KC ? (int64_t)op.rows * op.ld : (int64_t)K * op.ld;
+    rsrc = make_buffer_rsrc(op.p, (uint32_t)(span * 2));
+#pragma unroll
+    for (int w = 0; w < 4; ++w) rsrc[w] = __builtin_amdgcn_readfirstlane(rsrc[w]);
+    kstride = L == OP_KC ? 1u : (uint32_t)op.ld;
+    kend = min(ke, op.k_valid);
+#pragma unroll
+    for (int i = 0; i < kPerWave; ++i) {
+      const int o = (wave * kPerWave + i) * 1024 + lane * 16;  // byte offset in the tile
+      if (L == OP_KC) {
+        const int row = o >> 7, slot = (o >> 4) & 7;
+        const int c = slot ^ ((row >> 1) & 7);
+        kk[i] = c * 8;
+        base[i] = row0 + row < op.rows ? (uint32_t)((row0 + row) * (int64_t)op.ld + c * 8)
+                                       : kDmaOob;
+      } else {
+        const int k = o / (R * 2), slot = (o % (R * 2)) >> 4;
+        const int c = slot ^ (4 * (k & 3));
+        kk[i] = k;
+        base[i] = row0 + c * 8 < op.rows ? (uint32_t)(k * (int64_t)op.ld + row0 + c * 8)
+                                         : kDmaOob;
+      }
+    }
+  }
+
+  // loads of the k-step starting at k0 into the stage at lds_stage (byte address)
+  __device__ __forceinline__ void issue(uint32_t lds_stage, int k0, int wave) const {
+    const uint32_t koff = (uint32_t)k0 * kstride;
+#pragma unroll
+    for (int i = 0; i < kPerWave; ++i) {
+      const bool ok = base[i] != kDmaOob && k0 + kk[i] < kend;
+      const uint32_t voff = ok ? (base[i] + koff) * 2u : kDmaOob;
+      dma16(__builtin_amdgcn_readfirstlane(lds_stage + (uint32_t)((wave * kPerWave + i) * 1024)),
+            rsrc, voff, 0u);
+    }
+  }
+};
+
+// ---------------------------------------------------------------------------
+// Epilogues of the direct-to-LDS kernel.  Same outputs as the epilogues in
+// ltv_gemm_mfma.hpp, but written with buffer stores whose masked lanes carry an
+// out-of-range offset, so every call issues a wave-uniform, known number of
+// store instructions: store_block returns that number, which the kernel adds
+// to its vmcnt bookkeeping.  Output buffers must be at most kDmaMaxBytes.
+// ---------------------------------------------------------------------------
+constexpr int64_t kDmaMaxBytes = 1ll << 31;
+
+__device__ __forceinline__ i32x4_t uniform_rsrc(const void* p, int64_t bytes) {
+  i32x4_t r = make_buffer_rsrc(p, (uint32_t)bytes);
+#pragma unroll
+  for (int w = 0; w < 4; ++w) r[w] = __builtin_amdgcn_readfirstlane(r[w]);
+  return r;
+}
+
+__device__ __forceinline__ u32x2_t pack4_bf16_v(const f32x16_t& v, int q) {
+  u32x2_t r;
+  r[0] = cvt_pk_bf16(v[4 * q], v[4 * q + 1]);
+  r[1] = cvt_pk_bf16(v[4 * q + 2], v[4 * q + 3]);
+  return r;
+}
+
+template <class Epi>
+struct DmaEpi;
+
+template <>
+struct DmaEpi<EpiRowBF16> {
+  i32x4_t rsrc;
+  int64_t ldc;
+  int i_valid, j_valid;
+  __device__ __forceinline__ DmaEpi(const EpiRowBF16& e, const GemmArgs&)
+      : rsrc(uniform_rsrc(e.c, (int64_t)e.j_valid * e.ldc * 2)), ldc(e.ldc), i_valid(e.i_valid),
+        j_valid(e.j_valid) {}
+  __device__ __forceinline__ int store_block(int i, int j, int, int lane,
+                                             const f32x16_t& v) const {
+    const int il = i + 4 * (lane >> 5);
+    const uint32_t off = (uint32_t)((int64_t)j * ldc + il) * 2u;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const bool ok = j < j_valid && il + 8 * q < i_valid;
+      buf_store_b64(pack4_bf16_v(v, q), ok ? off + 16u * q : kDmaOob, rsrc);
+    }
+    return 4;
+  }
+};
+
+template <>
+struct DmaEpi<EpiRowF32Split> {
+  i32x4_t rsrc;
+  int64_t ldc, split_stride;
+  int i_valid, j_valid;
+  __device__ __forceinline__ DmaEpi(const EpiRowF32Split& e, const GemmArgs& g)
+      : rsrc(uniform_rsrc(e.c, (int64_t)g.splits * e.split_stride * 4)), ldc(e.ldc),
+        split_stride(e.split_stride), i_valid(e.i_valid), j_valid(e.j_valid) {}
+  __device__ __forceinline__ int store_block(int i, int j, int split, int lane,
+                                             const f32x16_t& v) const {
+    const int il = i + 4 * (lane >> 5);
+    const uint32_t off = (uint32_t)((int64_t)split * split_stride + (int64_t)j * ldc + il) * 4u;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const bool ok = j < j_valid && il + 8 * q < i_valid;
+      // (a whole-vector bit_cast: bit_cast of single vector elements reads
+      // element 0 with this compiler)
+      const f32x4_t f = {v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
+      buf_store_b128(__builtin_bit_cast(u32x4_t, f), ok ? off + 32u * q : kDmaOob, rsrc);
+    }
+    return 4;
+  }
+};
+
+// Value blocks go to the head-major values, logit blocks to the logit rows; a
+// block that straddles the two (or, with D not a multiple of 32, several heads)
+// issues the value and the logit stores.
+template <>
+struct DmaEpi<EpiProjectHM> {
+  i32x4_t rsrc_v, rsrc_l;
+  int H, D, T, Lp, n_logit_end, m_valid;
+  __device__ __forceinline__ DmaEpi(const EpiProjectHM& e, const GemmArgs&)
+      : rsrc_v(uniform_rsrc(e.values, (int64_t)e.m_valid * e.H * e.D * 2)),
+        rsrc_l(uniform_rsrc(e.logits, (int64_t)e.m_valid * e.Lp * 2)), H(e.H), D(e.D), T(e.T),
+        Lp(e.Lp), n_logit_end(e.n_logit_end), m_valid(e.m_valid) {}
+  // n: wave-uniform first feature of the block; m: this lane's token
+  __device__ __forceinline__ int store_block(int n, int m, int, int lane,
+                                             const f32x16_t& v) const {
+    const int HD = H * D;
+    const bool mok = m < m_valid;
+    const int b = m / T, t = m - b * T;
+    const int nl = n + 4 * (lane >> 5);
+    if (D % 32 == 0 && n + 32 <= HD) {
+      const int h = n / D;
+      const uint32_t off =
+          (uint32_t)(((((int64_t)b * H + h) * T + t) * D) + (nl - h * D)) * 2u;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) buf_store_b64(pack4_bf16_v(v, q), mok ? off + 16u * q : kDmaOob, rsrc_v);
+      return 4;
+    }
+    int count = 0;
+    if (n < HD) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int nq = nl + 8 * q;
+        const int h = nq / D, d = nq - h * D;
+        const bool ok = mok && nq < HD;
+        const uint32_t off = (uint32_t)((((int64_t)b * H + h) * T + t) * D + d) * 2u;
+        buf_store_b64(pack4_bf16_v(v, q), ok ? off : kDmaOob, rsrc_v);
+      }
+      count += 4;
+    }
+    if (n + 32 > HD && n < n_logit_end) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int nq = nl + 8 * q;
+        const bool ok = mok && nq >= HD && nq < n_logit_end;
+        const uint32_t off = (uint32_t)((int64_t)m * Lp + (nq - HD)) * 2u;
+        buf_store_b64(pack4_bf16_v(v, q), ok ? off : kDmaOob, rsrc_l);
+      }
+      count += 4;
+    }
+    return count;
+  }
+};
+
+// MFMA operand fragment (8 consecutive k of one row) for k16 sub-step ks (0..3)
+// of a stage.
+template <int R, int L>
+__device__ __forceinline__ bf16x8_t dma_read_frag(const bf16_t* stage, int row_base, int ks,
+                                                  int lane) {
+  typedef __attribute__((address_space(3))) const char lds_char;
+  lds_char* base = (lds_char*)stage;
+  if (L == OP_KC) {
+    const int r = row_base + (lane & 31);
+    const int c = 2 * ks + (lane >> 5);
+    const u32x4_t q = *(__attribute__((address_space(3))) const u32x4_t*)(
+        base + r * 128 + ((c ^ ((r >> 1) & 7)) << 4));
+    return __builtin_bit_cast(bf16x8_t, q);
+  } else {
+    const int g = lane >> 4, s = lane & 15;
+    const int row = row_base + (g & 1) * 16 + 4 * (s & 3);
+    const int k = ks * 16 + (g >> 1) * 8 + (s >> 2);
+    const int c = row >> 3, within = (row & 7) * 2;
+    typedef __attribute__((address_space(3))) i16x4_t lds_i16x4;
+    lds_char* p0 = base + k * (R * 2) + ((c ^ (4 * (k & 3))) << 4) + within;
+    lds_char* p1 = p0 + 4 * (R * 2);  // k + 4: same swizzle (k & 3 unchanged)
+    const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)p0);
+    const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)p1);
+    typedef short i16x8_t __attribute__((ext_vector_type(8)));
+    const i16x8_t v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    return __builtin_bit_cast(bf16x8_t, v);
+  }
+}
+
+// Persistent over (tile, split) work items like gemm_bf16_kernel, stepping the
+// reduction in kDmaBK slices through two LDS stages.
+template <int BI, int BJ, int WGI, int WGJ, int PL, int QL, class Epi>
+__global__ void __launch_bounds__(WGI * WGJ * 64)
+gemm_dma_kernel(const GemmArgs g, const Epi epi) {
+  constexpr int NW = WGI * WGJ;
+  constexpr int WI = BI / WGI, WJ = BJ / WGJ;
+  constexpr int MI = WI / 32, MJ = WJ / 32;
+  static_assert(MI >= 1 && MJ >= 1 && WI % 32 == 0 && WJ % 32 == 0, "bad wave tile");
+  constexpr int PB = BI * kDmaBK * 2, QB = BJ * kDmaBK * 2;  // stage bytes per operand
+  constexpr int KS = kDmaBK / 16;                             // MFMA k16 sub-steps per step
+  using OpP = DmaOperand<BI, PL, NW>;
+  using OpQ = DmaOperand<BJ, QL, NW>;
+
+  __shared__ __attribute__((aligned(1024))) bf16_t lds_p[2][PB / 2];
+  __shared__ __attribute__((aligned(1024))) bf16_t lds_q[2][QB / 2];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int wi = wave % WGI, wj = wave / WGI;
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+  const int wi_u = wave_u % WGI, wj_u = wave_u / WGI;
+
+  f32x16_t acc[MI][MJ];
+#pragma unroll
+  for (int a = 0; a < MI; ++a)
+#pragma unroll
+    for (int b = 0; b < MJ; ++b)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[a][b][v] = 0.0f;
+
+  OpP op_p;
+  OpQ op_q;
+
+  // cursors count k-steps of kDmaBK; reuse GemmCursor with nk in those units
+  auto decode = [&](GemmCursor& c) {
+    gemm_decode<BI, BJ>(g, c);
+    if (c.valid) c.nk = (c.ke - c.kb + kDmaBK - 1) / kDmaBK;
+  };
+  auto advance = [&](GemmCursor& c) {
+    if (++c.kt >= c.nk) {
+      ++c.k;
+      decode(c);
+    }
+  };
+  auto issue = [&](const GemmCursor& c, int stage) {
+    if (c.kt == 0) {
+      op_p.setup(g.P, g.K, c.i0, c.ke, wave_u, lane);
+      op_q.setup(g.Q, g.K, c.j0, c.ke, wave_u, lane);
+    }
+    const int k0 = c.kb + c.kt * kDmaBK;
+    op_p.issue(lds_addr(&lds_p[stage][0]), k0, wave_u);
+    op_q.issue(lds_addr(&lds_q[stage][0]), k0, wave_u);
+  };
+
+  GemmCursor lc, cc;
+  lc.k = 0;
+  decode(lc);
+  cc = lc;
+  if (!cc.valid) return;
+  const DmaEpi<Epi> de(epi, g);
+  issue(lc, 0);
+  advance(lc);
+  wait_vmcnt<0>();
+  __builtin_amdgcn_s_barrier();
+  lds_fence();
+
+  int stage = 0;
+  while (cc.valid) {
+    // the other stage was last read in the previous step, which every
+    // wavefront has finished (barrier below): refill it with the next step
+    const bool refill = lc.valid;
+    if (refill) {
+      issue(lc, stage ^ 1);
+      advance(lc);
+    }
+    // MFMAs of this step; the fragments of sub-step t + 1 are read during t
+    const bf16_t* sp = &lds_p[stage][0];
+    const bf16_t* sq = &lds_q[stage][0];
+    bf16x8_t fp[2][MI], fq[2][MJ];
+#pragma unroll
+    for (int a = 0; a < MI; ++a) fp[0][a] = dma_read_frag<BI, PL>(sp, wi * WI + a * 32, 0, lane);
+#pragma unroll
+    for (int b = 0; b < MJ; ++b) fq[0][b] = dma_read_frag<BJ, QL>(sq, wj * WJ + b * 32, 0, lane);
+    static_for<KS>([&](auto tc) {
+      constexpr int t = decltype(tc)::value;
+      constexpr int cur = t & 1;
+      if constexpr (t + 1 < KS) {
+#pragma unroll
+        for (int a = 0; a < MI; ++a)
+          fp[cur ^ 1][a] = dma_read_frag<BI, PL>(sp, wi * WI + a * 32, t + 1, lane);
+#pragma unroll
+        for (int b = 0; b < MJ; ++b)
+          fq[cur ^ 1][b] = dma_read_frag<BJ, QL>(sq, wj * WJ + b * 32, t + 1, lane);
+      }
+#pragma unroll
+      for (int a = 0; a < MI; ++a)
+#pragma unroll
+        for (int b = 0; b < MJ; ++b)
+          acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fp[cur][a], fq[cur][b], acc[a][b],
+                                                              0, 0, 0);
+    });
+    int stores = 0;
+    if (cc.kt == cc.nk - 1) {
+#pragma unroll
+      for (int a = 0; a < MI; ++a)
+#pragma unroll
+        for (int b = 0; b < MJ; ++b) {
+          const int j = cc.j0 + wj_u * WJ + b * 32 + (lane & 31);
+          const int i = cc.i0 + wi_u * WI + a * 32;
+          stores += de.store_block(i, j, cc.split, lane, acc[a][b]);
+#pragma unroll
+          for (int v = 0; v < 16; ++v) acc[a][b][v] = 0.0f;
+        }
+    }
+    advance(cc);
+    // the next step's loads have landed (only the stores above are younger)
+    if (refill) wait_vmcnt_rt(stores);
+    __builtin_amdgcn_s_barrier();
+    lds_fence();
+    stage ^= 1;
+  }
+  wait_vmcnt<0>();
+}
+
+}  // namespace ltv

@@ -20,6 +20,8 @@
 // (tile, split) work items.
 #pragma once
 
+#include <utility>
+
 #include "ltv_device.hpp"
 
 namespace ltv {
@@ -30,6 +32,8 @@ typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
 enum OpLayout { OP_KC = 0, OP_RC = 1 };
 
+// Every operand must span fewer than 2^31 elements (the kernels keep 32-bit
+// element offsets); the host entry points check this.
 struct GemmOperand {
   const bf16_t* p;
   int64_t ld;
@@ -72,28 +76,63 @@ __device__ __forceinline__ uint4 mask_k_tail(uint4 q, int k0, int k_valid) {
 }
 
 // Global -> registers -> LDS staging of one operand tile (R rows x 64 k).
+// setup() fixes the tile's rows (per-chunk base pointers and row validity);
+// load() then only offsets by k0, with per-chunk k checks only in the k-tile
+// that crosses k_valid / k_end.
 template <int R, int L, int NT>
 struct TileStage {
   static constexpr int CH = R * 8 / NT;  // 16-byte chunks per thread
   static_assert(CH >= 1 && R * 8 % NT == 0, "tile too small for the thread count");
   uint4 q[CH];
+  const bf16_t* p;
+  uint32_t off[CH];  // chunk element offset from p at k = 0 (operands span < 2^31 elements)
+  uint32_t row_ok;   // bit c: chunk c's row is inside the operand
+  int64_t ld;
 
-  __device__ __forceinline__ void load(const GemmOperand& op, int row0, int k0, int k_end) {
-    const int kv = min(k_end, op.k_valid);
+  __device__ __forceinline__ void setup(const GemmOperand& op, int row0) {
+    p = op.p;
+    ld = op.ld;
+    row_ok = 0;
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+      const int idx = threadIdx.x + c * NT;
+      if (L == OP_KC) {
+        const int row = idx >> 3, kc = (idx & 7) * 8;
+        const bool ok = row0 + row < op.rows;
+        off[c] = ok ? (uint32_t)((int64_t)(row0 + row) * op.ld + kc) : 0u;
+        if (ok) row_ok |= 1u << c;
+      } else {
+        const int kk = idx / (R / 8), rc = (idx % (R / 8)) * 8;
+        const bool ok = row0 + rc < op.rows;
+        off[c] = ok ? (uint32_t)((int64_t)kk * op.ld + row0 + rc) : 0u;
+        if (ok) row_ok |= 1u << c;
+      }
+    }
+  }
+
+  __device__ __forceinline__ void load(int k0, int kv) {
+    const bool full = k0 + kGemmBK <= kv;  // uniform across the workgroup
 #pragma unroll
     for (int c = 0; c < CH; ++c) {
       const int idx = threadIdx.x + c * NT;
       uint4 v = make_uint4(0u, 0u, 0u, 0u);
+      const bool rok = (row_ok >> c) & 1u;
       if (L == OP_KC) {
-        const int row = idx >> 3, kc = (idx & 7) * 8;
-        const int gr = row0 + row, gk = k0 + kc;
-        if (gr < op.rows && gk < kv)
-          v = mask_k_tail(*reinterpret_cast<const uint4*>(op.p + (int64_t)gr * op.ld + gk), gk, kv);
+        const bf16_t* ptr = p + off[c] + k0;
+        if (full) {
+          if (rok) v = *reinterpret_cast<const uint4*>(ptr);
+        } else {
+          const int gk = k0 + (idx & 7) * 8;
+          if (rok && gk < kv) v = mask_k_tail(*reinterpret_cast<const uint4*>(ptr), gk, kv);
+        }
       } else {
-        const int kk = idx / (R / 8), rc = (idx % (R / 8)) * 8;
-        const int gk = k0 + kk, gr = row0 + rc;
-        if (gk < kv && gr < op.rows)
-          v = *reinterpret_cast<const uint4*>(op.p + (int64_t)gk * op.ld + gr);
+        const bf16_t* ptr = p + off[c] + (int64_t)k0 * ld;
+        if (full) {
+          if (rok) v = *reinterpret_cast<const uint4*>(ptr);
+        } else {
+          const int gk = k0 + idx / (R / 8);
+          if (rok && gk < kv) v = *reinterpret_cast<const uint4*>(ptr);
+        }
       }
       q[c] = v;
     }
@@ -132,6 +171,30 @@ __device__ __forceinline__ bf16x8_t read_frag(const bf16_t* lds, int row_base, i
     typedef short i16x8_t __attribute__((ext_vector_type(8)));
     const i16x8_t v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
     return __builtin_bit_cast(bf16x8_t, v);
+  }
+}
+
+template <class F, int... I>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+
+// f(std::integral_constant<int, 0>{}), ..., f(std::integral_constant<int, N - 1>{})
+template <int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+// Scheduling pattern for one k-step: N times {one MFMA, RD LDS reads, WR LDS
+// writes, VM global loads}.  Instructions beyond the pattern are placed freely.
+template <int N, int RD, int WR, int VM>
+__device__ __forceinline__ void sched_interleave() {
+  if constexpr (N > 0) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                 // MFMA
+    if constexpr (RD > 0) __builtin_amdgcn_sched_group_barrier(0x100, RD, 0);  // DS read
+    if constexpr (WR > 0) __builtin_amdgcn_sched_group_barrier(0x200, WR, 0);  // DS write
+    if constexpr (VM > 0) __builtin_amdgcn_sched_group_barrier(0x020, VM, 0);  // VMEM read
+    sched_interleave<N - 1, RD, WR, VM>();
   }
 }
 
@@ -204,19 +267,28 @@ gemm_bf16_kernel(const GemmArgs g, const Epi epi) {
   TileStage<BI, PL, NT> sp;
   TileStage<BJ, QL, NT> sq;
 
-  // One k-tile of MFMAs from LDS; operand fragments double-buffered in
-  // registers (the next k-step's reads are in flight while this step's MFMAs
-  // issue), with a scheduling fence per step so at most two sets are live.
-  auto compute = [&](const bf16_t* lp, const bf16_t* lq) {
+  // One k-tile of MFMAs from LDS.  Operand fragments are double-buffered in
+  // registers (the next k-step's reads issue between this step's MFMAs).  The
+  // staging of the next k-tile overlaps the MFMAs too: during k-step 1 the
+  // registers loaded one k-tile ago go to the other LDS stage (free since the
+  // barrier that ended the previous k-tile), during k-step 2 the loads of the
+  // k-tile after next are issued into the freed registers.  sched_group_barrier
+  // interleaves MFMAs with those memory instructions.
+  constexpr int NMF = MI * MJ;  // MFMAs per k-step
+  constexpr int NRD = (PL == OP_RC ? 2 : 1) * MI + (QL == OP_RC ? 2 : 1) * MJ;  // LDS reads
+  constexpr int RD_PER_MF = (NRD + NMF - 1) / NMF;
+  auto ktile = [&](const bf16_t* lp, const bf16_t* lq, bf16_t* wp, bf16_t* wq, bool do_store,
+                   auto&& issue_loads) {
     bf16x8_t pf[2][MI], qf[2][MJ];
 #pragma unroll
     for (int a = 0; a < MI; ++a) pf[0][a] = read_frag<BI, PL>(lp, wi * WI + a * 32, 0, lane);
 #pragma unroll
     for (int b = 0; b < MJ; ++b) qf[0][b] = read_frag<BJ, QL>(lq, wj * WJ + b * 32, 0, lane);
-#pragma unroll
-    for (int ks = 0; ks < kGemmBK / 16; ++ks) {
-      const int cur = ks & 1;
-      if (ks + 1 < kGemmBK / 16) {
+    __builtin_amdgcn_sched_barrier(0);
+    static_for<kGemmBK / 16>([&](auto ksc) {
+      constexpr int ks = decltype(ksc)::value;
+      constexpr int cur = ks & 1;
+      if constexpr (ks + 1 < kGemmBK / 16) {
 #pragma unroll
         for (int a = 0; a < MI; ++a)
           pf[cur ^ 1][a] = read_frag<BI, PL>(lp, wi * WI + a * 32, ks + 1, lane);
@@ -224,20 +296,36 @@ gemm_bf16_kernel(const GemmArgs g, const Epi epi) {
         for (int b = 0; b < MJ; ++b)
           qf[cur ^ 1][b] = read_frag<BJ, QL>(lq, wj * WJ + b * 32, ks + 1, lane);
       }
+      if constexpr (ks == 1) {
+        if (do_store) {
+          sp.store(wp);
+          sq.store(wq);
+        }
+      }
+      if constexpr (ks == 2) issue_loads();
 #pragma unroll
       for (int a = 0; a < MI; ++a)
 #pragma unroll
         for (int b = 0; b < MJ; ++b)
           acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pf[cur][a], qf[cur][b], acc[a][b], 0,
                                                               0, 0);
+      sched_interleave<NMF, (ks + 1 < kGemmBK / 16) ? RD_PER_MF : 0, ks == 1 ? 1 : 0,
+                       ks == 2 ? 1 : 0>();
       __builtin_amdgcn_sched_barrier(0);
-    }
+    });
+  };
+  auto compute = [&](const bf16_t* lp, const bf16_t* lq) {
+    ktile(lp, lq, nullptr, nullptr, false, [] {});
   };
 
   auto load = [&](const GemmCursor& c) {
+    if (c.kt == 0) {
+      sp.setup(g.P, c.i0);
+      sq.setup(g.Q, c.j0);
+    }
     const int k0 = c.kb + c.kt * kGemmBK;
-    sp.load(g.P, c.i0, k0, c.ke);
-    sq.load(g.Q, c.j0, k0, c.ke);
+    sp.load(k0, min(c.ke, g.P.k_valid));
+    sq.load(k0, min(c.ke, g.Q.k_valid));
   };
 
   // Two LDS stages, one register stage: the step after next waits in
@@ -256,28 +344,25 @@ gemm_bf16_kernel(const GemmArgs g, const Epi epi) {
   __syncthreads();
   int stage = 0;
   while (cc.valid) {
-    compute(lds_p[stage], lds_q[stage]);
-    if (lc.valid) {
-      sp.store(lds_p[stage ^ 1]);
-      sq.store(lds_q[stage ^ 1]);
-      gemm_advance<BI, BJ>(g, lc);
-      if (lc.valid) load(lc);
-    }
+    // registers hold the step after cc (when lc is valid): it goes to the other
+    // LDS stage during this k-tile, then the step after that is loaded
+    const bool have_next = lc.valid;
+    ktile(lds_p[stage], lds_q[stage], lds_p[stage ^ 1], lds_q[stage ^ 1], have_next, [&] {
+      if (have_next) {
+        gemm_advance<BI, BJ>(g, lc);
+        if (lc.valid) load(lc);
+      }
+    });
     if (cc.kt == cc.nk - 1) {
       // epilogue: lane holds column j = lane % 32 of each 32 x 32 block and rows
-      // 8 (v / 4) + 4 (lane / 32) + v % 4: four consecutive i per group of 4
+      // 8 (v / 4) + 4 (lane / 32) + v % 4 of it
 #pragma unroll
       for (int a = 0; a < MI; ++a)
 #pragma unroll
         for (int b = 0; b < MJ; ++b) {
           const int j = cc.j0 + wj * WJ + b * 32 + (lane & 31);
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const int i = cc.i0 + wi * WI + a * 32 + 8 * q + 4 * (lane >> 5);
-            const float4 v = make_float4(acc[a][b][4 * q], acc[a][b][4 * q + 1],
-                                         acc[a][b][4 * q + 2], acc[a][b][4 * q + 3]);
-            epi.store4(i, j, cc.split, v);
-          }
+          const int i = cc.i0 + wi * WI + a * 32;
+          epi.store_block(i, j, cc.split, lane, acc[a][b]);
 #pragma unroll
           for (int v = 0; v < 16; ++v) acc[a][b][v] = 0.0f;
         }
@@ -289,10 +374,11 @@ gemm_bf16_kernel(const GemmArgs g, const Epi epi) {
 }
 
 // ---------------------------------------------------------------------------
-// Epilogues.  store4(i, j, split, v): v = Out(i .. i + 3, j).
+// Epilogues.  store_block(i, j, split, lane, v): v holds Out(i + 8 q + 4 (lane / 32)
+// + e, j) at v[4 q + e], q, e = 0..3 (one lane's share of a 32-row block).
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ uint2 pack4_bf16(const float4& v) {
-  return make_uint2(cvt_pk_bf16(v.x, v.y), cvt_pk_bf16(v.z, v.w));
+__device__ __forceinline__ uint2 pack4_bf16(const f32x16_t& v, int q) {
+  return make_uint2(cvt_pk_bf16(v[4 * q], v[4 * q + 1]), cvt_pk_bf16(v[4 * q + 2], v[4 * q + 3]));
 }
 
 // Row-major bf16 output C[j][i] (i contiguous), rows j < j_valid, i < i_valid
@@ -301,9 +387,14 @@ struct EpiRowBF16 {
   bf16_t* c;
   int64_t ldc;
   int i_valid, j_valid;
-  __device__ __forceinline__ void store4(int i, int j, int, const float4& v) const {
-    if (i < i_valid && j < j_valid)
-      *reinterpret_cast<uint2*>(c + (int64_t)j * ldc + i) = pack4_bf16(v);
+  __device__ __forceinline__ void store_block(int i, int j, int, int lane,
+                                              const f32x16_t& v) const {
+    if (j >= j_valid) return;
+    bf16_t* row = c + (int64_t)j * ldc + i + 4 * (lane >> 5);
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      if (i + 8 * q + 4 * (lane >> 5) < i_valid)
+        *reinterpret_cast<uint2*>(row + 8 * q) = pack4_bf16(v, q);
   }
 };
 
@@ -312,9 +403,15 @@ struct EpiRowF32Split {
   float* c;
   int64_t ldc, split_stride;
   int i_valid, j_valid;
-  __device__ __forceinline__ void store4(int i, int j, int split, const float4& v) const {
-    if (i < i_valid && j < j_valid)
-      *reinterpret_cast<float4*>(c + (int64_t)split * split_stride + (int64_t)j * ldc + i) = v;
+  __device__ __forceinline__ void store_block(int i, int j, int split, int lane,
+                                              const f32x16_t& v) const {
+    if (j >= j_valid) return;
+    float* row = c + (int64_t)split * split_stride + (int64_t)j * ldc + i + 4 * (lane >> 5);
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      if (i + 8 * q + 4 * (lane >> 5) < i_valid)
+        *reinterpret_cast<float4*>(row + 8 * q) =
+            make_float4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
   }
 };
 
@@ -322,20 +419,35 @@ struct EpiRowF32Split {
 //   n <  H D : value channel d = n % D of head h = n / D ->
 //              values[((b H + h) T + t) D + d]           (head-major, bf16)
 //   n >= H D : logit column n - H D ->  logits[m Lp + n - H D] (row-major, bf16)
-// D and Lp are multiples of 4, so four consecutive n stay in one head / row.
+// D and Lp are multiples of 4, so four consecutive n stay in one head / row;
+// when D is a multiple of 32 the whole 32-row block is one head.
 struct EpiProjectHM {
   bf16_t* values;
   bf16_t* logits;
   int H, D, T, Lp, n_logit_end, m_valid;
-  __device__ __forceinline__ void store4(int n, int m, int, const float4& v) const {
+  __device__ __forceinline__ void store_block(int n, int m, int, int lane,
+                                              const f32x16_t& v) const {
     if (m >= m_valid) return;
     const int HD = H * D;
-    if (n < HD) {
-      const int h = n / D, d = n - h * D;
-      const int b = m / T, t = m - b * T;
-      *reinterpret_cast<uint2*>(values + (((int64_t)b * H + h) * T + t) * D + d) = pack4_bf16(v);
-    } else if (n < n_logit_end) {
-      *reinterpret_cast<uint2*>(logits + (int64_t)m * Lp + (n - HD)) = pack4_bf16(v);
+    const int b = m / T, t = m - b * T;
+    const int nl = n + 4 * (lane >> 5);
+    if (D % 32 == 0 && n + 32 <= HD) {
+      const int h = n / D, d = nl - h * D;
+      bf16_t* dst = values + (((int64_t)b * H + h) * T + t) * D + d;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) *reinterpret_cast<uint2*>(dst + 8 * q) = pack4_bf16(v, q);
+      return;
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int nq = nl + 8 * q;
+      if (nq < HD) {
+        const int h = nq / D, d = nq - h * D;
+        *reinterpret_cast<uint2*>(values + (((int64_t)b * H + h) * T + t) * D + d) =
+            pack4_bf16(v, q);
+      } else if (nq < n_logit_end) {
+        *reinterpret_cast<uint2*>(logits + (int64_t)m * Lp + (nq - HD)) = pack4_bf16(v, q);
+      }
     }
   }
 };
