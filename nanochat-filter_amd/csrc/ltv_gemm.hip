@@ -387,8 +387,12 @@ extern "C" int ltv_qkv_project_forward(const void* x, const void* wpack, void* v
                  ltv_qkv_logit_width(H, Da), H * D + H * Da, M};
   hipStream_t st = (hipStream_t)stream;
   if (gemm_tuning().dma && dma_usable(a, OP_KC, OP_KC, e, 1)) {
-    a.tiles_i = (Fp + 255) / 256;
     a.tiles_j = (M + 255) / 256;
+    if (gemm_tuning().fwd == 3) {
+      a.tiles_i = (Fp + 127) / 128;
+      return launch_gemm_dma<128, 256, 2, 4, OP_KC, OP_KC>(a, e, 1, st);
+    }
+    a.tiles_i = (Fp + 255) / 256;
     return launch_gemm_dma<256, 256, 2, 4, OP_KC, OP_KC>(a, e, 1, st);
   }
   if (gemm_tuning().fwd == 1) {
@@ -462,6 +466,10 @@ extern "C" int ltv_qkv_project_backward_input(const void* x, const void* wpack,
                            reinterpret_cast<bf16_t*>(grad_combined), M,
                            (int64_t)Fp, Fvalid, Fv8);
         LTV_LAUNCH_CHECK();
+      }
+      if (gemm_tuning().dx == 3) {  // 128-row tiles: 2x the work items of the 256-row tiles
+        ad.tiles_i = (C + 127) / 128;
+        return launch_gemm_dma<128, 256, 2, 4, OP_RC, OP_KC>(ad, e, 1, st);
       }
       ad.tiles_i = (C + 255) / 256;
       return launch_gemm_dma<256, 256, 2, 4, OP_RC, OP_KC>(ad, e, 1, st);

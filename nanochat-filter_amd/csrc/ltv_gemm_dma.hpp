@@ -199,6 +199,40 @@ __device__ __forceinline__ u32x2_t pack4_bf16_v(const f32x16_t& v, int q) {
   return r;
 }
 
+// Per-wavefront LDS staging of output blocks for full-line stores: 32 rows of
+// 128 bytes, 16-byte chunk c of row r at slot c ^ (r & 7) (the row-wise reads
+// back are bank-conflict free).  A store instruction then writes 8 rows x 128
+// contiguous bytes instead of 32 rows x 16 bytes: the L2 takes one request per
+// line either way, so partial-line stores cost 4x the requests.
+constexpr int kEpiStageBytes = 4096;
+typedef __attribute__((address_space(3))) char lds_char_t;
+
+__device__ __forceinline__ lds_char_t* stage_slot(lds_char_t* st, int row, int byte) {
+  return st + row * 128 + ((((byte >> 4) ^ (row & 7))) << 4) + (byte & 15);
+}
+__device__ __forceinline__ void stage_put(lds_char_t* st, int row, int byte, u32x2_t v) {
+  *(__attribute__((address_space(3))) u32x2_t*)stage_slot(st, row, byte) = v;
+}
+__device__ __forceinline__ void stage_put(lds_char_t* st, int row, int byte, u32x4_t v) {
+  *(__attribute__((address_space(3))) u32x4_t*)stage_slot(st, row, byte) = v;
+}
+// chunk (16 bytes) c of row r
+__device__ __forceinline__ u32x4_t stage_get(lds_char_t* st, int row, int c) {
+  return *(__attribute__((address_space(3))) const u32x4_t*)stage_slot(st, row, c * 16);
+}
+
+// Stage two 32 x 32 bf16 blocks (output rows j = lane & 31, 64 columns) of one
+// wavefront: afterwards row r of the stage holds columns 0..63 of block row r.
+__device__ __forceinline__ void stage_bf16_pair(lds_char_t* st, const f32x16_t& lo,
+                                                const f32x16_t& hi, int lane) {
+  const int row = lane & 31, h4 = 4 * (lane >> 5);
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    stage_put(st, row, (8 * q + h4) * 2, pack4_bf16_v(lo, q));
+    stage_put(st, row, (32 + 8 * q + h4) * 2, pack4_bf16_v(hi, q));
+  }
+}
+
 template <class Epi>
 struct DmaEpi;
 
@@ -220,6 +254,27 @@ struct DmaEpi<EpiRowBF16> {
       buf_store_b64(pack4_bf16_v(v, q), ok ? off + 16u * q : kDmaOob, rsrc);
     }
     return 4;
+  }
+  // the wavefront's MI x MJ blocks at (i0 + 32 a, j0 + 32 b), through the stage
+  template <int MI, int MJ>
+  __device__ __forceinline__ int store_tile(const f32x16_t (&acc)[MI][MJ], int i0, int j0, int,
+                                            int lane, lds_char_t* st) const {
+    static_assert(MI % 2 == 0, "blocks are staged in pairs along i");
+#pragma unroll
+    for (int b = 0; b < MJ; ++b)
+#pragma unroll
+      for (int a2 = 0; a2 < MI / 2; ++a2) {
+        stage_bf16_pair(st, acc[2 * a2][b], acc[2 * a2 + 1][b], lane);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int row = 8 * r + (lane >> 3), c = lane & 7;
+          const int j = j0 + 32 * b + row, i = i0 + 64 * a2 + 8 * c;
+          const bool ok = j < j_valid && i < i_valid;
+          buf_store_b128(stage_get(st, row, c),
+                         ok ? (uint32_t)((int64_t)j * ldc + i) * 2u : kDmaOob, rsrc);
+        }
+      }
+    return MJ * (MI / 2) * 4;
   }
 };
 
@@ -244,6 +299,32 @@ struct DmaEpi<EpiRowF32Split> {
       buf_store_b128(__builtin_bit_cast(u32x4_t, f), ok ? off + 32u * q : kDmaOob, rsrc);
     }
     return 4;
+  }
+  template <int MI, int MJ>
+  __device__ __forceinline__ int store_tile(const f32x16_t (&acc)[MI][MJ], int i0, int j0,
+                                            int split, int lane, lds_char_t* st) const {
+    const int row_w = lane & 31, h4 = 4 * (lane >> 5);
+#pragma unroll
+    for (int b = 0; b < MJ; ++b)
+#pragma unroll
+      for (int a = 0; a < MI; ++a) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const f32x4_t f = {acc[a][b][4 * q], acc[a][b][4 * q + 1], acc[a][b][4 * q + 2],
+                             acc[a][b][4 * q + 3]};
+          stage_put(st, row_w, (8 * q + h4) * 4, __builtin_bit_cast(u32x4_t, f));
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int row = 8 * r + (lane >> 3), c = lane & 7;
+          const int j = j0 + 32 * b + row, i = i0 + 32 * a + 4 * c;
+          const bool ok = j < j_valid && i < i_valid;
+          const uint32_t off =
+              (uint32_t)((int64_t)split * split_stride + (int64_t)j * ldc + i) * 4u;
+          buf_store_b128(stage_get(st, row, c), ok ? off : kDmaOob, rsrc);
+        }
+      }
+    return MJ * MI * 4;
   }
 };
 
@@ -297,6 +378,40 @@ struct DmaEpi<EpiProjectHM> {
     }
     return count;
   }
+  // value blocks in pairs inside one head go through the stage (one token's 64
+  // channels = 128 contiguous bytes of values); other pairs use store_block
+  template <int MI, int MJ>
+  __device__ __forceinline__ int store_tile(const f32x16_t (&acc)[MI][MJ], int i0, int j0,
+                                            int split, int lane, lds_char_t* st) const {
+    static_assert(MI % 2 == 0, "blocks are staged in pairs along i");
+    const int HD = H * D;
+    int count = 0;
+#pragma unroll
+    for (int b = 0; b < MJ; ++b)
+#pragma unroll
+      for (int a2 = 0; a2 < MI / 2; ++a2) {
+        const int n0 = i0 + 64 * a2;
+        if (D % 64 == 0 && n0 + 64 <= HD) {
+          stage_bf16_pair(st, acc[2 * a2][b], acc[2 * a2 + 1][b], lane);
+          const int h = n0 / D, d0 = n0 - h * D;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int row = 8 * r + (lane >> 3), c = lane & 7;
+            const int m = j0 + 32 * b + row;
+            const int bb = m / T, t = m - bb * T;
+            const uint32_t off =
+                (uint32_t)((((int64_t)bb * H + h) * T + t) * D + d0 + 8 * c) * 2u;
+            buf_store_b128(stage_get(st, row, c), m < m_valid ? off : kDmaOob, rsrc_v);
+          }
+          count += 4;
+        } else {
+          const int m = j0 + 32 * b + (lane & 31);
+          count += store_block(n0, m, split, lane, acc[2 * a2][b]);
+          count += store_block(n0 + 32, m, split, lane, acc[2 * a2 + 1][b]);
+        }
+      }
+    return count;
+  }
 };
 
 // MFMA operand fragment (8 consecutive k of one row) for k16 sub-step ks (0..3)
@@ -344,6 +459,7 @@ gemm_dma_kernel(const GemmArgs g, const Epi epi) {
 
   __shared__ __attribute__((aligned(1024))) bf16_t lds_p[2][PB / 2];
   __shared__ __attribute__((aligned(1024))) bf16_t lds_q[2][QB / 2];
+  __shared__ __attribute__((aligned(16))) char lds_epi[NW][kEpiStageBytes];
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -432,16 +548,14 @@ gemm_dma_kernel(const GemmArgs g, const Epi epi) {
     });
     int stores = 0;
     if (cc.kt == cc.nk - 1) {
+      stores = de.template store_tile<MI, MJ>(acc, cc.i0 + wi_u * WI, cc.j0 + wj_u * WJ, cc.split,
+                                              lane, (lds_char_t*)&lds_epi[wave_u][0]);
 #pragma unroll
       for (int a = 0; a < MI; ++a)
 #pragma unroll
-        for (int b = 0; b < MJ; ++b) {
-          const int j = cc.j0 + wj_u * WJ + b * 32 + (lane & 31);
-          const int i = cc.i0 + wi_u * WI + a * 32;
-          stores += de.store_block(i, j, cc.split, lane, acc[a][b]);
+        for (int b = 0; b < MJ; ++b)
 #pragma unroll
           for (int v = 0; v < 16; ++v) acc[a][b][v] = 0.0f;
-        }
     }
     advance(cc);
     // the next step's loads have landed (only the stores above are younger)
