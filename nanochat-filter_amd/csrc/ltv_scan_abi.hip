@@ -3,18 +3,34 @@
 #include <stdio.h>
 #include <stdlib.h>
 
+#include <algorithm>
+
 #include "ltv_scan_launch.hpp"
 
 namespace ltv {
 
-// dbias[h, j] = sum_b partial[b, h, j], fixed order.
-__global__ void dbias_reduce_kernel(const float* __restrict__ partial, float* __restrict__ dbias,
-                                    int B, int HDa) {
-  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < HDa; i += gridDim.x * blockDim.x) {
-    float acc = 0.0f;
-    for (int b = 0; b < B; ++b) acc += partial[(int64_t)b * HDa + i];
-    dbias[i] = acc;
+// dbias[h, j] = sum over (b, c) of partial[b, h, c, j]: one workgroup per
+// output, thread i summing the pairs i, i + 256, ... in order, then a fixed
+// tree over the threads (deterministic).
+__global__ void __launch_bounds__(256) dbias_reduce_kernel(const float* __restrict__ partial,
+                                                           float* __restrict__ dbias, int B,
+                                                           int H, int NC, int Da) {
+  __shared__ float red[256];
+  const int i = blockIdx.x;  // h * Da + j
+  const int h = i / Da, j = i - h * Da;
+  const int n = B * NC;
+  float acc = 0.0f;
+  for (int k = threadIdx.x; k < n; k += 256) {
+    const int b = k / NC, c = k - b * NC;
+    acc += partial[(((int64_t)b * H + h) * NC + c) * Da + j];
   }
+  red[threadIdx.x] = acc;
+  __syncthreads();
+  for (int w = 128; w > 0; w >>= 1) {
+    if ((int)threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) dbias[i] = red[0];
 }
 
 int scan_launch_fwd(bool bf16, const FwdArgs& a, ScanCfg cfg, int grid, bool vec, int gm,
@@ -53,10 +69,51 @@ int scan_launch_bwd_channel(bool bf16, const BwdArgs& a, float* dalpha, hipStrea
   return LTV_OK;
 }
 
-int scan_launch_dbias_reduce(const float* partial, float* dbias, int B, int HDa,
+// carry[bh, k, c] = g entering chunk k from its end: the maps of chunks
+// nchunk - 1, ..., k + 1 applied to 0, in that order.
+__global__ void __launch_bounds__(256) scan_bwd_carry_kernel(const BwdArgs args) {
+  const ScanShape& S = args.sh;
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (int64_t)S.B * S.H * S.D) return;
+  const int c = (int)(idx % S.D);
+  const int64_t bh = idx / S.D;
+  const int64_t plane = (int64_t)S.B * S.H * args.nchunk * S.D;
+  float g = 0.0f;
+  for (int k = args.nchunk - 1; k >= 0; --k) {
+    const int64_t i = (bh * args.nchunk + k) * S.D + c;
+    args.carry[i] = g;
+    g = fmaf(args.agg[i], g, args.agg[plane + i]);
+  }
+}
+
+// The per-chunk maps of the reverse recurrence, then each chunk's carry.
+int scan_launch_bwd_chunk_maps(bool bf16, const BwdArgs& a, bool vec, hipStream_t st) {
+  const ScanShape& S = a.sh;
+  const int V = bf16 ? 8 : 4;
+  const int64_t n = (int64_t)S.B * S.H * a.nchunk * ((S.D + V - 1) / V);
+  const int blocks = (int)((n + 255) / 256);
+  if (bf16) {
+    if (vec)
+      hipLaunchKernelGGL((scan_bwd_agg_kernel<bf16_t, true>), dim3(blocks), dim3(256), 0, st, a);
+    else
+      hipLaunchKernelGGL((scan_bwd_agg_kernel<bf16_t, false>), dim3(blocks), dim3(256), 0, st, a);
+  } else {
+    if (vec)
+      hipLaunchKernelGGL((scan_bwd_agg_kernel<float, true>), dim3(blocks), dim3(256), 0, st, a);
+    else
+      hipLaunchKernelGGL((scan_bwd_agg_kernel<float, false>), dim3(blocks), dim3(256), 0, st, a);
+  }
+  LTV_LAUNCH_CHECK();
+  const int64_t nc = (int64_t)S.B * S.H * S.D;
+  hipLaunchKernelGGL(scan_bwd_carry_kernel, dim3((int)((nc + 255) / 256)), dim3(256), 0, st, a);
+  LTV_LAUNCH_CHECK();
+  return LTV_OK;
+}
+
+int scan_launch_dbias_reduce(const float* partial, float* dbias, int B, int H, int NC, int Da,
                              hipStream_t st) {
-  hipLaunchKernelGGL(dbias_reduce_kernel, dim3((HDa + 255) / 256), dim3(256), 0, st, partial,
-                     dbias, B, HDa);
+  hipLaunchKernelGGL(dbias_reduce_kernel, dim3(H * Da), dim3(256), 0, st, partial, dbias, B, H,
+                     NC, Da);
   LTV_LAUNCH_CHECK();
   return LTV_OK;
 }
@@ -90,7 +147,9 @@ inline bool vec_ok(const void* p, const int64_t* s, int nd_outer, int V) {
 struct ScanTuning {
   int fwd_cl = 0, fwd_l = 0, fwd_nw = 0;
   int bwd_l = 0, bwd_nw = 0;
+  int bwd_chunks = 0;  // time chunks per (b, h) in the backward; 0 = automatic
   ScanTuning() {
+    if (const char* e = getenv("LTV_SCAN_BWD_CHUNKS")) bwd_chunks = atoi(e) > 0 ? atoi(e) : 0;
     if (const char* e = getenv("LTV_SCAN_FWD_CFG")) {
       if (sscanf(e, "%d,%d,%d", &fwd_cl, &fwd_l, &fwd_nw) != 3) fwd_cl = fwd_l = fwd_nw = 0;
     }
@@ -179,13 +238,49 @@ int scan_forward_impl(int dtype, const HostView4& u, const HostView4& lg, const 
   return scan_launch_fwd(dtype == LTV_DTYPE_BF16, a, cfg, (int)grid, vec, gm, st);
 }
 
-size_t bwd_workspace_bytes(int dtype, int B, int T, int NH, int NKVH, int Da, int r) {
+// Upper bound on the backward's time chunks per (b, h).  With at least 512
+// (b, h) sequences (two per CU on MI355X) every CU already holds resident
+// workgroups and chunking only adds the chunk-map passes; with fewer (long T,
+// small batch) the sequences are cut into chunks of at least one 64-step tile
+// until about 1024 workgroups run.  The
+// launch rounds the chunk length up to whole tiles, which never raises the
+// count above this bound.
+int bwd_max_chunks(int B, int H, int T) {
+  const int64_t bh = (int64_t)B * H;
+  int nc = tuning().bwd_chunks;
+  if (nc == 0) nc = bh >= 512 ? 1 : (int)((1024 + bh - 1) / bh);
+  const int cap = (T + 63) / 64;
+  return std::max(1, std::min(nc, cap));
+}
+
+struct BwdWorkspace {
+  size_t partial = 0, agg = 0, carry = 0, dalpha = 0, total = 0;  // byte offsets
+};
+
+BwdWorkspace bwd_workspace_plan(int dtype, int B, int T, int NH, int NKVH, int Da, int r) {
   const int H = NH + 2 * NKVH;
   const int V = dtype == LTV_DTYPE_BF16 ? 8 : 4;
-  size_t bytes = (size_t)B * H * Da * sizeof(float);
-  bytes = (bytes + 255) & ~(size_t)255;
-  if (bwd_gate_mode(r, Da, V) < 0) bytes += (size_t)B * H * T * Da * r * sizeof(float);
-  return bytes;
+  const int D = Da * r;
+  const int NC = bwd_max_chunks(B, H, T);
+  auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
+  BwdWorkspace w;
+  size_t off = al((size_t)B * H * NC * Da * sizeof(float));
+  if (NC > 1) {
+    w.agg = off;
+    off += al((size_t)2 * B * H * NC * D * sizeof(float));
+    w.carry = off;
+    off += al((size_t)B * H * NC * D * sizeof(float));
+  }
+  if (bwd_gate_mode(r, Da, V) < 0) {
+    w.dalpha = off;
+    off += (size_t)B * H * T * D * sizeof(float);
+  }
+  w.total = off;
+  return w;
+}
+
+size_t bwd_workspace_bytes(int dtype, int B, int T, int NH, int NKVH, int Da, int r) {
+  return bwd_workspace_plan(dtype, B, T, NH, NKVH, Da, r).total;
 }
 
 int scan_backward_impl(int dtype, const HostView4& u, const HostView4& lg, const HostView4& init,
@@ -235,31 +330,52 @@ int scan_backward_impl(int dtype, const HostView4& u, const HostView4& lg, const
   a.du = to_dev(du);
   a.dlg = to_dev(dlg);
   a.dinit = to_dev(dinit);
-  a.dbias_partial = reinterpret_cast<float*>(ws);
+  const BwdWorkspace wp = bwd_workspace_plan(dtype, B, T, NH, NKVH, Da, r);
+  char* wsb = reinterpret_cast<char*>(ws);
+  a.dbias_partial = reinterpret_cast<float*>(wsb + wp.partial);
+  a.nchunk = 1;
+  a.chunk_steps = T;
+  a.agg = nullptr;
+  a.carry = nullptr;
 
-  const int64_t grid = (int64_t)B * H;
-  LTV_REQUIRE(grid < (1ll << 31), LTV_ERR_UNSUPPORTED, "grid too large");
   int gm = bwd_gate_mode(r, Da, V);
   if (gm == GATE_CHAN && vec && chanvec_ok(r, D, V, lg) && chanvec_ok(r, D, V, dlg))
     gm = GATE_CHANVEC;
   if (gm >= 0) {
-    // whole head per workgroup; 4 steps per lane keeps 3 wavefronts per SIMD
-    ScanCfg cfg{next_pow2((D + V - 1) / V), 4, 4};
+    // whole head per workgroup, 4 wavefronts.  Each lane keeps the next tile's
+    // loads in flight; at 16 channel lanes (D = 128 in bf16) 2 steps per lane
+    // keep 3 wavefronts per SIMD resident (measured fastest at d12), else 4.
+    const int cl = next_pow2((D + V - 1) / V);
+    ScanCfg cfg{cl, vec && cl == 16 ? 2 : 4, 4};
     const ScanTuning& tu = tuning();
     if (vec && tu.bwd_l > 0) {
       cfg.L = tu.bwd_l;
       cfg.NW = tu.bwd_nw;
     }
+    // time chunks of whole tiles; each chunk enters with its exact gradient
+    // carry from the chunk-map kernels
+    const int TW = cfg.NW * (64 / cfg.CL) * cfg.L;
+    const int nc_max = bwd_max_chunks(B, H, T);
+    const int per = (T + nc_max - 1) / nc_max;
+    a.chunk_steps = (per + TW - 1) / TW * TW;
+    a.nchunk = (T + a.chunk_steps - 1) / a.chunk_steps;
+    const int64_t grid = (int64_t)B * H * a.nchunk;
+    LTV_REQUIRE(grid < (1ll << 31), LTV_ERR_UNSUPPORTED, "grid too large");
+    if (a.nchunk > 1) {
+      a.agg = reinterpret_cast<float*>(wsb + wp.agg);
+      a.carry = reinterpret_cast<float*>(wsb + wp.carry);
+      rc = scan_launch_bwd_chunk_maps(dtype == LTV_DTYPE_BF16, a, vec, st);
+      if (rc) return rc;
+    }
     rc = scan_launch_bwd(dtype == LTV_DTYPE_BF16, a, cfg, (int)grid, vec, gm, st);
     if (rc) return rc;
   } else {
-    size_t off = ((size_t)B * H * Da * sizeof(float) + 255) & ~(size_t)255;
-    float* dalpha = reinterpret_cast<float*>(reinterpret_cast<char*>(ws) + off);
+    LTV_REQUIRE((int64_t)B * H < (1ll << 31), LTV_ERR_UNSUPPORTED, "grid too large");
+    float* dalpha = reinterpret_cast<float*>(wsb + wp.dalpha);
     rc = scan_launch_bwd_channel(dtype == LTV_DTYPE_BF16, a, dalpha, st);
     if (rc) return rc;
   }
-  const int HDa = H * Da;
-  return scan_launch_dbias_reduce(reinterpret_cast<const float*>(ws), dbias, B, HDa, st);
+  return scan_launch_dbias_reduce(a.dbias_partial, dbias, B, H, a.nchunk, Da, st);
 }
 
 // (B, T, F) interleaved tensor -> value / logit 4-D views

@@ -25,10 +25,10 @@
 // The lane then re-runs its L steps from its exact carry-in and stores, so every
 // element is read from HBM once and written once.
 //
-// The backward walks the tiles in reverse.  Per tile it first recomputes the
-// forward states h_{t-1} from the saved output row just before the tile (the
-// same three-level scan), rounds them to the I/O dtype (the state the reference
-// backward reads back, ltv_reference_ops.py:7-34), then runs the reverse scan
+// The backward walks the tiles in reverse.  Per tile it reads the forward
+// states h_{t-1} from the saved outputs of the previous steps (the inits at
+// t = 0) -- the I/O-dtype state the reference backward reads back,
+// ltv_reference_ops.py:7-34 -- then runs the reverse scan
 //   g_t = gy_t + (1 - alpha_{t+1}) g_{t+1},   g_T = 0
 // and emits du = alpha g, dalpha = (u - h_{t-1}) g reduced over each gate group,
 // dlogit = alpha (1 - alpha) dalpha, dinit = (1 - alpha_0) g_0 and a per-(b, h)
@@ -81,7 +81,14 @@ struct BwdArgs {
   View4 du;       // gradient of the value slots (B, H, T, D)
   View4 dlg;      // gradient of the logit slots (B, H, T, Da)
   View4 dinit;    // (B, H, D)
-  float* dbias_partial;  // (B, H, Da) fp32 workspace
+  float* dbias_partial;  // (B, H, nchunk, Da) fp32 workspace
+  // Time chunks: the tile kernel runs one workgroup per (b, h, chunk) of
+  // chunk_steps steps (a multiple of its tile), entering each chunk with the
+  // gradient carry g at the chunk's end from `carry` (B H, nchunk, D); with
+  // nchunk == 1 the carry is 0 and `carry` is unused.
+  int nchunk, chunk_steps;
+  float* agg;          // (2, B H, nchunk, D): each chunk's map g_start = A g_end + G
+  float* carry;        // (B H, nchunk, D)
 };
 
 // How a lane finds the gate of each of its V channels.
@@ -507,8 +514,10 @@ scan_bwd_kernel(const BwdArgs args) {
   const int cl = lane / TG;
   const int tg = lane % TG;
 
-  const int h = blockIdx.x % S.H;  // one workgroup per (b, head): every gate group inside
-  const int b = blockIdx.x / S.H;
+  // one workgroup per (b, head, time chunk): every gate group of the head inside
+  const int bh = blockIdx.x / args.nchunk, chunk = blockIdx.x % args.nchunk;
+  const int h = bh % S.H;
+  const int b = bh / S.H;
 
   const int c0 = cl * V;
   const int nvalid = min(V, S.D - c0);
@@ -545,8 +554,6 @@ scan_bwd_kernel(const BwdArgs args) {
   const bool use_sig = S.use_sigmoid != 0;
   const int gl_lanes = GL ? S.r / V : 1;           // lanes per gate group (GATE_LANE)
 
-  __shared__ float lds_fa[NW][CL][NA];
-  __shared__ float4 lds_fx[NW][CL][V / 4];
   __shared__ float lds_ba[NW][CL][NA];
   __shared__ float4 lds_bx[NW][CL][V / 4];
   // GATE_LANE: per-(step, lane) dalpha partials and per-(step, group) gate slopes
@@ -557,6 +564,11 @@ scan_bwd_kernel(const BwdArgs args) {
   float gcarry[V];  // g at the first step after the current tile
 #pragma unroll
   for (int v = 0; v < V; ++v) gcarry[v] = 0.0f;
+  if (args.nchunk > 1) {
+    const float* cp = args.carry + ((int64_t)bh * args.nchunk + chunk) * S.D + c0;
+#pragma unroll
+    for (int v = 0; v < V; ++v) gcarry[v] = v < nvalid ? cp[v] : 0.0f;
+  }
   // dbias accumulators: GATE_CHAN* keeps one per channel slot in registers;
   // GATE_LANE accumulates per group j in this thread's own row of lds_red.
   float dacc[GL ? 1 : V];
@@ -568,104 +580,48 @@ scan_bwd_kernel(const BwdArgs args) {
   }
 
   const int ntiles = (S.T + TW - 1) / TW;
-  for (int it = ntiles - 1; it >= 0; --it) {
-    const int T0 = it * TW;
-    const int t0 = T0 + (w * TG + tg) * L;
-
-    uint4 uq[L], gq[L];
+  const int tiles_pc = args.chunk_steps / TW;
+  const int it_lo = chunk * tiles_pc;
+  const int it_hi = min(ntiles, it_lo + tiles_pc) - 1;
+  // The next (earlier) tile's packed u, gy, h_{t-1} and raw logits are loaded
+  // while the current tile is processed, so each wavefront keeps its loads in
+  // flight across the tile's barriers.  h_{t-1} of a step is the saved forward
+  // output of the step before (the inits at t = 0): exactly the rounded state
+  // the forward stored.
+  const int tl0 = (w * TG + tg) * L;
+  uint4 nu[L], ng[L], nh[L];
+  LogitRaw<TIO, GM, L + 1> nl;
+  auto load_tile = [&](int it) {
+    const int t0 = it * TW + tl0;
 #pragma unroll
     for (int s = 0; s < L; ++s) {
-      const bool ok = active && (t0 + s) < S.T;
-      uq[s] = ok ? ld_vec<TIO, VEC>(up + (int64_t)(t0 + s) * ust, usc, nvalid)
+      const int t = t0 + s;
+      const bool ok = active && t < S.T;
+      nu[s] = ok ? ld_vec<TIO, VEC>(up + (int64_t)t * ust, usc, nvalid)
                  : make_uint4(0u, 0u, 0u, 0u);
-      gq[s] = ok ? ld_vec<TIO, VEC>(gp + (int64_t)(t0 + s) * gs[2], gs[3], nvalid)
+      ng[s] = ok ? ld_vec<TIO, VEC>(gp + (int64_t)t * gs[2], gs[3], nvalid)
                  : make_uint4(0u, 0u, 0u, 0u);
+      nh[s] = !ok      ? make_uint4(0u, 0u, 0u, 0u)
+              : t == 0 ? ld_vec<TIO, VEC>(ip, args.init.s[3], nvalid)
+                       : ld_vec<TIO, VEC>(hp + (int64_t)(t - 1) * hs[2], hs[3], nvalid);
     }
-    // state entering the tile: the saved output at T0 - 1, or the inits
-    float hc[V];
-    {
-      uint4 q = make_uint4(0u, 0u, 0u, 0u);
-      if (active) {
-        q = T0 == 0 ? ld_vec<TIO, VEC>(ip, args.init.s[3], nvalid)
-                    : ld_vec<TIO, VEC>(hp + (int64_t)(T0 - 1) * hs[2], hs[3], nvalid);
-      }
+    nl.load(lp + (int64_t)t0 * lst, lst, gi, t0, S.T, active, nvalid);
+  };
+  if (it_hi >= it_lo) load_tile(it_hi);
+  for (int it = it_hi; it >= it_lo; --it) {
+    const int T0 = it * TW;
+    const int t0 = T0 + tl0;
+
+    uint4 uq[L], gq[L], hq[L];
 #pragma unroll
-      for (int v = 0; v < V; ++v) hc[v] = Pack<TIO>::get(q, v);
+    for (int s = 0; s < L; ++s) {
+      uq[s] = nu[s];
+      gq[s] = ng[s];
+      hq[s] = nh[s];
     }
     float al[L + 1][NA];
-    {
-      LogitRaw<TIO, GM, L + 1> lr;
-      lr.load(lp + (int64_t)t0 * lst, lst, gi, t0, S.T, active, nvalid);
-      lr.gates(gi, t0, S.T, active, use_sig, al);
-    }
-
-    // ---- forward recompute of h_{t-1} inside the tile
-    uint4 hq[L];  // h_{t-1} for each step, rounded to the I/O dtype
-    {
-      float A[NA], X[V];
-#pragma unroll
-      for (int i = 0; i < NA; ++i) A[i] = 1.0f;
-#pragma unroll
-      for (int v = 0; v < V; ++v) X[v] = 0.0f;
-#pragma unroll
-      for (int s = 0; s < L; ++s) {
-#pragma unroll
-        for (int v = 0; v < V; ++v) {
-          const float a = al[s][GL ? 0 : v];
-          X[v] = fmaf(a, Pack<TIO>::get(uq[s], v) - X[v], X[v]);
-        }
-#pragma unroll
-        for (int i = 0; i < NA; ++i) A[i] = fmaf(-A[i], al[s][i], A[i]);
-      }
-      SegScan<TG, NA, V, GL>::template up_level<1>(tg, A, X);
-      float Ae[NA], Xe[V];
-#pragma unroll
-      for (int i = 0; i < NA; ++i) {
-        const float t = shift_up<TG, 1>(A[i]);
-        Ae[i] = tg == 0 ? 1.0f : t;
-      }
-#pragma unroll
-      for (int v = 0; v < V; ++v) {
-        const float t = shift_up<TG, 1>(X[v]);
-        Xe[v] = tg == 0 ? 0.0f : t;
-      }
-      if (tg == TG - 1) {
-#pragma unroll
-        for (int i = 0; i < NA; ++i) lds_fa[w][cl][i] = A[i];
-#pragma unroll
-        for (int q = 0; q < V / 4; ++q)
-          lds_fx[w][cl][q] = make_float4(X[4 * q], X[4 * q + 1], X[4 * q + 2], X[4 * q + 3]);
-      }
-      __syncthreads();  // (1)
-      for (int ww = 0; ww < w; ++ww) {
-        float Aw[NA];
-#pragma unroll
-        for (int i = 0; i < NA; ++i) Aw[i] = lds_fa[ww][cl][i];
-#pragma unroll
-        for (int q = 0; q < V / 4; ++q) {
-          const float4 x4 = lds_fx[ww][cl][q];
-          hc[4 * q + 0] = fmaf(Aw[GL ? 0 : 4 * q + 0], hc[4 * q + 0], x4.x);
-          hc[4 * q + 1] = fmaf(Aw[GL ? 0 : 4 * q + 1], hc[4 * q + 1], x4.y);
-          hc[4 * q + 2] = fmaf(Aw[GL ? 0 : 4 * q + 2], hc[4 * q + 2], x4.z);
-          hc[4 * q + 3] = fmaf(Aw[GL ? 0 : 4 * q + 3], hc[4 * q + 3], x4.w);
-        }
-      }
-      reload_barrier(uq);
-      float hv[V];
-#pragma unroll
-      for (int v = 0; v < V; ++v) hv[v] = fmaf(Ae[GL ? 0 : v], hc[v], Xe[v]);
-#pragma unroll
-      for (int s = 0; s < L; ++s) {
-        hq[s] = Pack<TIO>::pack(hv);
-        if (s + 1 < L) {
-#pragma unroll
-          for (int v = 0; v < V; ++v) {
-            const float a = al[s][GL ? 0 : v];
-            hv[v] = fmaf(a, Pack<TIO>::get(uq[s], v) - hv[v], hv[v]);
-          }
-        }
-      }
-    }
+    nl.gates(gi, t0, S.T, active, use_sig, al);
+    if (it > it_lo) load_tile(it - 1);
 
     // ---- reverse scan: g_t = gy_t + (1 - alpha_{t+1}) g_{t+1}
     // decay carrying g_{t+1} into g_t; zero for the last step of the sequence
@@ -859,7 +815,121 @@ scan_bwd_kernel(const BwdArgs args) {
       for (int ww = 0; ww < NW; ++ww)
         for (int q = 0; q < TG; ++q) acc += lds_red[ww * 64 + lcl * TG + q][k];
     }
-    args.dbias_partial[((int64_t)b * S.H + h) * S.Da + j] = acc;
+    args.dbias_partial[((int64_t)bh * args.nchunk + chunk) * S.Da + j] = acc;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Time-chunked backward.  Within a chunk [ts, te) the reverse recurrence maps
+// the gradient entering from the chunk's end affinely onto its first step:
+//   g_ts = A g_te + G,   A = prod_{t=ts}^{te-1} (1 - alpha_{t+1}),
+// with alpha_T taken as 1 (g_T = 0).  scan_bwd_agg_kernel computes (A, G) per
+// (b, h, chunk, channel) from gy and the logits alone; scan_bwd_carry_kernel
+// composes the maps of the later chunks, last to first, into each chunk's
+// carry g_te; the tile kernel then runs all chunks independently.  The
+// sequence of a (b, h) is one thread per channel vector and chunk, walking its
+// steps in reverse (V channels per lane: one 16-byte gy load per step).
+// ---------------------------------------------------------------------------
+template <typename TIO, bool VEC>
+__global__ void __launch_bounds__(256) scan_bwd_agg_kernel(const BwdArgs args) {
+  constexpr int V = Pack<TIO>::V;
+  const ScanShape& S = args.sh;
+  const int ncl = (S.D + V - 1) / V;
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (int64_t)S.B * S.H * args.nchunk * ncl) return;
+  const int cl = (int)(idx % ncl);
+  const int64_t rest = idx / ncl;
+  const int chunk = (int)(rest % args.nchunk);
+  const int bh = (int)(rest / args.nchunk);
+  const int h = bh % S.H, b = bh / S.H;
+  const int c0 = cl * V;
+  const int nvalid = min(V, S.D - c0);
+
+  int which, hl;
+  head_select(h, S.NH, S.NKVH, which, hl);
+  const int64_t* gs = args.gy.s[which];
+  const TIO* gp = reinterpret_cast<const TIO*>(args.gy.p[which]) + (int64_t)b * gs[0] +
+                  (int64_t)hl * gs[1] + (int64_t)c0 * gs[3];
+  const TIO* lp = reinterpret_cast<const TIO*>(args.lg.p) + (int64_t)b * args.lg.s[0] +
+                  (int64_t)h * args.lg.s[1];
+  const int64_t lst = args.lg.s[2];
+  const bool use_sig = S.use_sigmoid != 0;
+  int64_t loff[V];
+  float bias[V];
+#pragma unroll
+  for (int v = 0; v < V; ++v) {
+    const int j = min(c0 + v, S.D - 1) / S.r;
+    loff[v] = (int64_t)j * args.lg.s[3];
+    bias[v] = args.bias[h * S.Da + j];
+  }
+  const bool one_gate = S.r % V == 0;  // every channel of the lane in one gate group
+  auto decay = [&](int t, float (&an)[V]) {  // 1 - alpha_t, 0 past the sequence end
+    if (t >= S.T) {
+#pragma unroll
+      for (int v = 0; v < V; ++v) an[v] = 0.0f;
+    } else if (one_gate) {
+      const float a = gate_alpha(Pack<TIO>::load1(lp + (int64_t)t * lst + loff[0]) + bias[0],
+                                 use_sig);
+#pragma unroll
+      for (int v = 0; v < V; ++v) an[v] = 1.0f - a;
+    } else {
+#pragma unroll
+      for (int v = 0; v < V; ++v)
+        an[v] = 1.0f - gate_alpha(Pack<TIO>::load1(lp + (int64_t)t * lst + loff[v]) + bias[v],
+                                  use_sig);
+    }
+  };
+
+  const int ts = chunk * args.chunk_steps;
+  const int te = min(S.T, ts + args.chunk_steps);
+  float A[V], G[V], an[V];
+#pragma unroll
+  for (int v = 0; v < V; ++v) {
+    A[v] = 1.0f;
+    G[v] = 0.0f;
+  }
+  decay(te, an);
+  // blocks of KB steps, newest first: all of a block's loads are issued before
+  // its (sequential) arithmetic, so the walk is not one load latency per step
+  constexpr int KB = 16;
+  for (int tb = te; tb > ts; tb -= KB) {
+    uint4 q[KB];
+    float lraw[KB];
+#pragma unroll
+    for (int k = 0; k < KB; ++k) {
+      const int t = tb - 1 - k;
+      const bool ok = t >= ts;
+      q[k] = ok ? ld_vec<TIO, VEC>(gp + (int64_t)t * gs[2], gs[3], nvalid)
+                : make_uint4(0u, 0u, 0u, 0u);
+      lraw[k] = ok && one_gate ? Pack<TIO>::load1(lp + (int64_t)t * lst + loff[0]) : 0.0f;
+    }
+#pragma unroll
+    for (int k = 0; k < KB; ++k) {
+      const int t = tb - 1 - k;
+      if (t >= ts) {
+#pragma unroll
+        for (int v = 0; v < V; ++v) {
+          G[v] = fmaf(an[v], G[v], Pack<TIO>::get(q[k], v));
+          A[v] *= an[v];
+        }
+        if (one_gate) {
+          const float a = gate_alpha(lraw[k] + bias[0], use_sig);
+#pragma unroll
+          for (int v = 0; v < V; ++v) an[v] = 1.0f - a;
+        } else {
+          decay(t, an);
+        }
+      }
+    }
+  }
+  const int64_t o = ((int64_t)bh * args.nchunk + chunk) * S.D + c0;
+  const int64_t plane = (int64_t)S.B * S.H * args.nchunk * S.D;
+#pragma unroll
+  for (int v = 0; v < V; ++v) {
+    if (v < nvalid) {
+      args.agg[o + v] = A[v];
+      args.agg[plane + o + v] = G[v];
+    }
   }
 }
 
@@ -962,6 +1032,7 @@ int scan_launch_bwd(bool bf16, const BwdArgs& a, ScanCfg cfg, int grid, bool vec
 // Backward for gate groups outside the main kernel's reduction patterns.
 int scan_launch_bwd_channel(bool bf16, const BwdArgs& a, float* dalpha_ws, hipStream_t st);
 // dbias[h, j] = sum_b partial[b, h, j]
-int scan_launch_dbias_reduce(const float* partial, float* dbias, int B, int HDa, hipStream_t st);
+int scan_launch_dbias_reduce(const float* partial, float* dbias, int B, int H, int NC, int Da,
+                             hipStream_t st);
 
 }  // namespace ltv
