@@ -69,20 +69,41 @@ int scan_launch_bwd_channel(bool bf16, const BwdArgs& a, float* dalpha, hipStrea
   return LTV_OK;
 }
 
-// carry[bh, k, c] = g entering chunk k from its end: the maps of chunks
-// nchunk - 1, ..., k + 1 applied to 0, in that order.
+// carry[bh, k, c] = g entering chunk k from its end: the maps of the
+// sub-chunks after chunk k applied to 0, last to first.  One thread per
+// (b h, channel); the maps are read in batches so the walk is not one load
+// latency per sub-chunk.
 __global__ void __launch_bounds__(256) scan_bwd_carry_kernel(const BwdArgs args) {
   const ScanShape& S = args.sh;
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= (int64_t)S.B * S.H * S.D) return;
   const int c = (int)(idx % S.D);
   const int64_t bh = idx / S.D;
-  const int64_t plane = (int64_t)S.B * S.H * args.nchunk * S.D;
+  const int64_t plane = (int64_t)S.B * S.H * args.nfine * S.D;
+  const int fpc = args.chunk_steps / args.fine_steps;  // sub-chunks per chunk
+  const float* ap = args.agg + bh * args.nfine * S.D + c;
+  float* cp = args.carry + bh * args.nchunk * S.D + c;
+  cp[(int64_t)(args.nchunk - 1) * S.D] = 0.0f;
   float g = 0.0f;
-  for (int k = args.nchunk - 1; k >= 0; --k) {
-    const int64_t i = (bh * args.nchunk + k) * S.D + c;
-    args.carry[i] = g;
-    g = fmaf(args.agg[i], g, args.agg[plane + i]);
+  constexpr int KB = 16;
+  for (int fb = args.nfine; fb > 0; fb -= KB) {
+    float A[KB], G[KB];
+#pragma unroll
+    for (int q = 0; q < KB; ++q) {
+      const int f = fb - 1 - q;
+      A[q] = f >= 0 ? ap[(int64_t)f * S.D] : 1.0f;
+      G[q] = f >= 0 ? ap[plane + (int64_t)f * S.D] : 0.0f;
+    }
+#pragma unroll
+    for (int q = 0; q < KB; ++q) {
+      const int f = fb - 1 - q;
+      if (f >= 0) {
+        // f is the last sub-chunk of chunk k = f / fpc: g is that chunk's carry
+        const int k = f / fpc;
+        if ((f + 1) % fpc == 0 && k < args.nchunk - 1) cp[(int64_t)k * S.D] = g;
+        g = fmaf(A[q], g, G[q]);
+      }
+    }
   }
 }
 
@@ -90,7 +111,7 @@ __global__ void __launch_bounds__(256) scan_bwd_carry_kernel(const BwdArgs args)
 int scan_launch_bwd_chunk_maps(bool bf16, const BwdArgs& a, bool vec, hipStream_t st) {
   const ScanShape& S = a.sh;
   const int V = bf16 ? 8 : 4;
-  const int64_t n = (int64_t)S.B * S.H * a.nchunk * ((S.D + V - 1) / V);
+  const int64_t n = (int64_t)S.B * S.H * a.nfine * ((S.D + V - 1) / V);
   const int blocks = (int)((n + 255) / 256);
   if (bf16) {
     if (vec)
@@ -253,6 +274,9 @@ int bwd_max_chunks(int B, int H, int T) {
   return std::max(1, std::min(nc, cap));
 }
 
+// Sub-chunk length of the backward's chunk maps (steps).
+constexpr int kBwdFineSteps = 64;
+
 struct BwdWorkspace {
   size_t partial = 0, agg = 0, carry = 0, dalpha = 0, total = 0;  // byte offsets
 };
@@ -267,7 +291,7 @@ BwdWorkspace bwd_workspace_plan(int dtype, int B, int T, int NH, int NKVH, int D
   size_t off = al((size_t)B * H * NC * Da * sizeof(float));
   if (NC > 1) {
     w.agg = off;
-    off += al((size_t)2 * B * H * NC * D * sizeof(float));
+    off += al((size_t)2 * B * H * ((T + kBwdFineSteps - 1) / kBwdFineSteps) * D * sizeof(float));
     w.carry = off;
     off += al((size_t)B * H * NC * D * sizeof(float));
   }
@@ -335,6 +359,8 @@ int scan_backward_impl(int dtype, const HostView4& u, const HostView4& lg, const
   a.dbias_partial = reinterpret_cast<float*>(wsb + wp.partial);
   a.nchunk = 1;
   a.chunk_steps = T;
+  a.nfine = 1;
+  a.fine_steps = T;
   a.agg = nullptr;
   a.carry = nullptr;
 
@@ -354,11 +380,16 @@ int scan_backward_impl(int dtype, const HostView4& u, const HostView4& lg, const
     }
     // time chunks of whole tiles; each chunk enters with its exact gradient
     // carry from the chunk-map kernels
+    // (TW and the sub-chunk length are powers of two: the larger is a multiple
+    // of the smaller)
     const int TW = cfg.NW * (64 / cfg.CL) * cfg.L;
+    const int unit = std::max(TW, kBwdFineSteps);
     const int nc_max = bwd_max_chunks(B, H, T);
     const int per = (T + nc_max - 1) / nc_max;
-    a.chunk_steps = (per + TW - 1) / TW * TW;
+    a.chunk_steps = (per + unit - 1) / unit * unit;
     a.nchunk = (T + a.chunk_steps - 1) / a.chunk_steps;
+    a.fine_steps = kBwdFineSteps;
+    a.nfine = (T + kBwdFineSteps - 1) / kBwdFineSteps;
     const int64_t grid = (int64_t)B * H * a.nchunk;
     LTV_REQUIRE(grid < (1ll << 31), LTV_ERR_UNSUPPORTED, "grid too large");
     if (a.nchunk > 1) {

@@ -55,6 +55,22 @@ struct OutHeads {
   int64_t s[3][4];  // element strides (b, h_local, t, d)
 };
 
+// One of the q / k / v members of an OutHeads, picked with selects: indexing
+// the argument block with the run-time head group makes the compiler re-read
+// the strides from memory (and wait for them) before every use.
+struct HeadView {
+  void* p;
+  int64_t s[4];
+};
+
+__device__ __forceinline__ HeadView head_view(const OutHeads& o, int which) {
+  HeadView r;
+  r.p = which == 0 ? o.p[0] : which == 1 ? o.p[1] : o.p[2];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) r.s[k] = which == 0 ? o.s[0][k] : which == 1 ? o.s[1][k] : o.s[2][k];
+  return r;
+}
+
 struct ScanShape {
   int B, T, NH, NKVH, Da, r, D, H;
   int nslab;  // channel slabs per head (forward only)
@@ -87,7 +103,10 @@ struct BwdArgs {
   // gradient carry g at the chunk's end from `carry` (B H, nchunk, D); with
   // nchunk == 1 the carry is 0 and `carry` is unused.
   int nchunk, chunk_steps;
-  float* agg;          // (2, B H, nchunk, D): each chunk's map g_start = A g_end + G
+  // The chunk maps are formed over finer sub-chunks of fine_steps steps (a
+  // divisor of chunk_steps), nfine per sequence, for parallelism.
+  int nfine, fine_steps;
+  float* agg;          // (2, B H, nfine, D): each sub-chunk's map g_start = A g_end + G
   float* carry;        // (B H, nchunk, D)
 };
 
@@ -353,9 +372,10 @@ scan_fwd_kernel(const FwdArgs args) {
 
   int which, hl;
   head_select(h, S.NH, S.NKVH, which, hl);
-  TIO* outp = reinterpret_cast<TIO*>(args.out.p[which]);
-  const int64_t* os = args.out.s[which];
-  outp += (int64_t)b * os[0] + (int64_t)hl * os[1] + (int64_t)c0 * os[3];
+  const HeadView ov = head_view(args.out, which);
+  const int64_t os[4] = {ov.s[0], ov.s[1], ov.s[2], ov.s[3]};
+  TIO* outp = reinterpret_cast<TIO*>(ov.p) + (int64_t)b * os[0] + (int64_t)hl * os[1] +
+              (int64_t)c0 * os[3];
 
   const TIO* up = reinterpret_cast<const TIO*>(args.u.p) + (int64_t)b * args.u.s[0] +
                   (int64_t)h * args.u.s[1] + (int64_t)c0 * args.u.s[3];
@@ -525,11 +545,12 @@ scan_bwd_kernel(const BwdArgs args) {
 
   int which, hl;
   head_select(h, S.NH, S.NKVH, which, hl);
-  const int64_t* hs = args.h.s[which];
-  const TIO* hp = reinterpret_cast<const TIO*>(args.h.p[which]) + (int64_t)b * hs[0] +
+  const HeadView hvw = head_view(args.h, which), gvw = head_view(args.gy, which);
+  const int64_t hs[4] = {hvw.s[0], hvw.s[1], hvw.s[2], hvw.s[3]};
+  const int64_t gs[4] = {gvw.s[0], gvw.s[1], gvw.s[2], gvw.s[3]};
+  const TIO* hp = reinterpret_cast<const TIO*>(hvw.p) + (int64_t)b * hs[0] +
                   (int64_t)hl * hs[1] + (int64_t)c0 * hs[3];
-  const int64_t* gs = args.gy.s[which];
-  const TIO* gp = reinterpret_cast<const TIO*>(args.gy.p[which]) + (int64_t)b * gs[0] +
+  const TIO* gp = reinterpret_cast<const TIO*>(gvw.p) + (int64_t)b * gs[0] +
                   (int64_t)hl * gs[1] + (int64_t)c0 * gs[3];
   const TIO* up = reinterpret_cast<const TIO*>(args.u.p) + (int64_t)b * args.u.s[0] +
                   (int64_t)h * args.u.s[1] + (int64_t)c0 * args.u.s[3];
@@ -824,11 +845,11 @@ scan_bwd_kernel(const BwdArgs args) {
 // the gradient entering from the chunk's end affinely onto its first step:
 //   g_ts = A g_te + G,   A = prod_{t=ts}^{te-1} (1 - alpha_{t+1}),
 // with alpha_T taken as 1 (g_T = 0).  scan_bwd_agg_kernel computes (A, G) per
-// (b, h, chunk, channel) from gy and the logits alone; scan_bwd_carry_kernel
-// composes the maps of the later chunks, last to first, into each chunk's
-// carry g_te; the tile kernel then runs all chunks independently.  The
-// sequence of a (b, h) is one thread per channel vector and chunk, walking its
-// steps in reverse (V channels per lane: one 16-byte gy load per step).
+// (b, h, sub-chunk, channel) from gy and the logits alone, one thread per
+// channel vector and sub-chunk walking its steps in reverse (V channels per
+// lane: one 16-byte gy load per step); scan_bwd_carry_kernel composes the maps
+// of the later sub-chunks, last to first, into each chunk's carry g_te; the
+// tile kernel then runs all chunks independently.
 // ---------------------------------------------------------------------------
 template <typename TIO, bool VEC>
 __global__ void __launch_bounds__(256) scan_bwd_agg_kernel(const BwdArgs args) {
@@ -836,19 +857,20 @@ __global__ void __launch_bounds__(256) scan_bwd_agg_kernel(const BwdArgs args) {
   const ScanShape& S = args.sh;
   const int ncl = (S.D + V - 1) / V;
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= (int64_t)S.B * S.H * args.nchunk * ncl) return;
+  if (idx >= (int64_t)S.B * S.H * args.nfine * ncl) return;
   const int cl = (int)(idx % ncl);
   const int64_t rest = idx / ncl;
-  const int chunk = (int)(rest % args.nchunk);
-  const int bh = (int)(rest / args.nchunk);
+  const int chunk = (int)(rest % args.nfine);
+  const int bh = (int)(rest / args.nfine);
   const int h = bh % S.H, b = bh / S.H;
   const int c0 = cl * V;
   const int nvalid = min(V, S.D - c0);
 
   int which, hl;
   head_select(h, S.NH, S.NKVH, which, hl);
-  const int64_t* gs = args.gy.s[which];
-  const TIO* gp = reinterpret_cast<const TIO*>(args.gy.p[which]) + (int64_t)b * gs[0] +
+  const HeadView gvw = head_view(args.gy, which);
+  const int64_t gs[4] = {gvw.s[0], gvw.s[1], gvw.s[2], gvw.s[3]};
+  const TIO* gp = reinterpret_cast<const TIO*>(gvw.p) + (int64_t)b * gs[0] +
                   (int64_t)hl * gs[1] + (int64_t)c0 * gs[3];
   const TIO* lp = reinterpret_cast<const TIO*>(args.lg.p) + (int64_t)b * args.lg.s[0] +
                   (int64_t)h * args.lg.s[1];
@@ -880,8 +902,8 @@ __global__ void __launch_bounds__(256) scan_bwd_agg_kernel(const BwdArgs args) {
     }
   };
 
-  const int ts = chunk * args.chunk_steps;
-  const int te = min(S.T, ts + args.chunk_steps);
+  const int ts = chunk * args.fine_steps;
+  const int te = min(S.T, ts + args.fine_steps);
   float A[V], G[V], an[V];
 #pragma unroll
   for (int v = 0; v < V; ++v) {
@@ -922,8 +944,8 @@ __global__ void __launch_bounds__(256) scan_bwd_agg_kernel(const BwdArgs args) {
       }
     }
   }
-  const int64_t o = ((int64_t)bh * args.nchunk + chunk) * S.D + c0;
-  const int64_t plane = (int64_t)S.B * S.H * args.nchunk * S.D;
+  const int64_t o = ((int64_t)bh * args.nfine + chunk) * S.D + c0;
+  const int64_t plane = (int64_t)S.B * S.H * args.nfine * S.D;
 #pragma unroll
   for (int v = 0; v < V; ++v) {
     if (v < nvalid) {
@@ -950,11 +972,11 @@ __global__ void scan_bwd_channel_kernel(const BwdArgs args, float* __restrict__ 
   const int b = (int)(idx / ((int64_t)S.D * S.H));
   int which, hl;
   head_select(h, S.NH, S.NKVH, which, hl);
-  const TIO* hp = reinterpret_cast<const TIO*>(args.h.p[which]) + (int64_t)b * args.h.s[which][0] +
-                  (int64_t)hl * args.h.s[which][1] + (int64_t)c * args.h.s[which][3];
-  const TIO* gp = reinterpret_cast<const TIO*>(args.gy.p[which]) +
-                  (int64_t)b * args.gy.s[which][0] + (int64_t)hl * args.gy.s[which][1] +
-                  (int64_t)c * args.gy.s[which][3];
+  const HeadView hvw = head_view(args.h, which), gvw = head_view(args.gy, which);
+  const TIO* hp = reinterpret_cast<const TIO*>(hvw.p) + (int64_t)b * hvw.s[0] +
+                  (int64_t)hl * hvw.s[1] + (int64_t)c * hvw.s[3];
+  const TIO* gp = reinterpret_cast<const TIO*>(gvw.p) + (int64_t)b * gvw.s[0] +
+                  (int64_t)hl * gvw.s[1] + (int64_t)c * gvw.s[3];
   const TIO* up = reinterpret_cast<const TIO*>(args.u.p) + (int64_t)b * args.u.s[0] +
                   (int64_t)h * args.u.s[1] + (int64_t)c * args.u.s[3];
   TIO* dup = reinterpret_cast<TIO*>(const_cast<void*>(args.du.p)) + (int64_t)b * args.du.s[0] +
@@ -967,7 +989,7 @@ __global__ void scan_bwd_channel_kernel(const BwdArgs args, float* __restrict__ 
   float g = 0.0f, a_next = 0.0f;
   for (int t = S.T - 1; t >= 0; --t) {
     const float alpha = gate_alpha(Pack<TIO>::load1(lp + (int64_t)t * args.lg.s[2]) + bias, use_sig);
-    g = fmaf(a_next, g, Pack<TIO>::load1(gp + (int64_t)t * args.gy.s[which][2]));
+    g = fmaf(a_next, g, Pack<TIO>::load1(gp + (int64_t)t * gvw.s[2]));
     Pack<TIO>::store1(dup + (int64_t)t * args.du.s[2], alpha * g);
     float hprev;
     if (t == 0) {
@@ -979,7 +1001,7 @@ __global__ void scan_bwd_channel_kernel(const BwdArgs args, float* __restrict__ 
                  (int64_t)c * args.dinit.s[3];
       Pack<TIO>::store1(dip, (1.0f - alpha) * g);
     } else {
-      hprev = Pack<TIO>::load1(hp + (int64_t)(t - 1) * args.h.s[which][2]);
+      hprev = Pack<TIO>::load1(hp + (int64_t)(t - 1) * hvw.s[2]);
     }
     const float da = (Pack<TIO>::load1(up + (int64_t)t * args.u.s[2]) - hprev) * g;
     dalpha_ws[(((int64_t)b * S.H + h) * S.T + t) * S.D + c] = da;
