@@ -206,6 +206,28 @@ int ltv_qkv_project_backward_weight(const void* x, const void* grad_combined,
                                     float* grad_weight, void* workspace, size_t workspace_bytes,
                                     int M, int C, int H, int D, int Da, void* stream);
 
+/* ----------------------------------------------------------------------
+ * Decode (T = 1), fused: one launch computes the projection of the B new
+ * tokens and one step of the recurrence from each head's previous output row.
+ *   x          : (B, C) bf16, rows x_row_stride elements apart (a multiple of 8)
+ *   wpack      : the packed bf16 weight from ltv_qkv_pack_weight
+ *   prev_q/k/v : previous output rows (B, NH, D), (B, NKVH, D), (B, NKVH, D) bf16,
+ *                channel stride 1; prev_strides = {q_b, q_h, k_b, k_h, v_b, v_h}
+ *   logit_bias : (H, Da) fp32;  out : (B, H, D) bf16 contiguous (overwritten)
+ * The values and gate logits are rounded to bf16 exactly where the projection
+ * stores them, and the step is the scan's h + alpha (u - h), so a decode step
+ * matches the same step of a full recompute up to fp32 summation order in the
+ * projection.  Requires C % 16 == 0.
+ * Counterpart in the reference: its decode runs the general filter forward
+ * with T = 1 (nanochat/ltv_cuda_fused_concat_head_major_register_cast_blelloch_
+ * scan_qkv_filter.py:24-73) on the KV cache's last rows
+ * (nanochat/ltv_combined_qkv_computer_module.py:28-41).
+ * ---------------------------------------------------------------------- */
+int ltv_qkv_decode_step(const void* x, int64_t x_row_stride, const void* wpack,
+                        const void* prev_q, const void* prev_k, const void* prev_v,
+                        const int64_t prev_strides[6], const float* logit_bias, void* out, int B,
+                        int C, int NH, int NKVH, int D, int Da, int use_sigmoid, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

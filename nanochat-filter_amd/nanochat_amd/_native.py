@@ -87,6 +87,11 @@ SIGNATURES = {
         _c_int,
         [_c_vp, _c_vp, _c_vp, _c_vp, _c_sz, _c_int, _c_int, _c_int, _c_int, _c_int, _c_vp],
     ),
+    "ltv_qkv_decode_step": (
+        _c_int,
+        [_c_vp, ctypes.c_int64, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64p, _c_vp, _c_vp,
+         _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_vp],
+    ),
 }
 
 _lib = None

@@ -15,6 +15,9 @@ asks for float32, otherwise in the dtype of ``x``.
   * fp32: the reference-layout ops ``fused_linear_transpose`` (B, F, T) and the
     ``nanochat_cuda`` scan op read through the transposed (B, T, F) view,
     exactly the reference's dataflow.
+  * bf16 decode (one token per sequence, no autograd): one fused launch,
+    ``ltv_qkv_decode_step``, from the previous rows the KV cache feeds back
+    (or ``init_param``), with the packed bf16 weight reused across steps.
 """
 
 import torch
@@ -32,6 +35,7 @@ from nanochat_amd.ltv_fused_concat_register_cast_scan_util import (
     _R_THREADS_BACKWARD,
     _R_ITEMS_BACKWARD,
 )
+from nanochat_amd.ops import ltv_hm_fast as hm_fast
 from nanochat_amd.ops.ltv_cuda_ops import (
     fused_linear_transpose,
     ltv_cuda_fused_concat_head_major_register_cast_blelloch_scan,
@@ -48,6 +52,8 @@ class LtvCudaFusedConcatHeadMajorRegisterCastBlellochScanQkvFilter(
             autocast_dtype == torch.float32 if CUDA_SUPPORTS_NATIVE_BF16 else True
         )
         compute_dtype = torch.float32 if run_ltv_in_fp32 else x.dtype
+        if compute_dtype == torch.bfloat16 and x.size(1) == 1 and not torch.is_grad_enabled():
+            return self._decode_bf16(x, previous_values)
         inits = resolve_inits_original_dtype(B, self.init_param, previous_values)
         if compute_dtype == torch.bfloat16:
             return self._forward_bf16(x, inits)
@@ -67,6 +73,37 @@ class LtvCudaFusedConcatHeadMajorRegisterCastBlellochScanQkvFilter(
             self.r,
         )
         return hq.transpose(1, 2), hk.transpose(1, 2), hv.transpose(1, 2)
+
+    def _packed_weight(self):
+        """The bf16 packed weight, reused until ``c.weight`` changes (any in-place
+        update, e.g. an optimizer step or ``load_state_dict``, bumps its version)."""
+        w = self.c.weight
+        key = (w.data_ptr(), w._version, w.dtype, w.device)
+        cached = getattr(self, "_wpack_cache", None)
+        if cached is None or cached[0] != key:
+            H = self.n_head + 2 * self.n_kv_head
+            wpack = hm_fast.pack_weight(w.detach(), H, self.head_dim, self.num_alpha_groups)
+            cached = (key, wpack)
+            self._wpack_cache = cached
+        return cached[1]
+
+    def _decode_bf16(self, x, previous_values):
+        """T = 1 inference: one fused launch (projection of the new tokens and one
+        recurrence step from the previous rows)."""
+        B = x.size(0)
+        NH, NKVH = self.n_head, self.n_kv_head
+        if previous_values.q is not None:
+            prev = (previous_values.q, previous_values.k, previous_values.v)
+        else:
+            ip = self.init_param.detach().to(torch.bfloat16)
+            prev = (ip[:NH].unsqueeze(0).expand(B, -1, -1),
+                    ip[NH:NH + NKVH].unsqueeze(0).expand(B, -1, -1),
+                    ip[NH + NKVH:].unsqueeze(0).expand(B, -1, -1))
+        out = hm_fast.decode_step(x.to(torch.bfloat16), self._packed_weight(), prev,
+                                  self.logit_bias.detach().float().contiguous(), NH, NKVH,
+                                  self.num_alpha_groups, self.r)
+        return (out[:, :NH].unsqueeze(1), out[:, NH:NH + NKVH].unsqueeze(1),
+                out[:, NH + NKVH:].unsqueeze(1))
 
     def _forward_fp32(self, x, inits):
         out_buf = fused_linear_transpose(x.float().contiguous(), self.c.weight.float().contiguous())

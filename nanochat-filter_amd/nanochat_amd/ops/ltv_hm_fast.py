@@ -25,7 +25,9 @@ Ops in the ``nanochat_amd`` namespace, each with a fake implementation:
 
 The helpers ``project``, ``project_backward``, ``scan_forward`` and
 ``scan_backward`` call the library directly; the tests use them to check each
-stage on its own.
+stage on its own.  ``decode_step`` is the fused T = 1 inference step (one
+launch: projection of the new tokens plus one recurrence step from the previous
+rows), with ``pack_weight`` giving the weight operand it reuses across steps.
 """
 
 from __future__ import annotations
@@ -81,6 +83,61 @@ def project(x: torch.Tensor, weight: torch.Tensor, H: int, D: int, Da: int):
                                          logits.data_ptr(), B, T, C, H, D, Da, st)
     N.check(rc, "ltv_qkv_project_forward")
     return values, logits, wpack
+
+
+def pack_weight(weight: torch.Tensor, H: int, D: int, Da: int) -> torch.Tensor:
+    """weight (F, C) fp32/bf16 -> the packed bf16 (Fp, C) MFMA operand."""
+    N.require_device(weight)
+    F, C = weight.shape
+    if F != H * (D + Da):
+        raise RuntimeError(f"weight must have {H * (D + Da)} rows, got {F}")
+    weight = weight.contiguous()
+    wpack = torch.empty((packed_width(H, D, Da), C), dtype=torch.bfloat16, device=weight.device)
+    with N.span("pack_weight"):
+        rc = N.lib().ltv_qkv_pack_weight(N.dtype_code(weight.dtype), weight.data_ptr(),
+                                         wpack.data_ptr(), H, D, Da, C, N.stream_of(weight))
+    N.check(rc, "ltv_qkv_pack_weight")
+    return wpack
+
+
+def decode_step(x: torch.Tensor, wpack: torch.Tensor, prev, logit_bias: torch.Tensor, NH: int,
+                NKVH: int, Da: int, r: int, use_sigmoid: bool = True) -> torch.Tensor:
+    """One fused decode step: x (B, C) or (B, 1, C) bf16, the packed weight, the
+    previous output rows ``prev = (q (B, NH, D), k (B, NKVH, D), v (B, NKVH, D))``
+    bf16 with channel stride 1 -> the new rows (B, H, D) bf16, contiguous."""
+    if x.dim() == 3:
+        if x.shape[1] != 1:
+            raise RuntimeError(f"decode_step takes one token per sequence, got x {tuple(x.shape)}")
+        x = x[:, 0]
+    N.require_device(x, wpack, logit_bias, *prev)
+    if x.dtype != torch.bfloat16 or wpack.dtype != torch.bfloat16:
+        raise RuntimeError("decode_step computes in bf16")
+    B, C = x.shape
+    D = Da * r
+    H = NH + 2 * NKVH
+    if x.stride(1) != 1 or x.stride(0) % 8 != 0:
+        x = x.contiguous()
+    rows = []
+    for t, nh in zip(prev, (NH, NKVH, NKVH)):
+        if t.dtype != torch.bfloat16:
+            t = t.to(torch.bfloat16)
+        if tuple(t.shape) != (B, nh, D):
+            raise RuntimeError(f"previous rows must be {(B, nh, D)}, got {tuple(t.shape)}")
+        if t.stride(2) != 1:
+            t = t.contiguous()
+        rows.append(t)
+    if logit_bias.dtype != torch.float32 or not logit_bias.is_contiguous():
+        raise RuntimeError("logit_bias must be contiguous float32")
+    out = torch.empty((B, H, D), dtype=torch.bfloat16, device=x.device)
+    strides = _arr([s for t in rows for s in t.stride()[:2]])
+    with N.span("qkv_decode"):
+        rc = N.lib().ltv_qkv_decode_step(x.data_ptr(), x.stride(0), wpack.data_ptr(),
+                                         rows[0].data_ptr(), rows[1].data_ptr(),
+                                         rows[2].data_ptr(), strides, logit_bias.data_ptr(),
+                                         out.data_ptr(), B, C, NH, NKVH, D, Da,
+                                         int(use_sigmoid), N.stream_of(x))
+    N.check(rc, "ltv_qkv_decode_step")
+    return out
 
 
 def project_backward(x: torch.Tensor, wpack: torch.Tensor, grad_combined: torch.Tensor, H: int,

@@ -1,0 +1,182 @@
+"""GPU parity of the decode (KV-cache) path: one token per sequence, no autograd.
+
+The fused ``ltv_qkv_decode_step`` is pinned three ways:
+* one step against the CPU oracle (``filter_forward`` at T = 1 from the same
+  previous rows) and against the general GPU path at T = 1;
+* a chain of decode steps through ``LtvCombinedQkvComputerModule`` and a KV
+  cache (the reference protocol, ``ltv_combined_qkv_computer_module.py:28-41``)
+  against the same chain on the general path: both carry the state as the bf16
+  output row, so they agree to bf16 rounding;
+* config 5's decode (B = 64, 256 steps after a prefill) against a full
+  recompute of the whole sequence.  The cache holds bf16 rows, so every decode
+  step re-quantises the state that the full scan keeps in fp32; with a constant
+  decay a = 1 - alpha the difference is bounded by 2^-9 max|h| / alpha (the
+  bound of the reference's own decode), which the test asserts.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import ltv_oracle as O
+from ltv_test_utils import assert_close, np_of
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+TOL = 2e-2
+
+
+def _make_filter(NH, NKVH, D, r, seed=0, gate_scale=1.0, bias=(-0.5, 0.5)):
+    from nanochat_amd.ltv_cuda_fused_concat_head_major_register_cast_blelloch_scan_qkv_filter import (
+        LtvCudaFusedConcatHeadMajorRegisterCastBlellochScanQkvFilter as Filter,
+    )
+    torch.manual_seed(seed)
+    f = Filter(NH, NKVH, D, r)
+    C = NH * D  # the filter's input width is n_head * head_dim
+    Da = D // r
+    H = NH + 2 * NKVH
+    assert f.c.weight.shape == (H * (D + Da), C)
+    with torch.no_grad():
+        f.c.weight.normal_(0.0, C ** -0.5)
+        w = f.c.weight.view(H, D + Da, C)
+        w[:, D:, :] *= gate_scale
+        f.logit_bias.uniform_(*bias)
+        f.init_param.uniform_(-0.5, 0.5)
+    return f.to(DEV)
+
+
+class _Cache:
+    """The slice of nanochat's KV cache the filter uses (kv_cache.py:212-294)."""
+
+    class _Slot:
+        def __init__(self):
+            self.special = {}
+
+    class _Last:
+        def __init__(self):
+            self.q, self.k, self.v = _Cache._Slot(), _Cache._Slot(), _Cache._Slot()
+
+    def __init__(self):
+        self.last_qkv = _Cache._Last()
+
+    def has_last_qkv(self, layer):
+        return layer in self.last_qkv.q.special
+
+    def update_last_qkv(self, layer, q, k, v):
+        self.last_qkv.q.special[layer] = q
+        self.last_qkv.k.special[layer] = k
+        self.last_qkv.v.special[layer] = v
+
+    def __bool__(self):
+        return True
+
+
+def _general_step(f, x, prev):
+    """The general (autograd-capable) path at T = 1: projection GEMM + scan."""
+    from nanochat_amd.ltv.ltv_filter import LtvInitValues
+    with torch.enable_grad():
+        q, k, v = f(x, prev if prev is not None else LtvInitValues())
+    return q.detach(), k.detach(), v.detach()
+
+
+@pytest.mark.parametrize("NH,NKVH,D,r,B", [(6, 6, 128, 128, 64), (4, 2, 128, 32, 37),
+                                            (2, 1, 64, 1, 5), (3, 0, 64, 16, 33)])
+def test_decode_step_matches_oracle_and_general_path(NH, NKVH, D, r, B):
+    from nanochat_amd.ltv.ltv_filter import LtvInitValues
+    f = _make_filter(NH, NKVH, D, r, seed=NH + r)
+    C = NH * D
+    H = NH + 2 * NKVH
+    Da = D // r
+    g = torch.Generator().manual_seed(7)
+    x = torch.randn(B, 1, C, generator=g).to(torch.bfloat16).to(DEV)
+    prev_all = torch.randn(B, H, D, generator=g).to(torch.bfloat16).to(DEV)
+    prev = LtvInitValues(q=prev_all[:, :NH], k=prev_all[:, NH:NH + NKVH],
+                         v=prev_all[:, NH + NKVH:])
+    with torch.no_grad():
+        q, k, v = f(x, prev)
+    got = torch.cat([q, k, v], dim=2)[:, 0]  # (B, H, D)
+
+    # oracle: the reference dataflow at T = 1 from the same rows, bf16 I/O
+    w = O.bf16_round(f.c.weight.detach().float().cpu().numpy())
+    bias = f.logit_bias.detach().float().cpu().numpy()
+    ini = O.round_io(prev_all.float().cpu().numpy(), "bf16")
+    eq, ek, ev, _, _ = O.filter_forward(x.float().cpu().numpy(), w, ini, bias, NH, NKVH, Da, r,
+                                        "bf16")
+    exp = np.concatenate([eq, ek, ev], axis=2)[:, 0]
+    assert_close(np_of(got), exp, TOL, "decode vs oracle")
+
+    gq, gk, gv = _general_step(f, x, prev)
+    gen = torch.cat([gq, gk, gv], dim=2)[:, 0]
+    assert_close(np_of(got), np_of(gen), TOL, "decode vs general path")
+
+
+def test_decode_from_init_param_and_weight_updates():
+    """Without cache rows the step starts from init_param; an in-place weight
+    update (an optimizer step) invalidates the reused packed weight."""
+    from nanochat_amd.ltv.ltv_filter import LtvInitValues
+    f = _make_filter(2, 1, 128, 128, seed=3)
+    x = torch.randn(9, 1, 256).to(torch.bfloat16).to(DEV)
+    for _ in range(2):
+        with torch.no_grad():
+            got = torch.cat(f(x, LtvInitValues()), dim=2)
+        gen = torch.cat(_general_step(f, x, None), dim=2)
+        assert_close(np_of(got), np_of(gen), TOL, "decode from init_param")
+        with torch.no_grad():
+            f.c.weight.mul_(-1.5)
+
+
+def _chain(module, xs, cache, fused):
+    outs = []
+    for t in range(xs.shape[1]):
+        if fused:
+            with torch.no_grad():
+                q, k, v = module(xs[:, t:t + 1], cache)
+        else:
+            with torch.enable_grad():
+                q, k, v = module(xs[:, t:t + 1], cache)
+            q, k, v = q.detach(), k.detach(), v.detach()
+            cache.update_last_qkv(module.layer_idx, q=q[:, -1], k=k[:, -1], v=v[:, -1])
+        outs.append(torch.cat([q, k, v], dim=2))
+    return torch.cat(outs, dim=1)
+
+
+def test_decode_chain_matches_general_path_chain():
+    from nanochat_amd.ltv_combined_qkv_computer_module import LtvCombinedQkvComputerModule
+    f = _make_filter(6, 6, 128, 128, seed=5, gate_scale=1.0, bias=(-3.5, -2.5))
+    m = LtvCombinedQkvComputerModule(0, f)
+    g = torch.Generator().manual_seed(11)
+    xs = torch.randn(16, 40, 768, generator=g).to(torch.bfloat16).to(DEV)
+    ca, cb = _Cache(), _Cache()
+    with torch.no_grad():
+        m(xs[:, :8], ca)
+        m(xs[:, :8], cb)
+    fused = _chain(m, xs[:, 8:], ca, fused=True)
+    general = _chain(m, xs[:, 8:], cb, fused=False)
+    assert_close(np_of(fused), np_of(general), TOL, "decode chain")
+
+
+def test_decode_config5_vs_full_recompute():
+    """Config 5's decode: B = 64, 256 steps after a 16-token prefill, checked
+    against the full sequence in one call.  Gate rows zeroed and bias -3 give a
+    constant alpha = sigmoid(-3), so the bf16-state drift bound is exact."""
+    from nanochat_amd.ltv.ltv_filter import LtvInitValues
+    from nanochat_amd.ltv_combined_qkv_computer_module import LtvCombinedQkvComputerModule
+    f = _make_filter(6, 6, 128, 128, seed=2, gate_scale=0.0, bias=(-3.0, -3.0))
+    m = LtvCombinedQkvComputerModule(0, f)
+    B, T0, N = 64, 16, 256
+    g = torch.Generator().manual_seed(5)
+    xs = torch.randn(B, T0 + N, 768, generator=g).to(torch.bfloat16).to(DEV)
+    cache = _Cache()
+    with torch.no_grad():
+        m(xs[:, :T0], cache)
+    dec = _chain(m, xs[:, T0:], cache, fused=True)
+    with torch.no_grad():
+        full = torch.cat(f(xs, LtvInitValues()), dim=2)[:, T0:]
+    alpha = 1.0 / (1.0 + np.exp(3.0))
+    hmax = float(full.float().abs().max())
+    bound = 2.0 ** -9 * hmax / alpha
+    err = (dec.float() - full.float()).abs()
+    # the bound plus one bf16 rounding of the output
+    assert float(err.max()) <= bound + 2.0 ** -8 * hmax, (float(err.max()), bound)
+    # and the drift is far from the bound on average
+    assert float(err.mean()) <= 0.25 * bound
