@@ -215,6 +215,32 @@ def test_sigmoid_random(dtype, B, T, NH, NKVH, Da, r):
     assert_close(np_of(gb), egb, tol, "grad_logit_bias")
 
 
+@pytest.mark.parametrize("dtype", DTYPES, ids=io_name)
+def test_long_sequence_long_memory(dtype):
+    """Config 5's regime: T = 8192 with gate logits -z, z ~ N(3, 1.5) (decay
+    a = 1 - alpha around 0.95, so states carry over hundreds of steps).  Few
+    (b, h) sequences, so the backward runs in time chunks joined by the
+    chunk-map carries."""
+    io = io_name(dtype)
+    B, T, NH, NKVH, Da, r = 1, 8192, 1, 1, 1, 128
+    H = NH + 2 * NKVH
+    c, ini, bias, gy = _random_case(B, T, NH, NKVH, Da, r, seed=8192, z_mean=3.0, z_std=1.5,
+                                    io=io)
+    bias[:] = 0.0
+    (eq, ek, ev), (egc, egi, egb) = _expected(c, ini, bias, NH, NKVH, Da, r, True, io, gy)
+    grads = [to_torch(gy[:, :NH], dtype, DEV), to_torch(gy[:, NH:NH + NKVH], dtype, DEV),
+             to_torch(gy[:, NH + NKVH:H], dtype, DEV)]
+    (q, k, v), gc, gi, gb = _run(to_torch(c, dtype, DEV), to_torch(ini, dtype, DEV),
+                                 to_torch(bias, torch.float32, DEV), NH, NKVH, Da, r, True,
+                                 grads)
+    tol = TOL[dtype]
+    assert_close(np_of(q), eq, tol, "q")
+    assert_close(np_of(v), ev, tol, "v")
+    assert_close(np_of(gc), egc, tol, "grad_combined")
+    assert_close(np_of(gi), egi, tol, "grad_inits")
+    assert_close(np_of(gb), egb, tol, "grad_logit_bias")
+
+
 def test_backward_is_deterministic():
     B, T, NH, NKVH, Da, r = 2, 700, 2, 1, 1, 128
     c, ini, bias, gy = _random_case(B, T, NH, NKVH, Da, r, seed=5, io="bf16")
