@@ -1,6 +1,6 @@
 """Benchmark of the LTV combined-QKV filter path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload filter|gpt]
 
 Workload (the d12 training shape): x bf16
 [32, 1024, 768] ~ N(0, 1); c.weight [2322, 768] fp32 ~ N(0, 1/768) (value rows
@@ -121,6 +121,10 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--workload", choices=("filter", "gpt"), default="filter",
+                    help="filter: BASELINE.json configs[2] (the default, the metric's workload); "
+                         "gpt: configs[3], one training step of the 12-layer d12 GPT with the "
+                         "filter in every layer (tokens/s and the filter's share of the step)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="after the timed region, run a plain device copy of 256 MiB five times "
                          "(the known-size reference for rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -130,6 +134,10 @@ def main():
               "(the path shards over B with no exchange but the weight-gradient reduction; "
               "only the single-GPU figure is reported)", file=sys.stderr)
         sys.exit(2)
+
+    if args.workload == "gpt":
+        gpt_main(args)
+        return
 
     import torch
     from nanochat_amd import _native as N
@@ -225,6 +233,68 @@ def main():
     }
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+    print(json.dumps(out), flush=True)
+
+
+def gpt_main(args):
+    """one training step (forward + backward, no optimizer) of the
+    12-layer d12 GPT on B=16, T=1024 token ids ~ U[0, 65536), random-init weights,
+    bf16 autocast.  The filter's share is the summed duration of its library
+    calls (HIP events on the launch stream) over the step time."""
+    import torch
+    from nanochat_amd import _native as N
+    from nanochat_amd.gpt import GPT, GPTConfig
+
+    Bg, Tg = 16, 1024
+    dev = torch.device("cuda:0")
+    torch.manual_seed(0)
+    cfg = GPTConfig()
+    model = GPT(cfg).to(dev)
+    model.init_weights(randomise_output_projections=True)
+    model.wte.to(dtype=torch.bfloat16)
+    g = torch.Generator(device=dev).manual_seed(0)
+    idx = torch.randint(0, cfg.vocab_size, (Bg, Tg), generator=g, device=dev)
+    tgt = torch.randint(0, cfg.vocab_size, (Bg, Tg), generator=g, device=dev)
+
+    def step():
+        model.zero_grad(set_to_none=True)
+        with torch.autocast(device_type="cuda", dtype=torch.bfloat16):
+            loss = model(idx, tgt)
+        loss.backward()
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    with N.KernelRecorder() as rec:
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            step()
+        torch.cuda.synchronize()
+        elapsed = time.perf_counter() - t0
+    durs = rec.durations_ms()
+    filter_ms = sum(sum(v) for v in durs.values()) / args.steps
+    ms_per_step = elapsed * 1e3 / args.steps
+    out = {
+        "metric": "GPT d12 training step tokens/s (fwd+bwd) and LTV filter share of the step",
+        "value": round(Bg * Tg * args.steps / elapsed, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "configs[3]: 12-layer d12 GPT, filter in every layer, fwd+bwd "
+                               "(no optimizer step)",
+                   "B": Bg, "T": Tg, "n_layer": cfg.n_layer, "n_embd": cfg.n_embd,
+                   "vocab": cfg.vocab_size, "parallelism": "single GPU"},
+        "filter_ms_per_step": round(filter_ms, 4),
+        "filter_share": round(filter_ms / ms_per_step, 4),
+        "filter_kernels_us": {k: round(sum(v) / len(v) * 1e3, 2) for k, v in durs.items()},
+    }
     print(json.dumps(out), flush=True)
 
 

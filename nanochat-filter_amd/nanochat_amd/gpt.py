@@ -1,0 +1,160 @@
+"""A d12-class nanochat GPT with the LTV combined-QKV filter in every layer: the
+harness for the end-to-end training step (tokens/s and the filter's share).
+
+This restates the model of the reference's ``nanochat/gpt.py`` that the filter
+plugs into; only what a training step computes:
+  * ``norm``: RMSNorm without parameters (``gpt.py:96-98``);
+  * rotary embeddings on the two halves of each head, base 10000, cos/sin kept
+    in bfloat16 (``gpt.py:101-109, 339-352``);
+  * attention: q, k, v from the layer's qkv computer (the filter), rotary on q
+    and k, QK-norm, causal scaled-dot-product attention with scale
+    1/sqrt(head_dim), output projection (``gpt.py:218-297``);
+  * MLP: relu(x)^2 between two bias-free linears of width 4C (``gpt.py:298-310``);
+  * block: pre-norm residuals (``gpt.py:313-322``);
+  * GPT: bf16 token embedding, norm, blocks, norm, untied lm_head over the
+    vocabulary padded to a multiple of 64, fp32 logits soft-capped at 15,
+    cross-entropy (``gpt.py:631-706``);
+  * init as ``gpt.py:396-440``: wte ~ N(0, 1), lm_head ~ N(0, 0.001), c_fc and
+    the filter U(-s, s) with s = sqrt(3/C), output projections zero (the
+    harness can randomise them so gradients reach the filter at step 0).
+KV-cache inference, generation, optimizers and checkpoint loading are not
+part of the harness.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from nanochat_amd.ltv_combined_qkv_computer_module import LtvCombinedQkvComputerModule
+from nanochat_amd.ltv_cuda_fused_concat_head_major_register_cast_blelloch_scan_qkv_filter import (
+    LtvCudaFusedConcatHeadMajorRegisterCastBlellochScanQkvFilter,
+)
+
+
+@dataclass
+class GPTConfig:
+    sequence_len: int = 1024
+    vocab_size: int = 65536
+    n_layer: int = 12
+    n_head: int = 6
+    n_kv_head: int = 6
+    n_embd: int = 768
+    ltv_r: int = 128  # channels sharing one gate
+
+
+def norm(x: torch.Tensor) -> torch.Tensor:
+    return F.rms_norm(x, (x.size(-1),))
+
+
+def apply_rotary_emb(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    """x (B, T, H, D): rotate the pairs (x[..., i], x[..., i + D/2])."""
+    d = x.shape[3] // 2
+    if x.shape[3] % 2:
+        return x
+    x1, x2 = x[..., :d], x[..., d:]
+    return torch.cat([x1 * cos + x2 * sin, x2 * cos - x1 * sin], 3)
+
+
+def rotary_tables(seq_len: int, head_dim: int, base: float = 10000.0, device=None):
+    inv_freq = 1.0 / (base ** (torch.arange(0, head_dim, 2, dtype=torch.float32, device=device)
+                               / head_dim))
+    freqs = torch.outer(torch.arange(seq_len, dtype=torch.float32, device=device), inv_freq)
+    cos, sin = freqs.cos().bfloat16(), freqs.sin().bfloat16()
+    return cos[None, :, None, :], sin[None, :, None, :]
+
+
+class CausalSelfAttention(nn.Module):
+    def __init__(self, config: GPTConfig, layer_idx: int):
+        super().__init__()
+        self.n_head, self.n_kv_head = config.n_head, config.n_kv_head
+        self.head_dim = config.n_embd // config.n_head
+        self.qkv_computer = LtvCombinedQkvComputerModule(
+            layer_idx,
+            LtvCudaFusedConcatHeadMajorRegisterCastBlellochScanQkvFilter(
+                config.n_head, config.n_kv_head, self.head_dim, config.ltv_r),
+        )
+        self.c_proj = nn.Linear(config.n_embd, config.n_embd, bias=False)
+        self.scale = 1.0 / math.sqrt(self.head_dim)
+
+    def forward(self, x, cos_sin):
+        B, T, C = x.size()
+        q, k, v = self.qkv_computer(x, None)  # (B, T, H, D) views of head-major buffers
+        cos, sin = cos_sin
+        q, k = norm(apply_rotary_emb(q, cos, sin)), norm(apply_rotary_emb(k, cos, sin))
+        y = F.scaled_dot_product_attention(
+            q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2), is_causal=True,
+            scale=self.scale, enable_gqa=self.n_head != self.n_kv_head)
+        return self.c_proj(y.transpose(1, 2).reshape(B, T, C))
+
+
+class MLP(nn.Module):
+    def __init__(self, config: GPTConfig):
+        super().__init__()
+        self.c_fc = nn.Linear(config.n_embd, 4 * config.n_embd, bias=False)
+        self.c_proj = nn.Linear(4 * config.n_embd, config.n_embd, bias=False)
+
+    def forward(self, x):
+        return self.c_proj(F.relu(self.c_fc(x)).square())
+
+
+class Block(nn.Module):
+    def __init__(self, config: GPTConfig, layer_idx: int):
+        super().__init__()
+        self.attn = CausalSelfAttention(config, layer_idx)
+        self.mlp = MLP(config)
+
+    def forward(self, x, cos_sin):
+        x = x + self.attn(norm(x), cos_sin)
+        return x + self.mlp(norm(x))
+
+
+class GPT(nn.Module):
+    def __init__(self, config: GPTConfig, pad_vocab_to: int = 64):
+        super().__init__()
+        self.config = config
+        self.padded_vocab = (config.vocab_size + pad_vocab_to - 1) // pad_vocab_to * pad_vocab_to
+        self.wte = nn.Embedding(self.padded_vocab, config.n_embd)
+        self.h = nn.ModuleList([Block(config, i) for i in range(config.n_layer)])
+        self.lm_head = nn.Linear(config.n_embd, self.padded_vocab, bias=False)
+        cos, sin = rotary_tables(config.sequence_len, config.n_embd // config.n_head)
+        self.register_buffer("cos", cos, persistent=False)
+        self.register_buffer("sin", sin, persistent=False)
+
+    @torch.no_grad()
+    def init_weights(self, randomise_output_projections: bool = False, seed: int = 0):
+        g = torch.Generator(device=self.lm_head.weight.device).manual_seed(seed)
+        C = self.config.n_embd
+        s = math.sqrt(3.0 / C)
+        self.wte.weight.normal_(0.0, 1.0, generator=g)
+        self.lm_head.weight.normal_(0.0, 0.001, generator=g)
+        for blk in self.h:
+            filt = blk.attn.qkv_computer.ltv_filter
+            filt.c.weight.uniform_(-s, s, generator=g)
+            filt.logit_bias.uniform_(-s, s, generator=g)
+            filt.init_param.uniform_(-s, s, generator=g)
+            blk.mlp.c_fc.weight.uniform_(-s, s, generator=g)
+            for lin in (blk.attn.c_proj, blk.mlp.c_proj):
+                if randomise_output_projections:
+                    lin.weight.uniform_(-s, s, generator=g)
+                else:
+                    lin.weight.zero_()
+
+    def filters(self):
+        return [blk.attn.qkv_computer.ltv_filter for blk in self.h]
+
+    def forward(self, idx: torch.Tensor, targets: torch.Tensor | None = None):
+        B, T = idx.shape
+        cos_sin = (self.cos[:, :T], self.sin[:, :T])
+        x = norm(self.wte(idx))
+        for blk in self.h:
+            x = blk(x, cos_sin)
+        logits = self.lm_head(norm(x))[..., : self.config.vocab_size].float()
+        logits = 15.0 * torch.tanh(logits / 15.0)
+        if targets is None:
+            return logits
+        return F.cross_entropy(logits.view(-1, logits.size(-1)), targets.view(-1), ignore_index=-1)
