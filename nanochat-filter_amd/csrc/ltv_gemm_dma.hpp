@@ -86,6 +86,14 @@ __device__ __forceinline__ void wait_vmcnt_range(int n) {
 // outstanding (n above the 6-bit counter's range waits for 63).
 __device__ __forceinline__ void wait_vmcnt_rt(int n) { wait_vmcnt_range<0, 63>(n < 63 ? n : 63); }
 
+// Cache policy of the epilogue stores: streaming (nt) at device scope (sc1).
+// The output is not read again by the kernel, and every CU ends its tiles at
+// about the same time: measured on MI355X this burst drains faster than with
+// the default policy (a GEMM of the forward's shape: 139 vs 146 us).
+#ifndef LTV_EPI_STORE_POLICY
+#define LTV_EPI_STORE_POLICY " nt sc1"
+#endif
+
 typedef unsigned u32x2_t __attribute__((ext_vector_type(2)));
 typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
@@ -93,15 +101,15 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 // One buffer store instruction each (exactly one vmcnt event, whatever the
 // lanes' offsets; lanes with an offset past num_records write nothing).
 __device__ __forceinline__ void buf_store_b64(u32x2_t v, uint32_t voff, i32x4_t rsrc) {
-  asm volatile("buffer_store_dwordx2 %0, %1, %2, 0 offen" : : "v"(v), "v"(voff), "s"(rsrc)
-               : "memory");
+  asm volatile("buffer_store_dwordx2 %0, %1, %2, 0 offen" LTV_EPI_STORE_POLICY : : "v"(v),
+               "v"(voff), "s"(rsrc) : "memory");
 }
 // A store of more than 8 bytes reads its data registers a cycle late: the nop
 // keeps the next VALU write to them from landing first (the compiler inserts
 // such wait states for its own instructions, not around inline asm).
 __device__ __forceinline__ void buf_store_b128(u32x4_t v, uint32_t voff, i32x4_t rsrc) {
-  asm volatile("buffer_store_dwordx4 %0, %1, %2, 0 offen\n\ts_nop 1" : : "v"(v), "v"(voff),
-               "s"(rsrc) : "memory");
+  asm volatile("buffer_store_dwordx4 %0, %1, %2, 0 offen" LTV_EPI_STORE_POLICY "\n\ts_nop 1"
+               : : "v"(v), "v"(voff), "s"(rsrc) : "memory");
 }
 
 __device__ __forceinline__ void lds_fence() { asm volatile("" : : : "memory"); }

@@ -259,17 +259,18 @@ int scan_forward_impl(int dtype, const HostView4& u, const HostView4& lg, const 
   return scan_launch_fwd(dtype == LTV_DTYPE_BF16, a, cfg, (int)grid, vec, gm, st);
 }
 
-// Upper bound on the backward's time chunks per (b, h).  With at least 512
-// (b, h) sequences (two per CU on MI355X) every CU already holds resident
-// workgroups and chunking only adds the chunk-map passes; with fewer (long T,
-// small batch) the sequences are cut into chunks of at least one 64-step tile
-// until about 1024 workgroups run.  The
+// Upper bound on the backward's time chunks per (b, h).  With at least 256
+// (b, h) sequences (one per CU on MI355X) chunking only adds the chunk-map
+// passes (measured: 288 sequences, 1 chunk 132 us, 2-4 chunks 150 us); with
+// fewer (long T, small batch) the sequences are cut into chunks of at least
+// one 64-step tile until about 512 workgroups run (144 sequences at T = 8192:
+// 827 us unchunked, 504 us in 4 chunks).  The
 // launch rounds the chunk length up to whole tiles, which never raises the
 // count above this bound.
 int bwd_max_chunks(int B, int H, int T) {
   const int64_t bh = (int64_t)B * H;
   int nc = tuning().bwd_chunks;
-  if (nc == 0) nc = bh >= 512 ? 1 : (int)((1024 + bh - 1) / bh);
+  if (nc == 0) nc = bh >= 256 ? 1 : (int)((512 + bh - 1) / bh);
   const int cap = (T + 63) / 64;
   return std::max(1, std::min(nc, cap));
 }
