@@ -25,10 +25,11 @@
 // The lane then re-runs its L steps from its exact carry-in and stores, so every
 // element is read from HBM once and written once.
 //
-// The backward walks the tiles in reverse.  Per tile it reads the forward
-// states h_{t-1} from the saved outputs of the previous steps (the inits at
-// t = 0) -- the I/O-dtype state the reference backward reads back,
-// ltv_reference_ops.py:7-34 -- then runs the reverse scan
+// The backward walks the tiles in reverse.  Per tile each lane reads the state
+// entering its first step from the saved outputs (the inits at t = 0) -- the
+// I/O-dtype state the reference backward reads back, ltv_reference_ops.py:7-34
+// -- and recomputes the states of its other steps from it, rounded to the I/O
+// dtype like the saved outputs; then it runs the reverse scan
 //   g_t = gy_t + (1 - alpha_{t+1}) g_{t+1},   g_T = 0
 // and emits du = alpha g, dalpha = (u - h_{t-1}) g reduced over each gate group,
 // dlogit = alpha (1 - alpha) dalpha, dinit = (1 - alpha_0) g_0 and a per-(b, h)
@@ -604,13 +605,15 @@ scan_bwd_kernel(const BwdArgs args) {
   const int tiles_pc = args.chunk_steps / TW;
   const int it_lo = chunk * tiles_pc;
   const int it_hi = min(ntiles, it_lo + tiles_pc) - 1;
-  // The next (earlier) tile's packed u, gy, h_{t-1} and raw logits are loaded
-  // while the current tile is processed, so each wavefront keeps its loads in
-  // flight across the tile's barriers.  h_{t-1} of a step is the saved forward
-  // output of the step before (the inits at t = 0): exactly the rounded state
-  // the forward stored.
+  // The next (earlier) tile's packed u, gy and raw logits, and the state
+  // entering each lane's first step, are loaded while the current tile is
+  // processed, so each wavefront keeps its loads in flight across the tile's
+  // barriers.  The state h_{t0-1} entering a lane is the saved forward output
+  // of the step before (the inits at t = 0); the lane recomputes its other
+  // L - 1 states h_t = h_{t-1} + alpha_t (u_t - h_{t-1}) itself, rounded to the
+  // I/O dtype as the forward stores them.
   const int tl0 = (w * TG + tg) * L;
-  uint4 nu[L], ng[L], nh[L];
+  uint4 nu[L], ng[L], nh0;
   LogitRaw<TIO, GM, L + 1> nl;
   auto load_tile = [&](int it) {
     const int t0 = it * TW + tl0;
@@ -622,10 +625,11 @@ scan_bwd_kernel(const BwdArgs args) {
                  : make_uint4(0u, 0u, 0u, 0u);
       ng[s] = ok ? ld_vec<TIO, VEC>(gp + (int64_t)t * gs[2], gs[3], nvalid)
                  : make_uint4(0u, 0u, 0u, 0u);
-      nh[s] = !ok      ? make_uint4(0u, 0u, 0u, 0u)
-              : t == 0 ? ld_vec<TIO, VEC>(ip, args.init.s[3], nvalid)
-                       : ld_vec<TIO, VEC>(hp + (int64_t)(t - 1) * hs[2], hs[3], nvalid);
     }
+    const bool ok0 = active && t0 < S.T;
+    nh0 = !ok0      ? make_uint4(0u, 0u, 0u, 0u)
+          : t0 == 0 ? ld_vec<TIO, VEC>(ip, args.init.s[3], nvalid)
+                    : ld_vec<TIO, VEC>(hp + (int64_t)(t0 - 1) * hs[2], hs[3], nvalid);
     nl.load(lp + (int64_t)t0 * lst, lst, gi, t0, S.T, active, nvalid);
   };
   if (it_hi >= it_lo) load_tile(it_hi);
@@ -638,11 +642,22 @@ scan_bwd_kernel(const BwdArgs args) {
     for (int s = 0; s < L; ++s) {
       uq[s] = nu[s];
       gq[s] = ng[s];
-      hq[s] = nh[s];
     }
+    hq[0] = nh0;
     float al[L + 1][NA];
     nl.gates(gi, t0, S.T, active, use_sig, al);
     if (it > it_lo) load_tile(it - 1);
+    // h_{t-1} of the lane's later steps (padded steps have alpha = 0)
+#pragma unroll
+    for (int s = 1; s < L; ++s) {
+      float hv[V];
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        const float hp_ = Pack<TIO>::get(hq[s - 1], v);
+        hv[v] = fmaf(al[s - 1][GL ? 0 : v], Pack<TIO>::get(uq[s - 1], v) - hp_, hp_);
+      }
+      hq[s] = Pack<TIO>::pack(hv);
+    }
 
     // ---- reverse scan: g_t = gy_t + (1 - alpha_{t+1}) g_{t+1}
     // decay carrying g_{t+1} into g_t; zero for the last step of the sequence
