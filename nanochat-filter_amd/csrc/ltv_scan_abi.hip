@@ -246,10 +246,13 @@ int scan_forward_impl(int dtype, const HostView4& u, const HostView4& lg, const 
   else if (vec && chanvec_ok(r, D, V, lg)) gm = GATE_CHANVEC;
 
   // Channels are independent in the forward: slabs of up to 8 channel lanes
-  // (64 bf16 / 32 fp32 channels), 4 steps per lane, 4 wavefronts.  Measured on
-  // MI355X at d12 this is the fastest built shape: the whole grid is resident
-  // at once and each load instruction covers 8 rows of 128 bytes.
-  ScanCfg cfg{cl_full < 8 ? cl_full : 8, 4, 4};
+  // (64 bf16 / 32 fp32 channels), 4 wavefronts, 2 steps per lane at 8 lanes.
+  // Measured on MI355X at d12 this is the fastest built shape (74 us against
+  // 89 us with 4 steps per lane): 81 VGPRs let all 1152 workgroups be resident
+  // at once (111 VGPRs left 128 of them for a second round), and each load
+  // instruction covers 8 rows of 128 bytes.
+  const int fcl = cl_full < 8 ? cl_full : 8;
+  ScanCfg cfg{fcl, fcl == 8 && vec ? 2 : 4, 4};
   const ScanTuning& tu = tuning();
   if (vec && tu.fwd_cl > 0) cfg = ScanCfg{tu.fwd_cl < cl_full ? tu.fwd_cl : cl_full, tu.fwd_l, tu.fwd_nw};
   const int nslab = (D + cfg.CL * V - 1) / (cfg.CL * V);
