@@ -15,7 +15,9 @@ in HBM before the timed region.  ``value`` = tokens / s = B*T*K / elapsed.
 Printed as one JSON line, with
   roofline     -- the dominant kernel's algorithmic bytes (or FLOPs) per launch
                   over its average duration (HIP events on the launch stream
-                  across the timed steps), against MI355X's published peak;
+                  across the timed steps, created without the system-scope
+                  fence so that recording them does not flush the caches),
+                  against MI355X's published peak;
   kernels      -- the same figure for every kernel of the path;
   cpu_baseline -- the CPU oracle (oracle/ltv_oracle.py, a restatement of the
                   reference's sequential PyTorch path) timed on a bounded

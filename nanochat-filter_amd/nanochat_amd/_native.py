@@ -177,7 +177,7 @@ class KernelRecorder:
     the stream every op launches on."""
 
     def __init__(self):
-        self.spans: list[tuple[str, torch.cuda.Event, torch.cuda.Event]] = []
+        self.spans: list[tuple[str, TimingEvent, TimingEvent]] = []
 
     def __enter__(self):
         global _recorder
@@ -199,6 +199,62 @@ class KernelRecorder:
 _recorder: KernelRecorder | None = None
 
 
+# Timing events for the recorder, created through the HIP runtime this process
+# already uses (torch's) with hipEventDisableSystemFence: a default event's
+# system-scope fence writes back and invalidates the caches when it completes,
+# which idles the GPU for about 10 us per record on MI355X and perturbs the
+# next kernel.  These events only timestamp.
+_HIP_EVENT_DISABLE_SYSTEM_FENCE = 0x20000000
+_hip_rt = None
+
+
+def _hip():
+    global _hip_rt
+    if _hip_rt is None:
+        path = None
+        with open("/proc/self/maps") as fh:
+            for line in fh:
+                if "libamdhip64" in line:
+                    path = line.split()[-1]
+                    break
+        rt = ctypes.CDLL(path or "libamdhip64.so")
+        rt.hipEventCreateWithFlags.argtypes = [ctypes.POINTER(_c_vp), ctypes.c_uint]
+        rt.hipEventRecord.argtypes = [_c_vp, _c_vp]
+        rt.hipEventSynchronize.argtypes = [_c_vp]
+        rt.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), _c_vp, _c_vp]
+        rt.hipEventDestroy.argtypes = [_c_vp]
+        _hip_rt = rt
+    return _hip_rt
+
+
+class TimingEvent:
+    __slots__ = ("h",)
+
+    def __init__(self):
+        self.h = _c_vp()
+        rc = _hip().hipEventCreateWithFlags(ctypes.byref(self.h), _HIP_EVENT_DISABLE_SYSTEM_FENCE)
+        if rc != 0:
+            raise RuntimeError(f"hipEventCreateWithFlags failed ({rc})")
+
+    def record(self):
+        rc = _hip().hipEventRecord(self.h, _c_vp(torch.cuda.current_stream().cuda_stream))
+        if rc != 0:
+            raise RuntimeError(f"hipEventRecord failed ({rc})")
+
+    def elapsed_time(self, end: "TimingEvent") -> float:
+        rt = _hip()
+        rt.hipEventSynchronize(end.h)
+        ms = ctypes.c_float()
+        rc = rt.hipEventElapsedTime(ctypes.byref(ms), self.h, end.h)
+        if rc != 0:
+            raise RuntimeError(f"hipEventElapsedTime failed ({rc})")
+        return ms.value
+
+    def __del__(self):
+        if self.h and _hip_rt is not None:
+            _hip_rt.hipEventDestroy(self.h)
+
+
 class span:
     """``with span("scan_fwd"): lib.call(...)`` -- no-op unless recording."""
 
@@ -210,14 +266,14 @@ class span:
 
     def __enter__(self):
         if _recorder is not None:
-            a = torch.cuda.Event(enable_timing=True)
+            a = TimingEvent()
             a.record()
             self.ev = a
         return self
 
     def __exit__(self, *exc):
         if self.ev is not None and _recorder is not None:
-            b = torch.cuda.Event(enable_timing=True)
+            b = TimingEvent()
             b.record()
             _recorder.spans.append((self.name, self.ev, b))
         return False
