@@ -392,10 +392,6 @@ extern "C" int ltv_qkv_project_forward(const void* x, const void* wpack, void* v
       a.tiles_i = (Fp + 127) / 128;
       return launch_gemm_dma<128, 256, 2, 4, OP_KC, OP_KC>(a, e, 1, st);
     }
-    if (gemm_tuning().fwd == 4) {  // 4 wavefronts of 128 x 128
-      a.tiles_i = (Fp + 255) / 256;
-      return launch_gemm_dma<256, 256, 2, 2, OP_KC, OP_KC>(a, e, 1, st);
-    }
     a.tiles_i = (Fp + 255) / 256;
     return launch_gemm_dma<256, 256, 2, 4, OP_KC, OP_KC>(a, e, 1, st);
   }
