@@ -18,6 +18,9 @@ What it restates (all citations relative to the reference tree):
   (``ltv_reference_ops.py:7-34``): the alpha gradient uses the *I/O-rounded*
   previous state, exactly what the CUDA kernel reads back from its saved output
   (``cpp_ewma/src/ltv_fused_concat_head_major_register_cast_blelloch_scan_cuda_backward.cu:51-81``).
+* ``look_back_forward/backward`` -- the same loop with chunk restarts
+  (``ltv_reference_ops.py:37-124`` with general P, Q, K) and the autograd of
+  it summed over the overlapping windows.
 * ``linear_transpose_forward/backward`` -- ``fused_linear_transpose_reference``
   (``ltv_reference_ops.py:299-308``): ``matmul(x, W^T).transpose(1, 2)``.
 
@@ -34,6 +37,11 @@ How each function is pinned (tests/test_oracle.py):
     float64 finite differences of scan_forward for scan_backward; state
     continuity; and golden vectors written by the reference's own
     ltv_reference_ops.py (tests/golden/).
+  * look_back_forward / look_back_backward: P >= T reduces them to the
+    scan above; the exact-integer generators against a per-window
+    sample-and-hold closed form; each window equals scan_forward of its slice;
+    float64 finite differences over overlapping windows (K - 1 > Q included);
+    golden vectors of the reference's look-back function (tests/golden/).
   * linear_transpose_*: numpy/torch matmul (a library routine) and finite
     differences.
 """
@@ -51,6 +59,10 @@ __all__ = [
     "split_combined",
     "scan_forward",
     "scan_backward",
+    "UNBOUNDED_P",
+    "look_back_windows",
+    "look_back_forward",
+    "look_back_backward",
     "linear_transpose_forward",
     "linear_transpose_backward",
     "filter_forward",
@@ -260,6 +272,124 @@ def scan_backward(
     if T == 0:
         grad_init = np.zeros((B, H, D), dtype=cd)
 
+    grad_bias = grad_logit.sum(axis=(0, 1), dtype=np.float64).astype(
+        np.float64 if io_dtype == "f64" else np.float32
+    )
+    grad_combined = np.concatenate([grad_u, grad_logit], axis=-1).reshape(B, T, -1)
+    return (
+        round_io(grad_combined, io_dtype),
+        round_io(grad_init, io_dtype),
+        grad_bias,
+    )
+
+
+# ---------------------------------------------------------------------------
+# look-back scan: chunk restarts with a K - 1 step warm-up
+# ---------------------------------------------------------------------------
+UNBOUNDED_P = 2_147_483_647
+
+
+def look_back_windows(T: int, P: int, Q: int, K: int):
+    """Chunk windows ``(lo, st, hi)`` of the look-back scan.
+
+    ``ltv_reference_ops.py:65-75`` cuts T into ``[0, min(P, T))`` and then
+    chunks of Q steps ``[P + (i - 1) Q, min(P + i Q, T))``; each chunk
+    ``[st, hi)`` restarts from the inits at ``lo = max(0, st - (K - 1))``
+    (``:99-101``) and outputs only its own steps.  The same bounds as the CUDA
+    forward (``…look_back…blelloch_scan_cuda_forward.cu:36-37, 104-110``).
+    """
+    if T > P:
+        M = (T - P + Q - 1) // Q
+        chunks = [(0, min(P, T))]
+        for i in range(1, M + 1):
+            s, e = P + (i - 1) * Q, min(P + i * Q, T)
+            if s < T:
+                chunks.append((s, e))
+    else:
+        chunks = [(0, T)]
+    return [(max(0, s - (K - 1)), s, e) for s, e in chunks]
+
+
+def look_back_forward(combined, inits, logit_bias, NH, NKVH, Da, r, P, Q, K,
+                      use_sigmoid, io_dtype="f32"):
+    """Forward of ``ltv_look_back_fused_concat_head_major_register_cast_sequential_scan_minimal``
+    (``ltv_reference_ops.py:37-124``): every window of ``look_back_windows``
+    runs the recurrence from the inits over ``[lo, hi)`` in fp32 and writes
+    the I/O-rounded states of ``[st, hi)``.  Returns (out_q, out_k, out_v)."""
+    cd = _compute_dtype(io_dtype)
+    u, logits = split_combined(np.asarray(combined), NH, NKVH, Da, r)
+    B, T = u.shape[:2]
+    H = NH + 2 * NKVH
+    D = Da * r
+    u = u.astype(cd)
+    _, alpha_bc = _alphas(logits, np.asarray(logit_bias), use_sigmoid, r, cd)
+    one = cd(1.0)
+    init = np.asarray(inits, dtype=cd).reshape(B, H, D)
+    out = np.zeros((B, H, T, D), dtype=cd)
+    for lo, st, hi in look_back_windows(T, P, Q, K):
+        h = init.copy()
+        for t in range(lo, hi):
+            a = alpha_bc[:, t]
+            h = ((one - a) * h + a * u[:, t]).astype(cd)
+            if t >= st:
+                out[:, :, t] = round_io(h, io_dtype)
+    return _split_heads(out, NH, NKVH)
+
+
+def look_back_backward(combined, inits, logit_bias, grad_hq, grad_hk, grad_hv, NH, NKVH,
+                       Da, r, P, Q, K, use_sigmoid, io_dtype="f32"):
+    """Backward of ``look_back_forward``: the autograd of the reference loop
+    (``QuantizedStateUpdate.backward``, ``ltv_reference_ops.py:20-34``) summed
+    over the windows.  Each window ``(lo, st, hi)`` runs its own reverse chain
+    from ``g_hi = 0``, taking upstream gradients only on its own steps
+    ``[st, hi)``; its alpha gradient uses its own I/O-rounded states (the
+    warm-up states included); every window adds ``(1 - a_lo) g_lo`` to the
+    inits gradient.  A step inside later windows' warm-ups therefore collects
+    one contribution per covering window.  Contributions are summed in fp32 in
+    window order and rounded once.
+
+    Returns ``(grad_combined (B, T, F), grad_inits (B, H, D), grad_logit_bias (H, Da))``.
+    """
+    cd = _compute_dtype(io_dtype)
+    combined = np.asarray(combined)
+    u, logits = split_combined(combined, NH, NKVH, Da, r)
+    B, T = u.shape[:2]
+    H = NH + 2 * NKVH
+    D = Da * r
+    u = u.astype(cd)
+    alpha, alpha_bc = _alphas(logits, np.asarray(logit_bias), use_sigmoid, r, cd)
+    gy = np.concatenate([grad_hq, grad_hk, grad_hv], axis=1).astype(cd)
+    init = np.asarray(inits, dtype=cd).reshape(B, H, D)
+    one = cd(1.0)
+    grad_u = np.zeros((B, T, H, D), dtype=cd)
+    grad_logit = np.zeros((B, T, H, Da), dtype=cd)
+    grad_init = np.zeros((B, H, D), dtype=cd)
+    for lo, st, hi in look_back_windows(T, P, Q, K):
+        if hi <= lo:
+            continue
+        # I/O-rounded state entering each step of the window (state_quant)
+        hq = np.empty((hi - lo, B, H, D), dtype=cd)
+        h = init.copy()
+        for t in range(lo, hi):
+            hq[t - lo] = round_io(h, io_dtype)
+            a = alpha_bc[:, t]
+            h = ((one - a) * h + a * u[:, t]).astype(cd)
+        g = np.zeros((B, H, D), dtype=cd)
+        for t in range(hi - 1, lo - 1, -1):
+            gyt = gy[:, :, t] if t >= st else np.zeros((B, H, D), dtype=cd)
+            if t == hi - 1:
+                g = gyt.copy()
+            else:
+                g = (gyt + g * (one - alpha_bc[:, t + 1])).astype(cd)
+            grad_u[:, t] += g * alpha_bc[:, t]
+            d_alpha = g * (u[:, t] - hq[t - lo])
+            d_alpha_sum = d_alpha.reshape(B, H, Da, r).sum(axis=-1, dtype=cd)
+            if use_sigmoid:
+                at = alpha[:, t]
+                grad_logit[:, t] += (d_alpha_sum * ((one - at) * at)).astype(cd)
+            else:
+                grad_logit[:, t] += d_alpha_sum
+        grad_init += (g * (one - alpha_bc[:, lo])).astype(cd)
     grad_bias = grad_logit.sum(axis=(0, 1), dtype=np.float64).astype(
         np.float64 if io_dtype == "f64" else np.float32
     )

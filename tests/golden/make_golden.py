@@ -6,7 +6,9 @@ Run in the build container (where the read-only reference tree is mounted):
 
 It loads ``nanochat/ops/ltv_reference_ops.py`` by file path (that file imports
 only torch), runs ``ltv_fused_concat_head_major_register_cast_blelloch_scan_minimal``
-(``ltv_reference_ops.py:162-192``) forward and, through autograd, backward
+(``ltv_reference_ops.py:162-192``) and, for the look-back cases with several
+chunk windows, ``ltv_look_back_fused_concat_head_major_register_cast_sequential_scan_minimal``
+(``:37-124``), forward and, through autograd, backward
 (``QuantizedStateUpdate``, ``:7-34``) on small seeded inputs with the sigmoid
 gate on, in fp32 and in bf16, and stores inputs and outputs as ``.npz`` data
 (bf16 as uint16 bit patterns).  These cases are what the closed-form and
@@ -39,6 +41,16 @@ CASES = [
     ("bf16_r16_t64", torch.bfloat16, 1, 64, 1, 1, 1, 16, 6),
 ]
 
+# Look-back cases, several chunk windows each:
+# (name, dtype, B, T, NH, NKVH, Da, r, P, Q, K, seed)
+LOOK_BACK_CASES = [
+    ("f32_p8q6k4", torch.float32, 2, 37, 1, 1, 2, 2, 8, 6, 4, 10),
+    ("f32_p5q2k6", torch.float32, 1, 23, 1, 1, 1, 8, 5, 2, 6, 11),  # warm-up longer than Q
+    ("f32_r1_p4q3k3", torch.float32, 1, 13, 1, 1, 4, 1, 4, 3, 3, 12),
+    ("bf16_p16q16k9", torch.bfloat16, 2, 50, 2, 1, 1, 16, 16, 16, 9, 13),
+    ("bf16_p0q3k2", torch.bfloat16, 1, 11, 1, 1, 2, 4, 0, 3, 2, 14),  # empty first chunk
+]
+
 
 def _load_reference(ref_root: str):
     path = os.path.join(ref_root, "nanochat", "ops", "ltv_reference_ops.py")
@@ -55,7 +67,7 @@ def _np(t: torch.Tensor) -> np.ndarray:
     return t.numpy().copy()
 
 
-def make_case(ref, name, dtype, B, T, NH, NKVH, Da, r, seed):
+def make_case(ref, name, dtype, B, T, NH, NKVH, Da, r, seed, pqk=None):
     g = torch.Generator().manual_seed(seed)
     H = NH + 2 * NKVH
     D = Da * r
@@ -74,13 +86,20 @@ def make_case(ref, name, dtype, B, T, NH, NKVH, Da, r, seed):
     c_ref = combined.clone().requires_grad_(True)
     i_ref = inits.clone().requires_grad_(True)
     b_ref = logit_bias.clone().requires_grad_(True)
-    oq, ok, ov = ref.ltv_fused_concat_head_major_register_cast_blelloch_scan_minimal(
-        c_ref, i_ref, b_ref, NH, NKVH, Da, r, 2147483647, 1, 1, True
-    )
+    if pqk is None:
+        oq, ok, ov = ref.ltv_fused_concat_head_major_register_cast_blelloch_scan_minimal(
+            c_ref, i_ref, b_ref, NH, NKVH, Da, r, 2147483647, 1, 1, True
+        )
+        meta = [B, T, NH, NKVH, Da, r, 1 if dtype == torch.bfloat16 else 0]
+    else:
+        # ltv_reference_ops.py:37-124 with chunk restarts
+        oq, ok, ov = ref.ltv_look_back_fused_concat_head_major_register_cast_sequential_scan_minimal(
+            c_ref, i_ref, b_ref, NH, NKVH, Da, r, *pqk, True
+        )
+        meta = [B, T, NH, NKVH, Da, r, 1 if dtype == torch.bfloat16 else 0, *pqk]
     torch.autograd.backward([oq, ok, ov], [gq, gk, gv])
     return {
-        "meta": np.array([B, T, NH, NKVH, Da, r, 1 if dtype == torch.bfloat16 else 0],
-                         dtype=np.int64),
+        "meta": np.array(meta, dtype=np.int64),
         "combined": _np(combined),
         "inits": _np(inits),
         "logit_bias": _np(logit_bias),
@@ -103,6 +122,11 @@ def main():
     for case in CASES:
         data = make_case(ref, *case)
         out = os.path.join(HERE, f"scan_{case[0]}.npz")
+        np.savez_compressed(out, **data)
+        print("wrote", out, os.path.getsize(out), "bytes")
+    for name, dtype, B, T, NH, NKVH, Da, r, P, Q, K, seed in LOOK_BACK_CASES:
+        data = make_case(ref, name, dtype, B, T, NH, NKVH, Da, r, seed, pqk=(P, Q, K))
+        out = os.path.join(HERE, f"look_back_{name}.npz")
         np.savez_compressed(out, **data)
         print("wrote", out, os.path.getsize(out), "bytes")
 
