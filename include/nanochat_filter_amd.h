@@ -43,7 +43,7 @@ extern "C" {
 #define LTV_ERR_HIP 3
 #define LTV_ERR_WORKSPACE 4
 
-/* Version of this ABI (bumped on any signature change): 2. */
+/* Version of this ABI (bumped on any signature change or addition): 3. */
 int ltv_abi_version(void);
 
 /* Message of the last failing call on this host thread ("" if none). */
@@ -132,6 +132,77 @@ int ltv_hm_scan_backward_split(
     const int64_t grad_logits_strides[4], void* grad_inits, const int64_t grad_inits_strides[3],
     float* grad_logit_bias, void* workspace, size_t workspace_bytes, int B, int T, int NH,
     int NKVH, int Da, int r, int use_sigmoid, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Look-back scan: the same recurrence restarted in chunk windows.
+ *
+ * Chunk 0 covers steps [0, min(P, T)); chunk c >= 1 covers
+ * [P + (c - 1) Q, min(P + c Q, T)).  Each chunk [st, hi) runs the recurrence
+ * from the inits, starting K - 1 steps early at lo = max(0, st - (K - 1)) (the
+ * warm-up), and writes only its own outputs [st, hi).  P >= T is the full
+ * recurrence of ltv_hm_scan_forward (the reference passes P = 2147483647,
+ * Q = K = 1 for it).  Any P >= 0, Q >= 1, K >= 1 is accepted (the reference's
+ * CUDA dispatch builds a fixed list of (P, Q, K)).
+ *
+ * The backward is the exact gradient of that forward, as autograd gives it for
+ * the reference's Python loop (nanochat/ops/ltv_reference_ops.py:37-124): a
+ * step inside later chunks' warm-ups receives one contribution per chunk that
+ * reads it, and every chunk adds to grad_inits.  Same buffer contracts as
+ * ltv_hm_scan_backward; the workspace size depends on P, Q, K.  With several
+ * chunk windows the backward needs gate groups of r channels with r a multiple
+ * of V (8 for bf16, 4 for fp32) and Da <= 16, or r dividing V.
+ *
+ * Replace ltv_look_back_fused_concat_head_major_register_cast_{blelloch,sequential}_scan_cuda_{forward,backward}
+ * (cpp_ewma/src/ltv_look_back_fused_concat_head_major_register_cast_blelloch_scan_cuda_forward.cu:466-509,
+ *  …_blelloch_scan_cuda_backward.cu:809-927 and the sequential pair, called from
+ *  nanochat/ops/ltv_cuda_look_back_fused_concat_head_major_register_cast_{blelloch,sequential}_scan.py).
+ * The reference's CUDA backward kernels for more than one chunk differ from the
+ * autograd of its Python loop (its tests stay at T <= P); this one follows the
+ * Python loop.
+ * ---------------------------------------------------------------------- */
+int ltv_hm_look_back_scan_forward(int dtype, const void* combined,
+                                  const int64_t combined_strides[3], const void* inits,
+                                  const int64_t inits_strides[3], const float* logit_bias,
+                                  void* out_q, const int64_t out_q_strides[4], void* out_k,
+                                  const int64_t out_k_strides[4], void* out_v,
+                                  const int64_t out_v_strides[4], int B, int T, int NH, int NKVH,
+                                  int Da, int r, int P, int Q, int K, int use_sigmoid,
+                                  void* stream);
+
+size_t ltv_hm_look_back_scan_backward_workspace_size(int dtype, int B, int T, int NH, int NKVH,
+                                                     int Da, int r, int P, int Q, int K);
+
+int ltv_hm_look_back_scan_backward(
+    int dtype, const void* combined, const int64_t combined_strides[3], const void* inits,
+    const int64_t inits_strides[3], const float* logit_bias, const void* hq,
+    const int64_t hq_strides[4], const void* hk, const int64_t hk_strides[4], const void* hv,
+    const int64_t hv_strides[4], const void* grad_hq, const int64_t grad_hq_strides[4],
+    const void* grad_hk, const int64_t grad_hk_strides[4], const void* grad_hv,
+    const int64_t grad_hv_strides[4], void* grad_combined, const int64_t grad_combined_strides[3],
+    void* grad_inits, const int64_t grad_inits_strides[3], float* grad_logit_bias,
+    void* workspace, size_t workspace_bytes, int B, int T, int NH, int NKVH, int Da, int r, int P,
+    int Q, int K, int use_sigmoid, void* stream);
+
+/* Split-layout forms (value and logit slots as two 4-D views, as in
+ * ltv_hm_scan_forward_split). */
+int ltv_hm_look_back_scan_forward_split(
+    int dtype, const void* values, const int64_t values_strides[4], const void* logits,
+    const int64_t logits_strides[4], const void* inits, const int64_t inits_strides[3],
+    const float* logit_bias, void* out_q, const int64_t out_q_strides[4], void* out_k,
+    const int64_t out_k_strides[4], void* out_v, const int64_t out_v_strides[4], int B, int T,
+    int NH, int NKVH, int Da, int r, int P, int Q, int K, int use_sigmoid, void* stream);
+
+int ltv_hm_look_back_scan_backward_split(
+    int dtype, const void* values, const int64_t values_strides[4], const void* logits,
+    const int64_t logits_strides[4], const void* inits, const int64_t inits_strides[3],
+    const float* logit_bias, const void* hq, const int64_t hq_strides[4], const void* hk,
+    const int64_t hk_strides[4], const void* hv, const int64_t hv_strides[4],
+    const void* grad_hq, const int64_t grad_hq_strides[4], const void* grad_hk,
+    const int64_t grad_hk_strides[4], const void* grad_hv, const int64_t grad_hv_strides[4],
+    void* grad_values, const int64_t grad_values_strides[4], void* grad_logits,
+    const int64_t grad_logits_strides[4], void* grad_inits, const int64_t grad_inits_strides[3],
+    float* grad_logit_bias, void* workspace, size_t workspace_bytes, int B, int T, int NH,
+    int NKVH, int Da, int r, int P, int Q, int K, int use_sigmoid, void* stream);
 
 /* ------------------------------------------------------------------------
  * Projection, reference layout: out[b] (F x T) = weight (F x K) . x[b]^T

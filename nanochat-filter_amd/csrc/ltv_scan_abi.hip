@@ -40,9 +40,34 @@ int scan_launch_fwd(bool bf16, const FwdArgs& a, ScanCfg cfg, int grid, bool vec
 }
 
 int scan_launch_bwd(bool bf16, const BwdArgs& a, ScanCfg cfg, int grid, bool vec, int gm,
-                    hipStream_t st) {
-  return bf16 ? scan_bwd_launch_bf16(a, cfg, grid, vec, gm, st)
-              : scan_bwd_launch_f32(a, cfg, grid, vec, gm, st);
+                    bool lb, hipStream_t st) {
+  return bf16 ? scan_bwd_launch_bf16(a, cfg, grid, vec, gm, lb, st)
+              : scan_bwd_launch_f32(a, cfg, grid, vec, gm, lb, st);
+}
+
+int scan_launch_lb_fold(bool bf16, const BwdArgs& a, hipStream_t st) {
+  const ScanShape& S = a.sh;
+  const int64_t n = (int64_t)S.B * S.H * a.nchunk * a.kw * (S.D + S.Da);
+  const int64_t blocks = (n + 255) / 256;
+  LTV_REQUIRE(blocks < (1ll << 31), LTV_ERR_UNSUPPORTED, "look-back warm-up too large");
+  if (bf16)
+    hipLaunchKernelGGL(scan_lb_fold_kernel<bf16_t>, dim3((int)blocks), dim3(256), 0, st, a);
+  else
+    hipLaunchKernelGGL(scan_lb_fold_kernel<float>, dim3((int)blocks), dim3(256), 0, st, a);
+  LTV_LAUNCH_CHECK();
+  return LTV_OK;
+}
+
+int scan_launch_lb_dinit(bool bf16, const BwdArgs& a, hipStream_t st) {
+  const ScanShape& S = a.sh;
+  const int64_t n = (int64_t)S.B * S.H * S.D;
+  const int blocks = (int)((n + 255) / 256);
+  if (bf16)
+    hipLaunchKernelGGL(scan_lb_dinit_kernel<bf16_t>, dim3(blocks), dim3(256), 0, st, a);
+  else
+    hipLaunchKernelGGL(scan_lb_dinit_kernel<float>, dim3(blocks), dim3(256), 0, st, a);
+  LTV_LAUNCH_CHECK();
+  return LTV_OK;
 }
 
 int scan_launch_bwd_channel(bool bf16, const BwdArgs& a, float* dalpha, hipStream_t st) {
@@ -213,34 +238,20 @@ inline bool chanvec_ok(int r, int D, int V, const HostView4& lg) {
   return r == 1 && D % V == 0 && vec_ok(lg.p, lg.s, 3, V);
 }
 
-int scan_forward_impl(int dtype, const HostView4& u, const HostView4& lg, const HostView4& init,
-                      const float* bias, void* const outp[3], const int64_t* const outs[3], int B,
-                      int T, int NH, int NKVH, int Da, int r, int use_sigmoid, hipStream_t st) {
-  int rc = check_shape(dtype, B, T, NH, NKVH, Da, r);
-  if (rc) return rc;
+int check_pqk(int P, int Q, int K) {
+  LTV_REQUIRE(P >= 0 && Q >= 1 && K >= 1, LTV_ERR_INVALID_ARG,
+              "chunking needs P >= 0, Q >= 1, K >= 1 (P=%d Q=%d K=%d)", P, Q, K);
+  return LTV_OK;
+}
+
+// Forward launch over B * H * nwin windows x channel slabs (a.P/Q/K/nwin, and
+// a.wst / a.kw for the warm-up mode, already set): gate mode and launch shape.
+int launch_forward(int dtype, FwdArgs& a, bool vec, const HostView4& lg, int B, int T, int NH,
+                   int NKVH, int Da, int r, int use_sigmoid, hipStream_t st) {
   const int H = NH + 2 * NKVH;
   const int D = Da * r;
-  if (B == 0 || T == 0 || H == 0) return LTV_OK;
-  LTV_REQUIRE(bias != nullptr && u.p && lg.p && init.p, LTV_ERR_INVALID_ARG,
-              "null tensor pointer");
   const int V = dtype == LTV_DTYPE_BF16 ? 8 : 4;
   const int cl_full = next_pow2((D + V - 1) / V);
-
-  FwdArgs a;
-  a.u = to_dev(u);
-  a.lg = to_dev(lg);
-  a.init = to_dev(init);
-  a.bias = bias;
-  bool vec = (D % V == 0) && vec_ok(u.p, u.s, 3, V) && vec_ok(init.p, init.s, 3, V);
-  for (int i = 0; i < 3; ++i) {
-    a.out.p[i] = outp[i];
-    for (int k = 0; k < 4; ++k) a.out.s[i][k] = outs[i][k];
-    const int nh = i == 0 ? NH : NKVH;
-    if (nh > 0) {
-      LTV_REQUIRE(outp[i] != nullptr, LTV_ERR_INVALID_ARG, "null output pointer");
-      vec = vec && vec_ok(outp[i], outs[i], 3, V);
-    }
-  }
   int gm = GATE_CHAN;
   if (r % V == 0) gm = GATE_LANE;
   else if (vec && chanvec_ok(r, D, V, lg)) gm = GATE_CHANVEC;
@@ -257,9 +268,48 @@ int scan_forward_impl(int dtype, const HostView4& u, const HostView4& lg, const 
   if (vec && tu.fwd_cl > 0) cfg = ScanCfg{tu.fwd_cl < cl_full ? tu.fwd_cl : cl_full, tu.fwd_l, tu.fwd_nw};
   const int nslab = (D + cfg.CL * V - 1) / (cfg.CL * V);
   a.sh = ScanShape{B, T, NH, NKVH, Da, r, D, H, nslab, use_sigmoid};
-  const int64_t grid = (int64_t)B * H * nslab;
+  const int64_t grid = (int64_t)B * H * a.nwin * nslab;
   LTV_REQUIRE(grid < (1ll << 31), LTV_ERR_UNSUPPORTED, "grid too large");
   return scan_launch_fwd(dtype == LTV_DTYPE_BF16, a, cfg, (int)grid, vec, gm, st);
+}
+
+int scan_forward_impl(int dtype, const HostView4& u, const HostView4& lg, const HostView4& init,
+                      const float* bias, void* const outp[3], const int64_t* const outs[3], int B,
+                      int T, int NH, int NKVH, int Da, int r, int P, int Q, int K,
+                      int use_sigmoid, hipStream_t st) {
+  int rc = check_shape(dtype, B, T, NH, NKVH, Da, r);
+  if (rc) return rc;
+  rc = check_pqk(P, Q, K);
+  if (rc) return rc;
+  const int H = NH + 2 * NKVH;
+  const int D = Da * r;
+  if (B == 0 || T == 0 || H == 0) return LTV_OK;
+  LTV_REQUIRE(bias != nullptr && u.p && lg.p && init.p, LTV_ERR_INVALID_ARG,
+              "null tensor pointer");
+  const int V = dtype == LTV_DTYPE_BF16 ? 8 : 4;
+
+  FwdArgs a;
+  a.u = to_dev(u);
+  a.lg = to_dev(lg);
+  a.init = to_dev(init);
+  a.bias = bias;
+  a.P = P;
+  a.Q = Q;
+  a.K = K;
+  a.nwin = look_back_nwin(T, P, Q);
+  a.wst = nullptr;
+  a.kw = 0;
+  bool vec = (D % V == 0) && vec_ok(u.p, u.s, 3, V) && vec_ok(init.p, init.s, 3, V);
+  for (int i = 0; i < 3; ++i) {
+    a.out.p[i] = outp[i];
+    for (int k = 0; k < 4; ++k) a.out.s[i][k] = outs[i][k];
+    const int nh = i == 0 ? NH : NKVH;
+    if (nh > 0) {
+      LTV_REQUIRE(outp[i] != nullptr, LTV_ERR_INVALID_ARG, "null output pointer");
+      vec = vec && vec_ok(outp[i], outs[i], 3, V);
+    }
+  }
+  return launch_forward(dtype, a, vec, lg, B, T, NH, NKVH, Da, r, use_sigmoid, st);
 }
 
 // Upper bound on the backward's time chunks per (b, h).  With at least 256
@@ -282,16 +332,40 @@ int bwd_max_chunks(int B, int H, int T) {
 constexpr int kBwdFineSteps = 64;
 
 struct BwdWorkspace {
-  size_t partial = 0, agg = 0, carry = 0, dalpha = 0, total = 0;  // byte offsets
+  // byte offsets
+  size_t partial = 0, agg = 0, carry = 0, dalpha = 0;
+  size_t wst = 0, wdu = 0, wdl = 0, wdi = 0;  // look-back windows
+  size_t total = 0;
 };
 
-BwdWorkspace bwd_workspace_plan(int dtype, int B, int T, int NH, int NKVH, int Da, int r) {
+// Warm-up rows per look-back window (no window's warm-up is longer).
+inline int look_back_kw(int T, int K) { return std::min(K - 1, T); }
+
+BwdWorkspace bwd_workspace_plan(int dtype, int B, int T, int NH, int NKVH, int Da, int r, int P,
+                                int Q, int K) {
   const int H = NH + 2 * NKVH;
   const int V = dtype == LTV_DTYPE_BF16 ? 8 : 4;
   const int D = Da * r;
-  const int NC = bwd_max_chunks(B, H, T);
   auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
   BwdWorkspace w;
+  const int nwin = look_back_nwin(T, P, Q);
+  if (nwin > 1) {
+    const size_t es = dtype == LTV_DTYPE_BF16 ? 2 : 4;
+    const size_t rows = (size_t)B * H * nwin;
+    const size_t kw = (size_t)look_back_kw(T, K);
+    size_t off = al(rows * Da * sizeof(float));
+    w.wst = off;
+    off += al(rows * kw * D * es);
+    w.wdu = off;
+    off += al(rows * kw * D * sizeof(float));
+    w.wdl = off;
+    off += al(rows * kw * Da * sizeof(float));
+    w.wdi = off;
+    off += al(rows * D * sizeof(float));
+    w.total = off;
+    return w;
+  }
+  const int NC = bwd_max_chunks(B, H, T);
   size_t off = al((size_t)B * H * NC * Da * sizeof(float));
   if (NC > 1) {
     w.agg = off;
@@ -307,17 +381,20 @@ BwdWorkspace bwd_workspace_plan(int dtype, int B, int T, int NH, int NKVH, int D
   return w;
 }
 
-size_t bwd_workspace_bytes(int dtype, int B, int T, int NH, int NKVH, int Da, int r) {
-  return bwd_workspace_plan(dtype, B, T, NH, NKVH, Da, r).total;
+size_t bwd_workspace_bytes(int dtype, int B, int T, int NH, int NKVH, int Da, int r, int P,
+                          int Q, int K) {
+  return bwd_workspace_plan(dtype, B, T, NH, NKVH, Da, r, P, Q, K).total;
 }
 
 int scan_backward_impl(int dtype, const HostView4& u, const HostView4& lg, const HostView4& init,
                        const float* bias, const void* const hp[3], const int64_t* const hs[3],
                        const void* const gp[3], const int64_t* const gs[3], const HostView4& du,
                        const HostView4& dlg, const HostView4& dinit, float* dbias, void* ws,
-                       size_t ws_bytes, int B, int T, int NH, int NKVH, int Da, int r,
-                       int use_sigmoid, hipStream_t st) {
+                       size_t ws_bytes, int B, int T, int NH, int NKVH, int Da, int r, int P,
+                       int Q, int K, int use_sigmoid, hipStream_t st) {
   int rc = check_shape(dtype, B, T, NH, NKVH, Da, r);
+  if (rc) return rc;
+  rc = check_pqk(P, Q, K);
   if (rc) return rc;
   const int H = NH + 2 * NKVH;
   const int D = Da * r;
@@ -329,7 +406,7 @@ int scan_backward_impl(int dtype, const HostView4& u, const HostView4& lg, const
     LTV_HIP_CHECK(hipMemsetAsync(dbias, 0, sizeof(float) * H * Da, st));
     return LTV_OK;
   }
-  const size_t need = bwd_workspace_bytes(dtype, B, T, NH, NKVH, Da, r);
+  const size_t need = bwd_workspace_bytes(dtype, B, T, NH, NKVH, Da, r, P, Q, K);
   LTV_REQUIRE(ws != nullptr && ws_bytes >= need, LTV_ERR_WORKSPACE,
               "workspace too small: need %zu bytes, got %zu", need, ws_bytes);
   const int V = dtype == LTV_DTYPE_BF16 ? 8 : 4;
@@ -358,7 +435,7 @@ int scan_backward_impl(int dtype, const HostView4& u, const HostView4& lg, const
   a.du = to_dev(du);
   a.dlg = to_dev(dlg);
   a.dinit = to_dev(dinit);
-  const BwdWorkspace wp = bwd_workspace_plan(dtype, B, T, NH, NKVH, Da, r);
+  const BwdWorkspace wp = bwd_workspace_plan(dtype, B, T, NH, NKVH, Da, r, P, Q, K);
   char* wsb = reinterpret_cast<char*>(ws);
   a.dbias_partial = reinterpret_cast<float*>(wsb + wp.partial);
   a.nchunk = 1;
@@ -367,10 +444,66 @@ int scan_backward_impl(int dtype, const HostView4& u, const HostView4& lg, const
   a.fine_steps = T;
   a.agg = nullptr;
   a.carry = nullptr;
+  a.P = P;
+  a.Q = Q;
+  a.K = K;
+  a.kw = 0;
+  a.wst = nullptr;
+  a.wdu = a.wdl = a.wdi = nullptr;
 
   int gm = bwd_gate_mode(r, Da, V);
   if (gm == GATE_CHAN && vec && chanvec_ok(r, D, V, lg) && chanvec_ok(r, D, V, dlg))
     gm = GATE_CHANVEC;
+  const int nwin = look_back_nwin(T, P, Q);
+  if (nwin > 1) {
+    // Look-back windows: recompute each window's warm-up states, run every
+    // window's reverse chain, then fold the warm-up contributions into the
+    // owning windows' steps and sum the inits gradients.
+    LTV_REQUIRE(gm >= 0, LTV_ERR_UNSUPPORTED,
+                "look-back backward with several chunk windows needs gate groups of r "
+                "channels with r a multiple of %d and Da <= %d, or r dividing %d (r=%d Da=%d)",
+                V, kMaxLaneGroups, V, r, Da);
+    const int64_t grid = (int64_t)B * H * nwin;
+    LTV_REQUIRE(grid < (1ll << 31), LTV_ERR_UNSUPPORTED, "grid too large");
+    a.nchunk = nwin;
+    a.kw = look_back_kw(T, K);
+    a.wst = wsb + wp.wst;
+    a.wdu = reinterpret_cast<float*>(wsb + wp.wdu);
+    a.wdl = reinterpret_cast<float*>(wsb + wp.wdl);
+    a.wdi = reinterpret_cast<float*>(wsb + wp.wdi);
+    const bool bf16 = dtype == LTV_DTYPE_BF16;
+    if (a.kw > 0) {
+      FwdArgs f;
+      f.u = a.u;
+      f.lg = a.lg;
+      f.init = a.init;
+      f.bias = bias;
+      for (int i = 0; i < 3; ++i) {
+        f.out.p[i] = nullptr;
+        for (int k = 0; k < 4; ++k) f.out.s[i][k] = 0;
+      }
+      f.P = P;
+      f.Q = Q;
+      f.K = K;
+      f.nwin = nwin;
+      f.wst = const_cast<void*>(a.wst);
+      f.kw = a.kw;
+      const bool fvec = (D % V == 0) && vec_ok(u.p, u.s, 3, V) && vec_ok(init.p, init.s, 3, V);
+      rc = launch_forward(dtype, f, fvec, lg, B, T, NH, NKVH, Da, r, use_sigmoid, st);
+      if (rc) return rc;
+    }
+    const int cl = next_pow2((D + V - 1) / V);
+    const ScanCfg cfg{cl, vec && cl == 16 ? 2 : 4, 4};
+    rc = scan_launch_bwd(bf16, a, cfg, (int)grid, vec, gm, true, st);
+    if (rc) return rc;
+    if (a.kw > 0) {
+      rc = scan_launch_lb_fold(bf16, a, st);
+      if (rc) return rc;
+    }
+    rc = scan_launch_lb_dinit(bf16, a, st);
+    if (rc) return rc;
+    return scan_launch_dbias_reduce(a.dbias_partial, dbias, B, H, nwin, Da, st);
+  }
   if (gm >= 0) {
     // whole head per workgroup, 4 wavefronts.  Each lane keeps the next tile's
     // loads in flight; at 16 channel lanes (D = 128 in bf16) 2 steps per lane
@@ -402,7 +535,7 @@ int scan_backward_impl(int dtype, const HostView4& u, const HostView4& lg, const
       rc = scan_launch_bwd_chunk_maps(dtype == LTV_DTYPE_BF16, a, vec, st);
       if (rc) return rc;
     }
-    rc = scan_launch_bwd(dtype == LTV_DTYPE_BF16, a, cfg, (int)grid, vec, gm, st);
+    rc = scan_launch_bwd(dtype == LTV_DTYPE_BF16, a, cfg, (int)grid, vec, gm, false, st);
     if (rc) return rc;
   } else {
     LTV_REQUIRE((int64_t)B * H < (1ll << 31), LTV_ERR_UNSUPPORTED, "grid too large");
@@ -452,13 +585,16 @@ inline HostView4 view4(const void* p, const int64_t* s) {
 
 using namespace ltv;
 
-extern "C" int ltv_hm_scan_forward(int dtype, const void* combined,
-                                   const int64_t combined_strides[3], const void* inits,
-                                   const int64_t inits_strides[3], const float* logit_bias,
-                                   void* out_q, const int64_t out_q_strides[4], void* out_k,
-                                   const int64_t out_k_strides[4], void* out_v,
-                                   const int64_t out_v_strides[4], int B, int T, int NH, int NKVH,
-                                   int Da, int r, int use_sigmoid, void* stream) {
+namespace {
+constexpr int kUnboundedP = 2147483647;  // P of the full recurrence: one window
+}
+
+extern "C" int ltv_hm_look_back_scan_forward(
+    int dtype, const void* combined, const int64_t combined_strides[3], const void* inits,
+    const int64_t inits_strides[3], const float* logit_bias, void* out_q,
+    const int64_t out_q_strides[4], void* out_k, const int64_t out_k_strides[4], void* out_v,
+    const int64_t out_v_strides[4], int B, int T, int NH, int NKVH, int Da, int r, int P, int Q,
+    int K, int use_sigmoid, void* stream) {
   LTV_REQUIRE(combined_strides && inits_strides && out_q_strides && out_k_strides &&
                   out_v_strides,
               LTV_ERR_INVALID_ARG, "null stride array");
@@ -469,7 +605,36 @@ extern "C" int ltv_hm_scan_forward(int dtype, const void* combined,
   return scan_forward_impl(dtype, values_view(combined, combined_strides, D, Da),
                            logits_view(combined, combined_strides, D, Da, es),
                            view3(inits, inits_strides), logit_bias, outp, outs, B, T, NH, NKVH,
-                           Da, r, use_sigmoid, (hipStream_t)stream);
+                           Da, r, P, Q, K, use_sigmoid, (hipStream_t)stream);
+}
+
+extern "C" int ltv_hm_scan_forward(int dtype, const void* combined,
+                                   const int64_t combined_strides[3], const void* inits,
+                                   const int64_t inits_strides[3], const float* logit_bias,
+                                   void* out_q, const int64_t out_q_strides[4], void* out_k,
+                                   const int64_t out_k_strides[4], void* out_v,
+                                   const int64_t out_v_strides[4], int B, int T, int NH, int NKVH,
+                                   int Da, int r, int use_sigmoid, void* stream) {
+  return ltv_hm_look_back_scan_forward(dtype, combined, combined_strides, inits, inits_strides,
+                                       logit_bias, out_q, out_q_strides, out_k, out_k_strides,
+                                       out_v, out_v_strides, B, T, NH, NKVH, Da, r, kUnboundedP,
+                                       1, 1, use_sigmoid, stream);
+}
+
+extern "C" int ltv_hm_look_back_scan_forward_split(
+    int dtype, const void* values, const int64_t values_strides[4], const void* logits,
+    const int64_t logits_strides[4], const void* inits, const int64_t inits_strides[3],
+    const float* logit_bias, void* out_q, const int64_t out_q_strides[4], void* out_k,
+    const int64_t out_k_strides[4], void* out_v, const int64_t out_v_strides[4], int B, int T,
+    int NH, int NKVH, int Da, int r, int P, int Q, int K, int use_sigmoid, void* stream) {
+  LTV_REQUIRE(values_strides && logits_strides && inits_strides && out_q_strides &&
+                  out_k_strides && out_v_strides,
+              LTV_ERR_INVALID_ARG, "null stride array");
+  void* outp[3] = {out_q, out_k, out_v};
+  const int64_t* outs[3] = {out_q_strides, out_k_strides, out_v_strides};
+  return scan_forward_impl(dtype, view4(values, values_strides), view4(logits, logits_strides),
+                           view3(inits, inits_strides), logit_bias, outp, outs, B, T, NH, NKVH,
+                           Da, r, P, Q, K, use_sigmoid, (hipStream_t)stream);
 }
 
 extern "C" int ltv_hm_scan_forward_split(
@@ -478,22 +643,25 @@ extern "C" int ltv_hm_scan_forward_split(
     const float* logit_bias, void* out_q, const int64_t out_q_strides[4], void* out_k,
     const int64_t out_k_strides[4], void* out_v, const int64_t out_v_strides[4], int B, int T,
     int NH, int NKVH, int Da, int r, int use_sigmoid, void* stream) {
-  LTV_REQUIRE(values_strides && logits_strides && inits_strides && out_q_strides &&
-                  out_k_strides && out_v_strides,
-              LTV_ERR_INVALID_ARG, "null stride array");
-  void* outp[3] = {out_q, out_k, out_v};
-  const int64_t* outs[3] = {out_q_strides, out_k_strides, out_v_strides};
-  return scan_forward_impl(dtype, view4(values, values_strides), view4(logits, logits_strides),
-                           view3(inits, inits_strides), logit_bias, outp, outs, B, T, NH, NKVH,
-                           Da, r, use_sigmoid, (hipStream_t)stream);
+  return ltv_hm_look_back_scan_forward_split(
+      dtype, values, values_strides, logits, logits_strides, inits, inits_strides, logit_bias,
+      out_q, out_q_strides, out_k, out_k_strides, out_v, out_v_strides, B, T, NH, NKVH, Da, r,
+      kUnboundedP, 1, 1, use_sigmoid, stream);
+}
+
+extern "C" size_t ltv_hm_look_back_scan_backward_workspace_size(int dtype, int B, int T, int NH,
+                                                                int NKVH, int Da, int r, int P,
+                                                                int Q, int K) {
+  if (P < 0 || Q < 1 || K < 1) return 0;
+  return bwd_workspace_bytes(dtype, B, T, NH, NKVH, Da, r, P, Q, K);
 }
 
 extern "C" size_t ltv_hm_scan_backward_workspace_size(int dtype, int B, int T, int NH, int NKVH,
                                                       int Da, int r) {
-  return bwd_workspace_bytes(dtype, B, T, NH, NKVH, Da, r);
+  return bwd_workspace_bytes(dtype, B, T, NH, NKVH, Da, r, kUnboundedP, 1, 1);
 }
 
-extern "C" int ltv_hm_scan_backward(
+extern "C" int ltv_hm_look_back_scan_backward(
     int dtype, const void* combined, const int64_t combined_strides[3], const void* inits,
     const int64_t inits_strides[3], const float* logit_bias, const void* hq,
     const int64_t hq_strides[4], const void* hk, const int64_t hk_strides[4], const void* hv,
@@ -501,8 +669,8 @@ extern "C" int ltv_hm_scan_backward(
     const void* grad_hk, const int64_t grad_hk_strides[4], const void* grad_hv,
     const int64_t grad_hv_strides[4], void* grad_combined, const int64_t grad_combined_strides[3],
     void* grad_inits, const int64_t grad_inits_strides[3], float* grad_logit_bias,
-    void* workspace, size_t workspace_bytes, int B, int T, int NH, int NKVH, int Da, int r,
-    int use_sigmoid, void* stream) {
+    void* workspace, size_t workspace_bytes, int B, int T, int NH, int NKVH, int Da, int r, int P,
+    int Q, int K, int use_sigmoid, void* stream) {
   LTV_REQUIRE(combined_strides && inits_strides && hq_strides && hk_strides && hv_strides &&
                   grad_hq_strides && grad_hk_strides && grad_hv_strides &&
                   grad_combined_strides && grad_inits_strides,
@@ -519,10 +687,28 @@ extern "C" int ltv_hm_scan_backward(
       logit_bias, hp, hs, gp, gs, values_view(grad_combined, grad_combined_strides, D, Da),
       logits_view(grad_combined, grad_combined_strides, D, Da, es),
       view3(grad_inits, grad_inits_strides), grad_logit_bias, workspace, workspace_bytes, B, T,
-      NH, NKVH, Da, r, use_sigmoid, (hipStream_t)stream);
+      NH, NKVH, Da, r, P, Q, K, use_sigmoid, (hipStream_t)stream);
 }
 
-extern "C" int ltv_hm_scan_backward_split(
+extern "C" int ltv_hm_scan_backward(
+    int dtype, const void* combined, const int64_t combined_strides[3], const void* inits,
+    const int64_t inits_strides[3], const float* logit_bias, const void* hq,
+    const int64_t hq_strides[4], const void* hk, const int64_t hk_strides[4], const void* hv,
+    const int64_t hv_strides[4], const void* grad_hq, const int64_t grad_hq_strides[4],
+    const void* grad_hk, const int64_t grad_hk_strides[4], const void* grad_hv,
+    const int64_t grad_hv_strides[4], void* grad_combined, const int64_t grad_combined_strides[3],
+    void* grad_inits, const int64_t grad_inits_strides[3], float* grad_logit_bias,
+    void* workspace, size_t workspace_bytes, int B, int T, int NH, int NKVH, int Da, int r,
+    int use_sigmoid, void* stream) {
+  return ltv_hm_look_back_scan_backward(
+      dtype, combined, combined_strides, inits, inits_strides, logit_bias, hq, hq_strides, hk,
+      hk_strides, hv, hv_strides, grad_hq, grad_hq_strides, grad_hk, grad_hk_strides, grad_hv,
+      grad_hv_strides, grad_combined, grad_combined_strides, grad_inits, grad_inits_strides,
+      grad_logit_bias, workspace, workspace_bytes, B, T, NH, NKVH, Da, r, kUnboundedP, 1, 1,
+      use_sigmoid, stream);
+}
+
+extern "C" int ltv_hm_look_back_scan_backward_split(
     int dtype, const void* values, const int64_t values_strides[4], const void* logits,
     const int64_t logits_strides[4], const void* inits, const int64_t inits_strides[3],
     const float* logit_bias, const void* hq, const int64_t hq_strides[4], const void* hk,
@@ -532,7 +718,7 @@ extern "C" int ltv_hm_scan_backward_split(
     void* grad_values, const int64_t grad_values_strides[4], void* grad_logits,
     const int64_t grad_logits_strides[4], void* grad_inits, const int64_t grad_inits_strides[3],
     float* grad_logit_bias, void* workspace, size_t workspace_bytes, int B, int T, int NH,
-    int NKVH, int Da, int r, int use_sigmoid, void* stream) {
+    int NKVH, int Da, int r, int P, int Q, int K, int use_sigmoid, void* stream) {
   LTV_REQUIRE(values_strides && logits_strides && inits_strides && hq_strides && hk_strides &&
                   hv_strides && grad_hq_strides && grad_hk_strides && grad_hv_strides &&
                   grad_values_strides && grad_logits_strides && grad_inits_strides,
@@ -546,6 +732,25 @@ extern "C" int ltv_hm_scan_backward_split(
                             view4(grad_values, grad_values_strides),
                             view4(grad_logits, grad_logits_strides),
                             view3(grad_inits, grad_inits_strides), grad_logit_bias, workspace,
-                            workspace_bytes, B, T, NH, NKVH, Da, r, use_sigmoid,
+                            workspace_bytes, B, T, NH, NKVH, Da, r, P, Q, K, use_sigmoid,
                             (hipStream_t)stream);
+}
+
+extern "C" int ltv_hm_scan_backward_split(
+    int dtype, const void* values, const int64_t values_strides[4], const void* logits,
+    const int64_t logits_strides[4], const void* inits, const int64_t inits_strides[3],
+    const float* logit_bias, const void* hq, const int64_t hq_strides[4], const void* hk,
+    const int64_t hk_strides[4], const void* hv, const int64_t hv_strides[4],
+    const void* grad_hq, const int64_t grad_hq_strides[4], const void* grad_hk,
+    const int64_t grad_hk_strides[4], const void* grad_hv, const int64_t grad_hv_strides[4],
+    void* grad_values, const int64_t grad_values_strides[4], void* grad_logits,
+    const int64_t grad_logits_strides[4], void* grad_inits, const int64_t grad_inits_strides[3],
+    float* grad_logit_bias, void* workspace, size_t workspace_bytes, int B, int T, int NH,
+    int NKVH, int Da, int r, int use_sigmoid, void* stream) {
+  return ltv_hm_look_back_scan_backward_split(
+      dtype, values, values_strides, logits, logits_strides, inits, inits_strides, logit_bias,
+      hq, hq_strides, hk, hk_strides, hv, hv_strides, grad_hq, grad_hq_strides, grad_hk,
+      grad_hk_strides, grad_hv, grad_hv_strides, grad_values, grad_values_strides, grad_logits,
+      grad_logits_strides, grad_inits, grad_inits_strides, grad_logit_bias, workspace,
+      workspace_bytes, B, T, NH, NKVH, Da, r, kUnboundedP, 1, 1, use_sigmoid, stream);
 }

@@ -2,8 +2,8 @@
 #include "ltv_scan_launch.hpp"
 
 namespace ltv {
-int scan_bwd_launch_f32(const BwdArgs& a, ScanCfg c, int grid, bool vec, int gm,
+int scan_bwd_launch_f32(const BwdArgs& a, ScanCfg c, int grid, bool vec, int gm, bool lb,
                         hipStream_t st) {
-  return scan_bwd_launch_t<float>(a, c, grid, vec, gm, st);
+  return scan_bwd_launch_t<float>(a, c, grid, vec, gm, lb, st);
 }
 }  // namespace ltv

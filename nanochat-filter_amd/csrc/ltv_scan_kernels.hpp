@@ -78,6 +78,33 @@ struct ScanShape {
   int use_sigmoid;
 };
 
+// Chunk windows of the look-back scan (nanochat/ops/ltv_reference_ops.py:65-75,
+// 99-101): chunk 0 covers [0, min(P, T)), chunk c >= 1 covers
+// [P + (c - 1) Q, min(P + c Q, T)); each chunk [st, hi) restarts the recurrence
+// from the inits at lo = max(0, st - (K - 1)) and owns the outputs of [st, hi).
+// P >= T gives the single window [0, T) of the full recurrence.
+struct Window {
+  int lo, st, hi;
+};
+
+__host__ __device__ inline Window look_back_window(int c, int T, int P, int Q, int K) {
+  Window w;
+  if (c == 0) {
+    w.st = 0;
+    w.hi = P < T ? P : T;
+  } else {
+    w.st = P + (c - 1) * Q;  // < T for every chunk that exists
+    w.hi = (int64_t)w.st + Q < T ? w.st + Q : T;
+  }
+  w.lo = w.st - (K - 1) > 0 ? w.st - (K - 1) : 0;
+  return w;
+}
+
+// Number of chunk windows (1 when P >= T).
+__host__ __device__ inline int look_back_nwin(int T, int P, int Q) {
+  return T > P ? 1 + (int)(((int64_t)T - P + Q - 1) / Q) : 1;
+}
+
 struct FwdArgs {
   ScanShape sh;
   View4 u;     // values   (B, H, T, D)
@@ -85,6 +112,11 @@ struct FwdArgs {
   View4 init;  // inits    (B, H, D) -- s[2] unused
   const float* bias;  // (H, Da) contiguous fp32
   OutHeads out;
+  int P, Q, K, nwin;  // chunk windows; one workgroup per (b, h, window, slab)
+  // Warm-up mode (wst != null): each window runs only its warm-up [lo, st) and
+  // stores the states to wst (B, H, nwin, kw, D) in the I/O dtype, row t - lo.
+  void* wst;
+  int kw;
 };
 
 struct BwdArgs {
@@ -109,6 +141,18 @@ struct BwdArgs {
   int nfine, fine_steps;
   float* agg;          // (2, B H, nfine, D): each sub-chunk's map g_start = A g_end + G
   float* carry;        // (B H, nchunk, D)
+  // Look-back windows (the LB kernels): chunk c of the nchunk = nwin windows
+  // runs its own reverse chain over [lo, hi) from g_hi = 0 with upstream
+  // gradients on [st, hi) only.  The states entering its warm-up steps come
+  // from wst (B, H, nwin, kw, D), I/O dtype, row t - lo; its contributions on
+  // warm-up steps go to wdu (B, H, nwin, kw, D) and wdl (B, H, nwin, kw, Da)
+  // in fp32 (added to the owning chunk's gradient by scan_lb_fold_kernel), and
+  // its inits gradient to wdi (B, H, nwin, D).
+  int P, Q, K, kw;
+  const void* wst;
+  float* wdu;
+  float* wdl;
+  float* wdi;
 };
 
 // How a lane finds the gate of each of its V channels.
@@ -199,6 +243,21 @@ __device__ __forceinline__ void st_vec(TIO* base, int64_t sc, int nvalid,
 #pragma unroll
     for (int v = 0; v < Pack<TIO>::V; ++v)
       if (v < nvalid) Pack<TIO>::store1(base + v * sc, x[v]);
+  }
+}
+
+// V fp32 values to p[0], ..., p[nvalid - 1] (16-byte stores when VEC: p is
+// then 16-byte aligned and all V values are valid).
+template <bool VEC, int V>
+__device__ __forceinline__ void st_f32(float* p, int nvalid, const float (&x)[V]) {
+  if (VEC) {
+#pragma unroll
+    for (int q = 0; q < V / 4; ++q)
+      reinterpret_cast<float4*>(p)[q] = make_float4(x[4 * q], x[4 * q + 1], x[4 * q + 2], x[4 * q + 3]);
+  } else {
+#pragma unroll
+    for (int v = 0; v < V; ++v)
+      if (v < nvalid) p[v] = x[v];
   }
 }
 
@@ -364,8 +423,13 @@ scan_fwd_kernel(const FwdArgs args) {
   int bid = blockIdx.x;
   const int slab = bid % S.nslab;
   bid /= S.nslab;
+  const int win = bid % args.nwin;
+  bid /= args.nwin;
   const int h = bid % S.H;
   const int b = bid / S.H;
+  const Window wd = look_back_window(win, S.T, args.P, args.Q, args.K);
+  // steps [t_lo, t_hi) are scanned from the inits; [t_st, t_hi) are stored
+  int t_lo = wd.lo, t_st = wd.st, t_hi = wd.hi;
 
   const int c0 = (slab * CL + cl) * V;
   const int nvalid = min(V, S.D - c0);
@@ -374,9 +438,17 @@ scan_fwd_kernel(const FwdArgs args) {
   int which, hl;
   head_select(h, S.NH, S.NKVH, which, hl);
   const HeadView ov = head_view(args.out, which);
-  const int64_t os[4] = {ov.s[0], ov.s[1], ov.s[2], ov.s[3]};
+  int64_t os[4] = {ov.s[0], ov.s[1], ov.s[2], ov.s[3]};
   TIO* outp = reinterpret_cast<TIO*>(ov.p) + (int64_t)b * os[0] + (int64_t)hl * os[1] +
               (int64_t)c0 * os[3];
+  if (args.wst != nullptr) {  // warm-up mode: the states of [lo, st), rows t - lo
+    t_hi = t_st;
+    t_st = t_lo;
+    outp = reinterpret_cast<TIO*>(args.wst) +
+           ((((int64_t)b * S.H + h) * args.nwin + win) * args.kw - t_lo) * S.D + c0;
+    os[2] = S.D;
+    os[3] = 1;
+  }
 
   const TIO* up = reinterpret_cast<const TIO*>(args.u.p) + (int64_t)b * args.u.s[0] +
                   (int64_t)h * args.u.s[1] + (int64_t)c0 * args.u.s[3];
@@ -400,7 +472,7 @@ scan_fwd_kernel(const FwdArgs args) {
   __shared__ float lds_a[2][NW][CL][NA];
   __shared__ float4 lds_x[2][NW][CL][V / 4];
 
-  const int ntiles = (S.T + TW - 1) / TW;
+  const int ntiles = (t_hi - t_lo + TW - 1) / TW;
   const bool use_sig = S.use_sigmoid != 0;
   const int64_t ust = args.u.s[2], usc = args.u.s[3], lst = args.lg.s[2];
 
@@ -410,24 +482,24 @@ scan_fwd_kernel(const FwdArgs args) {
   uint4 nu[L];
   LogitRaw<TIO, GM, L> nl;
   auto load_tile = [&](int it) {
-    const int t0 = it * TW + tl0;
+    const int t0 = t_lo + it * TW + tl0;
 #pragma unroll
     for (int s = 0; s < L; ++s) {
-      const bool ok = active && (t0 + s) < S.T;
+      const bool ok = active && (t0 + s) < t_hi;
       nu[s] = ok ? ld_vec<TIO, VEC>(up + (int64_t)(t0 + s) * ust, usc, nvalid)
                  : make_uint4(0u, 0u, 0u, 0u);
     }
-    nl.load(lp + (int64_t)t0 * lst, lst, gi, t0, S.T, active, nvalid);
+    nl.load(lp + (int64_t)t0 * lst, lst, gi, t0, t_hi, active, nvalid);
   };
   load_tile(0);
 
   for (int it = 0; it < ntiles; ++it) {
-    const int t0 = it * TW + tl0;
+    const int t0 = t_lo + it * TW + tl0;
     uint4 uq[L];
 #pragma unroll
     for (int s = 0; s < L; ++s) uq[s] = nu[s];
     float al[L][NA];
-    nl.gates(gi, t0, S.T, active, use_sig, al);
+    nl.gates(gi, t0, t_hi, active, use_sig, al);
     if (it + 1 < ntiles) load_tile(it + 1);
 
     // level 1: lane-local fold (padded steps have alpha = 0: the identity)
@@ -505,7 +577,8 @@ scan_fwd_kernel(const FwdArgs args) {
         const float a = al[s][GL ? 0 : v];
         hv[v] = fmaf(a, Pack<TIO>::get(uq[s], v) - hv[v], hv[v]);
       }
-      if (active && (t0 + s) < S.T) st_vec<TIO, VEC>(outp + (int64_t)(t0 + s) * os[2], os[3], nvalid, hv);
+      if (active && (t0 + s) >= t_st && (t0 + s) < t_hi)
+        st_vec<TIO, VEC>(outp + (int64_t)(t0 + s) * os[2], os[3], nvalid, hv);
     }
   }
 }
@@ -518,7 +591,7 @@ scan_fwd_kernel(const FwdArgs args) {
 // GATE_CHAN / GATE_CHANVEC: V % r == 0; each lane holds V / r whole groups.
 constexpr int kMaxLaneGroups = 16;
 
-template <typename TIO, int CL, int L, int NW, bool VEC, int GM>
+template <typename TIO, int CL, int L, int NW, bool VEC, int GM, bool LB>
 __global__ void __launch_bounds__(NW * 64)
 scan_bwd_kernel(const BwdArgs args) {
   constexpr int V = Pack<TIO>::V;
@@ -586,7 +659,7 @@ scan_bwd_kernel(const BwdArgs args) {
   float gcarry[V];  // g at the first step after the current tile
 #pragma unroll
   for (int v = 0; v < V; ++v) gcarry[v] = 0.0f;
-  if (args.nchunk > 1) {
+  if (!LB && args.nchunk > 1) {
     const float* cp = args.carry + ((int64_t)bh * args.nchunk + chunk) * S.D + c0;
 #pragma unroll
     for (int v = 0; v < V; ++v) gcarry[v] = v < nvalid ? cp[v] : 0.0f;
@@ -601,10 +674,30 @@ scan_bwd_kernel(const BwdArgs args) {
     for (int k = 0; k < MAXG; ++k) lds_red[threadIdx.x][k] = 0.0f;
   }
 
-  const int ntiles = (S.T + TW - 1) / TW;
-  const int tiles_pc = args.chunk_steps / TW;
-  const int it_lo = chunk * tiles_pc;
-  const int it_hi = min(ntiles, it_lo + tiles_pc) - 1;
+  // tiles it_lo..it_hi of TW steps from t_base; steps < t_hi exist, upstream
+  // gradients and owned outputs start at t_st
+  int t_base, t_st, t_hi, it_lo, it_hi;
+  if (LB) {
+    const Window wd = look_back_window(chunk, S.T, args.P, args.Q, args.K);
+    t_base = wd.lo;
+    t_st = wd.st;
+    t_hi = wd.hi;
+    it_lo = 0;
+    it_hi = (t_hi - t_base + TW - 1) / TW - 1;  // -1: empty window
+  } else {
+    t_base = 0;
+    t_st = 0;
+    t_hi = S.T;
+    const int ntiles = (S.T + TW - 1) / TW;
+    const int tiles_pc = args.chunk_steps / TW;
+    it_lo = chunk * tiles_pc;
+    it_hi = min(ntiles, it_lo + tiles_pc) - 1;
+  }
+  // this window's rows of the look-back workspaces, indexed by absolute step
+  const int64_t wrow0 = LB ? ((int64_t)bh * args.nchunk + chunk) * args.kw - t_base : 0;
+  const TIO* wsp = LB ? reinterpret_cast<const TIO*>(args.wst) + wrow0 * S.D + c0 : nullptr;
+  float* wdup = LB ? args.wdu + wrow0 * S.D + c0 : nullptr;
+  float* wdlp = LB ? args.wdl + wrow0 * S.Da : nullptr;
   // The next (earlier) tile's packed u, gy and raw logits, and the state
   // entering each lane's first step, are loaded while the current tile is
   // processed, so each wavefront keeps its loads in flight across the tile's
@@ -616,25 +709,26 @@ scan_bwd_kernel(const BwdArgs args) {
   uint4 nu[L], ng[L], nh0;
   LogitRaw<TIO, GM, L + 1> nl;
   auto load_tile = [&](int it) {
-    const int t0 = it * TW + tl0;
+    const int t0 = t_base + it * TW + tl0;
 #pragma unroll
     for (int s = 0; s < L; ++s) {
       const int t = t0 + s;
-      const bool ok = active && t < S.T;
+      const bool ok = active && t < t_hi;
       nu[s] = ok ? ld_vec<TIO, VEC>(up + (int64_t)t * ust, usc, nvalid)
                  : make_uint4(0u, 0u, 0u, 0u);
-      ng[s] = ok ? ld_vec<TIO, VEC>(gp + (int64_t)t * gs[2], gs[3], nvalid)
-                 : make_uint4(0u, 0u, 0u, 0u);
+      ng[s] = ok && (!LB || t >= t_st) ? ld_vec<TIO, VEC>(gp + (int64_t)t * gs[2], gs[3], nvalid)
+                                       : make_uint4(0u, 0u, 0u, 0u);
     }
-    const bool ok0 = active && t0 < S.T;
-    nh0 = !ok0      ? make_uint4(0u, 0u, 0u, 0u)
-          : t0 == 0 ? ld_vec<TIO, VEC>(ip, args.init.s[3], nvalid)
-                    : ld_vec<TIO, VEC>(hp + (int64_t)(t0 - 1) * hs[2], hs[3], nvalid);
-    nl.load(lp + (int64_t)t0 * lst, lst, gi, t0, S.T, active, nvalid);
+    const bool ok0 = active && t0 < t_hi;
+    nh0 = !ok0                      ? make_uint4(0u, 0u, 0u, 0u)
+          : t0 == t_base            ? ld_vec<TIO, VEC>(ip, args.init.s[3], nvalid)
+          : (LB && t0 - 1 < t_st)   ? ld_vec<TIO, VEC>(wsp + (int64_t)(t0 - 1) * S.D, 1, nvalid)
+                                    : ld_vec<TIO, VEC>(hp + (int64_t)(t0 - 1) * hs[2], hs[3], nvalid);
+    nl.load(lp + (int64_t)t0 * lst, lst, gi, t0, t_hi, active, nvalid);
   };
   if (it_hi >= it_lo) load_tile(it_hi);
   for (int it = it_hi; it >= it_lo; --it) {
-    const int T0 = it * TW;
+    const int T0 = t_base + it * TW;
     const int t0 = T0 + tl0;
 
     uint4 uq[L], gq[L], hq[L];
@@ -645,7 +739,7 @@ scan_bwd_kernel(const BwdArgs args) {
     }
     hq[0] = nh0;
     float al[L + 1][NA];
-    nl.gates(gi, t0, S.T, active, use_sig, al);
+    nl.gates(gi, t0, t_hi, active, use_sig, al);
     if (it > it_lo) load_tile(it - 1);
     // h_{t-1} of the lane's later steps (padded steps have alpha = 0)
 #pragma unroll
@@ -671,8 +765,8 @@ scan_bwd_kernel(const BwdArgs args) {
 #pragma unroll
       for (int s = L - 1; s >= 0; --s) {
         const int t = t0 + s;
-        if (active && t < S.T) {
-          const bool nxt = t + 1 < S.T;
+        if (active && t < t_hi) {
+          const bool nxt = t + 1 < t_hi;
 #pragma unroll
           for (int v = 0; v < V; ++v) {
             const float an = nxt ? 1.0f - al[s + 1][GL ? 0 : v] : 0.0f;
@@ -734,8 +828,8 @@ scan_bwd_kernel(const BwdArgs args) {
 #pragma unroll
     for (int s = L - 1; s >= 0; --s) {
       const int t = t0 + s;
-      const bool ok = active && t < S.T;
-      const bool nxt = t + 1 < S.T;
+      const bool ok = active && t < t_hi;
+      const bool nxt = t + 1 < t_hi;
       float gv[V], duv[V], dav[V];
 #pragma unroll
       for (int v = 0; v < V; ++v) {
@@ -747,12 +841,18 @@ scan_bwd_kernel(const BwdArgs args) {
         dav[v] = (Pack<TIO>::get(uq[s], v) - Pack<TIO>::get(hq[s], v)) * gv[v];
       }
       if (ok) {
-        st_vec<TIO, VEC>(dup + (int64_t)t * args.du.s[2], args.du.s[3], nvalid, duv);
-        if (t == 0) {
+        if (LB && t < t_st)
+          st_f32<VEC, V>(wdup + (int64_t)t * S.D, nvalid, duv);
+        else
+          st_vec<TIO, VEC>(dup + (int64_t)t * args.du.s[2], args.du.s[3], nvalid, duv);
+        if (t == t_base) {
           float di[V];
 #pragma unroll
           for (int v = 0; v < V; ++v) di[v] = (1.0f - al[s][GL ? 0 : v]) * gv[v];
-          st_vec<TIO, VEC>(dip, args.dinit.s[3], nvalid, di);
+          if (LB)
+            st_f32<VEC, V>(args.wdi + ((int64_t)bh * args.nchunk + chunk) * S.D + c0, nvalid, di);
+          else
+            st_vec<TIO, VEC>(dip, args.dinit.s[3], nvalid, di);
         }
       }
       if (GL) {
@@ -783,7 +883,10 @@ scan_bwd_kernel(const BwdArgs args) {
           }
           if (GM == GATE_CHANVEC) {
             // r == 1: the V dlogits of this lane are contiguous
-            st_vec<TIO, true>(dlp + (int64_t)t * dlst + c0, 1, V, dl);
+            if (LB && t < t_st)
+              st_f32<true, V>(wdlp + (int64_t)t * S.Da + c0, V, dl);
+            else
+              st_vec<TIO, true>(dlp + (int64_t)t * dlst + c0, 1, V, dl);
 #pragma unroll
             for (int v = 0; v < V; ++v) dacc[v] += dl[v];
           } else {
@@ -791,8 +894,11 @@ scan_bwd_kernel(const BwdArgs args) {
             for (int v = 0; v < V; ++v) {
               if ((v & (S.r - 1)) == 0 && v < nvalid) {
                 dacc[v] += dl[v];
-                Pack<TIO>::store1(dlp + (int64_t)t * dlst + (int64_t)((c0 + v) / S.r) * dlsc,
-                                  dl[v]);
+                const int j = (c0 + v) / S.r;
+                if (LB && t < t_st)
+                  wdlp[(int64_t)t * S.Da + j] = dl[v];
+                else
+                  Pack<TIO>::store1(dlp + (int64_t)t * dlst + (int64_t)j * dlsc, dl[v]);
               }
             }
           }
@@ -815,7 +921,7 @@ scan_bwd_kernel(const BwdArgs args) {
       __syncthreads();  // (3)
       for (int tl = threadIdx.x; tl < TW; tl += NT) {
         const int t = T0 + tl;
-        if (t < S.T) {
+        if (t < t_hi) {
 #pragma unroll
           for (int j = 0; j < MAXG; ++j) {
             if (j < S.Da) {
@@ -823,7 +929,10 @@ scan_bwd_kernel(const BwdArgs args) {
               for (int q = 0; q < gl_lanes; ++q) p += lds_p[tl][j * gl_lanes + q];
               const float d = p * lds_sl[tl][j];
               lds_red[threadIdx.x][j] += d;
-              Pack<TIO>::store1(dlp + (int64_t)t * dlst + (int64_t)j * dlsc, d);
+              if (LB && t < t_st)
+                wdlp[(int64_t)t * S.Da + j] = d;
+              else
+                Pack<TIO>::store1(dlp + (int64_t)t * dlst + (int64_t)j * dlsc, d);
             }
           }
         }
@@ -971,6 +1080,78 @@ __global__ void __launch_bounds__(256) scan_bwd_agg_kernel(const BwdArgs args) {
 }
 
 // ---------------------------------------------------------------------------
+// Look-back backward: the contributions of later windows' warm-ups.
+//
+// A step t lies in the warm-up [lo_c, st_c) of the windows c = c0(t), c0(t)+1,
+// ... while lo_c <= t, where c0(t) is the first window starting after t.  Its
+// gradient is the owning window's (already in du / dlg, written by the LB tile
+// kernel) plus those windows' fp32 contributions, added in window order and
+// rounded once.  One thread per (b h, window, warm-up row, channel of the
+// D + Da value and logit slots); the thread whose window is c0(t) does the sum,
+// so each step is written by exactly one thread.
+// ---------------------------------------------------------------------------
+template <typename TIO>
+__global__ void __launch_bounds__(256) scan_lb_fold_kernel(const BwdArgs args) {
+  const ScanShape& S = args.sh;
+  const int nw = args.nchunk;
+  const int nch = S.D + S.Da;
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (int64_t)S.B * S.H * nw * args.kw * nch) return;
+  const int ch = (int)(idx % nch);
+  int64_t rest = idx / nch;
+  const int row = (int)(rest % args.kw);
+  rest /= args.kw;
+  const int win = (int)(rest % nw);
+  const int64_t bh = rest / nw;
+  if (win == 0) return;  // the first window has no warm-up
+  const Window wd = look_back_window(win, S.T, args.P, args.Q, args.K);
+  const int t = wd.lo + row;
+  if (t >= wd.st) return;
+  const int cfirst = t < args.P ? 1 : (t - args.P) / args.Q + 2;  // first window with st > t
+  if (win != cfirst) return;
+  const int h = (int)(bh % S.H), b = (int)(bh / S.H);
+  TIO* gp;
+  if (ch < S.D) {
+    gp = reinterpret_cast<TIO*>(const_cast<void*>(args.du.p)) + (int64_t)b * args.du.s[0] +
+         (int64_t)h * args.du.s[1] + (int64_t)t * args.du.s[2] + (int64_t)ch * args.du.s[3];
+  } else {
+    gp = reinterpret_cast<TIO*>(const_cast<void*>(args.dlg.p)) + (int64_t)b * args.dlg.s[0] +
+         (int64_t)h * args.dlg.s[1] + (int64_t)t * args.dlg.s[2] +
+         (int64_t)(ch - S.D) * args.dlg.s[3];
+  }
+  float acc = Pack<TIO>::load1(gp);
+  for (int c = win; c < nw; ++c) {
+    const Window wc = look_back_window(c, S.T, args.P, args.Q, args.K);
+    if (wc.lo > t) break;
+    const int64_t r = (bh * nw + c) * args.kw + (t - wc.lo);
+    acc += ch < S.D ? args.wdu[r * S.D + ch] : args.wdl[r * S.Da + (ch - S.D)];
+  }
+  Pack<TIO>::store1(gp, acc);
+}
+
+// grad_inits[b, h, d] = sum over the non-empty windows of their fp32
+// contributions, in window order.
+template <typename TIO>
+__global__ void __launch_bounds__(256) scan_lb_dinit_kernel(const BwdArgs args) {
+  const ScanShape& S = args.sh;
+  const int nw = args.nchunk;
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (int64_t)S.B * S.H * S.D) return;
+  const int d = (int)(idx % S.D);
+  const int64_t bh = idx / S.D;
+  const int h = (int)(bh % S.H), b = (int)(bh / S.H);
+  float acc = 0.0f;
+  for (int c = 0; c < nw; ++c) {
+    const Window wc = look_back_window(c, S.T, args.P, args.Q, args.K);
+    if (wc.hi > wc.lo) acc += args.wdi[(bh * nw + c) * S.D + d];
+  }
+  TIO* dip = reinterpret_cast<TIO*>(const_cast<void*>(args.dinit.p)) +
+             (int64_t)b * args.dinit.s[0] + (int64_t)h * args.dinit.s[1] +
+             (int64_t)d * args.dinit.s[3];
+  Pack<TIO>::store1(dip, acc);
+}
+
+// ---------------------------------------------------------------------------
 // Generic backward for gate groups that neither fill whole lanes nor fit inside
 // one (r neither a multiple nor a divisor of V, or too many groups per head).
 // One thread per (b, h, channel) walks T backwards; the per-channel dalpha terms
@@ -1063,9 +1244,13 @@ struct ScanCfg {
 // Forward: grid = B * H * nslab workgroups of NW * 64 threads.
 int scan_launch_fwd(bool bf16, const FwdArgs& a, ScanCfg cfg, int grid, bool vec, int gm,
                     hipStream_t st);
-// Backward main kernel: grid = B * H; CL channel lanes cover the whole head.
+// Backward main kernel: grid = B * H * nchunk; CL channel lanes cover the whole
+// head; lb selects the look-back window kernels.
 int scan_launch_bwd(bool bf16, const BwdArgs& a, ScanCfg cfg, int grid, bool vec, int gm,
-                    hipStream_t st);
+                    bool lb, hipStream_t st);
+// Look-back backward: warm-up contributions into du / dlg, then grad_inits.
+int scan_launch_lb_fold(bool bf16, const BwdArgs& a, hipStream_t st);
+int scan_launch_lb_dinit(bool bf16, const BwdArgs& a, hipStream_t st);
 // Backward for gate groups outside the main kernel's reduction patterns.
 int scan_launch_bwd_channel(bool bf16, const BwdArgs& a, float* dalpha_ws, hipStream_t st);
 // dbias[h, j] = sum_b partial[b, h, j]

@@ -51,19 +51,26 @@ bool fwd_dispatch(const FwdArgs& a, int grid, bool vec, int gm, hipStream_t st) 
   return false;
 }
 
-template <typename TIO, int CL, int L, int NW>
-bool bwd_dispatch(const BwdArgs& a, int grid, bool vec, int gm, hipStream_t st) {
+// The look-back backward is built for the base shapes and for the shape the
+// d12 heads use (16 channel lanes, 2 steps per lane).
+template <int CL, int L, int NW>
+constexpr bool is_lb_cfg() {
+  return is_base_cfg<CL, L, NW>() || (CL == 16 && L == 2 && NW == 4);
+}
+
+template <typename TIO, int CL, int L, int NW, bool LB>
+bool bwd_dispatch_lb(const BwdArgs& a, int grid, bool vec, int gm, hipStream_t st) {
   const dim3 blk(NW * 64);
   if (vec) {
     switch (gm) {
       case GATE_LANE:
-        hipLaunchKernelGGL((scan_bwd_kernel<TIO, CL, L, NW, true, GATE_LANE>), dim3(grid), blk, 0, st, a);
+        hipLaunchKernelGGL((scan_bwd_kernel<TIO, CL, L, NW, true, GATE_LANE, LB>), dim3(grid), blk, 0, st, a);
         return true;
       case GATE_CHAN:
-        hipLaunchKernelGGL((scan_bwd_kernel<TIO, CL, L, NW, true, GATE_CHAN>), dim3(grid), blk, 0, st, a);
+        hipLaunchKernelGGL((scan_bwd_kernel<TIO, CL, L, NW, true, GATE_CHAN, LB>), dim3(grid), blk, 0, st, a);
         return true;
       case GATE_CHANVEC:
-        hipLaunchKernelGGL((scan_bwd_kernel<TIO, CL, L, NW, true, GATE_CHANVEC>), dim3(grid), blk, 0, st, a);
+        hipLaunchKernelGGL((scan_bwd_kernel<TIO, CL, L, NW, true, GATE_CHANVEC, LB>), dim3(grid), blk, 0, st, a);
         return true;
       default:
         return false;
@@ -72,15 +79,22 @@ bool bwd_dispatch(const BwdArgs& a, int grid, bool vec, int gm, hipStream_t st) 
   if constexpr (is_base_cfg<CL, L, NW>()) {
     switch (gm) {
       case GATE_LANE:
-        hipLaunchKernelGGL((scan_bwd_kernel<TIO, CL, L, NW, false, GATE_LANE>), dim3(grid), blk, 0, st, a);
+        hipLaunchKernelGGL((scan_bwd_kernel<TIO, CL, L, NW, false, GATE_LANE, LB>), dim3(grid), blk, 0, st, a);
         return true;
       case GATE_CHAN:
-        hipLaunchKernelGGL((scan_bwd_kernel<TIO, CL, L, NW, false, GATE_CHAN>), dim3(grid), blk, 0, st, a);
+        hipLaunchKernelGGL((scan_bwd_kernel<TIO, CL, L, NW, false, GATE_CHAN, LB>), dim3(grid), blk, 0, st, a);
         return true;
       default:
         return false;
     }
   }
+  return false;
+}
+
+template <typename TIO, int CL, int L, int NW>
+bool bwd_dispatch(const BwdArgs& a, int grid, bool vec, int gm, bool lb, hipStream_t st) {
+  if (!lb) return bwd_dispatch_lb<TIO, CL, L, NW, false>(a, grid, vec, gm, st);
+  if constexpr (is_lb_cfg<CL, L, NW>()) return bwd_dispatch_lb<TIO, CL, L, NW, true>(a, grid, vec, gm, st);
   return false;
 }
 
@@ -112,16 +126,17 @@ int scan_fwd_launch_t(const FwdArgs& a, ScanCfg c, int grid, bool vec, int gm, h
 }
 
 template <typename TIO>
-int scan_bwd_launch_t(const BwdArgs& a, ScanCfg c, int grid, bool vec, int gm, hipStream_t st) {
+int scan_bwd_launch_t(const BwdArgs& a, ScanCfg c, int grid, bool vec, int gm, bool lb,
+                      hipStream_t st) {
   bool ok = false;
 #define LTV_X(CL_, L_, NW_)                                                   \
   if (!ok && c.CL == CL_ && c.L == L_ && c.NW == NW_)                         \
-    ok = detail::bwd_dispatch<TIO, CL_, L_, NW_>(a, grid, vec, gm, st);
+    ok = detail::bwd_dispatch<TIO, CL_, L_, NW_>(a, grid, vec, gm, lb, st);
   LTV_SCAN_BWD_CONFIGS(LTV_X)
 #undef LTV_X
   if (!ok) {
-    set_error("scan backward: launch shape CL=%d L=%d NW=%d (vec=%d gate=%d) is not built",
-              c.CL, c.L, c.NW, (int)vec, gm);
+    set_error("scan backward: launch shape CL=%d L=%d NW=%d (vec=%d gate=%d look-back=%d) is not built",
+              c.CL, c.L, c.NW, (int)vec, gm, (int)lb);
     return LTV_ERR_UNSUPPORTED;
   }
   LTV_LAUNCH_CHECK();
@@ -131,7 +146,9 @@ int scan_bwd_launch_t(const BwdArgs& a, ScanCfg c, int grid, bool vec, int gm, h
 // Per-dtype entry points (defined in the four translation units).
 int scan_fwd_launch_bf16(const FwdArgs& a, ScanCfg c, int grid, bool vec, int gm, hipStream_t st);
 int scan_fwd_launch_f32(const FwdArgs& a, ScanCfg c, int grid, bool vec, int gm, hipStream_t st);
-int scan_bwd_launch_bf16(const BwdArgs& a, ScanCfg c, int grid, bool vec, int gm, hipStream_t st);
-int scan_bwd_launch_f32(const BwdArgs& a, ScanCfg c, int grid, bool vec, int gm, hipStream_t st);
+int scan_bwd_launch_bf16(const BwdArgs& a, ScanCfg c, int grid, bool vec, int gm, bool lb,
+                         hipStream_t st);
+int scan_bwd_launch_f32(const BwdArgs& a, ScanCfg c, int grid, bool vec, int gm, bool lb,
+                        hipStream_t st);
 
 }  // namespace ltv

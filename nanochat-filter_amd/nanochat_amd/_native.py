@@ -60,6 +60,39 @@ SIGNATURES = {
          _c_vp, _c_i64p, _c_vp, _c_i64p, _c_vp, _c_i64p, _c_vp,
          _c_vp, _c_sz, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_vp],
     ),
+    # the look-back forms: the same arguments plus P, Q, K before use_sigmoid
+    "ltv_hm_look_back_scan_forward": (
+        _c_int,
+        [_c_int, _c_vp, _c_i64p, _c_vp, _c_i64p, _c_vp, _c_vp, _c_i64p, _c_vp, _c_i64p, _c_vp,
+         _c_i64p, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
+         _c_int, _c_vp],
+    ),
+    "ltv_hm_look_back_scan_backward_workspace_size": (
+        _c_sz, [_c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int]),
+    "ltv_hm_look_back_scan_backward": (
+        _c_int,
+        [_c_int, _c_vp, _c_i64p, _c_vp, _c_i64p, _c_vp,
+         _c_vp, _c_i64p, _c_vp, _c_i64p, _c_vp, _c_i64p,
+         _c_vp, _c_i64p, _c_vp, _c_i64p, _c_vp, _c_i64p,
+         _c_vp, _c_i64p, _c_vp, _c_i64p, _c_vp,
+         _c_vp, _c_sz, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
+         _c_int, _c_vp],
+    ),
+    "ltv_hm_look_back_scan_forward_split": (
+        _c_int,
+        [_c_int, _c_vp, _c_i64p, _c_vp, _c_i64p, _c_vp, _c_i64p, _c_vp, _c_vp, _c_i64p, _c_vp,
+         _c_i64p, _c_vp, _c_i64p, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
+         _c_int, _c_int, _c_int, _c_vp],
+    ),
+    "ltv_hm_look_back_scan_backward_split": (
+        _c_int,
+        [_c_int, _c_vp, _c_i64p, _c_vp, _c_i64p, _c_vp, _c_i64p, _c_vp,
+         _c_vp, _c_i64p, _c_vp, _c_i64p, _c_vp, _c_i64p,
+         _c_vp, _c_i64p, _c_vp, _c_i64p, _c_vp, _c_i64p,
+         _c_vp, _c_i64p, _c_vp, _c_i64p, _c_vp, _c_i64p, _c_vp,
+         _c_vp, _c_sz, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
+         _c_int, _c_vp],
+    ),
     "ltv_linear_transpose_forward": (
         _c_int, [_c_int, _c_vp, _c_vp, _c_vp, _c_int, _c_int, _c_int, _c_int, _c_vp]),
     "ltv_linear_transpose_backward": (

@@ -75,17 +75,9 @@ class LtvCudaFusedConcatHeadMajorRegisterCastBlellochScanQkvFilter(
         return hq.transpose(1, 2), hk.transpose(1, 2), hv.transpose(1, 2)
 
     def _packed_weight(self):
-        """The bf16 packed weight, reused until ``c.weight`` changes (any in-place
-        update, e.g. an optimizer step or ``load_state_dict``, bumps its version)."""
-        w = self.c.weight
-        key = (w.data_ptr(), w._version, w.dtype, w.device)
-        cached = getattr(self, "_wpack_cache", None)
-        if cached is None or cached[0] != key:
-            H = self.n_head + 2 * self.n_kv_head
-            wpack = hm_fast.pack_weight(w.detach(), H, self.head_dim, self.num_alpha_groups)
-            cached = (key, wpack)
-            self._wpack_cache = cached
-        return cached[1]
+        """The bf16 packed weight, reused until ``c.weight`` changes."""
+        return hm_fast.cached_packed_weight(self, self.n_head + 2 * self.n_kv_head,
+                                            self.head_dim, self.num_alpha_groups)
 
     def _decode_bf16(self, x, previous_values):
         """T = 1 inference: one fused launch (projection of the new tokens and one

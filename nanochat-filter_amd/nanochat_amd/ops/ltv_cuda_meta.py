@@ -45,3 +45,19 @@ def _flt_op_fake(x, weight):
 @torch.library.register_fake("nanochat_cuda::fused_linear_transpose_backward_kernel")
 def _flt_bwd_fake(x, weight, grad_out, grad_x, grad_weight):
     return None
+
+
+# Look-back ops (reference nanochat/ops/ltv_cuda_meta.py:380-580): outputs
+# (B, NH|NKVH, T, D) like the full-recurrence op; the kernels return nothing.
+def _look_back_op_fake(combined, inits, logit_bias, NH, NKVH, da, r, *pqk_tuning_and_flag):
+    B, T, _ = combined.shape
+    D = da * r
+    mk = lambda h: combined.new_empty((B, h, T, D))  # noqa: E731
+    return mk(NH), mk(NKVH), mk(NKVH)
+
+
+for _variant in ("blelloch", "sequential"):
+    _base = f"nanochat_cuda::ltv_look_back_fused_concat_head_major_register_cast_{_variant}_scan_cuda"
+    torch.library.register_fake(f"{_base}_op")(_look_back_op_fake)
+    torch.library.register_fake(f"{_base}_forward_kernel")(lambda *args: None)
+    torch.library.register_fake(f"{_base}_backward_kernel")(lambda *args: None)

@@ -8,6 +8,9 @@ the same ``nanochat_cuda`` namespace so callers written against the reference
 ``ltv_cuda_fused_concat_head_major_register_cast_blelloch_scan.py`` and call the
 gfx950 HIP library through its C ABI.
 
+The look-back ops (``:172-241``, wrappers ``:332-410``) are implemented in
+``ltv_cuda_look_back_fused_concat_head_major_register_cast_{blelloch,sequential}_scan.py``.
+
 The filter module's own fast path uses two further ops in the ``nanochat_amd``
 namespace (``ltv_hm_fast.py``).
 """
@@ -48,6 +51,78 @@ lib.define(
     ") -> ()"
 )
 
+# Look-back variants (chunk restarts with a K - 1 step warm-up), schemas of the
+# reference's ops/ltv_cuda_ops.py:172-241.
+lib.define(
+    "ltv_look_back_fused_concat_head_major_register_cast_blelloch_scan_cuda_op("
+    "Tensor combined, Tensor inits, Tensor logit_bias, "
+    "int NH, int NKVH, int da, int r, "
+    "int P, int Q, int K, "
+    "int scan_threads_forward, int r_threads_forward, int r_items_forward, "
+    "int scan_threads_backward, int r_threads_backward, int r_items_backward, "
+    "bool use_sigmoid"
+    ") -> (Tensor, Tensor, Tensor)"
+)
+
+lib.define(
+    "ltv_look_back_fused_concat_head_major_register_cast_blelloch_scan_cuda_forward_kernel("
+    "Tensor combined, Tensor inits, Tensor logit_bias, "
+    "Tensor(a!) out_q, Tensor(b!) out_k, Tensor(c!) out_v, "
+    "int B, int T, int NH, int NKVH, int da, int r, "
+    "int P, int Q, int K, "
+    "int scan_threads_forward, int r_threads_forward, int r_items_forward, "
+    "bool use_sigmoid"
+    ") -> ()"
+)
+
+lib.define(
+    "ltv_look_back_fused_concat_head_major_register_cast_blelloch_scan_cuda_backward_kernel("
+    "Tensor combined, Tensor inits, Tensor logit_bias, "
+    "Tensor hq, Tensor hk, Tensor hv, "
+    "Tensor grad_hq, Tensor grad_hk, Tensor grad_hv, "
+    "Tensor(a!) grad_combined, Tensor(b!) grad_inits, Tensor(c!) grad_logit_bias, "
+    "int NH, int NKVH, int da, int r, "
+    "int P, int Q, int K, "
+    "int scan_threads_backward, int r_threads_backward, int r_items_backward, "
+    "bool use_sigmoid"
+    ") -> ()"
+)
+
+lib.define(
+    "ltv_look_back_fused_concat_head_major_register_cast_sequential_scan_cuda_op("
+    "Tensor combined, Tensor inits, Tensor logit_bias, "
+    "int NH, int NKVH, int da, int r, "
+    "int P, int Q, int K, "
+    "int r_threads_forward, int r_items_forward, "
+    "int r_threads_backward, int r_items_backward, "
+    "bool use_sigmoid"
+    ") -> (Tensor, Tensor, Tensor)"
+)
+
+lib.define(
+    "ltv_look_back_fused_concat_head_major_register_cast_sequential_scan_cuda_forward_kernel("
+    "Tensor combined, Tensor inits, Tensor logit_bias, "
+    "Tensor(a!) out_q, Tensor(b!) out_k, Tensor(c!) out_v, "
+    "int B, int T, int NH, int NKVH, int da, int r, "
+    "int P, int Q, int K, "
+    "int r_threads_forward, int r_items_forward, "
+    "bool use_sigmoid"
+    ") -> ()"
+)
+
+lib.define(
+    "ltv_look_back_fused_concat_head_major_register_cast_sequential_scan_cuda_backward_kernel("
+    "Tensor combined, Tensor inits, Tensor logit_bias, "
+    "Tensor hq, Tensor hk, Tensor hv, "
+    "Tensor grad_hq, Tensor grad_hk, Tensor grad_hv, "
+    "Tensor(a!) grad_combined, Tensor(b!) grad_inits, Tensor(c!) grad_logit_bias, "
+    "int NH, int NKVH, int da, int r, "
+    "int P, int Q, int K, "
+    "int r_threads_backward, int r_items_backward, "
+    "bool use_sigmoid"
+    ") -> ()"
+)
+
 lib.define("fused_linear_transpose(Tensor x, Tensor weight, Tensor(a!) out) -> ()")
 
 lib.define("fused_linear_transpose_cuda_op(Tensor x, Tensor weight) -> Tensor")
@@ -61,6 +136,8 @@ lib.define(
 
 import nanochat_amd.ops.fused_linear_transpose  # noqa: E402,F401  (registers impls)
 import nanochat_amd.ops.ltv_cuda_fused_concat_head_major_register_cast_blelloch_scan  # noqa: E402,F401
+import nanochat_amd.ops.ltv_cuda_look_back_fused_concat_head_major_register_cast_blelloch_scan  # noqa: E402,F401
+import nanochat_amd.ops.ltv_cuda_look_back_fused_concat_head_major_register_cast_sequential_scan  # noqa: E402,F401
 import nanochat_amd.ops.ltv_cuda_meta  # noqa: E402,F401
 
 
@@ -102,4 +179,55 @@ def ltv_cuda_fused_concat_head_major_register_cast_blelloch_scan(
         r_threads_backward,
         r_items_backward,
         use_sigmoid,
+    )
+
+
+def ltv_cuda_look_back_fused_concat_head_major_register_cast_blelloch_scan(
+    combined: torch.Tensor,
+    inits: torch.Tensor,
+    logit_bias: torch.Tensor,
+    NH: int,
+    NKVH: int,
+    da: int,
+    r: int,
+    P: int,
+    Q: int,
+    K: int,
+    scan_threads_forward: int,
+    r_threads_forward: int,
+    r_items_forward: int,
+    scan_threads_backward: int,
+    r_threads_backward: int,
+    r_items_backward: int,
+    use_sigmoid: bool,
+):
+    """Reference wrapper ``ops/ltv_cuda_ops.py:332-371``."""
+    return torch.ops.nanochat_cuda.ltv_look_back_fused_concat_head_major_register_cast_blelloch_scan_cuda_op(
+        combined, inits, logit_bias, NH, NKVH, da, r, P, Q, K,
+        scan_threads_forward, r_threads_forward, r_items_forward,
+        scan_threads_backward, r_threads_backward, r_items_backward, use_sigmoid,
+    )
+
+
+def ltv_cuda_look_back_fused_concat_head_major_register_cast_sequential_scan(
+    combined: torch.Tensor,
+    inits: torch.Tensor,
+    logit_bias: torch.Tensor,
+    NH: int,
+    NKVH: int,
+    da: int,
+    r: int,
+    P: int,
+    Q: int,
+    K: int,
+    r_threads_forward: int,
+    r_items_forward: int,
+    r_threads_backward: int,
+    r_items_backward: int,
+    use_sigmoid: bool,
+):
+    """Reference wrapper ``ops/ltv_cuda_ops.py:374-410``."""
+    return torch.ops.nanochat_cuda.ltv_look_back_fused_concat_head_major_register_cast_sequential_scan_cuda_op(
+        combined, inits, logit_bias, NH, NKVH, da, r, P, Q, K,
+        r_threads_forward, r_items_forward, r_threads_backward, r_items_backward, use_sigmoid,
     )

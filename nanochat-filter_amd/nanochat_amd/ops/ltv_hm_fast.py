@@ -12,7 +12,7 @@ with Fp = ``packed_width`` and Lp = ``logit_width``.
 
 Ops in the ``nanochat_amd`` namespace, each with a fake implementation:
 
-``qkv_filter(x, weight, inits, logit_bias, NH, NKVH, Da, r)``
+``qkv_filter(x, weight, inits, logit_bias, NH, NKVH, Da, r, P, Q, K)``
     -> (q, k, v, values, logits, wpack).  q (B, NH, T, D), k and v
     (B, NKVH, T, D), contiguous.  The last three outputs are the intermediates
     the backward reads; callers use only q, k, v.  Same result as the
@@ -22,6 +22,9 @@ Ops in the ``nanochat_amd`` namespace, each with a fake implementation:
     with a bf16 copy of the weight as the MFMA operand.  Autograd through
     ``qkv_filter_backward``: the scan backward writes grad_combined, then the
     projection backward reads it (grad_x, and grad_weight in fp32).
+    (P, Q, K) are the look-back chunking of
+    ``nanochat/ops/ltv_cuda_look_back_fused_concat_head_major_register_cast_blelloch_scan.py``;
+    the default P = 2**31 - 1 is the full recurrence.
 
 The helpers ``project``, ``project_backward``, ``scan_forward`` and
 ``scan_backward`` call the library directly; the tests use them to check each
@@ -37,6 +40,8 @@ import ctypes
 import torch
 
 from nanochat_amd import _native as N
+
+UNBOUNDED_P = 2_147_483_647  # look-back P of the full recurrence (one chunk window)
 
 
 def packed_width(H: int, D: int, Da: int) -> int:
@@ -98,6 +103,19 @@ def pack_weight(weight: torch.Tensor, H: int, D: int, Da: int) -> torch.Tensor:
                                          wpack.data_ptr(), H, D, Da, C, N.stream_of(weight))
     N.check(rc, "ltv_qkv_pack_weight")
     return wpack
+
+
+def cached_packed_weight(module, H: int, D: int, Da: int) -> torch.Tensor:
+    """The packed bf16 weight of ``module.c.weight``, kept on the module and
+    rebuilt when the weight changes (any in-place update, e.g. an optimizer
+    step or ``load_state_dict``, bumps its version)."""
+    w = module.c.weight
+    key = (w.data_ptr(), w._version, w.dtype, w.device)
+    cached = getattr(module, "_wpack_cache", None)
+    if cached is None or cached[0] != key:
+        cached = (key, pack_weight(w.detach(), H, D, Da))
+        module._wpack_cache = cached
+    return cached[1]
 
 
 def decode_step(x: torch.Tensor, wpack: torch.Tensor, prev, logit_bias: torch.Tensor, NH: int,
@@ -168,7 +186,7 @@ def project_backward(x: torch.Tensor, wpack: torch.Tensor, grad_combined: torch.
 
 def scan_forward(values: torch.Tensor, logits: torch.Tensor, inits: torch.Tensor,
                  logit_bias: torch.Tensor, NH: int, NKVH: int, Da: int, r: int,
-                 use_sigmoid: bool):
+                 use_sigmoid: bool, P: int = UNBOUNDED_P, Q: int = 1, K: int = 1):
     N.require_device(values, logits, inits, logit_bias)
     B, H, T, D = values.shape
     if H != NH + 2 * NKVH or D != Da * r:
@@ -182,27 +200,28 @@ def scan_forward(values: torch.Tensor, logits: torch.Tensor, inits: torch.Tensor
     sb, st_, sl = logits.stride()
     lgs = (sb, Da * sl, st_, sl)
     with N.span("scan_fwd"):
-        rc = N.lib().ltv_hm_scan_forward_split(
+        rc = N.lib().ltv_hm_look_back_scan_forward_split(
             N.dtype_code(values.dtype),
             values.data_ptr(), N.strides(values, 4), logits.data_ptr(), _arr(lgs),
             inits.data_ptr(), N.strides(inits, 3), logit_bias.data_ptr(),
             out[0].data_ptr(), N.strides(out[0], 4), out[1].data_ptr(), N.strides(out[1], 4),
             out[2].data_ptr(), N.strides(out[2], 4),
-            B, T, NH, NKVH, Da, r, int(bool(use_sigmoid)), N.stream_of(values))
-    N.check(rc, "ltv_hm_scan_forward_split")
+            B, T, NH, NKVH, Da, r, P, Q, K, int(bool(use_sigmoid)), N.stream_of(values))
+    N.check(rc, "ltv_hm_look_back_scan_forward_split")
     return out[0], out[1], out[2]
 
 
 def scan_backward(values, logits, inits, logit_bias, hq, hk, hv, gq, gk, gv, NH: int,
                   NKVH: int, Da: int, r: int, use_sigmoid: bool,
-                  grad_combined: torch.Tensor):
+                  grad_combined: torch.Tensor, P: int = UNBOUNDED_P, Q: int = 1, K: int = 1):
     """Writes grad_combined (B, T, Fp); returns (grad_inits, grad_logit_bias)."""
     B, H, T, D = values.shape
     dt = N.dtype_code(values.dtype)
     lib = N.lib()
     grad_inits = torch.empty((B, H, D), dtype=inits.dtype, device=inits.device)
     grad_bias = torch.empty((H, Da), dtype=torch.float32, device=values.device)
-    ws_bytes = lib.ltv_hm_scan_backward_workspace_size(dt, B, T, NH, NKVH, Da, r)
+    ws_bytes = lib.ltv_hm_look_back_scan_backward_workspace_size(dt, B, T, NH, NKVH, Da, r,
+                                                                 P, Q, K)
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=values.device)
     sb, st_, sl = logits.stride()
     lgs = (sb, Da * sl, st_, sl)
@@ -211,7 +230,7 @@ def scan_backward(values, logits, inits, logit_bias, hq, hk, hv, gq, gk, gv, NH:
     glgs = (gsb, Da * gsc, gst, gsc)
     glg_ptr = grad_combined.data_ptr() + H * D * gsc * grad_combined.element_size()
     with N.span("scan_bwd"):
-        rc = lib.ltv_hm_scan_backward_split(
+        rc = lib.ltv_hm_look_back_scan_backward_split(
             dt,
             values.data_ptr(), N.strides(values, 4), logits.data_ptr(), _arr(lgs),
             inits.data_ptr(), N.strides(inits, 3), logit_bias.data_ptr(),
@@ -221,9 +240,9 @@ def scan_backward(values, logits, inits, logit_bias, hq, hk, hv, gq, gk, gv, NH:
             gv.data_ptr(), N.strides(gv, 4),
             grad_combined.data_ptr(), _arr(gvals), glg_ptr, _arr(glgs),
             grad_inits.data_ptr(), N.strides(grad_inits, 3), grad_bias.data_ptr(),
-            ws.data_ptr(), ws_bytes, B, T, NH, NKVH, Da, r, int(bool(use_sigmoid)),
+            ws.data_ptr(), ws_bytes, B, T, NH, NKVH, Da, r, P, Q, K, int(bool(use_sigmoid)),
             N.stream_of(values))
-    N.check(rc, "ltv_hm_scan_backward_split")
+    N.check(rc, "ltv_hm_look_back_scan_backward_split")
     return grad_inits, grad_bias
 
 
@@ -232,18 +251,19 @@ def scan_backward(values, logits, inits, logit_bias, hq, hk, hv, gq, gk, gv, NH:
 # ---------------------------------------------------------------------------
 @torch.library.custom_op("nanochat_amd::qkv_filter", mutates_args=())
 def qkv_filter(x: torch.Tensor, weight: torch.Tensor, inits: torch.Tensor,
-               logit_bias: torch.Tensor, NH: int, NKVH: int, Da: int,
-               r: int) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor,
-                                torch.Tensor, torch.Tensor]:
+               logit_bias: torch.Tensor, NH: int, NKVH: int, Da: int, r: int,
+               P: int = UNBOUNDED_P, Q: int = 1,
+               K: int = 1) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor,
+                                    torch.Tensor, torch.Tensor]:
     H = NH + 2 * NKVH
     D = Da * r
     values, logits, wpack = project(x, weight, H, D, Da)
-    q, k, v = scan_forward(values, logits, inits, logit_bias, NH, NKVH, Da, r, True)
+    q, k, v = scan_forward(values, logits, inits, logit_bias, NH, NKVH, Da, r, True, P, Q, K)
     return q, k, v, values, logits, wpack
 
 
 @qkv_filter.register_fake
-def _(x, weight, inits, logit_bias, NH, NKVH, Da, r):
+def _(x, weight, inits, logit_bias, NH, NKVH, Da, r, P=UNBOUNDED_P, Q=1, K=1):
     B, T, C = x.shape
     H = NH + 2 * NKVH
     D = Da * r
@@ -259,8 +279,9 @@ def qkv_filter_backward(x: torch.Tensor, wpack: torch.Tensor, values: torch.Tens
                         logits: torch.Tensor, inits: torch.Tensor, logit_bias: torch.Tensor,
                         hq: torch.Tensor, hk: torch.Tensor, hv: torch.Tensor, gq: torch.Tensor,
                         gk: torch.Tensor, gv: torch.Tensor, NH: int, NKVH: int, Da: int,
-                        r: int) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor,
-                                         torch.Tensor]:
+                        r: int, P: int = UNBOUNDED_P, Q: int = 1,
+                        K: int = 1) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor,
+                                             torch.Tensor]:
     B, T, C = x.shape
     H = NH + 2 * NKVH
     D = Da * r
@@ -268,13 +289,14 @@ def qkv_filter_backward(x: torch.Tensor, wpack: torch.Tensor, values: torch.Tens
                                 device=x.device)
     grad_inits, grad_bias = scan_backward(values, logits, inits, logit_bias, hq, hk, hv,
                                           gq.to(hq.dtype), gk.to(hk.dtype), gv.to(hv.dtype),
-                                          NH, NKVH, Da, r, True, grad_combined)
+                                          NH, NKVH, Da, r, True, grad_combined, P, Q, K)
     grad_x, grad_w = project_backward(x, wpack, grad_combined, H, D, Da)
     return grad_x, grad_w, grad_inits, grad_bias
 
 
 @qkv_filter_backward.register_fake
-def _(x, wpack, values, logits, inits, logit_bias, hq, hk, hv, gq, gk, gv, NH, NKVH, Da, r):
+def _(x, wpack, values, logits, inits, logit_bias, hq, hk, hv, gq, gk, gv, NH, NKVH, Da, r,
+      P=UNBOUNDED_P, Q=1, K=1):
     B, T, C = x.shape
     H = NH + 2 * NKVH
     D = Da * r
@@ -284,10 +306,10 @@ def _(x, wpack, values, logits, inits, logit_bias, hq, hk, hv, gq, gk, gv, NH, N
 
 
 def _filter_setup(ctx, inputs, output):
-    x, weight, inits, logit_bias, NH, NKVH, Da, r = inputs
+    x, weight, inits, logit_bias, *args = inputs  # NH, NKVH, Da, r, P, Q, K
     q, k, v, values, logits, wpack = output
     ctx.save_for_backward(x, wpack, values, logits, inits, logit_bias, q, k, v)
-    ctx.args = (NH, NKVH, Da, r)
+    ctx.args = tuple(args)
     ctx.weight_dtype = weight.dtype
     # values / logits / wpack are internal outputs: no zero gradients for them
     ctx.set_materialize_grads(False)
@@ -304,7 +326,7 @@ def _filter_backward(ctx, gq, gk, gv, g_values, g_logits, g_wpack):
         x, wpack, values, logits, inits, logit_bias, q, k, v, gq, gk, gv, *ctx.args)
     if ctx.weight_dtype != torch.float32:
         gw = gw.to(ctx.weight_dtype)
-    return gx, gw, gi, gb.view_as(logit_bias), None, None, None, None
+    return (gx, gw, gi, gb.view_as(logit_bias)) + (None,) * len(ctx.args)
 
 
 qkv_filter.register_autograd(_filter_backward, setup_context=_filter_setup)

@@ -47,7 +47,7 @@ def test_abi_version_and_host_only_queries():
     if not os.path.exists(N.LIB_PATH):
         pytest.skip("library not built")
     lib = N.load()
-    assert lib.ltv_abi_version() == 2
+    assert lib.ltv_abi_version() == 3
     # d12: 18 heads x (128 + 1) = 2322 -> padded to a multiple of 128; 18 logits -> 24
     assert lib.ltv_qkv_packed_width(18, 128, 1) == 2432
     assert lib.ltv_qkv_logit_width(18, 1) == 24
@@ -59,6 +59,20 @@ def test_abi_version_and_host_only_queries():
     rc = lib.ltv_hm_scan_forward(7, None, None, None, None, None, None, None, None, None, None,
                                  None, 1, 1, 1, 1, 1, 1, 1, None)
     assert rc == 1
+    # look-back: P >= T is the full recurrence (same workspace); chunk windows
+    # need the warm-up buffers on top; bad chunking is an argument error
+    full = lib.ltv_hm_scan_backward_workspace_size(1, 4, 64, 2, 1, 1, 16)
+    assert lib.ltv_hm_look_back_scan_backward_workspace_size(1, 4, 64, 2, 1, 1, 16,
+                                                             2147483647, 1, 1) == full
+    assert lib.ltv_hm_look_back_scan_backward_workspace_size(1, 4, 64, 2, 1, 1, 16,
+                                                             64, 5, 3) == full
+    # 4 x 4 heads x 13 windows x 8 warm-up rows x 16 channels of bf16 states alone
+    assert lib.ltv_hm_look_back_scan_backward_workspace_size(1, 4, 64, 2, 1, 1, 16,
+                                                             16, 4, 9) > 4 * 4 * 13 * 8 * 16 * 2
+    s3, s4 = (ctypes.c_int64 * 3)(1, 1, 1), (ctypes.c_int64 * 4)(1, 1, 1, 1)
+    rc = lib.ltv_hm_look_back_scan_forward(1, None, s3, None, s3, None, None, s4, None, s4,
+                                           None, s4, 1, 1, 1, 1, 1, 1, 4, 0, 1, 1, None)
+    assert rc == 1 and "Q >= 1" in N.last_error()
 
 
 def test_ops_import_without_gpu():
@@ -66,6 +80,9 @@ def test_ops_import_without_gpu():
     import nanochat_amd.ops  # noqa: F401
     assert hasattr(torch.ops.nanochat_cuda,
                    "ltv_fused_concat_head_major_register_cast_blelloch_scan_cuda_op")
+    for variant in ("blelloch", "sequential"):
+        assert hasattr(torch.ops.nanochat_cuda,
+                       f"ltv_look_back_fused_concat_head_major_register_cast_{variant}_scan_cuda_op")
     assert hasattr(torch.ops.nanochat_amd, "qkv_filter")
     assert hasattr(torch.ops.nanochat_amd, "qkv_filter_backward")
 

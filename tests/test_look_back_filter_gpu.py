@@ -1,0 +1,152 @@
+"""GPU parity of the look-back filter modules (projection + chunked scan) and
+of the KV-cache path, against the oracle.
+
+* bf16 through this package's ops takes the fused path (MFMA projection into
+  the head-major layout, look-back scan, fused backward): q, k, v and every
+  gradient against the oracle composition, tolerance 2e-2;
+* fp32 runs the reference dataflow (fused_linear_transpose, then the op on the
+  transposed view): tolerance 1e-4;
+* through ``LtvLookBackQkvComputerModule`` and a ``KVCache`` (the reference's
+  ``advance_kv_cache`` protocol, ``ltv_look_back_qkv_computer_module.py:15-165``)
+  feeding tokens whole, in groups, one at a time (the fused decode kernel) or
+  through a prefilled copy gives the rows of the chunked scan without a cache.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import ltv_oracle as O
+from ltv_test_utils import TOL, assert_close, np_of
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _make(variant, NH, NKVH, D, r, pqk, seed=0):
+    from nanochat_amd.gpt_config import ChunksAndHistory
+    from nanochat_amd.ops.ltv_cuda_ops import (
+        fused_linear_transpose,
+        ltv_cuda_look_back_fused_concat_head_major_register_cast_blelloch_scan as blelloch_op,
+        ltv_cuda_look_back_fused_concat_head_major_register_cast_sequential_scan as seq_op,
+    )
+    from nanochat_amd.ltv_look_back_fused_concat_head_major_register_cast_blelloch_scan_qkv_filter import (
+        LtvLookBackFusedConcatHeadMajorRegisterCastBlellochScanQkvFilter as Blelloch,
+    )
+    from nanochat_amd.ltv_look_back_fused_concat_head_major_register_cast_sequential_scan_qkv_filter import (
+        LtvLookBackFusedConcatHeadMajorRegisterCastSequentialScanQkvFilter as Sequential,
+    )
+    torch.manual_seed(seed)
+    spec = ChunksAndHistory(*pqk)
+    if variant == "blelloch":
+        f = Blelloch(NH, NKVH, D, r, spec, transpose_op=fused_linear_transpose,
+                     look_back_op=blelloch_op)
+    else:
+        f = Sequential(NH, NKVH, D, r, spec, sequential_look_back_op=seq_op)
+    C = NH * D
+    with torch.no_grad():
+        f.c.weight.normal_(0.0, C ** -0.5)
+        f.logit_bias.uniform_(-0.5, 0.5)
+        f.init_param.uniform_(-0.5, 0.5)
+    return f.to(DEV)
+
+
+def _oracle(f, x_np, gq, gk, gv, pqk, io):
+    """Projection (reference fused_linear_transpose) then the look-back scan,
+    forward and backward; q/k/v and their grads as (B, T, H, D)."""
+    NH, NKVH, Da, r = f.n_head, f.n_kv_head, f.num_alpha_groups, f.r
+    B = x_np.shape[0]
+    w = f.c.weight.detach().float().cpu().numpy()
+    if io == "bf16":
+        w = O.bf16_round(w)
+    ini = np.broadcast_to(f.init_param.detach().float().cpu().numpy(),
+                          (B,) + tuple(f.init_param.shape))
+    ini = O.round_io(np.ascontiguousarray(ini), io)
+    bias = f.logit_bias.detach().float().cpu().numpy()
+    comb = np.ascontiguousarray(O.linear_transpose_forward(x_np, w, io).transpose(0, 2, 1))
+    outs = O.look_back_forward(comb, ini, bias, NH, NKVH, Da, r, *pqk, True, io)
+    t = lambda a: np.ascontiguousarray(np.asarray(a).transpose(0, 2, 1, 3))  # noqa: E731
+    gc, gi, gb = O.look_back_backward(comb, ini, bias, t(gq), t(gk), t(gv), NH, NKVH, Da, r,
+                                      *pqk, True, io)
+    gx, gw = O.linear_transpose_backward(x_np, w, gc.transpose(0, 2, 1), io)
+    return tuple(t(o) for o in outs), gx, gw, gi.sum(axis=0), gb
+
+
+@pytest.mark.parametrize("variant", ["blelloch", "sequential"])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "f32"])
+@pytest.mark.parametrize("pqk", [(16, 16, 9), (64, 60, 5), (5, 2, 6)], ids=str)
+def test_look_back_filter_matches_oracle(variant, dtype, pqk):
+    if variant == "sequential" and dtype == torch.float32:
+        pytest.skip("the sequential filter's nn.Linear runs the fp32 projection in torch; "
+                    "covered by the reference-layout op tests")
+    io = "bf16" if dtype == torch.bfloat16 else "f32"
+    NH, NKVH, D, r = 2, 1, 128, 128
+    f = _make(variant, NH, NKVH, D, r, pqk)
+    B, T, C = 2, 133, NH * D
+    g = torch.Generator().manual_seed(1)
+    x = torch.randn(B, T, C, generator=g).to(dtype)
+    gq = torch.randn(B, T, NH, D, generator=g).to(dtype)
+    gk = torch.randn(B, T, NKVH, D, generator=g).to(dtype)
+    gv = torch.randn(B, T, NKVH, D, generator=g).to(dtype)
+    xd = x.to(DEV).requires_grad_(True)
+    inits = f.init_param.unsqueeze(0).expand(B, -1, -1)
+    q, k, v = f(xd, inits, full_recurrence=False)
+    assert q.shape == (B, T, NH, D) and q.dtype == dtype
+    torch.autograd.backward([q, k, v], [gq.to(DEV), gk.to(DEV), gv.to(DEV)])
+    (eq, ek, ev), egx, egw, egi, egb = _oracle(f, x.float().numpy(), gq.float().numpy(),
+                                              gk.float().numpy(), gv.float().numpy(), pqk, io)
+    tol = TOL[dtype]
+    case = f"{variant} {io} pqk={pqk}"
+    assert_close(np_of(q), eq, tol, "q " + case)
+    assert_close(np_of(k), ek, tol, "k " + case)
+    assert_close(np_of(v), ev, tol, "v " + case)
+    assert_close(np_of(xd.grad), egx, tol, "grad_x " + case)
+    assert_close(np_of(f.c.weight.grad), egw, tol, "grad_weight " + case)
+    assert_close(np_of(f.init_param.grad), egi, tol, "grad_init_param " + case)
+    assert_close(np_of(f.logit_bias.grad), egb, tol, "grad_logit_bias " + case)
+
+
+def _cache(B, NH, NKVH, D, spec, total):
+    from nanochat_amd.kv_cache import KVCache
+    return KVCache(batch_size=B, num_q_heads=NH, num_kv_heads=NKVH, seq_len=total + 10,
+                   head_dim=D, num_layers=1, layer_specs=[spec])
+
+
+@pytest.mark.parametrize("variant", ["blelloch", "sequential"])
+@pytest.mark.parametrize("pqk", [(16, 16, 9), (5, 2, 6), (0, 4, 3)], ids=str)
+def test_kv_cache_groupings_match_chunked_scan(variant, pqk):
+    from nanochat_amd.gpt_config import ChunksAndHistory
+    from nanochat_amd.ltv_look_back_qkv_computer_module import LtvLookBackQkvComputerModule
+    NH, NKVH, D, r = 2, 1, 128, 128
+    f = _make(variant, NH, NKVH, D, r, pqk, seed=3)
+    m = LtvLookBackQkvComputerModule(0, f)
+    spec = ChunksAndHistory(*pqk)
+    B = 8
+    counts = [7, 1, 1, 16, 3, 1, 1, 1, 9, 2]
+    total = sum(counts)
+    g = torch.Generator().manual_seed(2)
+    x = torch.randn(B, total, NH * D, generator=g).to(torch.bfloat16).to(DEV)
+    with torch.no_grad():
+        chunked = m(x, None)
+        whole = m(x, _cache(B, NH, NKVH, D, spec, total))
+        cache = _cache(B, NH, NKVH, D, spec, total)
+        prev = _cache(B, NH, NKVH, D, spec, total)
+        steps, steps3 = [], []
+        start = 0
+        for n in counts:
+            xs = x[:, start:start + n]
+            start += n
+            steps.append(m(xs, cache))
+            steps3.append(m(xs, prev))
+            fresh = _cache(B, NH, NKVH, D, spec, total)
+            fresh.prefill(prev)
+            prev = fresh
+    tol = TOL[torch.bfloat16]
+    for i, name in enumerate("qkv"):
+        ref = np_of(chunked[i])
+        assert_close(np_of(whole[i]), ref, tol, f"{name} whole")
+        assert_close(np_of(torch.cat([s[i] for s in steps], dim=1)), ref, tol, f"{name} steps")
+        assert_close(np_of(torch.cat([s[i] for s in steps3], dim=1)), ref, tol,
+                     f"{name} prefilled steps")
