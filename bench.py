@@ -1,6 +1,6 @@
 """Benchmark of the LTV combined-QKV filter path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload filter|gpt]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload filter|look_back|gpt]
 
 Workload (the d12 training shape): x bf16
 [32, 1024, 768] ~ N(0, 1); c.weight [2322, 768] fp32 ~ N(0, 1/768) (value rows
@@ -11,6 +11,11 @@ One step = one pass of the hot path through the drop-in filter module:
 forward (bf16 MFMA projection into the head-major layout, gated EWMA scan) and
 backward (reverse scan, projection dX and dW) via autograd.  Inputs are resident
 in HBM before the timed region.  ``value`` = tokens / s = B*T*K / elapsed.
+
+``--workload look_back`` runs the same shapes through the look-back filter
+with the d12 layer spec (P, Q, K) = (16, 16, 9): chunks of 16 steps, each
+restarted from the inits over an 8-step warm-up (the reference's production
+look-back configuration).  ``--workload gpt`` is BASELINE.json configs[3].
 
 Printed as one JSON line, with
   roofline     -- the dominant kernel's algorithmic bytes (or FLOPs) per launch
@@ -66,10 +71,13 @@ def algorithmic_work():
     }
 
 
-def profiled_traffic(span: str):
+LOOK_BACK_PQK = (16, 16, 9)
+
+
+def profiled_traffic(span: str, summary: str = "d12_traffic.json"):
     """HBM bytes per launch of a kernel span, from the committed rocprofv3 FETCH_SIZE /
     WRITE_SIZE summary of this workload (copy-calibrated); None if not profiled."""
-    path = os.path.join(ROOT, "profiles", "d12_traffic.json")
+    path = os.path.join(ROOT, "profiles", summary)
     try:
         with open(path) as fh:
             d = json.load(fh)
@@ -78,8 +86,9 @@ def profiled_traffic(span: str):
         return None, None
 
 
-def cpu_baseline(seconds_target: float = 10.0):
-    """Time the oracle's forward+backward on a sample of the workload."""
+def cpu_baseline(seconds_target: float = 10.0, pqk=None):
+    """Time the oracle's forward+backward on a sample of the workload (with
+    ``pqk``, the look-back scan in place of the full recurrence)."""
     import numpy as np
     from threadpoolctl import threadpool_limits
 
@@ -98,10 +107,20 @@ def cpu_baseline(seconds_target: float = 10.0):
     dv = rng.standard_normal((Bs, T, NKVH, D), dtype=np.float32)
     reps = 0
     t0 = time.perf_counter()
+    t_ = lambda a: np.ascontiguousarray(a.transpose(0, 2, 1, 3))  # noqa: E731
     with threadpool_limits(limits=cores):
         while True:
-            q, k, v, comb, saved = O.filter_forward(x, w, ini, bias, NH, NKVH, DA, R, "f32")
-            O.filter_backward(x, w, ini, bias, comb, saved, dq, dk, dv, NH, NKVH, DA, R, "f32")
+            if pqk is None:
+                q, k, v, comb, saved = O.filter_forward(x, w, ini, bias, NH, NKVH, DA, R, "f32")
+                O.filter_backward(x, w, ini, bias, comb, saved, dq, dk, dv, NH, NKVH, DA, R,
+                                  "f32")
+            else:
+                comb = np.ascontiguousarray(
+                    O.linear_transpose_forward(x, w, "f32").transpose(0, 2, 1))
+                O.look_back_forward(comb, ini, bias, NH, NKVH, DA, R, *pqk, True, "f32")
+                gc, _, _ = O.look_back_backward(comb, ini, bias, t_(dq), t_(dk), t_(dv), NH,
+                                                NKVH, DA, R, *pqk, True, "f32")
+                O.linear_transpose_backward(x, w, gc.transpose(0, 2, 1), "f32")
             reps += 1
             el = time.perf_counter() - t0
             if el >= seconds_target:
@@ -112,7 +131,8 @@ def cpu_baseline(seconds_target: float = 10.0):
         "cores": cores,
         "kind": "port",
         "sample": f"{reps} x fwd+bwd of {Bs} sequence(s) of the workload "
-                  f"(T={T}, C={C}, F={F}), fp32 numpy, {el:.1f} s",
+                  f"(T={T}, C={C}, F={F}{'' if pqk is None else f', look-back {pqk}'}), "
+                  f"fp32 numpy, {el:.1f} s",
     }
 
 
@@ -123,8 +143,10 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--workload", choices=("filter", "gpt"), default="filter",
+    ap.add_argument("--workload", choices=("filter", "look_back", "gpt"), default="filter",
                     help="filter: BASELINE.json configs[2] (the default, the metric's workload); "
+                         "look_back: the same shapes through the look-back filter with the d12 "
+                         "layer spec (16, 16, 9); "
                          "gpt: configs[3], one training step of the 12-layer d12 GPT with the "
                          "filter in every layer (tokens/s and the filter's share of the step)")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -143,14 +165,28 @@ def main():
 
     import torch
     from nanochat_amd import _native as N
-    from nanochat_amd.ltv.ltv_filter import LtvInitValues
-    from nanochat_amd.ltv_cuda_fused_concat_head_major_register_cast_blelloch_scan_qkv_filter import (
-        LtvCudaFusedConcatHeadMajorRegisterCastBlellochScanQkvFilter as Filter,
-    )
+
+    look_back = args.workload == "look_back"
+    if look_back:
+        from nanochat_amd.gpt_config import ChunksAndHistory
+        from nanochat_amd.ltv_look_back_fused_concat_head_major_register_cast_blelloch_scan_qkv_filter import (
+            LtvLookBackFusedConcatHeadMajorRegisterCastBlellochScanQkvFilter as LookBackFilter,
+        )
+        from nanochat_amd.ops.ltv_cuda_ops import (
+            fused_linear_transpose,
+            ltv_cuda_look_back_fused_concat_head_major_register_cast_blelloch_scan as look_back_op,
+        )
+        f = LookBackFilter(NH, NKVH, D, R, ChunksAndHistory(*LOOK_BACK_PQK),
+                           transpose_op=fused_linear_transpose, look_back_op=look_back_op)
+    else:
+        from nanochat_amd.ltv_cuda_fused_concat_head_major_register_cast_blelloch_scan_qkv_filter import (
+            LtvCudaFusedConcatHeadMajorRegisterCastBlellochScanQkvFilter as Filter,
+        )
+        from nanochat_amd.ltv.ltv_filter import LtvInitValues
+        f = Filter(NH, NKVH, D, R)
 
     dev = torch.device("cuda:0")
     torch.manual_seed(0)
-    f = Filter(NH, NKVH, D, R)
     with torch.no_grad():
         f.c.weight.normal_(0.0, C ** -0.5)
         f.logit_bias.zero_()
@@ -161,12 +197,20 @@ def main():
     dq = torch.randn(B, T, NH, D, generator=g, device=dev).to(torch.bfloat16)
     dk = torch.randn(B, T, NKVH, D, generator=g, device=dev).to(torch.bfloat16)
     dv = torch.randn(B, T, NKVH, D, generator=g, device=dev).to(torch.bfloat16)
-    none = LtvInitValues()
+    if look_back:
+        def forward():
+            inits = f.init_param.unsqueeze(0).expand(B, -1, -1)
+            return f(x, inits, full_recurrence=False)
+    else:
+        none = LtvInitValues()
+
+        def forward():
+            return f(x, none)
 
     def step():
         f.zero_grad(set_to_none=True)
         x.grad = None
-        q, k, v = f(x, none)
+        q, k, v = forward()
         torch.autograd.backward([q, k, v], [dq, dk, dv])
 
     for _ in range(args.warmup):
@@ -203,7 +247,8 @@ def main():
                          "frac": round(ach / peak, 4), "work_per_launch": amount}
     dominant = max(kernels, key=lambda k: kernels[k]["avg_us"] * kernels[k]["launches"])
     dk_ = kernels[dominant]
-    traffic, traffic_src = profiled_traffic(dominant)
+    traffic, traffic_src = profiled_traffic(
+        dominant, "d12_look_back_traffic.json" if look_back else "d12_traffic.json")
     roofline = {"kernel": dominant, "bound": dk_["bound"], "achieved": dk_["achieved"],
                 "peak": dk_["peak"], "unit": dk_["unit"], "frac": dk_["frac"], "traffic": traffic,
                 "traffic_source": traffic_src}
@@ -212,8 +257,15 @@ def main():
     scan_gbs = scan_bytes / (scan_time * 1e-6) / 1e9 if scan_time else None
 
     ms_per_step = elapsed * 1e3 / args.steps
+    metric = "QKV+EWMA scan fwd+bwd tokens/s and scan HBM GB/s (%peak) at B32 T1024 C768"
+    workload = "configs[2]: d12 fused QKV projection + EWMA scan, fwd+bwd"
+    if look_back:
+        metric = ("look-back (P, Q, K) = (16, 16, 9) QKV+EWMA scan fwd+bwd tokens/s and scan "
+                  "HBM GB/s (%peak) at B32 T1024 C768")
+        workload = ("configs[2] shapes through the look-back filter, layer spec "
+                    "(P, Q, K) = (16, 16, 9), fwd+bwd")
     out = {
-        "metric": "QKV+EWMA scan fwd+bwd tokens/s and scan HBM GB/s (%peak) at B32 T1024 C768",
+        "metric": metric,
         "value": round(B * T * args.steps / elapsed, 1),
         "unit": "tokens/s",
         "n_gpus": 1,
@@ -225,7 +277,7 @@ def main():
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic",
-        "config": {"workload": "configs[2]: d12 fused QKV projection + EWMA scan, fwd+bwd",
+        "config": {"workload": workload,
                    "B": B, "T": T, "C": C, "n_head": NH, "n_kv_head": NKVH, "head_dim": D,
                    "r": R, "F": F, "parallelism": "single GPU"},
         "scan_gbs": round(scan_gbs, 1) if scan_gbs else None,
@@ -233,8 +285,10 @@ def main():
         "roofline": roofline,
         "kernels": kernels,
     }
+    if look_back:
+        out["config"]["look_back_pqk"] = list(LOOK_BACK_PQK)
     if not args.no_cpu_baseline:
-        out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+        out["cpu_baseline"] = cpu_baseline(args.cpu_seconds, LOOK_BACK_PQK if look_back else None)
     print(json.dumps(out), flush=True)
 
 

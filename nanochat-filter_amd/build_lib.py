@@ -20,7 +20,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "nanochat_amd", "libnanochat_filter_amd.so")
 SOURCES = ["ltv_scan_fwd_bf16.hip", "ltv_scan_fwd_f32.hip", "ltv_scan_bwd_bf16.hip",
-           "ltv_scan_bwd_f32.hip", "ltv_scan_abi.hip", "ltv_gemm.hip", "ltv_decode.hip",
+           "ltv_scan_bwd_f32.hip", "ltv_scan_abi.hip", "ltv_scan_lb.hip", "ltv_gemm.hip", "ltv_decode.hip",
            "ltv_abi.cpp"]
 ARCH = "gfx950"
 

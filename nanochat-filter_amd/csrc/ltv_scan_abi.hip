@@ -238,6 +238,17 @@ inline bool chanvec_ok(int r, int D, int V, const HostView4& lg) {
   return r == 1 && D % V == 0 && vec_ok(lg.p, lg.s, 3, V);
 }
 
+// The short-window look-back kernels (one lane per window, ltv_scan_lb.hip)
+// take chunks of at most 64 steps, a warm-up no longer than 16 steps nor than
+// a chunk (so a step is read by at most its own and the next window), and gate
+// groups the reverse pass reduces: r | V inside a lane, or r / V lanes a power
+// of two.
+inline bool lb_short_ok(int V, int r, int Q, int K) {
+  if (Q > 64 || K - 1 > 16 || K - 1 > Q) return false;
+  if (r % V == 0) return is_pow2(r / V);
+  return V % r == 0;
+}
+
 int check_pqk(int P, int Q, int K) {
   LTV_REQUIRE(P >= 0 && Q >= 1 && K >= 1, LTV_ERR_INVALID_ARG,
               "chunking needs P >= 0, Q >= 1, K >= 1 (P=%d Q=%d K=%d)", P, Q, K);
@@ -309,6 +320,14 @@ int scan_forward_impl(int dtype, const HostView4& u, const HostView4& lg, const 
       vec = vec && vec_ok(outp[i], outs[i], 3, V);
     }
   }
+  if (a.nwin > 1 && lb_short_ok(V, r, Q, K)) {
+    a.sh = ScanShape{B, T, NH, NKVH, Da, r, D, H, 1, use_sigmoid};
+    a.lanes = next_pow2((D + V - 1) / V);
+    int gm = GATE_CHAN;
+    if (r % V == 0) gm = GATE_LANE;
+    else if (vec && chanvec_ok(r, D, V, lg)) gm = GATE_CHANVEC;
+    return scan_launch_lb_short_fwd(dtype == LTV_DTYPE_BF16, a, vec, gm, st);
+  }
   return launch_forward(dtype, a, vec, lg, B, T, NH, NKVH, Da, r, use_sigmoid, st);
 }
 
@@ -349,6 +368,15 @@ BwdWorkspace bwd_workspace_plan(int dtype, int B, int T, int NH, int NKVH, int D
   auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
   BwdWorkspace w;
   const int nwin = look_back_nwin(T, P, Q);
+  if (nwin > 1 && lb_short_ok(V, r, Q, K)) {
+    // short windows: dbias partials and per-window grad_inits shares only
+    const size_t rows = (size_t)B * H * nwin;
+    size_t off = al(rows * Da * sizeof(float));
+    w.wdi = off;
+    off += al(rows * D * sizeof(float));
+    w.total = off;
+    return w;
+  }
   if (nwin > 1) {
     const size_t es = dtype == LTV_DTYPE_BF16 ? 2 : 4;
     const size_t rows = (size_t)B * H * nwin;
@@ -455,6 +483,23 @@ int scan_backward_impl(int dtype, const HostView4& u, const HostView4& lg, const
   if (gm == GATE_CHAN && vec && chanvec_ok(r, D, V, lg) && chanvec_ok(r, D, V, dlg))
     gm = GATE_CHANVEC;
   const int nwin = look_back_nwin(T, P, Q);
+  if (nwin > 1 && lb_short_ok(V, r, Q, K)) {
+    // Short look-back windows: one lane per window gathers its steps' whole
+    // gradient (ltv_scan_lb.hip); then the per-window grad_inits shares and
+    // dbias partials are summed.
+    const bool bf16 = dtype == LTV_DTYPE_BF16;
+    a.nchunk = nwin;
+    a.lanes = next_pow2((D + V - 1) / V);
+    a.wdi = reinterpret_cast<float*>(wsb + wp.wdi);
+    int sgm = GATE_CHAN;
+    if (r % V == 0) sgm = GATE_LANE;
+    else if (vec && chanvec_ok(r, D, V, lg) && chanvec_ok(r, D, V, dlg)) sgm = GATE_CHANVEC;
+    rc = scan_launch_lb_short_bwd(bf16, a, vec, sgm, K - 1, st);
+    if (rc) return rc;
+    rc = scan_launch_lb_dinit(bf16, a, st);
+    if (rc) return rc;
+    return scan_launch_dbias_reduce(a.dbias_partial, dbias, B, H, nwin, Da, st);
+  }
   if (nwin > 1) {
     // Look-back windows: recompute each window's warm-up states, run every
     // window's reverse chain, then fold the warm-up contributions into the

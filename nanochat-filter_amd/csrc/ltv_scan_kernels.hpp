@@ -117,6 +117,7 @@ struct FwdArgs {
   // stores the states to wst (B, H, nwin, kw, D) in the I/O dtype, row t - lo.
   void* wst;
   int kw;
+  int lanes;  // short-window kernels: lanes per window (a power of two >= D / V)
 };
 
 struct BwdArgs {
@@ -153,6 +154,7 @@ struct BwdArgs {
   float* wdu;
   float* wdl;
   float* wdi;
+  int lanes;  // short-window kernel: lanes per window (a power of two >= D / V)
 };
 
 // How a lane finds the gate of each of its V channels.
@@ -1140,10 +1142,18 @@ __global__ void __launch_bounds__(256) scan_lb_dinit_kernel(const BwdArgs args) 
   const int d = (int)(idx % S.D);
   const int64_t bh = idx / S.D;
   const int h = (int)(bh % S.H), b = (int)(bh / S.H);
+  // only the first window can be empty (P = 0); the shares are read in batches
+  // so the walk over the windows is not one load latency per window
+  const Window w0 = look_back_window(0, S.T, args.P, args.Q, args.K);
+  const float* wp = args.wdi + bh * nw * S.D + d;
   float acc = 0.0f;
-  for (int c = 0; c < nw; ++c) {
-    const Window wc = look_back_window(c, S.T, args.P, args.Q, args.K);
-    if (wc.hi > wc.lo) acc += args.wdi[(bh * nw + c) * S.D + d];
+  constexpr int KB = 16;
+  for (int c0 = w0.hi > w0.lo ? 0 : 1; c0 < nw; c0 += KB) {
+    float x[KB];
+#pragma unroll
+    for (int k = 0; k < KB; ++k) x[k] = c0 + k < nw ? wp[(int64_t)(c0 + k) * S.D] : 0.0f;
+#pragma unroll
+    for (int k = 0; k < KB; ++k) acc += x[k];
   }
   TIO* dip = reinterpret_cast<TIO*>(const_cast<void*>(args.dinit.p)) +
              (int64_t)b * args.dinit.s[0] + (int64_t)h * args.dinit.s[1] +
@@ -1251,6 +1261,11 @@ int scan_launch_bwd(bool bf16, const BwdArgs& a, ScanCfg cfg, int grid, bool vec
 // Look-back backward: warm-up contributions into du / dlg, then grad_inits.
 int scan_launch_lb_fold(bool bf16, const BwdArgs& a, hipStream_t st);
 int scan_launch_lb_dinit(bool bf16, const BwdArgs& a, hipStream_t st);
+// Short-window look-back kernels (ltv_scan_lb.hip): one lane per (b, h,
+// window, channel vector).  The backward also needs kw_max >= K - 1 (8 or 16).
+int scan_launch_lb_short_fwd(bool bf16, const FwdArgs& a, bool vec, int gm, hipStream_t st);
+int scan_launch_lb_short_bwd(bool bf16, const BwdArgs& a, bool vec, int gm, int kw_max,
+                             hipStream_t st);
 // Backward for gate groups outside the main kernel's reduction patterns.
 int scan_launch_bwd_channel(bool bf16, const BwdArgs& a, float* dalpha_ws, hipStream_t st);
 // dbias[h, j] = sum_b partial[b, h, j]

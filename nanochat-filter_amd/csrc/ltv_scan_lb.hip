@@ -1,0 +1,506 @@
+// Look-back scan for short chunk windows: one lane per (b, head, window,
+// channel vector), walking its window sequentially in registers.
+//
+// With chunks of Q steps and a K - 1 step warm-up (the reference's production
+// layer spec is P = Q = 16, K = 9) a window spans Q + K - 1 steps: far less
+// than a tile of the full-recurrence kernels, whose cross-lane scan levels and
+// per-workgroup setup would then dominate.  Here the lanes of a wavefront are
+// the channel vectors (fastest, so a step's loads are contiguous 16-byte
+// vectors across lanes) of consecutive windows; a window's steps are walked
+// by its lanes one after another, loads issued a batch at a time.
+//
+// Forward: each window runs h_t = h + alpha_t (u_t - h) from the inits over
+// [lo, hi) and stores the outputs of [st, hi).
+//
+// Backward (the exact gradient; requires K - 1 <= Q, so a step is read by its
+// own window and at most the next one's warm-up): the lane of window o owns
+// the gradients of its steps [st, hi) and gathers both contributions:
+//   g1 -- its own chain, g1_t = gy_t + (1 - alpha_{t+1}) g1_{t+1}, g1_hi = 0,
+//         with the states h_{t-1}: the saved outputs inside the window, the
+//         recomputed warm-up end state at t = st;
+//   g2 -- window o + 1's chain on its warm-up [lo', st') = the tail of o:
+//         g2_t = (1 - alpha_{t+1}) g2_{t+1} from g2_st' = G, the value of
+//         o + 1's own chain at its first step (recomputed here from o + 1's
+//         gy and gates), with o + 1's warm-up states recomputed from the inits.
+//   du_t = alpha_t (g1_t + g2_t),  dalpha_t = (u_t - h_{t-1}) g1_t + (u_t - h'_{t-1}) g2_t
+// and window o's own share of grad_inits, prod_{j=lo}^{st} (1 - alpha_j) g1_st,
+// goes to a per-window fp32 slot (summed by scan_lb_dinit_kernel), dbias per
+// (b, h, window) to the partial buffer (summed by dbias_reduce_kernel).  Every
+// output element has exactly one writer: no atomics, no fold pass.
+#include "ltv_scan_kernels.hpp"
+
+namespace ltv {
+namespace {
+
+// Steps whose loads are issued together: per-channel gates load V logits per
+// step, so their batches are shorter (register budget).
+template <int GM>
+constexpr int fwd_batch() {
+  return GM == GATE_LANE ? 8 : 4;
+}
+template <int GM>
+constexpr int bwd_batch() {
+  return GM == GATE_LANE ? 4 : 2;
+}
+
+// Raw gate logits of step t (GATE_LANE: one value; per-channel modes: V values).
+template <typename TIO, int GM>
+struct GateRaw {
+  static constexpr int V = Pack<TIO>::V;
+  static constexpr int NA = GM == GATE_LANE ? 1 : V;
+  float x[NA];
+  __device__ __forceinline__ void load(const TIO* lp_t, const GateIdx<GM, V>& gi, bool ok,
+                                       int nvalid) {
+    if (GM == GATE_CHANVEC) {
+      const uint4 q = ok ? *reinterpret_cast<const uint4*>(lp_t) : make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+      for (int v = 0; v < NA; ++v) x[v] = Pack<TIO>::get(q, v);
+    } else {
+#pragma unroll
+      for (int i = 0; i < NA; ++i)
+        x[i] = ok && (GM == GATE_LANE || i < nvalid) ? Pack<TIO>::load1(lp_t + gi.off[i]) : 0.0f;
+    }
+  }
+  __device__ __forceinline__ void alpha(const GateIdx<GM, V>& gi, bool use_sig,
+                                        float (&a)[NA]) const {
+#pragma unroll
+    for (int i = 0; i < NA; ++i) a[i] = gate_alpha(x[i] + gi.bias[i], use_sig);
+  }
+};
+
+struct LaneMap {
+  int cv, win;
+  int64_t bh;
+};
+
+__device__ __forceinline__ LaneMap lane_map(int lanes, int nwin) {
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  LaneMap m;
+  m.cv = (int)(gid % lanes);
+  const int64_t rest = gid / lanes;
+  m.win = (int)(rest % nwin);
+  m.bh = rest / nwin;
+  return m;
+}
+
+// ---------------------------------------------------------------------------
+// Forward
+// ---------------------------------------------------------------------------
+template <typename TIO, int GM, bool VEC>
+__global__ void __launch_bounds__(256) scan_lb_short_fwd_kernel(const FwdArgs args) {
+  constexpr int V = Pack<TIO>::V;
+  constexpr int NA = GM == GATE_LANE ? 1 : V;
+  constexpr bool GL = GM == GATE_LANE;
+  constexpr int NB = fwd_batch<GM>();
+  const ScanShape& S = args.sh;
+  const LaneMap m = lane_map(args.lanes, args.nwin);
+  if (m.bh >= (int64_t)S.B * S.H) return;
+  const int h = (int)(m.bh % S.H), b = (int)(m.bh / S.H);
+  const int c0 = m.cv * V;
+  const int nvalid = min(V, S.D - c0);
+  if (nvalid <= 0) return;
+  const Window wd = look_back_window(m.win, S.T, args.P, args.Q, args.K);
+
+  int which, hl;
+  head_select(h, S.NH, S.NKVH, which, hl);
+  const HeadView ov = head_view(args.out, which);
+  TIO* outp = reinterpret_cast<TIO*>(ov.p) + (int64_t)b * ov.s[0] + (int64_t)hl * ov.s[1] +
+              (int64_t)c0 * ov.s[3];
+  const TIO* up = reinterpret_cast<const TIO*>(args.u.p) + (int64_t)b * args.u.s[0] +
+                  (int64_t)h * args.u.s[1] + (int64_t)c0 * args.u.s[3];
+  const TIO* lp = reinterpret_cast<const TIO*>(args.lg.p) + (int64_t)b * args.lg.s[0] +
+                  (int64_t)h * args.lg.s[1];
+  if (GM == GATE_CHANVEC) lp += (int64_t)c0;
+  GateIdx<GM, V> gi;
+  gi.init(args.bias + h * S.Da, c0, nvalid, S.D, S.r, args.lg.s[3]);
+  const bool use_sig = S.use_sigmoid != 0;
+  const int64_t ust = args.u.s[2], usc = args.u.s[3], lst = args.lg.s[2];
+
+  float hv[V];
+  {
+    const TIO* ip = reinterpret_cast<const TIO*>(args.init.p) + (int64_t)b * args.init.s[0] +
+                    (int64_t)h * args.init.s[1] + (int64_t)c0 * args.init.s[3];
+    const uint4 q = ld_vec<TIO, VEC>(ip, args.init.s[3], nvalid);
+#pragma unroll
+    for (int v = 0; v < V; ++v) hv[v] = Pack<TIO>::get(q, v);
+  }
+  for (int t0 = wd.lo; t0 < wd.hi; t0 += NB) {
+    uint4 uq[NB];
+    GateRaw<TIO, GM> gr[NB];
+#pragma unroll
+    for (int s = 0; s < NB; ++s) {
+      const int t = t0 + s;
+      const bool ok = t < wd.hi;
+      uq[s] = ok ? ld_vec<TIO, VEC>(up + (int64_t)t * ust, usc, nvalid) : make_uint4(0u, 0u, 0u, 0u);
+      gr[s].load(lp + (int64_t)t * lst, gi, ok, nvalid);
+    }
+#pragma unroll
+    for (int s = 0; s < NB; ++s) {
+      const int t = t0 + s;
+      if (t < wd.hi) {
+        float a[NA];
+        gr[s].alpha(gi, use_sig, a);
+#pragma unroll
+        for (int v = 0; v < V; ++v) hv[v] = fmaf(a[GL ? 0 : v], Pack<TIO>::get(uq[s], v) - hv[v], hv[v]);
+        if (t >= wd.st) st_vec<TIO, VEC>(outp + (int64_t)t * ov.s[2], ov.s[3], nvalid, hv);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Backward
+// ---------------------------------------------------------------------------
+// Sum of x over the aligned groups of `gl` adjacent lanes (gl a power of two).
+__device__ __forceinline__ float group_sum(float x, int gl) {
+  for (int m = 1; m < gl; m <<= 1) x += __shfl_xor(x, m, 64);
+  return x;
+}
+
+template <typename TIO, int GM, bool VEC, int KW>
+__global__ void __launch_bounds__(256) scan_lb_short_bwd_kernel(const BwdArgs args) {
+  constexpr int V = Pack<TIO>::V;
+  constexpr int NA = GM == GATE_LANE ? 1 : V;
+  constexpr bool GL = GM == GATE_LANE;
+  constexpr int NB = bwd_batch<GM>();
+  const ScanShape& S = args.sh;
+  const int nwin = args.nchunk;
+  const LaneMap m = lane_map(args.lanes, nwin);
+  // a window's lanes are consecutive and share bh: whole gate groups leave together
+  if (m.bh >= (int64_t)S.B * S.H) return;
+  const int h = (int)(m.bh % S.H), b = (int)(m.bh / S.H);
+  const int c0 = m.cv * V;
+  const int nvalid = min(V, S.D - c0);
+  const bool active = nvalid > 0;
+  const int gl = GL ? S.r / V : 1;  // lanes per gate group (GATE_LANE)
+
+  const Window wd = look_back_window(m.win, S.T, args.P, args.Q, args.K);
+  const bool has_next = m.win + 1 < nwin;
+  Window wn;
+  if (has_next) {
+    wn = look_back_window(m.win + 1, S.T, args.P, args.Q, args.K);
+  } else {
+    wn.lo = wn.st = wn.hi = wd.hi;
+  }
+
+  int which, hl;
+  head_select(h, S.NH, S.NKVH, which, hl);
+  const HeadView hvw = head_view(args.h, which), gvw = head_view(args.gy, which);
+  const TIO* hp = reinterpret_cast<const TIO*>(hvw.p) + (int64_t)b * hvw.s[0] +
+                  (int64_t)hl * hvw.s[1] + (int64_t)c0 * hvw.s[3];
+  const TIO* gp = reinterpret_cast<const TIO*>(gvw.p) + (int64_t)b * gvw.s[0] +
+                  (int64_t)hl * gvw.s[1] + (int64_t)c0 * gvw.s[3];
+  const TIO* up = reinterpret_cast<const TIO*>(args.u.p) + (int64_t)b * args.u.s[0] +
+                  (int64_t)h * args.u.s[1] + (int64_t)c0 * args.u.s[3];
+  TIO* dup = reinterpret_cast<TIO*>(const_cast<void*>(args.du.p)) + (int64_t)b * args.du.s[0] +
+             (int64_t)h * args.du.s[1] + (int64_t)c0 * args.du.s[3];
+  const TIO* lp = reinterpret_cast<const TIO*>(args.lg.p) + (int64_t)b * args.lg.s[0] +
+                  (int64_t)h * args.lg.s[1];
+  TIO* dlp = reinterpret_cast<TIO*>(const_cast<void*>(args.dlg.p)) + (int64_t)b * args.dlg.s[0] +
+             (int64_t)h * args.dlg.s[1];
+  if (GM == GATE_CHANVEC) lp += (int64_t)c0;
+  GateIdx<GM, V> gi;
+  gi.init(args.bias + h * S.Da, c0, nvalid, S.D, S.r, args.lg.s[3]);
+  const bool use_sig = S.use_sigmoid != 0;
+  const int64_t ust = args.u.s[2], usc = args.u.s[3], lst = args.lg.s[2];
+  const int64_t hst = hvw.s[2], hsc = hvw.s[3], gst = gvw.s[2], gsc = gvw.s[3];
+  const int64_t dust = args.du.s[2], dusc = args.du.s[3];
+  const int64_t dlst = args.dlg.s[2], dlsc = args.dlg.s[3];
+
+  float ini[V];
+  {
+    const TIO* ip = reinterpret_cast<const TIO*>(args.init.p) + (int64_t)b * args.init.s[0] +
+                    (int64_t)h * args.init.s[1] + (int64_t)c0 * args.init.s[3];
+    const uint4 q = active ? ld_vec<TIO, VEC>(ip, args.init.s[3], nvalid) : make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+    for (int v = 0; v < V; ++v) ini[v] = Pack<TIO>::get(q, v);
+  }
+
+  // ---- (A1) own warm-up [lo, st): the state entering st and prod (1 - alpha)
+  float h1[V], prodw[NA];
+#pragma unroll
+  for (int v = 0; v < V; ++v) h1[v] = ini[v];
+#pragma unroll
+  for (int i = 0; i < NA; ++i) prodw[i] = 1.0f;
+  for (int t0 = wd.lo; t0 < wd.st; t0 += NB) {
+    uint4 uq[NB];
+    GateRaw<TIO, GM> gr[NB];
+#pragma unroll
+    for (int s = 0; s < NB; ++s) {
+      const int t = t0 + s;
+      const bool ok = active && t < wd.st;
+      uq[s] = ok ? ld_vec<TIO, VEC>(up + (int64_t)t * ust, usc, nvalid) : make_uint4(0u, 0u, 0u, 0u);
+      gr[s].load(lp + (int64_t)t * lst, gi, ok, nvalid);
+    }
+#pragma unroll
+    for (int s = 0; s < NB; ++s) {
+      if (t0 + s < wd.st) {
+        float a[NA];
+        gr[s].alpha(gi, use_sig, a);
+#pragma unroll
+        for (int v = 0; v < V; ++v) h1[v] = fmaf(a[GL ? 0 : v], Pack<TIO>::get(uq[s], v) - h1[v], h1[v]);
+#pragma unroll
+        for (int i = 0; i < NA; ++i) prodw[i] *= 1.0f - a[i];
+      }
+    }
+  }
+  const uint4 h_st = Pack<TIO>::pack(h1);  // I/O-rounded, as the saved outputs
+
+  // ---- (A2) the next window's warm-up states: HN[s] enters step wn.lo + s
+  const int nt = wn.st - wn.lo;  // tail steps of this window read by the next (<= KW)
+  uint4 HN[KW];
+  {
+    float hn[V];
+#pragma unroll
+    for (int v = 0; v < V; ++v) hn[v] = ini[v];
+    uint4 uq[KW];
+    GateRaw<TIO, GM> gr[KW];
+#pragma unroll
+    for (int s = 0; s < KW; ++s) {
+      const int t = wn.lo + s;
+      const bool ok = active && s < nt;
+      uq[s] = ok ? ld_vec<TIO, VEC>(up + (int64_t)t * ust, usc, nvalid) : make_uint4(0u, 0u, 0u, 0u);
+      gr[s].load(lp + (int64_t)t * lst, gi, ok, nvalid);
+    }
+#pragma unroll
+    for (int s = 0; s < KW; ++s) {
+      HN[s] = Pack<TIO>::pack(hn);
+      if (s < nt) {
+        float a[NA];
+        gr[s].alpha(gi, use_sig, a);
+#pragma unroll
+        for (int v = 0; v < V; ++v) hn[v] = fmaf(a[GL ? 0 : v], Pack<TIO>::get(uq[s], v) - hn[v], hn[v]);
+      }
+    }
+  }
+
+  // ---- (G) the next window's own chain at its first step, and 1 - alpha there
+  float G[V], a_hi[NA];
+#pragma unroll
+  for (int v = 0; v < V; ++v) G[v] = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NA; ++i) a_hi[i] = 0.0f;
+  for (int tb = wn.hi; tb > wn.st; tb -= NB) {
+    uint4 gq[NB];
+    GateRaw<TIO, GM> gr[NB];
+#pragma unroll
+    for (int k = 0; k < NB; ++k) {
+      const int t = tb - 1 - k;
+      const bool ok = active && t >= wn.st;
+      gq[k] = ok ? ld_vec<TIO, VEC>(gp + (int64_t)t * gst, gsc, nvalid) : make_uint4(0u, 0u, 0u, 0u);
+      gr[k].load(lp + (int64_t)t * lst, gi, ok, nvalid);
+    }
+#pragma unroll
+    for (int k = 0; k < NB; ++k) {
+      if (tb - 1 - k >= wn.st) {
+        // a_hi holds 1 - alpha_{t+1} (0 past the window's last step)
+#pragma unroll
+        for (int v = 0; v < V; ++v) G[v] = fmaf(a_hi[GL ? 0 : v], G[v], Pack<TIO>::get(gq[k], v));
+        float a[NA];
+        gr[k].alpha(gi, use_sig, a);
+#pragma unroll
+        for (int i = 0; i < NA; ++i) a_hi[i] = 1.0f - a[i];
+      }
+    }
+  }
+
+  // ---- (B) own steps in reverse: g1 (own chain) and g2 (next window's warm-up)
+  float g1[V], g2[V], an[NA];
+#pragma unroll
+  for (int v = 0; v < V; ++v) {
+    g1[v] = 0.0f;
+    g2[v] = G[v];
+  }
+#pragma unroll
+  for (int i = 0; i < NA; ++i) an[i] = a_hi[i];
+  float dacc[GL ? 1 : V];
+#pragma unroll
+  for (int k = 0; k < (GL ? 1 : V); ++k) dacc[k] = 0.0f;
+
+  // one reverse step at t; with_g2: t lies in the next window's warm-up, hn its state
+  auto step = [&](int t, const uint4& gq, const uint4& uq, const uint4& hq, const GateRaw<TIO, GM>& gr,
+                  bool with_g2, const uint4& hn) {
+    float a[NA];
+    gr.alpha(gi, use_sig, a);
+    float duv[V], dav[V];
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      const int ia = GL ? 0 : v;
+      g1[v] = fmaf(an[ia], g1[v], Pack<TIO>::get(gq, v));
+      g2[v] = with_g2 ? an[ia] * g2[v] : 0.0f;
+      const float u = Pack<TIO>::get(uq, v);
+      duv[v] = a[ia] * (g1[v] + g2[v]);
+      dav[v] = (u - Pack<TIO>::get(hq, v)) * g1[v];
+      if (with_g2) dav[v] = fmaf(u - Pack<TIO>::get(hn, v), g2[v], dav[v]);
+    }
+#pragma unroll
+    for (int i = 0; i < NA; ++i) an[i] = 1.0f - a[i];
+    if (active) st_vec<TIO, VEC>(dup + (int64_t)t * dust, dusc, nvalid, duv);
+    if (GL) {
+      float p = 0.0f;
+#pragma unroll
+      for (int v = 0; v < V; ++v) p += v < nvalid ? dav[v] : 0.0f;
+      p = group_sum(p, gl);
+      const float d = use_sig ? p * (a[0] * (1.0f - a[0])) : p;
+      if (active && (m.cv % gl) == 0) {
+        dacc[0] += d;
+        Pack<TIO>::store1(dlp + (int64_t)t * dlst + (int64_t)(c0 / S.r) * dlsc, d);
+      }
+    } else {
+      // whole groups of r channels inside the lane (r | V)
+#pragma unroll
+      for (int mm = 1; mm < V; mm <<= 1) {
+        if (mm < S.r) {
+          float tsum[V];
+#pragma unroll
+          for (int v = 0; v < V; ++v) tsum[v] = dav[v] + dav[v ^ mm];
+#pragma unroll
+          for (int v = 0; v < V; ++v) dav[v] = tsum[v];
+        }
+      }
+      float dl[V];
+#pragma unroll
+      for (int v = 0; v < V; ++v) dl[v] = use_sig ? dav[v] * (a[v] * (1.0f - a[v])) : dav[v];
+      if (active) {
+        if (GM == GATE_CHANVEC) {
+          st_vec<TIO, true>(dlp + (int64_t)t * dlst + c0, 1, V, dl);
+#pragma unroll
+          for (int v = 0; v < V; ++v) dacc[v] += dl[v];
+        } else {
+#pragma unroll
+          for (int v = 0; v < V; ++v) {
+            if ((v & (S.r - 1)) == 0 && v < nvalid) {
+              dacc[v] += dl[v];
+              Pack<TIO>::store1(dlp + (int64_t)t * dlst + (int64_t)((c0 + v) / S.r) * dlsc, dl[v]);
+            }
+          }
+        }
+      }
+    }
+  };
+  // state entering step t of this window: the saved output of t - 1, or at st
+  // the recomputed warm-up end state
+  auto load_h = [&](int t, bool ok) -> uint4 {
+    if (!ok) return make_uint4(0u, 0u, 0u, 0u);
+    return t == wd.st ? h_st : ld_vec<TIO, VEC>(hp + (int64_t)(t - 1) * hst, hsc, nvalid);
+  };
+
+  // (B1) the tail [wn.lo, wn.st), read by the next window: compile-time rows of
+  // HN, in batches of NB steps whose loads are issued together
+#pragma unroll
+  for (int s0 = KW - NB; s0 >= 0; s0 -= NB) {
+    uint4 gq[NB], uq[NB], hq[NB];
+    GateRaw<TIO, GM> gr[NB];
+#pragma unroll
+    for (int k = NB - 1; k >= 0; --k) {
+      const int t = wn.lo + s0 + k;
+      const bool ok = active && s0 + k < nt;
+      gq[k] = ok ? ld_vec<TIO, VEC>(gp + (int64_t)t * gst, gsc, nvalid) : make_uint4(0u, 0u, 0u, 0u);
+      uq[k] = ok ? ld_vec<TIO, VEC>(up + (int64_t)t * ust, usc, nvalid) : make_uint4(0u, 0u, 0u, 0u);
+      hq[k] = load_h(t, ok);
+      gr[k].load(lp + (int64_t)t * lst, gi, ok, nvalid);
+    }
+#pragma unroll
+    for (int k = NB - 1; k >= 0; --k)
+      if (s0 + k < nt) step(wn.lo + s0 + k, gq[k], uq[k], hq[k], gr[k], true, HN[s0 + k]);
+  }
+  // (B2) the rest [st, wn.lo), batches in reverse
+  const int b2_hi = has_next ? wn.lo : wd.hi;
+  for (int tb = b2_hi; tb > wd.st; tb -= NB) {
+    uint4 gq[NB], uq[NB], hq[NB];
+    GateRaw<TIO, GM> gr[NB];
+#pragma unroll
+    for (int k = 0; k < NB; ++k) {
+      const int t = tb - 1 - k;
+      const bool ok = active && t >= wd.st;
+      gq[k] = ok ? ld_vec<TIO, VEC>(gp + (int64_t)t * gst, gsc, nvalid) : make_uint4(0u, 0u, 0u, 0u);
+      uq[k] = ok ? ld_vec<TIO, VEC>(up + (int64_t)t * ust, usc, nvalid) : make_uint4(0u, 0u, 0u, 0u);
+      hq[k] = load_h(t, ok);
+      gr[k].load(lp + (int64_t)t * lst, gi, ok, nvalid);
+    }
+#pragma unroll
+    for (int k = 0; k < NB; ++k) {
+      const int t = tb - 1 - k;
+      if (t >= wd.st) step(t, gq[k], uq[k], hq[k], gr[k], false, h_st);
+    }
+  }
+
+  // ---- this window's share of grad_inits: prod_{j=lo}^{st} (1 - alpha_j) g1_st
+  // (an = 1 - alpha_st after the last step; an empty window leaves g1 = 0)
+  if (active) {
+    float di[V];
+#pragma unroll
+    for (int v = 0; v < V; ++v) di[v] = prodw[GL ? 0 : v] * an[GL ? 0 : v] * g1[v];
+    st_f32<VEC, V>(args.wdi + ((int64_t)m.bh * nwin + m.win) * S.D + c0, nvalid, di);
+  }
+  // ---- dbias partial of (b, h, window)
+  float* pp = args.dbias_partial + ((int64_t)m.bh * nwin + m.win) * S.Da;
+  if (GL) {
+    if (active && (m.cv % gl) == 0) pp[c0 / S.r] = dacc[0];
+  } else if (active) {
+#pragma unroll
+    for (int v = 0; v < V; ++v)
+      if ((GM == GATE_CHANVEC || (v & (S.r - 1)) == 0) && v < nvalid) pp[(c0 + v) / S.r] = dacc[v];
+  }
+}
+
+template <typename TIO, int GM, bool VEC>
+void launch_fwd(const FwdArgs& a, int grid, hipStream_t st) {
+  hipLaunchKernelGGL((scan_lb_short_fwd_kernel<TIO, GM, VEC>), dim3(grid), dim3(256), 0, st, a);
+}
+
+template <typename TIO, int GM, bool VEC>
+void launch_bwd(const BwdArgs& a, int grid, int kw_max, hipStream_t st) {
+  if (kw_max <= 8)
+    hipLaunchKernelGGL((scan_lb_short_bwd_kernel<TIO, GM, VEC, 8>), dim3(grid), dim3(256), 0, st, a);
+  else
+    hipLaunchKernelGGL((scan_lb_short_bwd_kernel<TIO, GM, VEC, 16>), dim3(grid), dim3(256), 0, st, a);
+}
+
+template <typename TIO>
+int fwd_t(const FwdArgs& a, bool vec, int gm, hipStream_t st) {
+  const int64_t lanes = (int64_t)a.sh.B * a.sh.H * a.nwin * a.lanes;
+  const int64_t grid = (lanes + 255) / 256;
+  LTV_REQUIRE(grid < (1ll << 31), LTV_ERR_UNSUPPORTED, "grid too large");
+  if (vec) {
+    if (gm == GATE_LANE) launch_fwd<TIO, GATE_LANE, true>(a, (int)grid, st);
+    else if (gm == GATE_CHANVEC) launch_fwd<TIO, GATE_CHANVEC, true>(a, (int)grid, st);
+    else launch_fwd<TIO, GATE_CHAN, true>(a, (int)grid, st);
+  } else {
+    if (gm == GATE_LANE) launch_fwd<TIO, GATE_LANE, false>(a, (int)grid, st);
+    else launch_fwd<TIO, GATE_CHAN, false>(a, (int)grid, st);
+  }
+  LTV_LAUNCH_CHECK();
+  return LTV_OK;
+}
+
+template <typename TIO>
+int bwd_t(const BwdArgs& a, bool vec, int gm, int kw_max, hipStream_t st) {
+  const int64_t lanes = (int64_t)a.sh.B * a.sh.H * a.nchunk * a.lanes;
+  const int64_t grid = (lanes + 255) / 256;
+  LTV_REQUIRE(grid < (1ll << 31), LTV_ERR_UNSUPPORTED, "grid too large");
+  LTV_REQUIRE(kw_max <= 16, LTV_ERR_UNSUPPORTED, "warm-up of %d steps too long", kw_max);
+  if (vec) {
+    if (gm == GATE_LANE) launch_bwd<TIO, GATE_LANE, true>(a, (int)grid, kw_max, st);
+    else if (gm == GATE_CHANVEC) launch_bwd<TIO, GATE_CHANVEC, true>(a, (int)grid, kw_max, st);
+    else launch_bwd<TIO, GATE_CHAN, true>(a, (int)grid, kw_max, st);
+  } else {
+    if (gm == GATE_LANE) launch_bwd<TIO, GATE_LANE, false>(a, (int)grid, kw_max, st);
+    else launch_bwd<TIO, GATE_CHAN, false>(a, (int)grid, kw_max, st);
+  }
+  LTV_LAUNCH_CHECK();
+  return LTV_OK;
+}
+
+}  // namespace
+
+int scan_launch_lb_short_fwd(bool bf16, const FwdArgs& a, bool vec, int gm, hipStream_t st) {
+  return bf16 ? fwd_t<bf16_t>(a, vec, gm, st) : fwd_t<float>(a, vec, gm, st);
+}
+
+int scan_launch_lb_short_bwd(bool bf16, const BwdArgs& a, bool vec, int gm, int kw_max,
+                             hipStream_t st) {
+  return bf16 ? bwd_t<bf16_t>(a, vec, gm, kw_max, st) : bwd_t<float>(a, vec, gm, kw_max, st);
+}
+
+}  // namespace ltv
