@@ -61,3 +61,20 @@ for _variant in ("blelloch", "sequential"):
     torch.library.register_fake(f"{_base}_op")(_look_back_op_fake)
     torch.library.register_fake(f"{_base}_forward_kernel")(lambda *args: None)
     torch.library.register_fake(f"{_base}_backward_kernel")(lambda *args: None)
+
+
+# Legacy-layout scan op (reference nanochat/ops/ltv_cuda_meta.py:76-150).
+@torch.library.register_fake("nanochat_cuda::ltv_fused_concat_register_cast_blelloch_scan_cuda_op")
+def _legacy_op_fake(combined, inits, NH, NKVH, da, r, chunk_size, bank_count, use_sigmoid):
+    B, T, _ = combined.shape
+    D = da * r
+    mk = lambda h: combined.new_empty((B, h, T, D))  # noqa: E731
+    return mk(NH), mk(NKVH), mk(NKVH)
+
+
+torch.library.register_fake(
+    "nanochat_cuda::ltv_fused_concat_register_cast_blelloch_scan_cuda_forward_kernel")(
+    lambda *args: None)
+torch.library.register_fake(
+    "nanochat_cuda::ltv_fused_concat_register_cast_blelloch_scan_cuda_backward_kernel")(
+    lambda *args: None)

@@ -8,7 +8,9 @@ the same ``nanochat_cuda`` namespace so callers written against the reference
 ``ltv_cuda_fused_concat_head_major_register_cast_blelloch_scan.py`` and call the
 gfx950 HIP library through its C ABI.
 
-The look-back ops (``:172-241``, wrappers ``:332-410``) are implemented in
+The legacy-layout scan op (``:89-113``) is implemented in
+``ltv_cuda_fused_concat_register_cast_blelloch_scan.py``; the look-back ops
+(``:172-241``, wrappers ``:332-410``) in
 ``ltv_cuda_look_back_fused_concat_head_major_register_cast_{blelloch,sequential}_scan.py``.
 
 The filter module's own fast path uses two further ops in the ``nanochat_amd``
@@ -48,6 +50,34 @@ lib.define(
     "int NH, int NKVH, int da, int r, "
     "int scan_threads_backward, int r_threads_backward, int r_items_backward, "
     "bool use_sigmoid"
+    ") -> ()"
+)
+
+# Legacy projection layout [q | k | v | logits] (bias pre-added), schemas of the
+# reference's ops/ltv_cuda_ops.py:89-113.
+lib.define(
+    "ltv_fused_concat_register_cast_blelloch_scan_cuda_op("
+    "Tensor combined, Tensor inits, "
+    "int NH, int NKVH, int da, int r, int chunk_size, int bank_count, bool use_sigmoid"
+    ") -> (Tensor, Tensor, Tensor)"
+)
+
+lib.define(
+    "ltv_fused_concat_register_cast_blelloch_scan_cuda_forward_kernel("
+    "Tensor combined, Tensor inits, "
+    "Tensor(a!) out_q, Tensor(b!) out_k, Tensor(c!) out_v, "
+    "int T, int NH, int NKVH, int da, int r, int chunk_size, int bank_count, bool use_sigmoid"
+    ") -> ()"
+)
+
+lib.define(
+    "ltv_fused_concat_register_cast_blelloch_scan_cuda_backward_kernel("
+    "Tensor combined, Tensor inits, "
+    "Tensor hq, Tensor hk, Tensor hv, "
+    "Tensor grad_hq, Tensor grad_hk, Tensor grad_hv, "
+    "Tensor(a!) grad_combined, Tensor(b!) grad_inits, "
+    "Tensor(c!) grad_logits, "
+    "int NH, int NKVH, int da, int r, int chunk_size, int bank_count, bool use_sigmoid"
     ") -> ()"
 )
 
@@ -136,6 +166,7 @@ lib.define(
 
 import nanochat_amd.ops.fused_linear_transpose  # noqa: E402,F401  (registers impls)
 import nanochat_amd.ops.ltv_cuda_fused_concat_head_major_register_cast_blelloch_scan  # noqa: E402,F401
+import nanochat_amd.ops.ltv_cuda_fused_concat_register_cast_blelloch_scan  # noqa: E402,F401
 import nanochat_amd.ops.ltv_cuda_look_back_fused_concat_head_major_register_cast_blelloch_scan  # noqa: E402,F401
 import nanochat_amd.ops.ltv_cuda_look_back_fused_concat_head_major_register_cast_sequential_scan  # noqa: E402,F401
 import nanochat_amd.ops.ltv_cuda_meta  # noqa: E402,F401
