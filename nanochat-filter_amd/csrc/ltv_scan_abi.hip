@@ -249,6 +249,33 @@ inline bool lb_short_ok(int V, int r, int Q, int K) {
   return V % r == 0;
 }
 
+// The tile kernels address a view through 32-bit byte offsets from its (b, h)
+// slice at the tile's first step (or the step before): at most
+// kTileRowsMax time steps plus the channel extent.  Every such offset stays
+// below 2^31 when this holds.
+constexpr int64_t kTileRowsMax = 1024 + 2;  // the largest built tile, the step before, one spare
+inline bool tile_offsets_fit(const int64_t* s, int64_t chan_extent, int esize) {
+  const int64_t st = s[2] < 0 ? -s[2] : s[2], sc = s[3] < 0 ? -s[3] : s[3];
+  return (kTileRowsMax * st + chan_extent * sc) * esize + 64 < (1ll << 31);
+}
+
+int check_tile_offsets(const char* what, const int64_t* s, int64_t chan_extent, int esize) {
+  LTV_REQUIRE(tile_offsets_fit(s, chan_extent, esize), LTV_ERR_UNSUPPORTED,
+              "%s: time stride %lld / channel stride %lld too large for the scan's 32-bit tile "
+              "offsets", what, (long long)s[2], (long long)s[3]);
+  return LTV_OK;
+}
+
+// Backward launch shape for a head of cl channel lanes: 4 steps per lane and 4
+// wavefronts, except at 16 vector lanes (D = 128 in bf16, the d12 heads) where
+// 2 wavefronts are measured fastest on MI355X (134 us at d12 against 143 us
+// for 2 steps per lane x 4 wavefronts and 145 us for 2 x 2): a tile spans 32
+// steps either way, and fewer wavefronts shorten the per-tile composition of
+// the wavefront carries while 4 steps per lane amortise the lane scan levels.
+inline ScanCfg bwd_default_cfg(int cl, bool vec) {
+  return vec && cl == 16 ? ScanCfg{16, 4, 2} : ScanCfg{cl, 4, 4};
+}
+
 int check_pqk(int P, int Q, int K) {
   LTV_REQUIRE(P >= 0 && Q >= 1 && K >= 1, LTV_ERR_INVALID_ARG,
               "chunking needs P >= 0, Q >= 1, K >= 1 (P=%d Q=%d K=%d)", P, Q, K);
@@ -310,6 +337,9 @@ int scan_forward_impl(int dtype, const HostView4& u, const HostView4& lg, const 
   a.nwin = look_back_nwin(T, P, Q);
   a.wst = nullptr;
   a.kw = 0;
+  const int E = dtype == LTV_DTYPE_BF16 ? 2 : 4;
+  if ((rc = check_tile_offsets("values", u.s, D, E)) || (rc = check_tile_offsets("logits", lg.s, D, E)))
+    return rc;
   bool vec = (D % V == 0) && vec_ok(u.p, u.s, 3, V) && vec_ok(init.p, init.s, 3, V);
   for (int i = 0; i < 3; ++i) {
     a.out.p[i] = outp[i];
@@ -317,6 +347,7 @@ int scan_forward_impl(int dtype, const HostView4& u, const HostView4& lg, const 
     const int nh = i == 0 ? NH : NKVH;
     if (nh > 0) {
       LTV_REQUIRE(outp[i] != nullptr, LTV_ERR_INVALID_ARG, "null output pointer");
+      if ((rc = check_tile_offsets("outputs", outs[i], D, E))) return rc;
       vec = vec && vec_ok(outp[i], outs[i], 3, V);
     }
   }
@@ -445,6 +476,12 @@ int scan_backward_impl(int dtype, const HostView4& u, const HostView4& lg, const
   a.lg = to_dev(lg);
   a.init = to_dev(init);
   a.bias = bias;
+  const int E = dtype == LTV_DTYPE_BF16 ? 2 : 4;
+  if ((rc = check_tile_offsets("values", u.s, D, E)) || (rc = check_tile_offsets("logits", lg.s, D, E)) ||
+      (rc = check_tile_offsets("grad values", du.s, D, E)) ||
+      (rc = check_tile_offsets("grad logits", dlg.s, D, E)) ||
+      (rc = check_tile_offsets("inits", init.s, D, E)))
+    return rc;
   bool vec = (D % V == 0) && vec_ok(u.p, u.s, 3, V) && vec_ok(init.p, init.s, 3, V) &&
              vec_ok(du.p, du.s, 3, V) && vec_ok(dinit.p, dinit.s, 3, V);
   for (int i = 0; i < 3; ++i) {
@@ -457,6 +494,9 @@ int scan_backward_impl(int dtype, const HostView4& u, const HostView4& lg, const
     const int nh = i == 0 ? NH : NKVH;
     if (nh > 0) {
       LTV_REQUIRE(hp[i] && gp[i], LTV_ERR_INVALID_ARG, "null saved output or gradient pointer");
+      if ((rc = check_tile_offsets("saved outputs", hs[i], D, E)) ||
+          (rc = check_tile_offsets("output gradients", gs[i], D, E)))
+        return rc;
       vec = vec && vec_ok(hp[i], hs[i], 3, V) && vec_ok(gp[i], gs[i], 3, V);
     }
   }
@@ -537,8 +577,12 @@ int scan_backward_impl(int dtype, const HostView4& u, const HostView4& lg, const
       rc = launch_forward(dtype, f, fvec, lg, B, T, NH, NKVH, Da, r, use_sigmoid, st);
       if (rc) return rc;
     }
-    const int cl = next_pow2((D + V - 1) / V);
-    const ScanCfg cfg{cl, vec && cl == 16 ? 2 : 4, 4};
+    ScanCfg cfg = bwd_default_cfg(next_pow2((D + V - 1) / V), vec);
+    const ScanTuning& tu = tuning();
+    if (vec && tu.bwd_l > 0) {
+      cfg.L = tu.bwd_l;
+      cfg.NW = tu.bwd_nw;
+    }
     rc = scan_launch_bwd(bf16, a, cfg, (int)grid, vec, gm, true, st);
     if (rc) return rc;
     if (a.kw > 0) {
@@ -550,11 +594,8 @@ int scan_backward_impl(int dtype, const HostView4& u, const HostView4& lg, const
     return scan_launch_dbias_reduce(a.dbias_partial, dbias, B, H, nwin, Da, st);
   }
   if (gm >= 0) {
-    // whole head per workgroup, 4 wavefronts.  Each lane keeps the next tile's
-    // loads in flight; at 16 channel lanes (D = 128 in bf16) 2 steps per lane
-    // keep 3 wavefronts per SIMD resident (measured fastest at d12), else 4.
-    const int cl = next_pow2((D + V - 1) / V);
-    ScanCfg cfg{cl, vec && cl == 16 ? 2 : 4, 4};
+    // whole head per workgroup
+    ScanCfg cfg = bwd_default_cfg(next_pow2((D + V - 1) / V), vec);
     const ScanTuning& tu = tuning();
     if (vec && tu.bwd_l > 0) {
       cfg.L = tu.bwd_l;

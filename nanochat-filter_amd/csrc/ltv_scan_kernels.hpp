@@ -38,6 +38,8 @@
 
 #pragma once
 
+#include <type_traits>
+
 #include "ltv_device.hpp"
 #include "ltv_abi_internal.hpp"
 
@@ -263,6 +265,106 @@ __device__ __forceinline__ void st_f32(float* p, int nvalid, const float (&x)[V]
   }
 }
 
+// ---------------------------------------------------------------------------
+// Buffer accesses of the tile kernels.  A buffer resource holds a wave-uniform
+// base address (a view's (b, h) slice at the current tile's first step); each
+// lane adds a 32-bit byte offset.  A lane that must not touch memory passes
+// kOob: the range check turns its load into 0 and drops its store, so masked
+// accesses need no branch.  Without branches the compiler counts the vector
+// memory operations in flight exactly and waits only for those a use needs; a
+// load or store under a data-dependent branch makes it drain the queue
+// (vmcnt(0)) at the next wait, which puts the prefetch of the next tile
+// behind the stores of the current one.  The host keeps every in-tile offset
+// below 2^31 (scan_offsets_fit in the launcher).
+// ---------------------------------------------------------------------------
+using Rsrc = __amdgpu_buffer_rsrc_t;
+constexpr uint32_t kOob = 0x80000000u;
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ Rsrc make_rsrc(const void* base) {
+  // num_records 2^31 - 1 bytes, raw (stride 0) addressing, 32-bit data format
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, 0x7fffffff,
+                                           0x00020000);
+}
+__device__ __forceinline__ uint4 bld128(Rsrc r, uint32_t off) {
+  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+__device__ __forceinline__ void bst128(Rsrc r, uint32_t off, uint4 x) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4_t, x), r, off, 0, 0);
+}
+__device__ __forceinline__ void bst_b32(Rsrc r, uint32_t off, float x) {
+  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(x), r, off, 0, 0);
+}
+
+// Hides x's value from the optimiser: offsets derived from it are formed where
+// they are used instead of being hoisted out of the tile loop, where one live
+// register per (step, channel) offset would cost more than the adds.
+__device__ __forceinline__ uint32_t opaque(uint32_t x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
+
+// One element as raw bits (bf16: the 16 bits; fp32: the word) and its store.
+template <typename TIO>
+__device__ __forceinline__ uint32_t bld1(Rsrc r, uint32_t off) {
+  if constexpr (sizeof(TIO) == 2)
+    return __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
+  else
+    return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+}
+template <typename TIO>
+__device__ __forceinline__ void bst1(Rsrc r, uint32_t off, float x) {
+  if constexpr (sizeof(TIO) == 2)
+    __builtin_amdgcn_raw_buffer_store_b16((unsigned short)(cvt_pk_bf16(x, 0.0f) & 0xffffu), r,
+                                          off, 0, 0);
+  else
+    bst_b32(r, off, x);
+}
+
+// V channels at byte offset off, scb bytes apart; channels >= nvalid and
+// lanes with ok == false read 0.
+template <typename TIO, bool VEC>
+__device__ __forceinline__ uint4 bld_vec(Rsrc r, uint32_t off, uint32_t scb, int nvalid, bool ok) {
+  if (VEC) return bld128(r, ok ? off : kOob);
+  constexpr int V = Pack<TIO>::V;
+  off = opaque(off);
+  uint32_t w[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int v = 0; v < V; ++v)
+    Pack<TIO>::put_raw(w, v, bld1<TIO>(r, ok && v < nvalid ? off + v * scb : kOob));
+  return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+template <typename TIO, bool VEC>
+__device__ __forceinline__ void bst_vec(Rsrc r, uint32_t off, uint32_t scb, int nvalid, bool ok,
+                                        const float (&x)[Pack<TIO>::V]) {
+  if (VEC) {
+    bst128(r, ok ? off : kOob, Pack<TIO>::pack(x));
+  } else {
+    off = opaque(off);
+#pragma unroll
+    for (int v = 0; v < Pack<TIO>::V; ++v)
+      bst1<TIO>(r, ok && v < nvalid ? off + v * scb : kOob, x[v]);
+  }
+}
+
+// V fp32 values at off, off + 4, ... (16-byte stores when VEC: off is then
+// 16-byte aligned and all V values are valid).
+template <bool VEC, int V>
+__device__ __forceinline__ void bst_f32(Rsrc r, uint32_t off, int nvalid, bool ok,
+                                        const float (&x)[V]) {
+  if (VEC) {
+#pragma unroll
+    for (int q = 0; q < V / 4; ++q)
+      bst128(r, ok ? off + 16 * q : kOob,
+             make_uint4(__float_as_uint(x[4 * q]), __float_as_uint(x[4 * q + 1]),
+                        __float_as_uint(x[4 * q + 2]), __float_as_uint(x[4 * q + 3])));
+  } else {
+#pragma unroll
+    for (int v = 0; v < V; ++v) bst_b32(r, ok && v < nvalid ? off + 4 * v : kOob, x[v]);
+  }
+}
+
 // Makes the compiler treat the packed vectors as rewritten, so it widens them
 // again where they are next used instead of keeping L x V fp32 copies alive
 // across the scan levels (widening is one shift or mask per element).
@@ -358,31 +460,33 @@ struct GateIdx {
 };
 
 // Raw logits of NS steps as loaded from memory: GATE_LANE keeps one value per
-// step, the per-channel modes one packed 16-byte vector per step (the V
-// channels' logits, gathered for GATE_CHAN).
+// step (raw bits), the per-channel modes one packed 16-byte vector per step
+// (the V channels' logits, gathered for GATE_CHAN).  Step s lies at byte
+// offset off0 + s lstb of the buffer (off0 includes the lane's channel offset
+// for GATE_CHANVEC); steps at or beyond T and inactive lanes read 0.
 template <typename TIO, int GM, int NS>
 struct LogitRaw {
   static constexpr int V = Pack<TIO>::V;
-  float one[GM == GATE_LANE ? NS : 1];
+  uint32_t one[GM == GATE_LANE ? NS : 1];
   uint4 vec[GM == GATE_LANE ? 1 : NS];
 
-  __device__ __forceinline__ void load(const TIO* lp_t0, int64_t lst, const GateIdx<GM, V>& gi,
-                                       int t0, int T, bool active, int nvalid) {
+  __device__ __forceinline__ void load(Rsrc rs, uint32_t off0, uint32_t lstb,
+                                           const GateIdx<GM, V>& gi, int t0, int T, bool active,
+                                           int nvalid) {
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
       const bool ok = active && (t0 + s) < T;
-      const TIO* p = lp_t0 + (int64_t)s * lst;
+      const uint32_t o = GM == GATE_CHAN ? opaque(off0 + s * lstb) : off0 + s * lstb;
       if (GM == GATE_LANE) {
-        one[s] = ok ? Pack<TIO>::load1(p + gi.off[0]) : 0.0f;
+        one[s] = bld1<TIO>(rs, ok ? o + (uint32_t)(gi.off[0] * sizeof(TIO)) : kOob);
       } else if (GM == GATE_CHANVEC) {
-        vec[s] = ok ? *reinterpret_cast<const uint4*>(p) : make_uint4(0u, 0u, 0u, 0u);
+        vec[s] = bld128(rs, ok ? o : kOob);
       } else {
         uint32_t w[4] = {0u, 0u, 0u, 0u};
-        if (ok) {
 #pragma unroll
-          for (int v = 0; v < V; ++v)
-            if (v < nvalid) Pack<TIO>::put_raw(w, v, Pack<TIO>::raw(p + gi.off[v]));
-        }
+        for (int v = 0; v < V; ++v)
+          Pack<TIO>::put_raw(
+              w, v, bld1<TIO>(rs, ok && v < nvalid ? o + (uint32_t)(gi.off[v] * sizeof(TIO)) : kOob));
         vec[s] = make_uint4(w[0], w[1], w[2], w[3]);
       }
     }
@@ -397,7 +501,9 @@ struct LogitRaw {
       const bool ok = active && (t0 + s) < T;
 #pragma unroll
       for (int i = 0; i < NA; ++i) {
-        const float raw = GM == GATE_LANE ? one[s] : Pack<TIO>::get(vec[s], i);
+        const float raw = GM == GATE_LANE
+                              ? __uint_as_float(sizeof(TIO) == 2 ? one[s] << 16 : one[s])
+                              : Pack<TIO>::get(vec[s], i);
         al[s][i] = ok ? gate_alpha(raw + gi.bias[i], use_sig) : 0.0f;
       }
     }
@@ -437,26 +543,25 @@ scan_fwd_kernel(const FwdArgs args) {
   const int nvalid = min(V, S.D - c0);
   const bool active = nvalid > 0;
 
+  constexpr int E = sizeof(TIO);
   int which, hl;
   head_select(h, S.NH, S.NKVH, which, hl);
   const HeadView ov = head_view(args.out, which);
-  int64_t os[4] = {ov.s[0], ov.s[1], ov.s[2], ov.s[3]};
-  TIO* outp = reinterpret_cast<TIO*>(ov.p) + (int64_t)b * os[0] + (int64_t)hl * os[1] +
-              (int64_t)c0 * os[3];
+  // (b, h) slices (wave-uniform byte addresses)
+  char* obh = reinterpret_cast<char*>(ov.p) + ((int64_t)b * ov.s[0] + (int64_t)hl * ov.s[1]) * E;
+  int64_t ost = ov.s[2], osc = ov.s[3];
   if (args.wst != nullptr) {  // warm-up mode: the states of [lo, st), rows t - lo
     t_hi = t_st;
     t_st = t_lo;
-    outp = reinterpret_cast<TIO*>(args.wst) +
-           ((((int64_t)b * S.H + h) * args.nwin + win) * args.kw - t_lo) * S.D + c0;
-    os[2] = S.D;
-    os[3] = 1;
+    obh = reinterpret_cast<char*>(args.wst) +
+          ((((int64_t)b * S.H + h) * args.nwin + win) * args.kw - t_lo) * S.D * E;
+    ost = S.D;
+    osc = 1;
   }
-
-  const TIO* up = reinterpret_cast<const TIO*>(args.u.p) + (int64_t)b * args.u.s[0] +
-                  (int64_t)h * args.u.s[1] + (int64_t)c0 * args.u.s[3];
-  const TIO* lp = reinterpret_cast<const TIO*>(args.lg.p) + (int64_t)b * args.lg.s[0] +
-                  (int64_t)h * args.lg.s[1];
-  if (GM == GATE_CHANVEC) lp += (int64_t)c0;  // r == 1: gate j == channel
+  const char* ubh = reinterpret_cast<const char*>(args.u.p) +
+                    ((int64_t)b * args.u.s[0] + (int64_t)h * args.u.s[1]) * E;
+  const char* lbh = reinterpret_cast<const char*>(args.lg.p) +
+                    ((int64_t)b * args.lg.s[0] + (int64_t)h * args.lg.s[1]) * E;
 
   GateIdx<GM, V> gi;
   gi.init(args.bias + h * S.Da, c0, nvalid, S.D, S.r, args.lg.s[3]);
@@ -476,33 +581,43 @@ scan_fwd_kernel(const FwdArgs args) {
 
   const int ntiles = (t_hi - t_lo + TW - 1) / TW;
   const bool use_sig = S.use_sigmoid != 0;
-  const int64_t ust = args.u.s[2], usc = args.u.s[3], lst = args.lg.s[2];
+
+  // Step t of the tile starting at Tt lies (t - Tt) time strides after the
+  // tile's buffer base, so each lane's byte offsets are fixed for the run.
+  const int tl0 = (w * TG + tg) * L;
+  const uint32_t ustb = (uint32_t)(args.u.s[2] * E), uscb = (uint32_t)(args.u.s[3] * E);
+  const uint32_t lstb = (uint32_t)(args.lg.s[2] * E), ostb = (uint32_t)(ost * E);
+  const uint32_t oscb = (uint32_t)(osc * E);
+  const uint32_t uoff = (uint32_t)tl0 * ustb + (uint32_t)c0 * uscb;
+  const uint32_t loff = (uint32_t)tl0 * lstb +
+                        (GM == GATE_CHANVEC ? (uint32_t)c0 * (uint32_t)E : 0u);  // r == 1: j == c
+  const uint32_t ooff = (uint32_t)tl0 * ostb + (uint32_t)c0 * oscb;
 
   // the next tile's packed values and raw logits are loaded while the current
   // tile is scanned, so every wavefront keeps loads in flight
-  const int tl0 = (w * TG + tg) * L;
   uint4 nu[L];
   LogitRaw<TIO, GM, L> nl;
   auto load_tile = [&](int it) {
-    const int t0 = t_lo + it * TW + tl0;
+    const int Tt = t_lo + it * TW;
+    const int t0 = Tt + tl0;
+    const Rsrc ur = make_rsrc(ubh + (int64_t)Tt * args.u.s[2] * E);
 #pragma unroll
-    for (int s = 0; s < L; ++s) {
-      const bool ok = active && (t0 + s) < t_hi;
-      nu[s] = ok ? ld_vec<TIO, VEC>(up + (int64_t)(t0 + s) * ust, usc, nvalid)
-                 : make_uint4(0u, 0u, 0u, 0u);
-    }
-    nl.load(lp + (int64_t)t0 * lst, lst, gi, t0, t_hi, active, nvalid);
+    for (int s = 0; s < L; ++s)
+      nu[s] = bld_vec<TIO, VEC>(ur, uoff + s * ustb, uscb, nvalid, active && (t0 + s) < t_hi);
+    nl.load(make_rsrc(lbh + (int64_t)Tt * args.lg.s[2] * E), loff, lstb, gi, t0, t_hi,
+                active, nvalid);
   };
   load_tile(0);
 
   for (int it = 0; it < ntiles; ++it) {
-    const int t0 = t_lo + it * TW + tl0;
+    const int Tt = t_lo + it * TW;
+    const int t0 = Tt + tl0;
     uint4 uq[L];
 #pragma unroll
     for (int s = 0; s < L; ++s) uq[s] = nu[s];
     float al[L][NA];
     nl.gates(gi, t0, t_hi, active, use_sig, al);
-    if (it + 1 < ntiles) load_tile(it + 1);
+    load_tile(it + 1);  // past the end: every lane masked, no memory access
 
     // level 1: lane-local fold (padded steps have alpha = 0: the identity)
     float A[NA], X[V];
@@ -569,6 +684,7 @@ scan_fwd_kernel(const FwdArgs args) {
 
     // re-run the lane's steps from its exact carry-in and store
     reload_barrier(uq);
+    const Rsrc orr = make_rsrc(obh + (int64_t)Tt * ost * E);
     float hv[V];
 #pragma unroll
     for (int v = 0; v < V; ++v) hv[v] = fmaf(Ae[GL ? 0 : v], hw[v], Xe[v]);
@@ -579,8 +695,8 @@ scan_fwd_kernel(const FwdArgs args) {
         const float a = al[s][GL ? 0 : v];
         hv[v] = fmaf(a, Pack<TIO>::get(uq[s], v) - hv[v], hv[v]);
       }
-      if (active && (t0 + s) >= t_st && (t0 + s) < t_hi)
-        st_vec<TIO, VEC>(outp + (int64_t)(t0 + s) * os[2], os[3], nvalid, hv);
+      bst_vec<TIO, VEC>(orr, ooff + s * ostb, oscb, nvalid,
+                        active && (t0 + s) >= t_st && (t0 + s) < t_hi, hv);
     }
   }
 }
@@ -624,39 +740,36 @@ scan_bwd_kernel(const BwdArgs args) {
   const HeadView hvw = head_view(args.h, which), gvw = head_view(args.gy, which);
   const int64_t hs[4] = {hvw.s[0], hvw.s[1], hvw.s[2], hvw.s[3]};
   const int64_t gs[4] = {gvw.s[0], gvw.s[1], gvw.s[2], gvw.s[3]};
-  const TIO* hp = reinterpret_cast<const TIO*>(hvw.p) + (int64_t)b * hs[0] +
-                  (int64_t)hl * hs[1] + (int64_t)c0 * hs[3];
-  const TIO* gp = reinterpret_cast<const TIO*>(gvw.p) + (int64_t)b * gs[0] +
-                  (int64_t)hl * gs[1] + (int64_t)c0 * gs[3];
-  const TIO* up = reinterpret_cast<const TIO*>(args.u.p) + (int64_t)b * args.u.s[0] +
-                  (int64_t)h * args.u.s[1] + (int64_t)c0 * args.u.s[3];
-  TIO* dup = reinterpret_cast<TIO*>(const_cast<void*>(args.du.p)) + (int64_t)b * args.du.s[0] +
-             (int64_t)h * args.du.s[1] + (int64_t)c0 * args.du.s[3];
-  const TIO* lp = reinterpret_cast<const TIO*>(args.lg.p) + (int64_t)b * args.lg.s[0] +
-                  (int64_t)h * args.lg.s[1];
-  TIO* dlp = reinterpret_cast<TIO*>(const_cast<void*>(args.dlg.p)) + (int64_t)b * args.dlg.s[0] +
-             (int64_t)h * args.dlg.s[1];
-  if (GM == GATE_CHANVEC) lp += (int64_t)c0;
-  const TIO* ip = reinterpret_cast<const TIO*>(args.init.p) + (int64_t)b * args.init.s[0] +
-                  (int64_t)h * args.init.s[1] + (int64_t)c0 * args.init.s[3];
-  TIO* dip = reinterpret_cast<TIO*>(const_cast<void*>(args.dinit.p)) +
-             (int64_t)b * args.dinit.s[0] + (int64_t)h * args.dinit.s[1] +
-             (int64_t)c0 * args.dinit.s[3];
+  constexpr int E = sizeof(TIO);
+  // (b, h) slices (wave-uniform byte addresses)
+  const char* hbh = reinterpret_cast<const char*>(hvw.p) + ((int64_t)b * hs[0] + (int64_t)hl * hs[1]) * E;
+  const char* gbh = reinterpret_cast<const char*>(gvw.p) + ((int64_t)b * gs[0] + (int64_t)hl * gs[1]) * E;
+  const char* ubh = reinterpret_cast<const char*>(args.u.p) +
+                    ((int64_t)b * args.u.s[0] + (int64_t)h * args.u.s[1]) * E;
+  const char* lbh = reinterpret_cast<const char*>(args.lg.p) +
+                    ((int64_t)b * args.lg.s[0] + (int64_t)h * args.lg.s[1]) * E;
+  const char* dubh = reinterpret_cast<const char*>(args.du.p) +
+                     ((int64_t)b * args.du.s[0] + (int64_t)h * args.du.s[1]) * E;
+  const char* dlbh = reinterpret_cast<const char*>(args.dlg.p) +
+                     ((int64_t)b * args.dlg.s[0] + (int64_t)h * args.dlg.s[1]) * E;
+  const Rsrc irs = make_rsrc(reinterpret_cast<const char*>(args.init.p) +
+                             ((int64_t)b * args.init.s[0] + (int64_t)h * args.init.s[1]) * E);
 
   GateIdx<GM, V> gi;
   gi.init(args.bias + h * S.Da, c0, nvalid, S.D, S.r, args.lg.s[3]);
 
-  const int64_t ust = args.u.s[2], usc = args.u.s[3], lst = args.lg.s[2];
-  const int64_t dlst = args.dlg.s[2], dlsc = args.dlg.s[3];
   const bool use_sig = S.use_sigmoid != 0;
   const int gl_lanes = GL ? S.r / V : 1;           // lanes per gate group (GATE_LANE)
 
-  __shared__ float lds_ba[NW][CL][NA];
-  __shared__ float4 lds_bx[NW][CL][V / 4];
+  // wavefront totals, double-buffered by tile parity: with one barrier per
+  // tile (GATE_CHAN*) a wavefront may write the next tile's totals while
+  // another still reads this tile's
+  __shared__ float lds_ba[2][NW][CL][NA];
+  __shared__ float4 lds_bx[2][NW][CL][V / 4];
   // GATE_LANE: per-(step, lane) dalpha partials and per-(step, group) gate slopes
   __shared__ float lds_p[GL ? TW : 1][GL ? CL : 1];
   __shared__ float lds_sl[GL ? TW : 1][GL ? MAXG : 1];
-  __shared__ float lds_red[NT][MAXG];
+  __shared__ float lds_red[NT][GL ? 1 : V];
 
   float gcarry[V];  // g at the first step after the current tile
 #pragma unroll
@@ -666,15 +779,11 @@ scan_bwd_kernel(const BwdArgs args) {
 #pragma unroll
     for (int v = 0; v < V; ++v) gcarry[v] = v < nvalid ? cp[v] : 0.0f;
   }
-  // dbias accumulators: GATE_CHAN* keeps one per channel slot in registers;
-  // GATE_LANE accumulates per group j in this thread's own row of lds_red.
+  // dbias accumulators: GATE_CHAN* keeps one per channel slot; GATE_LANE one
+  // for the gate group this thread emits dlogits of (jt, below)
   float dacc[GL ? 1 : V];
 #pragma unroll
   for (int k = 0; k < (GL ? 1 : V); ++k) dacc[k] = 0.0f;
-  if (GL) {
-#pragma unroll
-    for (int k = 0; k < MAXG; ++k) lds_red[threadIdx.x][k] = 0.0f;
-  }
 
   // tiles it_lo..it_hi of TW steps from t_base; steps < t_hi exist, upstream
   // gradients and owned outputs start at t_st
@@ -695,54 +804,106 @@ scan_bwd_kernel(const BwdArgs args) {
     it_lo = chunk * tiles_pc;
     it_hi = min(ntiles, it_lo + tiles_pc) - 1;
   }
-  // this window's rows of the look-back workspaces, indexed by absolute step
-  const int64_t wrow0 = LB ? ((int64_t)bh * args.nchunk + chunk) * args.kw - t_base : 0;
-  const TIO* wsp = LB ? reinterpret_cast<const TIO*>(args.wst) + wrow0 * S.D + c0 : nullptr;
-  float* wdup = LB ? args.wdu + wrow0 * S.D + c0 : nullptr;
-  float* wdlp = LB ? args.wdl + wrow0 * S.Da : nullptr;
-  // The next (earlier) tile's packed u, gy and raw logits, and the state
+  // this window's rows of the look-back workspaces (row t - t_base)
+  const int64_t wrow0 = LB ? ((int64_t)bh * args.nchunk + chunk) * args.kw : 0;
+  const char* wsbh = LB ? reinterpret_cast<const char*>(args.wst) + wrow0 * S.D * E : nullptr;
+  const char* wdubh = LB ? reinterpret_cast<const char*>(args.wdu + wrow0 * S.D) : nullptr;
+  const char* wdlbh = LB ? reinterpret_cast<const char*>(args.wdl + wrow0 * S.Da) : nullptr;
+
+  // Step t of the tile starting at Tt lies (t - Tt) time strides after the
+  // tile's buffer base (the saved state h_{t-1} after the base at Tt - 1), so
+  // each lane's byte offsets are fixed for the run.
+  const int tl0 = (w * TG + tg) * L;
+  const uint32_t ustb = (uint32_t)(args.u.s[2] * E), uscb = (uint32_t)(args.u.s[3] * E);
+  const uint32_t gstb = (uint32_t)(gs[2] * E), gscb = (uint32_t)(gs[3] * E);
+  const uint32_t hstb = (uint32_t)(hs[2] * E), hscb = (uint32_t)(hs[3] * E);
+  const uint32_t lstb = (uint32_t)(args.lg.s[2] * E);
+  const uint32_t dustb = (uint32_t)(args.du.s[2] * E), duscb = (uint32_t)(args.du.s[3] * E);
+  const uint32_t dlstb = (uint32_t)(args.dlg.s[2] * E), dlscb = (uint32_t)(args.dlg.s[3] * E);
+  const uint32_t iscb = (uint32_t)(args.init.s[3] * E);
+  const uint32_t wstb = (uint32_t)(S.D * E), wdustb = (uint32_t)(S.D * 4), wdlstb = (uint32_t)(S.Da * 4);
+  const uint32_t uoff = (uint32_t)tl0 * ustb + (uint32_t)c0 * uscb;
+  const uint32_t goff = (uint32_t)tl0 * gstb + (uint32_t)c0 * gscb;
+  const uint32_t hoff = (uint32_t)tl0 * hstb + (uint32_t)c0 * hscb;
+  const uint32_t woff = (uint32_t)tl0 * wstb + (uint32_t)c0 * E;
+  const uint32_t ioff = (uint32_t)c0 * iscb;
+  const uint32_t loff = (uint32_t)tl0 * lstb +
+                        (GM == GATE_CHANVEC ? (uint32_t)c0 * (uint32_t)E : 0u);  // r == 1: j == c
+  const uint32_t duoff = (uint32_t)tl0 * dustb + (uint32_t)c0 * duscb;
+  const uint32_t wduoff = (uint32_t)tl0 * wdustb + (uint32_t)c0 * 4;
+
+  // The next PD (earlier) tiles' packed u, gy and raw logits, and the state
   // entering each lane's first step, are loaded while the current tile is
   // processed, so each wavefront keeps its loads in flight across the tile's
-  // barriers.  The state h_{t0-1} entering a lane is the saved forward output
-  // of the step before (the inits at t = 0); the lane recomputes its other
-  // L - 1 states h_t = h_{t-1} + alpha_t (u_t - h_{t-1}) itself, rounded to the
-  // I/O dtype as the forward stores them.
-  const int tl0 = (w * TG + tg) * L;
-  uint4 nu[L], ng[L], nh0;
-  LogitRaw<TIO, GM, L + 1> nl;
-  auto load_tile = [&](int it) {
-    const int t0 = t_base + it * TW + tl0;
+  // barriers and stores (two tiles when a lane's steps are few enough for the
+  // registers, else one).  The state h_{t0-1} entering a lane is the saved
+  // forward output of the step before (the inits at t = t_base; the warm-up
+  // states before t_st in a look-back window); the lane recomputes its other
+  // L - 1 states h_t = h_{t-1} + alpha_t (u_t - h_{t-1}) itself, rounded to
+  // the I/O dtype as the forward stores them.  A tile before it_lo is all
+  // masked: no memory access.
+  constexpr int PD = L <= 2 ? 2 : 1;
+  uint4 nu[PD][L], ng[PD][L], nh0[PD];
+  LogitRaw<TIO, GM, L + 1> nl[PD];
+  auto load_tile = [&](int it, auto bufc) {
+    constexpr int buf = decltype(bufc)::value;
+    const int Tt = t_base + it * TW;
+    const int t0 = Tt + tl0;
+    const bool tile_ok = active && it >= it_lo;
+    const Rsrc ur = make_rsrc(ubh + (int64_t)Tt * args.u.s[2] * E);
+    const Rsrc gr = make_rsrc(gbh + (int64_t)Tt * gs[2] * E);
 #pragma unroll
     for (int s = 0; s < L; ++s) {
       const int t = t0 + s;
-      const bool ok = active && t < t_hi;
-      nu[s] = ok ? ld_vec<TIO, VEC>(up + (int64_t)t * ust, usc, nvalid)
-                 : make_uint4(0u, 0u, 0u, 0u);
-      ng[s] = ok && (!LB || t >= t_st) ? ld_vec<TIO, VEC>(gp + (int64_t)t * gs[2], gs[3], nvalid)
-                                       : make_uint4(0u, 0u, 0u, 0u);
+      const bool ok = tile_ok && t < t_hi;
+      nu[buf][s] = bld_vec<TIO, VEC>(ur, uoff + s * ustb, uscb, nvalid, ok);
+      ng[buf][s] = bld_vec<TIO, VEC>(gr, goff + s * gstb, gscb, nvalid, ok && (!LB || t >= t_st));
     }
-    const bool ok0 = active && t0 < t_hi;
-    nh0 = !ok0                      ? make_uint4(0u, 0u, 0u, 0u)
-          : t0 == t_base            ? ld_vec<TIO, VEC>(ip, args.init.s[3], nvalid)
-          : (LB && t0 - 1 < t_st)   ? ld_vec<TIO, VEC>(wsp + (int64_t)(t0 - 1) * S.D, 1, nvalid)
-                                    : ld_vec<TIO, VEC>(hp + (int64_t)(t0 - 1) * hs[2], hs[3], nvalid);
-    nl.load(lp + (int64_t)t0 * lst, lst, gi, t0, t_hi, active, nvalid);
+    // exactly one of the sources is unmasked; the others read 0
+    const bool ok0 = tile_ok && t0 < t_hi;
+    const bool from_init = ok0 && t0 == t_base;
+    const bool from_wst = LB && ok0 && !from_init && t0 - 1 < t_st;
+    const bool from_h = ok0 && !from_init && !from_wst;
+    uint4 q = bld_vec<TIO, VEC>(make_rsrc(hbh + (int64_t)(Tt - 1) * hs[2] * E), hoff, hscb,
+                                nvalid, from_h);
+    const uint4 qi = bld_vec<TIO, VEC>(irs, ioff, iscb, nvalid, from_init);
+    q = make_uint4(q.x | qi.x, q.y | qi.y, q.z | qi.z, q.w | qi.w);
+    if (LB) {
+      const uint4 qw = bld_vec<TIO, VEC>(make_rsrc(wsbh + (int64_t)(Tt - 1 - t_base) * S.D * E),
+                                         woff, E, nvalid, from_wst);
+      q = make_uint4(q.x | qw.x, q.y | qw.y, q.z | qw.z, q.w | qw.w);
+    }
+    nh0[buf] = q;
+    nl[buf].load(make_rsrc(lbh + (int64_t)Tt * args.lg.s[2] * E), loff, lstb, gi, t0, t_hi,
+                 tile_ok, nvalid);
   };
-  if (it_hi >= it_lo) load_tile(it_hi);
-  for (int it = it_hi; it >= it_lo; --it) {
+
+  // GATE_LANE dlogit pass: thread item k covers (step tl, group jt) with
+  // idx = threadIdx.x + k NT = tl MAXG + jt; NT is a multiple of MAXG, so jt
+  // is fixed per thread
+  constexpr int NI = GL ? (TW * MAXG + NT - 1) / NT : 1;
+  const int jt = threadIdx.x % MAXG;
+  const bool jt_ok = jt < S.Da;
+  const int jtc = jt_ok ? jt : 0;
+  float dinit_v[V];  // (1 - alpha) g at each tile's first lane step; the last tile's is kept
+#pragma unroll
+  for (int v = 0; v < V; ++v) dinit_v[v] = 0.0f;
+
+  auto process_tile = [&](int it, auto bufc) {
+    constexpr int buf = decltype(bufc)::value;
     const int T0 = t_base + it * TW;
     const int t0 = T0 + tl0;
 
     uint4 uq[L], gq[L], hq[L];
 #pragma unroll
     for (int s = 0; s < L; ++s) {
-      uq[s] = nu[s];
-      gq[s] = ng[s];
+      uq[s] = nu[buf][s];
+      gq[s] = ng[buf][s];
     }
-    hq[0] = nh0;
+    hq[0] = nh0[buf];
     float al[L + 1][NA];
-    nl.gates(gi, t0, t_hi, active, use_sig, al);
-    if (it > it_lo) load_tile(it - 1);
+    nl[buf].gates(gi, t0, t_hi, active, use_sig, al);
+    load_tile(it - PD, bufc);
     // h_{t-1} of the lane's later steps (padded steps have alpha = 0)
 #pragma unroll
     for (int s = 1; s < L; ++s) {
@@ -756,27 +917,28 @@ scan_bwd_kernel(const BwdArgs args) {
     }
 
     // ---- reverse scan: g_t = gy_t + (1 - alpha_{t+1}) g_{t+1}
-    // decay carrying g_{t+1} into g_t; zero for the last step of the sequence
+    // dk[s][i]: decay carrying g_{t+1} into g_t, zero for the last step of the
+    // sequence.  Steps at or past t_hi (padding) need no guard: their gy reads
+    // 0, and the step before the first of them has decay 0, so they leave the
+    // lane's map as if skipped.
+    float dk[L][NA];
+#pragma unroll
+    for (int s = 0; s < L; ++s)
+#pragma unroll
+      for (int i = 0; i < NA; ++i) dk[s][i] = t0 + s + 1 < t_hi ? 1.0f - al[s + 1][i] : 0.0f;
     float gin[V];
     {
       float A[NA], G[V];
 #pragma unroll
-      for (int i = 0; i < NA; ++i) A[i] = 1.0f;
+      for (int i = 0; i < NA; ++i) A[i] = dk[L - 1][i];
 #pragma unroll
-      for (int v = 0; v < V; ++v) G[v] = 0.0f;
+      for (int v = 0; v < V; ++v) G[v] = Pack<TIO>::get(gq[L - 1], v);
 #pragma unroll
-      for (int s = L - 1; s >= 0; --s) {
-        const int t = t0 + s;
-        if (active && t < t_hi) {
-          const bool nxt = t + 1 < t_hi;
+      for (int s = L - 2; s >= 0; --s) {
 #pragma unroll
-          for (int v = 0; v < V; ++v) {
-            const float an = nxt ? 1.0f - al[s + 1][GL ? 0 : v] : 0.0f;
-            G[v] = fmaf(an, G[v], Pack<TIO>::get(gq[s], v));
-          }
+        for (int v = 0; v < V; ++v) G[v] = fmaf(dk[s][GL ? 0 : v], G[v], Pack<TIO>::get(gq[s], v));
 #pragma unroll
-          for (int i = 0; i < NA; ++i) A[i] *= nxt ? 1.0f - al[s + 1][i] : 0.0f;
-        }
+        for (int i = 0; i < NA; ++i) A[i] *= dk[s][i];
       }
       SegScan<TG, NA, V, GL>::template down_level<1>(tg, A, G);
       float Ae[NA], Ge[V];
@@ -790,12 +952,13 @@ scan_bwd_kernel(const BwdArgs args) {
         const float t = shift_down<TG, 1>(G[v]);
         Ge[v] = tg == TG - 1 ? 0.0f : t;
       }
+      const int par = it & 1;
       if (tg == 0) {
 #pragma unroll
-        for (int i = 0; i < NA; ++i) lds_ba[w][cl][i] = A[i];
+        for (int i = 0; i < NA; ++i) lds_ba[par][w][cl][i] = A[i];
 #pragma unroll
         for (int q = 0; q < V / 4; ++q)
-          lds_bx[w][cl][q] = make_float4(G[4 * q], G[4 * q + 1], G[4 * q + 2], G[4 * q + 3]);
+          lds_bx[par][w][cl][q] = make_float4(G[4 * q], G[4 * q + 1], G[4 * q + 2], G[4 * q + 3]);
       }
       __syncthreads();  // (2)
       float gw[V];
@@ -809,10 +972,10 @@ scan_bwd_kernel(const BwdArgs args) {
         }
         float Aw[NA];
 #pragma unroll
-        for (int i = 0; i < NA; ++i) Aw[i] = lds_ba[ww][cl][i];
+        for (int i = 0; i < NA; ++i) Aw[i] = lds_ba[par][ww][cl][i];
 #pragma unroll
         for (int q = 0; q < V / 4; ++q) {
-          const float4 x4 = lds_bx[ww][cl][q];
+          const float4 x4 = lds_bx[par][ww][cl][q];
           gcarry[4 * q + 0] = fmaf(Aw[GL ? 0 : 4 * q + 0], gcarry[4 * q + 0], x4.x);
           gcarry[4 * q + 1] = fmaf(Aw[GL ? 0 : 4 * q + 1], gcarry[4 * q + 1], x4.y);
           gcarry[4 * q + 2] = fmaf(Aw[GL ? 0 : 4 * q + 2], gcarry[4 * q + 2], x4.z);
@@ -823,40 +986,31 @@ scan_bwd_kernel(const BwdArgs args) {
       for (int v = 0; v < V; ++v) gin[v] = fmaf(Ae[GL ? 0 : v], gw[v], Ge[v]);
     }
 
-    // ---- re-run backwards: du, dinit and the gate-group dalpha sums
+    // ---- re-run backwards: du, dinit and the gate-group dalpha sums; steps
+    // before t_st (look-back warm-up) go to the fp32 workspaces
     reload_barrier(uq);
     reload_barrier(gq);
-      float pl[L];  // GATE_LANE: this lane's dalpha partial per step
+    const Rsrc dur = make_rsrc(dubh + (int64_t)T0 * args.du.s[2] * E);
+    const Rsrc dlr = make_rsrc(dlbh + (int64_t)T0 * args.dlg.s[2] * E);
+    const Rsrc wdur = make_rsrc(LB ? wdubh + (int64_t)(T0 - t_base) * S.D * 4 : dubh);
+    const Rsrc wdlr = make_rsrc(LB ? wdlbh + (int64_t)(T0 - t_base) * S.Da * 4 : dlbh);
+    float pl[L];  // GATE_LANE: this lane's dalpha partial per step
 #pragma unroll
     for (int s = L - 1; s >= 0; --s) {
       const int t = t0 + s;
       const bool ok = active && t < t_hi;
-      const bool nxt = t + 1 < t_hi;
+      const bool wu = LB && t < t_st;
       float gv[V], duv[V], dav[V];
 #pragma unroll
       for (int v = 0; v < V; ++v) {
         const int ia = GL ? 0 : v;
-        const float an = nxt ? 1.0f - al[s + 1][ia] : 0.0f;
-        gv[v] = ok ? fmaf(an, gin[v], Pack<TIO>::get(gq[s], v)) : gin[v];
+        gv[v] = fmaf(dk[s][ia], gin[v], Pack<TIO>::get(gq[s], v));
         gin[v] = gv[v];
         duv[v] = al[s][ia] * gv[v];
         dav[v] = (Pack<TIO>::get(uq[s], v) - Pack<TIO>::get(hq[s], v)) * gv[v];
       }
-      if (ok) {
-        if (LB && t < t_st)
-          st_f32<VEC, V>(wdup + (int64_t)t * S.D, nvalid, duv);
-        else
-          st_vec<TIO, VEC>(dup + (int64_t)t * args.du.s[2], args.du.s[3], nvalid, duv);
-        if (t == t_base) {
-          float di[V];
-#pragma unroll
-          for (int v = 0; v < V; ++v) di[v] = (1.0f - al[s][GL ? 0 : v]) * gv[v];
-          if (LB)
-            st_f32<VEC, V>(args.wdi + ((int64_t)bh * args.nchunk + chunk) * S.D + c0, nvalid, di);
-          else
-            st_vec<TIO, VEC>(dip, args.dinit.s[3], nvalid, di);
-        }
-      }
+      bst_vec<TIO, VEC>(dur, duoff + s * dustb, duscb, nvalid, ok && !wu, duv);
+      if (LB) bst_f32<VEC, V>(wdur, wduoff + s * wdustb, nvalid, ok && wu, duv);
       if (GL) {
         float p = 0.0f;
 #pragma unroll
@@ -876,41 +1030,37 @@ scan_bwd_kernel(const BwdArgs args) {
             for (int v = 0; v < V; ++v) dav[v] = tsum[v];
           }
         }
-        if (ok) {
-          float dl[V];
+        float dl[V];
+#pragma unroll
+        for (int v = 0; v < V; ++v) {
+          const float a = al[s][v];
+          dl[v] = use_sig ? dav[v] * (a * (1.0f - a)) : dav[v];
+        }
+        const uint32_t srow = GM == GATE_CHAN ? opaque(tl0 + s) : (uint32_t)(tl0 + s);
+        if (GM == GATE_CHANVEC) {
+          // r == 1: the V dlogits of this lane are contiguous
+          bst_vec<TIO, true>(dlr, srow * dlstb + (uint32_t)c0 * E, E, V, ok && !wu, dl);
+          if (LB) bst_f32<true, V>(wdlr, srow * wdlstb + (uint32_t)c0 * 4, V, ok && wu, dl);
+#pragma unroll
+          for (int v = 0; v < V; ++v) dacc[v] += ok ? dl[v] : 0.0f;
+        } else {
 #pragma unroll
           for (int v = 0; v < V; ++v) {
-            const float a = al[s][v];
-            dl[v] = use_sig ? dav[v] * (a * (1.0f - a)) : dav[v];
-          }
-          if (GM == GATE_CHANVEC) {
-            // r == 1: the V dlogits of this lane are contiguous
-            if (LB && t < t_st)
-              st_f32<true, V>(wdlp + (int64_t)t * S.Da + c0, V, dl);
-            else
-              st_vec<TIO, true>(dlp + (int64_t)t * dlst + c0, 1, V, dl);
-#pragma unroll
-            for (int v = 0; v < V; ++v) dacc[v] += dl[v];
-          } else {
-#pragma unroll
-            for (int v = 0; v < V; ++v) {
-              if ((v & (S.r - 1)) == 0 && v < nvalid) {
-                dacc[v] += dl[v];
-                const int j = (c0 + v) / S.r;
-                if (LB && t < t_st)
-                  wdlp[(int64_t)t * S.Da + j] = dl[v];
-                else
-                  Pack<TIO>::store1(dlp + (int64_t)t * dlst + (int64_t)j * dlsc, dl[v]);
-              }
-            }
+            const bool lead = ok && (v & (S.r - 1)) == 0 && v < nvalid;
+            const uint32_t j = (uint32_t)((c0 + v) / S.r);
+            dacc[v] += lead ? dl[v] : 0.0f;
+            bst1<TIO>(dlr, lead && !wu ? srow * dlstb + j * dlscb : kOob, dl[v]);
+            if (LB) bst_b32(wdlr, lead && wu ? srow * wdlstb + j * 4 : kOob, dl[v]);
           }
         }
       }
     }
+    // kept from the last tile processed (it_lo), whose lane tl0 == 0 holds t_base
+#pragma unroll
+    for (int v = 0; v < V; ++v) dinit_v[v] = (1.0f - al[0][GL ? 0 : v]) * gin[v];
 
     if (GL) {
       // ---- dlogit[t, j] = slope * sum of the group's lane partials (fixed order)
-      const int tl0 = (w * TG + tg) * L;
 #pragma unroll
       for (int s = 0; s < L; ++s) lds_p[tl0 + s][cl] = pl[s];
       if (active && (cl % gl_lanes) == 0 && cl / gl_lanes < MAXG) {
@@ -921,39 +1071,55 @@ scan_bwd_kernel(const BwdArgs args) {
         }
       }
       __syncthreads();  // (3)
-      for (int tl = threadIdx.x; tl < TW; tl += NT) {
-        const int t = T0 + tl;
-        if (t < t_hi) {
 #pragma unroll
-          for (int j = 0; j < MAXG; ++j) {
-            if (j < S.Da) {
-              float p = 0.0f;
-              for (int q = 0; q < gl_lanes; ++q) p += lds_p[tl][j * gl_lanes + q];
-              const float d = p * lds_sl[tl][j];
-              lds_red[threadIdx.x][j] += d;
-              if (LB && t < t_st)
-                wdlp[(int64_t)t * S.Da + j] = d;
-              else
-                Pack<TIO>::store1(dlp + (int64_t)t * dlst + (int64_t)j * dlsc, d);
-            }
-          }
-        }
+      for (int k = 0; k < NI; ++k) {
+        const int tl = (threadIdx.x + k * NT) / MAXG;
+        const int tlc = tl < TW ? tl : TW - 1;
+        const int t = T0 + tl;
+        const bool ok = jt_ok && tl < TW && t < t_hi;
+        const bool wu = LB && t < t_st;
+        float p = 0.0f;
+        for (int q = 0; q < gl_lanes; ++q) p += lds_p[tlc][jtc * gl_lanes + q];
+        const float d = p * lds_sl[tlc][jtc];
+        dacc[0] += ok ? d : 0.0f;
+        bst1<TIO>(dlr, ok && !wu ? (uint32_t)tl * dlstb + (uint32_t)jt * dlscb : kOob, d);
+        if (LB) bst_b32(wdlr, ok && wu ? (uint32_t)tl * wdlstb + (uint32_t)jt * 4 : kOob, d);
       }
     }
+  };
+  using B0 = std::integral_constant<int, 0>;
+  using B1 = std::integral_constant<int, 1>;
+  load_tile(it_hi, B0{});
+  if constexpr (PD == 2) {
+    load_tile(it_hi - 1, B1{});
+    for (int it = it_hi; it >= it_lo; it -= 2) {
+      process_tile(it, B0{});
+      if (it - 1 >= it_lo) process_tile(it - 1, B1{});
+    }
+  } else {
+    for (int it = it_hi; it >= it_lo; --it) process_tile(it, B0{});
+  }
+
+  // ---- dinit: the state gradient at t_base, from lane tl0 == 0 of tile it_lo
+  if (active && it_hi >= it_lo && it_lo == 0 && tl0 == 0) {
+    if (LB)
+      st_f32<VEC, V>(args.wdi + ((int64_t)bh * args.nchunk + chunk) * S.D + c0, nvalid, dinit_v);
+    else
+      st_vec<TIO, VEC>(reinterpret_cast<TIO*>(const_cast<void*>(args.dinit.p)) +
+                           (int64_t)b * args.dinit.s[0] + (int64_t)h * args.dinit.s[1] +
+                           (int64_t)c0 * args.dinit.s[3],
+                       args.dinit.s[3], nvalid, dinit_v);
   }
 
   // ---- dbias partial for (b, h): fixed-order sum of the accumulators
-  if (!GL) {
 #pragma unroll
-    for (int k = 0; k < V; ++k) lds_red[threadIdx.x][k] = dacc[k];
-  }
+  for (int k = 0; k < (GL ? 1 : V); ++k) lds_red[threadIdx.x][k] = dacc[k];
   __syncthreads();
   for (int j = threadIdx.x; j < S.Da; j += NT) {
     float acc = 0.0f;
     if (GL) {
-      // threads tl < min(TW, NT) hold group j in slot j
-      const int nth = TW < NT ? TW : NT;
-      for (int q = 0; q < nth; ++q) acc += lds_red[q][j];
+      // group j's dlogits were emitted by the threads q == j (mod MAXG)
+      for (int q = j; q < NT; q += MAXG) acc += lds_red[q][0];
     } else {
       // group j is led by channel c = j r: lane cl = c / V, slot c % V, in every
       // time lane (w, tg) of the workgroup

@@ -52,10 +52,10 @@ bool fwd_dispatch(const FwdArgs& a, int grid, bool vec, int gm, hipStream_t st) 
 }
 
 // The look-back backward is built for the base shapes and for the shape the
-// d12 heads use (16 channel lanes, 2 steps per lane).
+// d12 heads use (16 channel lanes, 4 steps per lane, 2 wavefronts).
 template <int CL, int L, int NW>
 constexpr bool is_lb_cfg() {
-  return is_base_cfg<CL, L, NW>() || (CL == 16 && L == 2 && NW == 4);
+  return is_base_cfg<CL, L, NW>() || (CL == 16 && L == 4 && NW == 2);
 }
 
 template <typename TIO, int CL, int L, int NW, bool LB>

@@ -73,6 +73,20 @@ def test_abi_version_and_host_only_queries():
     rc = lib.ltv_hm_look_back_scan_forward(1, None, s3, None, s3, None, None, s4, None, s4,
                                            None, s4, 1, 1, 1, 1, 1, 1, 4, 0, 1, 1, None)
     assert rc == 1 and "Q >= 1" in N.last_error()
+    # a view whose in-tile byte offsets would pass 2 GiB is refused before any
+    # launch (the scan tiles address memory through 32-bit offsets); the dummy
+    # pointer is never dereferenced
+    dummy = ctypes.create_string_buffer(64)
+    p = ctypes.cast(dummy, ctypes.c_void_p)
+    B, T, NH, NKVH, Da, r = 1, 8, 1, 0, 1, 128
+    wide = 1 << 21  # elements per time step: 1,026 steps x 4 MiB > 2 GiB
+    cs = (ctypes.c_int64 * 3)(T * wide, wide, 1)
+    ins = (ctypes.c_int64 * 3)(128, 128, 1)
+    outs = (ctypes.c_int64 * 4)(T * 128, T * 128, 128, 1)
+    bias = (ctypes.c_float * 1)(0.0)
+    rc = lib.ltv_hm_look_back_scan_forward(1, p, cs, p, ins, bias, p, outs, p, outs, p, outs,
+                                           B, T, NH, NKVH, Da, r, 2147483647, 1, 1, 1, None)
+    assert rc == 2 and "32-bit tile offsets" in N.last_error(), N.last_error()
 
 
 def test_ops_import_without_gpu():
