@@ -467,7 +467,10 @@ struct GateIdx {
 template <typename TIO, int GM, int NS>
 struct LogitRaw {
   static constexpr int V = Pack<TIO>::V;
-  uint32_t one[GM == GATE_LANE ? NS : 1];
+  // raw element bits as loaded (16-bit for bf16: widened only where used, so
+  // no zero-extension waits for the load right after it is issued)
+  using Raw = std::conditional_t<sizeof(TIO) == 2, uint16_t, uint32_t>;
+  Raw one[GM == GATE_LANE ? NS : 1];
   uint4 vec[GM == GATE_LANE ? 1 : NS];
 
   __device__ __forceinline__ void load(Rsrc rs, uint32_t off0, uint32_t lstb,
@@ -478,7 +481,7 @@ struct LogitRaw {
       const bool ok = active && (t0 + s) < T;
       const uint32_t o = GM == GATE_CHAN ? opaque(off0 + s * lstb) : off0 + s * lstb;
       if (GM == GATE_LANE) {
-        one[s] = bld1<TIO>(rs, ok ? o + (uint32_t)(gi.off[0] * sizeof(TIO)) : kOob);
+        one[s] = (Raw)bld1<TIO>(rs, ok ? o + (uint32_t)(gi.off[0] * sizeof(TIO)) : kOob);
       } else if (GM == GATE_CHANVEC) {
         vec[s] = bld128(rs, ok ? o : kOob);
       } else {
@@ -502,9 +505,15 @@ struct LogitRaw {
 #pragma unroll
       for (int i = 0; i < NA; ++i) {
         const float raw = GM == GATE_LANE
-                              ? __uint_as_float(sizeof(TIO) == 2 ? one[s] << 16 : one[s])
+                              ? __uint_as_float(sizeof(TIO) == 2 ? (uint32_t)one[s] << 16
+                                                                 : (uint32_t)one[s])
                               : Pack<TIO>::get(vec[s], i);
-        al[s][i] = ok ? gate_alpha(raw + gi.bias[i], use_sig) : 0.0f;
+        // computed for every lane, then selected: guarding the exp / rcp with
+        // a branch makes the compiler wait there for every outstanding
+        // memory operation, the previous tile's stores included
+        float a = gate_alpha(raw + gi.bias[i], use_sig);
+        asm volatile("" : "+v"(a));
+        al[s][i] = ok ? a : 0.0f;
       }
     }
   }
@@ -594,30 +603,35 @@ scan_fwd_kernel(const FwdArgs args) {
   const uint32_t ooff = (uint32_t)tl0 * ostb + (uint32_t)c0 * oscb;
 
   // the next tile's packed values and raw logits are loaded while the current
-  // tile is scanned, so every wavefront keeps loads in flight
-  uint4 nu[L];
-  LogitRaw<TIO, GM, L> nl;
-  auto load_tile = [&](int it) {
+  // tile is scanned, so every wavefront keeps loads in flight; alternate tiles
+  // use two buffers (with one, the compiler copies the new loads into the
+  // body's registers at the end of each tile, waiting there for every
+  // outstanding memory operation, the tile's stores included)
+  uint4 nu[2][L];
+  LogitRaw<TIO, GM, L> nl[2];
+  auto load_tile = [&](int it, auto bufc) {
+    constexpr int buf = decltype(bufc)::value;
     const int Tt = t_lo + it * TW;
     const int t0 = Tt + tl0;
     const Rsrc ur = make_rsrc(ubh + (int64_t)Tt * args.u.s[2] * E);
 #pragma unroll
     for (int s = 0; s < L; ++s)
-      nu[s] = bld_vec<TIO, VEC>(ur, uoff + s * ustb, uscb, nvalid, active && (t0 + s) < t_hi);
-    nl.load(make_rsrc(lbh + (int64_t)Tt * args.lg.s[2] * E), loff, lstb, gi, t0, t_hi,
-                active, nvalid);
+      nu[buf][s] = bld_vec<TIO, VEC>(ur, uoff + s * ustb, uscb, nvalid, active && (t0 + s) < t_hi);
+    nl[buf].load(make_rsrc(lbh + (int64_t)Tt * args.lg.s[2] * E), loff, lstb, gi, t0, t_hi,
+                 active, nvalid);
   };
-  load_tile(0);
 
-  for (int it = 0; it < ntiles; ++it) {
+  auto process_tile = [&](int it, auto bufc) {
+    constexpr int buf = decltype(bufc)::value;
     const int Tt = t_lo + it * TW;
     const int t0 = Tt + tl0;
     uint4 uq[L];
 #pragma unroll
-    for (int s = 0; s < L; ++s) uq[s] = nu[s];
+    for (int s = 0; s < L; ++s) uq[s] = nu[buf][s];
     float al[L][NA];
-    nl.gates(gi, t0, t_hi, active, use_sig, al);
-    load_tile(it + 1);  // past the end: every lane masked, no memory access
+    nl[buf].gates(gi, t0, t_hi, active, use_sig, al);
+    // past the end: every lane masked, no memory access
+    load_tile(it + 1, std::integral_constant<int, 1 - buf>{});
 
     // level 1: lane-local fold (padded steps have alpha = 0: the identity)
     float A[NA], X[V];
@@ -651,13 +665,13 @@ scan_fwd_kernel(const FwdArgs args) {
     }
 
     // level 3: wavefront totals through LDS, composed onto the running carry
-    const int buf = it & 1;
+    const int par = it & 1;
     if (tg == TG - 1) {
 #pragma unroll
-      for (int i = 0; i < NA; ++i) lds_a[buf][w][cl][i] = A[i];
+      for (int i = 0; i < NA; ++i) lds_a[par][w][cl][i] = A[i];
 #pragma unroll
       for (int q = 0; q < V / 4; ++q)
-        lds_x[buf][w][cl][q] = make_float4(X[4 * q], X[4 * q + 1], X[4 * q + 2], X[4 * q + 3]);
+        lds_x[par][w][cl][q] = make_float4(X[4 * q], X[4 * q + 1], X[4 * q + 2], X[4 * q + 3]);
     }
     __syncthreads();
     float hw[V];
@@ -671,10 +685,10 @@ scan_fwd_kernel(const FwdArgs args) {
       }
       float Aw[NA];
 #pragma unroll
-      for (int i = 0; i < NA; ++i) Aw[i] = lds_a[buf][ww][cl][i];
+      for (int i = 0; i < NA; ++i) Aw[i] = lds_a[par][ww][cl][i];
 #pragma unroll
       for (int q = 0; q < V / 4; ++q) {
-        const float4 x4 = lds_x[buf][ww][cl][q];
+        const float4 x4 = lds_x[par][ww][cl][q];
         carry[4 * q + 0] = fmaf(Aw[GL ? 0 : 4 * q + 0], carry[4 * q + 0], x4.x);
         carry[4 * q + 1] = fmaf(Aw[GL ? 0 : 4 * q + 1], carry[4 * q + 1], x4.y);
         carry[4 * q + 2] = fmaf(Aw[GL ? 0 : 4 * q + 2], carry[4 * q + 2], x4.z);
@@ -698,6 +712,14 @@ scan_fwd_kernel(const FwdArgs args) {
       bst_vec<TIO, VEC>(orr, ooff + s * ostb, oscb, nvalid,
                         active && (t0 + s) >= t_st && (t0 + s) < t_hi, hv);
     }
+  };
+
+  using B0 = std::integral_constant<int, 0>;
+  using B1 = std::integral_constant<int, 1>;
+  load_tile(0, B0{});
+  for (int it = 0; it < ntiles; it += 2) {
+    process_tile(it, B0{});
+    if (it + 1 < ntiles) process_tile(it + 1, B1{});
   }
 }
 
@@ -705,7 +727,8 @@ scan_fwd_kernel(const FwdArgs args) {
 // Backward
 // ---------------------------------------------------------------------------
 // GATE_LANE: r % V == 0; the gate group spans r / V adjacent channel lanes and
-//   dalpha is summed across them through LDS; at most kMaxLaneGroups groups.
+//   dalpha is summed across them with lane shuffles; at most kMaxLaneGroups
+//   groups.
 // GATE_CHAN / GATE_CHANVEC: V % r == 0; each lane holds V / r whole groups.
 constexpr int kMaxLaneGroups = 16;
 
@@ -718,7 +741,6 @@ scan_bwd_kernel(const BwdArgs args) {
   constexpr int TW = NW * TG * L;
   constexpr int NT = NW * 64;
   constexpr bool GL = GM == GATE_LANE;
-  constexpr int MAXG = GL ? (CL < kMaxLaneGroups ? CL : kMaxLaneGroups) : V;
   const ScanShape& S = args.sh;
 
   const int lane = threadIdx.x & 63;
@@ -766,9 +788,6 @@ scan_bwd_kernel(const BwdArgs args) {
   // another still reads this tile's
   __shared__ float lds_ba[2][NW][CL][NA];
   __shared__ float4 lds_bx[2][NW][CL][V / 4];
-  // GATE_LANE: per-(step, lane) dalpha partials and per-(step, group) gate slopes
-  __shared__ float lds_p[GL ? TW : 1][GL ? CL : 1];
-  __shared__ float lds_sl[GL ? TW : 1][GL ? MAXG : 1];
   __shared__ float lds_red[NT][GL ? 1 : V];
 
   float gcarry[V];  // g at the first step after the current tile
@@ -780,7 +799,7 @@ scan_bwd_kernel(const BwdArgs args) {
     for (int v = 0; v < V; ++v) gcarry[v] = v < nvalid ? cp[v] : 0.0f;
   }
   // dbias accumulators: GATE_CHAN* keeps one per channel slot; GATE_LANE one
-  // for the gate group this thread emits dlogits of (jt, below)
+  // in the last lane of each gate group (the lane that emits its dlogits)
   float dacc[GL ? 1 : V];
 #pragma unroll
   for (int k = 0; k < (GL ? 1 : V); ++k) dacc[k] = 0.0f;
@@ -832,19 +851,26 @@ scan_bwd_kernel(const BwdArgs args) {
   const uint32_t duoff = (uint32_t)tl0 * dustb + (uint32_t)c0 * duscb;
   const uint32_t wduoff = (uint32_t)tl0 * wdustb + (uint32_t)c0 * 4;
 
-  // The next PD (earlier) tiles' packed u, gy and raw logits, and the state
-  // entering each lane's first step, are loaded while the current tile is
-  // processed, so each wavefront keeps its loads in flight across the tile's
-  // barriers and stores (two tiles when a lane's steps are few enough for the
-  // registers, else one).  The state h_{t0-1} entering a lane is the saved
+  // The packed u, gy and raw logits of an earlier tile, and the state entering
+  // each lane's first step, are loaded while the current tile is processed, so
+  // each wavefront keeps its loads in flight across the tile's barriers and
+  // stores: PD tiles ahead (two when a lane's steps are few enough for the
+  // registers, else one).  Where the registers allow (NB = 2), alternate
+  // tiles use two buffers: with one buffer the compiler copies the new loads
+  // into the body's registers at the end of each tile, waiting there for
+  // every outstanding memory operation, the tile's own stores included.  The state h_{t0-1} entering a lane is the saved
   // forward output of the step before (the inits at t = t_base; the warm-up
   // states before t_st in a look-back window); the lane recomputes its other
   // L - 1 states h_t = h_{t-1} + alpha_t (u_t - h_{t-1}) itself, rounded to
   // the I/O dtype as the forward stores them.  A tile before it_lo is all
   // masked: no memory access.
   constexpr int PD = L <= 2 ? 2 : 1;
-  uint4 nu[PD][L], ng[PD][L], nh0[PD];
-  LogitRaw<TIO, GM, L + 1> nl[PD];
+  constexpr int NB = PD == 2 || (GL && L <= 4) ? 2 : 1;
+  // the state entering the lane comes from one of three masked loads, kept
+  // apart until the tile uses it (merging them at once would wait for the
+  // loads just issued)
+  uint4 nu[NB][L], ng[NB][L], nh0[NB], ni0[NB], nw0[LB ? NB : 1];
+  LogitRaw<TIO, GM, L + 1> nl[NB];
   auto load_tile = [&](int it, auto bufc) {
     constexpr int buf = decltype(bufc)::value;
     const int Tt = t_base + it * TW;
@@ -864,27 +890,21 @@ scan_bwd_kernel(const BwdArgs args) {
     const bool from_init = ok0 && t0 == t_base;
     const bool from_wst = LB && ok0 && !from_init && t0 - 1 < t_st;
     const bool from_h = ok0 && !from_init && !from_wst;
-    uint4 q = bld_vec<TIO, VEC>(make_rsrc(hbh + (int64_t)(Tt - 1) * hs[2] * E), hoff, hscb,
-                                nvalid, from_h);
-    const uint4 qi = bld_vec<TIO, VEC>(irs, ioff, iscb, nvalid, from_init);
-    q = make_uint4(q.x | qi.x, q.y | qi.y, q.z | qi.z, q.w | qi.w);
-    if (LB) {
-      const uint4 qw = bld_vec<TIO, VEC>(make_rsrc(wsbh + (int64_t)(Tt - 1 - t_base) * S.D * E),
-                                         woff, E, nvalid, from_wst);
-      q = make_uint4(q.x | qw.x, q.y | qw.y, q.z | qw.z, q.w | qw.w);
-    }
-    nh0[buf] = q;
+    nh0[buf] = bld_vec<TIO, VEC>(make_rsrc(hbh + (int64_t)(Tt - 1) * hs[2] * E), hoff, hscb,
+                                 nvalid, from_h);
+    ni0[buf] = bld_vec<TIO, VEC>(irs, ioff, iscb, nvalid, from_init);
+    if constexpr (LB)
+      nw0[buf] = bld_vec<TIO, VEC>(make_rsrc(wsbh + (int64_t)(Tt - 1 - t_base) * S.D * E), woff,
+                                   E, nvalid, from_wst);
     nl[buf].load(make_rsrc(lbh + (int64_t)Tt * args.lg.s[2] * E), loff, lstb, gi, t0, t_hi,
                  tile_ok, nvalid);
   };
 
-  // GATE_LANE dlogit pass: thread item k covers (step tl, group jt) with
-  // idx = threadIdx.x + k NT = tl MAXG + jt; NT is a multiple of MAXG, so jt
-  // is fixed per thread
-  constexpr int NI = GL ? (TW * MAXG + NT - 1) / NT : 1;
-  const int jt = threadIdx.x % MAXG;
-  const bool jt_ok = jt < S.Da;
-  const int jtc = jt_ok ? jt : 0;
+  // GATE_LANE: this lane's gate group j = cl / gl_lanes spans channel lanes
+  // [seg0, seg0 + gl_lanes); its last lane emits the group's dlogits
+  const int gj = GL ? cl / gl_lanes : 0;
+  const int seg0 = gj * gl_lanes;
+  const bool glead = GL && active && cl == seg0 + gl_lanes - 1;
   float dinit_v[V];  // (1 - alpha) g at each tile's first lane step; the last tile's is kept
 #pragma unroll
   for (int v = 0; v < V; ++v) dinit_v[v] = 0.0f;
@@ -900,10 +920,19 @@ scan_bwd_kernel(const BwdArgs args) {
       uq[s] = nu[buf][s];
       gq[s] = ng[buf][s];
     }
-    hq[0] = nh0[buf];
+    {
+      uint4 q = nh0[buf];
+      const uint4 qi = ni0[buf];
+      q = make_uint4(q.x | qi.x, q.y | qi.y, q.z | qi.z, q.w | qi.w);
+      if constexpr (LB) {
+        const uint4 qw = nw0[buf];
+        q = make_uint4(q.x | qw.x, q.y | qw.y, q.z | qw.z, q.w | qw.w);
+      }
+      hq[0] = q;
+    }
     float al[L + 1][NA];
     nl[buf].gates(gi, t0, t_hi, active, use_sig, al);
-    load_tile(it - PD, bufc);
+    load_tile(it - PD, std::integral_constant<int, PD == 1 && NB == 2 ? 1 - buf : buf>{});
     // h_{t-1} of the lane's later steps (padded steps have alpha = 0)
 #pragma unroll
     for (int s = 1; s < L; ++s) {
@@ -1060,38 +1089,41 @@ scan_bwd_kernel(const BwdArgs args) {
     for (int v = 0; v < V; ++v) dinit_v[v] = (1.0f - al[0][GL ? 0 : v]) * gin[v];
 
     if (GL) {
-      // ---- dlogit[t, j] = slope * sum of the group's lane partials (fixed order)
+      // ---- dlogit[t, j] = slope_t * sum of the group's lane partials: a
+      // segmented inclusive scan over the group's channel lanes (TG lanes
+      // apart), in a fixed order, leaves the total in the group's last lane,
+      // whose own gate gives the slope
+      // (compile-time levels with masked adds: a loop or a branch around the
+      // shuffles makes the compiler drain every outstanding memory operation
+      // at the top of the tile loop)
 #pragma unroll
-      for (int s = 0; s < L; ++s) lds_p[tl0 + s][cl] = pl[s];
-      if (active && (cl % gl_lanes) == 0 && cl / gl_lanes < MAXG) {
+      for (int d = 1; d < CL; d <<= 1) {
+        const bool take = d < gl_lanes && cl - d >= seg0;
 #pragma unroll
         for (int s = 0; s < L; ++s) {
-          const float a = al[s][0];
-          lds_sl[tl0 + s][cl / gl_lanes] = use_sig ? a * (1.0f - a) : 1.0f;
+          const float q = __shfl_up(pl[s], d * TG, 64);
+          pl[s] += take ? q : 0.0f;
         }
       }
-      __syncthreads();  // (3)
 #pragma unroll
-      for (int k = 0; k < NI; ++k) {
-        const int tl = (threadIdx.x + k * NT) / MAXG;
-        const int tlc = tl < TW ? tl : TW - 1;
-        const int t = T0 + tl;
-        const bool ok = jt_ok && tl < TW && t < t_hi;
+      for (int s = 0; s < L; ++s) {
+        const int t = t0 + s;
+        const bool ok = glead && t < t_hi;
         const bool wu = LB && t < t_st;
-        float p = 0.0f;
-        for (int q = 0; q < gl_lanes; ++q) p += lds_p[tlc][jtc * gl_lanes + q];
-        const float d = p * lds_sl[tlc][jtc];
+        const float a = al[s][0];
+        const float d = pl[s] * (use_sig ? a * (1.0f - a) : 1.0f);
         dacc[0] += ok ? d : 0.0f;
-        bst1<TIO>(dlr, ok && !wu ? (uint32_t)tl * dlstb + (uint32_t)jt * dlscb : kOob, d);
-        if (LB) bst_b32(wdlr, ok && wu ? (uint32_t)tl * wdlstb + (uint32_t)jt * 4 : kOob, d);
+        const uint32_t srow = (uint32_t)(tl0 + s);
+        bst1<TIO>(dlr, ok && !wu ? srow * dlstb + (uint32_t)gj * dlscb : kOob, d);
+        if (LB) bst_b32(wdlr, ok && wu ? srow * wdlstb + (uint32_t)gj * 4 : kOob, d);
       }
     }
   };
   using B0 = std::integral_constant<int, 0>;
   using B1 = std::integral_constant<int, 1>;
   load_tile(it_hi, B0{});
-  if constexpr (PD == 2) {
-    load_tile(it_hi - 1, B1{});
+  if constexpr (NB == 2) {
+    if constexpr (PD == 2) load_tile(it_hi - 1, B1{});
     for (int it = it_hi; it >= it_lo; it -= 2) {
       process_tile(it, B0{});
       if (it - 1 >= it_lo) process_tile(it - 1, B1{});
@@ -1118,8 +1150,11 @@ scan_bwd_kernel(const BwdArgs args) {
   for (int j = threadIdx.x; j < S.Da; j += NT) {
     float acc = 0.0f;
     if (GL) {
-      // group j's dlogits were emitted by the threads q == j (mod MAXG)
-      for (int q = j; q < NT; q += MAXG) acc += lds_red[q][0];
+      // group j's dlogits were emitted by its last channel lane, in every
+      // time lane (w, tg) of the workgroup
+      const int lcl = (j + 1) * gl_lanes - 1;
+      for (int ww = 0; ww < NW; ++ww)
+        for (int q = 0; q < TG; ++q) acc += lds_red[ww * 64 + lcl * TG + q][0];
     } else {
       // group j is led by channel c = j r: lane cl = c / V, slot c % V, in every
       // time lane (w, tg) of the workgroup

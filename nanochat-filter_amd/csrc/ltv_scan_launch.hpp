@@ -106,7 +106,7 @@ bool bwd_dispatch(const BwdArgs& a, int grid, bool vec, int gm, bool lb, hipStre
   X(8, 8, 4) X(8, 2, 4) X(8, 4, 2) X(16, 8, 4) X(4, 8, 4)
 #define LTV_SCAN_BWD_CONFIGS(X)                                                        \
   X(1, 4, 4) X(2, 4, 4) X(4, 4, 4) X(8, 4, 4) X(16, 4, 4) X(32, 4, 4) X(64, 4, 4)      \
-  X(16, 8, 4) X(16, 4, 2) X(16, 2, 4) X(32, 8, 4) X(8, 8, 4)
+  X(16, 4, 2) X(16, 2, 4)
 
 template <typename TIO>
 int scan_fwd_launch_t(const FwdArgs& a, ScanCfg c, int grid, bool vec, int gm, hipStream_t st) {
