@@ -19,10 +19,11 @@ look-back configuration).  ``--workload gpt`` is BASELINE.json configs[3].
 
 Printed as one JSON line, with
   roofline     -- the dominant kernel's algorithmic bytes (or FLOPs) per launch
-                  over its average duration (HIP events on the launch stream
-                  across the timed steps, created without the system-scope
-                  fence so that recording them does not flush the caches),
-                  against MI355X's published peak;
+                  over its average duration (HIP events on the launch stream,
+                  created without the system-scope fence, recorded in a second
+                  pass of the same number of steps: a record still idles the
+                  GPU for several microseconds, so the timed steps run
+                  without them), against MI355X's published peak;
   kernels      -- the same figure for every kernel of the path;
   cpu_baseline -- the CPU oracle (oracle/ltv_oracle.py, a restatement of the
                   reference's sequential PyTorch path) timed on a bounded
@@ -217,13 +218,20 @@ def main():
         step()
     torch.cuda.synchronize()
 
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+
+    # per-kernel durations from a second pass of the same steps: recording an
+    # event leaves the GPU idle for several microseconds, so the timed steps
+    # above run without them
     with N.KernelRecorder() as rec:
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
         for _ in range(args.steps):
             step()
         torch.cuda.synchronize()
-        elapsed = time.perf_counter() - t0
 
     if args.calibrate_copy:
         src = torch.empty(COPY_CAL_BYTES, dtype=torch.uint8, device=dev)
@@ -321,12 +329,17 @@ def gpt_main(args):
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    # the filter's calls timed with HIP events in a second pass (an event record
+    # idles the GPU for several microseconds, so the timed steps run without)
     with N.KernelRecorder() as rec:
-        t0 = time.perf_counter()
         for _ in range(args.steps):
             step()
         torch.cuda.synchronize()
-        elapsed = time.perf_counter() - t0
     durs = rec.durations_ms()
     filter_ms = sum(sum(v) for v in durs.values()) / args.steps
     ms_per_step = elapsed * 1e3 / args.steps
