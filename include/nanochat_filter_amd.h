@@ -6,6 +6,8 @@
  * Conventions for every entry point:
  *   - All tensor arguments are raw device pointers plus element strides
  *     (int64, in elements of the tensor's own dtype).  Shapes are plain ints.
+ *     The scan entry points take any batch and head strides; their time and
+ *     channel strides must be non-negative (LTV_ERR_UNSUPPORTED otherwise).
  *   - `dtype` selects the I/O element type: LTV_DTYPE_F32 or LTV_DTYPE_BF16
  *     (bf16 as raw 16-bit patterns).  State and arithmetic are always fp32;
  *     `logit_bias` / `grad_logit_bias` are always fp32.

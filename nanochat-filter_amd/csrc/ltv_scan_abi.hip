@@ -194,7 +194,9 @@ struct ScanTuning {
   int fwd_cl = 0, fwd_l = 0, fwd_nw = 0;
   int bwd_l = 0, bwd_nw = 0;
   int bwd_chunks = 0;  // time chunks per (b, h) in the backward; 0 = automatic
+  bool lb_short = true;  // LTV_SCAN_LB_SHORT=0: look-back windows through the tile kernels
   ScanTuning() {
+    if (const char* e = getenv("LTV_SCAN_LB_SHORT")) lb_short = atoi(e) != 0;
     if (const char* e = getenv("LTV_SCAN_BWD_CHUNKS")) bwd_chunks = atoi(e) > 0 ? atoi(e) : 0;
     if (const char* e = getenv("LTV_SCAN_FWD_CFG")) {
       if (sscanf(e, "%d,%d,%d", &fwd_cl, &fwd_l, &fwd_nw) != 3) fwd_cl = fwd_l = fwd_nw = 0;
@@ -254,15 +256,16 @@ inline bool lb_short_ok(int V, int r, int Q, int K) {
 // kTileRowsMax time steps plus the channel extent.  Every such offset stays
 // below 2^31 when this holds.
 constexpr int64_t kTileRowsMax = 1024 + 2;  // the largest built tile, the step before, one spare
+// The offsets are unsigned: time and channel strides must be non-negative.
 inline bool tile_offsets_fit(const int64_t* s, int64_t chan_extent, int esize) {
-  const int64_t st = s[2] < 0 ? -s[2] : s[2], sc = s[3] < 0 ? -s[3] : s[3];
-  return (kTileRowsMax * st + chan_extent * sc) * esize + 64 < (1ll << 31);
+  return s[2] >= 0 && s[3] >= 0 &&
+         (kTileRowsMax * s[2] + chan_extent * s[3]) * esize + 64 < (1ll << 31);
 }
 
 int check_tile_offsets(const char* what, const int64_t* s, int64_t chan_extent, int esize) {
   LTV_REQUIRE(tile_offsets_fit(s, chan_extent, esize), LTV_ERR_UNSUPPORTED,
-              "%s: time stride %lld / channel stride %lld too large for the scan's 32-bit tile "
-              "offsets", what, (long long)s[2], (long long)s[3]);
+              "%s: time stride %lld / channel stride %lld negative or too large for the scan's "
+              "32-bit tile offsets", what, (long long)s[2], (long long)s[3]);
   return LTV_OK;
 }
 
@@ -275,6 +278,14 @@ int check_tile_offsets(const char* what, const int64_t* s, int64_t chan_extent, 
 inline ScanCfg bwd_default_cfg(int cl, bool vec) {
   return vec && cl == 16 ? ScanCfg{16, 4, 2} : ScanCfg{cl, 4, 4};
 }
+
+// Bytes from a view's first to its last element, (B, NX, T, X) elements
+// (non-negative strides, checked by check_tile_offsets).
+inline int64_t view_span_bytes(const int64_t* s, int B, int NX, int T, int X, int esize) {
+  auto ext = [](int n, int64_t st) { return n > 0 ? (int64_t)(n - 1) * st : 0; };
+  return (ext(B, s[0]) + ext(NX, s[1]) + ext(T, s[2]) + ext(X, s[3]) + 1) * esize;
+}
+constexpr int64_t kBufSpanMax = (1ll << 31) - 64;
 
 int check_pqk(int P, int Q, int K) {
   LTV_REQUIRE(P >= 0 && Q >= 1 && K >= 1, LTV_ERR_INVALID_ARG,
@@ -338,7 +349,8 @@ int scan_forward_impl(int dtype, const HostView4& u, const HostView4& lg, const 
   a.wst = nullptr;
   a.kw = 0;
   const int E = dtype == LTV_DTYPE_BF16 ? 2 : 4;
-  if ((rc = check_tile_offsets("values", u.s, D, E)) || (rc = check_tile_offsets("logits", lg.s, D, E)))
+  if ((rc = check_tile_offsets("values", u.s, D, E)) || (rc = check_tile_offsets("logits", lg.s, D, E)) ||
+      (rc = check_tile_offsets("inits", init.s, D, E)))
     return rc;
   bool vec = (D % V == 0) && vec_ok(u.p, u.s, 3, V) && vec_ok(init.p, init.s, 3, V);
   for (int i = 0; i < 3; ++i) {
@@ -351,13 +363,20 @@ int scan_forward_impl(int dtype, const HostView4& u, const HostView4& lg, const 
       vec = vec && vec_ok(outp[i], outs[i], 3, V);
     }
   }
-  if (a.nwin > 1 && lb_short_ok(V, r, Q, K)) {
+  if (a.nwin > 1 && (tuning().lb_short && lb_short_ok(V, r, Q, K))) {
     a.sh = ScanShape{B, T, NH, NKVH, Da, r, D, H, 1, use_sigmoid};
     a.lanes = next_pow2((D + V - 1) / V);
     int gm = GATE_CHAN;
     if (r % V == 0) gm = GATE_LANE;
     else if (vec && chanvec_ok(r, D, V, lg)) gm = GATE_CHANVEC;
-    return scan_launch_lb_short_fwd(dtype == LTV_DTYPE_BF16, a, vec, gm, st);
+    // the buffer-addressed kernels take 32-bit offsets within each view's
+    // (b, h) slice
+    bool buf = view_span_bytes(u.s, 1, 1, T, D, E) <= kBufSpanMax &&
+               view_span_bytes(lg.s, 1, 1, T, std::max(D, Da), E) <= kBufSpanMax;
+    for (int i = 0; i < 3; ++i)
+      if ((i == 0 ? NH : NKVH) > 0)
+        buf = buf && view_span_bytes(outs[i], 1, 1, T, D, E) <= kBufSpanMax;
+    return scan_launch_lb_short_fwd(dtype == LTV_DTYPE_BF16, a, vec, gm, buf, st);
   }
   return launch_forward(dtype, a, vec, lg, B, T, NH, NKVH, Da, r, use_sigmoid, st);
 }
@@ -399,7 +418,7 @@ BwdWorkspace bwd_workspace_plan(int dtype, int B, int T, int NH, int NKVH, int D
   auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
   BwdWorkspace w;
   const int nwin = look_back_nwin(T, P, Q);
-  if (nwin > 1 && lb_short_ok(V, r, Q, K)) {
+  if (nwin > 1 && (tuning().lb_short && lb_short_ok(V, r, Q, K))) {
     // short windows: dbias partials and per-window grad_inits shares only
     const size_t rows = (size_t)B * H * nwin;
     size_t off = al(rows * Da * sizeof(float));
@@ -523,7 +542,7 @@ int scan_backward_impl(int dtype, const HostView4& u, const HostView4& lg, const
   if (gm == GATE_CHAN && vec && chanvec_ok(r, D, V, lg) && chanvec_ok(r, D, V, dlg))
     gm = GATE_CHANVEC;
   const int nwin = look_back_nwin(T, P, Q);
-  if (nwin > 1 && lb_short_ok(V, r, Q, K)) {
+  if (nwin > 1 && (tuning().lb_short && lb_short_ok(V, r, Q, K))) {
     // Short look-back windows: one lane per window gathers its steps' whole
     // gradient (ltv_scan_lb.hip); then the per-window grad_inits shares and
     // dbias partials are summed.
@@ -534,7 +553,15 @@ int scan_backward_impl(int dtype, const HostView4& u, const HostView4& lg, const
     int sgm = GATE_CHAN;
     if (r % V == 0) sgm = GATE_LANE;
     else if (vec && chanvec_ok(r, D, V, lg) && chanvec_ok(r, D, V, dlg)) sgm = GATE_CHANVEC;
-    rc = scan_launch_lb_short_bwd(bf16, a, vec, sgm, K - 1, st);
+    bool buf = view_span_bytes(u.s, 1, 1, T, D, E) <= kBufSpanMax &&
+               view_span_bytes(lg.s, 1, 1, T, std::max(D, Da), E) <= kBufSpanMax &&
+               view_span_bytes(du.s, 1, 1, T, D, E) <= kBufSpanMax &&
+               view_span_bytes(dlg.s, 1, 1, T, std::max(D, Da), E) <= kBufSpanMax;
+    for (int i = 0; i < 3; ++i)
+      if ((i == 0 ? NH : NKVH) > 0)
+        buf = buf && view_span_bytes(hs[i], 1, 1, T, D, E) <= kBufSpanMax &&
+              view_span_bytes(gs[i], 1, 1, T, D, E) <= kBufSpanMax;
+    rc = scan_launch_lb_short_bwd(bf16, a, vec, sgm, K - 1, buf, st);
     if (rc) return rc;
     rc = scan_launch_lb_dinit(bf16, a, st);
     if (rc) return rc;

@@ -473,12 +473,17 @@ struct LogitRaw {
   Raw one[GM == GATE_LANE ? NS : 1];
   uint4 vec[GM == GATE_LANE ? 1 : NS];
 
+  // (steps below Tlo read 0 too).  OPQ: an opaque step index per s, where the
+  // compiler would otherwise relate the bounds of consecutive steps and branch
+  // over the later loads (the look-back kernels' per-lane windows)
+  template <bool OPQ = false>
   __device__ __forceinline__ void load(Rsrc rs, uint32_t off0, uint32_t lstb,
                                            const GateIdx<GM, V>& gi, int t0, int T, bool active,
-                                           int nvalid) {
+                                           int nvalid, int Tlo = -2147483647 - 1) {
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
-      const bool ok = active && (t0 + s) < T;
+      const int ts = !OPQ || s == 0 ? t0 + s : (int)opaque((uint32_t)(t0 + s));
+      const bool ok = active && ts < T && ts >= Tlo;
       const uint32_t o = GM == GATE_CHAN ? opaque(off0 + s * lstb) : off0 + s * lstb;
       if (GM == GATE_LANE) {
         one[s] = (Raw)bld1<TIO>(rs, ok ? o + (uint32_t)(gi.off[0] * sizeof(TIO)) : kOob);
@@ -1464,8 +1469,10 @@ int scan_launch_lb_fold(bool bf16, const BwdArgs& a, hipStream_t st);
 int scan_launch_lb_dinit(bool bf16, const BwdArgs& a, hipStream_t st);
 // Short-window look-back kernels (ltv_scan_lb.hip): one lane per (b, h,
 // window, channel vector).  The backward also needs kw_max >= K - 1 (8 or 16).
-int scan_launch_lb_short_fwd(bool bf16, const FwdArgs& a, bool vec, int gm, hipStream_t st);
-int scan_launch_lb_short_bwd(bool bf16, const BwdArgs& a, bool vec, int gm, int kw_max,
+// buf: every view spans less than 2^31 bytes, so the buffer-addressed kernels apply
+int scan_launch_lb_short_fwd(bool bf16, const FwdArgs& a, bool vec, int gm, bool buf,
+                             hipStream_t st);
+int scan_launch_lb_short_bwd(bool bf16, const BwdArgs& a, bool vec, int gm, int kw_max, bool buf,
                              hipStream_t st);
 // Backward for gate groups outside the main kernel's reduction patterns.
 int scan_launch_bwd_channel(bool bf16, const BwdArgs& a, float* dalpha_ws, hipStream_t st);

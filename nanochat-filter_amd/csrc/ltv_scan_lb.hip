@@ -83,6 +83,24 @@ __device__ __forceinline__ LaneMap lane_map(int lanes, int nwin) {
   return m;
 }
 
+// Lanes per (b, h) in the buffer-addressed kernels: nwin x lanes rounded up to
+// whole wavefronts, so that a wavefront never spans two (b, h) (lanes is a
+// power of two: below 64 it divides 64, and a window never straddles
+// wavefronts either); the padding lanes get win >= nwin.
+__host__ __device__ inline int64_t lanes_per_bh(int lanes, int nwin) {
+  return ((int64_t)nwin * lanes + 63) / 64 * 64;
+}
+__device__ __forceinline__ LaneMap lane_map_bh(int lanes, int nwin) {
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t per = lanes_per_bh(lanes, nwin);
+  const int64_t rest = gid % per;
+  LaneMap m;
+  m.bh = gid / per;
+  m.win = (int)(rest / lanes);
+  m.cv = (int)(rest % lanes);
+  return m;
+}
+
 // ---------------------------------------------------------------------------
 // Forward
 // ---------------------------------------------------------------------------
@@ -444,49 +462,551 @@ __global__ void __launch_bounds__(256) scan_lb_short_bwd_kernel(const BwdArgs ar
   }
 }
 
-template <typename TIO, int GM, bool VEC>
-void launch_fwd(const FwdArgs& a, int grid, hipStream_t st) {
-  hipLaunchKernelGGL((scan_lb_short_fwd_kernel<TIO, GM, VEC>), dim3(grid), dim3(256), 0, st, a);
+// ---------------------------------------------------------------------------
+// Buffer-addressed versions (used when every view spans less than 2^31 bytes):
+// each access is a buffer instruction on the tensor's base with a 32-bit lane
+// offset, masked lanes pass kOob, the steps are branch-free (a masked step
+// leaves the carried state unchanged) and the step loops run a wave-uniform
+// number of batches with the next batch's loads in flight.  With loads and
+// stores under branches, or loops with per-lane trip counts, the compiler waits
+// for every outstanding memory operation at each use: these kernels spent
+// three quarters of their time waiting.
+// ---------------------------------------------------------------------------
+
+// Buffer resource over a view's (b, h) slice (wave-uniform: the launcher uses
+// these kernels only when every wavefront lies in one (b, h)), and a lane's
+// byte offset of channel c at t = 0 in it.
+template <class VW>
+__device__ __forceinline__ Rsrc slice_rsrc(const VW& v, int b, int h, int esize) {
+  return make_rsrc(reinterpret_cast<const char*>(v.p) +
+                   ((int64_t)b * v.s[0] + (int64_t)h * v.s[1]) * esize);
+}
+template <class VW>
+__device__ __forceinline__ uint32_t chan_off(const VW& v, int c, int esize) {
+  return (uint32_t)((int64_t)c * v.s[3] * esize);
+}
+
+// f(integral_constant<int, I>) for I = I0 .. N - 1
+template <int I, int N, class F>
+__device__ __forceinline__ void static_loop(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    static_loop<I + 1, N>(f);
+  }
+}
+
+// maximum over the wavefront (every lane active)
+__device__ __forceinline__ int wave_max(int x) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) x = max(x, __shfl_xor(x, m, 64));
+  return __builtin_amdgcn_readfirstlane(x);
+}
+
+// sum over aligned groups of gl adjacent lanes (gl a power of two <= 64), with
+// fixed levels and masked adds (no loop or branch around the shuffles)
+__device__ __forceinline__ float group_sum_fixed(float x, int gl) {
+#pragma unroll
+  for (int m = 1; m < 64; m <<= 1) {
+    const float y = __shfl_xor(x, m, 64);
+    x += m < gl ? y : 0.0f;
+  }
+  return x;
 }
 
 template <typename TIO, int GM, bool VEC>
-void launch_bwd(const BwdArgs& a, int grid, int kw_max, hipStream_t st) {
-  if (kw_max <= 8)
-    hipLaunchKernelGGL((scan_lb_short_bwd_kernel<TIO, GM, VEC, 8>), dim3(grid), dim3(256), 0, st, a);
+__global__ void __launch_bounds__(256) scan_lb_buf_fwd_kernel(const FwdArgs args) {
+  constexpr int V = Pack<TIO>::V;
+  constexpr int NA = GM == GATE_LANE ? 1 : V;
+  constexpr bool GL = GM == GATE_LANE;
+  constexpr int NB = fwd_batch<GM>();
+  constexpr int E = sizeof(TIO);
+  const ScanShape& S = args.sh;
+  const LaneMap m = lane_map_bh(args.lanes, args.nwin);
+  const int bhu = __builtin_amdgcn_readfirstlane(
+      (int)(m.bh < (int64_t)S.B * S.H ? m.bh : (int64_t)S.B * S.H));
+  const bool in_grid = bhu < S.B * S.H;
+  const int bhc = in_grid ? bhu : 0;
+  const int h = bhc % S.H, b = bhc / S.H;
+  const int c0 = m.cv * V;
+  const int nvalid = min(V, S.D - c0);
+  const bool active = in_grid && m.win < args.nwin && nvalid > 0;
+  const Window wd = look_back_window(m.win, S.T, args.P, args.Q, args.K);
+  const int nbatch = (wave_max(active ? wd.hi - wd.lo : 0) + NB - 1) / NB;
+
+  int which, hl;
+  head_select(h, S.NH, S.NKVH, which, hl);
+  const HeadView ov = head_view(args.out, which);
+  const Rsrc ur = slice_rsrc(args.u, b, h, E), lr = slice_rsrc(args.lg, b, h, E),
+             orr = slice_rsrc(ov, b, hl, E);
+  const uint32_t ustb = (uint32_t)(args.u.s[2] * E), uscb = (uint32_t)(args.u.s[3] * E);
+  const uint32_t lstb = (uint32_t)(args.lg.s[2] * E);
+  const uint32_t ostb = (uint32_t)(ov.s[2] * E), oscb = (uint32_t)(ov.s[3] * E);
+  const uint32_t ub = chan_off(args.u, c0, E);
+  const uint32_t lb = GM == GATE_CHANVEC ? chan_off(args.lg, c0, E) : 0u;
+  const uint32_t ob = chan_off(ov, c0, E);
+  GateIdx<GM, V> gi;
+  gi.init(args.bias + h * S.Da, c0, nvalid, S.D, S.r, args.lg.s[3]);
+  const bool use_sig = S.use_sigmoid != 0;
+
+  float hv[V];
+  {
+    const uint4 q = bld_vec<TIO, VEC>(slice_rsrc(args.init, b, h, E), chan_off(args.init, c0, E),
+                                      (uint32_t)(args.init.s[3] * E), nvalid, active);
+#pragma unroll
+    for (int v = 0; v < V; ++v) hv[v] = Pack<TIO>::get(q, v);
+  }
+  uint4 nu[2][NB];
+  LogitRaw<TIO, GM, NB> nl[2];
+  auto load = [&](int k, auto bufc) __attribute__((always_inline)) {
+    constexpr int buf = decltype(bufc)::value;
+    const int t0 = wd.lo + k * NB;
+#pragma unroll
+    for (int s = 0; s < NB; ++s)
+      nu[buf][s] = bld_vec<TIO, VEC>(ur, ub + (uint32_t)(t0 + s) * ustb, uscb, nvalid,
+                                     active && t0 + s < wd.hi);
+    nl[buf].template load<true>(lr, lb + (uint32_t)t0 * lstb, lstb, gi, t0, wd.hi, active, nvalid);
+  };
+  auto process = [&](int k, auto bufc) __attribute__((always_inline)) {
+    constexpr int buf = decltype(bufc)::value;
+    const int t0 = wd.lo + k * NB;
+    uint4 uq[NB];
+#pragma unroll
+    for (int s = 0; s < NB; ++s) uq[s] = nu[buf][s];
+    float al[NB][NA];
+    nl[buf].gates(gi, t0, wd.hi, active, use_sig, al);  // 0 (the identity) when masked
+    load(k + 1, std::integral_constant<int, 1 - buf>{});
+#pragma unroll
+    for (int s = 0; s < NB; ++s) {
+      const int t = t0 + s;
+#pragma unroll
+      for (int v = 0; v < V; ++v)
+        hv[v] = fmaf(al[s][GL ? 0 : v], Pack<TIO>::get(uq[s], v) - hv[v], hv[v]);
+      bst_vec<TIO, VEC>(orr, ob + (uint32_t)t * ostb, oscb, nvalid,
+                        active && t >= wd.st && t < wd.hi, hv);
+    }
+  };
+  using B0 = std::integral_constant<int, 0>;
+  using B1 = std::integral_constant<int, 1>;
+  load(0, B0{});
+  for (int k = 0; k < nbatch; k += 2) {
+    process(k, B0{});
+    if (k + 1 < nbatch) process(k + 1, B1{});
+  }
+}
+
+template <typename TIO, int GM, bool VEC, int KW>
+__global__ void __launch_bounds__(256) scan_lb_buf_bwd_kernel(const BwdArgs args) {
+  constexpr int V = Pack<TIO>::V;
+  constexpr int NA = GM == GATE_LANE ? 1 : V;
+  constexpr bool GL = GM == GATE_LANE;
+  constexpr int NB = bwd_batch<GM>();
+  constexpr int E = sizeof(TIO);
+  static_assert(KW % NB == 0, "warm-up rows in whole batches");
+  using B0 = std::integral_constant<int, 0>;
+  using B1 = std::integral_constant<int, 1>;
+  const ScanShape& S = args.sh;
+  const int nwin = args.nchunk;
+  const LaneMap m = lane_map_bh(args.lanes, nwin);
+  const int bhu = __builtin_amdgcn_readfirstlane(
+      (int)(m.bh < (int64_t)S.B * S.H ? m.bh : (int64_t)S.B * S.H));
+  const bool in_grid = bhu < S.B * S.H;
+  const int bhc = in_grid ? bhu : 0;
+  const int h = bhc % S.H, b = bhc / S.H;
+  const int c0 = m.cv * V;
+  const int nvalid = min(V, S.D - c0);
+  const bool active = in_grid && m.win < nwin && nvalid > 0;
+  const int gl = GL ? S.r / V : 1;  // lanes per gate group (GATE_LANE)
+
+  const Window wd = look_back_window(m.win, S.T, args.P, args.Q, args.K);
+  const bool has_next = m.win + 1 < nwin;
+  // the last window has an empty successor at wd.hi; selected without a branch
+  // and kept opaque, so the compiler does not specialise the loads on it
+  Window wn;
+  {
+    const Window wr = look_back_window(m.win + 1, S.T, args.P, args.Q, args.K);
+    wn.lo = (int)opaque((uint32_t)(has_next ? wr.lo : wd.hi));
+    wn.st = (int)opaque((uint32_t)(has_next ? wr.st : wd.hi));
+    wn.hi = (int)opaque((uint32_t)(has_next ? wr.hi : wd.hi));
+  }
+  const int nt = wn.st - wn.lo;  // tail steps of this window read by the next (<= KW)
+  const int b2_hi = has_next ? wn.lo : wd.hi;
+  // wave-uniform batch counts of the runtime-length phases
+  const int nb_g = (wave_max(active ? wn.hi - wn.st : 0) + NB - 1) / NB;
+  const int nb_b2 = (wave_max(active ? b2_hi - wd.st : 0) + NB - 1) / NB;
+
+  int which, hl;
+  head_select(h, S.NH, S.NKVH, which, hl);
+  const HeadView hvw = head_view(args.h, which), gvw = head_view(args.gy, which);
+  const Rsrc ur = slice_rsrc(args.u, b, h, E), lr = slice_rsrc(args.lg, b, h, E),
+             hr = slice_rsrc(hvw, b, hl, E), gr = slice_rsrc(gvw, b, hl, E),
+             dur = slice_rsrc(args.du, b, h, E), dlr = slice_rsrc(args.dlg, b, h, E);
+  const uint32_t ustb = (uint32_t)(args.u.s[2] * E), uscb = (uint32_t)(args.u.s[3] * E);
+  const uint32_t lstb = (uint32_t)(args.lg.s[2] * E);
+  const uint32_t hstb = (uint32_t)(hvw.s[2] * E), hscb = (uint32_t)(hvw.s[3] * E);
+  const uint32_t gstb = (uint32_t)(gvw.s[2] * E), gscb = (uint32_t)(gvw.s[3] * E);
+  const uint32_t dustb = (uint32_t)(args.du.s[2] * E), duscb = (uint32_t)(args.du.s[3] * E);
+  const uint32_t dlstb = (uint32_t)(args.dlg.s[2] * E), dlscb = (uint32_t)(args.dlg.s[3] * E);
+  const uint32_t ub = chan_off(args.u, c0, E);
+  const uint32_t lb = GM == GATE_CHANVEC ? chan_off(args.lg, c0, E) : 0u;
+  const uint32_t hb = chan_off(hvw, c0, E), gb = chan_off(gvw, c0, E);
+  const uint32_t dub = chan_off(args.du, c0, E);
+  const uint32_t dlb = 0u;
+  GateIdx<GM, V> gi;
+  gi.init(args.bias + h * S.Da, c0, nvalid, S.D, S.r, args.lg.s[3]);
+  const bool use_sig = S.use_sigmoid != 0;
+
+  float ini[V];
+  {
+    const uint4 q = bld_vec<TIO, VEC>(slice_rsrc(args.init, b, h, E), chan_off(args.init, c0, E),
+                                      (uint32_t)(args.init.s[3] * E), nvalid, active);
+#pragma unroll
+    for (int v = 0; v < V; ++v) ini[v] = Pack<TIO>::get(q, v);
+  }
+
+  // ---- (A1) own warm-up [lo, st) (at most KW steps): the state entering st
+  // and prod (1 - alpha); (A2) the next window's warm-up states: HN[s] enters
+  // step wn.lo + s.  Batches of NB steps, the next batch's loads in flight.
+  float h1[V], prodw[NA];
+#pragma unroll
+  for (int v = 0; v < V; ++v) h1[v] = ini[v];
+#pragma unroll
+  for (int i = 0; i < NA; ++i) prodw[i] = 1.0f;
+  uint4 HN[KW];
+  {
+    float hn[V];
+#pragma unroll
+    for (int v = 0; v < V; ++v) hn[v] = ini[v];
+    // the two warm-ups as one sequence of 2 KW / NB batches: batches [0, KW / NB)
+    // walk [lo, lo + KW), the rest [wn.lo, wn.lo + KW)
+    constexpr int NBW = KW / NB;
+    uint4 wu[2][NB];
+    LogitRaw<TIO, GM, NB> wl[2];
+    auto wload = [&](int k, auto bufc) __attribute__((always_inline)) {
+      constexpr int buf = decltype(bufc)::value;
+      const bool own = k < NBW;
+      const int t0 = own ? wd.lo + k * NB : wn.lo + (k - NBW) * NB;
+      const int tend = own ? wd.st : wn.st;
+#pragma unroll
+      for (int s = 0; s < NB; ++s)
+        wu[buf][s] = bld_vec<TIO, VEC>(ur, ub + (uint32_t)(t0 + s) * ustb, uscb, nvalid,
+                                       active && k < 2 * NBW && t0 + s < tend);
+      wl[buf].template load<true>(lr, lb + (uint32_t)t0 * lstb, lstb, gi, t0, tend, active && k < 2 * NBW, nvalid);
+    };
+    auto wstep = [&](auto kc) __attribute__((always_inline)) {
+      constexpr int k = decltype(kc)::value;
+      constexpr int buf = k & 1;
+      constexpr bool own = k < NBW;
+      const int t0 = own ? wd.lo + k * NB : wn.lo + (k - NBW) * NB;
+      const int tend = own ? wd.st : wn.st;
+      uint4 uq[NB];
+#pragma unroll
+      for (int s = 0; s < NB; ++s) uq[s] = wu[buf][s];
+      float al[NB][NA];
+      wl[buf].gates(gi, t0, tend, active, use_sig, al);  // 0 when masked: the identity step
+      wload(k + 1, std::integral_constant<int, 1 - buf>{});
+#pragma unroll
+      for (int s = 0; s < NB; ++s) {
+        if constexpr (own) {
+#pragma unroll
+          for (int v = 0; v < V; ++v)
+            h1[v] = fmaf(al[s][GL ? 0 : v], Pack<TIO>::get(uq[s], v) - h1[v], h1[v]);
+#pragma unroll
+          for (int i = 0; i < NA; ++i) prodw[i] *= 1.0f - al[s][i];
+        } else {
+          HN[(k - NBW) * NB + s] = Pack<TIO>::pack(hn);
+#pragma unroll
+          for (int v = 0; v < V; ++v)
+            hn[v] = fmaf(al[s][GL ? 0 : v], Pack<TIO>::get(uq[s], v) - hn[v], hn[v]);
+        }
+      }
+    };
+    wload(0, B0{});
+    static_loop<0, 2 * NBW>(wstep);
+  }
+  const uint4 h_st = Pack<TIO>::pack(h1);  // I/O-rounded, as the saved outputs
+
+  // ---- (G) the next window's own chain at its first step, and 1 - alpha there,
+  // walking [wn.st, wn.hi) in reverse; a_hi holds 1 - alpha_{t+1} (0 past the
+  // window's last step), masked steps leave both unchanged
+  float G[V], a_hi[NA];
+#pragma unroll
+  for (int v = 0; v < V; ++v) G[v] = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NA; ++i) a_hi[i] = 0.0f;
+  {
+    uint4 ng[2][NB];
+    LogitRaw<TIO, GM, NB> nl[2];
+    // batch k covers t = wn.hi - 1 - (k NB + j), j = 0..NB-1 (loads ascending in t)
+    auto gload = [&](int k, auto bufc) __attribute__((always_inline)) {
+      constexpr int buf = decltype(bufc)::value;
+      const int tl = wn.hi - (k + 1) * NB;  // lowest step of the batch
+#pragma unroll
+      for (int s = 0; s < NB; ++s)
+        ng[buf][s] = bld_vec<TIO, VEC>(gr, gb + (uint32_t)(tl + s) * gstb, gscb, nvalid,
+                                       active && k < nb_g && tl + s >= wn.st);
+      nl[buf].template load<true>(lr, lb + (uint32_t)tl * lstb, lstb, gi, tl, wn.hi,
+                   active && k < nb_g, nvalid, wn.st);
+    };
+    auto gstep = [&](int k, auto bufc) __attribute__((always_inline)) {
+      constexpr int buf = decltype(bufc)::value;
+      const int tl = wn.hi - (k + 1) * NB;
+      uint4 gq[NB];
+#pragma unroll
+      for (int s = 0; s < NB; ++s) gq[s] = ng[buf][s];
+      float al[NB][NA];
+      nl[buf].gates(gi, tl, wn.hi, active, use_sig, al);
+      gload(k + 1, std::integral_constant<int, 1 - buf>{});
+#pragma unroll
+      for (int s = NB - 1; s >= 0; --s) {
+        const bool ok = active && tl + s >= wn.st;
+#pragma unroll
+        for (int v = 0; v < V; ++v) {
+          const float gn = fmaf(a_hi[GL ? 0 : v], G[v], Pack<TIO>::get(gq[s], v));
+          G[v] = ok ? gn : G[v];
+        }
+#pragma unroll
+        for (int i = 0; i < NA; ++i) a_hi[i] = ok ? 1.0f - al[s][i] : a_hi[i];
+      }
+    };
+    gload(0, B0{});
+    for (int k = 0; k < nb_g; k += 2) {
+      gstep(k, B0{});
+      if (k + 1 < nb_g) gstep(k + 1, B1{});
+    }
+  }
+
+  // ---- (B) own steps in reverse: g1 (own chain) and g2 (next window's warm-up)
+  float g1[V], g2[V], an[NA];
+#pragma unroll
+  for (int v = 0; v < V; ++v) {
+    g1[v] = 0.0f;
+    g2[v] = G[v];
+  }
+#pragma unroll
+  for (int i = 0; i < NA; ++i) an[i] = a_hi[i];
+  float dacc[GL ? 1 : V];
+#pragma unroll
+  for (int k = 0; k < (GL ? 1 : V); ++k) dacc[k] = 0.0f;
+  const int gjl = GL ? c0 / S.r : 0;  // gate group of this lane (GATE_LANE)
+  const bool glead = GL && active && (m.cv % gl) == 0;
+
+  // one reverse step at t (branch-free; a masked step changes nothing); with_g2:
+  // t lies in the next window's warm-up, hn its state
+  auto step = [&](int t, bool ok, const uint4& gq, const uint4& uq, const uint4& hq,
+                  const float (&a)[NA], bool with_g2, const uint4& hn) {
+    float duv[V], dav[V];
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      const int ia = GL ? 0 : v;
+      const float g1n = fmaf(an[ia], g1[v], Pack<TIO>::get(gq, v));
+      const float g2n = with_g2 ? an[ia] * g2[v] : 0.0f;
+      g1[v] = ok ? g1n : g1[v];
+      g2[v] = ok ? g2n : g2[v];
+      const float u = Pack<TIO>::get(uq, v);
+      duv[v] = a[ia] * (g1n + g2n);
+      dav[v] = (u - Pack<TIO>::get(hq, v)) * g1n;
+      if (with_g2) dav[v] = fmaf(u - Pack<TIO>::get(hn, v), g2n, dav[v]);
+    }
+#pragma unroll
+    for (int i = 0; i < NA; ++i) an[i] = ok ? 1.0f - a[i] : an[i];
+    bst_vec<TIO, VEC>(dur, dub + (uint32_t)t * dustb, duscb, nvalid, ok, duv);
+    if (GL) {
+      float p = 0.0f;
+#pragma unroll
+      for (int v = 0; v < V; ++v) p += v < nvalid ? dav[v] : 0.0f;
+      p = group_sum_fixed(ok ? p : 0.0f, gl);
+      const float d = use_sig ? p * (a[0] * (1.0f - a[0])) : p;
+      const bool st = ok && glead;
+      dacc[0] += st ? d : 0.0f;
+      bst1<TIO>(dlr, st ? dlb + (uint32_t)t * dlstb + (uint32_t)gjl * dlscb : kOob, d);
+    } else {
+      // whole groups of r channels inside the lane (r | V)
+#pragma unroll
+      for (int mm = 1; mm < V; mm <<= 1) {
+        if (mm < S.r) {
+          float tsum[V];
+#pragma unroll
+          for (int v = 0; v < V; ++v) tsum[v] = dav[v] + dav[v ^ mm];
+#pragma unroll
+          for (int v = 0; v < V; ++v) dav[v] = tsum[v];
+        }
+      }
+      float dl[V];
+#pragma unroll
+      for (int v = 0; v < V; ++v) dl[v] = use_sig ? dav[v] * (a[v] * (1.0f - a[v])) : dav[v];
+      if (GM == GATE_CHANVEC) {
+        bst_vec<TIO, true>(dlr, dlb + (uint32_t)t * dlstb + (uint32_t)c0 * E, E, V, ok, dl);
+#pragma unroll
+        for (int v = 0; v < V; ++v) dacc[v] += ok ? dl[v] : 0.0f;
+      } else {
+#pragma unroll
+        for (int v = 0; v < V; ++v) {
+          const bool lead = ok && (v & (S.r - 1)) == 0 && v < nvalid;
+          dacc[v] += lead ? dl[v] : 0.0f;
+          bst1<TIO>(dlr, lead ? dlb + (uint32_t)t * dlstb +
+                                    (uint32_t)((c0 + v) / S.r) * dlscb
+                              : kOob,
+                    dl[v]);
+        }
+      }
+    }
+  };
+
+  // loads of one reverse step: gy, u, logits at t and the state entering t (the
+  // saved output of t - 1, or at st the recomputed warm-up end state)
+  uint4 bg[2][NB], bu[2][NB], bh[2][NB];
+  LogitRaw<TIO, GM, NB> bl[2];
+  auto bload = [&](int tlow, int tlim_lo, int tlim_hi, bool any, auto bufc) __attribute__((always_inline)) {
+    constexpr int buf = decltype(bufc)::value;
+#pragma unroll
+    for (int s = 0; s < NB; ++s) {
+      const int t = tlow + s;
+      const bool ok = active && any && t >= tlim_lo && t < tlim_hi;
+      bg[buf][s] = bld_vec<TIO, VEC>(gr, gb + (uint32_t)t * gstb, gscb, nvalid, ok);
+      bu[buf][s] = bld_vec<TIO, VEC>(ur, ub + (uint32_t)t * ustb, uscb, nvalid, ok);
+      bh[buf][s] = bld_vec<TIO, VEC>(hr, hb + (uint32_t)(t - 1) * hstb, hscb, nvalid,
+                                     ok && t != wd.st);
+    }
+    bl[buf].template load<true>(lr, lb + (uint32_t)tlow * lstb, lstb, gi, tlow, tlim_hi, active && any, nvalid,
+                 tlim_lo);
+  };
+
+  // (B1) the tail [wn.lo, wn.st), read by the next window: compile-time rows of
+  // HN, batches from the last
+  {
+    constexpr int NBW = KW / NB;
+    auto b1step = [&](int q, auto bufc) __attribute__((always_inline)) {  // q-th batch from the last: rows s0 .. s0 + NB - 1
+      constexpr int buf = decltype(bufc)::value;
+      const int s0 = KW - (q + 1) * NB;
+      const int tlow = wn.lo + s0;
+      uint4 gq[NB], uq[NB], hq[NB];
+#pragma unroll
+      for (int s = 0; s < NB; ++s) {
+        gq[s] = bg[buf][s];
+        uq[s] = bu[buf][s];
+        hq[s] = tlow + s == wd.st ? h_st : bh[buf][s];
+      }
+      float al[NB][NA];
+      bl[buf].gates(gi, tlow, wn.st, active, use_sig, al);
+      if (q + 1 < NBW)
+        bload(wn.lo + KW - (q + 2) * NB, wn.lo, wn.st, true, std::integral_constant<int, 1 - buf>{});
+      else  // the first batch of (B2)
+        bload(b2_hi - NB, wd.st, b2_hi, nb_b2 > 0, std::integral_constant<int, 1 - buf>{});
+#pragma unroll
+      for (int s = NB - 1; s >= 0; --s) {
+        const int t = tlow + s;
+        step(t, active && s0 + s < nt, gq[s], uq[s], hq[s], al[s], true, HN[s0 + s]);
+      }
+    };
+    bload(wn.lo + KW - NB, wn.lo, wn.st, true, B0{});
+    static_loop<0, NBW>([&](auto qc) __attribute__((always_inline)) {
+      constexpr int q = decltype(qc)::value;
+      b1step(q, std::integral_constant<int, q & 1>{});
+    });
+  }
+  // (B2) the rest [st, b2_hi) in reverse; its first batch was loaded into the
+  // buffer after the last (B1) batch
+  {
+    constexpr int NBW = KW / NB;
+    constexpr int first = NBW % 2;  // buffer holding the first (B2) batch
+    auto b2step = [&](int k, auto bufc) __attribute__((always_inline)) {
+      constexpr int buf = decltype(bufc)::value;
+      const int tlow = b2_hi - (k + 1) * NB;
+      uint4 gq[NB], uq[NB], hq[NB];
+#pragma unroll
+      for (int s = 0; s < NB; ++s) {
+        gq[s] = bg[buf][s];
+        uq[s] = bu[buf][s];
+        hq[s] = tlow + s == wd.st ? h_st : bh[buf][s];
+      }
+      float al[NB][NA];
+      bl[buf].gates(gi, tlow, b2_hi, active, use_sig, al);
+      bload(tlow - NB, wd.st, b2_hi, k + 1 < nb_b2, std::integral_constant<int, 1 - buf>{});
+#pragma unroll
+      for (int s = NB - 1; s >= 0; --s) {
+        const int t = tlow + s;
+        step(t, active && t >= wd.st && t < b2_hi, gq[s], uq[s], hq[s], al[s], false, h_st);
+      }
+    };
+    for (int k = 0; k < nb_b2; k += 2) {
+      b2step(k, std::integral_constant<int, first>{});
+      if (k + 1 < nb_b2) b2step(k + 1, std::integral_constant<int, 1 - first>{});
+    }
+  }
+
+  // ---- this window's share of grad_inits: prod_{j=lo}^{st} (1 - alpha_j) g1_st
+  // (an = 1 - alpha_st after the last step; an empty window leaves g1 = 0)
+  if (active) {
+    float di[V];
+#pragma unroll
+    for (int v = 0; v < V; ++v) di[v] = prodw[GL ? 0 : v] * an[GL ? 0 : v] * g1[v];
+    st_f32<VEC, V>(args.wdi + ((int64_t)bhc * nwin + m.win) * S.D + c0, nvalid, di);
+  }
+  // ---- dbias partial of (b, h, window)
+  float* pp = args.dbias_partial + ((int64_t)bhc * nwin + m.win) * S.Da;
+  if (GL) {
+    if (glead) pp[gjl] = dacc[0];
+  } else if (active) {
+#pragma unroll
+    for (int v = 0; v < V; ++v)
+      if ((GM == GATE_CHANVEC || (v & (S.r - 1)) == 0) && v < nvalid) pp[(c0 + v) / S.r] = dacc[v];
+  }
+}
+
+template <typename TIO, int GM, bool VEC>
+void launch_fwd(const FwdArgs& a, int grid, bool buf, hipStream_t st) {
+  if (buf)
+    hipLaunchKernelGGL((scan_lb_buf_fwd_kernel<TIO, GM, VEC>), dim3(grid), dim3(256), 0, st, a);
   else
+    hipLaunchKernelGGL((scan_lb_short_fwd_kernel<TIO, GM, VEC>), dim3(grid), dim3(256), 0, st, a);
+}
+
+template <typename TIO, int GM, bool VEC>
+void launch_bwd(const BwdArgs& a, int grid, int kw_max, bool buf, hipStream_t st) {
+  if (buf) {
+    if (kw_max <= 8)
+      hipLaunchKernelGGL((scan_lb_buf_bwd_kernel<TIO, GM, VEC, 8>), dim3(grid), dim3(256), 0, st, a);
+    else
+      hipLaunchKernelGGL((scan_lb_buf_bwd_kernel<TIO, GM, VEC, 16>), dim3(grid), dim3(256), 0, st, a);
+  } else if (kw_max <= 8) {
+    hipLaunchKernelGGL((scan_lb_short_bwd_kernel<TIO, GM, VEC, 8>), dim3(grid), dim3(256), 0, st, a);
+  } else {
     hipLaunchKernelGGL((scan_lb_short_bwd_kernel<TIO, GM, VEC, 16>), dim3(grid), dim3(256), 0, st, a);
+  }
 }
 
 template <typename TIO>
-int fwd_t(const FwdArgs& a, bool vec, int gm, hipStream_t st) {
-  const int64_t lanes = (int64_t)a.sh.B * a.sh.H * a.nwin * a.lanes;
+int fwd_t(const FwdArgs& a, bool vec, int gm, bool buf, hipStream_t st) {
+  const int64_t lanes =
+      (int64_t)a.sh.B * a.sh.H * (buf ? lanes_per_bh(a.lanes, a.nwin) : (int64_t)a.nwin * a.lanes);
   const int64_t grid = (lanes + 255) / 256;
   LTV_REQUIRE(grid < (1ll << 31), LTV_ERR_UNSUPPORTED, "grid too large");
   if (vec) {
-    if (gm == GATE_LANE) launch_fwd<TIO, GATE_LANE, true>(a, (int)grid, st);
-    else if (gm == GATE_CHANVEC) launch_fwd<TIO, GATE_CHANVEC, true>(a, (int)grid, st);
-    else launch_fwd<TIO, GATE_CHAN, true>(a, (int)grid, st);
+    if (gm == GATE_LANE) launch_fwd<TIO, GATE_LANE, true>(a, (int)grid, buf, st);
+    else if (gm == GATE_CHANVEC) launch_fwd<TIO, GATE_CHANVEC, true>(a, (int)grid, buf, st);
+    else launch_fwd<TIO, GATE_CHAN, true>(a, (int)grid, buf, st);
   } else {
-    if (gm == GATE_LANE) launch_fwd<TIO, GATE_LANE, false>(a, (int)grid, st);
-    else launch_fwd<TIO, GATE_CHAN, false>(a, (int)grid, st);
+    if (gm == GATE_LANE) launch_fwd<TIO, GATE_LANE, false>(a, (int)grid, buf, st);
+    else launch_fwd<TIO, GATE_CHAN, false>(a, (int)grid, buf, st);
   }
   LTV_LAUNCH_CHECK();
   return LTV_OK;
 }
 
 template <typename TIO>
-int bwd_t(const BwdArgs& a, bool vec, int gm, int kw_max, hipStream_t st) {
-  const int64_t lanes = (int64_t)a.sh.B * a.sh.H * a.nchunk * a.lanes;
+int bwd_t(const BwdArgs& a, bool vec, int gm, int kw_max, bool buf, hipStream_t st) {
+  const int64_t lanes = (int64_t)a.sh.B * a.sh.H *
+                        (buf ? lanes_per_bh(a.lanes, a.nchunk) : (int64_t)a.nchunk * a.lanes);
   const int64_t grid = (lanes + 255) / 256;
   LTV_REQUIRE(grid < (1ll << 31), LTV_ERR_UNSUPPORTED, "grid too large");
   LTV_REQUIRE(kw_max <= 16, LTV_ERR_UNSUPPORTED, "warm-up of %d steps too long", kw_max);
   if (vec) {
-    if (gm == GATE_LANE) launch_bwd<TIO, GATE_LANE, true>(a, (int)grid, kw_max, st);
-    else if (gm == GATE_CHANVEC) launch_bwd<TIO, GATE_CHANVEC, true>(a, (int)grid, kw_max, st);
-    else launch_bwd<TIO, GATE_CHAN, true>(a, (int)grid, kw_max, st);
+    if (gm == GATE_LANE) launch_bwd<TIO, GATE_LANE, true>(a, (int)grid, kw_max, buf, st);
+    else if (gm == GATE_CHANVEC) launch_bwd<TIO, GATE_CHANVEC, true>(a, (int)grid, kw_max, buf, st);
+    else launch_bwd<TIO, GATE_CHAN, true>(a, (int)grid, kw_max, buf, st);
   } else {
-    if (gm == GATE_LANE) launch_bwd<TIO, GATE_LANE, false>(a, (int)grid, kw_max, st);
-    else launch_bwd<TIO, GATE_CHAN, false>(a, (int)grid, kw_max, st);
+    if (gm == GATE_LANE) launch_bwd<TIO, GATE_LANE, false>(a, (int)grid, kw_max, buf, st);
+    else launch_bwd<TIO, GATE_CHAN, false>(a, (int)grid, kw_max, buf, st);
   }
   LTV_LAUNCH_CHECK();
   return LTV_OK;
@@ -494,13 +1014,15 @@ int bwd_t(const BwdArgs& a, bool vec, int gm, int kw_max, hipStream_t st) {
 
 }  // namespace
 
-int scan_launch_lb_short_fwd(bool bf16, const FwdArgs& a, bool vec, int gm, hipStream_t st) {
-  return bf16 ? fwd_t<bf16_t>(a, vec, gm, st) : fwd_t<float>(a, vec, gm, st);
+int scan_launch_lb_short_fwd(bool bf16, const FwdArgs& a, bool vec, int gm, bool buf,
+                             hipStream_t st) {
+  return bf16 ? fwd_t<bf16_t>(a, vec, gm, buf, st) : fwd_t<float>(a, vec, gm, buf, st);
 }
 
-int scan_launch_lb_short_bwd(bool bf16, const BwdArgs& a, bool vec, int gm, int kw_max,
+int scan_launch_lb_short_bwd(bool bf16, const BwdArgs& a, bool vec, int gm, int kw_max, bool buf,
                              hipStream_t st) {
-  return bf16 ? bwd_t<bf16_t>(a, vec, gm, kw_max, st) : bwd_t<float>(a, vec, gm, kw_max, st);
+  return bf16 ? bwd_t<bf16_t>(a, vec, gm, kw_max, buf, st)
+              : bwd_t<float>(a, vec, gm, kw_max, buf, st);
 }
 
 }  // namespace ltv

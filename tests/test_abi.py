@@ -87,6 +87,11 @@ def test_abi_version_and_host_only_queries():
     rc = lib.ltv_hm_look_back_scan_forward(1, p, cs, p, ins, bias, p, outs, p, outs, p, outs,
                                            B, T, NH, NKVH, Da, r, 2147483647, 1, 1, 1, None)
     assert rc == 2 and "32-bit tile offsets" in N.last_error(), N.last_error()
+    # so is a negative time stride (the offsets are unsigned)
+    back = (ctypes.c_int64 * 3)(T * 130, -130, 1)
+    rc = lib.ltv_hm_look_back_scan_forward(1, p, back, p, ins, bias, p, outs, p, outs, p, outs,
+                                           B, T, NH, NKVH, Da, r, 2147483647, 1, 1, 1, None)
+    assert rc == 2 and "negative" in N.last_error(), N.last_error()
 
 
 def test_ops_import_without_gpu():
