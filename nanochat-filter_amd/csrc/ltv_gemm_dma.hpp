@@ -34,7 +34,22 @@
 
 namespace ltv {
 
+// Reduction indices per k-step and LDS stages (kDmaStages - 1 k-steps in
+// flight).  Measured on MI355X at d12: 64 x 2 stages beats 32 x 4 stages
+// (forward GEMM 134 vs 148 us, dX 140 vs 166 us) -- twice the barriers and
+// half-line L2 requests cost more than the deeper pipeline gains.
 constexpr int kDmaBK = 64;
+constexpr int kDmaStages = 2;
+constexpr int kDmaRowBytes = kDmaBK * 2;          // a KC tile row
+constexpr int kDmaRowSlots = kDmaRowBytes / 16;   // 16-byte chunks per KC row
+constexpr int kDmaRowPhase = 256 / kDmaRowBytes;  // KC rows per 256-byte bank window
+static_assert(kDmaBK % 16 == 0 && kDmaRowPhase >= 1 && kDmaStages >= 2, "bad DMA step");
+
+// LDS slot of 16-byte chunk c in row r of a KC tile: any 16 consecutive rows
+// then cover 16 distinct 16-byte bank windows for one chunk index.
+__host__ __device__ constexpr int dma_kc_slot(int r, int c) {
+  return c ^ ((r / kDmaRowPhase) & (kDmaRowSlots - 1));
+}
 
 typedef int i32x4_t __attribute__((ext_vector_type(4)));
 
@@ -156,8 +171,8 @@ struct DmaOperand {
     for (int i = 0; i < kPerWave; ++i) {
       const int o = (wave * kPerWave + i) * 1024 + lane * 16;  // byte offset in the tile
       if (L == OP_KC) {
-        const int row = o >> 7, slot = (o >> 4) & 7;
-        const int c = slot ^ ((row >> 1) & 7);
+        const int row = o / kDmaRowBytes, slot = (o >> 4) % kDmaRowSlots;
+        const int c = dma_kc_slot(row, slot);  // the swizzle is an involution
         kk[i] = c * 8;
         base[i] = row0 + row < op.rows ? (uint32_t)((row0 + row) * (int64_t)op.ld + c * 8)
                                        : kDmaOob;
@@ -433,7 +448,7 @@ __device__ __forceinline__ bf16x8_t dma_read_frag(const bf16_t* stage, int row_b
     const int r = row_base + (lane & 31);
     const int c = 2 * ks + (lane >> 5);
     const u32x4_t q = *(__attribute__((address_space(3))) const u32x4_t*)(
-        base + r * 128 + ((c ^ ((r >> 1) & 7)) << 4));
+        base + r * kDmaRowBytes + (dma_kc_slot(r, c) << 4));
     return __builtin_bit_cast(bf16x8_t, q);
   } else {
     const int g = lane >> 4, s = lane & 15;
@@ -465,8 +480,10 @@ gemm_dma_kernel(const GemmArgs g, const Epi epi) {
   using OpP = DmaOperand<BI, PL, NW>;
   using OpQ = DmaOperand<BJ, QL, NW>;
 
-  __shared__ __attribute__((aligned(1024))) bf16_t lds_p[2][PB / 2];
-  __shared__ __attribute__((aligned(1024))) bf16_t lds_q[2][QB / 2];
+  constexpr int NST = kDmaStages;
+  constexpr int kLoads = OpP::kPerWave + OpQ::kPerWave;  // vm instructions per k-step
+  __shared__ __attribute__((aligned(1024))) bf16_t lds_p[NST][PB / 2];
+  __shared__ __attribute__((aligned(1024))) bf16_t lds_q[NST][QB / 2];
   __shared__ __attribute__((aligned(16))) char lds_epi[NW][kEpiStageBytes];
 
   const int lane = threadIdx.x & 63;
@@ -513,20 +530,41 @@ gemm_dma_kernel(const GemmArgs g, const Epi epi) {
   cc = lc;
   if (!cc.valid) return;
   const DmaEpi<Epi> de(epi, g);
-  issue(lc, 0);
-  advance(lc);
-  wait_vmcnt<0>();
+  // vmcnt bookkeeping over the last NST - 1 steps j (oldest first): st[] the
+  // store instructions of step j's epilogue, tot[] everything step j issued
+  // (the loads of step j + NST - 1, then those stores).  The prologue's loads of
+  // steps 0 .. NST - 2 count as issued in steps 1 - NST .. -1.
+  int st[NST - 1], tot[NST - 1];
+#pragma unroll
+  for (int i = 0; i < NST - 1; ++i) {
+    st[i] = 0;
+    tot[i] = 0;
+    if (lc.valid) {
+      issue(lc, i);
+      advance(lc);
+      tot[i] = kLoads;
+    }
+  }
+  // instructions younger than the loads of step k + 1, at the end of step k
+  auto younger = [&]() {
+    int n = st[0];
+#pragma unroll
+    for (int i = 1; i < NST - 1; ++i) n += tot[i];
+    return n;
+  };
+  wait_vmcnt_rt(younger());  // step 0 (nothing stored yet: st[0] = 0)
   __builtin_amdgcn_s_barrier();
   lds_fence();
 
   int stage = 0;
   while (cc.valid) {
-    // the other stage was last read in the previous step, which every
-    // wavefront has finished (barrier below): refill it with the next step
-    const bool refill = lc.valid;
-    if (refill) {
-      issue(lc, stage ^ 1);
+    // the stage of step k + NST - 1 was last read in step k - 1, which every
+    // wavefront has finished (barrier below): refill it
+    int loads = 0;
+    if (lc.valid) {
+      issue(lc, stage == 0 ? NST - 1 : stage - 1);
       advance(lc);
+      loads = kLoads;
     }
     // MFMAs of this step; the fragments of sub-step t + 1 are read during t
     const bf16_t* sp = &lds_p[stage][0];
@@ -554,6 +592,24 @@ gemm_dma_kernel(const GemmArgs g, const Epi epi) {
           acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fp[cur][a], fq[cur][b], acc[a][b],
                                                               0, 0, 0);
     });
+    // Schedule: the first sub-step's fragment reads, then in each sub-step the
+    // next one's reads spread between its MFMAs.  Left to itself the scheduler
+    // issues each read just before the MFMA that consumes it, and every MFMA
+    // group then waits for the LDS.
+    {
+      constexpr int RD = MI * (PL == OP_KC ? 1 : 2) + MJ * (QL == OP_KC ? 1 : 2);
+      constexpr int NM = MI * MJ;
+      __builtin_amdgcn_sched_group_barrier(0x100, RD, 0);
+      static_for<KS>([&](auto tc) {
+        constexpr int t = decltype(tc)::value;
+        static_for<NM>([&](auto ic) {
+          constexpr int i = decltype(ic)::value;
+          constexpr int n = t + 1 < KS ? RD / NM + (i < RD % NM ? 1 : 0) : 0;
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          if constexpr (n > 0) __builtin_amdgcn_sched_group_barrier(0x100, n, 0);
+        });
+      });
+    }
     int stores = 0;
     if (cc.kt == cc.nk - 1) {
       stores = de.template store_tile<MI, MJ>(acc, cc.i0 + wi_u * WI, cc.j0 + wj_u * WJ, cc.split,
@@ -566,11 +622,18 @@ gemm_dma_kernel(const GemmArgs g, const Epi epi) {
           for (int v = 0; v < 16; ++v) acc[a][b][v] = 0.0f;
     }
     advance(cc);
-    // the next step's loads have landed (only the stores above are younger)
-    if (refill) wait_vmcnt_rt(stores);
+#pragma unroll
+    for (int i = 0; i < NST - 2; ++i) {
+      st[i] = st[i + 1];
+      tot[i] = tot[i + 1];
+    }
+    st[NST - 2] = stores;
+    tot[NST - 2] = loads + stores;
+    // the next step's loads have landed
+    if (cc.valid) wait_vmcnt_rt(younger());
     __builtin_amdgcn_s_barrier();
     lds_fence();
-    stage ^= 1;
+    stage = stage == NST - 1 ? 0 : stage + 1;
   }
   wait_vmcnt<0>();
 }
