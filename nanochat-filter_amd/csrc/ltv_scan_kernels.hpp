@@ -380,11 +380,12 @@ __device__ __forceinline__ void reload_barrier(uint4 (&q)[N]) {
 // one 16-lane row and a DPP row shift is exact for every lane the caller keeps
 // (tg >= off, resp. tg + off < TG); wider segments go through ds_bpermute.
 // ---------------------------------------------------------------------------
+// Lanes without a source in the row read 0 (bound_ctrl): no old value to
+// materialise, and the move can fold into the instruction that consumes it.
 template <int TG, int OFF>
 __device__ __forceinline__ float shift_up(float x) {
   if constexpr (TG <= 16) {
-    return __int_as_float(
-        __builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x110 + OFF, 0xf, 0xf, false));
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x110 + OFF, 0xf, 0xf, true));
   } else {
     return __shfl_up(x, OFF, TG);
   }
@@ -393,8 +394,7 @@ __device__ __forceinline__ float shift_up(float x) {
 template <int TG, int OFF>
 __device__ __forceinline__ float shift_down(float x) {
   if constexpr (TG <= 16) {
-    return __int_as_float(
-        __builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x100 + OFF, 0xf, 0xf, false));
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x100 + OFF, 0xf, 0xf, true));
   } else {
     return __shfl_down(x, OFF, TG);
   }
