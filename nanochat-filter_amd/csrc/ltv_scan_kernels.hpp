@@ -304,6 +304,18 @@ __device__ __forceinline__ uint32_t opaque(uint32_t x) {
   return x;
 }
 
+// log2 of a power of two
+__host__ __device__ constexpr int ilog2(int n) { return n <= 1 ? 0 : 1 + ilog2(n / 2); }
+
+// f(integral_constant<int, I>) for I = I0 .. N - 1
+template <int I, int N, class F>
+__device__ __forceinline__ void static_loop(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    static_loop<I + 1, N>(f);
+  }
+}
+
 // One element as raw bits (bf16: the 16 bits; fp32: the word) and its store.
 template <typename TIO>
 __device__ __forceinline__ uint32_t bld1(Rsrc r, uint32_t off) {
@@ -1100,16 +1112,24 @@ scan_bwd_kernel(const BwdArgs args) {
       // whose own gate gives the slope
       // (compile-time levels with masked adds: a loop or a branch around the
       // shuffles makes the compiler drain every outstanding memory operation
-      // at the top of the tile loop)
-#pragma unroll
-      for (int d = 1; d < CL; d <<= 1) {
+      // at the top of the tile loop).  Shifts inside a 16-lane row are DPP
+      // moves: the lead lane ends a row (or a group within one), and so does
+      // every lane whose partial sum reaches it, so at each level these lanes
+      // read a source in their own row -- the same sums, in the same order,
+      // as the cross-lane shuffle, without the round trip through the LDS.
+      static_loop<0, ilog2(CL)>([&](auto lc) __attribute__((always_inline)) {
+        constexpr int d = 1 << decltype(lc)::value;
         const bool take = d < gl_lanes && cl - d >= seg0;
 #pragma unroll
         for (int s = 0; s < L; ++s) {
-          const float q = __shfl_up(pl[s], d * TG, 64);
+          float q;
+          if constexpr (d * TG < 16)
+            q = shift_up<16, d * TG>(pl[s]);
+          else
+            q = __shfl_up(pl[s], d * TG, 64);
           pl[s] += take ? q : 0.0f;
         }
-      }
+      });
 #pragma unroll
       for (int s = 0; s < L; ++s) {
         const int t = t0 + s;

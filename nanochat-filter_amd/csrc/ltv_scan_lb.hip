@@ -486,15 +486,6 @@ __device__ __forceinline__ uint32_t chan_off(const VW& v, int c, int esize) {
   return (uint32_t)((int64_t)c * v.s[3] * esize);
 }
 
-// f(integral_constant<int, I>) for I = I0 .. N - 1
-template <int I, int N, class F>
-__device__ __forceinline__ void static_loop(F&& f) {
-  if constexpr (I < N) {
-    f(std::integral_constant<int, I>{});
-    static_loop<I + 1, N>(f);
-  }
-}
-
 // maximum over the wavefront (every lane active)
 __device__ __forceinline__ int wave_max(int x) {
 #pragma unroll
