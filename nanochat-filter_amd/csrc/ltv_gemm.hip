@@ -50,6 +50,53 @@ __global__ void pack_weight_kernel(const TW* __restrict__ w, bf16_t* __restrict_
   }
 }
 
+// The same packing, 8 columns per thread (C % 8 == 0, 16-byte aligned
+// buffers, Fp * C < 2^31): 16-byte loads and stores, 32-bit index arithmetic,
+// the same rounding per element.
+template <typename TW>
+__global__ void __launch_bounds__(256)
+pack_weight8_kernel(const TW* __restrict__ w, bf16_t* __restrict__ wp, int H, int D, int Da, int C,
+                    int Fp) {
+  const int C8 = C / 8;
+  const int total = Fp * C8;
+  for (int i = blockIdx.x * 256 + threadIdx.x; i < total; i += gridDim.x * 256) {
+    const int fpk = i / C8, c = (i - fpk * C8) * 8;
+    int src = -1;  // parameter row of packed row fpk (-1: padding)
+    if (fpk < H * D) {
+      const int h = fpk / D;
+      src = h * (D + Da) + (fpk - h * D);
+    } else if (fpk < H * (D + Da)) {
+      const int q = fpk - H * D, h = q / Da;
+      src = h * (D + Da) + D + (q - h * Da);
+    }
+    float v[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) v[k] = 0.0f;
+    if (src >= 0) {
+      const TW* p = w + (int64_t)src * C + c;
+      if constexpr (sizeof(TW) == 4) {
+        const float4 a = reinterpret_cast<const float4*>(p)[0];
+        const float4 b = reinterpret_cast<const float4*>(p)[1];
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+        v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+      } else {
+        const uint4 q = *reinterpret_cast<const uint4*>(p);
+        const uint32_t u[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          v[2 * k] = __uint_as_float(u[k] << 16);
+          v[2 * k + 1] = __uint_as_float(u[k] & 0xffff0000u);
+        }
+      }
+    }
+    uint32_t o[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      o[k] = (uint32_t)f32_to_bf16_bits(v[2 * k]) | ((uint32_t)f32_to_bf16_bits(v[2 * k + 1]) << 16);
+    *reinterpret_cast<uint4*>(wp + (int64_t)i * 8) = make_uint4(o[0], o[1], o[2], o[3]);
+  }
+}
+
 // zero columns [c0, c1) of a row-major bf16 (rows, ld) buffer
 __global__ void zero_cols_kernel(bf16_t* __restrict__ p, int rows, int64_t ld, int c0, int c1) {
   const int w = c1 - c0;
@@ -390,6 +437,20 @@ extern "C" int ltv_qkv_pack_weight(int weight_dtype, const void* weight, void* w
   const int64_t total = (int64_t)Fp * C;
   const int blocks = (int)std::min<int64_t>((total + 255) / 256, 4096);
   hipStream_t st = (hipStream_t)stream;
+  if (C % 8 == 0 && (int64_t)Fp * C < (1ll << 31) && ((uintptr_t)weight & 15) == 0 &&
+      ((uintptr_t)wpack & 15) == 0) {
+    const int b8 = (int)std::min<int64_t>(((int64_t)Fp * C / 8 + 255) / 256, 8192);
+    if (weight_dtype == LTV_DTYPE_F32)
+      hipLaunchKernelGGL(pack_weight8_kernel<float>, dim3(b8), dim3(256), 0, st,
+                         reinterpret_cast<const float*>(weight), reinterpret_cast<bf16_t*>(wpack),
+                         H, D, Da, C, Fp);
+    else
+      hipLaunchKernelGGL(pack_weight8_kernel<bf16_t>, dim3(b8), dim3(256), 0, st,
+                         reinterpret_cast<const bf16_t*>(weight), reinterpret_cast<bf16_t*>(wpack),
+                         H, D, Da, C, Fp);
+    LTV_LAUNCH_CHECK();
+    return LTV_OK;
+  }
   if (weight_dtype == LTV_DTYPE_F32)
     hipLaunchKernelGGL(pack_weight_kernel<float>, dim3(blocks), dim3(256), 0, st,
                        reinterpret_cast<const float*>(weight), reinterpret_cast<bf16_t*>(wpack),
