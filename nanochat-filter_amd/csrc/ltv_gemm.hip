@@ -97,13 +97,17 @@ pack_weight8_kernel(const TW* __restrict__ w, bf16_t* __restrict__ wp, int H, in
   }
 }
 
-// zero columns [c0, c1) of a row-major bf16 (rows, ld) buffer
-__global__ void zero_cols_kernel(bf16_t* __restrict__ p, int rows, int64_t ld, int c0, int c1) {
-  const int w = c1 - c0;
-  const int64_t total = (int64_t)rows * w;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
-       i += (int64_t)gridDim.x * blockDim.x)
-    p[(i / w) * ld + c0 + (i % w)] = 0;
+// zero columns [c0, c1) of a row-major bf16 (rows, ld) buffer: one thread per
+// row, 4-byte stores where the row's strip is 4-byte aligned
+__global__ void __launch_bounds__(256)
+zero_cols_kernel(bf16_t* __restrict__ p, int rows, int64_t ld, int c0, int c1) {
+  const int r = blockIdx.x * 256 + threadIdx.x;
+  if (r >= rows) return;
+  bf16_t* q = p + (int64_t)r * ld;
+  int c = c0;
+  if (c < c1 && ((uintptr_t)(q + c) & 2)) q[c++] = 0;
+  for (; c + 2 <= c1; c += 2) *reinterpret_cast<uint32_t*>(q + c) = 0u;
+  if (c < c1) q[c] = 0;
 }
 
 // grad_weight[param row, c] = sum_s partial[s][packed row, c]  (fixed order)
@@ -560,8 +564,7 @@ extern "C" int ltv_qkv_project_backward_input(const void* x, const void* wpack,
     ad.Q.k_valid = Fv8;
     if (dma_usable(ad, OP_RC, OP_KC, e, 1)) {
       if (Fv8 > Fvalid) {
-        const int64_t total = (int64_t)M * (Fv8 - Fvalid);
-        const int blocks = (int)std::min<int64_t>((total + 255) / 256, 4096);
+        const int blocks = (M + 255) / 256;
         hipLaunchKernelGGL(zero_cols_kernel, dim3(blocks), dim3(256), 0, st,
                            reinterpret_cast<bf16_t*>(grad_combined), M,
                            (int64_t)Fp, Fvalid, Fv8);
