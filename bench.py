@@ -1,6 +1,7 @@
 """Benchmark of the LTV combined-QKV filter path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload filter|look_back|gpt]
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+                    [--workload filter|look_back|gpt|scan_fwd]
 
 Workload (the d12 training shape): x bf16
 [32, 1024, 768] ~ N(0, 1); c.weight [2322, 768] fp32 ~ N(0, 1/768) (value rows
@@ -16,6 +17,10 @@ in HBM before the timed region.  ``value`` = tokens / s = B*T*K / elapsed.
 with the d12 layer spec (P, Q, K) = (16, 16, 9): chunks of 16 steps, each
 restarted from the inits over an 8-step warm-up (the reference's production
 look-back configuration).  ``--workload gpt`` is BASELINE.json configs[3].
+``--workload scan_fwd`` is configs[1], the standalone scan forward: bf16 head-major
+values [32, 3 x 6, 1024, 128] ~ N(0, 1) with a per-element decay (r = 1)
+a = sigmoid(z), z ~ N(2, 1), i.e. logit + bias = -z; fp32 state, bf16 out; a
+step is one scan launch and ``value`` is its algorithmic GB/s.
 
 Printed as one JSON line, with
   roofline     -- the dominant kernel's algorithmic bytes (or FLOPs) per launch
@@ -144,12 +149,15 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--workload", choices=("filter", "look_back", "gpt"), default="filter",
+    ap.add_argument("--workload", choices=("filter", "look_back", "gpt", "scan_fwd"),
+                    default="filter",
                     help="filter: BASELINE.json configs[2] (the default, the metric's workload); "
                          "look_back: the same shapes through the look-back filter with the d12 "
                          "layer spec (16, 16, 9); "
                          "gpt: configs[3], one training step of the 12-layer d12 GPT with the "
-                         "filter in every layer (tokens/s and the filter's share of the step)")
+                         "filter in every layer (tokens/s and the filter's share of the step); "
+                         "scan_fwd: configs[1], the standalone per-element-decay scan forward "
+                         "(GB/s)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="after the timed region, run a plain device copy of 256 MiB five times "
                          "(the known-size reference for rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -162,6 +170,9 @@ def main():
 
     if args.workload == "gpt":
         gpt_main(args)
+        return
+    if args.workload == "scan_fwd":
+        scan_fwd_main(args)
         return
 
     import torch
@@ -297,6 +308,112 @@ def main():
         out["config"]["look_back_pqk"] = list(LOOK_BACK_PQK)
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(args.cpu_seconds, LOOK_BACK_PQK if look_back else None)
+    print(json.dumps(out), flush=True)
+
+
+# the standalone scan forward, per-element decay
+SF_B, SF_H, SF_T, SF_D = 32, 18, 1024, 128
+
+
+def scan_fwd_bytes():
+    """Algorithmic bytes of one configs[1] launch: read the values and the
+    per-element logits, write the outputs (bf16), read the inits (bf16) and the
+    fp32 bias (formula of the scan forward with Da = D, r = 1)."""
+    n = SF_B * SF_H * SF_T * SF_D
+    return 3 * n * S_IO + SF_B * SF_H * SF_D * S_IO + 4 * SF_H * SF_D
+
+
+def scan_fwd_cpu_baseline(seconds_target: float):
+    """The oracle's scan forward on one batch row of configs[1] (fp32 numpy)."""
+    import numpy as np
+    from threadpoolctl import threadpool_limits
+
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import ltv_oracle as O
+
+    cores = len(os.sched_getaffinity(0))
+    rng = np.random.default_rng(0)
+    u = rng.standard_normal((1, SF_T, SF_H, SF_D), dtype=np.float32)
+    z = (2.0 + rng.standard_normal((1, SF_T, SF_H, SF_D))).astype(np.float32)
+    comb = np.concatenate([u, -z], axis=-1).reshape(1, SF_T, -1)
+    ini = np.zeros((1, SF_H, SF_D), np.float32)
+    bias = np.zeros((SF_H, SF_D), np.float32)
+    reps = 0
+    t0 = time.perf_counter()
+    with threadpool_limits(limits=cores):
+        while True:
+            O.scan_forward(comb, ini, bias, 6, 6, SF_D, 1, True, "f32")
+            reps += 1
+            el = time.perf_counter() - t0
+            if el >= seconds_target:
+                break
+    per_row = scan_fwd_bytes() / SF_B
+    return {"value": round(per_row * reps / el / 1e9, 3), "unit": "GB/s", "cores": cores,
+            "kind": "port",
+            "sample": f"{reps} x the scan forward of 1 of the {SF_B} batch rows "
+                      f"(18 heads, T={SF_T}, D={SF_D}, r=1), fp32 numpy, {el:.1f} s"}
+
+
+def scan_fwd_main(args):
+    """one launch of the scan forward over bf16 head-major values
+    (B, 18, T, D) with head-major per-element logits (B, 18, T, D) = -z."""
+    import torch
+    from nanochat_amd import _native as N
+    from nanochat_amd.ops import ltv_hm_fast as hm
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(0)
+    shape = (SF_B, SF_H, SF_T, SF_D)
+    u = torch.randn(shape, generator=g, device=dev).to(torch.bfloat16)
+    logits = (-(2.0 + torch.randn(shape, generator=g, device=dev))).to(torch.bfloat16)
+    inits = torch.zeros((SF_B, SF_H, SF_D), dtype=torch.bfloat16, device=dev)
+    bias = torch.zeros((SF_H, SF_D), dtype=torch.float32, device=dev)
+
+    def step():
+        return hm.scan_forward(u, logits, inits, bias, 6, 6, SF_D, 1, True)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    with N.KernelRecorder() as rec:
+        for _ in range(args.steps):
+            step()
+        torch.cuda.synchronize()
+    ms = rec.durations_ms()["scan_fwd"]
+    avg_us = sum(ms) / len(ms) * 1e3
+    nbytes = scan_fwd_bytes()
+    ach = nbytes / (avg_us * 1e-6) / 1e9
+    traffic, traffic_src = profiled_traffic("scan_fwd", "scan_fwd_r1_traffic.json")
+    ms_per_step = elapsed * 1e3 / args.steps
+    out = {
+        "metric": "standalone EWMA scan forward HBM GB/s (%peak), bf16 [32,3,6,1024,128], "
+                  "per-element decay",
+        "value": round(nbytes * args.steps / elapsed / 1e9, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "configs[1]: standalone scan forward, per-element decay (r = 1)",
+                   "B": SF_B, "heads": SF_H, "T": SF_T, "D": SF_D, "r": 1,
+                   "parallelism": "single GPU"},
+        "roofline": {"kernel": "scan_fwd", "bound": "hbm", "achieved": round(ach, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4),
+                     "traffic": traffic, "traffic_source": traffic_src,
+                     "avg_us": round(avg_us, 2), "work_per_launch": nbytes},
+    }
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = scan_fwd_cpu_baseline(args.cpu_seconds)
     print(json.dumps(out), flush=True)
 
 

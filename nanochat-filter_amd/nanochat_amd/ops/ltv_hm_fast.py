@@ -187,6 +187,8 @@ def project_backward(x: torch.Tensor, wpack: torch.Tensor, grad_combined: torch.
 def scan_forward(values: torch.Tensor, logits: torch.Tensor, inits: torch.Tensor,
                  logit_bias: torch.Tensor, NH: int, NKVH: int, Da: int, r: int,
                  use_sigmoid: bool, P: int = UNBOUNDED_P, Q: int = 1, K: int = 1):
+    """values (B, H, T, D); logits (B, T, >= H Da) with column h Da + j, or
+    head-major (B, H, T, Da) -> out_q (B, NH, T, D), out_k, out_v (B, NKVH, T, D)."""
     N.require_device(values, logits, inits, logit_bias)
     B, H, T, D = values.shape
     if H != NH + 2 * NKVH or D != Da * r:
@@ -197,8 +199,13 @@ def scan_forward(values: torch.Tensor, logits: torch.Tensor, inits: torch.Tensor
         raise RuntimeError("logit_bias must be contiguous float32")
     out = [torch.empty((B, nh, T, D), dtype=values.dtype, device=values.device)
            for nh in (NH, NKVH, NKVH)]
-    sb, st_, sl = logits.stride()
-    lgs = (sb, Da * sl, st_, sl)
+    if logits.dim() == 4:  # head-major (B, H, T, Da)
+        if tuple(logits.shape) != (B, H, T, Da) or logits.dtype != values.dtype:
+            raise RuntimeError(f"head-major logits must be {(B, H, T, Da)} in the values' dtype")
+        lgs = logits.stride()
+    else:  # (B, T, >= H Da), column h Da + j
+        sb, st_, sl = logits.stride()
+        lgs = (sb, Da * sl, st_, sl)
     with N.span("scan_fwd"):
         rc = N.lib().ltv_hm_look_back_scan_forward_split(
             N.dtype_code(values.dtype),

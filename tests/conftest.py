@@ -28,3 +28,19 @@ def pytest_collection_modifyitems(config, items):
     for item in items:
         if "gpu" in item.keywords:
             item.add_marker(skip)
+
+
+def pytest_sessionfinish(session, exitstatus):
+    """With LTV_ERR_REPORT=<path>, write every assert_close's error statistics
+    (label, tolerance, max abs, normwise and element-wise relative error)."""
+    path = os.environ.get("LTV_ERR_REPORT")
+    if not path:
+        return
+    try:
+        from ltv_test_utils import ERR_LOG
+    except Exception:
+        return
+    import json
+    os.makedirs(os.path.dirname(os.path.abspath(path)), exist_ok=True)
+    with open(path, "w") as fh:
+        json.dump(ERR_LOG, fh, indent=0)

@@ -88,9 +88,34 @@ def io_name(dtype: torch.dtype) -> str:
 # tolerances: fp32 1e-4, bf16 I/O with fp32 state 2e-2
 TOL = {torch.float32: 1e-4, torch.bfloat16: 2e-2}
 
+# error statistics of every assert_close call, written out at session end when
+# LTV_ERR_REPORT names a file (tests/conftest.py)
+ERR_LOG: list = []
+
+
+def err_stats(actual, expected):
+    """max |a - e|; normwise relative error max|a - e| / max|e|; element-wise
+    relative error max |a - e| / |e| over the elements with |e| >= 1e-2 max|e|
+    (below that floor a relative error measures cancellation in the inputs,
+    not the kernel)."""
+    a = np.asarray(actual, np.float64)
+    e = np.asarray(expected, np.float64)
+    if e.size == 0:
+        return {"max_abs": 0.0, "norm_rel": 0.0, "elem_rel": 0.0}
+    diff = np.abs(a - e)
+    emax = float(np.abs(e).max())
+    max_abs = float(diff.max())
+    norm_rel = max_abs / emax if emax > 0 else (0.0 if max_abs == 0 else float("inf"))
+    big = np.abs(e) >= 1e-2 * emax
+    elem_rel = float((diff[big] / np.abs(e[big])).max()) if emax > 0 and big.any() else 0.0
+    return {"max_abs": max_abs, "norm_rel": norm_rel, "elem_rel": elem_rel}
+
 
 def assert_close(actual, expected, tol, label=""):
-    """|a - e| <= tol * (|e| + max(1, max|e|)) elementwise; tol = 0 means exact."""
+    """|a - e| <= tol * (|e| + max(1, max|e|)) elementwise; tol = 0 means exact.
+
+    Returns (and logs) the error statistics of ``err_stats``: the normwise and
+    element-wise relative errors are reported beside this rule."""
     a = np.asarray(actual, np.float64)
     e = np.asarray(expected, np.float64)
     assert a.shape == e.shape, (label, a.shape, e.shape)
@@ -103,3 +128,15 @@ def assert_close(actual, expected, tol, label=""):
         idx = np.argwhere(bad)[:5]
         msg = ", ".join(f"{tuple(i)}: got {a[tuple(i)]} want {e[tuple(i)]}" for i in idx)
         raise AssertionError(f"{label}: {int(bad.sum())}/{bad.size} mismatches (tol={tol}): {msg}")
+    stats = err_stats(a, e)
+    ERR_LOG.append({"label": label, "tol": tol, "size": int(e.size), **stats})
+    return stats
+
+
+def assert_norm_rel(actual, expected, tol, label=""):
+    """The north star's "max rel err" read normwise: max|a - e| <= tol * max|e|."""
+    stats = err_stats(actual, expected)
+    assert stats["norm_rel"] <= tol, f"{label}: normwise relative error {stats['norm_rel']:.3e} > {tol}"
+    ERR_LOG.append({"label": label + " (normwise)", "tol": tol,
+                    "size": int(np.asarray(expected).size), **stats})
+    return stats
