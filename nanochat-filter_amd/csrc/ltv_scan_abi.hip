@@ -33,6 +33,26 @@ __global__ void __launch_bounds__(256) dbias_reduce_kernel(const float* __restri
   if (threadIdx.x == 0) dbias[i] = red[0];
 }
 
+// Zeroes a (B, H, D) view of any strides in the I/O dtype (esize bytes per
+// element) and, from the first workgroup, n0 floats at f0.  A kernel rather
+// than a memset so that the calls stay valid inside a captured HIP graph.
+__global__ void __launch_bounds__(256) zero_bhd_kernel(char* __restrict__ p, View4 v, int B, int H,
+                                                       int D, int esize, float* __restrict__ f0,
+                                                       int n0) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (blockIdx.x == 0)
+    for (int k = threadIdx.x; k < n0; k += 256) f0[k] = 0.0f;
+  if (i >= (int64_t)B * H * D) return;
+  const int d = (int)(i % D);
+  const int64_t bh = i / D;
+  const int h = (int)(bh % H), b = (int)(bh / H);
+  char* q = p + (b * v.s[0] + h * v.s[1] + d * v.s[3]) * esize;
+  if (esize == 2)
+    *reinterpret_cast<uint16_t*>(q) = 0;
+  else
+    *reinterpret_cast<float*>(q) = 0.0f;
+}
+
 int scan_launch_fwd(bool bf16, const FwdArgs& a, ScanCfg cfg, int grid, bool vec, int gm,
                     hipStream_t st) {
   return bf16 ? scan_fwd_launch_bf16(a, cfg, grid, vec, gm, st)
@@ -479,9 +499,15 @@ int scan_backward_impl(int dtype, const HostView4& u, const HostView4& lg, const
   if (H == 0) return LTV_OK;
   LTV_REQUIRE(dbias != nullptr, LTV_ERR_INVALID_ARG, "null grad_logit_bias");
   if (B == 0 || T == 0) {
-    // nothing flows back: zero grad_logit_bias (inits receive no gradient terms
-    // either; with T == 0 the caller's grad_inits are left as allocated zeros)
-    LTV_HIP_CHECK(hipMemsetAsync(dbias, 0, sizeof(float) * H * Da, st));
+    // nothing flows back: grad_logit_bias and grad_inits are zero
+    const int64_t n = (int64_t)B * H * D;
+    LTV_REQUIRE(n == 0 || dinit.p != nullptr, LTV_ERR_INVALID_ARG, "null grad_inits");
+    const int64_t blocks = std::max<int64_t>(1, (n + 255) / 256);
+    LTV_REQUIRE(blocks < (1ll << 31), LTV_ERR_UNSUPPORTED, "grad_inits too large");
+    hipLaunchKernelGGL(zero_bhd_kernel, dim3((int)blocks), dim3(256), 0, st,
+                       reinterpret_cast<char*>(const_cast<void*>(dinit.p)), to_dev(dinit), B, H, D,
+                       dtype == LTV_DTYPE_BF16 ? 2 : 4, dbias, H * Da);
+    LTV_LAUNCH_CHECK();
     return LTV_OK;
   }
   const size_t need = bwd_workspace_bytes(dtype, B, T, NH, NKVH, Da, r, P, Q, K);

@@ -275,7 +275,7 @@ def scan_backward(
     grad_bias = grad_logit.sum(axis=(0, 1), dtype=np.float64).astype(
         np.float64 if io_dtype == "f64" else np.float32
     )
-    grad_combined = np.concatenate([grad_u, grad_logit], axis=-1).reshape(B, T, -1)
+    grad_combined = np.concatenate([grad_u, grad_logit], axis=-1).reshape(B, T, H * (D + Da))
     return (
         round_io(grad_combined, io_dtype),
         round_io(grad_init, io_dtype),
@@ -393,7 +393,7 @@ def look_back_backward(combined, inits, logit_bias, grad_hq, grad_hk, grad_hv, N
     grad_bias = grad_logit.sum(axis=(0, 1), dtype=np.float64).astype(
         np.float64 if io_dtype == "f64" else np.float32
     )
-    grad_combined = np.concatenate([grad_u, grad_logit], axis=-1).reshape(B, T, -1)
+    grad_combined = np.concatenate([grad_u, grad_logit], axis=-1).reshape(B, T, H * (D + Da))
     return (
         round_io(grad_combined, io_dtype),
         round_io(grad_init, io_dtype),

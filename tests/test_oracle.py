@@ -252,3 +252,19 @@ def test_bf16_rounding_is_round_to_nearest_even():
                     np.float32)
     want = torch.tensor(vals).to(torch.bfloat16).float().numpy()
     np.testing.assert_array_equal(O.bf16_round(vals), want)
+
+
+def test_oracle_empty_time():
+    """T == 0: no step runs, so the outputs are empty and no gradient reaches
+    the inits or the bias (the autograd of an empty loop)."""
+    B, NH, NKVH, Da, r = 2, 1, 1, 2, 3
+    H, D = NH + 2 * NKVH, Da * r
+    c = np.zeros((B, 0, H * (D + Da)), np.float32)
+    ini = np.ones((B, H, D), np.float32)
+    bias = np.ones((H, Da), np.float32)
+    hq, hk, hv = O.scan_forward(c, ini, bias, NH, NKVH, Da, r, True, "f32")
+    assert hq.shape == (B, NH, 0, D) and hk.shape == (B, NKVH, 0, D) and hv.shape == (B, NKVH, 0, D)
+    gc, gi, gb = O.scan_backward(c, ini, bias, hq, hk, hv, hq, hk, hv, NH, NKVH, Da, r, True, "f32")
+    assert gc.shape == c.shape
+    assert gi.shape == (B, H, D) and not np.any(gi)
+    assert gb.shape == (H, Da) and not np.any(gb)

@@ -264,3 +264,39 @@ def test_rejects_unsupported_tuning_values():
         op(c, ini, bias, 1, 1, 1, 2, 7, 8, 4, 32, 2, 8, True)
     with pytest.raises(RuntimeError, match="Unsupported r_items"):
         op(c, ini, bias, 1, 1, 1, 2, 8, 8, 3, 32, 2, 8, True)
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=io_name)
+def test_backward_empty_time_zeroes_grads(dtype):
+    """T == 0: no step reads the inits or the bias, so both gradients are zero
+    (as the oracle and the reference's autograd give); the kernel must write
+    them, whatever the caller's buffers held, also through strided views."""
+    import nanochat_amd.ops  # noqa: F401
+    kern = torch.ops.nanochat_cuda.ltv_fused_concat_head_major_register_cast_blelloch_scan_cuda_backward_kernel
+    B, NH, NKVH, Da, r = 3, 2, 1, 2, 4
+    H, D = NH + 2 * NKVH, Da * r
+    c = torch.zeros(B, 0, H * (D + Da), device=DEV, dtype=dtype)
+    ini = torch.randn(B, H, D, device=DEV).to(dtype)
+    bias = torch.randn(H, Da, device=DEV)
+    hq = torch.zeros(B, NH, 0, D, device=DEV, dtype=dtype)
+    hk = torch.zeros(B, NKVH, 0, D, device=DEV, dtype=dtype)
+    hv = torch.zeros(B, NKVH, 0, D, device=DEV, dtype=dtype)
+    gc = torch.zeros_like(c)
+    # grad_inits as a (B, H, D) view with a gap between heads
+    gi_store = torch.full((B, H, D + 3), float("nan"), device=DEV, dtype=dtype)
+    gi = gi_store[:, :, :D]
+    gb = torch.full((H, Da), float("nan"), device=DEV)
+    kern(c, ini, bias, hq, hk, hv, hq, hk, hv, gc, gi, gb, NH, NKVH, Da, r, 32, 2, 8, True)
+    torch.cuda.synchronize()
+    assert torch.equal(gi.float().cpu(), torch.zeros(B, H, D))
+    assert torch.equal(gb.cpu(), torch.zeros(H, Da))
+    # the gap columns are not part of the view and stay untouched
+    assert torch.isnan(gi_store[:, :, D:].float()).all()
+    # the oracle agrees: empty T gives zero gradients
+    eg = O.scan_backward(np.zeros((B, 0, H * (D + Da)), np.float32), np.ones((B, H, D), np.float32),
+                         np.zeros((H, Da), np.float32),
+                         np.zeros((B, NH, 0, D), np.float32), np.zeros((B, NKVH, 0, D), np.float32),
+                         np.zeros((B, NKVH, 0, D), np.float32),
+                         np.zeros((B, NH, 0, D), np.float32), np.zeros((B, NKVH, 0, D), np.float32),
+                         np.zeros((B, NKVH, 0, D), np.float32), NH, NKVH, Da, r, True, "f32")
+    assert not np.any(eg[1]) and not np.any(eg[2])
