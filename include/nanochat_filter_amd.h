@@ -301,6 +301,37 @@ int ltv_qkv_decode_step(const void* x, int64_t x_row_stride, const void* wpack,
                         const int64_t prev_strides[6], const float* logit_bias, void* out, int B,
                         int C, int NH, int NKVH, int D, int Da, int use_sigmoid, void* stream);
 
+/* ----------------------------------------------------------------------
+ * Allocation-free form of ltv_hm_scan_backward: the same arguments without
+ * the workspace, the same kernels and results (bitwise).  No counterpart in
+ * the reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  It calls no hipMalloc/hipFree and no allocating library
+ * routine; the workspace is a device array built into the library, one per
+ * GPU, held until the process ends.
+ *   Limit: the backward's workspace (ltv_hm_scan_backward_workspace_size) must
+ *   fit in ltv_hm_scan_backward_noalloc_max_workspace() bytes (32 MiB: d12,
+ *   B = 8 x T = 8192 prefill and smaller fit); larger shapes get
+ *   LTV_ERR_WORKSPACE.
+ *   Concurrency: every call on one GPU shares that GPU's array, so calls that
+ *   overlap on one GPU (other streams, other host threads) race; calls in
+ *   one stream are ordered.  The stream must belong to the current device.
+ * ---------------------------------------------------------------------- */
+size_t ltv_hm_scan_backward_noalloc_max_workspace(void);
+int ltv_hm_scan_backward_noalloc(int dtype, const void* combined,
+                                 const int64_t combined_strides[3], const void* inits,
+                                 const int64_t inits_strides[3], const float* logit_bias,
+                                 const void* hq, const int64_t hq_strides[4], const void* hk,
+                                 const int64_t hk_strides[4], const void* hv,
+                                 const int64_t hv_strides[4], const void* grad_hq,
+                                 const int64_t grad_hq_strides[4], const void* grad_hk,
+                                 const int64_t grad_hk_strides[4], const void* grad_hv,
+                                 const int64_t grad_hv_strides[4], void* grad_combined,
+                                 const int64_t grad_combined_strides[3], void* grad_inits,
+                                 const int64_t grad_inits_strides[3], float* grad_logit_bias,
+                                 int B, int T, int NH, int NKVH, int Da, int r, int use_sigmoid,
+                                 void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -893,3 +893,84 @@ extern "C" int ltv_hm_scan_backward_split(
       grad_logits_strides, grad_inits, grad_inits_strides, grad_logit_bias, workspace,
       workspace_bytes, B, T, NH, NKVH, Da, r, kUnboundedP, 1, 1, use_sigmoid, stream);
 }
+
+// ---------------------------------------------------------------------------
+// Allocation-free backward: ltv_hm_scan_backward with its workspace in a
+// file-scope device array instead of a caller buffer.
+//
+// `scratch` exists once per GPU (each device holds its own copy, at its own
+// address, from the library's load until the process ends).  In host code the
+// array's name is only a host-side stand-in: the device address is looked up
+// once per device with hipGetSymbolAddress, with that device current, and
+// only that address is ever handed to kernels.  Every call on one GPU shares
+// the array, so calls that overlap on one GPU (different streams, or host
+// threads) race on it; calls in one stream are ordered.  The backward writes
+// every workspace element it later reads, so nothing has to start at zero.
+// ---------------------------------------------------------------------------
+#include <mutex>
+
+namespace {
+
+constexpr size_t kNoAllocScratchBytes = (size_t)32 << 20;
+constexpr int kMaxScratchDevices = 64;
+
+static __device__ __align__(256) char scratch[kNoAllocScratchBytes];
+
+std::mutex g_scratch_mu;
+void* g_scratch_dev[kMaxScratchDevices] = {};
+
+// Device address of the current device's `scratch` (looked up on the first
+// call per device).  The stream, when given, must belong to that device.
+int scratch_for_current_device(hipStream_t st, void** out) {
+  int dev = -1;
+  LTV_HIP_CHECK(hipGetDevice(&dev));
+  LTV_REQUIRE(dev >= 0 && dev < kMaxScratchDevices, LTV_ERR_UNSUPPORTED,
+              "device index %d beyond the %d devices the scratch table holds", dev,
+              kMaxScratchDevices);
+  if (st != nullptr) {
+    hipDevice_t sdev = -1;
+    LTV_HIP_CHECK(hipStreamGetDevice(st, &sdev));
+    LTV_REQUIRE((int)sdev == dev, LTV_ERR_INVALID_ARG,
+                "stream belongs to device %d but device %d is current", (int)sdev, dev);
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_dev[dev] == nullptr) {
+    void* p = nullptr;
+    LTV_HIP_CHECK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    LTV_REQUIRE(p != nullptr, LTV_ERR_HIP, "hipGetSymbolAddress returned a null scratch address");
+    g_scratch_dev[dev] = p;
+  }
+  *out = g_scratch_dev[dev];
+  return LTV_OK;
+}
+
+}  // namespace
+
+extern "C" size_t ltv_hm_scan_backward_noalloc_max_workspace(void) { return kNoAllocScratchBytes; }
+
+extern "C" int ltv_hm_scan_backward_noalloc(
+    int dtype, const void* combined, const int64_t combined_strides[3], const void* inits,
+    const int64_t inits_strides[3], const float* logit_bias, const void* hq,
+    const int64_t hq_strides[4], const void* hk, const int64_t hk_strides[4], const void* hv,
+    const int64_t hv_strides[4], const void* grad_hq, const int64_t grad_hq_strides[4],
+    const void* grad_hk, const int64_t grad_hk_strides[4], const void* grad_hv,
+    const int64_t grad_hv_strides[4], void* grad_combined, const int64_t grad_combined_strides[3],
+    void* grad_inits, const int64_t grad_inits_strides[3], float* grad_logit_bias, int B, int T,
+    int NH, int NKVH, int Da, int r, int use_sigmoid, void* stream) {
+  int rc = check_shape(dtype, B, T, NH, NKVH, Da, r);
+  if (rc) return rc;
+  const size_t need = bwd_workspace_bytes(dtype, B, T, NH, NKVH, Da, r, kUnboundedP, 1, 1);
+  LTV_REQUIRE(need <= kNoAllocScratchBytes, LTV_ERR_WORKSPACE,
+              "this backward needs %zu bytes of workspace; the allocation-free entry point holds "
+              "%zu (use ltv_hm_scan_backward with a caller workspace)",
+              need, kNoAllocScratchBytes);
+  void* ws = nullptr;
+  rc = scratch_for_current_device((hipStream_t)stream, &ws);
+  if (rc) return rc;
+  return ltv_hm_scan_backward(dtype, combined, combined_strides, inits, inits_strides, logit_bias,
+                              hq, hq_strides, hk, hk_strides, hv, hv_strides, grad_hq,
+                              grad_hq_strides, grad_hk, grad_hk_strides, grad_hv, grad_hv_strides,
+                              grad_combined, grad_combined_strides, grad_inits,
+                              grad_inits_strides, grad_logit_bias, ws, kNoAllocScratchBytes, B, T,
+                              NH, NKVH, Da, r, use_sigmoid, stream);
+}
