@@ -286,14 +286,24 @@ __device__ __forceinline__ Rsrc make_rsrc(const void* base) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, 0x7fffffff,
                                            0x00020000);
 }
+// Store cache policy (the instruction's aux bits): kStNormal, or kStStream
+// (gfx950 `nt`: non-temporal).  Measured on MI355X: streaming stores take the
+// per-channel-gate forward (r = 1, configs[1]) from 106 to 91 us; they slow the
+// d12 forward (62 -> 69 us) and the d12 backward (124 -> 128 us with streaming
+// value gradients, 168 us with streaming 2-byte logit gradients: partial-line
+// streaming writes), so everything else stores normally.
+constexpr int kStNormal = 0;
+constexpr int kStStream = 2;
 __device__ __forceinline__ uint4 bld128(Rsrc r, uint32_t off) {
   return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
 }
+template <int AUX = kStNormal>
 __device__ __forceinline__ void bst128(Rsrc r, uint32_t off, uint4 x) {
-  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4_t, x), r, off, 0, 0);
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4_t, x), r, off, 0, AUX);
 }
+template <int AUX = kStNormal>
 __device__ __forceinline__ void bst_b32(Rsrc r, uint32_t off, float x) {
-  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(x), r, off, 0, 0);
+  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(x), r, off, 0, AUX);
 }
 
 // Hides x's value from the optimiser: offsets derived from it are formed where
@@ -324,13 +334,13 @@ __device__ __forceinline__ uint32_t bld1(Rsrc r, uint32_t off) {
   else
     return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
 }
-template <typename TIO>
+template <typename TIO, int AUX = kStNormal>
 __device__ __forceinline__ void bst1(Rsrc r, uint32_t off, float x) {
   if constexpr (sizeof(TIO) == 2)
     __builtin_amdgcn_raw_buffer_store_b16((unsigned short)(cvt_pk_bf16(x, 0.0f) & 0xffffu), r,
-                                          off, 0, 0);
+                                          off, 0, AUX);
   else
-    bst_b32(r, off, x);
+    bst_b32<AUX>(r, off, x);
 }
 
 // V channels at byte offset off, scb bytes apart; channels >= nvalid and
@@ -347,16 +357,16 @@ __device__ __forceinline__ uint4 bld_vec(Rsrc r, uint32_t off, uint32_t scb, int
   return make_uint4(w[0], w[1], w[2], w[3]);
 }
 
-template <typename TIO, bool VEC>
+template <typename TIO, bool VEC, int AUX = kStNormal>
 __device__ __forceinline__ void bst_vec(Rsrc r, uint32_t off, uint32_t scb, int nvalid, bool ok,
                                         const float (&x)[Pack<TIO>::V]) {
   if (VEC) {
-    bst128(r, ok ? off : kOob, Pack<TIO>::pack(x));
+    bst128<AUX>(r, ok ? off : kOob, Pack<TIO>::pack(x));
   } else {
     off = opaque(off);
 #pragma unroll
     for (int v = 0; v < Pack<TIO>::V; ++v)
-      bst1<TIO>(r, ok && v < nvalid ? off + v * scb : kOob, x[v]);
+      bst1<TIO, AUX>(r, ok && v < nvalid ? off + v * scb : kOob, x[v]);
   }
 }
 
@@ -726,8 +736,8 @@ scan_fwd_kernel(const FwdArgs args) {
         const float a = al[s][GL ? 0 : v];
         hv[v] = fmaf(a, Pack<TIO>::get(uq[s], v) - hv[v], hv[v]);
       }
-      bst_vec<TIO, VEC>(orr, ooff + s * ostb, oscb, nvalid,
-                        active && (t0 + s) >= t_st && (t0 + s) < t_hi, hv);
+      bst_vec<TIO, VEC, GM == GATE_CHANVEC ? kStStream : kStNormal>(
+          orr, ooff + s * ostb, oscb, nvalid, active && (t0 + s) >= t_st && (t0 + s) < t_hi, hv);
     }
   };
 
