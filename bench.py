@@ -1,7 +1,7 @@
 """Benchmark of the LTV combined-QKV filter path on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
-                    [--workload filter|look_back|gpt|scan_fwd]
+                    [--workload filter|look_back|gpt|scan_fwd|prefill]
 
 Workload (the d12 training shape): x bf16
 [32, 1024, 768] ~ N(0, 1); c.weight [2322, 768] fp32 ~ N(0, 1/768) (value rows
@@ -20,7 +20,9 @@ look-back configuration).  ``--workload gpt`` is BASELINE.json configs[3].
 ``--workload scan_fwd`` is configs[1], the standalone scan forward: bf16 head-major
 values [32, 3 x 6, 1024, 128] ~ N(0, 1) with a per-element decay (r = 1)
 a = sigmoid(z), z ~ N(2, 1), i.e. logit + bias = -z; fp32 state, bf16 out; a
-step is one scan launch and ``value`` is its algorithmic GB/s.
+step is one scan launch and ``value`` is its algorithmic GB/s.  ``--workload
+prefill`` is configs[4]'s prefill: one forward of the filter at B = 8,
+T = 8192 with long-memory decays (tokens / s).
 
 Printed as one JSON line, with
   roofline     -- the dominant kernel's algorithmic bytes (or FLOPs) per launch
@@ -149,7 +151,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--workload", choices=("filter", "look_back", "gpt", "scan_fwd"),
+    ap.add_argument("--workload", choices=("filter", "look_back", "gpt", "scan_fwd", "prefill"),
                     default="filter",
                     help="filter: BASELINE.json configs[2] (the default, the metric's workload); "
                          "look_back: the same shapes through the look-back filter with the d12 "
@@ -157,7 +159,8 @@ def main():
                          "gpt: configs[3], one training step of the 12-layer d12 GPT with the "
                          "filter in every layer (tokens/s and the filter's share of the step); "
                          "scan_fwd: configs[1], the standalone per-element-decay scan forward "
-                         "(GB/s)")
+                         "(GB/s); prefill: configs[4]'s prefill, the filter forward at B=8, "
+                         "T=8192 with decay sigmoid(N(3, 1.5)) (tokens/s)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="after the timed region, run a plain device copy of 256 MiB five times "
                          "(the known-size reference for rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -173,6 +176,9 @@ def main():
         return
     if args.workload == "scan_fwd":
         scan_fwd_main(args)
+        return
+    if args.workload == "prefill":
+        prefill_main(args)
         return
 
     import torch
@@ -384,6 +390,12 @@ def scan_fwd_main(args):
         for _ in range(args.steps):
             step()
         torch.cuda.synchronize()
+    if args.calibrate_copy:
+        src = torch.empty(COPY_CAL_BYTES, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
     ms = rec.durations_ms()["scan_fwd"]
     avg_us = sum(ms) / len(ms) * 1e3
     nbytes = scan_fwd_bytes()
@@ -414,6 +426,100 @@ def scan_fwd_main(args):
     }
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = scan_fwd_cpu_baseline(args.cpu_seconds)
+    print(json.dumps(out), flush=True)
+
+
+# long-sequence prefill
+PF_B, PF_T = 8, 8192
+
+
+def prefill_main(args):
+    """configs[4]'s prefill: one forward of the drop-in filter (pack, bf16 MFMA
+    projection, scan) on x bf16 [8, 8192, 768] ~ N(0, 1), c.weight ~
+    N(0, 1/768) with the 18 gate rows scaled by 1.5 and logit_bias = -3, so
+    logit + bias ~ N(-3, 1.5) and the decay a = sigmoid(z), z ~ N(3, 1.5), sits
+    around 0.95 (long memory).  value = tokens / s of the forward."""
+    import torch
+    from nanochat_amd import _native as N
+    from nanochat_amd.ltv.ltv_filter import LtvInitValues
+    from nanochat_amd.ltv_cuda_fused_concat_head_major_register_cast_blelloch_scan_qkv_filter import (
+        LtvCudaFusedConcatHeadMajorRegisterCastBlellochScanQkvFilter as Filter,
+    )
+
+    dev = torch.device("cuda:0")
+    torch.manual_seed(0)
+    f = Filter(NH, NKVH, D, R)
+    with torch.no_grad():
+        f.c.weight.normal_(0.0, C ** -0.5)
+        f.c.weight.view(H, D + DA, C)[:, D:] *= 1.5
+        f.logit_bias.fill_(-3.0)
+        f.init_param.normal_(0.0, C ** -0.5)
+    f = f.to(dev)
+    g = torch.Generator(device=dev).manual_seed(0)
+    x = torch.randn(PF_B, PF_T, C, generator=g, device=dev).to(torch.bfloat16)
+    none = LtvInitValues()
+
+    def step():
+        with torch.no_grad():
+            return f(x, none)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    with N.KernelRecorder() as rec:
+        for _ in range(args.steps):
+            step()
+        torch.cuda.synchronize()
+    if args.calibrate_copy:
+        src = torch.empty(COPY_CAL_BYTES, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+    M = PF_B * PF_T
+    work = {"pack_weight": ("hbm", F * C * 4 + FP * C * S_IO),
+            "qkv_project_fwd": ("mfma", 2 * M * C * F),
+            "scan_fwd": ("hbm", M * (F + H * D) * S_IO + PF_B * H * D * S_IO + 4 * H * DA)}
+    kernels = {}
+    for name, ms in rec.durations_ms().items():
+        bound, amount = work[name]
+        avg = sum(ms) / len(ms)
+        if bound == "hbm":
+            ach, peak, unit = amount / (avg * 1e-3) / 1e9, HBM_PEAK_GBS, "GB/s"
+        else:
+            ach, peak, unit = amount / (avg * 1e-3) / 1e12, BF16_PEAK_TFLOPS, "TFLOP/s"
+        kernels[name] = {"bound": bound, "avg_us": round(avg * 1e3, 2), "launches": len(ms),
+                         "achieved": round(ach, 1), "peak": peak, "unit": unit,
+                         "frac": round(ach / peak, 4), "work_per_launch": amount}
+    dominant = max(kernels, key=lambda k: kernels[k]["avg_us"] * kernels[k]["launches"])
+    dk_ = kernels[dominant]
+    traffic, traffic_src = profiled_traffic(dominant, "prefill_traffic.json")
+    out = {
+        "metric": "long-sequence prefill: LTV QKV filter forward tokens/s at B8 T8192 C768",
+        "value": round(M * args.steps / elapsed, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(elapsed * 1e3 / args.steps, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "configs[4] prefill: filter forward, decay sigmoid(N(3, 1.5))",
+                   "B": PF_B, "T": PF_T, "C": C, "n_head": NH, "n_kv_head": NKVH,
+                   "head_dim": D, "r": R, "parallelism": "single GPU"},
+        "roofline": {"kernel": dominant, "bound": dk_["bound"], "achieved": dk_["achieved"],
+                     "peak": dk_["peak"], "unit": dk_["unit"], "frac": dk_["frac"],
+                     "traffic": traffic, "traffic_source": traffic_src},
+        "kernels": kernels,
+    }
     print(json.dumps(out), flush=True)
 
 

@@ -331,8 +331,15 @@ int launch_forward(int dtype, FwdArgs& a, bool vec, const HostView4& lg, int B, 
   // 89 us with 4 steps per lane): 81 VGPRs let all 1152 workgroups be resident
   // at once (111 VGPRs left 128 of them for a second round), and each load
   // instruction covers 8 rows of 128 bytes.
+  // With fewer workgroups than fill the chip once (long T at small batch:
+  // B = 8, T = 8192 at d12 heads gives 288), each one is latency-bound and 4
+  // steps per lane put twice the bytes in flight: 174 against 190 us there.
+  // (Cutting T into chunks entered from composed chunk maps measured no
+  // better, 199 us: the maps cost a second read of all but the last chunk.)
   const int fcl = cl_full < 8 ? cl_full : 8;
-  ScanCfg cfg{fcl, fcl == 8 && vec ? 2 : 4, 4};
+  const int nslab0 = (D + fcl * V - 1) / (fcl * V);
+  const bool few = (int64_t)B * H * a.nwin * nslab0 < 1024;
+  ScanCfg cfg{fcl, fcl == 8 && vec && !few ? 2 : 4, 4};
   const ScanTuning& tu = tuning();
   if (vec && tu.fwd_cl > 0) cfg = ScanCfg{tu.fwd_cl < cl_full ? tu.fwd_cl : cl_full, tu.fwd_l, tu.fwd_nw};
   const int nslab = (D + cfg.CL * V - 1) / (cfg.CL * V);

@@ -300,3 +300,52 @@ def test_backward_empty_time_zeroes_grads(dtype):
                          np.zeros((B, NH, 0, D), np.float32), np.zeros((B, NKVH, 0, D), np.float32),
                          np.zeros((B, NKVH, 0, D), np.float32), NH, NKVH, Da, r, True, "f32")
     assert not np.any(eg[1]) and not np.any(eg[2])
+
+
+# ---------------------------------------------------------------------------
+# long sequences at small batch (configs[4] prefill)
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("dtype", DTYPES, ids=io_name)
+@pytest.mark.parametrize("D,r", [(128, 128), (128, 1), (64, 16)])
+def test_forward_long_exact(dtype, D, r):
+    """The reference's integer generators (gates 0 / 1, sigmoid off) at T =
+    2000 with one sequence slab: hundreds of tiles walked by one workgroup
+    (the few-workgroup launch shape), every output exact."""
+    B, T, NH, NKVH = 1, 2000, 1, 0
+    Da = D // r
+    c = int_combined(B, T, NH, NKVH, Da, r)
+    ini = int_inits(B, NH, NKVH, Da, r)
+    bias = int_logit_bias(NH, NKVH, Da, False)
+    eq, ek, ev = _expected(c, ini, bias, NH, NKVH, Da, r, False, io_name(dtype))
+    q, k, v = _run(to_torch(c, dtype, DEV), to_torch(ini, dtype, DEV),
+                   to_torch(bias, torch.float32, DEV), NH, NKVH, Da, r, False)
+    assert_close(np_of(q), eq, 0, f"q D={D} r={r}")
+
+
+def test_forward_config5_prefill():
+    """configs[4]'s prefill shape (B = 8, T = 8192, 18 heads of 128, r = 128,
+    bf16, decay sigmoid(z), z ~ N(3, 1.5)) through the fast path's scan: two
+    batch rows (all heads) against the oracle within the bf16 tolerance, and
+    two runs bitwise equal."""
+    from nanochat_amd.ops import ltv_hm_fast as F_
+    B, T, NH, NKVH, D = 8, 8192, 6, 6, 128
+    H = NH + 2 * NKVH
+    g = torch.Generator().manual_seed(5)
+    values = torch.randn(B, H, T, D, generator=g).to(torch.bfloat16)
+    logits = (-(3.0 + 1.5 * torch.randn(B, T, H, generator=g))).to(torch.bfloat16)
+    inits = (0.5 * torch.randn(B, H, D, generator=g)).to(torch.bfloat16)
+    bias = torch.zeros(H, 1)
+    vd, ld, idv, bd = values.to(DEV), logits.to(DEV), inits.to(DEV), bias.to(DEV)
+    outs = F_.scan_forward(vd, ld, idv, bd, NH, NKVH, 1, D, True)
+    outs2 = F_.scan_forward(vd, ld, idv, bd, NH, NKVH, 1, D, True)
+    for a, b in zip(outs, outs2):
+        assert torch.equal(a, b)
+    got = torch.cat(outs, dim=1)  # (B, H, T, D)
+    for b in (0, 7):
+        # the oracle's (B, T, F) layout: per head [values D | logit]
+        comb = torch.cat([values[b].permute(1, 0, 2), logits[b].unsqueeze(-1)], dim=-1)
+        comb = comb.reshape(1, T, H * (D + 1)).float().numpy()
+        eq, ek, ev = O.scan_forward(comb, inits[b:b + 1].float().numpy(), bias.numpy(), NH, NKVH,
+                                    1, D, True, "bf16")
+        want = np.concatenate([eq, ek, ev], axis=1)[0]
+        assert_close(np_of(got[b]), want, 2e-2, f"config5 prefill b={b}")
