@@ -244,7 +244,7 @@ int ltv_linear_transpose_backward(int dtype, const void* x, const void* weight,
  * ltv_qkv_project_forward: x (B T, C) bf16 contiguous ->
  *   values (B, H, T, D) bf16 contiguous (head-major: what the scan reads) and
  *   logits (B T, Lp) bf16 contiguous (column h Da + j = logit j of head h;
- *   columns >= H Da are unspecified).  One kernel launch.
+ *   columns >= H Da are written as zeros).  One kernel launch.
  *
  * ltv_qkv_project_backward: grad_combined (B T, Fp) bf16 row-major with column
  *   h D + d = gradient of value channel d of head h and column H D + h Da + j =

@@ -487,8 +487,10 @@ extern "C" int ltv_qkv_project_forward(const void* x, const void* wpack, void* v
   a.Q = GemmOperand{reinterpret_cast<const bf16_t*>(x), C, M, C};       // (m, k) KC
   a.K = C;
   a.k_split = round_up(C, kGemmBK);
+  // the logit rows' padding columns [H Da, Lp) come out as zeros (the packed
+  // weight's rows past F are zero), so every element of the output is defined
   EpiProjectHM e{reinterpret_cast<bf16_t*>(values), reinterpret_cast<bf16_t*>(logits), H, D, T,
-                 ltv_qkv_logit_width(H, Da), H * D + H * Da, M};
+                 ltv_qkv_logit_width(H, Da), H * D + ltv_qkv_logit_width(H, Da), M};
   hipStream_t st = (hipStream_t)stream;
   if (gemm_tuning().dma && dma_usable(a, OP_KC, OP_KC, e, 1)) {
     a.tiles_j = (M + 255) / 256;

@@ -86,6 +86,10 @@ class CausalSelfAttention(nn.Module):
         q, k, v = self.qkv_computer(x, None)  # (B, T, H, D) views of head-major buffers
         cos, sin = cos_sin
         q, k = norm(apply_rotary_emb(q, cos, sin)), norm(apply_rotary_emb(k, cos, sin))
+        # v in the (B, T, H, D) memory layout of q and k: ROCm's flash-attention
+        # backward returns dv in q's layout while its compile-time shape function
+        # predicts v's, which fails torch.compile's stride check when they differ
+        v = v.contiguous()
         y = F.scaled_dot_product_attention(
             q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2), is_causal=True,
             scale=self.scale, enable_gqa=self.n_head != self.n_kv_head)

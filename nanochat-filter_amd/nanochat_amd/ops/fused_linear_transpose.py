@@ -89,6 +89,12 @@ def _fused_linear_transpose_setup(ctx, inputs, output):
 
 def _fused_linear_transpose_backward(ctx, grad_out):
     x, weight = ctx.saved_tensors
+    # the kernel reads grad_out as (B, F, T) or as its transposed (B, T, F)
+    # view; autograd can hand over other layouts (an expanded zero gradient
+    # under AOT tracing, say), which are made contiguous here rather than
+    # refused as the reference does -- every layout it accepts is unchanged
+    if not (grad_out.is_contiguous() or _is_transposed_grad_out(grad_out)):
+        grad_out = grad_out.contiguous()
     if (
         not x.is_contiguous()
         or not weight.is_contiguous()
