@@ -347,7 +347,7 @@ int launch_gemm_dma(GemmArgs a, const Epi& e, int splits, hipStream_t st) {
 // Defaults measured on MI355X at d12: 256 x 256 tiles with 8 wavefronts for the
 // forward and dX, 128 x 256 tiles with 8192-row splits for dW.
 struct GemmTuning {
-  int fwd = 1, dx = 1, dw = 0, dw_split = 4096, dma = 1;
+  int fwd = 1, dx = 1, dw = 0, dw_split = 0, dma = 1;  // dw_split 0: automatic
   GemmTuning() {
     if (const char* e = getenv("LTV_GEMM_CFG")) {
       int a = 0, b = 0, c = 0, d = 4096, f = 0;
@@ -519,12 +519,26 @@ extern "C" int ltv_qkv_project_forward(const void* x, const void* wpack, void* v
 namespace {
 inline int dw_splits(int M, int rows) { return std::max(1, (M + rows - 1) / rows); }
 inline int dw_rows(int Fp, int variant) { return variant == 1 ? round_up(Fp, 128) : round_up(Fp, 256); }
+// Rows of the M reduction per dW split (a multiple of the 64-row k-step).
+// Automatic: as many splits as give about one (tile, split) item per CU over
+// the 256 x 256 output tiles -- at d12 (M = 32768) 8 splits of 4096 rows, 240
+// items; at B = 16 (M = 16384) 8 of 2048 (fixed 4096-row splits left 120 items
+// and half the CUs idle).
+inline int dw_split_rows(int M, int C, int Fp) {
+  const GemmTuning& tu = gemm_tuning();
+  if (tu.dw_split > 0) return tu.dw_split;
+  const int tiles = std::max(1, ((C + 255) / 256) * (dw_rows(Fp, tu.dw) / 256));
+  const int S = std::max(1, device_cu_count() / tiles);
+  // at least 1024 rows (16 k-steps) per split: shorter splits cost more in
+  // per-item overhead and partial sums than they gain in parallelism
+  return std::max(1024, round_up((M + S - 1) / S, 64));
+}
 }  // namespace
 
 extern "C" size_t ltv_qkv_project_backward_workspace_size(int M, int C, int H, int D, int Da) {
   const int Fp = ltv_qkv_packed_width(H, D, Da);
   const GemmTuning& tu = gemm_tuning();
-  return (size_t)dw_splits(M, tu.dw_split) * dw_rows(Fp, tu.dw) * C * sizeof(float);
+  return (size_t)dw_splits(M, dw_split_rows(M, C, Fp)) * dw_rows(Fp, tu.dw) * C * sizeof(float);
 }
 
 namespace {
@@ -612,13 +626,14 @@ extern "C" int ltv_qkv_project_backward_weight(const void* x, const void* grad_c
   const GemmTuning& tu = gemm_tuning();
   // dW^T[c, f] = sum_m X[m, c] dC[m, f]:  i = c (RC: X[m * C + c]), j = f (RC: dC[m * Fp + f]),
   // the reduction over m split into fp32 partials P_s[f][c]
-  const int S = dw_splits(M, tu.dw_split);
+  const int split_rows = dw_split_rows(M, C, Fp);
+  const int S = dw_splits(M, split_rows);
   const int Fr = dw_rows(Fp, tu.dw);
   GemmArgs a;
   a.P = GemmOperand{reinterpret_cast<const bf16_t*>(x), C, C, M};
   a.Q = GemmOperand{reinterpret_cast<const bf16_t*>(grad_combined), Fp, Fp, M};
   a.K = M;
-  a.k_split = tu.dw_split;
+  a.k_split = split_rows;
   EpiRowF32Split e{reinterpret_cast<float*>(workspace), C, (int64_t)Fr * C, C, Fr};
   if (tu.dma && dma_usable(a, OP_RC, OP_RC, e, S)) {
     a.tiles_i = (C + 255) / 256;
