@@ -210,6 +210,9 @@ int ltv_hm_look_back_scan_backward_split(
  * Projection, reference layout: out[b] (F x T) = weight (F x K) . x[b]^T
  *
  * x (B, T, K), weight (F, K), out (B, F, T): all contiguous, all `dtype`.
+ * bf16 with T a multiple of 256 and K of 8 (16-byte aligned buffers) runs on
+ * bf16 MFMA (fp32 accumulation) and writes the (B, F, T) layout directly; other
+ * shapes and fp32 run a SIMT fp32-accumulation kernel.
  * Replaces fused_linear_transpose (cpp_ewma/src/fused_linear_transpose_forward.cu:23-58,
  * called from nanochat/ops/fused_linear_transpose.py:20-40).
  * ---------------------------------------------------------------------- */
@@ -227,6 +230,20 @@ int ltv_linear_transpose_forward(int dtype, const void* x, const void* weight, v
 int ltv_linear_transpose_backward(int dtype, const void* x, const void* weight,
                                   const void* grad_out, int grad_out_is_btf, void* grad_x,
                                   void* grad_weight, int B, int T, int K, int F, void* stream);
+
+/* The same backward with a workspace: bf16 with grad_out (B, F, T) contiguous,
+ * T a multiple of 256 and K of 8 (16-byte aligned buffers) runs both GEMMs on
+ * bf16 MFMA -- grad_x directly, grad_weight as fp32 split partials in the
+ * workspace summed in a fixed order (deterministic) -- and needs
+ * ltv_linear_transpose_backward_workspace_size bytes; every other case runs
+ * ltv_linear_transpose_backward (workspace size 0, workspace may be NULL).
+ * Same contract and counterpart as ltv_linear_transpose_backward. */
+size_t ltv_linear_transpose_backward_workspace_size(int dtype, int B, int T, int K, int F,
+                                                    int grad_out_is_btf);
+int ltv_linear_transpose_backward_ws(int dtype, const void* x, const void* weight,
+                                     const void* grad_out, int grad_out_is_btf, void* grad_x,
+                                     void* grad_weight, void* workspace, size_t workspace_bytes,
+                                     int B, int T, int K, int F, void* stream);
 
 /* ------------------------------------------------------------------------
  * Fused QKV projection for the filter module (bf16 MFMA, fp32 accumulate).

@@ -110,6 +110,20 @@ zero_cols_kernel(bf16_t* __restrict__ p, int rows, int64_t ld, int c0, int c1) {
   if (c < c1) q[c] = 0;
 }
 
+// out[f, k] = sum_s part[s][f, k]  (rows in their own order; fixed order,
+// deterministic), written as TO.
+template <typename TO>
+__global__ void __launch_bounds__(256)
+reduce_splits_kernel(const float* __restrict__ part, TO* __restrict__ out, int S,
+                     int64_t split_stride, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * 256) {
+    float acc = 0.0f;
+    for (int s = 0; s < S; ++s) acc += part[(int64_t)s * split_stride + i];
+    io_traits<TO>::store(out + i, acc);
+  }
+}
+
 // grad_weight[param row, c] = sum_s partial[s][packed row, c]  (fixed order)
 __global__ void dw_reduce_kernel(const float* __restrict__ part, float* __restrict__ gw, int S,
                                  int64_t split_stride, int H, int D, int Da, int C) {
@@ -285,6 +299,7 @@ int device_cu_count() {
 // Elements an operand spans: rows x k for K-contiguous (ld = row pitch), k x rows for
 // row-contiguous (ld = k pitch).
 inline int64_t operand_span(const GemmOperand& o, int K, int layout) {
+  if (o.blen > 0) return dma_batched_span(o, K, layout);
   return layout == OP_KC ? (int64_t)o.rows * o.ld : (int64_t)K * o.ld;
 }
 
@@ -312,7 +327,7 @@ inline bool dma_ok(const GemmOperand& op, int64_t K, int layout) {
 }
 
 // Largest output buffer an epilogue of the direct-to-LDS kernel addresses.
-inline int64_t dma_epi_bytes(const EpiRowBF16& e, int) { return (int64_t)e.j_valid * e.ldc * 2; }
+inline int64_t dma_epi_bytes(const EpiRowBF16& e, int) { return epi_row_bf16_bytes(e); }
 inline int64_t dma_epi_bytes(const EpiRowF32Split& e, int splits) {
   return (int64_t)splits * e.split_stride * 4;
 }
@@ -382,13 +397,33 @@ extern "C" int ltv_linear_transpose_forward(int dtype, const void* x, const void
   LTV_REQUIRE(B >= 0 && T >= 0 && K >= 0 && F >= 0, LTV_ERR_INVALID_ARG, "negative size");
   if ((int64_t)B * T * F == 0) return LTV_OK;
   LTV_REQUIRE(x && weight && out, LTV_ERR_INVALID_ARG, "null tensor pointer");
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == LTV_DTYPE_BF16 && gemm_tuning().dma && T % 256 == 0 && K % 8 == 0 && K > 0 &&
+      aligned16(x) && aligned16(weight) && aligned16(out) && (int64_t)B * T < (1ll << 31)) {
+    // bf16 MFMA: Out(i = token m, j = feature f) = sum_k x[m, k] W[f, k] written
+    // to out[b, f, t] (m = b T + t): i runs along t, batches F T apart
+    const int M = B * T;
+    GemmArgs g;
+    g.P = GemmOperand{reinterpret_cast<const bf16_t*>(x), K, M, K};       // (m, k) KC
+    g.Q = GemmOperand{reinterpret_cast<const bf16_t*>(weight), K, F, K};  // (f, k) KC
+    g.K = K;
+    g.k_split = round_up(K, kGemmBK);
+    EpiRowBF16 e{reinterpret_cast<bf16_t*>(out), T, M, F};
+    e.bstride = (int64_t)F * T;
+    e.blen = T;
+    if (dma_usable(g, OP_KC, OP_KC, e, 1)) {
+      g.tiles_i = M / 256;
+      g.tiles_j = (F + 255) / 256;
+      return launch_gemm_dma<256, 256, 2, 4, OP_KC, OP_KC>(g, e, 1, st);
+    }
+  }
   // per batch: out_b (F x T) = W (F x K) . x_b^T
   SimtArgs a;
   a.A = weight; a.sam = K; a.sako = 0; a.saki = 1; a.sab = 0;
   a.B = x; a.sbn = K; a.sbko = 0; a.sbki = 1; a.sbb = (int64_t)T * K;
   a.C = out; a.scm = T; a.scn = 1; a.scb = (int64_t)F * T;
   a.M = F; a.N = T; a.K = K; a.kin = K > 0 ? K : 1;
-  return launch_simt(dtype, dtype, a, B, (hipStream_t)stream);
+  return launch_simt(dtype, dtype, a, B, st);
 }
 
 extern "C" int ltv_linear_transpose_backward(int dtype, const void* x, const void* weight,
@@ -423,6 +458,107 @@ extern "C" int ltv_linear_transpose_backward(int dtype, const void* x, const voi
     return LTV_OK;
   }
   return launch_simt(dtype, dtype, w, 1, st);
+}
+
+namespace {
+// The bf16 MFMA path of the reference-layout backward: grad_out (B, F, T)
+// contiguous, T a multiple of the 256-token tile, K a multiple of 8.
+bool lt_backward_mfma(int dtype, int is_btf, int B, int T, int K, int F) {
+  return dtype == LTV_DTYPE_BF16 && !is_btf && gemm_tuning().dma && T % 256 == 0 && K % 8 == 0 &&
+         K > 0 && F > 0 && (int64_t)B * T < (1ll << 31) && (int64_t)B * F * T < kDmaMaxSpan &&
+         (int64_t)B * T * K < kDmaMaxSpan;
+}
+
+struct LtSplits {
+  int rows, S, Fr;
+};
+// dW split-K: about one (tile, split) item per CU over the 256 x 256 tiles,
+// at least 1024 reduction rows per split
+LtSplits lt_splits(int M, int K, int F) {
+  LtSplits p;
+  p.Fr = round_up(F, 256);
+  const int tiles = std::max(1, ((K + 255) / 256) * (p.Fr / 256));
+  const int S = std::max(1, device_cu_count() / tiles);
+  p.rows = std::max(1024, round_up((M + S - 1) / S, 64));
+  p.S = std::max(1, (M + p.rows - 1) / p.rows);
+  return p;
+}
+}  // namespace
+
+extern "C" size_t ltv_linear_transpose_backward_workspace_size(int dtype, int B, int T, int K,
+                                                                int F, int grad_out_is_btf) {
+  if (B <= 0 || T <= 0 || K <= 0 || F <= 0) return 0;
+  if (!lt_backward_mfma(dtype, grad_out_is_btf, B, T, K, F)) return 0;
+  const LtSplits p = lt_splits(B * T, K, F);
+  return (size_t)p.S * p.Fr * K * sizeof(float);
+}
+
+extern "C" int ltv_linear_transpose_backward_ws(int dtype, const void* x, const void* weight,
+                                                const void* grad_out, int grad_out_is_btf,
+                                                void* grad_x, void* grad_weight, void* workspace,
+                                                size_t workspace_bytes, int B, int T, int K,
+                                                int F, void* stream) {
+  LTV_REQUIRE(dtype == LTV_DTYPE_F32 || dtype == LTV_DTYPE_BF16, LTV_ERR_INVALID_ARG,
+              "dtype must be LTV_DTYPE_F32 or LTV_DTYPE_BF16, got %d", dtype);
+  LTV_REQUIRE(B >= 0 && T >= 0 && K >= 0 && F >= 0, LTV_ERR_INVALID_ARG, "negative size");
+  if (!lt_backward_mfma(dtype, grad_out_is_btf, B, T, K, F) ||
+      !(aligned16(x) && aligned16(weight) && aligned16(grad_out) && aligned16(grad_x) &&
+        aligned16(grad_weight)))
+    return ltv_linear_transpose_backward(dtype, x, weight, grad_out, grad_out_is_btf, grad_x,
+                                         grad_weight, B, T, K, F, stream);
+  LTV_REQUIRE(x && weight && grad_out && grad_x && grad_weight, LTV_ERR_INVALID_ARG,
+              "null tensor pointer");
+  hipStream_t st = (hipStream_t)stream;
+  const int M = B * T;
+  const LtSplits sp = lt_splits(M, K, F);
+  const size_t need = (size_t)sp.S * sp.Fr * K * sizeof(float);
+  LTV_REQUIRE(workspace && workspace_bytes >= need, LTV_ERR_WORKSPACE,
+              "workspace too small: need %zu bytes, got %zu", need, workspace_bytes);
+  const bf16_t* gp = reinterpret_cast<const bf16_t*>(grad_out);
+  // grad_x[m, k] = sum_f g[b, f, t] W[f, k]:  i = k (RC: W[f K + k]), j = m (RC, batched:
+  // g at (m / T) F T + f T + m % T)
+  {
+    GemmArgs a;
+    a.P = GemmOperand{reinterpret_cast<const bf16_t*>(weight), K, K, F};
+    a.Q = GemmOperand{gp, T, M, F};
+    a.Q.bstride = (int64_t)F * T;
+    a.Q.blen = T;
+    a.K = F;
+    a.k_split = round_up(F, kGemmBK);
+    EpiRowBF16 e{reinterpret_cast<bf16_t*>(grad_x), K, K, M};
+    LTV_REQUIRE(dma_usable(a, OP_RC, OP_RC, e, 1), LTV_ERR_UNSUPPORTED,
+                "grad_x operands not supported by the MFMA kernel");
+    a.tiles_i = (K + 255) / 256;
+    a.tiles_j = M / 256;
+    int rc = launch_gemm_dma<256, 256, 2, 4, OP_RC, OP_RC>(a, e, 1, st);
+    if (rc) return rc;
+  }
+  // grad_weight[f, k] = sum_m x[m, k] g[b, f, t]:  i = k (RC: x[m K + k]), j = f (KC with the
+  // reduction index m batched: g at (m / T) F T + f T + m % T); fp32 split partials, then a
+  // fixed-order sum into grad_weight (bf16)
+  {
+    GemmArgs a;
+    a.P = GemmOperand{reinterpret_cast<const bf16_t*>(x), K, K, M};
+    a.Q = GemmOperand{gp, T, F, M};
+    a.Q.bstride = (int64_t)F * T;
+    a.Q.blen = T;
+    a.K = M;
+    a.k_split = sp.rows;
+    EpiRowF32Split e{reinterpret_cast<float*>(workspace), K, (int64_t)sp.Fr * K, K, sp.Fr};
+    LTV_REQUIRE(dma_usable(a, OP_RC, OP_KC, e, sp.S), LTV_ERR_UNSUPPORTED,
+                "grad_weight operands not supported by the MFMA kernel");
+    a.tiles_i = (K + 255) / 256;
+    a.tiles_j = sp.Fr / 256;
+    int rc = launch_gemm_dma<256, 256, 2, 4, OP_RC, OP_KC>(a, e, sp.S, st);
+    if (rc) return rc;
+    const int64_t n = (int64_t)F * K;
+    const int blocks = (int)std::min<int64_t>((n + 255) / 256, 8192);
+    hipLaunchKernelGGL(reduce_splits_kernel<bf16_t>, dim3(blocks), dim3(256), 0, st,
+                       reinterpret_cast<const float*>(workspace),
+                       reinterpret_cast<bf16_t*>(grad_weight), sp.S, (int64_t)sp.Fr * K, n);
+    LTV_LAUNCH_CHECK();
+  }
+  return LTV_OK;
 }
 
 extern "C" int ltv_qkv_packed_width(int H, int D, int Da) {

@@ -147,6 +147,13 @@ constexpr int64_t kDmaMaxSpan = 1ll << 30;
 //   KC: row < rows and k0 + c8 < kend   (kend a multiple of 8 or the chunk
 //       straddling it reads buffer contents past kend, which must then be 0)
 //   RC: rows a multiple of 8, row0 + c8 < rows and k < kend
+// Elements an operand in the batched layout spans (the batched index's
+// extent -- rows for RC, the reduction K for KC -- rounded up to whole batches).
+__host__ __device__ inline int64_t dma_batched_span(const GemmOperand& op, int K, int layout) {
+  const int n = layout == OP_KC ? K : op.rows;
+  return (int64_t)((n + op.blen - 1) / op.blen) * op.bstride;
+}
+
 template <int R, int L, int NW>
 struct DmaOperand {
   static constexpr int kInstr = R * kDmaBK * 2 / 1024;  // 1 KB instructions per stage
@@ -158,11 +165,19 @@ struct DmaOperand {
   int kk[kPerWave];         // this lane's reduction offset within a k-step
   uint32_t kstride;         // elements per unit of k
   int kend;
+  int64_t kbstride;  // KC batched reduction index (kblen > 0): k0 -> batch k0 / kblen
+  int kblen;
 
   __device__ __forceinline__ void setup(const GemmOperand& op, int K, int row0, int ke, int wave,
                                         int lane) {
-    const int64_t span = L == OP_KC ? (int64_t)op.rows * op.ld : (int64_t)K * op.ld;
+    const int64_t span = op.blen > 0 ? dma_batched_span(op, K, L)
+                                     : L == OP_KC ? (int64_t)op.rows * op.ld : (int64_t)K * op.ld;
     rsrc = make_buffer_rsrc(op.p, (uint32_t)(span * 2));
+    kbstride = L == OP_KC ? op.bstride : 0;
+    kblen = L == OP_KC ? op.blen : 0;
+    // RC batched rows: the tile's rows lie in batch row0 / blen
+    const int64_t rbase =
+        L == OP_RC && op.blen > 0 ? (int64_t)(row0 / op.blen) * op.bstride + row0 % op.blen : row0;
 #pragma unroll
     for (int w = 0; w < 4; ++w) rsrc[w] = __builtin_amdgcn_readfirstlane(rsrc[w]);
     kstride = L == OP_KC ? 1u : (uint32_t)op.ld;
@@ -180,7 +195,7 @@ struct DmaOperand {
         const int k = o / (R * 2), slot = (o % (R * 2)) >> 4;
         const int c = slot ^ (4 * (k & 3));
         kk[i] = k;
-        base[i] = row0 + c * 8 < op.rows ? (uint32_t)(k * (int64_t)op.ld + row0 + c * 8)
+        base[i] = row0 + c * 8 < op.rows ? (uint32_t)(k * (int64_t)op.ld + rbase + c * 8)
                                          : kDmaOob;
       }
     }
@@ -188,7 +203,8 @@ struct DmaOperand {
 
   // loads of the k-step starting at k0 into the stage at lds_stage (byte address)
   __device__ __forceinline__ void issue(uint32_t lds_stage, int k0, int wave) const {
-    const uint32_t koff = (uint32_t)k0 * kstride;
+    const uint32_t koff = kblen > 0 ? (uint32_t)((int64_t)(k0 / kblen) * kbstride + k0 % kblen)
+                                    : (uint32_t)k0 * kstride;
 #pragma unroll
     for (int i = 0; i < kPerWave; ++i) {
       const bool ok = base[i] != kDmaOob && k0 + kk[i] < kend;
@@ -259,18 +275,28 @@ __device__ __forceinline__ void stage_bf16_pair(lds_char_t* st, const f32x16_t& 
 template <class Epi>
 struct DmaEpi;
 
+// Bytes an EpiRowBF16 output spans.
+__host__ __device__ inline int64_t epi_row_bf16_bytes(const EpiRowBF16& e) {
+  if (e.blen > 0) return (int64_t)((e.i_valid + e.blen - 1) / e.blen) * e.bstride * 2;
+  return (int64_t)e.j_valid * e.ldc * 2;
+}
+
 template <>
 struct DmaEpi<EpiRowBF16> {
   i32x4_t rsrc;
-  int64_t ldc;
-  int i_valid, j_valid;
+  int64_t ldc, bstride;
+  int i_valid, j_valid, blen;
   __device__ __forceinline__ DmaEpi(const EpiRowBF16& e, const GemmArgs&)
-      : rsrc(uniform_rsrc(e.c, (int64_t)e.j_valid * e.ldc * 2)), ldc(e.ldc), i_valid(e.i_valid),
-        j_valid(e.j_valid) {}
+      : rsrc(uniform_rsrc(e.c, epi_row_bf16_bytes(e))), ldc(e.ldc), bstride(e.bstride),
+        i_valid(e.i_valid), j_valid(e.j_valid), blen(e.blen) {}
+  // element offset of column i (in a batch-aligned tile) at row 0
+  __device__ __forceinline__ int64_t col(int i) const {
+    return blen > 0 ? (int64_t)(i / blen) * bstride + i % blen : i;
+  }
   __device__ __forceinline__ int store_block(int i, int j, int, int lane,
                                              const f32x16_t& v) const {
     const int il = i + 4 * (lane >> 5);
-    const uint32_t off = (uint32_t)((int64_t)j * ldc + il) * 2u;
+    const uint32_t off = (uint32_t)((int64_t)j * ldc + col(il)) * 2u;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const bool ok = j < j_valid && il + 8 * q < i_valid;
@@ -294,7 +320,7 @@ struct DmaEpi<EpiRowBF16> {
           const int j = j0 + 32 * b + row, i = i0 + 64 * a2 + 8 * c;
           const bool ok = j < j_valid && i < i_valid;
           buf_store_b128(stage_get(st, row, c),
-                         ok ? (uint32_t)((int64_t)j * ldc + i) * 2u : kDmaOob, rsrc);
+                         ok ? (uint32_t)((int64_t)j * ldc + col(i)) * 2u : kDmaOob, rsrc);
         }
       }
     return MJ * (MI / 2) * 4;

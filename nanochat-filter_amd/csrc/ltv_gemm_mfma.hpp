@@ -39,6 +39,13 @@ struct GemmOperand {
   int64_t ld;
   int rows;     // rows >= this read as zero
   int k_valid;  // k >= this reads as zero
+  // Batched layout (blen > 0, direct-to-LDS kernel only): the batched index --
+  // the rows of an RC operand, the reduction index of a KC one -- runs in
+  // batches of blen whose storage lies bstride elements apart: index n sits
+  // at (n / blen) bstride + n % blen.  A tile's rows (RC) or a k-step (KC)
+  // must not straddle two batches.
+  int64_t bstride = 0;
+  int blen = 0;
 };
 
 struct GemmArgs {
@@ -387,6 +394,10 @@ struct EpiRowBF16 {
   bf16_t* c;
   int64_t ldc;
   int i_valid, j_valid;
+  // Batched output (blen > 0, direct-to-LDS kernel only): element (i, j) at
+  // (i / blen) bstride + j ldc + i % blen; a tile's i range must lie in one batch.
+  int64_t bstride = 0;
+  int blen = 0;
   __device__ __forceinline__ void store_block(int i, int j, int, int lane,
                                               const f32x16_t& v) const {
     if (j >= j_valid) return;

@@ -100,6 +100,13 @@ SIGNATURES = {
         [_c_int, _c_vp, _c_vp, _c_vp, _c_int, _c_vp, _c_vp, _c_int, _c_int, _c_int, _c_int,
          _c_vp],
     ),
+    "ltv_linear_transpose_backward_workspace_size": (
+        _c_sz, [_c_int, _c_int, _c_int, _c_int, _c_int, _c_int]),
+    "ltv_linear_transpose_backward_ws": (
+        _c_int,
+        [_c_int, _c_vp, _c_vp, _c_vp, _c_int, _c_vp, _c_vp, _c_vp, _c_sz, _c_int, _c_int, _c_int,
+         _c_int, _c_vp],
+    ),
     "ltv_qkv_packed_width": (_c_int, [_c_int, _c_int, _c_int]),
     "ltv_qkv_logit_width": (_c_int, [_c_int, _c_int]),
     "ltv_qkv_pack_weight": (

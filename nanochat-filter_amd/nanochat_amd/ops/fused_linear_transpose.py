@@ -41,7 +41,10 @@ def fused_linear_transpose(x, weight, out):
 def fused_linear_transpose_cuda_op(x, weight):
     B, T, K = x.shape
     F = weight.size(0)
-    out = torch.zeros((B, F, T), dtype=x.dtype, device=x.device)
+    # the kernel writes every element (the reference zero-fills first, a 152 MB
+    # memset at d12); an empty reduction (K == 0) still gets zeros
+    alloc = torch.zeros if K == 0 else torch.empty
+    out = alloc((B, F, T), dtype=x.dtype, device=x.device)
     torch.ops.nanochat_cuda.fused_linear_transpose(x, weight, out)
     return out
 
@@ -75,10 +78,16 @@ def fused_linear_transpose_backward_kernel(x, weight, grad_out, grad_x, grad_wei
     B, T, K = x.shape
     F = weight.size(0)
     is_btf = 1 if (not grad_out.is_contiguous()) else 0
-    rc = N.lib().ltv_linear_transpose_backward(
+    lib = N.lib()
+    # bf16 (B, F, T) gradients run on MFMA; the weight gradient's split
+    # partials need a workspace (0 bytes where the SIMT kernel runs)
+    ws_bytes = lib.ltv_linear_transpose_backward_workspace_size(N.dtype_code(dt), B, T, K, F, is_btf)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=x.device)
+    rc = lib.ltv_linear_transpose_backward_ws(
         N.dtype_code(dt), x.data_ptr(), weight.data_ptr(), grad_out.data_ptr(), is_btf,
-        grad_x.data_ptr(), grad_weight.data_ptr(), B, T, K, F, N.stream_of(x))
-    N.check(rc, "ltv_linear_transpose_backward")
+        grad_x.data_ptr(), grad_weight.data_ptr(), ws.data_ptr(), ws_bytes, B, T, K, F,
+        N.stream_of(x))
+    N.check(rc, "ltv_linear_transpose_backward_ws")
     return None
 
 
@@ -105,8 +114,14 @@ def _fused_linear_transpose_backward(ctx, grad_out):
             "and either contiguous or transposed grad_out. Found strides: "
             f"x={x.stride()}, weight={weight.stride()}, grad_out={grad_out.stride()}"
         )
-    grad_x = torch.zeros_like(x, memory_format=torch.contiguous_format)
-    grad_weight = torch.zeros_like(weight, memory_format=torch.contiguous_format)
+    # overwritten by the kernels; empty reductions (F == 0 for grad_x, B T == 0
+    # for grad_weight) still get zeros
+    B, T, _ = x.shape
+    F = weight.size(0)
+    grad_x = (torch.zeros_like if F == 0 else torch.empty_like)(
+        x, memory_format=torch.contiguous_format)
+    grad_weight = (torch.zeros_like if B * T == 0 else torch.empty_like)(
+        weight, memory_format=torch.contiguous_format)
     torch.ops.nanochat_cuda.fused_linear_transpose_backward_kernel(
         x, weight, grad_out, grad_x, grad_weight
     )

@@ -122,3 +122,50 @@ def test_projection_ragged_token_counts(M):
     assert_close(np_of(gx), (gc_i @ _bf(w)).numpy(), 2e-2, "grad_x")
     assert_close(np_of(gw), torch.einsum("btf,btc->fc", gc_i, _bf(x)).numpy(), 2e-2,
                  "grad_weight")
+
+
+@pytest.mark.parametrize("B,T,K,F", [
+    (32, 1024, 768, 2322),   # d12: the reference filter's projection at configs[2]
+    (2, 256, 64, 100),       # one token tile per batch, F not a multiple of 8
+    (3, 512, 136, 700),      # K a multiple of 8 but not of 64
+])
+def test_fused_linear_transpose_bf16_mfma(B, T, K, F):
+    """bf16 reference-layout projection on the MFMA kernels (T a multiple of
+    256, K of 8): out (B, F, T), grad_x and grad_weight against an fp32 torch
+    product of the same bf16 operands, and against the SIMT kernel
+    (ltv_linear_transpose_backward) -- both fp32-accumulated, so within
+    accumulation-order rounding; the weight gradient twice bitwise equal
+    (fixed-order split sum)."""
+    from nanochat_amd import _native as N
+    ops = _ops()
+    lib = N.lib()
+    assert lib.ltv_linear_transpose_backward_workspace_size(N.DTYPE_BF16, B, T, K, F, 0) > 0
+    g = torch.Generator().manual_seed(B + T + K + F)
+    x = (torch.randn(B, T, K, generator=g) / K ** 0.5).to(torch.bfloat16).to(DEV)
+    w = (torch.randn(F, K, generator=g) / K ** 0.5).to(torch.bfloat16).to(DEV)
+    go = torch.randn(B, F, T, generator=g).to(torch.bfloat16).to(DEV)
+    xf, wf, gof = x.float(), w.float(), go.float()
+    out = ops.nanochat_cuda.fused_linear_transpose_cuda_op(x, w)
+    ref = torch.matmul(wf, xf.transpose(1, 2))
+    assert_close(np_of(out), np_of(ref), 2e-2, "out")
+    grads = []
+    for _ in range(2):
+        gx = torch.empty_like(x)
+        gw = torch.empty_like(w)
+        ops.nanochat_cuda.fused_linear_transpose_backward_kernel(x, w, go, gx, gw)
+        grads.append((gx, gw))
+    assert torch.equal(grads[0][0], grads[1][0]) and torch.equal(grads[0][1], grads[1][1])
+    gx, gw = grads[0]
+    want_gx = torch.matmul(gof.transpose(1, 2), wf)                        # (B, T, K)
+    want_gw = torch.matmul(gof.reshape(B, F, T).permute(1, 0, 2).reshape(F, B * T),
+                           xf.reshape(B * T, K))                          # (F, K)
+    assert_close(np_of(gx), np_of(want_gx), 2e-2, "grad_x")
+    assert_close(np_of(gw), np_of(want_gw), 2e-2, "grad_weight")
+    # the SIMT kernel on the same operands
+    sx, sw = torch.empty_like(x), torch.empty_like(w)
+    N.check(lib.ltv_linear_transpose_backward(N.DTYPE_BF16, x.data_ptr(), w.data_ptr(),
+                                              go.data_ptr(), 0, sx.data_ptr(), sw.data_ptr(),
+                                              B, T, K, F, N.stream_of(x)), "simt backward")
+    torch.cuda.synchronize()
+    assert_close(np_of(gx), np_of(sx), 2e-2, "grad_x vs SIMT")
+    assert_close(np_of(gw), np_of(sw), 2e-2, "grad_weight vs SIMT")
