@@ -45,6 +45,20 @@ from nanochat_amd.ops.ltv_cuda_ops import (
 class LtvCudaFusedConcatHeadMajorRegisterCastBlellochScanQkvFilter(
     LtvCombinedHeadMajorQkvFilter
 ):
+    def __init__(self, n_head: int, n_kv_head: int, head_dim: int, r: int):
+        super().__init__(n_head, n_kv_head, head_dim, r)
+        # loading a checkpoint replaces c.weight's values: drop the decode
+        # path's packed copy of it
+        self.register_load_state_dict_post_hook(
+            lambda module, incompatible_keys: hm_fast.invalidate_packed_weight(module))
+
+    def invalidate_packed_weight(self):
+        """Drop the decode path's packed bf16 copy of ``c.weight``.  Needed only
+        after writing the weight through ``c.weight.data`` (which does not bump
+        the parameter's version counter); optimizer steps, in-place updates of
+        the parameter and ``load_state_dict`` are tracked."""
+        hm_fast.invalidate_packed_weight(self)
+
     def forward(self, x, previous_values: LtvInitValues):
         B, _, _ = x.size()
         autocast_dtype = torch.get_autocast_dtype("cuda")

@@ -107,8 +107,10 @@ def pack_weight(weight: torch.Tensor, H: int, D: int, Da: int) -> torch.Tensor:
 
 def cached_packed_weight(module, H: int, D: int, Da: int) -> torch.Tensor:
     """The packed bf16 weight of ``module.c.weight``, kept on the module and
-    rebuilt when the weight changes (any in-place update, e.g. an optimizer
-    step or ``load_state_dict``, bumps its version)."""
+    rebuilt when the weight changes: in-place updates of the Parameter (an
+    optimizer step, ``copy_`` under ``no_grad``) bump its version counter, and
+    ``load_state_dict`` drops the cache.  Writes through ``weight.data`` do not
+    bump the version; after one, call ``invalidate_packed_weight(module)``."""
     w = module.c.weight
     key = (w.data_ptr(), w._version, w.dtype, w.device)
     cached = getattr(module, "_wpack_cache", None)
@@ -116,6 +118,11 @@ def cached_packed_weight(module, H: int, D: int, Da: int) -> torch.Tensor:
         cached = (key, pack_weight(w.detach(), H, D, Da))
         module._wpack_cache = cached
     return cached[1]
+
+
+def invalidate_packed_weight(module) -> None:
+    """Drop the packed weight cached by ``cached_packed_weight``."""
+    module._wpack_cache = None
 
 
 def decode_step(x: torch.Tensor, wpack: torch.Tensor, prev, logit_bias: torch.Tensor, NH: int,

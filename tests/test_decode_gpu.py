@@ -125,6 +125,29 @@ def test_decode_from_init_param_and_weight_updates():
             f.c.weight.mul_(-1.5)
 
 
+def test_decode_after_data_writes_and_load_state_dict():
+    """A write through c.weight.data does not bump the parameter's version: the
+    packed weight is refreshed by invalidate_packed_weight(); load_state_dict
+    refreshes it by itself."""
+    from nanochat_amd.ltv.ltv_filter import LtvInitValues
+    f = _make_filter(2, 1, 128, 128, seed=4)
+    x = torch.randn(5, 1, 256).to(torch.bfloat16).to(DEV)
+    with torch.no_grad():
+        f(x, LtvInitValues())  # fills the cache
+    f.c.weight.data.mul_(-2.0)
+    f.invalidate_packed_weight()
+    with torch.no_grad():
+        got = torch.cat(f(x, LtvInitValues()), dim=2)
+    gen = torch.cat(_general_step(f, x, None), dim=2)
+    assert_close(np_of(got), np_of(gen), TOL, "decode after a .data write")
+    other = _make_filter(2, 1, 128, 128, seed=5)
+    f.load_state_dict(other.state_dict())
+    with torch.no_grad():
+        got = torch.cat(f(x, LtvInitValues()), dim=2)
+    gen = torch.cat(_general_step(other, x, None), dim=2)
+    assert_close(np_of(got), np_of(gen), TOL, "decode after load_state_dict")
+
+
 def _chain(module, xs, cache, fused):
     outs = []
     for t in range(xs.shape[1]):

@@ -109,3 +109,16 @@ def test_uniform_stream_splits_like_one_draw():
     a = torch.empty(300).uniform_(0.0, 1.0)
     b = torch.empty(700).uniform_(0.0, 1.0)
     assert torch.equal(one, torch.cat([a, b]))
+
+
+def test_load_state_dict_drops_the_packed_weight_cache():
+    """The decode path caches a packed copy of c.weight on the module; loading a
+    state dict must drop it (checked on the CPU: the cache attribute only)."""
+    f = Filter(2, 1, 16, 4)
+    f._wpack_cache = ("stale-key", torch.zeros(1))
+    g = Filter(2, 1, 16, 4)
+    f.load_state_dict(g.state_dict())
+    assert f._wpack_cache is None
+    f._wpack_cache = ("stale-key", torch.zeros(1))
+    f.invalidate_packed_weight()
+    assert f._wpack_cache is None

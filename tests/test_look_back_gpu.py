@@ -242,3 +242,30 @@ def test_d12_windows_match_full_recurrence_per_window():
     assert_close(np_of(gc), np_of(e_gc), tol, "grad_combined")
     assert_close(np_of(gi), np_of(e_gi), tol, "grad_inits")
     assert_close(np_of(gb), np_of(e_gb), 1e-3, "grad_logit_bias")
+
+
+@pytest.mark.parametrize("pqk", [(128, 112, 17), (224, 100, 125)], ids=str)
+def test_look_back_tile_backward_is_deterministic_per_channel_gates(pqk):
+    """The look-back backward on the tile kernels with per-channel gates (r = 1,
+    D = 128, bf16: 16 channel lanes, 4 steps per lane, 2 wavefronts; windows
+    longer than the short-window kernels take): two runs bitwise equal, and
+    within tolerance of the oracle.  This is the instantiation whose parity
+    buffers once gave run-dependent gradients in a build with a wave-uniform
+    wavefront index."""
+    B, NH, NKVH, T, D, r = 2, 2, 1, 700, 128, 1
+    Da = D // r
+    H = NH + 2 * NKVH
+    dtype = torch.bfloat16
+    rng = np.random.default_rng(700 + pqk[0])
+    c = O.round_io(rng.standard_normal((B, T, H * (D + Da))).astype(np.float32), "bf16")
+    ini = O.round_io(rng.standard_normal((B, H, D)).astype(np.float32), "bf16")
+    bias = (rng.standard_normal((H, Da)) * 0.5).astype(np.float32)
+    gy = O.round_io(rng.standard_normal((B, H, T, D)).astype(np.float32), "bf16")
+    runs = [_run("blelloch", to_torch(c, dtype, DEV), to_torch(ini, dtype, DEV),
+                 to_torch(bias, torch.float32, DEV), NH, NKVH, Da, r, pqk, True,
+                 _grads(gy, NH, NKVH, dtype)) for _ in range(3)]
+    for other in runs[1:]:
+        for a, b in zip(runs[0][1:], other[1:]):
+            assert torch.equal(a, b)
+    want = _expected(c, ini, bias, NH, NKVH, Da, r, pqk, True, "bf16", gy)
+    _check(runs[0], want, TOL[dtype], f"pqk={pqk}")
