@@ -8,8 +8,9 @@
 // every row of a KC operand is fetched as one full 128-byte line: the L2 serves
 // about one request per channel per clock whatever its size, and 64-byte
 // requests halve its throughput.  Two stages (2 x 64 KB for a 256 x 256 tile)
-// double-buffer the k-steps: the loads of step s + 1 are issued before the
-// MFMAs of step s and waited for after them, one barrier per step.
+// double-buffer the k-steps: the loads of step s + 1 are issued at the start of
+// step s, by half of the wavefronts, and waited for at its end, one barrier per
+// step; the last k16 sub-step of each step runs after that barrier.
 //
 // LDS layouts (no padding; 16-byte chunks XOR-swizzled so both fragment reads
 // are bank-conflict free):
@@ -134,11 +135,13 @@ __device__ __forceinline__ uint32_t lds_addr(const T* p) {
   return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p;
 }
 
-// Byte offset that the buffer range check rejects (operands are limited to
-// kDmaMaxSpan elements, so num_records <= this offset and offset + 16 does not
-// wrap): such a lane's load writes zeros to LDS.
+// Byte offset that the buffer range check rejects: such a lane's load writes
+// zeros to LDS.  Operands are limited to kDmaMaxSpan elements, so num_records
+// <= kDmaOob, and kDmaOob plus any in-range byte offset (< 2^31 - 2^21) plus
+// 16 stays below 2^32: a row past the operand keeps a rejected offset when the
+// k-step's offset is added to it.
 constexpr uint32_t kDmaOob = 0x80000000u;
-constexpr int64_t kDmaMaxSpan = 1ll << 30;
+constexpr int64_t kDmaMaxSpan = (1ll << 30) - (1ll << 20);
 
 // Per-operand DMA plan: which global 8-element chunk each lane fetches for each
 // of its wavefront's instructions in a stage (fixed per work item), plus the
@@ -161,7 +164,7 @@ struct DmaOperand {
   static_assert(kInstr % NW == 0 && kPerWave >= 1, "tile too small for the wavefronts");
   static_assert(L == OP_KC || R >= 128, "RC tiles need >= 16 chunks per k-row");
   i32x4_t rsrc;
-  uint32_t base[kPerWave];  // element offset at k0 = 0, or kDmaOob
+  uint32_t base[kPerWave];  // byte offset at k0 = 0, or kDmaOob
   int kk[kPerWave];         // this lane's reduction offset within a k-step
   uint32_t kstride;         // elements per unit of k
   int kend;
@@ -189,13 +192,13 @@ struct DmaOperand {
         const int row = o / kDmaRowBytes, slot = (o >> 4) % kDmaRowSlots;
         const int c = dma_kc_slot(row, slot);  // the swizzle is an involution
         kk[i] = c * 8;
-        base[i] = row0 + row < op.rows ? (uint32_t)((row0 + row) * (int64_t)op.ld + c * 8)
+        base[i] = row0 + row < op.rows ? (uint32_t)((row0 + row) * (int64_t)op.ld + c * 8) * 2u
                                        : kDmaOob;
       } else {
         const int k = o / (R * 2), slot = (o % (R * 2)) >> 4;
         const int c = slot ^ (4 * (k & 3));
         kk[i] = k;
-        base[i] = row0 + c * 8 < op.rows ? (uint32_t)(k * (int64_t)op.ld + rbase + c * 8)
+        base[i] = row0 + c * 8 < op.rows ? (uint32_t)(k * (int64_t)op.ld + rbase + c * 8) * 2u
                                          : kDmaOob;
       }
     }
@@ -205,12 +208,21 @@ struct DmaOperand {
   __device__ __forceinline__ void issue(uint32_t lds_stage, int k0, int wave) const {
     const uint32_t koff = kblen > 0 ? (uint32_t)((int64_t)(k0 / kblen) * kbstride + k0 % kblen)
                                     : (uint32_t)k0 * kstride;
+    const uint32_t koff2 = koff * 2u;
+    if (k0 + kDmaBK <= kend) {
+      // every reduction index of the step is valid: one add per load (a row
+      // past the operand keeps an offset >= kDmaOob)
 #pragma unroll
-    for (int i = 0; i < kPerWave; ++i) {
-      const bool ok = base[i] != kDmaOob && k0 + kk[i] < kend;
-      const uint32_t voff = ok ? (base[i] + koff) * 2u : kDmaOob;
-      dma16(__builtin_amdgcn_readfirstlane(lds_stage + (uint32_t)((wave * kPerWave + i) * 1024)),
-            rsrc, voff, 0u);
+      for (int i = 0; i < kPerWave; ++i)
+        dma16(__builtin_amdgcn_readfirstlane(lds_stage + (uint32_t)((wave * kPerWave + i) * 1024)),
+              rsrc, base[i] + koff2, 0u);
+    } else {
+#pragma unroll
+      for (int i = 0; i < kPerWave; ++i) {
+        const bool ok = base[i] != kDmaOob && k0 + kk[i] < kend;
+        dma16(__builtin_amdgcn_readfirstlane(lds_stage + (uint32_t)((wave * kPerWave + i) * 1024)),
+              rsrc, ok ? base[i] + koff2 : kDmaOob, 0u);
+      }
     }
   }
 };
@@ -503,8 +515,15 @@ gemm_dma_kernel(const GemmArgs g, const Epi epi) {
   static_assert(MI >= 1 && MJ >= 1 && WI % 32 == 0 && WJ % 32 == 0, "bad wave tile");
   constexpr int PB = BI * kDmaBK * 2, QB = BJ * kDmaBK * 2;  // stage bytes per operand
   constexpr int KS = kDmaBK / 16;                             // MFMA k16 sub-steps per step
-  using OpP = DmaOperand<BI, PL, NW>;
-  using OpQ = DmaOperand<BJ, QL, NW>;
+  // The loads are issued by the last NWL wavefronts only (with 8 wavefronts,
+  // one per SIMD).  A wavefront that issues a burst of direct-to-LDS loads
+  // stalls until the texture unit has taken them, and cannot issue MFMAs
+  // meanwhile; the other wavefront of its SIMD, which issues none, keeps the
+  // matrix core busy.  Measured on MI355X at the d12 forward shape: 123 ->
+  // 110 us (with the single-add load offsets) against every wavefront loading.
+  constexpr int NWL = NW >= 2 ? NW / 2 : 1;
+  using OpP = DmaOperand<BI, PL, NWL>;
+  using OpQ = DmaOperand<BJ, QL, NWL>;
 
   constexpr int NST = kDmaStages;
   constexpr int kLoads = OpP::kPerWave + OpQ::kPerWave;  // vm instructions per k-step
@@ -540,14 +559,18 @@ gemm_dma_kernel(const GemmArgs g, const Epi epi) {
       decode(c);
     }
   };
+  const bool loader = wave_u >= NW - NWL;
+  const int lw = wave_u - (NW - NWL);  // index among the loaders
+  const int my_loads = loader ? kLoads : 0;
   auto issue = [&](const GemmCursor& c, int stage) {
+    if (!loader) return;
     if (c.kt == 0) {
-      op_p.setup(g.P, g.K, c.i0, c.ke, wave_u, lane);
-      op_q.setup(g.Q, g.K, c.j0, c.ke, wave_u, lane);
+      op_p.setup(g.P, g.K, c.i0, c.ke, lw, lane);
+      op_q.setup(g.Q, g.K, c.j0, c.ke, lw, lane);
     }
     const int k0 = c.kb + c.kt * kDmaBK;
-    op_p.issue(lds_addr(&lds_p[stage][0]), k0, wave_u);
-    op_q.issue(lds_addr(&lds_q[stage][0]), k0, wave_u);
+    op_p.issue(lds_addr(&lds_p[stage][0]), k0, lw);
+    op_q.issue(lds_addr(&lds_q[stage][0]), k0, lw);
   };
 
   GemmCursor lc, cc;
@@ -568,7 +591,7 @@ gemm_dma_kernel(const GemmArgs g, const Epi epi) {
     if (lc.valid) {
       issue(lc, i);
       advance(lc);
-      tot[i] = kLoads;
+      tot[i] = my_loads;
     }
   }
   // instructions younger than the loads of step k + 1, at the end of step k
@@ -582,72 +605,52 @@ gemm_dma_kernel(const GemmArgs g, const Epi epi) {
   __builtin_amdgcn_s_barrier();
   lds_fence();
 
-  int stage = 0;
-  while (cc.valid) {
-    // the stage of step k + NST - 1 was last read in step k - 1, which every
-    // wavefront has finished (barrier below): refill it
-    int loads = 0;
-    if (lc.valid) {
-      issue(lc, stage == 0 ? NST - 1 : stage - 1);
-      advance(lc);
-      loads = kLoads;
-    }
-    // MFMAs of this step; the fragments of sub-step t + 1 are read during t
-    const bf16_t* sp = &lds_p[stage][0];
-    const bf16_t* sq = &lds_q[stage][0];
-    bf16x8_t fp[2][MI], fq[2][MJ];
+  // Rotated k-step loop.  A step's last k16 sub-step runs after the barrier
+  // that ends the step -- its fragments are in registers by then -- so its
+  // MFMAs cover the barrier skew and the next step's first fragment reads
+  // (the stage that barrier frees is refilled at the same time).  One pass:
+  //   loads of step k + NST - 1; sub-step 0 reads of step k, with the last
+  //   sub-step's MFMAs of step k - 1; the epilogue if step k - 1 ended a tile;
+  //   sub-steps 0 .. KS - 2 of step k, reading sub-step t + 1 during t;
+  //   wait for the loads of step k + 1; barrier.
+  // The rotation keeps a sub-step's fragments live across the barrier and the
+  // next step's load set-up; with row-contiguous operands (two reads and more
+  // addresses per fragment) that exceeds the 256 registers of two wavefronts
+  // per SIMD, and those kernels keep the plain loop below.
+  constexpr bool kRotate = PL == OP_KC && QL == OP_KC;
+  static_assert(KS % 2 == 0, "the last sub-step must use fragment set 1");
+  constexpr int RD = MI * (PL == OP_KC ? 1 : 2) + MJ * (QL == OP_KC ? 1 : 2);  // LDS reads per sub-step
+  constexpr int NM = MI * MJ;
+  bf16x8_t fp[2][MI], fq[2][MJ];
+  auto read_sub = [&](auto setc, int stg, int t) {
+    constexpr int set = decltype(setc)::value;
+    const bf16_t* sp = &lds_p[stg][0];
+    const bf16_t* sq = &lds_q[stg][0];
 #pragma unroll
-    for (int a = 0; a < MI; ++a) fp[0][a] = dma_read_frag<BI, PL>(sp, wi * WI + a * 32, 0, lane);
+    for (int a = 0; a < MI; ++a) fp[set][a] = dma_read_frag<BI, PL>(sp, wi * WI + a * 32, t, lane);
 #pragma unroll
-    for (int b = 0; b < MJ; ++b) fq[0][b] = dma_read_frag<BJ, QL>(sq, wj * WJ + b * 32, 0, lane);
-    static_for<KS>([&](auto tc) {
-      constexpr int t = decltype(tc)::value;
-      constexpr int cur = t & 1;
-      if constexpr (t + 1 < KS) {
+    for (int b = 0; b < MJ; ++b) fq[set][b] = dma_read_frag<BJ, QL>(sq, wj * WJ + b * 32, t, lane);
+  };
+  auto mfma_sub = [&](auto setc) {
+    constexpr int set = decltype(setc)::value;
 #pragma unroll
-        for (int a = 0; a < MI; ++a)
-          fp[cur ^ 1][a] = dma_read_frag<BI, PL>(sp, wi * WI + a * 32, t + 1, lane);
+    for (int a = 0; a < MI; ++a)
 #pragma unroll
-        for (int b = 0; b < MJ; ++b)
-          fq[cur ^ 1][b] = dma_read_frag<BJ, QL>(sq, wj * WJ + b * 32, t + 1, lane);
-      }
-#pragma unroll
-      for (int a = 0; a < MI; ++a)
-#pragma unroll
-        for (int b = 0; b < MJ; ++b)
-          acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fp[cur][a], fq[cur][b], acc[a][b],
-                                                              0, 0, 0);
+      for (int b = 0; b < MJ; ++b)
+        acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fp[set][a], fq[set][b], acc[a][b], 0, 0, 0);
+  };
+  // Left to itself the scheduler issues each read right before the MFMA that
+  // consumes it, and every MFMA group then waits for the LDS: one MFMA, then
+  // its share of the reads, for each MFMA of a sub-step.
+  auto interleave = [&]() {
+    static_for<NM>([&](auto ic) {
+      constexpr int i = decltype(ic)::value;
+      constexpr int n = RD / NM + (i < RD % NM ? 1 : 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      if constexpr (n > 0) __builtin_amdgcn_sched_group_barrier(0x100, n, 0);
     });
-    // Schedule: the first sub-step's fragment reads, then in each sub-step the
-    // next one's reads spread between its MFMAs.  Left to itself the scheduler
-    // issues each read just before the MFMA that consumes it, and every MFMA
-    // group then waits for the LDS.
-    {
-      constexpr int RD = MI * (PL == OP_KC ? 1 : 2) + MJ * (QL == OP_KC ? 1 : 2);
-      constexpr int NM = MI * MJ;
-      __builtin_amdgcn_sched_group_barrier(0x100, RD, 0);
-      static_for<KS>([&](auto tc) {
-        constexpr int t = decltype(tc)::value;
-        static_for<NM>([&](auto ic) {
-          constexpr int i = decltype(ic)::value;
-          constexpr int n = t + 1 < KS ? RD / NM + (i < RD % NM ? 1 : 0) : 0;
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-          if constexpr (n > 0) __builtin_amdgcn_sched_group_barrier(0x100, n, 0);
-        });
-      });
-    }
-    int stores = 0;
-    if (cc.kt == cc.nk - 1) {
-      stores = de.template store_tile<MI, MJ>(acc, cc.i0 + wi_u * WI, cc.j0 + wj_u * WJ, cc.split,
-                                              lane, (lds_char_t*)&lds_epi[wave_u][0]);
-#pragma unroll
-      for (int a = 0; a < MI; ++a)
-#pragma unroll
-        for (int b = 0; b < MJ; ++b)
-#pragma unroll
-          for (int v = 0; v < 16; ++v) acc[a][b][v] = 0.0f;
-    }
-    advance(cc);
+  };
+  auto record = [&](int loads, int stores) {
 #pragma unroll
     for (int i = 0; i < NST - 2; ++i) {
       st[i] = st[i + 1];
@@ -655,11 +658,104 @@ gemm_dma_kernel(const GemmArgs g, const Epi epi) {
     }
     st[NST - 2] = stores;
     tot[NST - 2] = loads + stores;
-    // the next step's loads have landed
-    if (cc.valid) wait_vmcnt_rt(younger());
+  };
+
+  auto wait_next = [&]() {
+    const int n = younger();
+    if (n == 0)
+      wait_vmcnt<0>();
+    else
+      wait_vmcnt_rt(n);
+  };
+  auto epilogue = [&](int ti0, int tj0, int tsplit) {
+    const int stores = de.template store_tile<MI, MJ>(acc, ti0 + wi_u * WI, tj0 + wj_u * WJ, tsplit,
+                                                      lane, (lds_char_t*)&lds_epi[wave_u][0]);
+#pragma unroll
+    for (int a = 0; a < MI; ++a)
+#pragma unroll
+      for (int b = 0; b < MJ; ++b)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[a][b][v] = 0.0f;
+    return stores;
+  };
+
+  int stage = 0;
+  if constexpr (!kRotate) {
+    while (cc.valid) {
+      // the stage of step k + NST - 1 was last read in step k - 1, which every
+      // wavefront has finished (barrier below): refill it
+      int loads = 0;
+      if (lc.valid) {
+        issue(lc, stage == 0 ? NST - 1 : stage - 1);
+        advance(lc);
+        loads = my_loads;
+      }
+      // the first sub-step's reads, then in each sub-step the next one's reads
+      // spread between its MFMAs
+      read_sub(std::integral_constant<int, 0>{}, stage, 0);
+      static_for<KS>([&](auto tc) {
+        constexpr int t = decltype(tc)::value;
+        if constexpr (t + 1 < KS) read_sub(std::integral_constant<int, (t + 1) & 1>{}, stage, t + 1);
+        mfma_sub(std::integral_constant<int, t & 1>{});
+      });
+      __builtin_amdgcn_sched_group_barrier(0x100, RD, 0);
+      static_for<KS - 1>([&](auto) { interleave(); });
+      static_for<NM>([&](auto) { __builtin_amdgcn_sched_group_barrier(0x008, 1, 0); });
+      int stores = 0;
+      if (cc.kt == cc.nk - 1) stores = epilogue(cc.i0, cc.j0, cc.split);
+      advance(cc);
+      record(loads, stores);
+      // the next step's loads have landed
+      if (cc.valid) wait_next();
+      __builtin_amdgcn_s_barrier();
+      lds_fence();
+      stage = stage == NST - 1 ? 0 : stage + 1;
+    }
+    wait_vmcnt<0>();
+    return;
+  }
+  {
+    int loads = 0;
+    if (lc.valid) {
+      issue(lc, NST - 1);
+      advance(lc);
+      loads = my_loads;
+    }
+    record(loads, 0);
+  }
+  read_sub(std::integral_constant<int, 0>{}, 0, 0);
+  while (true) {
+    static_for<KS - 1>([&](auto tc) {
+      constexpr int t = decltype(tc)::value;
+      read_sub(std::integral_constant<int, (t + 1) & 1>{}, stage, t + 1);
+      mfma_sub(std::integral_constant<int, t & 1>{});
+    });
+    static_for<KS - 1>([&](auto) { interleave(); });
+    const bool tile_end = cc.kt == cc.nk - 1;
+    const int ti0 = cc.i0, tj0 = cc.j0, tsplit = cc.split;
+    advance(cc);
+    // every fragment read of this stage is done before the barrier lets the
+    // stage be refilled, and the next step's loads have landed (instructions
+    // issued after them: the previous epilogue's stores, if any)
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    if (cc.valid) wait_next();
     __builtin_amdgcn_s_barrier();
     lds_fence();
     stage = stage == NST - 1 ? 0 : stage + 1;
+    int loads = 0;
+    if (lc.valid) {
+      issue(lc, stage == 0 ? NST - 1 : stage - 1);
+      advance(lc);
+      loads = my_loads;
+    }
+    // after the last step the reads fetch stale stage data, never used
+    read_sub(std::integral_constant<int, 0>{}, stage, 0);
+    mfma_sub(std::integral_constant<int, 1>{});
+    interleave();
+    int stores = 0;
+    if (tile_end) stores = epilogue(ti0, tj0, tsplit);
+    record(loads, stores);
+    if (!cc.valid) break;
   }
   wait_vmcnt<0>();
 }
