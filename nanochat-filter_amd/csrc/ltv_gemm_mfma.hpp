@@ -321,10 +321,6 @@ gemm_bf16_kernel(const GemmArgs g, const Epi epi) {
       __builtin_amdgcn_sched_barrier(0);
     });
   };
-  auto compute = [&](const bf16_t* lp, const bf16_t* lq) {
-    ktile(lp, lq, nullptr, nullptr, false, [] {});
-  };
-
   auto load = [&](const GemmCursor& c) {
     if (c.kt == 0) {
       sp.setup(g.P, c.i0);
