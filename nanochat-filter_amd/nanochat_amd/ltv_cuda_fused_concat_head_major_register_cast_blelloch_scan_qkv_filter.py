@@ -42,6 +42,24 @@ from nanochat_amd.ops.ltv_cuda_ops import (
 )
 
 
+class _BatchSharedInits(torch.autograd.Function):
+    """``init_param`` (H, D) as the bf16 inits of every sequence: its bf16
+    rounding broadcast to (B, H, D) as a view with batch stride 0, which the
+    scan kernels read in place.  The gradient is the batch sum of the (B, H, D)
+    bf16 inits gradient, accumulated in float32: what the cast's and the
+    broadcast's backward compute (``init_param.expand(B, H, D).to(bfloat16)``),
+    in one reduction instead of a cast, a (B, H, D) copy and a reduction."""
+
+    @staticmethod
+    def forward(ctx, init_param, B):
+        ctx.param_dtype = init_param.dtype
+        return init_param.to(torch.bfloat16).unsqueeze(0).expand(B, -1, -1)
+
+    @staticmethod
+    def backward(ctx, grad):
+        return grad.sum(0, dtype=torch.float32).to(ctx.param_dtype), None
+
+
 class LtvCudaFusedConcatHeadMajorRegisterCastBlellochScanQkvFilter(
     LtvCombinedHeadMajorQkvFilter
 ):
@@ -68,18 +86,24 @@ class LtvCudaFusedConcatHeadMajorRegisterCastBlellochScanQkvFilter(
         compute_dtype = torch.float32 if run_ltv_in_fp32 else x.dtype
         if compute_dtype == torch.bfloat16 and x.size(1) == 1 and not torch.is_grad_enabled():
             return self._decode_bf16(x, previous_values)
-        inits = resolve_inits_original_dtype(B, self.init_param, previous_values)
         if compute_dtype == torch.bfloat16:
+            if previous_values.q is None:
+                inits = _BatchSharedInits.apply(self.init_param, B)
+            else:
+                inits = resolve_inits_original_dtype(B, self.init_param, previous_values).to(
+                    dtype=torch.bfloat16).contiguous()
             return self._forward_bf16(x, inits)
+        inits = resolve_inits_original_dtype(B, self.init_param, previous_values)
         if compute_dtype != torch.float32:
             raise TypeError(f"LTV filter computes in bfloat16 or float32, not {compute_dtype}")
         return self._forward_fp32(x, inits)
 
     def _forward_bf16(self, x, inits):
+        """inits: (B, H, D) bf16, contiguous or the batch-shared view."""
         hq, hk, hv, _, _, _ = torch.ops.nanochat_amd.qkv_filter(
             x.to(torch.bfloat16).contiguous(),
             self.c.weight,
-            inits.to(dtype=torch.bfloat16).contiguous(),
+            inits,
             self.logit_bias.float().contiguous(),
             self.n_head,
             self.n_kv_head,
