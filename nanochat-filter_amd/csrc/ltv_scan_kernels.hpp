@@ -294,8 +294,18 @@ __device__ __forceinline__ Rsrc make_rsrc(const void* base) {
 // streaming writes), so everything else stores normally.
 constexpr int kStNormal = 0;
 constexpr int kStStream = 2;
+// Load cache policy, the same bits: kLdStream (`nt`) marks data read once.
+// Measured on MI355X at d12: the backward's value, output-gradient and state
+// loads as streaming take it from 125 to 117 us, and the grad_x GEMM that
+// follows it from 135 to 122 us (the grad_combined it reads stays cached);
+// the forwards lose with them (configs[1] 95 -> 104 us, the look-back
+// window kernels 67 -> 72 and 176 -> 179 us), so only the tile backward
+// streams its loads.
+constexpr int kLdNormal = 0;
+constexpr int kLdStream = 2;
+template <int AUX = kLdNormal>
 __device__ __forceinline__ uint4 bld128(Rsrc r, uint32_t off) {
-  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, AUX));
 }
 template <int AUX = kStNormal>
 __device__ __forceinline__ void bst128(Rsrc r, uint32_t off, uint4 x) {
@@ -327,12 +337,12 @@ __device__ __forceinline__ void static_loop(F&& f) {
 }
 
 // One element as raw bits (bf16: the 16 bits; fp32: the word) and its store.
-template <typename TIO>
+template <typename TIO, int AUX = kLdNormal>
 __device__ __forceinline__ uint32_t bld1(Rsrc r, uint32_t off) {
   if constexpr (sizeof(TIO) == 2)
-    return __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
+    return __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, AUX);
   else
-    return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+    return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, AUX);
 }
 template <typename TIO, int AUX = kStNormal>
 __device__ __forceinline__ void bst1(Rsrc r, uint32_t off, float x) {
@@ -345,15 +355,15 @@ __device__ __forceinline__ void bst1(Rsrc r, uint32_t off, float x) {
 
 // V channels at byte offset off, scb bytes apart; channels >= nvalid and
 // lanes with ok == false read 0.
-template <typename TIO, bool VEC>
+template <typename TIO, bool VEC, int AUX = kLdNormal>
 __device__ __forceinline__ uint4 bld_vec(Rsrc r, uint32_t off, uint32_t scb, int nvalid, bool ok) {
-  if (VEC) return bld128(r, ok ? off : kOob);
+  if (VEC) return bld128<AUX>(r, ok ? off : kOob);
   constexpr int V = Pack<TIO>::V;
   off = opaque(off);
   uint32_t w[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
   for (int v = 0; v < V; ++v)
-    Pack<TIO>::put_raw(w, v, bld1<TIO>(r, ok && v < nvalid ? off + v * scb : kOob));
+    Pack<TIO>::put_raw(w, v, bld1<TIO, AUX>(r, ok && v < nvalid ? off + v * scb : kOob));
   return make_uint4(w[0], w[1], w[2], w[3]);
 }
 
@@ -909,16 +919,17 @@ scan_bwd_kernel(const BwdArgs args) {
     for (int s = 0; s < L; ++s) {
       const int t = t0 + s;
       const bool ok = tile_ok && t < t_hi;
-      nu[buf][s] = bld_vec<TIO, VEC>(ur, uoff + s * ustb, uscb, nvalid, ok);
-      ng[buf][s] = bld_vec<TIO, VEC>(gr, goff + s * gstb, gscb, nvalid, ok && (!LB || t >= t_st));
+      nu[buf][s] = bld_vec<TIO, VEC, kLdStream>(ur, uoff + s * ustb, uscb, nvalid, ok);
+      ng[buf][s] = bld_vec<TIO, VEC, kLdStream>(gr, goff + s * gstb, gscb, nvalid,
+                                                ok && (!LB || t >= t_st));
     }
     // exactly one of the sources is unmasked; the others read 0
     const bool ok0 = tile_ok && t0 < t_hi;
     const bool from_init = ok0 && t0 == t_base;
     const bool from_wst = LB && ok0 && !from_init && t0 - 1 < t_st;
     const bool from_h = ok0 && !from_init && !from_wst;
-    nh0[buf] = bld_vec<TIO, VEC>(make_rsrc(hbh + (int64_t)(Tt - 1) * hs[2] * E), hoff, hscb,
-                                 nvalid, from_h);
+    nh0[buf] = bld_vec<TIO, VEC, kLdStream>(make_rsrc(hbh + (int64_t)(Tt - 1) * hs[2] * E), hoff,
+                                            hscb, nvalid, from_h);
     ni0[buf] = bld_vec<TIO, VEC>(irs, ioff, iscb, nvalid, from_init);
     if constexpr (LB)
       nw0[buf] = bld_vec<TIO, VEC>(make_rsrc(wsbh + (int64_t)(Tt - 1 - t_base) * S.D * E), woff,
