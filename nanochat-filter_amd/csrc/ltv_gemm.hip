@@ -119,7 +119,7 @@ reduce_splits_kernel(const float* __restrict__ part, TO* __restrict__ out, int S
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n;
        i += (int64_t)gridDim.x * 256) {
     float acc = 0.0f;
-    for (int s = 0; s < S; ++s) acc += part[(int64_t)s * split_stride + i];
+    for (int s = 0; s < S; ++s) acc += __builtin_nontemporal_load(&part[(int64_t)s * split_stride + i]);
     io_traits<TO>::store(out + i, acc);
   }
 }
@@ -136,7 +136,8 @@ __global__ void dw_reduce_kernel(const float* __restrict__ part, float* __restri
     const int h = f / (D + Da), e = f % (D + Da);
     const int fpk = e < D ? h * D + e : H * D + h * Da + (e - D);
     float acc = 0.0f;
-    for (int s = 0; s < S; ++s) acc += part[(int64_t)s * split_stride + (int64_t)fpk * C + c];
+    for (int s = 0; s < S; ++s)
+      acc += __builtin_nontemporal_load(&part[(int64_t)s * split_stride + (int64_t)fpk * C + c]);
     gw[i] = acc;
   }
 }
@@ -144,7 +145,16 @@ __global__ void dw_reduce_kernel(const float* __restrict__ part, float* __restri
 // The same sum, 4 columns per thread (C % 4 == 0, 16-byte aligned buffers,
 // F * C < 2^31): 16-byte loads and stores, 32-bit index arithmetic, and the
 // partials' loads issued 8 at a time.  The additions run in the same order
-// (s = 0 .. S - 1 from 0), so the result is bit-identical.
+// (s = 0 .. S - 1 from 0), so the result is bit-identical.  The partials are
+// read once: streaming (nt) loads keep them from evicting what the next
+// kernels read (measured at d12: the next step's forward GEMM and scan
+// 2-3 us faster).
+__device__ __forceinline__ float4 ld_stream4(const float4* p) {
+  typedef float f4_t __attribute__((ext_vector_type(4)));
+  const f4_t q = __builtin_nontemporal_load(reinterpret_cast<const f4_t*>(p));
+  return make_float4(q[0], q[1], q[2], q[3]);
+}
+
 __global__ void __launch_bounds__(256)
 dw_reduce4_kernel(const float4* __restrict__ part, float4* __restrict__ gw, int S,
                   int64_t split_stride4, int H, int D, int Da, int C4) {
@@ -160,7 +170,7 @@ dw_reduce4_kernel(const float4* __restrict__ part, float4* __restrict__ gw, int 
     for (; s + 8 <= S; s += 8) {
       float4 v[8];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) v[j] = p[(int64_t)(s + j) * split_stride4];
+      for (int j = 0; j < 8; ++j) v[j] = ld_stream4(&p[(int64_t)(s + j) * split_stride4]);
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         acc.x += v[j].x;
@@ -170,7 +180,7 @@ dw_reduce4_kernel(const float4* __restrict__ part, float4* __restrict__ gw, int 
       }
     }
     for (; s < S; ++s) {
-      const float4 v = p[(int64_t)s * split_stride4];
+      const float4 v = ld_stream4(&p[(int64_t)s * split_stride4]);
       acc.x += v.x;
       acc.y += v.y;
       acc.z += v.z;
