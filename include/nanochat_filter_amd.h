@@ -45,7 +45,7 @@ extern "C" {
 #define LTV_ERR_HIP 3
 #define LTV_ERR_WORKSPACE 4
 
-/* Version of this ABI (bumped on any signature change or addition): 3. */
+/* Version of this ABI (bumped on any signature change or addition): 4. */
 int ltv_abi_version(void);
 
 /* Message of the last failing call on this host thread ("" if none). */
@@ -72,6 +72,43 @@ int ltv_hm_scan_forward(int dtype, const void* combined, const int64_t combined_
                         void* out_k, const int64_t out_k_strides[4], void* out_v,
                         const int64_t out_v_strides[4], int B, int T, int NH, int NKVH, int Da,
                         int r, int use_sigmoid, void* stream);
+
+/* ------------------------------------------------------------------------
+ * ltv_hm_scan_forward with a chain workspace: the same scan and results,
+ * computed by workgroups that each own one chunk of T and hand the state at
+ * the chunk's end to the next chunk through `chain_workspace` (one pass over
+ * HBM, with parallelism over T as well as over (b, head); long sequences at
+ * small batch are the case it is for).
+ *
+ * chain_workspace: 256-byte aligned device memory of at least
+ *   ltv_hm_scan_forward_chain_workspace_size(...) bytes, ALL ZERO before the
+ *   first call.  Every call leaves it all zero again, so one zeroed buffer
+ *   serves all later calls on one stream, in a captured HIP graph too; calls
+ *   that overlap in time (other streams) need buffers of their own.
+ *   NULL selects the kernel of ltv_hm_scan_forward.  The chained kernel is
+ *   used where it is the faster one: fewer than 1,024 (b, head, channel slab)
+ *   sequences, 16-byte channel vectors, gate groups of whole lanes or r = 1;
+ *   elsewhere the size query returns 0 and a workspace passed is not
+ *   touched.  (LTV_SCAN_CHAIN_CFG="CL,L,NW" forces it, "0" turns it off.)
+ *   The workspace's second
+ *   32-bit word becomes nonzero only if a chunk's wait ran past its bound
+ *   (never expected; the outputs of that call are then invalid and the buffer
+ *   must be zeroed again).
+ *
+ * Replaces the same reference forward as ltv_hm_scan_forward; the workspace
+ * has no counterpart there (the reference walks T serially per block,
+ * cpp_ewma/src/ltv_fused_concat_head_major_register_cast_blelloch_scan_cuda_forward.cu:157-220).
+ * ---------------------------------------------------------------------- */
+size_t ltv_hm_scan_forward_chain_workspace_size(int dtype, int B, int T, int NH, int NKVH, int Da,
+                                                int r);
+
+int ltv_hm_scan_forward_ws(int dtype, const void* combined, const int64_t combined_strides[3],
+                           const void* inits, const int64_t inits_strides[3],
+                           const float* logit_bias, void* out_q, const int64_t out_q_strides[4],
+                           void* out_k, const int64_t out_k_strides[4], void* out_v,
+                           const int64_t out_v_strides[4], void* chain_workspace,
+                           size_t chain_workspace_bytes, int B, int T, int NH, int NKVH, int Da,
+                           int r, int use_sigmoid, void* stream);
 
 /* Workspace bytes needed by ltv_hm_scan_backward / ltv_hm_scan_backward_split. */
 size_t ltv_hm_scan_backward_workspace_size(int dtype, int B, int T, int NH, int NKVH, int Da,
@@ -193,6 +230,17 @@ int ltv_hm_look_back_scan_forward_split(
     const float* logit_bias, void* out_q, const int64_t out_q_strides[4], void* out_k,
     const int64_t out_k_strides[4], void* out_v, const int64_t out_v_strides[4], int B, int T,
     int NH, int NKVH, int Da, int r, int P, int Q, int K, int use_sigmoid, void* stream);
+
+/* ltv_hm_look_back_scan_forward_split with the chain workspace of
+ * ltv_hm_scan_forward_ws (same contract), used when there is one window (P >= T);
+ * with several windows the workspace is not touched. */
+int ltv_hm_look_back_scan_forward_split_ws(
+    int dtype, const void* values, const int64_t values_strides[4], const void* logits,
+    const int64_t logits_strides[4], const void* inits, const int64_t inits_strides[3],
+    const float* logit_bias, void* out_q, const int64_t out_q_strides[4], void* out_k,
+    const int64_t out_k_strides[4], void* out_v, const int64_t out_v_strides[4],
+    void* chain_workspace, size_t chain_workspace_bytes, int B, int T, int NH, int NKVH, int Da,
+    int r, int P, int Q, int K, int use_sigmoid, void* stream);
 
 int ltv_hm_look_back_scan_backward_split(
     int dtype, const void* values, const int64_t values_strides[4], const void* logits,

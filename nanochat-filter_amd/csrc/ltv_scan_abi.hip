@@ -59,6 +59,12 @@ int scan_launch_fwd(bool bf16, const FwdArgs& a, ScanCfg cfg, int grid, bool vec
               : scan_fwd_launch_f32(a, cfg, grid, vec, gm, st);
 }
 
+int scan_launch_fwd_chain(bool bf16, const FwdArgs& a, const ChainArgs& ch, ScanCfg cfg, int gm,
+                          hipStream_t st) {
+  return bf16 ? scan_fwd_chain_launch_bf16(a, ch, cfg, gm, st)
+              : scan_fwd_chain_launch_f32(a, ch, cfg, gm, st);
+}
+
 int scan_launch_bwd(bool bf16, const BwdArgs& a, ScanCfg cfg, int grid, bool vec, int gm,
                     bool lb, hipStream_t st) {
   return bf16 ? scan_bwd_launch_bf16(a, cfg, grid, vec, gm, lb, st)
@@ -212,6 +218,9 @@ inline bool vec_ok(const void* p, const int64_t* s, int nd_outer, int V) {
 // LTV_SCAN_BWD_CFG="L,NW" (the backward always spans the whole head).
 struct ScanTuning {
   int fwd_cl = 0, fwd_l = 0, fwd_nw = 0;
+  // LTV_SCAN_CHAIN_CFG="CL,L,NW" (chained forward shape) or "0" (tile kernel only)
+  int chain_cl = 0, chain_l = 0, chain_nw = 0;
+  bool chain = true;
   int bwd_l = 0, bwd_nw = 0;
   int bwd_chunks = 0;  // time chunks per (b, h) in the backward; 0 = automatic
   bool lb_short = true;  // LTV_SCAN_LB_SHORT=0: look-back windows through the tile kernels
@@ -220,6 +229,12 @@ struct ScanTuning {
     if (const char* e = getenv("LTV_SCAN_BWD_CHUNKS")) bwd_chunks = atoi(e) > 0 ? atoi(e) : 0;
     if (const char* e = getenv("LTV_SCAN_FWD_CFG")) {
       if (sscanf(e, "%d,%d,%d", &fwd_cl, &fwd_l, &fwd_nw) != 3) fwd_cl = fwd_l = fwd_nw = 0;
+    }
+    if (const char* e = getenv("LTV_SCAN_CHAIN_CFG")) {
+      if (sscanf(e, "%d,%d,%d", &chain_cl, &chain_l, &chain_nw) != 3) {
+        chain_cl = chain_l = chain_nw = 0;
+        chain = atoi(e) != 0;
+      }
     }
     if (const char* e = getenv("LTV_SCAN_BWD_CFG")) {
       if (sscanf(e, "%d,%d", &bwd_l, &bwd_nw) != 2) bwd_l = bwd_nw = 0;
@@ -313,6 +328,61 @@ int check_pqk(int P, int Q, int K) {
   return LTV_OK;
 }
 
+// The chained forward (scan_fwd_chain_kernel): its launch shape for a head of
+// D channels with gate groups of r, or CL = 0 where it is not used.  It needs
+// the full recurrence, 16-byte channel vectors and one gate per lane or r == 1,
+// and it is chosen where the tile kernel would run fewer than 1,024
+// workgroups (long T at small batch).  Measured on MI355X:
+//   configs[4] prefill (B = 8, T = 8192, 288 sequences): tile 172 us, chained
+//     (8, 8, 8) 127 us, (8, 16, 4) 128 us, (8, 8, 4) 145 us, (8, 4, 8) 135 us;
+//   d12 (1,152 sequences, T = 1024): tile 62.6 us, chained (8, 8, 8) 66.6 us,
+//     (8, 16, 4) 70.4 us -- with every sequence's workgroup resident the tile
+//     kernel streams without per-chunk start-up;
+//   configs[1] (r = 1, 1,152 sequences): tile 99.6 us, chained (8, 8, 4)
+//     96.5 us, (8, 4, 4) 128 us.
+// Chunks shorter than 256 steps lose to the per-workgroup start-up (ticket,
+// two barriers, the hand-off): (8, 4, 4) 124 us, (8, 2, 4) 222 us at d12.
+// LTV_SCAN_CHAIN_CFG="CL,L,NW" forces the chained kernel with that shape.
+struct ChainPlan {
+  ScanCfg cfg;
+  int gm, nslab, nchunk;
+  int64_t nseq;
+  size_t bytes;  // workspace: header + tagged states
+};
+constexpr size_t kChainHeader = 256;
+
+ChainPlan chain_plan(int dtype, int B, int T, int H, int Da, int r) {
+  ChainPlan p{{0, 0, 0}, -1, 0, 0, 0, 0};
+  const ScanTuning& tu = tuning();
+  const int V = dtype == LTV_DTYPE_BF16 ? 8 : 4;
+  const int D = Da * r;
+  if (!tu.chain || B <= 0 || T <= 0 || H <= 0 || D % V != 0) return p;
+  int gm = -1;
+  if (r % V == 0) gm = GATE_LANE;
+  else if (r == 1) gm = GATE_CHANVEC;
+  else return p;
+  ScanCfg c{8, 8, 8};
+  if (gm == GATE_CHANVEC) c = ScanCfg{8, 8, 4};
+  if (tu.chain_cl > 0) {
+    c = ScanCfg{tu.chain_cl, tu.chain_l, tu.chain_nw};
+  } else {
+    // the tile kernel's workgroups: slabs of up to 8 channel lanes
+    const int cl_full = next_pow2(D / V);
+    const int fcl = cl_full < 8 ? cl_full : 8;
+    const int64_t tile_wgs = (int64_t)B * H * ((D + fcl * V - 1) / (fcl * V));
+    if (tile_wgs >= 1024) return p;
+  }
+  if (c.CL * V > 64 || c.CL < 1 || c.L < 1 || c.NW < 1) return p;
+  const int TW = c.NW * (64 / c.CL) * c.L;
+  p.cfg = c;
+  p.gm = gm;
+  p.nslab = (D + c.CL * V - 1) / (c.CL * V);
+  p.nchunk = (int)(((int64_t)T + TW - 1) / TW);
+  p.nseq = (int64_t)B * H * p.nslab;
+  p.bytes = kChainHeader + (size_t)p.nseq * (size_t)(p.nchunk - 1) * (size_t)(c.CL * V) * 8u;
+  return p;
+}
+
 // Forward launch over B * H * nwin windows x channel slabs (a.P/Q/K/nwin, and
 // a.wst / a.kw for the warm-up mode, already set): gate mode and launch shape.
 int launch_forward(int dtype, FwdArgs& a, bool vec, const HostView4& lg, int B, int T, int NH,
@@ -352,7 +422,7 @@ int launch_forward(int dtype, FwdArgs& a, bool vec, const HostView4& lg, int B, 
 int scan_forward_impl(int dtype, const HostView4& u, const HostView4& lg, const HostView4& init,
                       const float* bias, void* const outp[3], const int64_t* const outs[3], int B,
                       int T, int NH, int NKVH, int Da, int r, int P, int Q, int K,
-                      int use_sigmoid, hipStream_t st) {
+                      int use_sigmoid, void* chain_ws, size_t chain_ws_bytes, hipStream_t st) {
   int rc = check_shape(dtype, B, T, NH, NKVH, Da, r);
   if (rc) return rc;
   rc = check_pqk(P, Q, K);
@@ -404,6 +474,27 @@ int scan_forward_impl(int dtype, const HostView4& u, const HostView4& lg, const 
       if ((i == 0 ? NH : NKVH) > 0)
         buf = buf && view_span_bytes(outs[i], 1, 1, T, D, E) <= kBufSpanMax;
     return scan_launch_lb_short_fwd(dtype == LTV_DTYPE_BF16, a, vec, gm, buf, st);
+  }
+  if (a.nwin == 1 && chain_ws != nullptr) {
+    const ChainPlan pl = chain_plan(dtype, B, T, H, Da, r);
+    const bool lg_ok = pl.gm == GATE_LANE || (pl.gm == GATE_CHANVEC && chanvec_ok(r, D, V, lg));
+    if (pl.cfg.CL > 0 && vec && lg_ok) {
+      LTV_REQUIRE(chain_ws_bytes >= pl.bytes, LTV_ERR_WORKSPACE,
+                  "chained scan workspace too small: %zu bytes, need %zu", chain_ws_bytes,
+                  pl.bytes);
+      LTV_REQUIRE((reinterpret_cast<uintptr_t>(chain_ws) & 255u) == 0, LTV_ERR_INVALID_ARG,
+                  "chained scan workspace must be 256-byte aligned");
+      a.sh = ScanShape{B, T, NH, NKVH, Da, r, D, H, pl.nslab, use_sigmoid};
+      ChainArgs ch;
+      ch.ticket = reinterpret_cast<uint32_t*>(chain_ws);
+      ch.err = reinterpret_cast<uint32_t*>(chain_ws) + 1;
+      ch.words = reinterpret_cast<unsigned long long*>(reinterpret_cast<char*>(chain_ws) +
+                                                       kChainHeader);
+      LTV_REQUIRE(pl.nseq * pl.nchunk < (1ll << 31), LTV_ERR_UNSUPPORTED, "grid too large");
+      ch.nseq = (int)pl.nseq;
+      ch.nchunk = pl.nchunk;
+      return scan_launch_fwd_chain(dtype == LTV_DTYPE_BF16, a, ch, pl.cfg, pl.gm, st);
+    }
   }
   return launch_forward(dtype, a, vec, lg, B, T, NH, NKVH, Da, r, use_sigmoid, st);
 }
@@ -751,7 +842,7 @@ extern "C" int ltv_hm_look_back_scan_forward(
   return scan_forward_impl(dtype, values_view(combined, combined_strides, D, Da),
                            logits_view(combined, combined_strides, D, Da, es),
                            view3(inits, inits_strides), logit_bias, outp, outs, B, T, NH, NKVH,
-                           Da, r, P, Q, K, use_sigmoid, (hipStream_t)stream);
+                           Da, r, P, Q, K, use_sigmoid, nullptr, 0, (hipStream_t)stream);
 }
 
 extern "C" int ltv_hm_scan_forward(int dtype, const void* combined,
@@ -780,7 +871,7 @@ extern "C" int ltv_hm_look_back_scan_forward_split(
   const int64_t* outs[3] = {out_q_strides, out_k_strides, out_v_strides};
   return scan_forward_impl(dtype, view4(values, values_strides), view4(logits, logits_strides),
                            view3(inits, inits_strides), logit_bias, outp, outs, B, T, NH, NKVH,
-                           Da, r, P, Q, K, use_sigmoid, (hipStream_t)stream);
+                           Da, r, P, Q, K, use_sigmoid, nullptr, 0, (hipStream_t)stream);
 }
 
 extern "C" int ltv_hm_scan_forward_split(
@@ -793,6 +884,52 @@ extern "C" int ltv_hm_scan_forward_split(
       dtype, values, values_strides, logits, logits_strides, inits, inits_strides, logit_bias,
       out_q, out_q_strides, out_k, out_k_strides, out_v, out_v_strides, B, T, NH, NKVH, Da, r,
       kUnboundedP, 1, 1, use_sigmoid, stream);
+}
+
+extern "C" size_t ltv_hm_scan_forward_chain_workspace_size(int dtype, int B, int T, int NH,
+                                                          int NKVH, int Da, int r) {
+  if (check_shape(dtype, B, T, NH, NKVH, Da, r) != LTV_OK) return 0;
+  return chain_plan(dtype, B, T, NH + 2 * NKVH, Da, r).bytes;
+}
+
+extern "C" int ltv_hm_scan_forward_ws(int dtype, const void* combined,
+                                      const int64_t combined_strides[3], const void* inits,
+                                      const int64_t inits_strides[3], const float* logit_bias,
+                                      void* out_q, const int64_t out_q_strides[4], void* out_k,
+                                      const int64_t out_k_strides[4], void* out_v,
+                                      const int64_t out_v_strides[4], void* chain_workspace,
+                                      size_t chain_workspace_bytes, int B, int T, int NH,
+                                      int NKVH, int Da, int r, int use_sigmoid, void* stream) {
+  LTV_REQUIRE(combined_strides && inits_strides && out_q_strides && out_k_strides &&
+                  out_v_strides,
+              LTV_ERR_INVALID_ARG, "null stride array");
+  const int D = Da * r;
+  const int es = dtype == LTV_DTYPE_BF16 ? 2 : 4;
+  void* outp[3] = {out_q, out_k, out_v};
+  const int64_t* outs[3] = {out_q_strides, out_k_strides, out_v_strides};
+  return scan_forward_impl(dtype, values_view(combined, combined_strides, D, Da),
+                           logits_view(combined, combined_strides, D, Da, es),
+                           view3(inits, inits_strides), logit_bias, outp, outs, B, T, NH, NKVH,
+                           Da, r, kUnboundedP, 1, 1, use_sigmoid, chain_workspace,
+                           chain_workspace_bytes, (hipStream_t)stream);
+}
+
+extern "C" int ltv_hm_look_back_scan_forward_split_ws(
+    int dtype, const void* values, const int64_t values_strides[4], const void* logits,
+    const int64_t logits_strides[4], const void* inits, const int64_t inits_strides[3],
+    const float* logit_bias, void* out_q, const int64_t out_q_strides[4], void* out_k,
+    const int64_t out_k_strides[4], void* out_v, const int64_t out_v_strides[4],
+    void* chain_workspace, size_t chain_workspace_bytes, int B, int T, int NH, int NKVH, int Da,
+    int r, int P, int Q, int K, int use_sigmoid, void* stream) {
+  LTV_REQUIRE(values_strides && logits_strides && inits_strides && out_q_strides &&
+                  out_k_strides && out_v_strides,
+              LTV_ERR_INVALID_ARG, "null stride array");
+  void* outp[3] = {out_q, out_k, out_v};
+  const int64_t* outs[3] = {out_q_strides, out_k_strides, out_v_strides};
+  return scan_forward_impl(dtype, view4(values, values_strides), view4(logits, logits_strides),
+                           view3(inits, inits_strides), logit_bias, outp, outs, B, T, NH, NKVH,
+                           Da, r, P, Q, K, use_sigmoid, chain_workspace, chain_workspace_bytes,
+                           (hipStream_t)stream);
 }
 
 extern "C" size_t ltv_hm_look_back_scan_backward_workspace_size(int dtype, int B, int T, int NH,

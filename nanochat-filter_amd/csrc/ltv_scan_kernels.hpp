@@ -761,6 +761,263 @@ scan_fwd_kernel(const FwdArgs args) {
 }
 
 // ---------------------------------------------------------------------------
+// Forward with chained chunk states (one pass over HBM, parallel over T)
+// ---------------------------------------------------------------------------
+// Each workgroup scans one chunk of TW = NW * TG * L steps of one (b, head,
+// channel slab) sequence, holding all of the chunk's values and logits in
+// registers, so the grid grows with T instead of one workgroup walking all of
+// T (the tile kernel above).  The state entering chunk c is the state leaving
+// chunk c - 1: that chunk's workgroup publishes it as soon as it has its own
+// entering state, so only this short hand-off is sequential.
+//   * Publication: one 64-bit word per channel, fp32 state in the low half and
+//     a nonzero tag in the high half, stored and polled with device-scope
+//     atomics (coherent across the XCDs' L2s).  A word is either absent or
+//     whole, so no fence has to order it against other memory.
+//   * Order: a workgroup takes a ticket from a counter when it starts, and
+//     tickets map chunk-major onto (sequence, chunk).  The chunk a workgroup
+//     waits for holds an earlier ticket, so it is already running and itself
+//     waits only on earlier tickets: every wait ends.  A wait is still bounded
+//     (kChainSpinMax polls, about a second; a chunk's wait is normally a few
+//     microseconds); past the bound the kernel sets *err = 1, goes on with a
+//     zero state and exits normally.
+//   * Zero invariant: the reader of a word clears it, the last chunk of a
+//     sequence publishes nothing, and the workgroup that draws the last ticket
+//     resets the counter, so the workspace is all zeros again when the kernel
+//     ends and a launch needs no clearing pass (nor a memset in a captured
+//     graph).
+// The chunk composes its wavefront totals onto the entering state in the
+// tile kernel's order, so with the same launch shape (CL, L, NW) both kernels
+// give bitwise equal outputs.
+struct ChainArgs {
+  uint32_t* ticket;           // chunk ticket counter (0 between launches)
+  uint32_t* err;              // 1: a wait ran past kChainSpinMax polls; 2: counter not 0 at launch
+  unsigned long long* words;  // (nseq, nchunk - 1, CL * V) tagged states (0 between launches)
+  int nseq;                   // B * H * nslab
+  int nchunk;                 // chunks per sequence
+};
+constexpr int kChainSpinMax = 1 << 20;
+constexpr unsigned long long kChainTag = 1ull << 32;
+
+template <typename TIO, int CL, int L, int NW, bool VEC, int GM>
+__global__ void __launch_bounds__(NW * 64)
+scan_fwd_chain_kernel(const FwdArgs args, const ChainArgs ch) {
+  constexpr int V = Pack<TIO>::V;
+  constexpr int TG = 64 / CL;
+  constexpr int NA = GM == GATE_LANE ? 1 : V;
+  constexpr int TW = NW * TG * L;
+  constexpr int NCH = CL * V;  // channels per slab: one per lane of wavefront 0
+  static_assert(NCH <= 64, "a slab's channels must fit one wavefront");
+  constexpr bool GL = GM == GATE_LANE;
+  const ScanShape& S = args.sh;
+
+  const int lane = threadIdx.x & 63;
+  const int w = threadIdx.x >> 6;
+  const int cl = lane / TG;
+  const int tg = lane % TG;
+
+  __shared__ int lds_ticket;
+  __shared__ float lds_a[NW][CL][NA];
+  __shared__ float4 lds_x[NW][CL][V / 4];
+  __shared__ float lds_c[NCH];  // the state entering the chunk
+
+  if (threadIdx.x == 0) {
+    const uint32_t t =
+        __hip_atomic_fetch_add(ch.ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // every other workgroup has drawn its ticket: leave the counter at 0
+    if (t == gridDim.x - 1)
+      __hip_atomic_store(ch.ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    lds_ticket = (int)t;
+  }
+  __syncthreads();
+  const int ticket = lds_ticket;
+  // a counter that was not zero at the launch (a workspace not zeroed before
+  // its first use) hands out tickets past the grid: such a workgroup only
+  // reports it (the waits of the others end at their bound)
+  if (ticket >= (int)gridDim.x) {
+    if (threadIdx.x == 0) __hip_atomic_store(ch.err, 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return;
+  }
+  const int seq = ticket % ch.nseq;
+  const int chunk = ticket / ch.nseq;
+  const int slab = seq % S.nslab;
+  const int h = (seq / S.nslab) % S.H;
+  const int b = seq / S.nslab / S.H;
+  const int T = S.T;
+  const int Tt = chunk * TW;  // the chunk's first step
+
+  const int c0 = (slab * CL + cl) * V;
+  const int nvalid = min(V, S.D - c0);
+  const bool active = nvalid > 0;
+
+  constexpr int E = sizeof(TIO);
+  int which, hl;
+  head_select(h, S.NH, S.NKVH, which, hl);
+  const HeadView ov = head_view(args.out, which);
+  const char* obh = reinterpret_cast<const char*>(ov.p) +
+                    ((int64_t)b * ov.s[0] + (int64_t)hl * ov.s[1]) * E;
+  const char* ubh = reinterpret_cast<const char*>(args.u.p) +
+                    ((int64_t)b * args.u.s[0] + (int64_t)h * args.u.s[1]) * E;
+  const char* lbh = reinterpret_cast<const char*>(args.lg.p) +
+                    ((int64_t)b * args.lg.s[0] + (int64_t)h * args.lg.s[1]) * E;
+
+  GateIdx<GM, V> gi;
+  gi.init(args.bias + h * S.Da, c0, nvalid, S.D, S.r, args.lg.s[3]);
+  const bool use_sig = S.use_sigmoid != 0;
+
+  const int tl0 = (w * TG + tg) * L;
+  const int t0 = Tt + tl0;
+  const uint32_t ustb = (uint32_t)(args.u.s[2] * E), uscb = (uint32_t)(args.u.s[3] * E);
+  const uint32_t lstb = (uint32_t)(args.lg.s[2] * E), ostb = (uint32_t)(ov.s[2] * E);
+  const uint32_t oscb = (uint32_t)(ov.s[3] * E);
+  const uint32_t uoff = (uint32_t)tl0 * ustb + (uint32_t)c0 * uscb;
+  const uint32_t loff = (uint32_t)tl0 * lstb +
+                        (GM == GATE_CHANVEC ? (uint32_t)c0 * (uint32_t)E : 0u);  // r == 1: j == c
+  const uint32_t ooff = (uint32_t)tl0 * ostb + (uint32_t)c0 * oscb;
+
+  // the whole chunk is loaded at once: L vectors and logits per lane in flight
+  uint4 uq[L];
+  LogitRaw<TIO, GM, L> lr;
+  {
+    const Rsrc ur = make_rsrc(ubh + (int64_t)Tt * args.u.s[2] * E);
+#pragma unroll
+    for (int s = 0; s < L; ++s)
+      uq[s] = bld_vec<TIO, VEC>(ur, uoff + s * ustb, uscb, nvalid, active && (t0 + s) < T);
+    lr.load(make_rsrc(lbh + (int64_t)Tt * args.lg.s[2] * E), loff, lstb, gi, t0, T, active,
+            nvalid);
+  }
+  // chunk 0 enters from the inits (lanes of wavefront 0's first time group
+  // hand them to the chain step through lds_c)
+  if (chunk == 0 && w == 0 && tg == 0) {
+    const TIO* ip = reinterpret_cast<const TIO*>(args.init.p) + (int64_t)b * args.init.s[0] +
+                    (int64_t)h * args.init.s[1] + (int64_t)c0 * args.init.s[3];
+    uint4 q = make_uint4(0u, 0u, 0u, 0u);
+    if (active) q = ld_vec<TIO, VEC>(ip, args.init.s[3], nvalid);
+#pragma unroll
+    for (int v = 0; v < V; ++v) lds_c[cl * V + v] = Pack<TIO>::get(q, v);
+  }
+
+  float al[L][NA];
+  lr.gates(gi, t0, T, active, use_sig, al);
+
+  // level 1: lane-local fold (padded steps have alpha = 0: the identity)
+  float A[NA], X[V];
+#pragma unroll
+  for (int i = 0; i < NA; ++i) A[i] = 1.0f;
+#pragma unroll
+  for (int v = 0; v < V; ++v) X[v] = 0.0f;
+#pragma unroll
+  for (int s = 0; s < L; ++s) {
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      const float a = al[s][GL ? 0 : v];
+      X[v] = fmaf(a, Pack<TIO>::get(uq[s], v) - X[v], X[v]);
+    }
+#pragma unroll
+    for (int i = 0; i < NA; ++i) A[i] = fmaf(-A[i], al[s][i], A[i]);
+  }
+
+  // level 2: inclusive scan over the time-group lanes, then the exclusive prefix
+  SegScan<TG, NA, V, GL>::template up_level<1>(tg, A, X);
+  float Ae[NA], Xe[V];
+#pragma unroll
+  for (int i = 0; i < NA; ++i) {
+    const float t = shift_up<TG, 1>(A[i]);
+    Ae[i] = tg == 0 ? 1.0f : t;
+  }
+#pragma unroll
+  for (int v = 0; v < V; ++v) {
+    const float t = shift_up<TG, 1>(X[v]);
+    Xe[v] = tg == 0 ? 0.0f : t;
+  }
+
+  // level 3: wavefront totals through LDS
+  if (tg == TG - 1) {
+#pragma unroll
+    for (int i = 0; i < NA; ++i) lds_a[w][cl][i] = A[i];
+#pragma unroll
+    for (int q = 0; q < V / 4; ++q)
+      lds_x[w][cl][q] = make_float4(X[4 * q], X[4 * q + 1], X[4 * q + 2], X[4 * q + 3]);
+  }
+  __syncthreads();
+
+  // the chain step: wavefront 0, lane j = slab channel j, takes the entering
+  // state, publishes the leaving one and hands the entering one to the others
+  if (w == 0 && lane < NCH) {
+    const int j = lane;
+    float cin;
+    if (chunk == 0) {
+      cin = lds_c[j];
+    } else {
+      unsigned long long* pw = ch.words + ((int64_t)seq * (ch.nchunk - 1) + chunk - 1) * NCH + j;
+      unsigned long long wv = 0;
+      for (int spin = 0;; ++spin) {
+        wv = __hip_atomic_load(pw, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if ((wv >> 32) != 0) break;
+        if (spin >= kChainSpinMax) {
+          __hip_atomic_store(ch.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          wv = 0;
+          break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+      }
+      __hip_atomic_store(pw, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      cin = __uint_as_float((uint32_t)wv);
+    }
+    if (chunk + 1 < ch.nchunk) {
+      const float* xa = reinterpret_cast<const float*>(&lds_x[0][0][0]);
+      float p = cin;
+#pragma unroll
+      for (int ww = 0; ww < NW; ++ww)
+        p = fmaf(lds_a[ww][j / V][GL ? 0 : j % V], p, xa[ww * NCH + j]);
+      __hip_atomic_store(ch.words + ((int64_t)seq * (ch.nchunk - 1) + chunk) * NCH + j,
+                         kChainTag | __float_as_uint(p), __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+    }
+    lds_c[j] = cin;
+  }
+  __syncthreads();
+
+  // the state entering this wavefront: the chunk's entering state composed
+  // with the totals of the wavefronts before it
+  float hw[V];
+#pragma unroll
+  for (int v = 0; v < V; ++v) hw[v] = lds_c[cl * V + v];
+#pragma unroll
+  for (int ww = 0; ww < NW - 1; ++ww) {
+    if (ww < w) {
+      float Aw[NA];
+#pragma unroll
+      for (int i = 0; i < NA; ++i) Aw[i] = lds_a[ww][cl][i];
+#pragma unroll
+      for (int q = 0; q < V / 4; ++q) {
+        const float4 x4 = lds_x[ww][cl][q];
+        hw[4 * q + 0] = fmaf(Aw[GL ? 0 : 4 * q + 0], hw[4 * q + 0], x4.x);
+        hw[4 * q + 1] = fmaf(Aw[GL ? 0 : 4 * q + 1], hw[4 * q + 1], x4.y);
+        hw[4 * q + 2] = fmaf(Aw[GL ? 0 : 4 * q + 2], hw[4 * q + 2], x4.z);
+        hw[4 * q + 3] = fmaf(Aw[GL ? 0 : 4 * q + 3], hw[4 * q + 3], x4.w);
+      }
+    }
+  }
+
+  // re-run the lane's steps from its exact carry-in and store
+  reload_barrier(uq);
+  const Rsrc orr = make_rsrc(obh + (int64_t)Tt * ov.s[2] * E);
+  float hv[V];
+#pragma unroll
+  for (int v = 0; v < V; ++v) hv[v] = fmaf(Ae[GL ? 0 : v], hw[v], Xe[v]);
+#pragma unroll
+  for (int s = 0; s < L; ++s) {
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      const float a = al[s][GL ? 0 : v];
+      hv[v] = fmaf(a, Pack<TIO>::get(uq[s], v) - hv[v], hv[v]);
+    }
+    bst_vec<TIO, VEC, GM == GATE_CHANVEC ? kStStream : kStNormal>(
+        orr, ooff + s * ostb, oscb, nvalid, active && (t0 + s) < T, hv);
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Backward
 // ---------------------------------------------------------------------------
 // GATE_LANE: r % V == 0; the gate group spans r / V adjacent channel lanes and
@@ -1501,6 +1758,10 @@ struct ScanCfg {
 // Forward: grid = B * H * nslab workgroups of NW * 64 threads.
 int scan_launch_fwd(bool bf16, const FwdArgs& a, ScanCfg cfg, int grid, bool vec, int gm,
                     hipStream_t st);
+// Forward with chained chunk states: grid = nseq * nchunk workgroups (vector
+// accesses only; gate modes GATE_LANE and GATE_CHANVEC).
+int scan_launch_fwd_chain(bool bf16, const FwdArgs& a, const ChainArgs& ch, ScanCfg cfg, int gm,
+                          hipStream_t st);
 // Backward main kernel: grid = B * H * nchunk; CL channel lanes cover the whole
 // head; lb selects the look-back window kernels.
 int scan_launch_bwd(bool bf16, const BwdArgs& a, ScanCfg cfg, int grid, bool vec, int gm,

@@ -51,6 +51,21 @@ bool fwd_dispatch(const FwdArgs& a, int grid, bool vec, int gm, hipStream_t st) 
   return false;
 }
 
+template <typename TIO, int CL, int L, int NW>
+bool fwd_chain_dispatch(const FwdArgs& a, const ChainArgs& ch, int grid, int gm, hipStream_t st) {
+  const dim3 blk(NW * 64);
+  switch (gm) {
+    case GATE_LANE:
+      hipLaunchKernelGGL((scan_fwd_chain_kernel<TIO, CL, L, NW, true, GATE_LANE>), dim3(grid), blk, 0, st, a, ch);
+      return true;
+    case GATE_CHANVEC:
+      hipLaunchKernelGGL((scan_fwd_chain_kernel<TIO, CL, L, NW, true, GATE_CHANVEC>), dim3(grid), blk, 0, st, a, ch);
+      return true;
+    default:
+      return false;
+  }
+}
+
 // The look-back backward is built for the base shapes and for the shape the
 // d12 heads use (16 channel lanes, 4 steps per lane, 2 wavefronts).
 template <int CL, int L, int NW>
@@ -125,6 +140,34 @@ int scan_fwd_launch_t(const FwdArgs& a, ScanCfg c, int grid, bool vec, int gm, h
   return LTV_OK;
 }
 
+// Chained forward shapes (CL, L, NW); a slab's CL * V channels fit one
+// wavefront (CL <= 8 for bf16, <= 16 for fp32).
+#define LTV_SCAN_FWD_CHAIN_CONFIGS(X) \
+  X(8, 16, 4) X(8, 8, 4) X(8, 8, 8) X(8, 4, 4) X(8, 4, 8) X(8, 2, 4)
+
+template <typename TIO>
+int scan_fwd_chain_launch_t(const FwdArgs& a, const ChainArgs& ch, ScanCfg c, int gm,
+                            hipStream_t st) {
+  const int64_t grid = (int64_t)ch.nseq * ch.nchunk;
+  if (grid <= 0 || grid >= (1ll << 31)) {
+    set_error("scan forward (chained): grid of %lld workgroups", (long long)grid);
+    return LTV_ERR_UNSUPPORTED;
+  }
+  bool ok = false;
+#define LTV_X(CL_, L_, NW_)                                                   \
+  if (!ok && c.CL == CL_ && c.L == L_ && c.NW == NW_)                         \
+    ok = detail::fwd_chain_dispatch<TIO, CL_, L_, NW_>(a, ch, (int)grid, gm, st);
+  LTV_SCAN_FWD_CHAIN_CONFIGS(LTV_X)
+#undef LTV_X
+  if (!ok) {
+    set_error("scan forward (chained): launch shape CL=%d L=%d NW=%d (gate=%d) is not built",
+              c.CL, c.L, c.NW, gm);
+    return LTV_ERR_UNSUPPORTED;
+  }
+  LTV_LAUNCH_CHECK();
+  return LTV_OK;
+}
+
 template <typename TIO>
 int scan_bwd_launch_t(const BwdArgs& a, ScanCfg c, int grid, bool vec, int gm, bool lb,
                       hipStream_t st) {
@@ -146,6 +189,10 @@ int scan_bwd_launch_t(const BwdArgs& a, ScanCfg c, int grid, bool vec, int gm, b
 // Per-dtype entry points (defined in the four translation units).
 int scan_fwd_launch_bf16(const FwdArgs& a, ScanCfg c, int grid, bool vec, int gm, hipStream_t st);
 int scan_fwd_launch_f32(const FwdArgs& a, ScanCfg c, int grid, bool vec, int gm, hipStream_t st);
+int scan_fwd_chain_launch_bf16(const FwdArgs& a, const ChainArgs& ch, ScanCfg c, int gm,
+                               hipStream_t st);
+int scan_fwd_chain_launch_f32(const FwdArgs& a, const ChainArgs& ch, ScanCfg c, int gm,
+                              hipStream_t st);
 int scan_bwd_launch_bf16(const BwdArgs& a, ScanCfg c, int grid, bool vec, int gm, bool lb,
                          hipStream_t st);
 int scan_bwd_launch_f32(const BwdArgs& a, ScanCfg c, int grid, bool vec, int gm, bool lb,

@@ -37,6 +37,13 @@ SIGNATURES = {
         [_c_int, _c_vp, _c_i64p, _c_vp, _c_i64p, _c_vp, _c_vp, _c_i64p, _c_vp, _c_i64p, _c_vp,
          _c_i64p, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_vp],
     ),
+    "ltv_hm_scan_forward_chain_workspace_size": (
+        _c_sz, [_c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int]),
+    "ltv_hm_scan_forward_ws": (
+        _c_int,
+        [_c_int, _c_vp, _c_i64p, _c_vp, _c_i64p, _c_vp, _c_vp, _c_i64p, _c_vp, _c_i64p, _c_vp,
+         _c_i64p, _c_vp, _c_sz, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_vp],
+    ),
     "ltv_hm_scan_backward_workspace_size": (
         _c_sz, [_c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int]),
     "ltv_hm_scan_backward": (
@@ -83,6 +90,12 @@ SIGNATURES = {
         [_c_int, _c_vp, _c_i64p, _c_vp, _c_i64p, _c_vp, _c_i64p, _c_vp, _c_vp, _c_i64p, _c_vp,
          _c_i64p, _c_vp, _c_i64p, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
          _c_int, _c_int, _c_int, _c_vp],
+    ),
+    "ltv_hm_look_back_scan_forward_split_ws": (
+        _c_int,
+        [_c_int, _c_vp, _c_i64p, _c_vp, _c_i64p, _c_vp, _c_i64p, _c_vp, _c_vp, _c_i64p, _c_vp,
+         _c_i64p, _c_vp, _c_i64p, _c_vp, _c_sz, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
+         _c_int, _c_int, _c_int, _c_int, _c_vp],
     ),
     "ltv_hm_look_back_scan_backward_split": (
         _c_int,
@@ -207,6 +220,43 @@ def dtype_code(dt: torch.dtype) -> int:
 
 def stream_of(t: torch.Tensor) -> int:
     return torch.cuda.current_stream(t.device).cuda_stream
+
+
+# Chain workspaces of the chained scan forward (ltv_hm_scan_forward_ws): zeroed
+# once, left zeroed by every call, so one buffer per (device, stream) serves
+# every later call on that stream.  Under graph capture each call gets a fresh
+# zeroed buffer from the graph's pool (its zero fill is captured with it).
+_CHAIN_WS: dict = {}
+
+
+def chain_workspace(device: torch.device, nbytes: int):
+    """A 256-byte aligned, all-zero device buffer of at least ``nbytes`` bytes
+    reserved for the chained scan forward on the current stream, or None when
+    nbytes == 0."""
+    if nbytes <= 0:
+        return None
+    n = (nbytes + 255) // 256 * 256
+    if torch.cuda.is_current_stream_capturing():
+        return torch.zeros(n, dtype=torch.uint8, device=device)
+    key = (device.index if device.index is not None else torch.cuda.current_device(),
+           torch.cuda.current_stream(device).cuda_stream)
+    buf = _CHAIN_WS.get(key)
+    if buf is None or buf.numel() < n:
+        buf = torch.zeros(n, dtype=torch.uint8, device=device)
+        _CHAIN_WS[key] = buf
+    return buf
+
+
+def chain_workspace_for(dtype: torch.dtype, device: torch.device, B: int, T: int, NH: int,
+                        NKVH: int, Da: int, r: int):
+    """(pointer, bytes) of the chain workspace for this scan shape, (None, 0)
+    where the chained forward does not apply."""
+    nbytes = lib().ltv_hm_scan_forward_chain_workspace_size(dtype_code(dtype), B, T, NH, NKVH,
+                                                           Da, r)
+    buf = chain_workspace(device, nbytes)
+    if buf is None:
+        return None, 0
+    return buf.data_ptr(), buf.numel()
 
 
 def require_device(*tensors: torch.Tensor) -> None:

@@ -82,7 +82,8 @@ def forward_kernel(
     if T_ != T:
         raise RuntimeError(f"T={T} does not match combined.shape[1]={T_}")
     lib = N.lib()
-    rc = lib.ltv_hm_scan_forward(
+    ws, ws_bytes = N.chain_workspace_for(combined.dtype, combined.device, B, T, NH, NKVH, da, r)
+    rc = lib.ltv_hm_scan_forward_ws(
         N.dtype_code(combined.dtype),
         combined.data_ptr(), N.strides(combined, 3),
         inits.data_ptr(), N.strides(inits, 3),
@@ -90,10 +91,11 @@ def forward_kernel(
         out_q.data_ptr(), _s4(out_q),
         out_k.data_ptr(), _s4(out_k),
         out_v.data_ptr(), _s4(out_v),
+        ws, ws_bytes,
         B, T, NH, NKVH, da, r, int(bool(use_sigmoid)),
         N.stream_of(combined),
     )
-    N.check(rc, "ltv_hm_scan_forward")
+    N.check(rc, "ltv_hm_scan_forward_ws")
 
 
 @torch.library.impl(

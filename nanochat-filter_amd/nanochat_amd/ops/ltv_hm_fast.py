@@ -213,15 +213,17 @@ def scan_forward(values: torch.Tensor, logits: torch.Tensor, inits: torch.Tensor
     else:  # (B, T, >= H Da), column h Da + j
         sb, st_, sl = logits.stride()
         lgs = (sb, Da * sl, st_, sl)
+    ws, ws_bytes = (N.chain_workspace_for(values.dtype, values.device, B, T, NH, NKVH, Da, r)
+                    if P >= T else (None, 0))
     with N.span("scan_fwd"):
-        rc = N.lib().ltv_hm_look_back_scan_forward_split(
+        rc = N.lib().ltv_hm_look_back_scan_forward_split_ws(
             N.dtype_code(values.dtype),
             values.data_ptr(), N.strides(values, 4), logits.data_ptr(), _arr(lgs),
             inits.data_ptr(), N.strides(inits, 3), logit_bias.data_ptr(),
             out[0].data_ptr(), N.strides(out[0], 4), out[1].data_ptr(), N.strides(out[1], 4),
-            out[2].data_ptr(), N.strides(out[2], 4),
+            out[2].data_ptr(), N.strides(out[2], 4), ws, ws_bytes,
             B, T, NH, NKVH, Da, r, P, Q, K, int(bool(use_sigmoid)), N.stream_of(values))
-    N.check(rc, "ltv_hm_look_back_scan_forward_split")
+    N.check(rc, "ltv_hm_look_back_scan_forward_split_ws")
     return out[0], out[1], out[2]
 
 

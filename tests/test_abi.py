@@ -47,12 +47,24 @@ def test_abi_version_and_host_only_queries():
     if not os.path.exists(N.LIB_PATH):
         pytest.skip("library not built")
     lib = N.load()
-    assert lib.ltv_abi_version() == 3
+    assert lib.ltv_abi_version() == 4
     # d12: 18 heads x (128 + 1) = 2322 -> padded to a multiple of 128; 18 logits -> 24
     assert lib.ltv_qkv_packed_width(18, 128, 1) == 2432
     assert lib.ltv_qkv_logit_width(18, 1) == 24
     assert lib.ltv_hm_scan_backward_workspace_size(1, 32, 1024, 6, 6, 1, 128) >= 32 * 18 * 4
     assert lib.ltv_qkv_project_backward_workspace_size(32768, 768, 18, 128, 1) > 0
+    # chained scan forward: 256-byte header + one 8-byte word per channel of
+    # every chunk but a sequence's last.  configs[4] prefill (8 x 18 heads x 2
+    # slabs of 64 channels): 16 chunks of 512 steps; fp32: slabs of 32
+    # channels; d12 (1,152 tile workgroups), gate groups that are neither whole
+    # lanes nor r = 1, or T = 0: no chained kernel
+    assert lib.ltv_hm_scan_forward_chain_workspace_size(1, 8, 8192, 6, 6, 1, 128) == \
+        256 + 8 * 18 * 2 * 15 * 64 * 8
+    assert lib.ltv_hm_scan_forward_chain_workspace_size(0, 2, 1024, 6, 6, 1, 128) == \
+        256 + 2 * 18 * 4 * 1 * 32 * 8
+    assert lib.ltv_hm_scan_forward_chain_workspace_size(1, 32, 1024, 6, 6, 1, 128) == 0
+    assert lib.ltv_hm_scan_forward_chain_workspace_size(1, 2, 64, 1, 1, 32, 4) == 0
+    assert lib.ltv_hm_scan_forward_chain_workspace_size(1, 2, 0, 1, 1, 1, 128) == 0
     # argument errors are reported without touching a device
     rc = lib.ltv_qkv_project_forward(None, None, None, None, 2, 8, 12, 3, 64, 1, None)
     assert rc == 2 and "multiple of 8" in N.last_error()

@@ -1,0 +1,324 @@
+"""GPU parity of the chained scan forward (``ltv_hm_scan_forward_ws`` and the
+split-layout ``ltv_hm_look_back_scan_forward_split_ws``, called here): one
+workgroup per chunk of T, the state at a chunk's end handed to the next
+chunk's workgroup through a zero-invariant workspace.
+
+Checked against the CPU oracle (exact on the reference's integer generators,
+within the stated tolerance with the sigmoid), against the tile kernel (the
+same entry point without a workspace) on the same inputs, for bitwise
+run-to-run equality, and for the workspace contract: all zero after every call, the ticket counter
+back at 0 and no wait past its bound.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+import ltv_oracle as O
+from ltv_test_utils import (TOL, assert_close, int_combined, int_inits, int_logit_bias, io_name,
+                            np_of, to_torch)
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+DTYPES = [torch.bfloat16, torch.float32]
+
+
+def _lib():
+    from nanochat_amd import _native as N
+    return N, N.lib()
+
+
+def _s(t):
+    from nanochat_amd import _native as N
+    return N.strides(t)
+
+
+def _outs(B, T, NH, NKVH, D, dtype):
+    return [torch.full((B, nh, T, D), float("nan"), dtype=dtype, device=DEV)
+            for nh in (NH, NKVH, NKVH)]
+
+
+def _split(comb, NH, NKVH, Da, r):
+    """(B, T, H (D + Da)) -> head-major values (B, H, T, D) and logits
+    (B, H, T, Da), contiguous: the layout the fast path hands the scan, with
+    16-byte channel vectors (the combined layout's heads start at multiples of
+    D + Da columns, which the chained kernel does not take)."""
+    B, T, _ = comb.shape
+    H, D = NH + 2 * NKVH, Da * r
+    x = comb.reshape(B, T, H, D + Da).permute(0, 2, 1, 3)
+    return x[..., :D].contiguous(), x[..., D:].contiguous()
+
+
+UNBOUNDED_P = 2147483647
+
+
+def _forward(comb, ini, bias, NH, NKVH, Da, r, sig, ws=None):
+    """Scan forward of the split layout through the C ABI: the chained kernel
+    with a workspace tensor, the tile kernel without one."""
+    N, lib = _lib()
+    B, T, _ = comb.shape
+    D = Da * r
+    values, logits = _split(comb, NH, NKVH, Da, r)
+    out = _outs(B, T, NH, NKVH, D, comb.dtype)
+    args = [N.dtype_code(comb.dtype), values.data_ptr(), _s(values), logits.data_ptr(),
+            _s(logits), ini.data_ptr(), _s(ini), bias.data_ptr(), out[0].data_ptr(),
+            _s(out[0]), out[1].data_ptr(), _s(out[1]), out[2].data_ptr(), _s(out[2])]
+    tail = [B, T, NH, NKVH, Da, r, UNBOUNDED_P, 1, 1, int(sig), N.stream_of(comb)]
+    if ws is None:
+        rc = lib.ltv_hm_look_back_scan_forward_split(*args, *tail)
+    else:
+        rc = lib.ltv_hm_look_back_scan_forward_split_ws(*args, ws.data_ptr(), ws.numel(), *tail)
+    N.check(rc, "scan forward")
+    return out
+
+
+def _ws_bytes(dtype, B, T, NH, NKVH, Da, r):
+    N, lib = _lib()
+    return lib.ltv_hm_scan_forward_chain_workspace_size(N.dtype_code(dtype), B, T, NH, NKVH, Da, r)
+
+
+def _zero_ws(nbytes):
+    return torch.zeros((nbytes + 255) // 256 * 256, dtype=torch.uint8, device=DEV)
+
+
+def _random_case(B, T, NH, NKVH, Da, r, seed, io, z_mean=2.0, z_std=1.0):
+    rng = np.random.default_rng(seed)
+    H, D = NH + 2 * NKVH, Da * r
+    c = rng.standard_normal((B, T, H, D + Da)).astype(np.float32)
+    c[..., D:] = -(z_mean + z_std * rng.standard_normal((B, T, H, Da)))
+    c = O.round_io(c.reshape(B, T, -1), io)
+    ini = O.round_io(rng.standard_normal((B, H, D)).astype(np.float32), io)
+    bias = (0.1 * rng.standard_normal((H, Da))).astype(np.float32)
+    return c, ini, bias
+
+
+def _assert_same_up_to_association(a, b, dtype, label):
+    """Two kernels that evaluate the same fp32 recurrence in different
+    association orders: their fp32 states differ by a few fp32 rounding errors
+    of the largest state (bound 1e-5 max|b| here), and a bf16 output can then
+    round to the neighbouring value (one bf16 step, <= 2^-7 |b|)."""
+    if b.numel() == 0:
+        return
+    a, b = a.float(), b.float()
+    scale = float(b.abs().max())
+    d = (a - b).abs()
+    step = b.abs() * 2.0 ** -7 if dtype == torch.bfloat16 else torch.zeros_like(b)
+    bad = d > step + 1e-5 * scale
+    assert not bool(bad.any()), (
+        f"{label}: {int(bad.sum())} elements differ beyond association; max |a-b| = "
+        f"{float(d.max()):.3e}, max|b| = {scale:.3e}")
+
+
+def _check_ws_clean(ws, label):
+    torch.cuda.synchronize()
+    nz = int(torch.count_nonzero(ws))
+    assert nz == 0, f"{label}: {nz} nonzero workspace bytes after the call (ticket/err/words)"
+
+
+# T spans one partial chunk, exactly one chunk, and several chunks with a
+# ragged tail, for the d12 gate shape (one gate per head), gate groups of 16
+# channels, and per-channel gates (r = 1).
+CASES = [
+    # (B, T, NH, NKVH, Da, r)
+    (2, 1, 2, 1, 1, 128),
+    (2, 300, 2, 1, 1, 128),
+    (2, 512, 1, 1, 1, 128),
+    (2, 1537, 2, 1, 1, 128),
+    (1, 4133, 1, 1, 8, 16),
+    (2, 700, 1, 1, 64, 1),
+    (1, 129, 1, 0, 128, 1),
+]
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=io_name)
+@pytest.mark.parametrize("B,T,NH,NKVH,Da,r", CASES)
+def test_chain_exact_integer(dtype, B, T, NH, NKVH, Da, r):
+    """The reference's integer generators without the sigmoid (gates 0 / 1):
+    every output exact, across chunk boundaries."""
+    nbytes = _ws_bytes(dtype, B, T, NH, NKVH, Da, r)
+    assert nbytes > 0
+    c = int_combined(B, T, NH, NKVH, Da, r)
+    ini = int_inits(B, NH, NKVH, Da, r)
+    bias = int_logit_bias(NH, NKVH, Da, False)
+    eq, ek, ev = O.scan_forward(c, ini, bias, NH, NKVH, Da, r, False, io_name(dtype))
+    ws = _zero_ws(nbytes)
+    q, k, v = _forward(to_torch(c, dtype, DEV), to_torch(ini, dtype, DEV),
+                       to_torch(bias, torch.float32, DEV), NH, NKVH, Da, r, False, ws)
+    case = f"T={T} Da={Da} r={r}"
+    assert_close(np_of(q), eq, 0, "q " + case)
+    if NKVH:
+        assert_close(np_of(k), ek, 0, "k " + case)
+        assert_close(np_of(v), ev, 0, "v " + case)
+    _check_ws_clean(ws, case)
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=io_name)
+@pytest.mark.parametrize("B,T,NH,NKVH,Da,r", CASES)
+def test_chain_sigmoid_vs_oracle_and_tile(dtype, B, T, NH, NKVH, Da, r):
+    """Sigmoid gates, decay sigmoid(N(2, 1)): within the tolerance of the
+    oracle; against the tile kernel (a different association of the same fp32
+    recurrence) within one bf16 rounding step or 1e-5 in fp32; three calls on
+    one workspace bitwise equal."""
+    io = io_name(dtype)
+    c, ini, bias = _random_case(B, T, NH, NKVH, Da, r, seed=T * 7 + r, io=io)
+    eq, ek, ev = O.scan_forward(c, ini, bias, NH, NKVH, Da, r, True, io)
+    cd, idv, bd = to_torch(c, dtype, DEV), to_torch(ini, dtype, DEV), to_torch(bias, torch.float32, DEV)
+    ws = _zero_ws(_ws_bytes(dtype, B, T, NH, NKVH, Da, r))
+    runs = [_forward(cd, idv, bd, NH, NKVH, Da, r, True, ws) for _ in range(3)]
+    for run in runs[1:]:
+        for a, b in zip(runs[0], run):
+            assert torch.equal(a, b)
+    q, k, v = runs[0]
+    tol = TOL[dtype]
+    case = f"T={T} Da={Da} r={r}"
+    assert_close(np_of(q), eq, tol, "q " + case)
+    if NKVH:
+        assert_close(np_of(k), ek, tol, "k " + case)
+        assert_close(np_of(v), ev, tol, "v " + case)
+    tile = _forward(cd, idv, bd, NH, NKVH, Da, r, True)
+    for a, b in zip(runs[0], tile):
+        _assert_same_up_to_association(a, b, dtype, "chained vs tile " + case)
+    _check_ws_clean(ws, case)
+
+
+def test_chain_workspace_reuse_across_shapes():
+    """One zeroed buffer serves calls of different shapes in a row (the
+    invariant leaves it zeroed), including one with more chunks than the
+    buffer's previous user."""
+    dtype = torch.bfloat16
+    shapes = [(2, 2100, 2, 1, 1, 128), (3, 600, 1, 1, 1, 128), (1, 5000, 1, 1, 128, 1),
+              (2, 2100, 2, 1, 1, 128)]
+    need = max(_ws_bytes(dtype, *s) for s in shapes)
+    ws = _zero_ws(need)
+    for B, T, NH, NKVH, Da, r in shapes:
+        c, ini, bias = _random_case(B, T, NH, NKVH, Da, r, seed=B + T, io="bf16")
+        eq, _, _ = O.scan_forward(c, ini, bias, NH, NKVH, Da, r, True, "bf16")
+        q, _, _ = _forward(to_torch(c, dtype, DEV), to_torch(ini, dtype, DEV),
+                           to_torch(bias, torch.float32, DEV), NH, NKVH, Da, r, True, ws)
+        assert_close(np_of(q), eq, TOL[dtype], f"reuse T={T}")
+        _check_ws_clean(ws, f"reuse T={T}")
+
+
+def test_chain_workspace_errors():
+    """A workspace below the queried size or off 256-byte alignment is
+    refused before any launch; no workspace selects the tile kernel."""
+    N, lib = _lib()
+    B, T, NH, NKVH, Da, r = 1, 2000, 1, 1, 1, 128
+    dtype = torch.bfloat16
+    nbytes = _ws_bytes(dtype, B, T, NH, NKVH, Da, r)
+    c, ini, bias = _random_case(B, T, NH, NKVH, Da, r, seed=1, io="bf16")
+    cd, idv, bd = to_torch(c, dtype, DEV), to_torch(ini, dtype, DEV), to_torch(bias, torch.float32, DEV)
+    small = _zero_ws(nbytes - 512)
+    with pytest.raises(RuntimeError, match="workspace too small"):
+        _forward(cd, idv, bd, NH, NKVH, Da, r, True, small[: nbytes - 512])
+    big = _zero_ws(nbytes + 256)
+    with pytest.raises(RuntimeError, match="256-byte aligned"):
+        _forward(cd, idv, bd, NH, NKVH, Da, r, True, big[16:])
+    torch.cuda.synchronize()
+    assert int(torch.count_nonzero(small)) == 0 and int(torch.count_nonzero(big)) == 0
+
+
+def test_chain_combined_layout():
+    """ltv_hm_scan_forward_ws on the reference's combined (B, T, F) layout,
+    where every head's values start on a 16-byte boundary (D + Da = 136
+    columns): the chained kernel runs (a short workspace is refused) and is
+    exact on the integer generators."""
+    N, lib = _lib()
+    B, T, NH, NKVH, Da, r = 2, 1100, 1, 1, 8, 16
+    D = Da * r
+    dtype = torch.bfloat16
+    c = int_combined(B, T, NH, NKVH, Da, r)
+    ini = int_inits(B, NH, NKVH, Da, r)
+    bias = int_logit_bias(NH, NKVH, Da, False)
+    eq, ek, ev = O.scan_forward(c, ini, bias, NH, NKVH, Da, r, False, "bf16")
+    comb, idv = to_torch(c, dtype, DEV), to_torch(ini, dtype, DEV)
+    bd = to_torch(bias, torch.float32, DEV)
+    nbytes = _ws_bytes(dtype, B, T, NH, NKVH, Da, r)
+
+    def run(ws, nb):
+        out = _outs(B, T, NH, NKVH, D, dtype)
+        rc = lib.ltv_hm_scan_forward_ws(
+            N.dtype_code(dtype), comb.data_ptr(), _s(comb), idv.data_ptr(), _s(idv),
+            bd.data_ptr(), out[0].data_ptr(), _s(out[0]), out[1].data_ptr(), _s(out[1]),
+            out[2].data_ptr(), _s(out[2]), ws.data_ptr(), nb, B, T, NH, NKVH, Da, r, 0,
+            N.stream_of(comb))
+        N.check(rc, "ltv_hm_scan_forward_ws")
+        return out
+
+    ws = _zero_ws(nbytes)
+    with pytest.raises(RuntimeError, match="workspace too small"):
+        run(ws, nbytes - 8)
+    q, k, v = run(ws, nbytes)
+    assert_close(np_of(q), eq, 0, "q combined")
+    assert_close(np_of(k), ek, 0, "k combined")
+    assert_close(np_of(v), ev, 0, "v combined")
+    _check_ws_clean(ws, "combined")
+
+
+def test_chain_config5_prefill_vs_tile():
+    """configs[4]'s prefill (B = 8, T = 8192, 18 heads of 128, r = 128, bf16,
+    decay sigmoid(z), z ~ N(3, 1.5)): the chained kernel (16 chunks per
+    sequence, 4,608 workgroups) against the oracle on two batch rows and
+    against the tile kernel everywhere."""
+    N, lib = _lib()
+    B, T, NH, NKVH, D = 8, 8192, 6, 6, 128
+    H = NH + 2 * NKVH
+    g = torch.Generator().manual_seed(11)
+    comb = torch.empty(B, T, H, D + 1)
+    comb[..., :D] = torch.randn(B, T, H, D, generator=g)
+    comb[..., D] = -(3.0 + 1.5 * torch.randn(B, T, H, generator=g))
+    comb = comb.reshape(B, T, H * (D + 1)).to(torch.bfloat16)
+    inits = (0.5 * torch.randn(B, H, D, generator=g)).to(torch.bfloat16)
+    bias = torch.zeros(H, 1)
+    cd, idv, bd = comb.to(DEV), inits.to(DEV), bias.to(DEV)
+    ws = _zero_ws(_ws_bytes(torch.bfloat16, B, T, NH, NKVH, 1, D))
+    chain = _forward(cd, idv, bd, NH, NKVH, 1, D, True, ws)
+    tile = _forward(cd, idv, bd, NH, NKVH, 1, D, True)
+    for a, b in zip(chain, tile):
+        _assert_same_up_to_association(a, b, torch.bfloat16, "config5 prefill chained vs tile")
+    got = torch.cat(chain, dim=1)
+    for b in (0, 5):
+        eq, ek, ev = O.scan_forward(comb[b:b + 1].float().numpy(), inits[b:b + 1].float().numpy(),
+                                    bias.numpy(), NH, NKVH, 1, D, True, "bf16")
+        want = np.concatenate([eq, ek, ev], axis=1)[0]
+        assert_close(np_of(got[b]), want, 2e-2, f"config5 prefill chained b={b}")
+    _check_ws_clean(ws, "config5 prefill")
+
+
+def test_chain_graph_replays_match_eager():
+    """The fast path's scan forward (chained, workspace from the graph's pool)
+    captured in a HIP graph: every replay equals the eager result, with eager
+    work and synchronisation between replays."""
+    from nanochat_amd.ops import ltv_hm_fast as F_
+    B, T, NH, NKVH, D = 2, 3000, 2, 1, 128
+    H = NH + 2 * NKVH
+    g = torch.Generator().manual_seed(3)
+    values = torch.randn(B, H, T, D, generator=g).to(torch.bfloat16).to(DEV)
+    logits = (-(2.0 + torch.randn(B, T, H, generator=g))).to(torch.bfloat16).to(DEV)
+    inits = torch.randn(B, H, D, generator=g).to(torch.bfloat16).to(DEV)
+    bias = torch.zeros(H, 1, device=DEV)
+    eager = F_.scan_forward(values, logits, inits, bias, NH, NKVH, 1, D, True)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        F_.scan_forward(values, logits, inits, bias, NH, NKVH, 1, D, True)  # warm-up
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        outs = F_.scan_forward(values, logits, inits, bias, NH, NKVH, 1, D, True)
+    for i in range(3):
+        for o in outs:
+            o.fill_(0)
+        graph.replay()
+        torch.cuda.synchronize()
+        for a, b in zip(outs, eager):
+            assert torch.equal(a, b), f"replay {i}"
+        # eager work between the replays, on the same buffers' stream
+        again = F_.scan_forward(values, logits, inits, bias, NH, NKVH, 1, D, True)
+        for a, b in zip(again, eager):
+            assert torch.equal(a, b)
