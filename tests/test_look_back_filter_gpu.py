@@ -78,9 +78,6 @@ def _oracle(f, x_np, gq, gk, gv, pqk, io):
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "f32"])
 @pytest.mark.parametrize("pqk", [(16, 16, 9), (64, 60, 5), (5, 2, 6)], ids=str)
 def test_look_back_filter_matches_oracle(variant, dtype, pqk):
-    if variant == "sequential" and dtype == torch.float32:
-        pytest.skip("the sequential filter's nn.Linear runs the fp32 projection in torch; "
-                    "covered by the reference-layout op tests")
     io = "bf16" if dtype == torch.bfloat16 else "f32"
     NH, NKVH, D, r = 2, 1, 128, 128
     f = _make(variant, NH, NKVH, D, r, pqk)
