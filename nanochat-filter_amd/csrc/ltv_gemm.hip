@@ -720,10 +720,14 @@ extern "C" int ltv_qkv_project_backward_input(const void* x, const void* wpack,
   hipStream_t st = (hipStream_t)stream;
   if (gemm_tuning().dma) {
     // the direct-to-LDS loads fetch dC in 8-column chunks: columns up to the
-    // next multiple of 8 past Fvalid are read, so they are set to zero first
+    // next multiple of 8 past Fvalid are read, so they are set to zero first;
+    // the reduction stops there (Fp would add k-steps that only load padding:
+    // 38 instead of 37 at d12)
     const int Fv8 = round_up(Fvalid, 8);
     GemmArgs ad = a;
     ad.Q.k_valid = Fv8;
+    ad.K = Fv8;
+    ad.k_split = Fv8;
     if (dma_usable(ad, OP_RC, OP_KC, e, 1)) {
       if (Fv8 > Fvalid) {
         const int blocks = (M + 255) / 256;
