@@ -1,7 +1,7 @@
 """Benchmark of the LTV combined-QKV filter path on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
-                    [--workload filter|look_back|gpt|scan_fwd|prefill]
+                    [--workload filter|look_back|gpt|scan_fwd|prefill|decode]
 
 Workload (the d12 training shape): x bf16
 [32, 1024, 768] ~ N(0, 1); c.weight [2322, 768] fp32 ~ N(0, 1/768) (value rows
@@ -22,7 +22,10 @@ values [32, 3 x 6, 1024, 128] ~ N(0, 1) with a per-element decay (r = 1)
 a = sigmoid(z), z ~ N(2, 1), i.e. logit + bias = -z; fp32 state, bf16 out; a
 step is one scan launch and ``value`` is its algorithmic GB/s.  ``--workload
 prefill`` is configs[4]'s prefill: one forward of the filter at B = 8,
-T = 8192 with long-memory decays (tokens / s).
+T = 8192 with long-memory decays (tokens / s).  ``--workload decode`` is
+configs[4]'s decode: 256 single-token steps at B = 64 through the KV-cache
+protocol after a 16-token prefill (tokens / s through the module), and the same
+256 steps replayed from a captured HIP graph.
 
 Printed as one JSON line, with
   roofline     -- the dominant kernel's algorithmic bytes (or FLOPs) per launch
@@ -151,7 +154,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--workload", choices=("filter", "look_back", "gpt", "scan_fwd", "prefill"),
+    ap.add_argument("--workload",
+                    choices=("filter", "look_back", "gpt", "scan_fwd", "prefill", "decode"),
                     default="filter",
                     help="filter: BASELINE.json configs[2] (the default, the metric's workload); "
                          "look_back: the same shapes through the look-back filter with the d12 "
@@ -179,6 +183,9 @@ def main():
         return
     if args.workload == "prefill":
         prefill_main(args)
+        return
+    if args.workload == "decode":
+        decode_main(args)
         return
 
     import torch
@@ -519,6 +526,129 @@ def prefill_main(args):
                      "peak": dk_["peak"], "unit": dk_["unit"], "frac": dk_["frac"],
                      "traffic": traffic, "traffic_source": traffic_src},
         "kernels": kernels,
+    }
+    print(json.dumps(out), flush=True)
+
+
+# decode
+DC_B, DC_T0, DC_N = 64, 16, 256
+
+
+def decode_main(args):
+    """configs[4]'s decode: B = 64 sequences, a 16-token prefill, then 256
+    single-token steps through LtvCombinedQkvComputerModule and a KVCache (the
+    filter state carried in the cache's last q/k/v rows).  A step is one token
+    for the whole batch; ``--steps`` counts passes over the 256 tokens.
+    value = decoded tokens / s through the module (what a serving loop calling
+    the module sees, host dispatch included).  The same 256 steps captured in
+    one HIP graph of fused decode kernels (each step's rows feeding the next)
+    and replayed give the GPU-side rate without the Python dispatch."""
+    import torch
+    from nanochat_amd import _native as N
+    from nanochat_amd.gpt_config import ChunksAndHistory
+    from nanochat_amd.kv_cache import KVCache
+    from nanochat_amd.ltv_combined_qkv_computer_module import LtvCombinedQkvComputerModule
+    from nanochat_amd.ltv_cuda_fused_concat_head_major_register_cast_blelloch_scan_qkv_filter import (
+        LtvCudaFusedConcatHeadMajorRegisterCastBlellochScanQkvFilter as Filter,
+    )
+    from nanochat_amd.ops import ltv_hm_fast as hm
+
+    dev = torch.device("cuda:0")
+    torch.manual_seed(0)
+    f = Filter(NH, NKVH, D, R)
+    with torch.no_grad():
+        f.c.weight.normal_(0.0, C ** -0.5)
+        f.c.weight.view(H, D + DA, C)[:, D:] *= 1.5
+        f.logit_bias.fill_(-3.0)
+        f.init_param.normal_(0.0, C ** -0.5)
+    f = f.to(dev)
+    m = LtvCombinedQkvComputerModule(0, f)
+    g = torch.Generator(device=dev).manual_seed(0)
+    xs = torch.randn(DC_B, DC_T0 + DC_N, C, generator=g, device=dev).to(torch.bfloat16)
+
+    def new_cache():
+        cache = KVCache(DC_B, NH, NKVH, DC_T0 + DC_N, D, 1,
+                        [ChunksAndHistory(2147483647, 1, 1)])
+        with torch.no_grad():
+            m(xs[:, :DC_T0], cache)
+        return cache
+
+    def decode_pass(cache):
+        with torch.no_grad():
+            for t in range(DC_T0, DC_T0 + DC_N):
+                m(xs[:, t:t + 1], cache)
+
+    for _ in range(max(args.warmup, 1)):
+        decode_pass(new_cache())
+    caches = [new_cache() for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for c in caches:
+        decode_pass(c)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    tokens = DC_B * DC_N * args.steps
+
+    # the fused kernel alone (HIP events), and the 256 steps as one HIP graph
+    wpack = f._packed_weight()
+    bias = f.logit_bias.detach().float().contiguous()
+    with N.KernelRecorder() as rec:
+        decode_pass(new_cache())
+        torch.cuda.synchronize()
+    cache = new_cache()
+    last = cache.last_qkv
+    prev0 = tuple(t.special[0].clone() for t in (last.q, last.k, last.v))
+
+    def chain():
+        prev = prev0
+        for t in range(DC_T0, DC_T0 + DC_N):
+            out = hm.decode_step(xs[:, t], wpack, prev, bias, NH, NKVH, DA, R, True)
+            prev = (out[:, :NH], out[:, NH:NH + NKVH], out[:, NH + NKVH:])
+        return out
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        chain()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        chain()
+    graph.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        graph.replay()
+    torch.cuda.synchronize()
+    graph_s = time.perf_counter() - t0
+
+    ms = rec.durations_ms()["qkv_decode"]
+    avg_us = sum(ms) / len(ms) * 1e3
+    fp = hm.packed_width(H, D, DA)
+    nbytes = fp * C * S_IO + DC_B * (C + 2 * H * D) * S_IO  # weight, x, previous and new rows
+    ach = nbytes / (avg_us * 1e-6) / 1e9
+    out = {
+        "metric": "decode: LTV QKV filter tokens/s at B64 (256 single-token steps, KV cache)",
+        "value": round(tokens / elapsed, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(elapsed * 1e3 / (args.steps * DC_N), 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "configs[4] decode: 256 steps at B = 64 after a 16-token prefill, "
+                               "through LtvCombinedQkvComputerModule + KVCache",
+                   "B": DC_B, "prefill": DC_T0, "decode_steps": DC_N, "C": C, "n_head": NH,
+                   "n_kv_head": NKVH, "head_dim": D, "r": R, "parallelism": "single GPU"},
+        "graph": {"tokens_per_s": round(tokens / graph_s, 1),
+                  "us_per_step": round(graph_s * 1e6 / (args.steps * DC_N), 2)},
+        "roofline": {"kernel": "qkv_decode", "bound": "hbm", "achieved": round(ach, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4),
+                     "traffic": None, "avg_us": round(avg_us, 2), "work_per_launch": nbytes},
     }
     print(json.dumps(out), flush=True)
 
