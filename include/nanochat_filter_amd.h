@@ -45,7 +45,7 @@ extern "C" {
 #define LTV_ERR_HIP 3
 #define LTV_ERR_WORKSPACE 4
 
-/* Version of this ABI (bumped on any signature change or addition): 4. */
+/* Version of this ABI (bumped on any signature change or addition): 5. */
 int ltv_abi_version(void);
 
 /* Message of the last failing call on this host thread ("" if none). */
@@ -141,6 +141,47 @@ int ltv_hm_scan_backward(int dtype, const void* combined, const int64_t combined
                          const int64_t grad_inits_strides[3], float* grad_logit_bias,
                          void* workspace, size_t workspace_bytes, int B, int T, int NH, int NKVH,
                          int Da, int r, int use_sigmoid, void* stream);
+
+/* ------------------------------------------------------------------------
+ * ltv_hm_scan_backward with a chain workspace: the same gradients, computed
+ * by workgroups that each own one tile-long chunk of T, last chunk first, and
+ * hand the gradient carry at the chunk's start to the chunk before it through
+ * `chain_workspace` (one pass over HBM, parallel over T as well as over
+ * (b, head)).  grad_combined and grad_inits are bitwise those of the
+ * unchunked tile kernel with the same steps per lane; grad_logit_bias sums
+ * per-chunk partials (a different fp32 association, fixed from call to call).
+ *
+ * chain_workspace: the contract of ltv_hm_scan_forward_ws's, sized by
+ *   ltv_hm_scan_backward_chain_workspace_size(...) (one zeroed buffer can serve
+ *   the chained forward and backward on one stream: each call leaves it
+ *   zeroed).  NULL selects the kernels of ltv_hm_scan_backward.  The chained
+ *   kernel is used below 512 (b, head) sequences with 16-byte channel
+ *   vectors, gate groups of whole lanes (at most 16 per head) or r = 1, and
+ *   at least two chunks; elsewhere the size query returns 0 and a workspace
+ *   passed is not touched.  (LTV_SCAN_BWD_CHAIN_CFG="L,NW" forces it, "0"
+ *   turns it off.)  `workspace` is sized by ltv_hm_scan_backward_workspace_size
+ *   as before (it covers either kernel's dbias partials).
+ *
+ * Replaces the same reference backward as ltv_hm_scan_backward; the chain
+ * workspace has no counterpart there (the reference walks T serially per
+ * block, cpp_ewma/src/ltv_fused_concat_head_major_register_cast_blelloch_scan_cuda_backward.cu:882-976).
+ * ---------------------------------------------------------------------- */
+size_t ltv_hm_scan_backward_chain_workspace_size(int dtype, int B, int T, int NH, int NKVH,
+                                                 int Da, int r);
+
+int ltv_hm_scan_backward_ws(int dtype, const void* combined, const int64_t combined_strides[3],
+                            const void* inits, const int64_t inits_strides[3],
+                            const float* logit_bias, const void* hq, const int64_t hq_strides[4],
+                            const void* hk, const int64_t hk_strides[4], const void* hv,
+                            const int64_t hv_strides[4], const void* grad_hq,
+                            const int64_t grad_hq_strides[4], const void* grad_hk,
+                            const int64_t grad_hk_strides[4], const void* grad_hv,
+                            const int64_t grad_hv_strides[4], void* grad_combined,
+                            const int64_t grad_combined_strides[3], void* grad_inits,
+                            const int64_t grad_inits_strides[3], float* grad_logit_bias,
+                            void* workspace, size_t workspace_bytes, void* chain_workspace,
+                            size_t chain_workspace_bytes, int B, int T, int NH, int NKVH, int Da,
+                            int r, int use_sigmoid, void* stream);
 
 /* ------------------------------------------------------------------------
  * Same scan with the value and logit slots given as two separate 4-D views
@@ -253,6 +294,22 @@ int ltv_hm_look_back_scan_backward_split(
     const int64_t grad_logits_strides[4], void* grad_inits, const int64_t grad_inits_strides[3],
     float* grad_logit_bias, void* workspace, size_t workspace_bytes, int B, int T, int NH,
     int NKVH, int Da, int r, int P, int Q, int K, int use_sigmoid, void* stream);
+
+/* ltv_hm_look_back_scan_backward_split with the chain workspace of
+ * ltv_hm_scan_backward_ws (same contract), used when there is one window
+ * (P >= T); with several windows the chain workspace is not touched. */
+int ltv_hm_look_back_scan_backward_split_ws(
+    int dtype, const void* values, const int64_t values_strides[4], const void* logits,
+    const int64_t logits_strides[4], const void* inits, const int64_t inits_strides[3],
+    const float* logit_bias, const void* hq, const int64_t hq_strides[4], const void* hk,
+    const int64_t hk_strides[4], const void* hv, const int64_t hv_strides[4],
+    const void* grad_hq, const int64_t grad_hq_strides[4], const void* grad_hk,
+    const int64_t grad_hk_strides[4], const void* grad_hv, const int64_t grad_hv_strides[4],
+    void* grad_values, const int64_t grad_values_strides[4], void* grad_logits,
+    const int64_t grad_logits_strides[4], void* grad_inits, const int64_t grad_inits_strides[3],
+    float* grad_logit_bias, void* workspace, size_t workspace_bytes, void* chain_workspace,
+    size_t chain_workspace_bytes, int B, int T, int NH, int NKVH, int Da, int r, int P, int Q,
+    int K, int use_sigmoid, void* stream);
 
 /* ------------------------------------------------------------------------
  * Projection, reference layout: out[b] (F x T) = weight (F x K) . x[b]^T

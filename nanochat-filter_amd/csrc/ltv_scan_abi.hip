@@ -71,6 +71,12 @@ int scan_launch_bwd(bool bf16, const BwdArgs& a, ScanCfg cfg, int grid, bool vec
               : scan_bwd_launch_f32(a, cfg, grid, vec, gm, lb, st);
 }
 
+int scan_launch_bwd_chain(bool bf16, const BwdArgs& a, ScanCfg cfg, int grid, int gm,
+                          hipStream_t st) {
+  return bf16 ? scan_bwd_chain_launch_bf16(a, cfg, grid, gm, st)
+              : scan_bwd_chain_launch_f32(a, cfg, grid, gm, st);
+}
+
 int scan_launch_lb_fold(bool bf16, const BwdArgs& a, hipStream_t st) {
   const ScanShape& S = a.sh;
   const int64_t n = (int64_t)S.B * S.H * a.nchunk * a.kw * (S.D + S.Da);
@@ -223,6 +229,10 @@ struct ScanTuning {
   bool chain = true;
   int bwd_l = 0, bwd_nw = 0;
   int bwd_chunks = 0;  // time chunks per (b, h) in the backward; 0 = automatic
+  // LTV_SCAN_BWD_CHAIN_CFG="L,NW" (chained backward shape, forced) or "0"
+  // (never chained)
+  int bwd_chain_l = 0, bwd_chain_nw = 0;
+  bool bwd_chain = true;
   bool lb_short = true;  // LTV_SCAN_LB_SHORT=0: look-back windows through the tile kernels
   ScanTuning() {
     if (const char* e = getenv("LTV_SCAN_LB_SHORT")) lb_short = atoi(e) != 0;
@@ -238,6 +248,12 @@ struct ScanTuning {
     }
     if (const char* e = getenv("LTV_SCAN_BWD_CFG")) {
       if (sscanf(e, "%d,%d", &bwd_l, &bwd_nw) != 2) bwd_l = bwd_nw = 0;
+    }
+    if (const char* e = getenv("LTV_SCAN_BWD_CHAIN_CFG")) {
+      if (sscanf(e, "%d,%d", &bwd_chain_l, &bwd_chain_nw) != 2) {
+        bwd_chain_l = bwd_chain_nw = 0;
+        bwd_chain = atoi(e) != 0;
+      }
     }
   }
 };
@@ -350,6 +366,14 @@ struct ChainPlan {
   size_t bytes;  // workspace: header + tagged states
 };
 constexpr size_t kChainHeader = 256;
+// (b, h) sequences from which the backward keeps the tile kernel.  Measured on
+// MI355X (heads of 128, r = 128, bf16; chained shape L = 4, NW = 4):
+//   B = 32, T = 1024 (576 sequences): tile 118 us, chained 171 us (L = 4,
+//     NW = 2: 242 us) -- 16 chunks per sequence and about two chunk rows
+//     resident make the chain's critical path the time;
+//   B = 16, T = 1024 (288): tile 102 us, chained 93.5 us;
+//   B = 2, T = 8192 (36): tile with the chunk-map passes 144 us, chained 125 us.
+constexpr int64_t kBwdChainMaxSeqs = 512;
 
 ChainPlan chain_plan(int dtype, int B, int T, int H, int Da, int r) {
   ChainPlan p{{0, 0, 0}, -1, 0, 0, 0, 0};
@@ -518,6 +542,56 @@ int bwd_max_chunks(int B, int H, int T) {
 // Sub-chunk length of the backward's chunk maps (steps).
 constexpr int kBwdFineSteps = 64;
 
+// The chained backward (scan_bwd_kernel in its CHAIN mode): launch shape,
+// gate mode and chunk count for a head of D channels, or CL = 0 where it is
+// not used.  It needs the full recurrence, 16-byte channel vectors, one gate
+// per lane group or r == 1, and a built shape; it is chosen below
+// kBwdChainMaxSeqs sequences, where the tile kernel's workgroups are too few
+// to hide its per-tile latency (and below 256, where the tile kernel needs the
+// chunk-map passes).  LTV_SCAN_BWD_CHAIN_CFG="L,NW" forces it with that shape.
+struct BwdChainPlan {
+  ScanCfg cfg;
+  int gm, nchunk;
+  int64_t nseq;
+  size_t bytes;  // workspace: header + tagged carries
+};
+
+bool bwd_chain_built(ScanCfg c, int V) {
+  bool built = false;
+#define LTV_X(CL_, L_, NW_) \
+  built = built || (c.CL == CL_ && c.L == L_ && c.NW == NW_ && CL_ * V <= NW_ * 64);
+  LTV_SCAN_BWD_CHAIN_CONFIGS(LTV_X)
+#undef LTV_X
+  return built;
+}
+
+BwdChainPlan bwd_chain_plan(int dtype, int B, int T, int H, int Da, int r) {
+  BwdChainPlan p{{0, 0, 0}, -1, 0, 0, 0};
+  const ScanTuning& tu = tuning();
+  const int V = dtype == LTV_DTYPE_BF16 ? 8 : 4;
+  const int D = Da * r;
+  if (!tu.bwd_chain || B <= 0 || T <= 0 || H <= 0 || D % V != 0) return p;
+  int gm = bwd_gate_mode(r, Da, V);
+  if (gm == GATE_CHAN) gm = r == 1 ? GATE_CHANVEC : -1;
+  if (gm < 0) return p;
+  const int cl = next_pow2(D / V);
+  ScanCfg c{cl, 4, 4};
+  if (tu.bwd_chain_l > 0) {
+    c = ScanCfg{cl, tu.bwd_chain_l, tu.bwd_chain_nw};
+  } else {
+    if ((int64_t)B * H >= kBwdChainMaxSeqs) return p;
+  }
+  if (!bwd_chain_built(c, V)) return p;
+  const int TW = c.NW * (64 / c.CL) * c.L;
+  p.nchunk = (int)(((int64_t)T + TW - 1) / TW);
+  if (p.nchunk < 2) return BwdChainPlan{{0, 0, 0}, -1, 0, 0, 0};
+  p.cfg = c;
+  p.gm = gm;
+  p.nseq = (int64_t)B * H;
+  p.bytes = kChainHeader + (size_t)p.nseq * (size_t)(p.nchunk - 1) * (size_t)(c.CL * V) * 8u;
+  return p;
+}
+
 struct BwdWorkspace {
   // byte offsets
   size_t partial = 0, agg = 0, carry = 0, dalpha = 0;
@@ -562,7 +636,9 @@ BwdWorkspace bwd_workspace_plan(int dtype, int B, int T, int NH, int NKVH, int D
     return w;
   }
   const int NC = bwd_max_chunks(B, H, T);
-  size_t off = al((size_t)B * H * NC * Da * sizeof(float));
+  // dbias partials for the tile kernel's chunks or the chained kernel's
+  const int NP = std::max(NC, bwd_chain_plan(dtype, B, T, H, Da, r).nchunk);
+  size_t off = al((size_t)B * H * NP * Da * sizeof(float));
   if (NC > 1) {
     w.agg = off;
     off += al((size_t)2 * B * H * ((T + kBwdFineSteps - 1) / kBwdFineSteps) * D * sizeof(float));
@@ -586,8 +662,9 @@ int scan_backward_impl(int dtype, const HostView4& u, const HostView4& lg, const
                        const float* bias, const void* const hp[3], const int64_t* const hs[3],
                        const void* const gp[3], const int64_t* const gs[3], const HostView4& du,
                        const HostView4& dlg, const HostView4& dinit, float* dbias, void* ws,
-                       size_t ws_bytes, int B, int T, int NH, int NKVH, int Da, int r, int P,
-                       int Q, int K, int use_sigmoid, hipStream_t st) {
+                       size_t ws_bytes, void* chain_ws, size_t chain_ws_bytes, int B, int T,
+                       int NH, int NKVH, int Da, int r, int P, int Q, int K, int use_sigmoid,
+                       hipStream_t st) {
   int rc = check_shape(dtype, B, T, NH, NKVH, Da, r);
   if (rc) return rc;
   rc = check_pqk(P, Q, K);
@@ -661,6 +738,8 @@ int scan_backward_impl(int dtype, const HostView4& u, const HostView4& lg, const
   a.kw = 0;
   a.wst = nullptr;
   a.wdu = a.wdl = a.wdi = nullptr;
+  a.ch_ticket = a.ch_err = nullptr;
+  a.ch_words = nullptr;
 
   int gm = bwd_gate_mode(r, Da, V);
   if (gm == GATE_CHAN && vec && chanvec_ok(r, D, V, lg) && chanvec_ok(r, D, V, dlg))
@@ -743,6 +822,28 @@ int scan_backward_impl(int dtype, const HostView4& u, const HostView4& lg, const
     rc = scan_launch_lb_dinit(bf16, a, st);
     if (rc) return rc;
     return scan_launch_dbias_reduce(a.dbias_partial, dbias, B, H, nwin, Da, st);
+  }
+  if (gm >= 0 && vec && chain_ws != nullptr) {
+    // chained: one tile per chunk, the carries handed between workgroups
+    const BwdChainPlan pl = bwd_chain_plan(dtype, B, T, H, Da, r);
+    if (pl.cfg.CL > 0 && pl.gm == gm) {
+      LTV_REQUIRE(chain_ws_bytes >= pl.bytes, LTV_ERR_WORKSPACE,
+                  "chained scan workspace too small: %zu bytes, need %zu", chain_ws_bytes,
+                  pl.bytes);
+      LTV_REQUIRE((reinterpret_cast<uintptr_t>(chain_ws) & 255u) == 0, LTV_ERR_INVALID_ARG,
+                  "chained scan workspace must be 256-byte aligned");
+      const int64_t grid = pl.nseq * pl.nchunk;
+      LTV_REQUIRE(grid < (1ll << 31), LTV_ERR_UNSUPPORTED, "grid too large");
+      a.nchunk = pl.nchunk;
+      a.chunk_steps = pl.cfg.NW * (64 / pl.cfg.CL) * pl.cfg.L;
+      a.ch_ticket = reinterpret_cast<uint32_t*>(chain_ws);
+      a.ch_err = reinterpret_cast<uint32_t*>(chain_ws) + 1;
+      a.ch_words = reinterpret_cast<unsigned long long*>(reinterpret_cast<char*>(chain_ws) +
+                                                         kChainHeader);
+      rc = scan_launch_bwd_chain(dtype == LTV_DTYPE_BF16, a, pl.cfg, (int)grid, gm, st);
+      if (rc) return rc;
+      return scan_launch_dbias_reduce(a.dbias_partial, dbias, B, H, a.nchunk, Da, st);
+    }
   }
   if (gm >= 0) {
     // whole head per workgroup
@@ -944,7 +1045,8 @@ extern "C" size_t ltv_hm_scan_backward_workspace_size(int dtype, int B, int T, i
   return bwd_workspace_bytes(dtype, B, T, NH, NKVH, Da, r, kUnboundedP, 1, 1);
 }
 
-extern "C" int ltv_hm_look_back_scan_backward(
+namespace {
+int scan_backward_combined(
     int dtype, const void* combined, const int64_t combined_strides[3], const void* inits,
     const int64_t inits_strides[3], const float* logit_bias, const void* hq,
     const int64_t hq_strides[4], const void* hk, const int64_t hk_strides[4], const void* hv,
@@ -952,8 +1054,8 @@ extern "C" int ltv_hm_look_back_scan_backward(
     const void* grad_hk, const int64_t grad_hk_strides[4], const void* grad_hv,
     const int64_t grad_hv_strides[4], void* grad_combined, const int64_t grad_combined_strides[3],
     void* grad_inits, const int64_t grad_inits_strides[3], float* grad_logit_bias,
-    void* workspace, size_t workspace_bytes, int B, int T, int NH, int NKVH, int Da, int r, int P,
-    int Q, int K, int use_sigmoid, void* stream) {
+    void* workspace, size_t workspace_bytes, void* chain_ws, size_t chain_ws_bytes, int B, int T,
+    int NH, int NKVH, int Da, int r, int P, int Q, int K, int use_sigmoid, void* stream) {
   LTV_REQUIRE(combined_strides && inits_strides && hq_strides && hk_strides && hv_strides &&
                   grad_hq_strides && grad_hk_strides && grad_hv_strides &&
                   grad_combined_strides && grad_inits_strides,
@@ -969,8 +1071,51 @@ extern "C" int ltv_hm_look_back_scan_backward(
       logits_view(combined, combined_strides, D, Da, es), view3(inits, inits_strides),
       logit_bias, hp, hs, gp, gs, values_view(grad_combined, grad_combined_strides, D, Da),
       logits_view(grad_combined, grad_combined_strides, D, Da, es),
-      view3(grad_inits, grad_inits_strides), grad_logit_bias, workspace, workspace_bytes, B, T,
-      NH, NKVH, Da, r, P, Q, K, use_sigmoid, (hipStream_t)stream);
+      view3(grad_inits, grad_inits_strides), grad_logit_bias, workspace, workspace_bytes,
+      chain_ws, chain_ws_bytes, B, T, NH, NKVH, Da, r, P, Q, K, use_sigmoid, (hipStream_t)stream);
+}
+}  // namespace
+
+extern "C" int ltv_hm_look_back_scan_backward(
+    int dtype, const void* combined, const int64_t combined_strides[3], const void* inits,
+    const int64_t inits_strides[3], const float* logit_bias, const void* hq,
+    const int64_t hq_strides[4], const void* hk, const int64_t hk_strides[4], const void* hv,
+    const int64_t hv_strides[4], const void* grad_hq, const int64_t grad_hq_strides[4],
+    const void* grad_hk, const int64_t grad_hk_strides[4], const void* grad_hv,
+    const int64_t grad_hv_strides[4], void* grad_combined, const int64_t grad_combined_strides[3],
+    void* grad_inits, const int64_t grad_inits_strides[3], float* grad_logit_bias,
+    void* workspace, size_t workspace_bytes, int B, int T, int NH, int NKVH, int Da, int r, int P,
+    int Q, int K, int use_sigmoid, void* stream) {
+  return scan_backward_combined(
+      dtype, combined, combined_strides, inits, inits_strides, logit_bias, hq, hq_strides, hk,
+      hk_strides, hv, hv_strides, grad_hq, grad_hq_strides, grad_hk, grad_hk_strides, grad_hv,
+      grad_hv_strides, grad_combined, grad_combined_strides, grad_inits, grad_inits_strides,
+      grad_logit_bias, workspace, workspace_bytes, nullptr, 0, B, T, NH, NKVH, Da, r, P, Q, K,
+      use_sigmoid, stream);
+}
+
+extern "C" size_t ltv_hm_scan_backward_chain_workspace_size(int dtype, int B, int T, int NH,
+                                                           int NKVH, int Da, int r) {
+  if (check_shape(dtype, B, T, NH, NKVH, Da, r) != LTV_OK) return 0;
+  return bwd_chain_plan(dtype, B, T, NH + 2 * NKVH, Da, r).bytes;
+}
+
+extern "C" int ltv_hm_scan_backward_ws(
+    int dtype, const void* combined, const int64_t combined_strides[3], const void* inits,
+    const int64_t inits_strides[3], const float* logit_bias, const void* hq,
+    const int64_t hq_strides[4], const void* hk, const int64_t hk_strides[4], const void* hv,
+    const int64_t hv_strides[4], const void* grad_hq, const int64_t grad_hq_strides[4],
+    const void* grad_hk, const int64_t grad_hk_strides[4], const void* grad_hv,
+    const int64_t grad_hv_strides[4], void* grad_combined, const int64_t grad_combined_strides[3],
+    void* grad_inits, const int64_t grad_inits_strides[3], float* grad_logit_bias,
+    void* workspace, size_t workspace_bytes, void* chain_workspace, size_t chain_workspace_bytes,
+    int B, int T, int NH, int NKVH, int Da, int r, int use_sigmoid, void* stream) {
+  return scan_backward_combined(
+      dtype, combined, combined_strides, inits, inits_strides, logit_bias, hq, hq_strides, hk,
+      hk_strides, hv, hv_strides, grad_hq, grad_hq_strides, grad_hk, grad_hk_strides, grad_hv,
+      grad_hv_strides, grad_combined, grad_combined_strides, grad_inits, grad_inits_strides,
+      grad_logit_bias, workspace, workspace_bytes, chain_workspace, chain_workspace_bytes, B, T,
+      NH, NKVH, Da, r, kUnboundedP, 1, 1, use_sigmoid, stream);
 }
 
 extern "C" int ltv_hm_scan_backward(
@@ -991,7 +1136,7 @@ extern "C" int ltv_hm_scan_backward(
       use_sigmoid, stream);
 }
 
-extern "C" int ltv_hm_look_back_scan_backward_split(
+extern "C" int ltv_hm_look_back_scan_backward_split_ws(
     int dtype, const void* values, const int64_t values_strides[4], const void* logits,
     const int64_t logits_strides[4], const void* inits, const int64_t inits_strides[3],
     const float* logit_bias, const void* hq, const int64_t hq_strides[4], const void* hk,
@@ -1000,8 +1145,9 @@ extern "C" int ltv_hm_look_back_scan_backward_split(
     const int64_t grad_hk_strides[4], const void* grad_hv, const int64_t grad_hv_strides[4],
     void* grad_values, const int64_t grad_values_strides[4], void* grad_logits,
     const int64_t grad_logits_strides[4], void* grad_inits, const int64_t grad_inits_strides[3],
-    float* grad_logit_bias, void* workspace, size_t workspace_bytes, int B, int T, int NH,
-    int NKVH, int Da, int r, int P, int Q, int K, int use_sigmoid, void* stream) {
+    float* grad_logit_bias, void* workspace, size_t workspace_bytes, void* chain_workspace,
+    size_t chain_workspace_bytes, int B, int T, int NH, int NKVH, int Da, int r, int P, int Q,
+    int K, int use_sigmoid, void* stream) {
   LTV_REQUIRE(values_strides && logits_strides && inits_strides && hq_strides && hk_strides &&
                   hv_strides && grad_hq_strides && grad_hk_strides && grad_hv_strides &&
                   grad_values_strides && grad_logits_strides && grad_inits_strides,
@@ -1015,8 +1161,27 @@ extern "C" int ltv_hm_look_back_scan_backward_split(
                             view4(grad_values, grad_values_strides),
                             view4(grad_logits, grad_logits_strides),
                             view3(grad_inits, grad_inits_strides), grad_logit_bias, workspace,
-                            workspace_bytes, B, T, NH, NKVH, Da, r, P, Q, K, use_sigmoid,
-                            (hipStream_t)stream);
+                            workspace_bytes, chain_workspace, chain_workspace_bytes, B, T, NH,
+                            NKVH, Da, r, P, Q, K, use_sigmoid, (hipStream_t)stream);
+}
+
+extern "C" int ltv_hm_look_back_scan_backward_split(
+    int dtype, const void* values, const int64_t values_strides[4], const void* logits,
+    const int64_t logits_strides[4], const void* inits, const int64_t inits_strides[3],
+    const float* logit_bias, const void* hq, const int64_t hq_strides[4], const void* hk,
+    const int64_t hk_strides[4], const void* hv, const int64_t hv_strides[4],
+    const void* grad_hq, const int64_t grad_hq_strides[4], const void* grad_hk,
+    const int64_t grad_hk_strides[4], const void* grad_hv, const int64_t grad_hv_strides[4],
+    void* grad_values, const int64_t grad_values_strides[4], void* grad_logits,
+    const int64_t grad_logits_strides[4], void* grad_inits, const int64_t grad_inits_strides[3],
+    float* grad_logit_bias, void* workspace, size_t workspace_bytes, int B, int T, int NH,
+    int NKVH, int Da, int r, int P, int Q, int K, int use_sigmoid, void* stream) {
+  return ltv_hm_look_back_scan_backward_split_ws(
+      dtype, values, values_strides, logits, logits_strides, inits, inits_strides, logit_bias,
+      hq, hq_strides, hk, hk_strides, hv, hv_strides, grad_hq, grad_hq_strides, grad_hk,
+      grad_hk_strides, grad_hv, grad_hv_strides, grad_values, grad_values_strides, grad_logits,
+      grad_logits_strides, grad_inits, grad_inits_strides, grad_logit_bias, workspace,
+      workspace_bytes, nullptr, 0, B, T, NH, NKVH, Da, r, P, Q, K, use_sigmoid, stream);
 }
 
 extern "C" int ltv_hm_scan_backward_split(

@@ -157,6 +157,13 @@ struct BwdArgs {
   float* wdl;
   float* wdi;
   int lanes;  // short-window kernel: lanes per window (a power of two >= D / V)
+  // Chained mode of the tile kernel (one tile per chunk, chunks of a sequence
+  // handed their gradient carry through tagged words): the ticket counter, the
+  // error word and the words, (B H, nchunk - 1, CL V) -- the same zeroed
+  // workspace layout as the chained forward's.
+  uint32_t* ch_ticket;
+  uint32_t* ch_err;
+  unsigned long long* ch_words;
 };
 
 // How a lane finds the gate of each of its V channels.
@@ -1026,7 +1033,16 @@ scan_fwd_chain_kernel(const FwdArgs args, const ChainArgs ch) {
 // GATE_CHAN / GATE_CHANVEC: V % r == 0; each lane holds V / r whole groups.
 constexpr int kMaxLaneGroups = 16;
 
-template <typename TIO, int CL, int L, int NW, bool VEC, int GM, bool LB>
+// CHAIN: one tile per chunk (chunk_steps == TW), chunks taken last to first in
+// ticket order, each entering with the gradient carry that the workgroup of
+// the chunk after it publishes (the chained forward's hand-off, run in
+// reverse).  The carry is composed from the same wavefront totals in the same
+// order as the tile loop's, so every output but the dbias partials (one per
+// chunk instead of one per sequence) is bitwise that of the unchunked kernel
+// with the same launch shape.  Deadlock-free for the chained forward's
+// reason: a workgroup waits only for a smaller ticket, drawn by a workgroup
+// that is already running.
+template <typename TIO, int CL, int L, int NW, bool VEC, int GM, bool LB, bool CHAIN = false>
 __global__ void __launch_bounds__(NW * 64)
 scan_bwd_kernel(const BwdArgs args) {
   constexpr int V = Pack<TIO>::V;
@@ -1034,7 +1050,10 @@ scan_bwd_kernel(const BwdArgs args) {
   constexpr int NA = GM == GATE_LANE ? 1 : V;
   constexpr int TW = NW * TG * L;
   constexpr int NT = NW * 64;
+  constexpr int NCH = CL * V;  // chained mode: one carry word per channel slot
   constexpr bool GL = GM == GATE_LANE;
+  static_assert(!(CHAIN && LB), "the chained backward runs the full recurrence");
+  static_assert(!CHAIN || NCH <= NT, "the chain step takes one thread per channel slot");
   const ScanShape& S = args.sh;
 
   const int lane = threadIdx.x & 63;
@@ -1043,7 +1062,32 @@ scan_bwd_kernel(const BwdArgs args) {
   const int tg = lane % TG;
 
   // one workgroup per (b, head, time chunk): every gate group of the head inside
-  const int bh = blockIdx.x / args.nchunk, chunk = blockIdx.x % args.nchunk;
+  int bh = blockIdx.x / args.nchunk, chunk = blockIdx.x % args.nchunk;
+  __shared__ int lds_ticket;
+  __shared__ float lds_cin[CHAIN ? NCH : 1];  // the carry entering the chunk
+  if constexpr (CHAIN) {
+    if (threadIdx.x == 0) {
+      const uint32_t t =
+          __hip_atomic_fetch_add(args.ch_ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      // every other workgroup has drawn its ticket: leave the counter at 0
+      if (t == gridDim.x - 1)
+        __hip_atomic_store(args.ch_ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      lds_ticket = (int)t;
+    }
+    __syncthreads();
+    const int ticket = lds_ticket;
+    // a counter that was not zero at the launch hands out tickets past the
+    // grid: such a workgroup only reports it (the others' waits end at their
+    // bound)
+    if (ticket >= (int)gridDim.x) {
+      if (threadIdx.x == 0)
+        __hip_atomic_store(args.ch_err, 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      return;
+    }
+    const int nseq = S.B * S.H;
+    bh = ticket % nseq;
+    chunk = args.nchunk - 1 - ticket / nseq;
+  }
   const int h = bh % S.H;
   const int b = bh / S.H;
 
@@ -1087,7 +1131,7 @@ scan_bwd_kernel(const BwdArgs args) {
   float gcarry[V];  // g at the first step after the current tile
 #pragma unroll
   for (int v = 0; v < V; ++v) gcarry[v] = 0.0f;
-  if (!LB && args.nchunk > 1) {
+  if (!LB && !CHAIN && args.nchunk > 1) {
     const float* cp = args.carry + ((int64_t)bh * args.nchunk + chunk) * S.D + c0;
 #pragma unroll
     for (int v = 0; v < V; ++v) gcarry[v] = v < nvalid ? cp[v] : 0.0f;
@@ -1158,8 +1202,9 @@ scan_bwd_kernel(const BwdArgs args) {
   // L - 1 states h_t = h_{t-1} + alpha_t (u_t - h_{t-1}) itself, rounded to
   // the I/O dtype as the forward stores them.  A tile before it_lo is all
   // masked: no memory access.
-  constexpr int PD = L <= 2 ? 2 : 1;
-  constexpr int NB = PD == 2 || (GL && L <= 4) ? 2 : 1;
+  // (The chained mode runs one tile: no prefetch, one buffer.)
+  constexpr int PD = CHAIN || L > 2 ? 1 : 2;
+  constexpr int NB = !CHAIN && (PD == 2 || (GL && L <= 4)) ? 2 : 1;
   // the state entering the lane comes from one of three masked loads, kept
   // apart until the tile uses it (merging them at once would wait for the
   // loads just issued)
@@ -1227,7 +1272,8 @@ scan_bwd_kernel(const BwdArgs args) {
     }
     float al[L + 1][NA];
     nl[buf].gates(gi, t0, t_hi, active, use_sig, al);
-    load_tile(it - PD, std::integral_constant<int, PD == 1 && NB == 2 ? 1 - buf : buf>{});
+    if constexpr (!CHAIN)
+      load_tile(it - PD, std::integral_constant<int, PD == 1 && NB == 2 ? 1 - buf : buf>{});
     // h_{t-1} of the lane's later steps (padded steps have alpha = 0)
 #pragma unroll
     for (int s = 1; s < L; ++s) {
@@ -1285,6 +1331,49 @@ scan_bwd_kernel(const BwdArgs args) {
           lds_bx[par][w][cl][q] = make_float4(G[4 * q], G[4 * q + 1], G[4 * q + 2], G[4 * q + 3]);
       }
       __syncthreads();  // (2)
+      if constexpr (CHAIN) {
+        // the chain step: thread j (channel slot j) takes the carry entering
+        // the chunk from the chunk after it, publishes the carry leaving it
+        // for the chunk before, and hands the entering one to every lane
+        if (threadIdx.x < NCH) {
+          const int j = threadIdx.x, jl = j / V, jv = j % V;
+          float cin = 0.0f;
+          if (j < S.D) {
+            const int64_t row = (int64_t)bh * (args.nchunk - 1);
+            if (chunk + 1 < args.nchunk) {
+              unsigned long long* pw = args.ch_words + (row + chunk) * NCH + j;
+              unsigned long long wv = 0;
+              for (int spin = 0;; ++spin) {
+                wv = __hip_atomic_load(pw, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if ((wv >> 32) != 0) break;
+                if (spin >= kChainSpinMax) {
+                  __hip_atomic_store(args.ch_err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                  wv = 0;
+                  break;
+                }
+                __builtin_amdgcn_s_sleep(1);
+              }
+              __hip_atomic_store(pw, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+              cin = __uint_as_float((uint32_t)wv);
+            }
+            if (chunk > 0) {
+              // the tile loop's composition, last wavefront first
+              const float* xb = reinterpret_cast<const float*>(&lds_bx[par][0][0][0]);
+              float p = cin;
+#pragma unroll
+              for (int ww = NW - 1; ww >= 0; --ww)
+                p = fmaf(lds_ba[par][ww][jl][GL ? 0 : jv], p, xb[(ww * CL + jl) * V + jv]);
+              __hip_atomic_store(args.ch_words + (row + chunk - 1) * NCH + j,
+                                 kChainTag | __float_as_uint(p), __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_AGENT);
+            }
+          }
+          lds_cin[j] = cin;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int v = 0; v < V; ++v) gcarry[v] = lds_cin[c0 + v];
+      }
       float gw[V];
 #pragma unroll
       for (int v = 0; v < V; ++v) gw[v] = gcarry[v];
@@ -1766,6 +1855,10 @@ int scan_launch_fwd_chain(bool bf16, const FwdArgs& a, const ChainArgs& ch, Scan
 // head; lb selects the look-back window kernels.
 int scan_launch_bwd(bool bf16, const BwdArgs& a, ScanCfg cfg, int grid, bool vec, int gm,
                     bool lb, hipStream_t st);
+// Chained backward: grid = B * H * nchunk workgroups, one tile per chunk
+// (vector accesses only; gate modes GATE_LANE and GATE_CHANVEC).
+int scan_launch_bwd_chain(bool bf16, const BwdArgs& a, ScanCfg cfg, int grid, int gm,
+                          hipStream_t st);
 // Look-back backward: warm-up contributions into du / dlg, then grad_inits.
 int scan_launch_lb_fold(bool bf16, const BwdArgs& a, hipStream_t st);
 int scan_launch_lb_dinit(bool bf16, const BwdArgs& a, hipStream_t st);

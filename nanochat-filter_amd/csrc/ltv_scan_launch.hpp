@@ -113,6 +113,21 @@ bool bwd_dispatch(const BwdArgs& a, int grid, bool vec, int gm, bool lb, hipStre
   return false;
 }
 
+template <typename TIO, int CL, int L, int NW>
+bool bwd_chain_dispatch(const BwdArgs& a, int grid, int gm, hipStream_t st) {
+  const dim3 blk(NW * 64);
+  switch (gm) {
+    case GATE_LANE:
+      hipLaunchKernelGGL((scan_bwd_kernel<TIO, CL, L, NW, true, GATE_LANE, false, true>), dim3(grid), blk, 0, st, a);
+      return true;
+    case GATE_CHANVEC:
+      hipLaunchKernelGGL((scan_bwd_kernel<TIO, CL, L, NW, true, GATE_CHANVEC, false, true>), dim3(grid), blk, 0, st, a);
+      return true;
+    default:
+      return false;
+  }
+}
+
 }  // namespace detail
 
 // The launch shapes built for each direction: (CL, L, NW).
@@ -186,6 +201,29 @@ int scan_bwd_launch_t(const BwdArgs& a, ScanCfg c, int grid, bool vec, int gm, b
   return LTV_OK;
 }
 
+// Chained backward shapes (CL, L, NW): a whole head per workgroup, its CL V
+// channel slots at most the workgroup's threads.
+#define LTV_SCAN_BWD_CHAIN_CONFIGS(X) \
+  X(16, 4, 2) X(16, 4, 4) X(16, 8, 2) X(16, 8, 4) X(16, 2, 4) X(8, 4, 4) X(32, 4, 4) X(32, 4, 2)
+
+template <typename TIO>
+int scan_bwd_chain_launch_t(const BwdArgs& a, ScanCfg c, int grid, int gm, hipStream_t st) {
+  bool ok = false;
+#define LTV_X(CL_, L_, NW_)                                                   \
+  if constexpr (CL_ * Pack<TIO>::V <= NW_ * 64)                               \
+    if (!ok && c.CL == CL_ && c.L == L_ && c.NW == NW_)                       \
+      ok = detail::bwd_chain_dispatch<TIO, CL_, L_, NW_>(a, grid, gm, st);
+  LTV_SCAN_BWD_CHAIN_CONFIGS(LTV_X)
+#undef LTV_X
+  if (!ok) {
+    set_error("scan backward (chained): launch shape CL=%d L=%d NW=%d (gate=%d) is not built",
+              c.CL, c.L, c.NW, gm);
+    return LTV_ERR_UNSUPPORTED;
+  }
+  LTV_LAUNCH_CHECK();
+  return LTV_OK;
+}
+
 // Per-dtype entry points (defined in the four translation units).
 int scan_fwd_launch_bf16(const FwdArgs& a, ScanCfg c, int grid, bool vec, int gm, hipStream_t st);
 int scan_fwd_launch_f32(const FwdArgs& a, ScanCfg c, int grid, bool vec, int gm, hipStream_t st);
@@ -197,5 +235,7 @@ int scan_bwd_launch_bf16(const BwdArgs& a, ScanCfg c, int grid, bool vec, int gm
                          hipStream_t st);
 int scan_bwd_launch_f32(const BwdArgs& a, ScanCfg c, int grid, bool vec, int gm, bool lb,
                         hipStream_t st);
+int scan_bwd_chain_launch_bf16(const BwdArgs& a, ScanCfg c, int grid, int gm, hipStream_t st);
+int scan_bwd_chain_launch_f32(const BwdArgs& a, ScanCfg c, int grid, int gm, hipStream_t st);
 
 }  // namespace ltv

@@ -106,6 +106,27 @@ SIGNATURES = {
          _c_vp, _c_sz, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
          _c_int, _c_vp],
     ),
+    "ltv_hm_scan_backward_chain_workspace_size": (
+        _c_sz, [_c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int]),
+    # the backward with a chain workspace: (chain workspace, bytes) after the workspace
+    "ltv_hm_scan_backward_ws": (
+        _c_int,
+        [_c_int, _c_vp, _c_i64p, _c_vp, _c_i64p, _c_vp,
+         _c_vp, _c_i64p, _c_vp, _c_i64p, _c_vp, _c_i64p,
+         _c_vp, _c_i64p, _c_vp, _c_i64p, _c_vp, _c_i64p,
+         _c_vp, _c_i64p, _c_vp, _c_i64p, _c_vp,
+         _c_vp, _c_sz, _c_vp, _c_sz, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
+         _c_vp],
+    ),
+    "ltv_hm_look_back_scan_backward_split_ws": (
+        _c_int,
+        [_c_int, _c_vp, _c_i64p, _c_vp, _c_i64p, _c_vp, _c_i64p, _c_vp,
+         _c_vp, _c_i64p, _c_vp, _c_i64p, _c_vp, _c_i64p,
+         _c_vp, _c_i64p, _c_vp, _c_i64p, _c_vp, _c_i64p,
+         _c_vp, _c_i64p, _c_vp, _c_i64p, _c_vp, _c_i64p, _c_vp,
+         _c_vp, _c_sz, _c_vp, _c_sz, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
+         _c_int, _c_int, _c_int, _c_vp],
+    ),
     "ltv_linear_transpose_forward": (
         _c_int, [_c_int, _c_vp, _c_vp, _c_vp, _c_int, _c_int, _c_int, _c_int, _c_vp]),
     "ltv_linear_transpose_backward": (
@@ -222,16 +243,18 @@ def stream_of(t: torch.Tensor) -> int:
     return torch.cuda.current_stream(t.device).cuda_stream
 
 
-# Chain workspaces of the chained scan forward (ltv_hm_scan_forward_ws): zeroed
-# once, left zeroed by every call, so one buffer per (device, stream) serves
-# every later call on that stream.  Under graph capture each call gets a fresh
-# zeroed buffer from the graph's pool (its zero fill is captured with it).
+# Chain workspaces of the chained scan forward and backward (the library's
+# *_ws entry points): zeroed once, left zeroed by every call, so one buffer per
+# (device, stream) serves every later call on that stream, in either
+# direction (calls on one stream run one after another).  Under graph capture
+# each call gets a fresh zeroed buffer from the graph's pool (its zero fill is
+# captured with it).
 _CHAIN_WS: dict = {}
 
 
 def chain_workspace(device: torch.device, nbytes: int):
     """A 256-byte aligned, all-zero device buffer of at least ``nbytes`` bytes
-    reserved for the chained scan forward on the current stream, or None when
+    reserved for the chained scans on the current stream, or None when
     nbytes == 0."""
     if nbytes <= 0:
         return None
@@ -248,11 +271,13 @@ def chain_workspace(device: torch.device, nbytes: int):
 
 
 def chain_workspace_for(dtype: torch.dtype, device: torch.device, B: int, T: int, NH: int,
-                        NKVH: int, Da: int, r: int):
+                        NKVH: int, Da: int, r: int, backward: bool = False):
     """(pointer, bytes) of the chain workspace for this scan shape, (None, 0)
-    where the chained forward does not apply."""
-    nbytes = lib().ltv_hm_scan_forward_chain_workspace_size(dtype_code(dtype), B, T, NH, NKVH,
-                                                           Da, r)
+    where the chained forward (or, with ``backward``, the chained backward)
+    does not apply."""
+    size = (lib().ltv_hm_scan_backward_chain_workspace_size if backward
+            else lib().ltv_hm_scan_forward_chain_workspace_size)
+    nbytes = size(dtype_code(dtype), B, T, NH, NKVH, Da, r)
     buf = chain_workspace(device, nbytes)
     if buf is None:
         return None, 0

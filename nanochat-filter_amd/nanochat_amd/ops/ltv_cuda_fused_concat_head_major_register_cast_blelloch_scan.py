@@ -6,7 +6,8 @@ Behavioural mirror of the reference's
 ``:141-193``, autograd ``:196-289``): same schemas, same buffer ownership
 (Python allocates every output; kernels only write), same argument checks.
 The work is done by the gfx950 library through
-``ltv_hm_scan_forward`` / ``ltv_hm_scan_backward``.
+``ltv_hm_scan_forward`` / ``ltv_hm_scan_backward`` (their ``_ws`` forms, with the chain
+workspace of the chained scans).
 """
 
 import torch
@@ -184,7 +185,9 @@ def backward_kernel(
     lib = N.lib()
     ws_bytes = lib.ltv_hm_scan_backward_workspace_size(dt, B, T, NH, NKVH, da, r)
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=combined.device)
-    rc = lib.ltv_hm_scan_backward(
+    cws, cws_bytes = N.chain_workspace_for(combined.dtype, combined.device, B, T, NH, NKVH, da, r,
+                                           backward=True)
+    rc = lib.ltv_hm_scan_backward_ws(
         dt,
         combined.data_ptr(), N.strides(combined, 3),
         inits.data_ptr(), N.strides(inits, 3),
@@ -195,11 +198,11 @@ def backward_kernel(
         grad_combined.data_ptr(), N.strides(grad_combined, 3),
         grad_inits.data_ptr(), N.strides(grad_inits, 3),
         grad_logit_bias.data_ptr(),
-        ws.data_ptr(), ws_bytes,
+        ws.data_ptr(), ws_bytes, cws, cws_bytes,
         B, T, NH, NKVH, da, r, int(bool(use_sigmoid)),
         N.stream_of(combined),
     )
-    N.check(rc, "ltv_hm_scan_backward")
+    N.check(rc, "ltv_hm_scan_backward_ws")
 
 
 def _setup(ctx, inputs, output):

@@ -245,8 +245,11 @@ def scan_backward(values, logits, inits, logit_bias, hq, hk, hv, gq, gk, gv, NH:
     gvals = (gsb, D * gsc, gst, gsc)
     glgs = (gsb, Da * gsc, gst, gsc)
     glg_ptr = grad_combined.data_ptr() + H * D * gsc * grad_combined.element_size()
+    cws, cws_bytes = (N.chain_workspace_for(values.dtype, values.device, B, T, NH, NKVH, Da, r,
+                                            backward=True)
+                      if P >= T else (None, 0))
     with N.span("scan_bwd"):
-        rc = lib.ltv_hm_look_back_scan_backward_split(
+        rc = lib.ltv_hm_look_back_scan_backward_split_ws(
             dt,
             values.data_ptr(), N.strides(values, 4), logits.data_ptr(), _arr(lgs),
             inits.data_ptr(), N.strides(inits, 3), logit_bias.data_ptr(),
@@ -256,9 +259,9 @@ def scan_backward(values, logits, inits, logit_bias, hq, hk, hv, gq, gk, gv, NH:
             gv.data_ptr(), N.strides(gv, 4),
             grad_combined.data_ptr(), _arr(gvals), glg_ptr, _arr(glgs),
             grad_inits.data_ptr(), N.strides(grad_inits, 3), grad_bias.data_ptr(),
-            ws.data_ptr(), ws_bytes, B, T, NH, NKVH, Da, r, P, Q, K, int(bool(use_sigmoid)),
-            N.stream_of(values))
-    N.check(rc, "ltv_hm_look_back_scan_backward_split")
+            ws.data_ptr(), ws_bytes, cws, cws_bytes, B, T, NH, NKVH, Da, r, P, Q, K,
+            int(bool(use_sigmoid)), N.stream_of(values))
+    N.check(rc, "ltv_hm_look_back_scan_backward_split_ws")
     return grad_inits, grad_bias
 
 

@@ -47,7 +47,7 @@ def test_abi_version_and_host_only_queries():
     if not os.path.exists(N.LIB_PATH):
         pytest.skip("library not built")
     lib = N.load()
-    assert lib.ltv_abi_version() == 4
+    assert lib.ltv_abi_version() == 5
     # d12: 18 heads x (128 + 1) = 2322 -> padded to a multiple of 128; 18 logits -> 24
     assert lib.ltv_qkv_packed_width(18, 128, 1) == 2432
     assert lib.ltv_qkv_logit_width(18, 1) == 24
@@ -65,6 +65,23 @@ def test_abi_version_and_host_only_queries():
     assert lib.ltv_hm_scan_forward_chain_workspace_size(1, 32, 1024, 6, 6, 1, 128) == 0
     assert lib.ltv_hm_scan_forward_chain_workspace_size(1, 2, 64, 1, 1, 32, 4) == 0
     assert lib.ltv_hm_scan_forward_chain_workspace_size(1, 2, 0, 1, 1, 1, 128) == 0
+    # chained scan backward: the same layout, one word per channel of a whole
+    # head (CL V = 128) per chunk but a sequence's first.  B = 16 at d12 heads
+    # (288 sequences): 16 chunks of 64 steps (16 channel lanes x 4 time groups
+    # x 4 steps x 4 wavefronts); fp32: 32 channel lanes, chunks of 32 steps;
+    # d12 itself (576 sequences), one chunk (T = 64), gate groups of 4
+    # channels, or T = 0: no chained kernel
+    assert lib.ltv_hm_scan_backward_chain_workspace_size(1, 16, 1024, 6, 6, 1, 128) == \
+        256 + 16 * 18 * 15 * 128 * 8
+    assert lib.ltv_hm_scan_backward_chain_workspace_size(0, 2, 1024, 6, 6, 1, 128) == \
+        256 + 2 * 18 * 31 * 128 * 8
+    assert lib.ltv_hm_scan_backward_chain_workspace_size(1, 32, 1024, 6, 6, 1, 128) == 0
+    assert lib.ltv_hm_scan_backward_chain_workspace_size(1, 2, 64, 6, 6, 1, 128) == 0
+    assert lib.ltv_hm_scan_backward_chain_workspace_size(1, 2, 1024, 1, 1, 32, 4) == 0
+    assert lib.ltv_hm_scan_backward_chain_workspace_size(1, 2, 0, 1, 1, 1, 128) == 0
+    # the scan backward's own workspace holds the chained kernel's dbias
+    # partials (one per (b, h, chunk)) as well as the tile kernel's
+    assert lib.ltv_hm_scan_backward_workspace_size(1, 16, 1024, 6, 6, 1, 128) >= 16 * 18 * 16 * 4
     # argument errors are reported without touching a device
     rc = lib.ltv_qkv_project_forward(None, None, None, None, 2, 8, 12, 3, 64, 1, None)
     assert rc == 2 and "multiple of 8" in N.last_error()

@@ -1,7 +1,9 @@
-"""GPU parity of the chained scan forward (``ltv_hm_scan_forward_ws`` and the
+"""GPU parity of the chained scans.  Forward (``ltv_hm_scan_forward_ws`` and the
 split-layout ``ltv_hm_look_back_scan_forward_split_ws``, called here): one
 workgroup per chunk of T, the state at a chunk's end handed to the next
-chunk's workgroup through a zero-invariant workspace.
+chunk's workgroup through a zero-invariant workspace.  Backward
+(``ltv_hm_look_back_scan_backward_split_ws``): one tile-long chunk per
+workgroup, last chunk first, the gradient carry handed to the chunk before.
 
 Checked against the CPU oracle (exact on the reference's integer generators,
 within the stated tolerance with the sigmoid), against the tile kernel (the
@@ -322,3 +324,274 @@ def test_chain_graph_replays_match_eager():
         again = F_.scan_forward(values, logits, inits, bias, NH, NKVH, 1, D, True)
         for a, b in zip(again, eager):
             assert torch.equal(a, b)
+
+
+# ---------------------------------------------------------------------------
+# chained backward (ltv_hm_look_back_scan_backward_split_ws /
+# ltv_hm_scan_backward_ws): one tile-long chunk per workgroup, last chunk
+# first, the gradient carry handed backwards through the same kind of
+# zero-invariant workspace
+# ---------------------------------------------------------------------------
+def _bwd_ws_bytes(dtype, B, T, NH, NKVH, Da, r):
+    N, lib = _lib()
+    return lib.ltv_hm_scan_backward_chain_workspace_size(N.dtype_code(dtype), B, T, NH, NKVH,
+                                                         Da, r)
+
+
+def _backward(comb, ini, bias, outs, grads, NH, NKVH, Da, r, sig, ws=None):
+    """Scan backward of the split layout through the C ABI: the chained kernel
+    with a chain workspace tensor, the tile kernels (with their chunk-map
+    passes below 256 sequences) without one.  Returns grad_values
+    (B, H, T, D), grad_logits (B, H, T, Da), grad_inits (B, H, D) and
+    grad_logit_bias (H, Da)."""
+    N, lib = _lib()
+    B, T, _ = comb.shape
+    H, D = NH + 2 * NKVH, Da * r
+    dt = N.dtype_code(comb.dtype)
+    values, logits = _split(comb, NH, NKVH, Da, r)
+    nan = float("nan")
+    gval = torch.full((B, H, T, D), nan, dtype=comb.dtype, device=DEV)
+    glog = torch.full((B, H, T, Da), nan, dtype=comb.dtype, device=DEV)
+    gini = torch.full((B, H, D), nan, dtype=comb.dtype, device=DEV)
+    gbias = torch.full((H, Da), nan, dtype=torch.float32, device=DEV)
+    nbytes = lib.ltv_hm_look_back_scan_backward_workspace_size(dt, B, T, NH, NKVH, Da, r,
+                                                               UNBOUNDED_P, 1, 1)
+    scratch = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=DEV)
+    args = [dt, values.data_ptr(), _s(values), logits.data_ptr(), _s(logits), ini.data_ptr(),
+            _s(ini), bias.data_ptr()]
+    for t in list(outs) + list(grads):
+        args += [t.data_ptr(), _s(t)]
+    args += [gval.data_ptr(), _s(gval), glog.data_ptr(), _s(glog), gini.data_ptr(), _s(gini),
+             gbias.data_ptr(), scratch.data_ptr(), nbytes]
+    tail = [B, T, NH, NKVH, Da, r, UNBOUNDED_P, 1, 1, int(sig), N.stream_of(comb)]
+    if ws is None:
+        rc = lib.ltv_hm_look_back_scan_backward_split(*args, *tail)
+    else:
+        rc = lib.ltv_hm_look_back_scan_backward_split_ws(*args, ws.data_ptr(), ws.numel(), *tail)
+    N.check(rc, "scan backward")
+    return gval, glog, gini, gbias
+
+
+def _expected_backward(c, ini, bias, outs, gy, NH, NKVH, Da, r, sig, io):
+    """The oracle's backward from the given saved outputs, in the split
+    layout: (grad_values (B, H, T, D), grad_logits (B, H, T, Da), grad_inits,
+    grad_logit_bias)."""
+    H, D = NH + 2 * NKVH, Da * r
+    B, T = c.shape[:2]
+    gc, gi, gb = O.scan_backward(c, ini, bias, *outs, gy[:, :NH], gy[:, NH:NH + NKVH],
+                                 gy[:, NH + NKVH:H], NH, NKVH, Da, r, sig, io)
+    x = gc.reshape(B, T, H, D + Da).transpose(0, 2, 1, 3)
+    return x[..., :D], x[..., D:], gi, gb
+
+
+def _torch_grads(gy, NH, NKVH, dtype):
+    """Upstream gradients (B, H, T, D) as the (B, T, nh, D)-contiguous views a
+    caller's transposes hand the scan."""
+    H = gy.shape[1]
+    out = []
+    for lo, hi in ((0, NH), (NH, NH + NKVH), (NH + NKVH, H)):
+        g = to_torch(np.ascontiguousarray(gy[:, lo:hi].transpose(0, 2, 1, 3)), dtype, DEV)
+        out.append(g.transpose(1, 2))
+    return out
+
+
+# chained-eligible shapes: several chunks (64 steps in bf16, 32 in fp32 at
+# 128 channels), ragged tails, one gate per head, gate groups of 16 channels,
+# and per-channel gates (r = 1)
+BWD_CASES = [
+    # (B, T, NH, NKVH, Da, r)
+    (2, 65, 2, 1, 1, 128),
+    (2, 300, 2, 1, 1, 128),
+    (1, 1537, 1, 1, 1, 128),
+    (1, 4133, 1, 1, 8, 16),
+    (2, 700, 1, 1, 64, 1),
+    (1, 129, 1, 0, 128, 1),
+]
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=io_name)
+@pytest.mark.parametrize("B,T,NH,NKVH,Da,r", BWD_CASES)
+def test_chain_backward_exact_integer(dtype, B, T, NH, NKVH, Da, r):
+    """The reference's integer generators without the sigmoid, upstream
+    gradients of ones (its own backward check): every gradient exact, the
+    dbias sums included (integers below 2^24), across chunk hand-offs."""
+    nbytes = _bwd_ws_bytes(dtype, B, T, NH, NKVH, Da, r)
+    assert nbytes > 0, "the chained backward should apply to this shape"
+    io = io_name(dtype)
+    H, D = NH + 2 * NKVH, Da * r
+    c = int_combined(B, T, NH, NKVH, Da, r)
+    ini = int_inits(B, NH, NKVH, Da, r)
+    bias = int_logit_bias(NH, NKVH, Da, False)
+    outs = O.scan_forward(c, ini, bias, NH, NKVH, Da, r, False, io)
+    gy = np.ones((B, H, T, D), np.float32)
+    want = _expected_backward(c, ini, bias, outs, gy, NH, NKVH, Da, r, False, io)
+    ws = _zero_ws(nbytes)
+    got = _backward(to_torch(c, dtype, DEV), to_torch(ini, dtype, DEV),
+                    to_torch(bias, torch.float32, DEV), [to_torch(o, dtype, DEV) for o in outs],
+                    _torch_grads(gy, NH, NKVH, dtype), NH, NKVH, Da, r, False, ws)
+    case = f"T={T} Da={Da} r={r}"
+    for name, g, w in zip(("grad_values", "grad_logits", "grad_inits", "grad_logit_bias"),
+                          got, want):
+        assert_close(np_of(g), w, 0, f"{name} {case}")
+    _check_ws_clean(ws, case)
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=io_name)
+@pytest.mark.parametrize("B,T,NH,NKVH,Da,r", BWD_CASES)
+def test_chain_backward_sigmoid_vs_oracle_and_tile(dtype, B, T, NH, NKVH, Da, r):
+    """Sigmoid gates, decay sigmoid(N(2, 1)), random upstream gradients:
+    within the tolerance of the oracle; against the tile kernels (chunk-map
+    carries at these sequence counts: another association of the same fp32
+    recurrence) within one bf16 rounding step or 1e-5 in fp32; three calls on
+    one workspace bitwise equal."""
+    io = io_name(dtype)
+    H, D = NH + 2 * NKVH, Da * r
+    c, ini, bias = _random_case(B, T, NH, NKVH, Da, r, seed=T * 5 + r, io=io)
+    gy = O.round_io(np.random.default_rng(T).standard_normal((B, H, T, D)).astype(np.float32),
+                    io)
+    cd, idv, bd = to_torch(c, dtype, DEV), to_torch(ini, dtype, DEV), to_torch(bias, torch.float32, DEV)
+    outs = _forward(cd, idv, bd, NH, NKVH, Da, r, True)
+    grads = _torch_grads(gy, NH, NKVH, dtype)
+    want = _expected_backward(c, ini, bias, [np_of(o) for o in outs], gy, NH, NKVH, Da, r, True,
+                              io)
+    ws = _zero_ws(_bwd_ws_bytes(dtype, B, T, NH, NKVH, Da, r))
+    runs = [_backward(cd, idv, bd, outs, grads, NH, NKVH, Da, r, True, ws) for _ in range(3)]
+    for run in runs[1:]:
+        for a, b in zip(runs[0], run):
+            assert torch.equal(a, b)
+    tol = TOL[dtype]
+    case = f"T={T} Da={Da} r={r}"
+    names = ("grad_values", "grad_logits", "grad_inits", "grad_logit_bias")
+    for name, g, w in zip(names, runs[0], want):
+        assert_close(np_of(g), w, tol, f"{name} {case}")
+    tile = _backward(cd, idv, bd, outs, grads, NH, NKVH, Da, r, True)
+    for name, a, b, w in zip(names, runs[0], tile, want):
+        assert_close(np_of(b), w, tol, f"tile {name} {case}")
+        _assert_same_up_to_association(a, b, dtype if name != "grad_logit_bias" else torch.float32,
+                                       f"chained vs tile {name} {case}")
+    _check_ws_clean(ws, case)
+
+
+def test_chain_backward_bitwise_equals_unchunked_tile():
+    """288 (b, h) sequences of d12 heads (B = 16): the tile kernel runs them
+    unchunked, 4 steps per lane like the chained kernel, and the chained
+    carries are composed in the tile loop's order -- so grad_values,
+    grad_logits and grad_inits are bitwise equal; grad_logit_bias sums
+    per-chunk partials instead of per-sequence ones (rel. 1e-5)."""
+    B, T, NH, NKVH, Da, r = 16, 333, 6, 6, 1, 128
+    dtype = torch.bfloat16
+    H, D = NH + 2 * NKVH, Da * r
+    assert _bwd_ws_bytes(dtype, B, T, NH, NKVH, Da, r) > 0
+    c, ini, bias = _random_case(B, T, NH, NKVH, Da, r, seed=16, io="bf16")
+    gy = O.round_io(np.random.default_rng(7).standard_normal((B, H, T, D)).astype(np.float32),
+                    "bf16")
+    cd, idv, bd = to_torch(c, dtype, DEV), to_torch(ini, dtype, DEV), to_torch(bias, torch.float32, DEV)
+    outs = _forward(cd, idv, bd, NH, NKVH, Da, r, True)
+    grads = _torch_grads(gy, NH, NKVH, dtype)
+    ws = _zero_ws(_bwd_ws_bytes(dtype, B, T, NH, NKVH, Da, r))
+    chain = _backward(cd, idv, bd, outs, grads, NH, NKVH, Da, r, True, ws)
+    tile = _backward(cd, idv, bd, outs, grads, NH, NKVH, Da, r, True)
+    for name, a, b in zip(("grad_values", "grad_logits", "grad_inits"), chain[:3], tile[:3]):
+        assert torch.equal(a, b), name
+    assert torch.allclose(chain[3], tile[3], rtol=1e-5, atol=1e-5 * float(tile[3].abs().max()))
+    _check_ws_clean(ws, "B=16 d12 heads")
+
+
+def test_chain_backward_workspace_errors():
+    """A chain workspace below the queried size or off 256-byte alignment is
+    refused before any launch and left untouched."""
+    B, T, NH, NKVH, Da, r = 1, 2000, 1, 1, 1, 128
+    dtype = torch.bfloat16
+    H, D = NH + 2 * NKVH, Da * r
+    nbytes = _bwd_ws_bytes(dtype, B, T, NH, NKVH, Da, r)
+    c, ini, bias = _random_case(B, T, NH, NKVH, Da, r, seed=2, io="bf16")
+    cd, idv, bd = to_torch(c, dtype, DEV), to_torch(ini, dtype, DEV), to_torch(bias, torch.float32, DEV)
+    outs = _forward(cd, idv, bd, NH, NKVH, Da, r, True)
+    grads = _torch_grads(np.ones((B, H, T, D), np.float32), NH, NKVH, dtype)
+    small = _zero_ws(nbytes - 512)
+    with pytest.raises(RuntimeError, match="workspace too small"):
+        _backward(cd, idv, bd, outs, grads, NH, NKVH, Da, r, True, small[: nbytes - 512])
+    big = _zero_ws(nbytes + 256)
+    with pytest.raises(RuntimeError, match="256-byte aligned"):
+        _backward(cd, idv, bd, outs, grads, NH, NKVH, Da, r, True, big[16:])
+    torch.cuda.synchronize()
+    assert int(torch.count_nonzero(small)) == 0 and int(torch.count_nonzero(big)) == 0
+
+
+def test_chain_forward_and_backward_share_one_workspace():
+    """The fast path's per-stream buffer serves the chained forward and the
+    chained backward in turn: a filter step (B = 2, T = 3000, d12 heads)
+    through the module's autograd, twice, bitwise equal, the buffer zeroed
+    after each."""
+    from nanochat_amd import _native as N
+    from nanochat_amd.ops import ltv_hm_fast as F_
+    B, T, NH, NKVH, D, C = 2, 3000, 2, 1, 128, 256
+    H = NH + 2 * NKVH
+    assert _ws_bytes(torch.bfloat16, B, T, NH, NKVH, 1, D) > 0
+    assert _bwd_ws_bytes(torch.bfloat16, B, T, NH, NKVH, 1, D) > 0
+    g = torch.Generator().manual_seed(4)
+    x = torch.randn(B, T, C, generator=g).to(torch.bfloat16).to(DEV)
+    w = (torch.randn(H * (D + 1), C, generator=g) * C ** -0.5).to(DEV)
+    inits = torch.randn(B, H, D, generator=g).to(torch.bfloat16).to(DEV)
+    bias = torch.zeros(H, 1, device=DEV)
+    dq = torch.randn(B, NH, T, D, generator=g).to(torch.bfloat16).to(DEV)
+    dk = torch.randn(B, NKVH, T, D, generator=g).to(torch.bfloat16).to(DEV)
+    dv = torch.randn(B, NKVH, T, D, generator=g).to(torch.bfloat16).to(DEV)
+
+    def step():
+        xs, ws_, bs = (t.detach().clone().requires_grad_(True) for t in (x, w, bias))
+        q, k, v, *_ = F_.qkv_filter(xs, ws_, inits, bs, NH, NKVH, 1, D)
+        torch.autograd.backward([q, k, v], [dq, dk, dv])
+        return q, xs.grad, ws_.grad, bs.grad
+
+    first, second = step(), step()
+    for a, b in zip(first, second):
+        assert torch.equal(a, b)
+    torch.cuda.synchronize()
+    for buf in N._CHAIN_WS.values():
+        assert int(torch.count_nonzero(buf)) == 0
+
+
+def test_chain_backward_graph_replays_match_eager():
+    """The fast path's scan backward (chained, chain workspace from the
+    graph's pool) captured in a HIP graph: every replay equals the eager
+    result, with eager work and synchronisation between replays."""
+    from nanochat_amd.ops import ltv_hm_fast as F_
+    B, T, NH, NKVH, D = 2, 3000, 2, 1, 128
+    H = NH + 2 * NKVH
+    g = torch.Generator().manual_seed(5)
+    values = torch.randn(B, H, T, D, generator=g).to(torch.bfloat16).to(DEV)
+    logits = (-(2.0 + torch.randn(B, T, H, generator=g))).to(torch.bfloat16).to(DEV)
+    inits = torch.randn(B, H, D, generator=g).to(torch.bfloat16).to(DEV)
+    bias = torch.zeros(H, 1, device=DEV)
+    gys = [torch.randn(B, nh, T, D, generator=g).to(torch.bfloat16).to(DEV) for nh in (NH, NKVH, NKVH)]
+    hq, hk, hv = F_.scan_forward(values, logits, inits, bias, NH, NKVH, 1, D, True)
+    Fp = F_.packed_width(H, D, 1)
+
+    def run(gc):
+        return F_.scan_backward(values, logits, inits, bias, hq, hk, hv, *gys, NH, NKVH, 1, D,
+                                True, gc)
+
+    gc_eager = torch.zeros(B, T, Fp, dtype=torch.bfloat16, device=DEV)
+    gi_eager, gb_eager = run(gc_eager)
+    gc = torch.zeros_like(gc_eager)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        run(gc)  # warm-up
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        gi, gb = run(gc)
+    F = H * (D + 1)
+    for i in range(3):
+        gc.zero_()
+        gi.fill_(0)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(gc[..., :F], gc_eager[..., :F]), f"replay {i}"
+        assert torch.equal(gi, gi_eager) and torch.equal(gb, gb_eager), f"replay {i}"
+        # eager work between the replays
+        gc2 = torch.zeros_like(gc_eager)
+        gi2, gb2 = run(gc2)
+        assert torch.equal(gc2[..., :F], gc_eager[..., :F]) and torch.equal(gi2, gi_eager)

@@ -219,8 +219,9 @@ def test_sigmoid_random(dtype, B, T, NH, NKVH, Da, r):
 def test_long_sequence_long_memory(dtype):
     """Config 5's regime: T = 8192 with gate logits -z, z ~ N(3, 1.5) (decay
     a = 1 - alpha around 0.95, so states carry over hundreds of steps).  Few
-    (b, h) sequences, so the backward runs in time chunks joined by the
-    chunk-map carries."""
+    (b, h) sequences, so the op's backward runs chained (one tile-long chunk
+    per workgroup, the carries handed between them); its tile kernels with the
+    chunk-map carries are compared with it in test_scan_chain_gpu.py."""
     io = io_name(dtype)
     B, T, NH, NKVH, Da, r = 1, 8192, 1, 1, 1, 128
     H = NH + 2 * NKVH
