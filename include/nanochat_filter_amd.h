@@ -45,7 +45,7 @@ extern "C" {
 #define LTV_ERR_HIP 3
 #define LTV_ERR_WORKSPACE 4
 
-/* Version of this ABI (bumped on any signature change or addition): 5. */
+/* Version of this ABI (bumped on any signature change or addition): 6. */
 int ltv_abi_version(void);
 
 /* Message of the last failing call on this host thread ("" if none). */
@@ -274,11 +274,17 @@ int ltv_hm_look_back_scan_forward_split(
 
 /* ltv_hm_look_back_scan_forward_split with the chain workspace of
  * ltv_hm_scan_forward_ws (same contract), used when there is one window (P >= T);
- * with several windows the workspace is not touched. */
+ * with several windows the workspace is not touched.
+ * inits_dtype: the dtype of `inits` -- `dtype`, or LTV_DTYPE_F32 with bf16
+ *   values: fp32 inits (the parameter itself, e.g. (H, D) with batch stride 0)
+ *   rounded to bf16 when read, exactly the reference's
+ *   `init_param.expand(B, H, D).to(bfloat16)` before its kernel, without the
+ *   cast's copy.  The fp32 form needs the full recurrence (P >= T). */
 int ltv_hm_look_back_scan_forward_split_ws(
     int dtype, const void* values, const int64_t values_strides[4], const void* logits,
     const int64_t logits_strides[4], const void* inits, const int64_t inits_strides[3],
-    const float* logit_bias, void* out_q, const int64_t out_q_strides[4], void* out_k,
+    int inits_dtype, const float* logit_bias, void* out_q, const int64_t out_q_strides[4],
+    void* out_k,
     const int64_t out_k_strides[4], void* out_v, const int64_t out_v_strides[4],
     void* chain_workspace, size_t chain_workspace_bytes, int B, int T, int NH, int NKVH, int Da,
     int r, int P, int Q, int K, int use_sigmoid, void* stream);
@@ -297,11 +303,23 @@ int ltv_hm_look_back_scan_backward_split(
 
 /* ltv_hm_look_back_scan_backward_split with the chain workspace of
  * ltv_hm_scan_backward_ws (same contract), used when there is one window
- * (P >= T); with several windows the chain workspace is not touched. */
+ * (P >= T); with several windows the chain workspace is not touched.
+ * inits_dtype: as in ltv_hm_look_back_scan_forward_split_ws; grad_inits has
+ *   the same dtype.  With fp32 inits and bf16 values each sequence's inits
+ *   gradient is the bf16 value widened to fp32 (the cast's backward).
+ * grad_inits with batch stride 0 (e.g. the (H, D) parameter's gradient):
+ *   receives the sum over the batch -- each sequence's gradient rounded to
+ *   the values' dtype, summed in fp32 in batch order, stored in inits_dtype --
+ *   which is what the broadcast's backward computes (the reference sums the
+ *   expanded inits' gradient over B).  Needs the full recurrence and gate
+ *   groups the tile kernels take (r a multiple of 8 bf16 / 4 fp32 channels
+ *   with Da <= 16, or r dividing it); the sum is formed by the launch that
+ *   reduces grad_logit_bias, in `workspace`. */
 int ltv_hm_look_back_scan_backward_split_ws(
     int dtype, const void* values, const int64_t values_strides[4], const void* logits,
     const int64_t logits_strides[4], const void* inits, const int64_t inits_strides[3],
-    const float* logit_bias, const void* hq, const int64_t hq_strides[4], const void* hk,
+    int inits_dtype, const float* logit_bias, const void* hq, const int64_t hq_strides[4],
+    const void* hk,
     const int64_t hk_strides[4], const void* hv, const int64_t hv_strides[4],
     const void* grad_hq, const int64_t grad_hq_strides[4], const void* grad_hk,
     const int64_t grad_hk_strides[4], const void* grad_hv, const int64_t grad_hv_strides[4],

@@ -11,10 +11,25 @@ namespace ltv {
 
 // dbias[h, j] = sum over (b, c) of partial[b, h, c, j]: one workgroup per
 // output, thread i summing the pairs i, i + 256, ... in order, then a fixed
-// tree over the threads (deterministic).
+// tree over the threads (deterministic).  Workgroups from H Da on form the
+// inits gradient's batch sum (DinitSum), one thread per (h, d), in batch order.
 __global__ void __launch_bounds__(256) dbias_reduce_kernel(const float* __restrict__ partial,
                                                            float* __restrict__ dbias, int B,
-                                                           int H, int NC, int Da) {
+                                                           int H, int NC, int Da, DinitSum ds) {
+  if ((int)blockIdx.x >= H * Da) {
+    const int i = ((int)blockIdx.x - H * Da) * 256 + (int)threadIdx.x;
+    if (i < H * ds.D) {
+      const int h = i / ds.D, d = i - h * ds.D;
+      float acc = 0.0f;
+      for (int b = 0; b < B; ++b) acc += ds.ws[((int64_t)b * H + h) * ds.D + d];
+      const int64_t o = (int64_t)h * ds.sh + (int64_t)d * ds.sd;
+      if (ds.out_bf16)
+        reinterpret_cast<bf16_t*>(ds.out)[o] = (bf16_t)(cvt_pk_bf16(acc, 0.0f) & 0xffffu);
+      else
+        reinterpret_cast<float*>(ds.out)[o] = acc;
+    }
+    return;
+  }
   __shared__ float red[256];
   const int i = blockIdx.x;  // h * Da + j
   const int h = i / Da, j = i - h * Da;
@@ -189,9 +204,10 @@ int scan_launch_bwd_chunk_maps(bool bf16, const BwdArgs& a, bool vec, hipStream_
 }
 
 int scan_launch_dbias_reduce(const float* partial, float* dbias, int B, int H, int NC, int Da,
-                             hipStream_t st) {
-  hipLaunchKernelGGL(dbias_reduce_kernel, dim3(H * Da), dim3(256), 0, st, partial, dbias, B, H,
-                     NC, Da);
+                             hipStream_t st, const DinitSum& ds) {
+  const int extra = ds.ws != nullptr ? (H * ds.D + 255) / 256 : 0;
+  hipLaunchKernelGGL(dbias_reduce_kernel, dim3(H * Da + extra), dim3(256), 0, st, partial, dbias,
+                     B, H, NC, Da, ds);
   LTV_LAUNCH_CHECK();
   return LTV_OK;
 }
@@ -443,14 +459,28 @@ int launch_forward(int dtype, FwdArgs& a, bool vec, const HostView4& lg, int B, 
   return scan_launch_fwd(dtype == LTV_DTYPE_BF16, a, cfg, (int)grid, vec, gm, st);
 }
 
+// The inits' dtype: the values' own, or fp32 with bf16 values (the parameter
+// the reference casts to bf16 before its kernel; rounded to bf16 when read).
+int check_inits_dtype(int dtype, int inits_dtype) {
+  LTV_REQUIRE(inits_dtype == dtype || (inits_dtype == LTV_DTYPE_F32 && dtype == LTV_DTYPE_BF16),
+              LTV_ERR_INVALID_ARG,
+              "inits dtype %d: must be the values' dtype (%d), or fp32 with bf16 values",
+              inits_dtype, dtype);
+  return LTV_OK;
+}
+
 int scan_forward_impl(int dtype, const HostView4& u, const HostView4& lg, const HostView4& init,
-                      const float* bias, void* const outp[3], const int64_t* const outs[3], int B,
-                      int T, int NH, int NKVH, int Da, int r, int P, int Q, int K,
-                      int use_sigmoid, void* chain_ws, size_t chain_ws_bytes, hipStream_t st) {
+                      int inits_dtype, const float* bias, void* const outp[3],
+                      const int64_t* const outs[3], int B, int T, int NH, int NKVH, int Da, int r,
+                      int P, int Q, int K, int use_sigmoid, void* chain_ws,
+                      size_t chain_ws_bytes, hipStream_t st) {
   int rc = check_shape(dtype, B, T, NH, NKVH, Da, r);
   if (rc) return rc;
   rc = check_pqk(P, Q, K);
   if (rc) return rc;
+  rc = check_inits_dtype(dtype, inits_dtype);
+  if (rc) return rc;
+  const bool init_f32 = inits_dtype != dtype;
   const int H = NH + 2 * NKVH;
   const int D = Da * r;
   if (B == 0 || T == 0 || H == 0) return LTV_OK;
@@ -462,6 +492,7 @@ int scan_forward_impl(int dtype, const HostView4& u, const HostView4& lg, const 
   a.u = to_dev(u);
   a.lg = to_dev(lg);
   a.init = to_dev(init);
+  a.init_f32 = init_f32 ? 1 : 0;
   a.bias = bias;
   a.P = P;
   a.Q = Q;
@@ -469,9 +500,11 @@ int scan_forward_impl(int dtype, const HostView4& u, const HostView4& lg, const 
   a.nwin = look_back_nwin(T, P, Q);
   a.wst = nullptr;
   a.kw = 0;
+  LTV_REQUIRE(!init_f32 || a.nwin == 1, LTV_ERR_UNSUPPORTED,
+              "fp32 inits with bf16 values need the full recurrence (P >= T)");
   const int E = dtype == LTV_DTYPE_BF16 ? 2 : 4;
   if ((rc = check_tile_offsets("values", u.s, D, E)) || (rc = check_tile_offsets("logits", lg.s, D, E)) ||
-      (rc = check_tile_offsets("inits", init.s, D, E)))
+      (rc = check_tile_offsets("inits", init.s, D, init_f32 ? 4 : E)))
     return rc;
   bool vec = (D % V == 0) && vec_ok(u.p, u.s, 3, V) && vec_ok(init.p, init.s, 3, V);
   for (int i = 0; i < 3; ++i) {
@@ -595,6 +628,7 @@ BwdChainPlan bwd_chain_plan(int dtype, int B, int T, int H, int Da, int r) {
 struct BwdWorkspace {
   // byte offsets
   size_t partial = 0, agg = 0, carry = 0, dalpha = 0;
+  size_t dinit = 0;  // per-(b, h) inits gradients for their batch sum
   size_t wst = 0, wdu = 0, wdl = 0, wdi = 0;  // look-back windows
   size_t total = 0;
 };
@@ -645,6 +679,8 @@ BwdWorkspace bwd_workspace_plan(int dtype, int B, int T, int NH, int NKVH, int D
     w.carry = off;
     off += al((size_t)B * H * NC * D * sizeof(float));
   }
+  w.dinit = off;
+  off += al((size_t)B * H * D * sizeof(float));
   if (bwd_gate_mode(r, Da, V) < 0) {
     w.dalpha = off;
     off += (size_t)B * H * T * D * sizeof(float);
@@ -659,16 +695,23 @@ size_t bwd_workspace_bytes(int dtype, int B, int T, int NH, int NKVH, int Da, in
 }
 
 int scan_backward_impl(int dtype, const HostView4& u, const HostView4& lg, const HostView4& init,
-                       const float* bias, const void* const hp[3], const int64_t* const hs[3],
-                       const void* const gp[3], const int64_t* const gs[3], const HostView4& du,
-                       const HostView4& dlg, const HostView4& dinit, float* dbias, void* ws,
-                       size_t ws_bytes, void* chain_ws, size_t chain_ws_bytes, int B, int T,
-                       int NH, int NKVH, int Da, int r, int P, int Q, int K, int use_sigmoid,
-                       hipStream_t st) {
+                       int inits_dtype, const float* bias, const void* const hp[3],
+                       const int64_t* const hs[3], const void* const gp[3],
+                       const int64_t* const gs[3], const HostView4& du, const HostView4& dlg,
+                       const HostView4& dinit, float* dbias, void* ws, size_t ws_bytes,
+                       void* chain_ws, size_t chain_ws_bytes, int B, int T, int NH, int NKVH,
+                       int Da, int r, int P, int Q, int K, int use_sigmoid, hipStream_t st) {
   int rc = check_shape(dtype, B, T, NH, NKVH, Da, r);
   if (rc) return rc;
   rc = check_pqk(P, Q, K);
   if (rc) return rc;
+  rc = check_inits_dtype(dtype, inits_dtype);
+  if (rc) return rc;
+  const bool init_f32 = inits_dtype != dtype;
+  const int EI = inits_dtype == LTV_DTYPE_BF16 ? 2 : 4;  // bytes per inits element
+  // grad_inits with batch stride 0: the sum over the batch (what the
+  // broadcast of one set of inits to every sequence gives back)
+  const bool dinit_sum = B > 1 && dinit.s[0] == 0;
   const int H = NH + 2 * NKVH;
   const int D = Da * r;
   if (H == 0) return LTV_OK;
@@ -681,7 +724,7 @@ int scan_backward_impl(int dtype, const HostView4& u, const HostView4& lg, const
     LTV_REQUIRE(blocks < (1ll << 31), LTV_ERR_UNSUPPORTED, "grad_inits too large");
     hipLaunchKernelGGL(zero_bhd_kernel, dim3((int)blocks), dim3(256), 0, st,
                        reinterpret_cast<char*>(const_cast<void*>(dinit.p)), to_dev(dinit), B, H, D,
-                       dtype == LTV_DTYPE_BF16 ? 2 : 4, dbias, H * Da);
+                       EI, dbias, H * Da);
     LTV_LAUNCH_CHECK();
     return LTV_OK;
   }
@@ -695,12 +738,14 @@ int scan_backward_impl(int dtype, const HostView4& u, const HostView4& lg, const
   a.u = to_dev(u);
   a.lg = to_dev(lg);
   a.init = to_dev(init);
+  a.init_f32 = init_f32 ? 1 : 0;
+  a.dinit_ws = nullptr;
   a.bias = bias;
   const int E = dtype == LTV_DTYPE_BF16 ? 2 : 4;
   if ((rc = check_tile_offsets("values", u.s, D, E)) || (rc = check_tile_offsets("logits", lg.s, D, E)) ||
       (rc = check_tile_offsets("grad values", du.s, D, E)) ||
       (rc = check_tile_offsets("grad logits", dlg.s, D, E)) ||
-      (rc = check_tile_offsets("inits", init.s, D, E)))
+      (rc = check_tile_offsets("inits", init.s, D, EI)))
     return rc;
   bool vec = (D % V == 0) && vec_ok(u.p, u.s, 3, V) && vec_ok(init.p, init.s, 3, V) &&
              vec_ok(du.p, du.s, 3, V) && vec_ok(dinit.p, dinit.s, 3, V);
@@ -745,6 +790,21 @@ int scan_backward_impl(int dtype, const HostView4& u, const HostView4& lg, const
   if (gm == GATE_CHAN && vec && chanvec_ok(r, D, V, lg) && chanvec_ok(r, D, V, dlg))
     gm = GATE_CHANVEC;
   const int nwin = look_back_nwin(T, P, Q);
+  LTV_REQUIRE(!(init_f32 || dinit_sum) || (nwin == 1 && gm >= 0), LTV_ERR_UNSUPPORTED,
+              "fp32 inits with bf16 values, or grad_inits summed over the batch (batch stride "
+              "0), need the full recurrence (P >= T) and gate groups of r channels with r a "
+              "multiple of %d and Da <= %d, or r dividing %d (r=%d Da=%d)",
+              V, kMaxLaneGroups, V, r, Da);
+  DinitSum ds;
+  if (dinit_sum) {
+    a.dinit_ws = reinterpret_cast<float*>(wsb + wp.dinit);
+    ds.ws = a.dinit_ws;
+    ds.out = const_cast<void*>(dinit.p);
+    ds.sh = dinit.s[1];
+    ds.sd = dinit.s[3];
+    ds.D = D;
+    ds.out_bf16 = inits_dtype == LTV_DTYPE_BF16 ? 1 : 0;
+  }
   if (nwin > 1 && (tuning().lb_short && lb_short_ok(V, r, Q, K))) {
     // Short look-back windows: one lane per window gathers its steps' whole
     // gradient (ltv_scan_lb.hip); then the per-window grad_inits shares and
@@ -792,6 +852,7 @@ int scan_backward_impl(int dtype, const HostView4& u, const HostView4& lg, const
       f.u = a.u;
       f.lg = a.lg;
       f.init = a.init;
+      f.init_f32 = 0;
       f.bias = bias;
       for (int i = 0; i < 3; ++i) {
         f.out.p[i] = nullptr;
@@ -842,7 +903,7 @@ int scan_backward_impl(int dtype, const HostView4& u, const HostView4& lg, const
                                                          kChainHeader);
       rc = scan_launch_bwd_chain(dtype == LTV_DTYPE_BF16, a, pl.cfg, (int)grid, gm, st);
       if (rc) return rc;
-      return scan_launch_dbias_reduce(a.dbias_partial, dbias, B, H, a.nchunk, Da, st);
+      return scan_launch_dbias_reduce(a.dbias_partial, dbias, B, H, a.nchunk, Da, st, ds);
     }
   }
   if (gm >= 0) {
@@ -881,7 +942,7 @@ int scan_backward_impl(int dtype, const HostView4& u, const HostView4& lg, const
     rc = scan_launch_bwd_channel(dtype == LTV_DTYPE_BF16, a, dalpha, st);
     if (rc) return rc;
   }
-  return scan_launch_dbias_reduce(a.dbias_partial, dbias, B, H, a.nchunk, Da, st);
+  return scan_launch_dbias_reduce(a.dbias_partial, dbias, B, H, a.nchunk, Da, st, ds);
 }
 
 // (B, T, F) interleaved tensor -> value / logit 4-D views
@@ -942,7 +1003,7 @@ extern "C" int ltv_hm_look_back_scan_forward(
   const int64_t* outs[3] = {out_q_strides, out_k_strides, out_v_strides};
   return scan_forward_impl(dtype, values_view(combined, combined_strides, D, Da),
                            logits_view(combined, combined_strides, D, Da, es),
-                           view3(inits, inits_strides), logit_bias, outp, outs, B, T, NH, NKVH,
+                           view3(inits, inits_strides), dtype, logit_bias, outp, outs, B, T, NH, NKVH,
                            Da, r, P, Q, K, use_sigmoid, nullptr, 0, (hipStream_t)stream);
 }
 
@@ -971,7 +1032,7 @@ extern "C" int ltv_hm_look_back_scan_forward_split(
   void* outp[3] = {out_q, out_k, out_v};
   const int64_t* outs[3] = {out_q_strides, out_k_strides, out_v_strides};
   return scan_forward_impl(dtype, view4(values, values_strides), view4(logits, logits_strides),
-                           view3(inits, inits_strides), logit_bias, outp, outs, B, T, NH, NKVH,
+                           view3(inits, inits_strides), dtype, logit_bias, outp, outs, B, T, NH, NKVH,
                            Da, r, P, Q, K, use_sigmoid, nullptr, 0, (hipStream_t)stream);
 }
 
@@ -1010,7 +1071,7 @@ extern "C" int ltv_hm_scan_forward_ws(int dtype, const void* combined,
   const int64_t* outs[3] = {out_q_strides, out_k_strides, out_v_strides};
   return scan_forward_impl(dtype, values_view(combined, combined_strides, D, Da),
                            logits_view(combined, combined_strides, D, Da, es),
-                           view3(inits, inits_strides), logit_bias, outp, outs, B, T, NH, NKVH,
+                           view3(inits, inits_strides), dtype, logit_bias, outp, outs, B, T, NH, NKVH,
                            Da, r, kUnboundedP, 1, 1, use_sigmoid, chain_workspace,
                            chain_workspace_bytes, (hipStream_t)stream);
 }
@@ -1018,8 +1079,8 @@ extern "C" int ltv_hm_scan_forward_ws(int dtype, const void* combined,
 extern "C" int ltv_hm_look_back_scan_forward_split_ws(
     int dtype, const void* values, const int64_t values_strides[4], const void* logits,
     const int64_t logits_strides[4], const void* inits, const int64_t inits_strides[3],
-    const float* logit_bias, void* out_q, const int64_t out_q_strides[4], void* out_k,
-    const int64_t out_k_strides[4], void* out_v, const int64_t out_v_strides[4],
+    int inits_dtype, const float* logit_bias, void* out_q, const int64_t out_q_strides[4],
+    void* out_k, const int64_t out_k_strides[4], void* out_v, const int64_t out_v_strides[4],
     void* chain_workspace, size_t chain_workspace_bytes, int B, int T, int NH, int NKVH, int Da,
     int r, int P, int Q, int K, int use_sigmoid, void* stream) {
   LTV_REQUIRE(values_strides && logits_strides && inits_strides && out_q_strides &&
@@ -1028,9 +1089,9 @@ extern "C" int ltv_hm_look_back_scan_forward_split_ws(
   void* outp[3] = {out_q, out_k, out_v};
   const int64_t* outs[3] = {out_q_strides, out_k_strides, out_v_strides};
   return scan_forward_impl(dtype, view4(values, values_strides), view4(logits, logits_strides),
-                           view3(inits, inits_strides), logit_bias, outp, outs, B, T, NH, NKVH,
-                           Da, r, P, Q, K, use_sigmoid, chain_workspace, chain_workspace_bytes,
-                           (hipStream_t)stream);
+                           view3(inits, inits_strides), inits_dtype, logit_bias, outp, outs, B, T,
+                           NH, NKVH, Da, r, P, Q, K, use_sigmoid, chain_workspace,
+                           chain_workspace_bytes, (hipStream_t)stream);
 }
 
 extern "C" size_t ltv_hm_look_back_scan_backward_workspace_size(int dtype, int B, int T, int NH,
@@ -1068,7 +1129,7 @@ int scan_backward_combined(
   const int64_t* gs[3] = {grad_hq_strides, grad_hk_strides, grad_hv_strides};
   return scan_backward_impl(
       dtype, values_view(combined, combined_strides, D, Da),
-      logits_view(combined, combined_strides, D, Da, es), view3(inits, inits_strides),
+      logits_view(combined, combined_strides, D, Da, es), view3(inits, inits_strides), dtype,
       logit_bias, hp, hs, gp, gs, values_view(grad_combined, grad_combined_strides, D, Da),
       logits_view(grad_combined, grad_combined_strides, D, Da, es),
       view3(grad_inits, grad_inits_strides), grad_logit_bias, workspace, workspace_bytes,
@@ -1139,8 +1200,8 @@ extern "C" int ltv_hm_scan_backward(
 extern "C" int ltv_hm_look_back_scan_backward_split_ws(
     int dtype, const void* values, const int64_t values_strides[4], const void* logits,
     const int64_t logits_strides[4], const void* inits, const int64_t inits_strides[3],
-    const float* logit_bias, const void* hq, const int64_t hq_strides[4], const void* hk,
-    const int64_t hk_strides[4], const void* hv, const int64_t hv_strides[4],
+    int inits_dtype, const float* logit_bias, const void* hq, const int64_t hq_strides[4],
+    const void* hk, const int64_t hk_strides[4], const void* hv, const int64_t hv_strides[4],
     const void* grad_hq, const int64_t grad_hq_strides[4], const void* grad_hk,
     const int64_t grad_hk_strides[4], const void* grad_hv, const int64_t grad_hv_strides[4],
     void* grad_values, const int64_t grad_values_strides[4], void* grad_logits,
@@ -1157,7 +1218,7 @@ extern "C" int ltv_hm_look_back_scan_backward_split_ws(
   const void* gp[3] = {grad_hq, grad_hk, grad_hv};
   const int64_t* gs[3] = {grad_hq_strides, grad_hk_strides, grad_hv_strides};
   return scan_backward_impl(dtype, view4(values, values_strides), view4(logits, logits_strides),
-                            view3(inits, inits_strides), logit_bias, hp, hs, gp, gs,
+                            view3(inits, inits_strides), inits_dtype, logit_bias, hp, hs, gp, gs,
                             view4(grad_values, grad_values_strides),
                             view4(grad_logits, grad_logits_strides),
                             view3(grad_inits, grad_inits_strides), grad_logit_bias, workspace,
@@ -1177,7 +1238,8 @@ extern "C" int ltv_hm_look_back_scan_backward_split(
     float* grad_logit_bias, void* workspace, size_t workspace_bytes, int B, int T, int NH,
     int NKVH, int Da, int r, int P, int Q, int K, int use_sigmoid, void* stream) {
   return ltv_hm_look_back_scan_backward_split_ws(
-      dtype, values, values_strides, logits, logits_strides, inits, inits_strides, logit_bias,
+      dtype, values, values_strides, logits, logits_strides, inits, inits_strides, dtype,
+      logit_bias,
       hq, hq_strides, hk, hk_strides, hv, hv_strides, grad_hq, grad_hq_strides, grad_hk,
       grad_hk_strides, grad_hv, grad_hv_strides, grad_values, grad_values_strides, grad_logits,
       grad_logits_strides, grad_inits, grad_inits_strides, grad_logit_bias, workspace,

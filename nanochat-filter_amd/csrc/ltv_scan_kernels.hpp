@@ -112,6 +112,8 @@ struct FwdArgs {
   View4 u;     // values   (B, H, T, D)
   View4 lg;    // logits   (B, H, T, Da)
   View4 init;  // inits    (B, H, D) -- s[2] unused
+  // 1: the inits are fp32 in memory (with bf16 I/O), rounded to bf16 when read
+  int init_f32;
   const float* bias;  // (H, Da) contiguous fp32
   OutHeads out;
   int P, Q, K, nwin;  // chunk windows; one workgroup per (b, h, window, slab)
@@ -133,6 +135,13 @@ struct BwdArgs {
   View4 du;       // gradient of the value slots (B, H, T, D)
   View4 dlg;      // gradient of the logit slots (B, H, T, Da)
   View4 dinit;    // (B, H, D)
+  // 1: inits and dinit are fp32 in memory (with bf16 I/O); the inits are
+  // rounded to bf16 when read, the dinit values to bf16 before they are
+  // widened and stored (the gradient of a bf16 tensor cast from fp32)
+  int init_f32;
+  // non-null: dinit goes here instead, (B H, D) fp32 contiguous, rounded to
+  // the I/O dtype, for the reduction that sums it over the batch
+  float* dinit_ws;
   float* dbias_partial;  // (B, H, nchunk, Da) fp32 workspace
   // Time chunks: the tile kernel runs one workgroup per (b, h, chunk) of
   // chunk_steps steps (a multiple of its tile), entering each chunk with the
@@ -387,6 +396,69 @@ __device__ __forceinline__ void bst_vec(Rsrc r, uint32_t off, uint32_t scb, int 
   }
 }
 
+// x rounded to the I/O dtype (the value a store and a reload would give).
+template <typename TIO>
+__device__ __forceinline__ float round_io(float x) {
+  if constexpr (sizeof(TIO) == 2)
+    return __uint_as_float(cvt_pk_bf16(x, 0.0f) << 16);
+  else
+    return x;
+}
+
+// The inits of V channels as a packed I/O vector.  With f32 (bf16 I/O only)
+// they are fp32 in memory -- the parameter before the cast that feeds the
+// reference's bf16 kernel -- and are rounded to bf16 here as that cast
+// rounds them.  Pointer form (channel stride sc elements) and buffer form
+// (byte offset off, channel stride scb bytes; lanes with ok == false read 0).
+template <typename TIO, bool VEC>
+__device__ __forceinline__ uint4 ld_init(const void* base, int64_t sc, int nvalid, bool f32) {
+  if constexpr (sizeof(TIO) == 2 && VEC) {
+    // no branch on the dtype (its join would wait for every load in flight):
+    // the second 16 bytes are read from the fp32 row's second half, or again
+    // from the first (never past the inits), and the result is selected
+    const uint4* p4 = reinterpret_cast<const uint4*>(base);
+    const uint4 a = p4[0];
+    const uint4 b = *(f32 ? p4 + 1 : p4);
+    const float x[8] = {__uint_as_float(a.x), __uint_as_float(a.y), __uint_as_float(a.z),
+                        __uint_as_float(a.w), __uint_as_float(b.x), __uint_as_float(b.y),
+                        __uint_as_float(b.z), __uint_as_float(b.w)};
+    const uint4 cv = Pack<bf16_t>::pack(x);
+    return make_uint4(f32 ? cv.x : a.x, f32 ? cv.y : a.y, f32 ? cv.z : a.z, f32 ? cv.w : a.w);
+  } else if constexpr (sizeof(TIO) == 2) {
+    if (f32) {
+      const float* fp = reinterpret_cast<const float*>(base);
+      float x[8];
+#pragma unroll
+      for (int v = 0; v < 8; ++v) x[v] = v < nvalid ? fp[v * sc] : 0.0f;
+      return Pack<bf16_t>::pack(x);
+    }
+  }
+  return ld_vec<TIO, VEC>(reinterpret_cast<const TIO*>(base), sc, nvalid);
+}
+template <typename TIO, bool VEC>
+__device__ __forceinline__ uint4 bld_init(Rsrc r, uint32_t off, uint32_t scb, int nvalid, bool ok,
+                                          bool f32) {
+  if constexpr (sizeof(TIO) == 2) {
+    if (f32) {
+      float x[8];
+      if (VEC) {
+        const uint4 lo = bld128(r, ok ? off : kOob), hi = bld128(r, ok ? off + 16u : kOob);
+        x[0] = __uint_as_float(lo.x); x[1] = __uint_as_float(lo.y);
+        x[2] = __uint_as_float(lo.z); x[3] = __uint_as_float(lo.w);
+        x[4] = __uint_as_float(hi.x); x[5] = __uint_as_float(hi.y);
+        x[6] = __uint_as_float(hi.z); x[7] = __uint_as_float(hi.w);
+      } else {
+        off = opaque(off);
+#pragma unroll
+        for (int v = 0; v < 8; ++v)
+          x[v] = __uint_as_float(bld1<float>(r, ok && v < nvalid ? off + v * scb : kOob));
+      }
+      return Pack<bf16_t>::pack(x);
+    }
+  }
+  return bld_vec<TIO, VEC>(r, off, scb, nvalid, ok);
+}
+
 // V fp32 values at off, off + 4, ... (16-byte stores when VEC: off is then
 // 16-byte aligned and all V values are valid).
 template <bool VEC, int V>
@@ -621,10 +693,12 @@ scan_fwd_kernel(const FwdArgs args) {
 
   float carry[V];
   {
-    const TIO* ip = reinterpret_cast<const TIO*>(args.init.p) + (int64_t)b * args.init.s[0] +
-                    (int64_t)h * args.init.s[1] + (int64_t)c0 * args.init.s[3];
+    const int64_t ie = (int64_t)b * args.init.s[0] + (int64_t)h * args.init.s[1] +
+                       (int64_t)c0 * args.init.s[3];
+    const void* ip = reinterpret_cast<const char*>(args.init.p) +
+                     ie * (args.init_f32 ? (int64_t)sizeof(float) : (int64_t)sizeof(TIO));
     uint4 q = make_uint4(0u, 0u, 0u, 0u);
-    if (active) q = ld_vec<TIO, VEC>(ip, args.init.s[3], nvalid);
+    if (active) q = ld_init<TIO, VEC>(ip, args.init.s[3], nvalid, args.init_f32 != 0);
 #pragma unroll
     for (int v = 0; v < V; ++v) carry[v] = Pack<TIO>::get(q, v);
   }
@@ -895,10 +969,12 @@ scan_fwd_chain_kernel(const FwdArgs args, const ChainArgs ch) {
   // chunk 0 enters from the inits (lanes of wavefront 0's first time group
   // hand them to the chain step through lds_c)
   if (chunk == 0 && w == 0 && tg == 0) {
-    const TIO* ip = reinterpret_cast<const TIO*>(args.init.p) + (int64_t)b * args.init.s[0] +
-                    (int64_t)h * args.init.s[1] + (int64_t)c0 * args.init.s[3];
+    const int64_t ie = (int64_t)b * args.init.s[0] + (int64_t)h * args.init.s[1] +
+                       (int64_t)c0 * args.init.s[3];
+    const void* ip = reinterpret_cast<const char*>(args.init.p) +
+                     ie * (args.init_f32 ? (int64_t)sizeof(float) : (int64_t)sizeof(TIO));
     uint4 q = make_uint4(0u, 0u, 0u, 0u);
-    if (active) q = ld_vec<TIO, VEC>(ip, args.init.s[3], nvalid);
+    if (active) q = ld_init<TIO, VEC>(ip, args.init.s[3], nvalid, args.init_f32 != 0);
 #pragma unroll
     for (int v = 0; v < V; ++v) lds_c[cl * V + v] = Pack<TIO>::get(q, v);
   }
@@ -1112,8 +1188,10 @@ scan_bwd_kernel(const BwdArgs args) {
                      ((int64_t)b * args.du.s[0] + (int64_t)h * args.du.s[1]) * E;
   const char* dlbh = reinterpret_cast<const char*>(args.dlg.p) +
                      ((int64_t)b * args.dlg.s[0] + (int64_t)h * args.dlg.s[1]) * E;
+  const bool init_f32 = args.init_f32 != 0;
+  const int64_t EI = init_f32 ? (int64_t)sizeof(float) : (int64_t)E;  // bytes per init element
   const Rsrc irs = make_rsrc(reinterpret_cast<const char*>(args.init.p) +
-                             ((int64_t)b * args.init.s[0] + (int64_t)h * args.init.s[1]) * E);
+                             ((int64_t)b * args.init.s[0] + (int64_t)h * args.init.s[1]) * EI);
 
   GateIdx<GM, V> gi;
   gi.init(args.bias + h * S.Da, c0, nvalid, S.D, S.r, args.lg.s[3]);
@@ -1177,7 +1255,7 @@ scan_bwd_kernel(const BwdArgs args) {
   const uint32_t lstb = (uint32_t)(args.lg.s[2] * E);
   const uint32_t dustb = (uint32_t)(args.du.s[2] * E), duscb = (uint32_t)(args.du.s[3] * E);
   const uint32_t dlstb = (uint32_t)(args.dlg.s[2] * E), dlscb = (uint32_t)(args.dlg.s[3] * E);
-  const uint32_t iscb = (uint32_t)(args.init.s[3] * E);
+  const uint32_t iscb = (uint32_t)(args.init.s[3] * EI);
   const uint32_t wstb = (uint32_t)(S.D * E), wdustb = (uint32_t)(S.D * 4), wdlstb = (uint32_t)(S.Da * 4);
   const uint32_t uoff = (uint32_t)tl0 * ustb + (uint32_t)c0 * uscb;
   const uint32_t goff = (uint32_t)tl0 * gstb + (uint32_t)c0 * gscb;
@@ -1208,7 +1286,34 @@ scan_bwd_kernel(const BwdArgs args) {
   // the state entering the lane comes from one of three masked loads, kept
   // apart until the tile uses it (merging them at once would wait for the
   // loads just issued)
-  uint4 nu[NB][L], ng[NB][L], nh0[NB], ni0[NB], nw0[LB ? NB : 1];
+  uint4 nu[NB][L], ng[NB][L], nh0[NB], nw0[LB ? NB : 1];
+  // The inits of this lane's channels are read once, here, raw (16-byte
+  // vectors; fp32 inits with bf16 I/O are two), and converted by selects in
+  // the tile whose lane starts at t_base: a branch on the dtype inside the
+  // tile loop would make the compiler wait for the prefetched loads at its
+  // join.  Only that lane (tl0 == 0 of tile 0) needs them.
+  uint4 init_a = make_uint4(0u, 0u, 0u, 0u), init_b = make_uint4(0u, 0u, 0u, 0u);
+  {
+    const bool need = active && tl0 == 0 && it_lo == 0;
+    if constexpr (VEC) {
+      init_a = bld128(irs, need ? ioff : kOob);
+      if constexpr (sizeof(TIO) == 2) init_b = bld128(irs, need && init_f32 ? ioff + 16u : kOob);
+    } else {
+      init_a = bld_init<TIO, false>(irs, ioff, iscb, nvalid, need, init_f32);
+    }
+  }
+  auto init_vec = [&]() -> uint4 {
+    if constexpr (VEC && sizeof(TIO) == 2) {
+      const float x[8] = {__uint_as_float(init_a.x), __uint_as_float(init_a.y),
+                          __uint_as_float(init_a.z), __uint_as_float(init_a.w),
+                          __uint_as_float(init_b.x), __uint_as_float(init_b.y),
+                          __uint_as_float(init_b.z), __uint_as_float(init_b.w)};
+      const uint4 cv = Pack<bf16_t>::pack(x);
+      return make_uint4(init_f32 ? cv.x : init_a.x, init_f32 ? cv.y : init_a.y,
+                        init_f32 ? cv.z : init_a.z, init_f32 ? cv.w : init_a.w);
+    }
+    return init_a;
+  };
   LogitRaw<TIO, GM, L + 1> nl[NB];
   auto load_tile = [&](int it, auto bufc) {
     constexpr int buf = decltype(bufc)::value;
@@ -1232,7 +1337,6 @@ scan_bwd_kernel(const BwdArgs args) {
     const bool from_h = ok0 && !from_init && !from_wst;
     nh0[buf] = bld_vec<TIO, VEC, kLdStream>(make_rsrc(hbh + (int64_t)(Tt - 1) * hs[2] * E), hoff,
                                             hscb, nvalid, from_h);
-    ni0[buf] = bld_vec<TIO, VEC>(irs, ioff, iscb, nvalid, from_init);
     if constexpr (LB)
       nw0[buf] = bld_vec<TIO, VEC>(make_rsrc(wsbh + (int64_t)(Tt - 1 - t_base) * S.D * E), woff,
                                    E, nvalid, from_wst);
@@ -1262,7 +1366,11 @@ scan_bwd_kernel(const BwdArgs args) {
     }
     {
       uint4 q = nh0[buf];
-      const uint4 qi = ni0[buf];
+      // the lane that starts at t_base enters from the inits (its h load was
+      // masked); every other lane ORs zeros
+      const bool at_init = active && t0 == t_base && t0 < t_hi;
+      const uint4 iv = init_vec();
+      const uint4 qi = at_init ? iv : make_uint4(0u, 0u, 0u, 0u);
       q = make_uint4(q.x | qi.x, q.y | qi.y, q.z | qi.z, q.w | qi.w);
       if constexpr (LB) {
         const uint4 qw = nw0[buf];
@@ -1526,13 +1634,30 @@ scan_bwd_kernel(const BwdArgs args) {
 
   // ---- dinit: the state gradient at t_base, from lane tl0 == 0 of tile it_lo
   if (active && it_hi >= it_lo && it_lo == 0 && tl0 == 0) {
-    if (LB)
+    if (LB) {
       st_f32<VEC, V>(args.wdi + ((int64_t)bh * args.nchunk + chunk) * S.D + c0, nvalid, dinit_v);
-    else
+    } else if (args.dinit_ws != nullptr || init_f32) {
+      // the gradient of the I/O-dtype inits, widened to fp32: into the batch
+      // sum's workspace, or straight to fp32 grad_inits
+      float rv[V];
+#pragma unroll
+      for (int v = 0; v < V; ++v) rv[v] = round_io<TIO>(dinit_v[v]);
+      if (args.dinit_ws != nullptr) {
+        st_f32<VEC, V>(args.dinit_ws + (int64_t)bh * S.D + c0, nvalid, rv);
+      } else {
+        float* p = reinterpret_cast<float*>(const_cast<void*>(args.dinit.p)) +
+                   (int64_t)b * args.dinit.s[0] + (int64_t)h * args.dinit.s[1] +
+                   (int64_t)c0 * args.dinit.s[3];
+#pragma unroll
+        for (int v = 0; v < V; ++v)
+          if (v < nvalid) p[v * args.dinit.s[3]] = rv[v];
+      }
+    } else {
       st_vec<TIO, VEC>(reinterpret_cast<TIO*>(const_cast<void*>(args.dinit.p)) +
                            (int64_t)b * args.dinit.s[0] + (int64_t)h * args.dinit.s[1] +
                            (int64_t)c0 * args.dinit.s[3],
                        args.dinit.s[3], nvalid, dinit_v);
+    }
   }
 
   // ---- dbias partial for (b, h): fixed-order sum of the accumulators
@@ -1871,8 +1996,17 @@ int scan_launch_lb_short_bwd(bool bf16, const BwdArgs& a, bool vec, int gm, int 
                              hipStream_t st);
 // Backward for gate groups outside the main kernel's reduction patterns.
 int scan_launch_bwd_channel(bool bf16, const BwdArgs& a, float* dalpha_ws, hipStream_t st);
-// dbias[h, j] = sum_b partial[b, h, j]
+// The batch sum of the inits gradient, done by the dbias reduction's launch:
+// out[h, d] (strides sh, sd elements; fp32, or bf16 with out_bf16) = the sum
+// over b, in batch order, of ws[(b H + h) D + d].
+struct DinitSum {
+  const float* ws = nullptr;  // null: no sum
+  void* out = nullptr;
+  int64_t sh = 0, sd = 0;
+  int D = 0, out_bf16 = 0;
+};
+// dbias[h, j] = sum_b partial[b, h, j] (and the inits gradient's batch sum)
 int scan_launch_dbias_reduce(const float* partial, float* dbias, int B, int H, int NC, int Da,
-                             hipStream_t st);
+                             hipStream_t st, const DinitSum& ds = DinitSum());
 
 }  // namespace ltv

@@ -93,7 +93,8 @@ SIGNATURES = {
     ),
     "ltv_hm_look_back_scan_forward_split_ws": (
         _c_int,
-        [_c_int, _c_vp, _c_i64p, _c_vp, _c_i64p, _c_vp, _c_i64p, _c_vp, _c_vp, _c_i64p, _c_vp,
+        [_c_int, _c_vp, _c_i64p, _c_vp, _c_i64p, _c_vp, _c_i64p, _c_int, _c_vp, _c_vp, _c_i64p,
+         _c_vp,
          _c_i64p, _c_vp, _c_i64p, _c_vp, _c_sz, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
          _c_int, _c_int, _c_int, _c_int, _c_vp],
     ),
@@ -120,7 +121,7 @@ SIGNATURES = {
     ),
     "ltv_hm_look_back_scan_backward_split_ws": (
         _c_int,
-        [_c_int, _c_vp, _c_i64p, _c_vp, _c_i64p, _c_vp, _c_i64p, _c_vp,
+        [_c_int, _c_vp, _c_i64p, _c_vp, _c_i64p, _c_vp, _c_i64p, _c_int, _c_vp,
          _c_vp, _c_i64p, _c_vp, _c_i64p, _c_vp, _c_i64p,
          _c_vp, _c_i64p, _c_vp, _c_i64p, _c_vp, _c_i64p,
          _c_vp, _c_i64p, _c_vp, _c_i64p, _c_vp, _c_i64p, _c_vp,

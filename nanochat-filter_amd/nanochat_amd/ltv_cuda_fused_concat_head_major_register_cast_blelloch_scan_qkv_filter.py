@@ -48,7 +48,10 @@ class _BatchSharedInits(torch.autograd.Function):
     scan kernels read in place.  The gradient is the batch sum of the (B, H, D)
     bf16 inits gradient, accumulated in float32: what the cast's and the
     broadcast's backward compute (``init_param.expand(B, H, D).to(bfloat16)``),
-    in one reduction instead of a cast, a (B, H, D) copy and a reduction."""
+    in one reduction instead of a cast, a (B, H, D) copy and a reduction.
+    Used for gate shapes whose scan takes no (H, D) inits; for the others the
+    parameter goes to the scan as it is (``_shared_inits_in_kernel``), which
+    does the rounding and the batch sum itself."""
 
     @staticmethod
     def forward(ctx, init_param, B):
@@ -87,7 +90,12 @@ class LtvCudaFusedConcatHeadMajorRegisterCastBlellochScanQkvFilter(
         if compute_dtype == torch.bfloat16 and x.size(1) == 1 and not torch.is_grad_enabled():
             return self._decode_bf16(x, previous_values)
         if compute_dtype == torch.bfloat16:
-            if previous_values.q is None:
+            if previous_values.q is None and self._shared_inits_in_kernel():
+                # the (H, D) parameter itself: the scan reads it for every
+                # sequence, rounding fp32 to bf16, and returns its gradient
+                # summed over the batch
+                inits = self.init_param
+            elif previous_values.q is None:
                 inits = _BatchSharedInits.apply(self.init_param, B)
             else:
                 inits = resolve_inits_original_dtype(B, self.init_param, previous_values).to(
@@ -98,8 +106,13 @@ class LtvCudaFusedConcatHeadMajorRegisterCastBlellochScanQkvFilter(
             raise TypeError(f"LTV filter computes in bfloat16 or float32, not {compute_dtype}")
         return self._forward_fp32(x, inits)
 
+    def _shared_inits_in_kernel(self):
+        return (self.init_param.dtype in (torch.float32, torch.bfloat16)
+                and hm_fast.shared_inits_ok(self.head_dim, self.num_alpha_groups, self.r))
+
     def _forward_bf16(self, x, inits):
-        """inits: (B, H, D) bf16, contiguous or the batch-shared view."""
+        """inits: (B, H, D) bf16, contiguous or the batch-shared view, or the
+        (H, D) parameter (fp32 or bf16) shared by every sequence."""
         hq, hk, hv, _, _, _ = torch.ops.nanochat_amd.qkv_filter(
             x.to(torch.bfloat16).contiguous(),
             self.c.weight,

@@ -14,7 +14,9 @@ Ops in the ``nanochat_amd`` namespace, each with a fake implementation:
 
 ``qkv_filter(x, weight, inits, logit_bias, NH, NKVH, Da, r, P, Q, K)``
     -> (q, k, v, values, logits, wpack).  q (B, NH, T, D), k and v
-    (B, NKVH, T, D), contiguous.  The last three outputs are the intermediates
+    (B, NKVH, T, D), contiguous.  inits (B, H, D) bf16, or the (H, D)
+    parameter shared by every sequence (fp32 or bf16; ``shared_inits_ok``),
+    whose gradient comes back summed over the batch.  The last three outputs are the intermediates
     the backward reads; callers use only q, k, v.  Same result as the
     reference's ``fused_linear_transpose`` (``cpp_ewma/src/fused_linear_transpose_forward.cu:23-58``)
     followed by its head-major scan
@@ -191,17 +193,46 @@ def project_backward(x: torch.Tensor, wpack: torch.Tensor, grad_combined: torch.
     return grad_x, grad_w
 
 
+def shared_inits_ok(D: int, Da: int, r: int) -> bool:
+    """Whether the bf16 scan takes one (H, D) set of inits for every sequence,
+    fp32 or bf16, with the inits gradient summed over the batch by the
+    library (gate groups the tile kernels reduce: r a multiple of 8 with at
+    most 16 groups per head, or r dividing 8; 16-byte channel vectors)."""
+    return D % 8 == 0 and ((r % 8 == 0 and Da <= 16) or 8 % r == 0)
+
+
+def _inits_view(inits: torch.Tensor, values: torch.Tensor):
+    """(strides (b, h, d), dtype code) of the inits: (B, H, D) per sequence,
+    or (H, D) shared by every sequence (batch stride 0); the values' dtype,
+    or fp32 with bf16 values (rounded to bf16 by the kernels)."""
+    B, H, _, D = values.shape
+    if inits.dim() == 2:
+        if tuple(inits.shape) != (H, D):
+            raise RuntimeError(f"shared inits must be {(H, D)}, got {tuple(inits.shape)}")
+        st = (0, inits.stride(0), inits.stride(1))
+    elif tuple(inits.shape) == (B, H, D):
+        st = tuple(inits.stride())
+    else:
+        raise RuntimeError(f"inits must be {(B, H, D)} or {(H, D)}, got {tuple(inits.shape)}")
+    if inits.dtype != values.dtype and not (inits.dtype == torch.float32
+                                            and values.dtype == torch.bfloat16):
+        raise RuntimeError(f"inits must be in the values' dtype, or float32 with bfloat16 "
+                           f"values; got {inits.dtype} with {values.dtype}")
+    return st, N.dtype_code(inits.dtype)
+
+
 def scan_forward(values: torch.Tensor, logits: torch.Tensor, inits: torch.Tensor,
                  logit_bias: torch.Tensor, NH: int, NKVH: int, Da: int, r: int,
                  use_sigmoid: bool, P: int = UNBOUNDED_P, Q: int = 1, K: int = 1):
     """values (B, H, T, D); logits (B, T, >= H Da) with column h Da + j, or
-    head-major (B, H, T, Da) -> out_q (B, NH, T, D), out_k, out_v (B, NKVH, T, D)."""
+    head-major (B, H, T, Da) -> out_q (B, NH, T, D), out_k, out_v (B, NKVH, T, D).
+    inits: (B, H, D), or (H, D) for every sequence; fp32 inits with bf16 values
+    are rounded to bf16 as they are read (the full recurrence only)."""
     N.require_device(values, logits, inits, logit_bias)
     B, H, T, D = values.shape
     if H != NH + 2 * NKVH or D != Da * r:
         raise RuntimeError("values shape does not match (NH, NKVH, Da, r)")
-    if inits.dtype != values.dtype or tuple(inits.shape) != (B, H, D):
-        raise RuntimeError("inits must be (B, H, D) in the values' dtype")
+    ist, idt = _inits_view(inits, values)
     if logit_bias.dtype != torch.float32 or not logit_bias.is_contiguous():
         raise RuntimeError("logit_bias must be contiguous float32")
     out = [torch.empty((B, nh, T, D), dtype=values.dtype, device=values.device)
@@ -219,7 +250,7 @@ def scan_forward(values: torch.Tensor, logits: torch.Tensor, inits: torch.Tensor
         rc = N.lib().ltv_hm_look_back_scan_forward_split_ws(
             N.dtype_code(values.dtype),
             values.data_ptr(), N.strides(values, 4), logits.data_ptr(), _arr(lgs),
-            inits.data_ptr(), N.strides(inits, 3), logit_bias.data_ptr(),
+            inits.data_ptr(), _arr(ist), idt, logit_bias.data_ptr(),
             out[0].data_ptr(), N.strides(out[0], 4), out[1].data_ptr(), N.strides(out[1], 4),
             out[2].data_ptr(), N.strides(out[2], 4), ws, ws_bytes,
             B, T, NH, NKVH, Da, r, P, Q, K, int(bool(use_sigmoid)), N.stream_of(values))
@@ -230,11 +261,16 @@ def scan_forward(values: torch.Tensor, logits: torch.Tensor, inits: torch.Tensor
 def scan_backward(values, logits, inits, logit_bias, hq, hk, hv, gq, gk, gv, NH: int,
                   NKVH: int, Da: int, r: int, use_sigmoid: bool,
                   grad_combined: torch.Tensor, P: int = UNBOUNDED_P, Q: int = 1, K: int = 1):
-    """Writes grad_combined (B, T, Fp); returns (grad_inits, grad_logit_bias)."""
+    """Writes grad_combined (B, T, Fp); returns (grad_inits, grad_logit_bias).
+    grad_inits is shaped like inits: with (H, D) inits it is the sum over the
+    batch of every sequence's gradient (each rounded to the values' dtype,
+    summed in fp32 in batch order), in the inits' dtype."""
     B, H, T, D = values.shape
     dt = N.dtype_code(values.dtype)
     lib = N.lib()
-    grad_inits = torch.empty((B, H, D), dtype=inits.dtype, device=inits.device)
+    ist, idt = _inits_view(inits, values)
+    grad_inits = torch.empty(inits.shape, dtype=inits.dtype, device=inits.device)
+    gist = ((0,) + tuple(grad_inits.stride())) if inits.dim() == 2 else tuple(grad_inits.stride())
     grad_bias = torch.empty((H, Da), dtype=torch.float32, device=values.device)
     ws_bytes = lib.ltv_hm_look_back_scan_backward_workspace_size(dt, B, T, NH, NKVH, Da, r,
                                                                  P, Q, K)
@@ -252,13 +288,13 @@ def scan_backward(values, logits, inits, logit_bias, hq, hk, hv, gq, gk, gv, NH:
         rc = lib.ltv_hm_look_back_scan_backward_split_ws(
             dt,
             values.data_ptr(), N.strides(values, 4), logits.data_ptr(), _arr(lgs),
-            inits.data_ptr(), N.strides(inits, 3), logit_bias.data_ptr(),
+            inits.data_ptr(), _arr(ist), idt, logit_bias.data_ptr(),
             hq.data_ptr(), N.strides(hq, 4), hk.data_ptr(), N.strides(hk, 4),
             hv.data_ptr(), N.strides(hv, 4),
             gq.data_ptr(), N.strides(gq, 4), gk.data_ptr(), N.strides(gk, 4),
             gv.data_ptr(), N.strides(gv, 4),
             grad_combined.data_ptr(), _arr(gvals), glg_ptr, _arr(glgs),
-            grad_inits.data_ptr(), N.strides(grad_inits, 3), grad_bias.data_ptr(),
+            grad_inits.data_ptr(), _arr(gist), grad_bias.data_ptr(),
             ws.data_ptr(), ws_bytes, cws, cws_bytes, B, T, NH, NKVH, Da, r, P, Q, K,
             int(bool(use_sigmoid)), N.stream_of(values))
     N.check(rc, "ltv_hm_look_back_scan_backward_split_ws")
@@ -321,7 +357,7 @@ def _(x, wpack, values, logits, inits, logit_bias, hq, hk, hv, gq, gk, gv, NH, N
     D = Da * r
     return (x.new_empty((B, T, C), dtype=torch.bfloat16),
             x.new_empty((H * (D + Da), C), dtype=torch.float32),
-            inits.new_empty((B, H, D)), x.new_empty((H, Da), dtype=torch.float32))
+            inits.new_empty(inits.shape), x.new_empty((H, Da), dtype=torch.float32))
 
 
 def _filter_setup(ctx, inputs, output):

@@ -20,6 +20,28 @@ def declared_functions():
     return sorted(set(names))
 
 
+def declared_arg_counts():
+    """{name: number of parameters} of every declaration in the header."""
+    src = open(HEADER).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    out = {}
+    for m in re.finditer(r"^\s*(?:const\s+)?[A-Za-z_][A-Za-z0-9_]*\s*\*?\s*(ltv_[a-z0-9_]+)\s*"
+                         r"\(([^;]*?)\)\s*;", src, flags=re.M | re.S):
+        args = " ".join(m.group(2).split())
+        out[m.group(1)] = 0 if args in ("", "void") else len(re.split(r",(?![^\[]*\])", args))
+    return out
+
+
+def test_ctypes_argument_counts_match_header():
+    """A ctypes prototype with one argument too few or too many shifts every
+    later argument; each binding has exactly the header's parameter count."""
+    from nanochat_amd import _native as N
+    counts = declared_arg_counts()
+    bad = {n: (len(args), counts.get(n)) for n, (_, args) in N.SIGNATURES.items()
+           if len(args) != counts.get(n)}
+    assert not bad, bad
+
+
 def test_header_declares_entry_points():
     names = declared_functions()
     for must in ("ltv_hm_scan_forward", "ltv_hm_scan_backward", "ltv_qkv_project_forward",
@@ -47,7 +69,7 @@ def test_abi_version_and_host_only_queries():
     if not os.path.exists(N.LIB_PATH):
         pytest.skip("library not built")
     lib = N.load()
-    assert lib.ltv_abi_version() == 5
+    assert lib.ltv_abi_version() == 6
     # d12: 18 heads x (128 + 1) = 2322 -> padded to a multiple of 128; 18 logits -> 24
     assert lib.ltv_qkv_packed_width(18, 128, 1) == 2432
     assert lib.ltv_qkv_logit_width(18, 1) == 24

@@ -67,14 +67,16 @@ def _forward(comb, ini, bias, NH, NKVH, Da, r, sig, ws=None):
     D = Da * r
     values, logits = _split(comb, NH, NKVH, Da, r)
     out = _outs(B, T, NH, NKVH, D, comb.dtype)
-    args = [N.dtype_code(comb.dtype), values.data_ptr(), _s(values), logits.data_ptr(),
-            _s(logits), ini.data_ptr(), _s(ini), bias.data_ptr(), out[0].data_ptr(),
-            _s(out[0]), out[1].data_ptr(), _s(out[1]), out[2].data_ptr(), _s(out[2])]
+    head = [N.dtype_code(comb.dtype), values.data_ptr(), _s(values), logits.data_ptr(),
+            _s(logits), ini.data_ptr(), _s(ini)]
+    rest = [bias.data_ptr(), out[0].data_ptr(), _s(out[0]), out[1].data_ptr(), _s(out[1]),
+            out[2].data_ptr(), _s(out[2])]
     tail = [B, T, NH, NKVH, Da, r, UNBOUNDED_P, 1, 1, int(sig), N.stream_of(comb)]
     if ws is None:
-        rc = lib.ltv_hm_look_back_scan_forward_split(*args, *tail)
+        rc = lib.ltv_hm_look_back_scan_forward_split(*head, *rest, *tail)
     else:
-        rc = lib.ltv_hm_look_back_scan_forward_split_ws(*args, ws.data_ptr(), ws.numel(), *tail)
+        rc = lib.ltv_hm_look_back_scan_forward_split_ws(*head, N.dtype_code(ini.dtype), *rest,
+                                                        ws.data_ptr(), ws.numel(), *tail)
     N.check(rc, "scan forward")
     return out
 
@@ -357,17 +359,19 @@ def _backward(comb, ini, bias, outs, grads, NH, NKVH, Da, r, sig, ws=None):
     nbytes = lib.ltv_hm_look_back_scan_backward_workspace_size(dt, B, T, NH, NKVH, Da, r,
                                                                UNBOUNDED_P, 1, 1)
     scratch = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=DEV)
-    args = [dt, values.data_ptr(), _s(values), logits.data_ptr(), _s(logits), ini.data_ptr(),
-            _s(ini), bias.data_ptr()]
+    head = [dt, values.data_ptr(), _s(values), logits.data_ptr(), _s(logits), ini.data_ptr(),
+            _s(ini)]
+    rest = [bias.data_ptr()]
     for t in list(outs) + list(grads):
-        args += [t.data_ptr(), _s(t)]
-    args += [gval.data_ptr(), _s(gval), glog.data_ptr(), _s(glog), gini.data_ptr(), _s(gini),
+        rest += [t.data_ptr(), _s(t)]
+    rest += [gval.data_ptr(), _s(gval), glog.data_ptr(), _s(glog), gini.data_ptr(), _s(gini),
              gbias.data_ptr(), scratch.data_ptr(), nbytes]
     tail = [B, T, NH, NKVH, Da, r, UNBOUNDED_P, 1, 1, int(sig), N.stream_of(comb)]
     if ws is None:
-        rc = lib.ltv_hm_look_back_scan_backward_split(*args, *tail)
+        rc = lib.ltv_hm_look_back_scan_backward_split(*head, *rest, *tail)
     else:
-        rc = lib.ltv_hm_look_back_scan_backward_split_ws(*args, ws.data_ptr(), ws.numel(), *tail)
+        rc = lib.ltv_hm_look_back_scan_backward_split_ws(*head, dt, *rest, ws.data_ptr(),
+                                                         ws.numel(), *tail)
     N.check(rc, "scan backward")
     return gval, glog, gini, gbias
 
