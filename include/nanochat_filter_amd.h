@@ -45,7 +45,7 @@ extern "C" {
 #define LTV_ERR_HIP 3
 #define LTV_ERR_WORKSPACE 4
 
-/* Version of this ABI (bumped on any signature change or addition): 6. */
+/* Version of this ABI (bumped on any signature change or addition): 7. */
 int ltv_abi_version(void);
 
 /* Message of the last failing call on this host thread ("" if none). */
@@ -314,7 +314,12 @@ int ltv_hm_look_back_scan_backward_split(
  *   expanded inits' gradient over B).  Needs the full recurrence and gate
  *   groups the tile kernels take (r a multiple of 8 bf16 / 4 fp32 channels
  *   with Da <= 16, or r dividing it); the sum is formed by the launch that
- *   reduces grad_logit_bias, in `workspace`. */
+ *   reduces grad_logit_bias, in `workspace`.
+ * grad_logits_pad: 0 .. 64 logit slots past the last head's last gate that
+ *   are set to zero in every (b, t) row, slot q = H Da + p at
+ *   b s0 + t s2 + q s3 of the grad_logits view (needs s1 = Da s3): the
+ *   padding columns F .. round_up(F, 8) - 1 of a (B T, Fp) grad_combined,
+ *   which ltv_qkv_project_backward_input_zero_padded then need not zero. */
 int ltv_hm_look_back_scan_backward_split_ws(
     int dtype, const void* values, const int64_t values_strides[4], const void* logits,
     const int64_t logits_strides[4], const void* inits, const int64_t inits_strides[3],
@@ -324,10 +329,10 @@ int ltv_hm_look_back_scan_backward_split_ws(
     const void* grad_hq, const int64_t grad_hq_strides[4], const void* grad_hk,
     const int64_t grad_hk_strides[4], const void* grad_hv, const int64_t grad_hv_strides[4],
     void* grad_values, const int64_t grad_values_strides[4], void* grad_logits,
-    const int64_t grad_logits_strides[4], void* grad_inits, const int64_t grad_inits_strides[3],
-    float* grad_logit_bias, void* workspace, size_t workspace_bytes, void* chain_workspace,
-    size_t chain_workspace_bytes, int B, int T, int NH, int NKVH, int Da, int r, int P, int Q,
-    int K, int use_sigmoid, void* stream);
+    const int64_t grad_logits_strides[4], int grad_logits_pad, void* grad_inits,
+    const int64_t grad_inits_strides[3], float* grad_logit_bias, void* workspace,
+    size_t workspace_bytes, void* chain_workspace, size_t chain_workspace_bytes, int B, int T,
+    int NH, int NKVH, int Da, int r, int P, int Q, int K, int use_sigmoid, void* stream);
 
 /* ------------------------------------------------------------------------
  * Projection, reference layout: out[b] (F x T) = weight (F x K) . x[b]^T
@@ -415,6 +420,14 @@ int ltv_qkv_project_backward(const void* x, const void* wpack, void* grad_combin
 int ltv_qkv_project_backward_input(const void* x, const void* wpack, void* grad_combined,
                                    void* grad_x, int M, int C, int H, int D, int Da,
                                    void* stream);
+/* ltv_qkv_project_backward_input for a grad_combined whose columns
+ * F .. round_up(F, 8) - 1 are zero already (the scan backward writes them
+ * with grad_logits_pad = round_up(F, 8) - F): the same grad_x, without the
+ * launch that zeroes them, and grad_combined is only read.  Counterpart in
+ * the reference: the same grad_x GEMM (fused_linear_transpose_backward.cu:67-95). */
+int ltv_qkv_project_backward_input_zero_padded(const void* x, const void* wpack,
+                                               const void* grad_combined, void* grad_x, int M,
+                                               int C, int H, int D, int Da, void* stream);
 int ltv_qkv_project_backward_weight(const void* x, const void* grad_combined,
                                     float* grad_weight, void* workspace, size_t workspace_bytes,
                                     int M, int C, int H, int D, int Da, void* stream);

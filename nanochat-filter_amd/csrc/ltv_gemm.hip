@@ -699,9 +699,12 @@ int project_backward_check(const void* x, const void* wpack, const void* grad_co
 }
 }  // namespace
 
-extern "C" int ltv_qkv_project_backward_input(const void* x, const void* wpack,
-                                              void* grad_combined, void* grad_x, int M,
-                                              int C, int H, int D, int Da, void* stream) {
+namespace {
+// grad_x; pad_zeroed: the caller guarantees grad_combined's columns F ..
+// round_up(F, 8) - 1 are zero already (no zeroing launch)
+int project_backward_input_impl(const void* x, const void* wpack, void* grad_combined,
+                                void* grad_x, int M, int C, int H, int D, int Da, bool pad_zeroed,
+                                void* stream) {
   int rc = project_backward_check(x, wpack, grad_combined, M, C, H, D, Da);
   if (rc) return rc;
   LTV_REQUIRE(grad_x && aligned16(grad_x), LTV_ERR_INVALID_ARG, "grad_x null or misaligned");
@@ -729,7 +732,7 @@ extern "C" int ltv_qkv_project_backward_input(const void* x, const void* wpack,
     ad.K = Fv8;
     ad.k_split = Fv8;
     if (dma_usable(ad, OP_RC, OP_KC, e, 1)) {
-      if (Fv8 > Fvalid) {
+      if (Fv8 > Fvalid && !pad_zeroed) {
         const int blocks = (M + 255) / 256;
         hipLaunchKernelGGL(zero_cols_kernel, dim3(blocks), dim3(256), 0, st,
                            reinterpret_cast<bf16_t*>(grad_combined), M,
@@ -754,6 +757,23 @@ extern "C" int ltv_qkv_project_backward_input(const void* x, const void* wpack,
   }
   a.tiles_i = (C + 127) / 128;
   return launch_gemm<128, 256, 2, 2, OP_RC, OP_KC>(a, e, 1, st);
+}
+
+}  // namespace
+
+extern "C" int ltv_qkv_project_backward_input(const void* x, const void* wpack,
+                                              void* grad_combined, void* grad_x, int M,
+                                              int C, int H, int D, int Da, void* stream) {
+  return project_backward_input_impl(x, wpack, grad_combined, grad_x, M, C, H, D, Da, false,
+                                     stream);
+}
+
+extern "C" int ltv_qkv_project_backward_input_zero_padded(const void* x, const void* wpack,
+                                                          const void* grad_combined,
+                                                          void* grad_x, int M, int C, int H,
+                                                          int D, int Da, void* stream) {
+  return project_backward_input_impl(x, wpack, const_cast<void*>(grad_combined), grad_x, M, C, H,
+                                     D, Da, true, stream);
 }
 
 extern "C" int ltv_qkv_project_backward_weight(const void* x, const void* grad_combined,

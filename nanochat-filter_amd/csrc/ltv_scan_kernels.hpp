@@ -2005,8 +2005,19 @@ struct DinitSum {
   int64_t sh = 0, sd = 0;
   int D = 0, out_bf16 = 0;
 };
-// dbias[h, j] = sum_b partial[b, h, j] (and the inits gradient's batch sum)
+// Zeroes `pad` slots of the logit-gradient view past the last head's last
+// gate in every (b, t) row: slot q = q0 + p at b sb + t st + q sq elements
+// (esize bytes each), done by the dbias reduction's launch.  For a consumer
+// that reads whole 16-byte chunks past the last logit column.
+struct PadZero {
+  char* base = nullptr;  // null: nothing to zero
+  int64_t sb = 0, st = 0, sq = 0;
+  int B = 0, T = 0, q0 = 0, pad = 0, esize = 2;
+};
+// dbias[h, j] = sum_b partial[b, h, j] (and the inits gradient's batch sum,
+// and the padding slots' zeros)
 int scan_launch_dbias_reduce(const float* partial, float* dbias, int B, int H, int NC, int Da,
-                             hipStream_t st, const DinitSum& ds = DinitSum());
+                             hipStream_t st, const DinitSum& ds = DinitSum(),
+                             const PadZero& pz = PadZero());
 
 }  // namespace ltv

@@ -124,7 +124,7 @@ SIGNATURES = {
         [_c_int, _c_vp, _c_i64p, _c_vp, _c_i64p, _c_vp, _c_i64p, _c_int, _c_vp,
          _c_vp, _c_i64p, _c_vp, _c_i64p, _c_vp, _c_i64p,
          _c_vp, _c_i64p, _c_vp, _c_i64p, _c_vp, _c_i64p,
-         _c_vp, _c_i64p, _c_vp, _c_i64p, _c_vp, _c_i64p, _c_vp,
+         _c_vp, _c_i64p, _c_vp, _c_i64p, _c_int, _c_vp, _c_i64p, _c_vp,
          _c_vp, _c_sz, _c_vp, _c_sz, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
          _c_int, _c_int, _c_int, _c_vp],
     ),
@@ -157,6 +157,8 @@ SIGNATURES = {
          _c_int, _c_vp],
     ),
     "ltv_qkv_project_backward_input": (
+        _c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_int, _c_int, _c_int, _c_int, _c_int, _c_vp]),
+    "ltv_qkv_project_backward_input_zero_padded": (
         _c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_int, _c_int, _c_int, _c_int, _c_int, _c_vp]),
     "ltv_qkv_project_backward_weight": (
         _c_int,

@@ -168,8 +168,10 @@ def decode_step(x: torch.Tensor, wpack: torch.Tensor, prev, logit_bias: torch.Te
 
 
 def project_backward(x: torch.Tensor, wpack: torch.Tensor, grad_combined: torch.Tensor, H: int,
-                     D: int, Da: int):
-    """grad_combined (B, T, Fp) -> (grad_x (B, T, C) bf16, grad_weight (F, C) fp32)."""
+                     D: int, Da: int, pad_zeroed: bool = False):
+    """grad_combined (B, T, Fp) -> (grad_x (B, T, C) bf16, grad_weight (F, C) fp32).
+    pad_zeroed: columns F .. round_up(F, 8) - 1 of grad_combined are zero
+    already (``scan_backward(..., zero_pad=True)``), so grad_x skips zeroing them."""
     B, T, C = x.shape
     M = B * T
     x = x.contiguous()
@@ -180,10 +182,11 @@ def project_backward(x: torch.Tensor, wpack: torch.Tensor, grad_combined: torch.
     grad_w = torch.empty((H * (D + Da), C), dtype=torch.float32, device=x.device)
     ws_bytes = lib.ltv_qkv_project_backward_workspace_size(M, C, H, D, Da)
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=x.device)
+    fn = (lib.ltv_qkv_project_backward_input_zero_padded if pad_zeroed
+          else lib.ltv_qkv_project_backward_input)
     with N.span("qkv_project_bwd_input"):
-        rc = lib.ltv_qkv_project_backward_input(x.data_ptr(), wpack.data_ptr(),
-                                                grad_combined.data_ptr(), grad_x.data_ptr(),
-                                                M, C, H, D, Da, st)
+        rc = fn(x.data_ptr(), wpack.data_ptr(), grad_combined.data_ptr(), grad_x.data_ptr(),
+                M, C, H, D, Da, st)
     N.check(rc, "ltv_qkv_project_backward_input")
     with N.span("qkv_project_bwd_weight"):
         rc = lib.ltv_qkv_project_backward_weight(x.data_ptr(), grad_combined.data_ptr(),
@@ -260,11 +263,14 @@ def scan_forward(values: torch.Tensor, logits: torch.Tensor, inits: torch.Tensor
 
 def scan_backward(values, logits, inits, logit_bias, hq, hk, hv, gq, gk, gv, NH: int,
                   NKVH: int, Da: int, r: int, use_sigmoid: bool,
-                  grad_combined: torch.Tensor, P: int = UNBOUNDED_P, Q: int = 1, K: int = 1):
+                  grad_combined: torch.Tensor, P: int = UNBOUNDED_P, Q: int = 1, K: int = 1,
+                  zero_pad: bool = False):
     """Writes grad_combined (B, T, Fp); returns (grad_inits, grad_logit_bias).
     grad_inits is shaped like inits: with (H, D) inits it is the sum over the
     batch of every sequence's gradient (each rounded to the values' dtype,
-    summed in fp32 in batch order), in the inits' dtype."""
+    summed in fp32 in batch order), in the inits' dtype.  zero_pad: also set
+    grad_combined's columns F .. round_up(F, 8) - 1 to zero (what
+    ``project_backward(..., pad_zeroed=True)`` relies on)."""
     B, H, T, D = values.shape
     dt = N.dtype_code(values.dtype)
     lib = N.lib()
@@ -281,6 +287,8 @@ def scan_backward(values, logits, inits, logit_bias, hq, hk, hv, gq, gk, gv, NH:
     gvals = (gsb, D * gsc, gst, gsc)
     glgs = (gsb, Da * gsc, gst, gsc)
     glg_ptr = grad_combined.data_ptr() + H * D * gsc * grad_combined.element_size()
+    F = H * (D + Da)
+    pad = (-F) % 8 if zero_pad else 0
     cws, cws_bytes = (N.chain_workspace_for(values.dtype, values.device, B, T, NH, NKVH, Da, r,
                                             backward=True)
                       if P >= T else (None, 0))
@@ -293,7 +301,7 @@ def scan_backward(values, logits, inits, logit_bias, hq, hk, hv, gq, gk, gv, NH:
             hv.data_ptr(), N.strides(hv, 4),
             gq.data_ptr(), N.strides(gq, 4), gk.data_ptr(), N.strides(gk, 4),
             gv.data_ptr(), N.strides(gv, 4),
-            grad_combined.data_ptr(), _arr(gvals), glg_ptr, _arr(glgs),
+            grad_combined.data_ptr(), _arr(gvals), glg_ptr, _arr(glgs), pad,
             grad_inits.data_ptr(), _arr(gist), grad_bias.data_ptr(),
             ws.data_ptr(), ws_bytes, cws, cws_bytes, B, T, NH, NKVH, Da, r, P, Q, K,
             int(bool(use_sigmoid)), N.stream_of(values))
@@ -344,8 +352,9 @@ def qkv_filter_backward(x: torch.Tensor, wpack: torch.Tensor, values: torch.Tens
                                 device=x.device)
     grad_inits, grad_bias = scan_backward(values, logits, inits, logit_bias, hq, hk, hv,
                                           gq.to(hq.dtype), gk.to(hk.dtype), gv.to(hv.dtype),
-                                          NH, NKVH, Da, r, True, grad_combined, P, Q, K)
-    grad_x, grad_w = project_backward(x, wpack, grad_combined, H, D, Da)
+                                          NH, NKVH, Da, r, True, grad_combined, P, Q, K,
+                                          zero_pad=True)
+    grad_x, grad_w = project_backward(x, wpack, grad_combined, H, D, Da, pad_zeroed=True)
     return grad_x, grad_w, grad_inits, grad_bias
 
 

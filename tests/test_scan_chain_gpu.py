@@ -364,14 +364,14 @@ def _backward(comb, ini, bias, outs, grads, NH, NKVH, Da, r, sig, ws=None):
     rest = [bias.data_ptr()]
     for t in list(outs) + list(grads):
         rest += [t.data_ptr(), _s(t)]
-    rest += [gval.data_ptr(), _s(gval), glog.data_ptr(), _s(glog), gini.data_ptr(), _s(gini),
-             gbias.data_ptr(), scratch.data_ptr(), nbytes]
+    rest += [gval.data_ptr(), _s(gval), glog.data_ptr(), _s(glog)]
+    rest2 = [gini.data_ptr(), _s(gini), gbias.data_ptr(), scratch.data_ptr(), nbytes]
     tail = [B, T, NH, NKVH, Da, r, UNBOUNDED_P, 1, 1, int(sig), N.stream_of(comb)]
     if ws is None:
-        rc = lib.ltv_hm_look_back_scan_backward_split(*head, *rest, *tail)
+        rc = lib.ltv_hm_look_back_scan_backward_split(*head, *rest, *rest2, *tail)
     else:
-        rc = lib.ltv_hm_look_back_scan_backward_split_ws(*head, dt, *rest, ws.data_ptr(),
-                                                         ws.numel(), *tail)
+        rc = lib.ltv_hm_look_back_scan_backward_split_ws(*head, dt, *rest, 0, *rest2,
+                                                         ws.data_ptr(), ws.numel(), *tail)
     N.check(rc, "scan backward")
     return gval, glog, gini, gbias
 

@@ -208,3 +208,35 @@ def test_filter_shared_inits_match_cast_and_broadcast(B, T, Da, r):
         assert torch.equal(a, b), name
     assert new[4].dtype == torch.float32
     torch.testing.assert_close(new[4], old[4], rtol=1e-5, atol=1e-6)
+
+
+def test_zero_pad_and_zero_padded_grad_x():
+    """scan_backward(zero_pad=True) sets grad_combined's columns F ..
+    round_up(F, 8) - 1 to zero and leaves every other column it does not own
+    untouched; grad_x through ltv_qkv_project_backward_input_zero_padded on it
+    equals the zeroing entry point's bitwise."""
+    F_ = _F()
+    B, T, NH, NKVH, Da, r, C = 2, 300, 6, 6, 1, 128, 256
+    H, D = NH + 2 * NKVH, Da * r
+    Fv, Fp = H * (D + Da), F_.packed_width(H, D, Da)
+    pad_end = (Fv + 7) // 8 * 8
+    assert pad_end > Fv
+    values, logits, param, bias, gys = _case(B, T, NH, NKVH, Da, r, seed=21)
+    q, k, v = F_.scan_forward(values, logits, param, bias, NH, NKVH, Da, r, True)
+    gc = torch.full((B, T, Fp), float("nan"), dtype=torch.bfloat16, device=DEV)
+    F_.scan_backward(values, logits, param, bias, q, k, v, *gys, NH, NKVH, Da, r, True, gc,
+                     zero_pad=True)
+    assert int(torch.count_nonzero(gc[..., Fv:pad_end])) == 0
+    assert bool(torch.isnan(gc[..., pad_end:].float()).all())
+    assert not bool(torch.isnan(gc[..., :Fv].float()).any())
+    ref = torch.full_like(gc, float("nan"))
+    F_.scan_backward(values, logits, param, bias, q, k, v, *gys, NH, NKVH, Da, r, True, ref)
+    assert torch.equal(gc[..., :Fv], ref[..., :Fv])
+    assert bool(torch.isnan(ref[..., Fv:pad_end].float()).all())  # not asked: untouched
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(B, T, C, generator=g).to(torch.bfloat16).to(DEV)
+    w = (torch.randn(Fv, C, generator=g) * C ** -0.5).to(DEV)
+    wpack = F_.pack_weight(w, H, D, Da)
+    gx_p, gw_p = F_.project_backward(x, wpack, gc, H, D, Da, pad_zeroed=True)
+    gx_z, gw_z = F_.project_backward(x, wpack, ref, H, D, Da)
+    assert torch.equal(gx_p, gx_z) and torch.equal(gw_p, gw_z)
