@@ -122,6 +122,8 @@ size_t ltv_hm_scan_backward_workspace_size(int dtype, int B, int T, int NH, int 
  * grad_combined  : (B, T, F), any strides (fully overwritten)
  * grad_inits     : (B, H, D), any strides (overwritten)
  * grad_logit_bias: (H, Da) fp32 contiguous (overwritten, not accumulated)
+ * (grad_inits with batch stride 0 and B > 1 receives the sum over the batch,
+ *  as described at ltv_hm_look_back_scan_backward_split_ws.)
  *
  * Replaces ltv_fused_concat_head_major_register_cast_blelloch_scan_cuda_backward
  * (cpp_ewma/src/ltv_fused_concat_head_major_register_cast_blelloch_scan_cuda_backward.cu:882-976,
