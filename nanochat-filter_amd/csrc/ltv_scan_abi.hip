@@ -421,7 +421,9 @@ constexpr size_t kChainHeader = 256;
 //     NW = 2: 242 us) -- 16 chunks per sequence and about two chunk rows
 //     resident make the chain's critical path the time;
 //   B = 16, T = 1024 (288): tile 102 us, chained 93.5 us;
-//   B = 2, T = 8192 (36): tile with the chunk-map passes 144 us, chained 125 us.
+//   B = 2, T = 8192 (36): tile with the chunk-map passes 144 us, chained 125 us;
+//   B = 4 / 8, T = 8192 (72 / 144; configs[4]'s shape): tile with the chunk-map
+//     passes 242 / 412 us, chained 173 / 336 us ((4, 2) and (2, 4): 462, 465 us).
 constexpr int64_t kBwdChainMaxSeqs = 512;
 
 ChainPlan chain_plan(int dtype, int B, int T, int H, int Da, int r) {
