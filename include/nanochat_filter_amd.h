@@ -45,7 +45,7 @@ extern "C" {
 #define LTV_ERR_HIP 3
 #define LTV_ERR_WORKSPACE 4
 
-/* Version of this ABI (bumped on any signature change or addition): 7. */
+/* Version of this ABI (bumped on any signature change or addition): 8. */
 int ltv_abi_version(void);
 
 /* Message of the last failing call on this host thread ("" if none). */
@@ -455,6 +455,21 @@ int ltv_qkv_decode_step(const void* x, int64_t x_row_stride, const void* wpack,
                         const void* prev_q, const void* prev_k, const void* prev_v,
                         const int64_t prev_strides[6], const float* logit_bias, void* out, int B,
                         int C, int NH, int NKVH, int D, int Da, int use_sigmoid, void* stream);
+
+/* ltv_qkv_decode_step that also stores the new rows to rows_q/k/v (shaped
+ * like prev_q/k/v, channel stride 1; rows_strides as prev_strides) -- e.g. the
+ * KV cache's last-row buffers, which may be the prev rows themselves: every
+ * previous element is read before it is overwritten, by the thread that
+ * writes it.  `out` is written as well.  Counterpart in the reference: the
+ * decode step above followed by the computer module's copy of the last
+ * output rows into the cache (nanochat/ltv_combined_qkv_computer_module.py:28-41,
+ * nanochat/kv_cache.py:212), done by the kernel's stores. */
+int ltv_qkv_decode_step_rows(const void* x, int64_t x_row_stride, const void* wpack,
+                             void* prev_q, void* prev_k, void* prev_v,
+                             const int64_t prev_strides[6], const float* logit_bias, void* out,
+                             void* rows_q, void* rows_k, void* rows_v,
+                             const int64_t rows_strides[6], int B, int C, int NH, int NKVH, int D,
+                             int Da, int use_sigmoid, void* stream);
 
 /* ----------------------------------------------------------------------
  * Allocation-free form of ltv_hm_scan_backward: the same arguments without

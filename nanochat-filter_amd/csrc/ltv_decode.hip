@@ -41,6 +41,13 @@ struct DecodeArgs {
   int64_t prev_s[3][2];
   const float* bias;  // (H, Da)
   bf16_t* out;        // (B, H, D) contiguous
+  // optional second copy of the new rows of q, k, v: (B, H_g, D), strides
+  // (b, h), d = 1 (null: none).  May be the previous rows themselves: every
+  // element of prev is read, before it is written, by the thread that writes
+  // it (one workgroup per (head, 32 channels), and in it one thread per
+  // (token, channel) for the read and the store alike).
+  bf16_t* rows[3];
+  int64_t rows_s[3][2];
   int B, C, NH, NKVH, D, Da, r, Fp, use_sigmoid;
 };
 
@@ -91,6 +98,9 @@ __global__ void __launch_bounds__(kDecThreads) qkv_decode_kernel(const DecodeArg
   const int64_t psb = g == 0 ? a.prev_s[0][0] : g == 1 ? a.prev_s[1][0] : a.prev_s[2][0];
   const int64_t psh = g == 0 ? a.prev_s[0][1] : g == 1 ? a.prev_s[1][1] : a.prev_s[2][1];
   prevp += (int64_t)hl * psh;
+  bf16_t* rowsp = a.rows[g];
+  const int64_t rsb = a.rows_s[g][0];
+  if (rowsp != nullptr) rowsp += (int64_t)hl * a.rows_s[g][1];
 
   const int nk = a.C / 16;
   const int per = (nk + kDecKSlices - 1) / kDecKSlices;
@@ -167,7 +177,9 @@ __global__ void __launch_bounds__(kDecThreads) qkv_decode_kernel(const DecodeArg
         const float alpha = gate_alpha(z, a.use_sigmoid != 0);
         const float hp = hp_pre[q];
         const float hn = fmaf(alpha, u - hp, hp);
-        a.out[((int64_t)m * H + h) * a.D + ch] = (bf16_t)f32_to_bf16_bits(hn);
+        const bf16_t hb = (bf16_t)f32_to_bf16_bits(hn);
+        a.out[((int64_t)m * H + h) * a.D + ch] = hb;
+        if (rowsp != nullptr) rowsp[(int64_t)m * rsb + ch] = hb;
       }
     }
     __syncthreads();
@@ -179,11 +191,12 @@ __global__ void __launch_bounds__(kDecThreads) qkv_decode_kernel(const DecodeArg
 
 using namespace ltv;
 
-extern "C" int ltv_qkv_decode_step(const void* x, int64_t x_row_stride, const void* wpack,
-                                   const void* prev_q, const void* prev_k, const void* prev_v,
-                                   const int64_t prev_strides[6], const float* logit_bias,
-                                   void* out, int B, int C, int NH, int NKVH, int D, int Da,
-                                   int use_sigmoid, void* stream) {
+namespace {
+int decode_step_impl(const void* x, int64_t x_row_stride, const void* wpack, const void* prev_q,
+                     const void* prev_k, const void* prev_v, const int64_t prev_strides[6],
+                     const float* logit_bias, void* out, void* rows_q, void* rows_k,
+                     void* rows_v, const int64_t rows_strides[6], int B, int C, int NH, int NKVH,
+                     int D, int Da, int use_sigmoid, void* stream) {
   LTV_REQUIRE(B >= 0 && C > 0 && NH >= 0 && NKVH >= 0 && D > 0 && Da > 0, LTV_ERR_INVALID_ARG,
               "bad shape (B=%d C=%d NH=%d NKVH=%d D=%d Da=%d)", B, C, NH, NKVH, D, Da);
   LTV_REQUIRE(D % Da == 0, LTV_ERR_INVALID_ARG, "Da=%d must divide D=%d", Da, D);
@@ -212,6 +225,16 @@ extern "C" int ltv_qkv_decode_step(const void* x, int64_t x_row_stride, const vo
   }
   a.bias = logit_bias;
   a.out = reinterpret_cast<bf16_t*>(out);
+  void* const rows[3] = {rows_q, rows_k, rows_v};
+  for (int i = 0; i < 3; ++i) {
+    a.rows[i] = nullptr;
+    a.rows_s[i][0] = a.rows_s[i][1] = 0;
+    if (rows_strides != nullptr && rows[i] != nullptr && (i == 0 ? NH : NKVH) > 0) {
+      a.rows[i] = reinterpret_cast<bf16_t*>(rows[i]);
+      a.rows_s[i][0] = rows_strides[2 * i];
+      a.rows_s[i][1] = rows_strides[2 * i + 1];
+    }
+  }
   a.B = B;
   a.C = C;
   a.NH = NH;
@@ -225,4 +248,29 @@ extern "C" int ltv_qkv_decode_step(const void* x, int64_t x_row_stride, const vo
   hipLaunchKernelGGL(qkv_decode_kernel, dim3(grid), dim3(kDecThreads), 0, (hipStream_t)stream, a);
   LTV_LAUNCH_CHECK();
   return LTV_OK;
+}
+}  // namespace
+
+extern "C" int ltv_qkv_decode_step(const void* x, int64_t x_row_stride, const void* wpack,
+                                   const void* prev_q, const void* prev_k, const void* prev_v,
+                                   const int64_t prev_strides[6], const float* logit_bias,
+                                   void* out, int B, int C, int NH, int NKVH, int D, int Da,
+                                   int use_sigmoid, void* stream) {
+  return decode_step_impl(x, x_row_stride, wpack, prev_q, prev_k, prev_v, prev_strides,
+                          logit_bias, out, nullptr, nullptr, nullptr, nullptr, B, C, NH, NKVH, D,
+                          Da, use_sigmoid, stream);
+}
+
+extern "C" int ltv_qkv_decode_step_rows(const void* x, int64_t x_row_stride, const void* wpack,
+                                        void* prev_q, void* prev_k, void* prev_v,
+                                        const int64_t prev_strides[6], const float* logit_bias,
+                                        void* out, void* rows_q, void* rows_k, void* rows_v,
+                                        const int64_t rows_strides[6], int B, int C, int NH,
+                                        int NKVH, int D, int Da, int use_sigmoid, void* stream) {
+  LTV_REQUIRE(rows_strides != nullptr, LTV_ERR_INVALID_ARG, "null rows stride array");
+  LTV_REQUIRE((NH == 0 || rows_q) && (NKVH == 0 || (rows_k && rows_v)), LTV_ERR_INVALID_ARG,
+              "null rows pointer");
+  return decode_step_impl(x, x_row_stride, wpack, prev_q, prev_k, prev_v, prev_strides,
+                          logit_bias, out, rows_q, rows_k, rows_v, rows_strides, B, C, NH, NKVH,
+                          D, Da, use_sigmoid, stream);
 }

@@ -169,6 +169,12 @@ SIGNATURES = {
         [_c_vp, ctypes.c_int64, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64p, _c_vp, _c_vp,
          _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_vp],
     ),
+    "ltv_qkv_decode_step_rows": (
+        _c_int,
+        [_c_vp, ctypes.c_int64, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64p, _c_vp, _c_vp,
+         _c_vp, _c_vp, _c_vp, _c_i64p,
+         _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_vp],
+    ),
     "ltv_hm_scan_backward_noalloc_max_workspace": (_c_sz, []),
     "ltv_hm_scan_backward_noalloc": (
         _c_int,

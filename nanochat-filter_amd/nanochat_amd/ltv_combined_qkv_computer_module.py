@@ -12,6 +12,7 @@ from typing import Optional
 
 import torch.nn as nn
 
+from nanochat_amd.kv_cache import KVCache
 from nanochat_amd.ltv.ltv_filter import LtvInitValues
 from nanochat_amd.ltv_combined_qkv_filter_base import LtvCombinedQkvFilterBase
 
@@ -34,6 +35,21 @@ class LtvCombinedQkvComputerModule(nn.Module):
             )
         else:
             previous_values = LtvInitValues(None, None, None)
+
+        # A filter that can store its new last rows itself (the fused decode
+        # step) writes them straight into the cache's row buffers -- the rows
+        # it read as previous_values -- which is what update_last_qkv below
+        # would copy there (the cache already holds this layer's rows, so its
+        # bookkeeping has nothing to change).  Only for KVCache, whose row
+        # buffers are its own (a cache that kept references to earlier outputs
+        # would see them overwritten).
+        decode_into = getattr(self.ltv_filter, "decode_into_rows", None)
+        if (decode_into is not None and previous_values.q is not None
+                and isinstance(kv_cache, KVCache)):
+            out = decode_into(x, previous_values,
+                              (previous_values.q, previous_values.k, previous_values.v))
+            if out is not None:
+                return out
 
         q, k, v = self.ltv_filter(x, previous_values)
 

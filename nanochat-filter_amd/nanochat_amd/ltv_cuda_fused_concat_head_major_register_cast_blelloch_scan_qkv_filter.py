@@ -80,13 +80,29 @@ class LtvCudaFusedConcatHeadMajorRegisterCastBlellochScanQkvFilter(
         the parameter and ``load_state_dict`` are tracked."""
         hm_fast.invalidate_packed_weight(self)
 
-    def forward(self, x, previous_values: LtvInitValues):
-        B, _, _ = x.size()
+    def _compute_dtype(self, x):
         autocast_dtype = torch.get_autocast_dtype("cuda")
         run_ltv_in_fp32 = (
             autocast_dtype == torch.float32 if CUDA_SUPPORTS_NATIVE_BF16 else True
         )
-        compute_dtype = torch.float32 if run_ltv_in_fp32 else x.dtype
+        return torch.float32 if run_ltv_in_fp32 else x.dtype
+
+    def decode_into_rows(self, x, previous_values: LtvInitValues, rows):
+        """``forward``'s fused T = 1 bf16 decode step from the cache's previous
+        rows, which also stores the new last rows into ``rows`` (q, k, v, e.g.
+        the KV cache's last-row buffers, which may be the previous rows
+        themselves) in the same launch.  Returns (q, k, v) as ``forward`` does,
+        or None where ``forward`` would not take that path (then nothing is
+        written)."""
+        if (x.size(1) != 1 or torch.is_grad_enabled() or previous_values.q is None
+                or any(t is None for t in rows)
+                or self._compute_dtype(x) != torch.bfloat16):
+            return None
+        return self._decode_bf16(x, previous_values, rows)
+
+    def forward(self, x, previous_values: LtvInitValues):
+        B, _, _ = x.size()
+        compute_dtype = self._compute_dtype(x)
         if compute_dtype == torch.bfloat16 and x.size(1) == 1 and not torch.is_grad_enabled():
             return self._decode_bf16(x, previous_values)
         if compute_dtype == torch.bfloat16:
@@ -130,9 +146,9 @@ class LtvCudaFusedConcatHeadMajorRegisterCastBlellochScanQkvFilter(
         return hm_fast.cached_packed_weight(self, self.n_head + 2 * self.n_kv_head,
                                             self.head_dim, self.num_alpha_groups)
 
-    def _decode_bf16(self, x, previous_values):
+    def _decode_bf16(self, x, previous_values, rows=None):
         """T = 1 inference: one fused launch (projection of the new tokens and one
-        recurrence step from the previous rows)."""
+        recurrence step from the previous rows; the new rows also to ``rows``)."""
         B = x.size(0)
         NH, NKVH = self.n_head, self.n_kv_head
         if previous_values.q is not None:
@@ -144,7 +160,7 @@ class LtvCudaFusedConcatHeadMajorRegisterCastBlellochScanQkvFilter(
                     ip[NH + NKVH:].unsqueeze(0).expand(B, -1, -1))
         out = hm_fast.decode_step(x.to(torch.bfloat16), self._packed_weight(), prev,
                                   self.logit_bias.detach().float().contiguous(), NH, NKVH,
-                                  self.num_alpha_groups, self.r)
+                                  self.num_alpha_groups, self.r, rows=rows)
         return (out[:, :NH].unsqueeze(1), out[:, NH:NH + NKVH].unsqueeze(1),
                 out[:, NH + NKVH:].unsqueeze(1))
 

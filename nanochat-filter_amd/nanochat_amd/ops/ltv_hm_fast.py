@@ -128,10 +128,14 @@ def invalidate_packed_weight(module) -> None:
 
 
 def decode_step(x: torch.Tensor, wpack: torch.Tensor, prev, logit_bias: torch.Tensor, NH: int,
-                NKVH: int, Da: int, r: int, use_sigmoid: bool = True) -> torch.Tensor:
+                NKVH: int, Da: int, r: int, use_sigmoid: bool = True, rows=None) -> torch.Tensor:
     """One fused decode step: x (B, C) or (B, 1, C) bf16, the packed weight, the
     previous output rows ``prev = (q (B, NH, D), k (B, NKVH, D), v (B, NKVH, D))``
-    bf16 with channel stride 1 -> the new rows (B, H, D) bf16, contiguous."""
+    bf16 with channel stride 1 -> the new rows (B, H, D) bf16, contiguous.
+    rows: three more (B, nh, D) bf16 tensors, channel stride 1, that receive the
+    new rows as well -- e.g. the KV cache's last-row buffers, which may be the
+    prev tensors themselves (the kernel reads each previous element before
+    the same thread overwrites it)."""
     if x.dim() == 3:
         if x.shape[1] != 1:
             raise RuntimeError(f"decode_step takes one token per sequence, got x {tuple(x.shape)}")
@@ -144,7 +148,7 @@ def decode_step(x: torch.Tensor, wpack: torch.Tensor, prev, logit_bias: torch.Te
     H = NH + 2 * NKVH
     if x.stride(1) != 1 or x.stride(0) % 8 != 0:
         x = x.contiguous()
-    rows = []
+    prevs = []
     for t, nh in zip(prev, (NH, NKVH, NKVH)):
         if t.dtype != torch.bfloat16:
             t = t.to(torch.bfloat16)
@@ -152,18 +156,35 @@ def decode_step(x: torch.Tensor, wpack: torch.Tensor, prev, logit_bias: torch.Te
             raise RuntimeError(f"previous rows must be {(B, nh, D)}, got {tuple(t.shape)}")
         if t.stride(2) != 1:
             t = t.contiguous()
-        rows.append(t)
+        prevs.append(t)
     if logit_bias.dtype != torch.float32 or not logit_bias.is_contiguous():
         raise RuntimeError("logit_bias must be contiguous float32")
     out = torch.empty((B, H, D), dtype=torch.bfloat16, device=x.device)
-    strides = _arr([s for t in rows for s in t.stride()[:2]])
+    strides = _arr([s for t in prevs for s in t.stride()[:2]])
+    if rows is None:
+        with N.span("qkv_decode"):
+            rc = N.lib().ltv_qkv_decode_step(x.data_ptr(), x.stride(0), wpack.data_ptr(),
+                                             prevs[0].data_ptr(), prevs[1].data_ptr(),
+                                             prevs[2].data_ptr(), strides, logit_bias.data_ptr(),
+                                             out.data_ptr(), B, C, NH, NKVH, D, Da,
+                                             int(use_sigmoid), N.stream_of(x))
+        N.check(rc, "ltv_qkv_decode_step")
+        return out
+    for t, nh in zip(rows, (NH, NKVH, NKVH)):
+        if (t.dtype != torch.bfloat16 or tuple(t.shape) != (B, nh, D) or t.stride(2) != 1
+                or t.device != x.device):
+            raise RuntimeError(f"rows must be ({B}, {nh}, {D}) bf16 with channel stride 1 on "
+                               f"{x.device}, got {tuple(t.shape)} {t.dtype} {t.device}")
+    rstrides = _arr([s for t in rows for s in t.stride()[:2]])
     with N.span("qkv_decode"):
-        rc = N.lib().ltv_qkv_decode_step(x.data_ptr(), x.stride(0), wpack.data_ptr(),
-                                         rows[0].data_ptr(), rows[1].data_ptr(),
-                                         rows[2].data_ptr(), strides, logit_bias.data_ptr(),
-                                         out.data_ptr(), B, C, NH, NKVH, D, Da,
-                                         int(use_sigmoid), N.stream_of(x))
-    N.check(rc, "ltv_qkv_decode_step")
+        rc = N.lib().ltv_qkv_decode_step_rows(x.data_ptr(), x.stride(0), wpack.data_ptr(),
+                                              prevs[0].data_ptr(), prevs[1].data_ptr(),
+                                              prevs[2].data_ptr(), strides, logit_bias.data_ptr(),
+                                              out.data_ptr(), rows[0].data_ptr(),
+                                              rows[1].data_ptr(), rows[2].data_ptr(), rstrides,
+                                              B, C, NH, NKVH, D, Da, int(use_sigmoid),
+                                              N.stream_of(x))
+    N.check(rc, "ltv_qkv_decode_step_rows")
     return out
 
 

@@ -203,3 +203,47 @@ def test_decode_config5_vs_full_recompute():
     assert float(err.max()) <= bound + 2.0 ** -8 * hmax, (float(err.max()), bound)
     # and the drift is far from the bound on average
     assert float(err.mean()) <= 0.25 * bound
+
+
+def test_decode_writes_cache_rows_in_place():
+    """Through LtvCombinedQkvComputerModule and a KVCache, the fused decode step
+    stores the new last rows into the cache's row buffers itself
+    (ltv_qkv_decode_step_rows): every step's q, k, v and the cache rows are
+    bitwise those of the step with the module's copy (update_last_qkv), and the
+    rows returned by earlier steps are never modified."""
+    from nanochat_amd.gpt_config import ChunksAndHistory
+    from nanochat_amd.kv_cache import KVCache
+    from nanochat_amd.ltv_combined_qkv_computer_module import LtvCombinedQkvComputerModule
+    f = _make_filter(6, 6, 128, 128, seed=8, gate_scale=1.0, bias=(-2.5, -1.5))
+    m = LtvCombinedQkvComputerModule(0, f)
+    B, T0, N = 8, 5, 12
+    g = torch.Generator().manual_seed(9)
+    xs = torch.randn(B, T0 + N, 768, generator=g).to(torch.bfloat16).to(DEV)
+
+    def run(in_place):
+        cache = KVCache(B, 6, 6, T0 + N, 128, 1, [ChunksAndHistory(2147483647, 1, 1)])
+        if not in_place:
+            f.decode_into_rows = lambda *args: None  # the module falls back to its copy
+        try:
+            outs, kept = [], []
+            with torch.no_grad():
+                m(xs[:, :T0], cache)
+                for t in range(T0, T0 + N):
+                    q, k, v = m(xs[:, t:t + 1], cache)
+                    kept.append((q, q.clone()))
+                    outs.append(torch.cat([q, k, v], dim=2))
+            last = cache.last_qkv
+            rows = [t.special[0].clone() for t in (last.q, last.k, last.v)]
+        finally:
+            if not in_place:
+                del f.decode_into_rows
+        for q, q0 in kept:
+            assert torch.equal(q, q0), "a returned row changed after a later step"
+        return torch.cat(outs, dim=1), rows
+
+    a, rows_a = run(True)
+    b, rows_b = run(False)
+    assert torch.equal(a, b)
+    for x, y in zip(rows_a, rows_b):
+        assert torch.equal(x, y)
+    assert torch.equal(rows_a[0], a[:, -1, :6])
