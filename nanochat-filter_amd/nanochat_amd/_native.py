@@ -248,7 +248,16 @@ def dtype_code(dt: torch.dtype) -> int:
     raise TypeError(f"LTV kernels support float32 and bfloat16 tensors, got {dt}")
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_of(t: torch.Tensor) -> int:
+    """The current HIP stream of t's device, as the raw handle the library
+    takes (read without building a torch Stream object where torch offers it:
+    host time matters on the single-token decode path)."""
+    if _raw_stream is not None:
+        return _raw_stream(t.device.index if t.device.index is not None
+                           else torch.cuda.current_device())
     return torch.cuda.current_stream(t.device).cuda_stream
 
 

@@ -158,11 +158,14 @@ class LtvCudaFusedConcatHeadMajorRegisterCastBlellochScanQkvFilter(
             prev = (ip[:NH].unsqueeze(0).expand(B, -1, -1),
                     ip[NH:NH + NKVH].unsqueeze(0).expand(B, -1, -1),
                     ip[NH + NKVH:].unsqueeze(0).expand(B, -1, -1))
-        out = hm_fast.decode_step(x.to(torch.bfloat16), self._packed_weight(), prev,
-                                  self.logit_bias.detach().float().contiguous(), NH, NKVH,
+        bias = self.logit_bias
+        if bias.dtype != torch.float32 or not bias.is_contiguous():
+            bias = bias.detach().float().contiguous()
+        out = hm_fast.decode_step(x if x.dtype == torch.bfloat16 else x.to(torch.bfloat16),
+                                  self._packed_weight(), prev, bias, NH, NKVH,
                                   self.num_alpha_groups, self.r, rows=rows)
-        return (out[:, :NH].unsqueeze(1), out[:, NH:NH + NKVH].unsqueeze(1),
-                out[:, NH + NKVH:].unsqueeze(1))
+        # (B, 1, nh, D) views of the new rows, in one split
+        return out.unsqueeze(1).split((NH, NKVH, NKVH), dim=2)
 
     def _forward_fp32(self, x, inits):
         out_buf = fused_linear_transpose(x.float().contiguous(), self.c.weight.float().contiguous())

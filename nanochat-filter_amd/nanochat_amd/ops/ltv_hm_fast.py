@@ -55,8 +55,20 @@ def logit_width(H: int, Da: int) -> int:
     return (H * Da + 7) // 8 * 8
 
 
+_ARR_CACHE: dict = {}
+
+
 def _arr(s):
-    return (ctypes.c_int64 * len(s))(*s)
+    """An int64 ctypes array of s.  The arrays of recurring stride tuples are
+    kept (the library only reads them during the call), which saves their
+    construction on every decode step."""
+    key = tuple(s)
+    a = _ARR_CACHE.get(key)
+    if a is None:
+        a = (ctypes.c_int64 * len(key))(*key)
+        if len(_ARR_CACHE) < 4096:
+            _ARR_CACHE[key] = a
+    return a
 
 
 # ---------------------------------------------------------------------------
