@@ -1369,7 +1369,7 @@ scan_bwd_kernel(const BwdArgs args) {
       // the lane that starts at t_base enters from the inits (its h load was
       // masked); every other lane ORs zeros
       const bool at_init = active && t0 == t_base && t0 < t_hi;
-      const uint4 iv = init_vec();
+      const uint4 iv = init_vec();  // loop-invariant: formed once, before the tile loop
       const uint4 qi = at_init ? iv : make_uint4(0u, 0u, 0u, 0u);
       q = make_uint4(q.x | qi.x, q.y | qi.y, q.z | qi.z, q.w | qi.w);
       if constexpr (LB) {
@@ -1535,7 +1535,10 @@ scan_bwd_kernel(const BwdArgs args) {
       if (GL) {
         float p = 0.0f;
 #pragma unroll
-        for (int v = 0; v < V; ++v) p += v < nvalid ? dav[v] : 0.0f;
+        // (16-byte vectors: every channel of an active lane is valid, and an
+        // inactive lane's partial is dropped by `ok` below -- no per-channel
+        // select)
+        for (int v = 0; v < V; ++v) p += (VEC || v < nvalid) ? dav[v] : 0.0f;
         pl[s] = ok ? p : 0.0f;
       } else {
         // whole groups of r channels (r | V, a power of two) inside the lane:
