@@ -1509,8 +1509,10 @@ scan_bwd_kernel(const BwdArgs args) {
 
     // ---- re-run backwards: du, dinit and the gate-group dalpha sums; steps
     // before t_st (look-back warm-up) go to the fp32 workspaces
-    reload_barrier(uq);
-    reload_barrier(gq);
+    // (No reload_barrier on uq / gq here: re-widening them for the re-run
+    // cost 12% of the tile loop's instructions at d12, and keeping their
+    // fp32 forms fits the registers -- 229 VGPRs at (16, 4, 2), 186 for the
+    // chained (16, 4, 4).)
     const Rsrc dur = make_rsrc(dubh + (int64_t)T0 * args.du.s[2] * E);
     const Rsrc dlr = make_rsrc(dlbh + (int64_t)T0 * args.dlg.s[2] * E);
     const Rsrc wdur = make_rsrc(LB ? wdubh + (int64_t)(T0 - t_base) * S.D * 4 : dubh);
