@@ -157,7 +157,7 @@ int ltv_hm_scan_backward(int dtype, const void* combined, const int64_t combined
  *   ltv_hm_scan_backward_chain_workspace_size(...) (one zeroed buffer can serve
  *   the chained forward and backward on one stream: each call leaves it
  *   zeroed).  NULL selects the kernels of ltv_hm_scan_backward.  The chained
- *   kernel is used below 512 (b, head) sequences with 16-byte channel
+ *   kernel is used below 256 (b, head) sequences with 16-byte channel
  *   vectors, gate groups of whole lanes (at most 16 per head) or r = 1, and
  *   at least two chunks; elsewhere the size query returns 0 and a workspace
  *   passed is not touched.  (LTV_SCAN_BWD_CHAIN_CFG="L,NW" forces it, "0"

@@ -415,16 +415,18 @@ struct ChainPlan {
   size_t bytes;  // workspace: header + tagged states
 };
 constexpr size_t kChainHeader = 256;
-// (b, h) sequences from which the backward keeps the tile kernel.  Measured on
-// MI355X (heads of 128, r = 128, bf16; chained shape L = 4, NW = 4):
-//   B = 32, T = 1024 (576 sequences): tile 118 us, chained 171 us (L = 4,
-//     NW = 2: 242 us) -- 16 chunks per sequence and about two chunk rows
-//     resident make the chain's critical path the time;
-//   B = 16, T = 1024 (288): tile 102 us, chained 93.5 us;
-//   B = 2, T = 8192 (36): tile with the chunk-map passes 144 us, chained 125 us;
-//   B = 4 / 8, T = 8192 (72 / 144; configs[4]'s shape): tile with the chunk-map
-//     passes 242 / 412 us, chained 173 / 336 us ((4, 2) and (2, 4): 462, 465 us).
-constexpr int64_t kBwdChainMaxSeqs = 512;
+// (b, h) sequences from which the backward keeps the tile kernel (which runs
+// unchunked from 256 sequences on).  Measured on MI355X (heads of 128,
+// r = 128, bf16; chained shape L = 4, NW = 4), tile against chained:
+//   B = 32, T = 1024 (576 sequences): 112 against 171 us (L = 4, NW = 2:
+//     242 us) -- 16 chunks per sequence and about two chunk rows resident
+//     make the chain's critical path the time;
+//   B = 16 (288): T = 1024 84 against 89 us, T = 2048 160 against 156 us;
+//   below 256, where the tile kernel needs the chunk-map passes: B = 8 / 4,
+//     T = 1024 (144 / 72) 90 / 72 against 54 / 36 us; B = 8, T = 4096 222
+//     against 157 us; T = 8192: B = 8 / 4 / 2 / 1 (configs[4]'s shape is
+//     B = 8) 400 / 232 / 139 / 108 against 298 / 166 / 120 / 103 us.
+constexpr int64_t kBwdChainMaxSeqs = 256;
 
 ChainPlan chain_plan(int dtype, int B, int T, int H, int Da, int r) {
   ChainPlan p{{0, 0, 0}, -1, 0, 0, 0, 0};
@@ -615,8 +617,7 @@ constexpr int kBwdFineSteps = 64;
 // not used.  It needs the full recurrence, 16-byte channel vectors, one gate
 // per lane group or r == 1, and a built shape; it is chosen below
 // kBwdChainMaxSeqs sequences, where the tile kernel's workgroups are too few
-// to hide its per-tile latency (and below 256, where the tile kernel needs the
-// chunk-map passes).  LTV_SCAN_BWD_CHAIN_CFG="L,NW" forces it with that shape.
+// to hide its per-tile latency and it needs the chunk-map passes.  LTV_SCAN_BWD_CHAIN_CFG="L,NW" forces it with that shape.
 struct BwdChainPlan {
   ScanCfg cfg;
   int gm, nchunk;

@@ -88,22 +88,23 @@ def test_abi_version_and_host_only_queries():
     assert lib.ltv_hm_scan_forward_chain_workspace_size(1, 2, 64, 1, 1, 32, 4) == 0
     assert lib.ltv_hm_scan_forward_chain_workspace_size(1, 2, 0, 1, 1, 1, 128) == 0
     # chained scan backward: the same layout, one word per channel of a whole
-    # head (CL V = 128) per chunk but a sequence's first.  B = 16 at d12 heads
-    # (288 sequences): 16 chunks of 64 steps (16 channel lanes x 4 time groups
+    # head (CL V = 128) per chunk but a sequence's first.  B = 8 at d12 heads
+    # (144 sequences): 16 chunks of 64 steps (16 channel lanes x 4 time groups
     # x 4 steps x 4 wavefronts); fp32: 32 channel lanes, chunks of 32 steps;
-    # d12 itself (576 sequences), one chunk (T = 64), gate groups of 4
-    # channels, or T = 0: no chained kernel
-    assert lib.ltv_hm_scan_backward_chain_workspace_size(1, 16, 1024, 6, 6, 1, 128) == \
-        256 + 16 * 18 * 15 * 128 * 8
+    # 256 sequences and more (B = 16: 288; d12: 576), one chunk (T = 64), gate
+    # groups of 4 channels, or T = 0: no chained kernel
+    assert lib.ltv_hm_scan_backward_chain_workspace_size(1, 8, 1024, 6, 6, 1, 128) == \
+        256 + 8 * 18 * 15 * 128 * 8
     assert lib.ltv_hm_scan_backward_chain_workspace_size(0, 2, 1024, 6, 6, 1, 128) == \
         256 + 2 * 18 * 31 * 128 * 8
+    assert lib.ltv_hm_scan_backward_chain_workspace_size(1, 16, 1024, 6, 6, 1, 128) == 0
     assert lib.ltv_hm_scan_backward_chain_workspace_size(1, 32, 1024, 6, 6, 1, 128) == 0
     assert lib.ltv_hm_scan_backward_chain_workspace_size(1, 2, 64, 6, 6, 1, 128) == 0
     assert lib.ltv_hm_scan_backward_chain_workspace_size(1, 2, 1024, 1, 1, 32, 4) == 0
     assert lib.ltv_hm_scan_backward_chain_workspace_size(1, 2, 0, 1, 1, 1, 128) == 0
     # the scan backward's own workspace holds the chained kernel's dbias
     # partials (one per (b, h, chunk)) as well as the tile kernel's
-    assert lib.ltv_hm_scan_backward_workspace_size(1, 16, 1024, 6, 6, 1, 128) >= 16 * 18 * 16 * 4
+    assert lib.ltv_hm_scan_backward_workspace_size(1, 8, 1024, 6, 6, 1, 128) >= 8 * 18 * 16 * 4
     # argument errors are reported without touching a device
     rc = lib.ltv_qkv_project_forward(None, None, None, None, 2, 8, 12, 3, 64, 1, None)
     assert rc == 2 and "multiple of 8" in N.last_error()

@@ -477,18 +477,18 @@ def test_chain_backward_sigmoid_vs_oracle_and_tile(dtype, B, T, NH, NKVH, Da, r)
 
 
 def test_chain_backward_bitwise_equals_unchunked_tile():
-    """288 (b, h) sequences of d12 heads (B = 16): the tile kernel runs them
-    unchunked, 4 steps per lane like the chained kernel, and the chained
-    carries are composed in the tile loop's order -- so grad_values,
+    """fp32 I/O at T = 64 (72 (b, h) sequences of heads of 128, r = 16): the
+    chained kernel runs two 32-step chunks, the tile kernel one unchunked pass
+    (no chunk-map carries up to 64 steps), both with 4 steps per lane, and the
+    chained carries are composed in the tile loop's order -- so grad_values,
     grad_logits and grad_inits are bitwise equal; grad_logit_bias sums
     per-chunk partials instead of per-sequence ones (rel. 1e-5)."""
-    B, T, NH, NKVH, Da, r = 16, 333, 6, 6, 1, 128
-    dtype = torch.bfloat16
+    B, T, NH, NKVH, Da, r = 4, 64, 6, 6, 8, 16
+    dtype = torch.float32
     H, D = NH + 2 * NKVH, Da * r
     assert _bwd_ws_bytes(dtype, B, T, NH, NKVH, Da, r) > 0
-    c, ini, bias = _random_case(B, T, NH, NKVH, Da, r, seed=16, io="bf16")
-    gy = O.round_io(np.random.default_rng(7).standard_normal((B, H, T, D)).astype(np.float32),
-                    "bf16")
+    c, ini, bias = _random_case(B, T, NH, NKVH, Da, r, seed=16, io="f32")
+    gy = np.random.default_rng(7).standard_normal((B, H, T, D)).astype(np.float32)
     cd, idv, bd = to_torch(c, dtype, DEV), to_torch(ini, dtype, DEV), to_torch(bias, torch.float32, DEV)
     outs = _forward(cd, idv, bd, NH, NKVH, Da, r, True)
     grads = _torch_grads(gy, NH, NKVH, dtype)
@@ -498,7 +498,7 @@ def test_chain_backward_bitwise_equals_unchunked_tile():
     for name, a, b in zip(("grad_values", "grad_logits", "grad_inits"), chain[:3], tile[:3]):
         assert torch.equal(a, b), name
     assert torch.allclose(chain[3], tile[3], rtol=1e-5, atol=1e-5 * float(tile[3].abs().max()))
-    _check_ws_clean(ws, "B=16 d12 heads")
+    _check_ws_clean(ws, "fp32 T = 64")
 
 
 def test_chain_backward_workspace_errors():
