@@ -68,7 +68,11 @@ S_IO = 2  # bf16
 
 
 def algorithmic_work():
-    """Per-launch algorithmic bytes / FLOPs (formulas of BASELINE.md section 2)."""
+    """Per-launch algorithmic bytes / FLOPs: the scan forward reads the values
+    and logits (F columns) and the inits and writes the H·D outputs; the
+    backward reads values, logits and upstream gradients and writes the
+    F-column gradient (states recomputed, not re-read), plus the inits and
+    their gradient; each projection GEMM is 2·M·C·F FLOPs."""
     scan_fwd = B * T * (F + H * D) * S_IO + B * H * D * S_IO + 4 * H * DA
     scan_bwd = B * T * (2 * F + H * D) * S_IO + 2 * B * H * D * S_IO + 4 * H * DA
     gemm = 2 * B * T * C * F
