@@ -87,7 +87,8 @@ int ltv_hm_scan_forward(int dtype, const void* combined, const int64_t combined_
  *   that overlap in time (other streams) need buffers of their own.
  *   NULL selects the kernel of ltv_hm_scan_forward.  The chained kernel is
  *   used where it is the faster one: fewer than 1,024 (b, head, channel slab)
- *   sequences, 16-byte channel vectors, gate groups of whole lanes or r = 1;
+ *   sequences of at least 8 chunks (T > 3,584; r = 1: T > 1,792), 16-byte
+ *   channel vectors, gate groups of whole lanes or r = 1;
  *   elsewhere the size query returns 0 and a workspace passed is not
  *   touched.  (LTV_SCAN_CHAIN_CFG="CL,L,NW" forces it, "0" turns it off.)
  *   The workspace's second

@@ -397,7 +397,8 @@ int check_pqk(int P, int Q, int K) {
 // D channels with gate groups of r, or CL = 0 where it is not used.  It needs
 // the full recurrence, 16-byte channel vectors and one gate per lane or r == 1,
 // and it is chosen where the tile kernel would run fewer than 1,024
-// workgroups (long T at small batch).  Measured on MI355X:
+// workgroups and each sequence spans at least 8 chunks (long T at small
+// batch).  Measured on MI355X:
 //   configs[4] prefill (B = 8, T = 8192, 288 sequences): tile 172 us, chained
 //     (8, 8, 8) 127 us, (8, 16, 4) 128 us, (8, 8, 4) 145 us, (8, 4, 8) 135 us;
 //   d12 (1,152 sequences, T = 1024): tile 62.6 us, chained (8, 8, 8) 66.6 us,
@@ -407,6 +408,11 @@ int check_pqk(int P, int Q, int K) {
 //     96.5 us, (8, 4, 4) 128 us.
 // Chunks shorter than 256 steps lose to the per-workgroup start-up (ticket,
 // two barriers, the hand-off): (8, 4, 4) 124 us, (8, 2, 4) 222 us at d12.
+// Few chunks per sequence do not repay it either: tile against chained (8, 8, 8)
+// at T = 1024 (2 chunks): B = 4 / 8 / 16 18.5 / 23.3 / 32.9 against 22.8 /
+// 26.2 / 39.4 us; T = 2048 (4): B = 8 / 16 37.9 / 70.0 against 39.4 / 70.9 us;
+// T = 4096 (8): B = 2 / 4 / 16 49.0 / 48.6 / 146.9 against 27.8 / 40.7 /
+// 126.6 us; so the automatic choice also needs kFwdChainMinChunks chunks.
 // LTV_SCAN_CHAIN_CFG="CL,L,NW" forces the chained kernel with that shape.
 struct ChainPlan {
   ScanCfg cfg;
@@ -415,6 +421,7 @@ struct ChainPlan {
   size_t bytes;  // workspace: header + tagged states
 };
 constexpr size_t kChainHeader = 256;
+constexpr int kFwdChainMinChunks = 8;
 // (b, h) sequences from which the backward keeps the tile kernel (which runs
 // unchunked from 256 sequences on).  Measured on MI355X (heads of 128,
 // r = 128, bf16; chained shape L = 4, NW = 4), tile against chained:
@@ -451,10 +458,13 @@ ChainPlan chain_plan(int dtype, int B, int T, int H, int Da, int r) {
   }
   if (c.CL * V > 64 || c.CL < 1 || c.L < 1 || c.NW < 1) return p;
   const int TW = c.NW * (64 / c.CL) * c.L;
+  const int nchunk = (int)(((int64_t)T + TW - 1) / TW);
+  // (and only for sequences of at least kFwdChainMinChunks chunks)
+  if (tu.chain_cl == 0 && nchunk < kFwdChainMinChunks) return p;
   p.cfg = c;
   p.gm = gm;
   p.nslab = (D + c.CL * V - 1) / (c.CL * V);
-  p.nchunk = (int)(((int64_t)T + TW - 1) / TW);
+  p.nchunk = nchunk;
   p.nseq = (int64_t)B * H * p.nslab;
   p.bytes = kChainHeader + (size_t)p.nseq * (size_t)(p.nchunk - 1) * (size_t)(c.CL * V) * 8u;
   return p;

@@ -78,12 +78,15 @@ def test_abi_version_and_host_only_queries():
     # chained scan forward: 256-byte header + one 8-byte word per channel of
     # every chunk but a sequence's last.  configs[4] prefill (8 x 18 heads x 2
     # slabs of 64 channels): 16 chunks of 512 steps; fp32: slabs of 32
-    # channels; d12 (1,152 tile workgroups), gate groups that are neither whole
-    # lanes nor r = 1, or T = 0: no chained kernel
+    # channels; d12 (1,152 tile workgroups), fewer than 8 chunks (T = 3584),
+    # gate groups that are neither whole lanes nor r = 1, or T = 0: no chained
+    # kernel
     assert lib.ltv_hm_scan_forward_chain_workspace_size(1, 8, 8192, 6, 6, 1, 128) == \
         256 + 8 * 18 * 2 * 15 * 64 * 8
-    assert lib.ltv_hm_scan_forward_chain_workspace_size(0, 2, 1024, 6, 6, 1, 128) == \
-        256 + 2 * 18 * 4 * 1 * 32 * 8
+    assert lib.ltv_hm_scan_forward_chain_workspace_size(0, 2, 4096, 6, 6, 1, 128) == \
+        256 + 2 * 18 * 4 * 7 * 32 * 8
+    assert lib.ltv_hm_scan_forward_chain_workspace_size(1, 2, 3584, 6, 6, 1, 128) == 0
+    assert lib.ltv_hm_scan_forward_chain_workspace_size(1, 2, 3585, 6, 6, 1, 128) > 0
     assert lib.ltv_hm_scan_forward_chain_workspace_size(1, 32, 1024, 6, 6, 1, 128) == 0
     assert lib.ltv_hm_scan_forward_chain_workspace_size(1, 2, 64, 1, 1, 32, 4) == 0
     assert lib.ltv_hm_scan_forward_chain_workspace_size(1, 2, 0, 1, 1, 1, 128) == 0

@@ -124,18 +124,18 @@ def _check_ws_clean(ws, label):
     assert nz == 0, f"{label}: {nz} nonzero workspace bytes after the call (ticket/err/words)"
 
 
-# T spans one partial chunk, exactly one chunk, and several chunks with a
-# ragged tail, for the d12 gate shape (one gate per head), gate groups of 16
-# channels, and per-channel gates (r = 1).
+# The library takes the chained kernel from 8 chunks per sequence on (chunks
+# of 512 steps, 256 for r = 1): T spans 8 chunks whose last holds one step,
+# exactly 8 chunks, and more with a ragged tail, for the d12 gate shape (one
+# gate per head), gate groups of 16 channels, and per-channel gates (r = 1).
 CASES = [
     # (B, T, NH, NKVH, Da, r)
-    (2, 1, 2, 1, 1, 128),
-    (2, 300, 2, 1, 1, 128),
-    (2, 512, 1, 1, 1, 128),
-    (2, 1537, 2, 1, 1, 128),
+    (2, 3585, 2, 1, 1, 128),
+    (2, 4096, 1, 1, 1, 128),
+    (2, 4700, 2, 1, 1, 128),
     (1, 4133, 1, 1, 8, 16),
-    (2, 700, 1, 1, 64, 1),
-    (1, 129, 1, 0, 128, 1),
+    (2, 2000, 1, 1, 64, 1),
+    (1, 1793, 1, 0, 128, 1),
 ]
 
 
@@ -195,8 +195,8 @@ def test_chain_workspace_reuse_across_shapes():
     invariant leaves it zeroed), including one with more chunks than the
     buffer's previous user."""
     dtype = torch.bfloat16
-    shapes = [(2, 2100, 2, 1, 1, 128), (3, 600, 1, 1, 1, 128), (1, 5000, 1, 1, 128, 1),
-              (2, 2100, 2, 1, 1, 128)]
+    shapes = [(2, 4100, 2, 1, 1, 128), (3, 3700, 1, 1, 1, 128), (1, 5000, 1, 1, 128, 1),
+              (2, 4100, 2, 1, 1, 128)]
     need = max(_ws_bytes(dtype, *s) for s in shapes)
     ws = _zero_ws(need)
     for B, T, NH, NKVH, Da, r in shapes:
@@ -212,9 +212,10 @@ def test_chain_workspace_errors():
     """A workspace below the queried size or off 256-byte alignment is
     refused before any launch; no workspace selects the tile kernel."""
     N, lib = _lib()
-    B, T, NH, NKVH, Da, r = 1, 2000, 1, 1, 1, 128
+    B, T, NH, NKVH, Da, r = 1, 4000, 1, 1, 1, 128
     dtype = torch.bfloat16
     nbytes = _ws_bytes(dtype, B, T, NH, NKVH, Da, r)
+    assert nbytes > 0
     c, ini, bias = _random_case(B, T, NH, NKVH, Da, r, seed=1, io="bf16")
     cd, idv, bd = to_torch(c, dtype, DEV), to_torch(ini, dtype, DEV), to_torch(bias, torch.float32, DEV)
     small = _zero_ws(nbytes - 512)
@@ -233,7 +234,7 @@ def test_chain_combined_layout():
     columns): the chained kernel runs (a short workspace is refused) and is
     exact on the integer generators."""
     N, lib = _lib()
-    B, T, NH, NKVH, Da, r = 2, 1100, 1, 1, 8, 16
+    B, T, NH, NKVH, Da, r = 2, 4000, 1, 1, 8, 16
     D = Da * r
     dtype = torch.bfloat16
     c = int_combined(B, T, NH, NKVH, Da, r)
@@ -299,8 +300,9 @@ def test_chain_graph_replays_match_eager():
     captured in a HIP graph: every replay equals the eager result, with eager
     work and synchronisation between replays."""
     from nanochat_amd.ops import ltv_hm_fast as F_
-    B, T, NH, NKVH, D = 2, 3000, 2, 1, 128
+    B, T, NH, NKVH, D = 2, 4000, 2, 1, 128
     H = NH + 2 * NKVH
+    assert _ws_bytes(torch.bfloat16, B, T, NH, NKVH, 1, D) > 0
     g = torch.Generator().manual_seed(3)
     values = torch.randn(B, H, T, D, generator=g).to(torch.bfloat16).to(DEV)
     logits = (-(2.0 + torch.randn(B, T, H, generator=g))).to(torch.bfloat16).to(DEV)
@@ -524,12 +526,12 @@ def test_chain_backward_workspace_errors():
 
 def test_chain_forward_and_backward_share_one_workspace():
     """The fast path's per-stream buffer serves the chained forward and the
-    chained backward in turn: a filter step (B = 2, T = 3000, d12 heads)
+    chained backward in turn: a filter step (B = 2, T = 4000, d12 heads)
     through the module's autograd, twice, bitwise equal, the buffer zeroed
     after each."""
     from nanochat_amd import _native as N
     from nanochat_amd.ops import ltv_hm_fast as F_
-    B, T, NH, NKVH, D, C = 2, 3000, 2, 1, 128, 256
+    B, T, NH, NKVH, D, C = 2, 4000, 2, 1, 128, 256
     H = NH + 2 * NKVH
     assert _ws_bytes(torch.bfloat16, B, T, NH, NKVH, 1, D) > 0
     assert _bwd_ws_bytes(torch.bfloat16, B, T, NH, NKVH, 1, D) > 0

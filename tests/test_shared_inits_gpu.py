@@ -45,10 +45,11 @@ def _case(B, T, NH, NKVH, Da, r, seed, init_dtype=torch.float32):
     return values, logits, param, bias, gys
 
 
-# (B, T, NH, NKVH, Da, r): the d12 gate shape through the tile kernels and the
-# chained forward / backward, gate groups of 16 channels, per-channel gates
-SHAPES = [(32, 256, 6, 6, 1, 128), (2, 700, 2, 1, 1, 128), (3, 300, 1, 1, 8, 16),
-          (2, 129, 1, 1, 64, 1), (1, 200, 2, 1, 1, 128)]
+# (B, T, NH, NKVH, Da, r): the d12 gate shape through the tile kernels, the
+# chained backward, the chained forward (8 chunks of 512 steps), gate groups of
+# 16 channels, per-channel gates
+SHAPES = [(32, 256, 6, 6, 1, 128), (2, 700, 2, 1, 1, 128), (1, 3600, 1, 1, 1, 128),
+          (3, 300, 1, 1, 8, 16), (2, 129, 1, 1, 64, 1), (1, 200, 2, 1, 1, 128)]
 
 
 @pytest.mark.parametrize("B,T,NH,NKVH,Da,r", SHAPES)
