@@ -45,7 +45,7 @@ extern "C" {
 #define LTV_ERR_HIP 3
 #define LTV_ERR_WORKSPACE 4
 
-/* Version of this ABI (bumped on any signature change or addition): 8. */
+/* Version of this ABI (bumped on any signature change or addition): 9. */
 int ltv_abi_version(void);
 
 /* Message of the last failing call on this host thread ("" if none). */
@@ -91,10 +91,15 @@ int ltv_hm_scan_forward(int dtype, const void* combined, const int64_t combined_
  *   channel vectors, gate groups of whole lanes or r = 1;
  *   elsewhere the size query returns 0 and a workspace passed is not
  *   touched.  (LTV_SCAN_CHAIN_CFG="CL,L,NW" forces it, "0" turns it off.)
- *   The workspace's second
- *   32-bit word becomes nonzero only if a chunk's wait ran past its bound
- *   (never expected; the outputs of that call are then invalid and the buffer
- *   must be zeroed again).
+ *   Failure: a chunk's wait for its carry is bounded (about a second); past
+ *   it, or with a workspace that was not zero at the launch, the kernel still
+ *   exits normally, but the outputs of that call are invalid.  It then sets
+ *   the workspace's second 32-bit word to the error code (1: a wait ran out,
+ *   2: the workspace was not zero) and stores the code into the library's
+ *   host mailbox, which ltv_chain_take_error() reads without synchronising
+ *   the device.  After an error the workspace must be zeroed again.  (A wait
+ *   that runs out leaves no late carry behind: the reader marks the word
+ *   abandoned and the late publisher clears it.)
  *
  * Replaces the same reference forward as ltv_hm_scan_forward; the workspace
  * has no counterpart there (the reference walks T serially per block,
@@ -110,6 +115,29 @@ int ltv_hm_scan_forward_ws(int dtype, const void* combined, const int64_t combin
                            const int64_t out_v_strides[4], void* chain_workspace,
                            size_t chain_workspace_bytes, int B, int T, int NH, int NKVH, int Da,
                            int r, int use_sigmoid, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Error mailbox of the chained kernels (ltv_hm_scan_forward_ws,
+ * ltv_hm_scan_backward_ws and the look-back *_split_ws variants): returns the
+ * error code (1 or 2, see ltv_hm_scan_forward_ws) that a chained launch has
+ * reported since the previous call, or 0, and clears it.  Reads mapped host
+ * memory: no device synchronisation, so a launch still running is seen by a
+ * later call.  Synchronise the stream first to check one call.
+ *
+ * No reference counterpart: the reference's scans launch no kernel that
+ * waits on another workgroup; its launch checks are
+ * cpp_ewma/src/ltv_fused_concat_head_major_register_cast_blelloch_scan_cuda_forward.cu:452,465,495,504
+ * (C10_CUDA_KERNEL_LAUNCH_CHECK), which this library's status codes replace.
+ * ---------------------------------------------------------------------- */
+int ltv_chain_take_error(void);
+
+/* Test control of the chained kernels' waits, for failure-handling tests that
+ * must not hang: spin_max = polls before a wait gives up (0 restores the
+ * default bound), no_publish != 0 makes every chained launch publish no carry,
+ * so every wait runs out after spin_max polls and every kernel still exits
+ * normally.  Applies to launches made after the call.  No reference
+ * counterpart. */
+int ltv_chain_set_test_controls(int spin_max, int no_publish);
 
 /* Workspace bytes needed by ltv_hm_scan_backward / ltv_hm_scan_backward_split. */
 size_t ltv_hm_scan_backward_workspace_size(int dtype, int B, int T, int NH, int NKVH, int Da,

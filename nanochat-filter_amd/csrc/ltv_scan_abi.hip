@@ -4,6 +4,7 @@
 #include <stdlib.h>
 
 #include <algorithm>
+#include <mutex>
 
 #include "ltv_scan_launch.hpp"
 
@@ -422,6 +423,46 @@ struct ChainPlan {
 };
 constexpr size_t kChainHeader = 256;
 constexpr int kFwdChainMinChunks = 8;
+
+// Error mailbox of the chained kernels: one mapped, pinned host word that a
+// failing launch stores its code into (ChainCtl::host_err), read and cleared
+// by ltv_chain_take_error without synchronising the device.  Allocated once,
+// on the first chained launch; if the allocation fails the kernels report
+// into the workspace header only.
+struct ChainHost {
+  std::mutex mu;
+  bool tried = false;
+  uint32_t* host = nullptr;  // host view
+  uint32_t* dev = nullptr;   // device view
+  int spin_max = kChainSpinMax;
+  int no_publish = 0;
+};
+ChainHost& chain_host() {
+  static ChainHost h;
+  return h;
+}
+
+ChainCtl chain_ctl() {
+  ChainHost& h = chain_host();
+  std::lock_guard<std::mutex> lk(h.mu);
+  if (!h.tried) {
+    h.tried = true;
+    void* p = nullptr;
+    if (hipHostMalloc(&p, 256, hipHostMallocMapped | hipHostMallocPortable |
+                                   hipHostMallocCoherent) == hipSuccess) {
+      void* d = nullptr;
+      if (hipHostGetDevicePointer(&d, p, 0) == hipSuccess && d != nullptr) {
+        h.host = static_cast<uint32_t*>(p);
+        h.dev = static_cast<uint32_t*>(d);
+        __atomic_store_n(h.host, 0u, __ATOMIC_SEQ_CST);
+      } else {
+        (void)hipHostFree(p);
+      }
+    }
+    (void)hipGetLastError();  // a failed allocation is not the caller's error
+  }
+  return ChainCtl{h.dev, h.spin_max, h.no_publish};
+}
 // (b, h) sequences from which the backward keeps the tile kernel (which runs
 // unchunked from 256 sequences on).  Measured on MI355X (heads of 128,
 // r = 128, bf16; chained shape L = 4, NW = 4), tile against chained:
@@ -597,6 +638,7 @@ int scan_forward_impl(int dtype, const HostView4& u, const HostView4& lg, const 
       LTV_REQUIRE(pl.nseq * pl.nchunk < (1ll << 31), LTV_ERR_UNSUPPORTED, "grid too large");
       ch.nseq = (int)pl.nseq;
       ch.nchunk = pl.nchunk;
+      ch.ctl = chain_ctl();
       return scan_launch_fwd_chain(dtype == LTV_DTYPE_BF16, a, ch, pl.cfg, pl.gm, st);
     }
   }
@@ -836,6 +878,7 @@ int scan_backward_impl(int dtype, const HostView4& u, const HostView4& lg, const
   a.wst = nullptr;
   a.wdu = a.wdl = a.wdi = nullptr;
   a.ch_ticket = a.ch_err = nullptr;
+  a.ch_ctl = ChainCtl{nullptr, kChainSpinMax, 0};
   a.ch_words = nullptr;
 
   int gm = bwd_gate_mode(r, Da, V);
@@ -965,6 +1008,7 @@ int scan_backward_impl(int dtype, const HostView4& u, const HostView4& lg, const
       a.ch_err = reinterpret_cast<uint32_t*>(chain_ws) + 1;
       a.ch_words = reinterpret_cast<unsigned long long*>(reinterpret_cast<char*>(chain_ws) +
                                                          kChainHeader);
+      a.ch_ctl = chain_ctl();
       rc = scan_launch_bwd_chain(dtype == LTV_DTYPE_BF16, a, pl.cfg, (int)grid, gm, st);
       if (rc) return rc;
       return scan_launch_dbias_reduce(a.dbias_partial, dbias, B, H, a.nchunk, Da, st, ds, pz);
@@ -1223,6 +1267,22 @@ extern "C" size_t ltv_hm_scan_backward_chain_workspace_size(int dtype, int B, in
                                                            int NKVH, int Da, int r) {
   if (check_shape(dtype, B, T, NH, NKVH, Da, r) != LTV_OK) return 0;
   return bwd_chain_plan(dtype, B, T, NH + 2 * NKVH, Da, r).bytes;
+}
+
+extern "C" int ltv_chain_take_error(void) {
+  ltv::ChainHost& h = ltv::chain_host();
+  std::lock_guard<std::mutex> lk(h.mu);
+  if (h.host == nullptr) return 0;
+  return (int)__atomic_exchange_n(h.host, 0u, __ATOMIC_SEQ_CST);
+}
+
+extern "C" int ltv_chain_set_test_controls(int spin_max, int no_publish) {
+  LTV_REQUIRE(spin_max >= 0, LTV_ERR_INVALID_ARG, "spin_max must be >= 0 (got %d)", spin_max);
+  ltv::ChainHost& h = ltv::chain_host();
+  std::lock_guard<std::mutex> lk(h.mu);
+  h.spin_max = spin_max == 0 ? ltv::kChainSpinMax : spin_max;
+  h.no_publish = no_publish != 0;
+  return LTV_OK;
 }
 
 extern "C" int ltv_hm_scan_backward_ws(

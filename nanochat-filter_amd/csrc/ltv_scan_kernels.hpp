@@ -107,6 +107,16 @@ __host__ __device__ inline int look_back_nwin(int T, int P, int Q) {
   return T > P ? 1 + (int)(((int64_t)T - P + Q - 1) / Q) : 1;
 }
 
+// Host-set control of the chained kernels' bounded carry waits.
+struct ChainCtl {
+  // Mapped host word (or null): a chained launch that fails stores its error
+  // code there as well as in the workspace header, so the host learns of it
+  // without a device synchronisation.
+  uint32_t* host_err;
+  int spin_max;    // polls before a carry wait gives up
+  int no_publish;  // test hook: publishers publish nothing, every wait runs out
+};
+
 struct FwdArgs {
   ScanShape sh;
   View4 u;     // values   (B, H, T, D)
@@ -173,6 +183,7 @@ struct BwdArgs {
   uint32_t* ch_ticket;
   uint32_t* ch_err;
   unsigned long long* ch_words;
+  ChainCtl ch_ctl;
 };
 
 // How a lane finds the gate of each of its V channels.
@@ -858,26 +869,94 @@ scan_fwd_kernel(const FwdArgs args) {
 //     tickets map chunk-major onto (sequence, chunk).  The chunk a workgroup
 //     waits for holds an earlier ticket, so it is already running and itself
 //     waits only on earlier tickets: every wait ends.  A wait is still bounded
-//     (kChainSpinMax polls, about a second; a chunk's wait is normally a few
-//     microseconds); past the bound the kernel sets *err = 1, goes on with a
-//     zero state and exits normally.
+//     (ChainCtl::spin_max polls, by default kChainSpinMax, about a second; a
+//     chunk's wait is normally a few microseconds); past the bound the kernel
+//     reports error 1 (chain_report), goes on with a zero state and exits
+//     normally.
 //   * Zero invariant: the reader of a word clears it, the last chunk of a
 //     sequence publishes nothing, and the workgroup that draws the last ticket
 //     resets the counter, so the workspace is all zeros again when the kernel
 //     ends and a launch needs no clearing pass (nor a memset in a captured
-//     graph).
+//     graph).  A reader that gives up swaps an "abandoned" marker into the
+//     empty word (compare-and-swap); the publisher's own compare-and-swap
+//     then fails on it, and the publisher clears the word instead: a late
+//     carry is never left behind for a later launch to read.
 // The chunk composes its wavefront totals onto the entering state in the
 // tile kernel's order, so with the same launch shape (CL, L, NW) both kernels
 // give bitwise equal outputs.
 struct ChainArgs {
   uint32_t* ticket;           // chunk ticket counter (0 between launches)
-  uint32_t* err;              // 1: a wait ran past kChainSpinMax polls; 2: counter not 0 at launch
+  uint32_t* err;              // 1: a wait ran past its bound; 2: counter not 0 at launch
   unsigned long long* words;  // (nseq, nchunk - 1, CL * V) tagged states (0 between launches)
   int nseq;                   // B * H * nslab
   int nchunk;                 // chunks per sequence
+  ChainCtl ctl;
 };
 constexpr int kChainSpinMax = 1 << 20;
-constexpr unsigned long long kChainTag = 1ull << 32;
+constexpr unsigned long long kChainTag = 1ull << 32;        // a published carry
+constexpr unsigned long long kChainAbandoned = 2ull << 32;  // its reader gave up
+
+// Record error `code` in the workspace header and the host's mailbox.
+__device__ __forceinline__ void chain_report(uint32_t* err, const ChainCtl& ctl, uint32_t code) {
+  __hip_atomic_store(err, code, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (ctl.host_err != nullptr)
+    __hip_atomic_store(ctl.host_err, code, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+// The carry published in *pw, waited for at most ctl.spin_max polls; the word
+// is left zero.  Past the bound: an abandoned marker replaces the empty word
+// (unless the carry landed meanwhile), error 1 is reported and 0 returned.
+__device__ __forceinline__ float chain_take(unsigned long long* pw, uint32_t* err,
+                                            const ChainCtl& ctl) {
+  unsigned long long wv = 0;
+  for (int spin = 0;; ++spin) {
+    wv = __hip_atomic_load(pw, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if ((wv >> 32) == (kChainTag >> 32)) break;
+    if (spin >= ctl.spin_max) {
+      unsigned long long expect = 0;
+      if (__hip_atomic_compare_exchange_strong(pw, &expect, kChainAbandoned, __ATOMIC_RELAXED,
+                                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
+        chain_report(err, ctl, 1u);
+        return 0.0f;
+      }
+      if ((expect >> 32) != (kChainTag >> 32)) {
+        // a marker left by an earlier failed launch: the workspace was not
+        // zeroed after that error
+        chain_report(err, ctl, 2u);
+        __hip_atomic_store(pw, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return 0.0f;
+      }
+      wv = expect;  // the carry landed between the last poll and the swap
+      break;
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
+  __hip_atomic_store(pw, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return __uint_as_float((uint32_t)wv);
+}
+
+// Publish carry p into the empty word *pw.  Returns the word's previous
+// value: non-zero (the abandoned marker) means the reader gave up, and the
+// caller must then clear the word with chain_clear_abandoned -- late, so the
+// atomic's round trip is not waited for on the chain's path.
+__device__ __forceinline__ unsigned long long chain_publish(unsigned long long* pw, float p,
+                                                            const ChainCtl& ctl) {
+  if (ctl.no_publish) return 0ull;
+  unsigned long long expect = 0;
+  __hip_atomic_compare_exchange_strong(pw, &expect, kChainTag | __float_as_uint(p),
+                                       __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+  return expect;
+}
+
+__device__ __forceinline__ void chain_clear_abandoned(unsigned long long* pw,
+                                                      unsigned long long prev) {
+  // The empty asm keeps the whole returned value live up to here: otherwise
+  // the compiler tests it right after the compare-and-swap and waits for the
+  // atomic's round trip before the workgroup barrier that follows it.
+  asm volatile("" : "+v"(prev));
+  if (prev != 0ull) __hip_atomic_store(pw, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 template <typename TIO, int CL, int L, int NW, bool VEC, int GM>
 __global__ void __launch_bounds__(NW * 64)
@@ -915,7 +994,7 @@ scan_fwd_chain_kernel(const FwdArgs args, const ChainArgs ch) {
   // its first use) hands out tickets past the grid: such a workgroup only
   // reports it (the waits of the others end at their bound)
   if (ticket >= (int)gridDim.x) {
-    if (threadIdx.x == 0) __hip_atomic_store(ch.err, 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (threadIdx.x == 0) chain_report(ch.err, ch.ctl, 2u);
     return;
   }
   const int seq = ticket % ch.nseq;
@@ -1025,26 +1104,16 @@ scan_fwd_chain_kernel(const FwdArgs args, const ChainArgs ch) {
 
   // the chain step: wavefront 0, lane j = slab channel j, takes the entering
   // state, publishes the leaving one and hands the entering one to the others
+  unsigned long long* pub_word = nullptr;
+  unsigned long long pub_prev = 0ull;
   if (w == 0 && lane < NCH) {
     const int j = lane;
     float cin;
     if (chunk == 0) {
       cin = lds_c[j];
     } else {
-      unsigned long long* pw = ch.words + ((int64_t)seq * (ch.nchunk - 1) + chunk - 1) * NCH + j;
-      unsigned long long wv = 0;
-      for (int spin = 0;; ++spin) {
-        wv = __hip_atomic_load(pw, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if ((wv >> 32) != 0) break;
-        if (spin >= kChainSpinMax) {
-          __hip_atomic_store(ch.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          wv = 0;
-          break;
-        }
-        __builtin_amdgcn_s_sleep(1);
-      }
-      __hip_atomic_store(pw, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      cin = __uint_as_float((uint32_t)wv);
+      cin = chain_take(ch.words + ((int64_t)seq * (ch.nchunk - 1) + chunk - 1) * NCH + j, ch.err,
+                       ch.ctl);
     }
     if (chunk + 1 < ch.nchunk) {
       const float* xa = reinterpret_cast<const float*>(&lds_x[0][0][0]);
@@ -1052,9 +1121,8 @@ scan_fwd_chain_kernel(const FwdArgs args, const ChainArgs ch) {
 #pragma unroll
       for (int ww = 0; ww < NW; ++ww)
         p = fmaf(lds_a[ww][j / V][GL ? 0 : j % V], p, xa[ww * NCH + j]);
-      __hip_atomic_store(ch.words + ((int64_t)seq * (ch.nchunk - 1) + chunk) * NCH + j,
-                         kChainTag | __float_as_uint(p), __ATOMIC_RELAXED,
-                         __HIP_MEMORY_SCOPE_AGENT);
+      pub_word = ch.words + ((int64_t)seq * (ch.nchunk - 1) + chunk) * NCH + j;
+      pub_prev = chain_publish(pub_word, p, ch.ctl);
     }
     lds_c[j] = cin;
   }
@@ -1098,6 +1166,7 @@ scan_fwd_chain_kernel(const FwdArgs args, const ChainArgs ch) {
     bst_vec<TIO, VEC, GM == GATE_CHANVEC ? kStStream : kStNormal>(
         orr, ooff + s * ostb, oscb, nvalid, active && (t0 + s) < T, hv);
   }
+  if (pub_word != nullptr) chain_clear_abandoned(pub_word, pub_prev);
 }
 
 // ---------------------------------------------------------------------------
@@ -1156,8 +1225,7 @@ scan_bwd_kernel(const BwdArgs args) {
     // grid: such a workgroup only reports it (the others' waits end at their
     // bound)
     if (ticket >= (int)gridDim.x) {
-      if (threadIdx.x == 0)
-        __hip_atomic_store(args.ch_err, 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (threadIdx.x == 0) chain_report(args.ch_err, args.ch_ctl, 2u);
       return;
     }
     const int nseq = S.B * S.H;
@@ -1353,6 +1421,10 @@ scan_bwd_kernel(const BwdArgs args) {
 #pragma unroll
   for (int v = 0; v < V; ++v) dinit_v[v] = 0.0f;
 
+  // the chained mode's published word and its previous value (cleared at the
+  // end if the reader gave up)
+  unsigned long long* pub_word = nullptr;
+  unsigned long long pub_prev = 0ull;
   auto process_tile = [&](int it, auto bufc) {
     constexpr int buf = decltype(bufc)::value;
     const int T0 = t_base + it * TW;
@@ -1448,22 +1520,9 @@ scan_bwd_kernel(const BwdArgs args) {
           float cin = 0.0f;
           if (j < S.D) {
             const int64_t row = (int64_t)bh * (args.nchunk - 1);
-            if (chunk + 1 < args.nchunk) {
-              unsigned long long* pw = args.ch_words + (row + chunk) * NCH + j;
-              unsigned long long wv = 0;
-              for (int spin = 0;; ++spin) {
-                wv = __hip_atomic_load(pw, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                if ((wv >> 32) != 0) break;
-                if (spin >= kChainSpinMax) {
-                  __hip_atomic_store(args.ch_err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                  wv = 0;
-                  break;
-                }
-                __builtin_amdgcn_s_sleep(1);
-              }
-              __hip_atomic_store(pw, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-              cin = __uint_as_float((uint32_t)wv);
-            }
+            if (chunk + 1 < args.nchunk)
+              cin = chain_take(args.ch_words + (row + chunk) * NCH + j, args.ch_err,
+                               args.ch_ctl);
             if (chunk > 0) {
               // the tile loop's composition, last wavefront first
               const float* xb = reinterpret_cast<const float*>(&lds_bx[par][0][0][0]);
@@ -1471,9 +1530,8 @@ scan_bwd_kernel(const BwdArgs args) {
 #pragma unroll
               for (int ww = NW - 1; ww >= 0; --ww)
                 p = fmaf(lds_ba[par][ww][jl][GL ? 0 : jv], p, xb[(ww * CL + jl) * V + jv]);
-              __hip_atomic_store(args.ch_words + (row + chunk - 1) * NCH + j,
-                                 kChainTag | __float_as_uint(p), __ATOMIC_RELAXED,
-                                 __HIP_MEMORY_SCOPE_AGENT);
+              pub_word = args.ch_words + (row + chunk - 1) * NCH + j;
+              pub_prev = chain_publish(pub_word, p, args.ch_ctl);
             }
           }
           lds_cin[j] = cin;
@@ -1686,6 +1744,9 @@ scan_bwd_kernel(const BwdArgs args) {
         for (int q = 0; q < TG; ++q) acc += lds_red[ww * 64 + lcl * TG + q][k];
     }
     args.dbias_partial[((int64_t)bh * args.nchunk + chunk) * S.Da + j] = acc;
+  }
+  if constexpr (CHAIN) {
+    if (pub_word != nullptr) chain_clear_abandoned(pub_word, pub_prev);
   }
 }
 

@@ -11,6 +11,7 @@ from __future__ import annotations
 import ctypes
 import os
 import threading
+from typing import NamedTuple
 
 import torch
 
@@ -175,6 +176,8 @@ SIGNATURES = {
          _c_vp, _c_vp, _c_vp, _c_i64p,
          _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_vp],
     ),
+    "ltv_chain_take_error": (_c_int, []),
+    "ltv_chain_set_test_controls": (_c_int, [_c_int, _c_int]),
     "ltv_hm_scan_backward_noalloc_max_workspace": (_c_sz, []),
     "ltv_hm_scan_backward_noalloc": (
         _c_int,
@@ -269,6 +272,43 @@ def stream_of(t: torch.Tensor) -> int:
 # captured with it).
 _CHAIN_WS: dict = {}
 
+CHAIN_ERRORS = {1: "a chunk's wait for its carry ran past its bound",
+                2: "the chain workspace was not zero at the launch"}
+
+
+class ChainWorkspace(NamedTuple):
+    """A chained call's workspace: hold ``buf`` until the library call has
+    been made (the pointer is only valid while the tensor lives)."""
+    buf: torch.Tensor | None
+    ptr: int | None
+    nbytes: int
+
+
+_NO_CHAIN = ChainWorkspace(None, None, 0)
+
+
+def chain_sync_check() -> bool:
+    """Whether every chained call synchronises its stream and checks the
+    library's error mailbox at once (LTV_CHAIN_SYNC_CHECK=1; the tests set
+    it).  Otherwise a failure is reported by the next chained call."""
+    return os.environ.get("LTV_CHAIN_SYNC_CHECK", "0") not in ("", "0")
+
+
+def check_chain_errors() -> None:
+    """Raise if a chained scan launched since the last check reported a
+    failure (read from the library's host mailbox, no device
+    synchronisation).  The chain workspaces are then dropped, so the next
+    call starts from a fresh zeroed one."""
+    code = lib().ltv_chain_take_error()
+    if code == 0:
+        return
+    torch.cuda.synchronize()
+    _CHAIN_WS.clear()
+    raise RuntimeError(
+        f"chained LTV scan failed (code {code}: {CHAIN_ERRORS.get(code, 'unknown')}); the "
+        "outputs of chained scan calls since the previous check are invalid, and the chain "
+        "workspaces have been reset")
+
 
 def chain_workspace(device: torch.device, nbytes: int):
     """A 256-byte aligned, all-zero device buffer of at least ``nbytes`` bytes
@@ -289,17 +329,27 @@ def chain_workspace(device: torch.device, nbytes: int):
 
 
 def chain_workspace_for(dtype: torch.dtype, device: torch.device, B: int, T: int, NH: int,
-                        NKVH: int, Da: int, r: int, backward: bool = False):
-    """(pointer, bytes) of the chain workspace for this scan shape, (None, 0)
-    where the chained forward (or, with ``backward``, the chained backward)
-    does not apply."""
+                        NKVH: int, Da: int, r: int, backward: bool = False) -> ChainWorkspace:
+    """The chain workspace for this scan shape (pointer None and 0 bytes where
+    the chained forward -- or, with ``backward``, the chained backward -- does
+    not apply).  Raises first if an earlier chained call reported a failure."""
     size = (lib().ltv_hm_scan_backward_chain_workspace_size if backward
             else lib().ltv_hm_scan_forward_chain_workspace_size)
     nbytes = size(dtype_code(dtype), B, T, NH, NKVH, Da, r)
+    if nbytes == 0:
+        return _NO_CHAIN
+    check_chain_errors()
     buf = chain_workspace(device, nbytes)
-    if buf is None:
-        return None, 0
-    return buf.data_ptr(), buf.numel()
+    return ChainWorkspace(buf, buf.data_ptr(), buf.numel())
+
+
+def chain_done(cw: ChainWorkspace) -> None:
+    """After a library call that was given ``cw``: with LTV_CHAIN_SYNC_CHECK
+    set (and outside graph capture), wait for it and raise if it failed."""
+    if cw.buf is None or not chain_sync_check() or torch.cuda.is_current_stream_capturing():
+        return
+    torch.cuda.current_stream(cw.buf.device).synchronize()
+    check_chain_errors()
 
 
 def require_device(*tensors: torch.Tensor) -> None:

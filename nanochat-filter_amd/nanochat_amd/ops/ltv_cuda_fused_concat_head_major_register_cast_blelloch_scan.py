@@ -83,7 +83,7 @@ def forward_kernel(
     if T_ != T:
         raise RuntimeError(f"T={T} does not match combined.shape[1]={T_}")
     lib = N.lib()
-    ws, ws_bytes = N.chain_workspace_for(combined.dtype, combined.device, B, T, NH, NKVH, da, r)
+    cw = N.chain_workspace_for(combined.dtype, combined.device, B, T, NH, NKVH, da, r)
     rc = lib.ltv_hm_scan_forward_ws(
         N.dtype_code(combined.dtype),
         combined.data_ptr(), N.strides(combined, 3),
@@ -92,11 +92,12 @@ def forward_kernel(
         out_q.data_ptr(), _s4(out_q),
         out_k.data_ptr(), _s4(out_k),
         out_v.data_ptr(), _s4(out_v),
-        ws, ws_bytes,
+        cw.ptr, cw.nbytes,
         B, T, NH, NKVH, da, r, int(bool(use_sigmoid)),
         N.stream_of(combined),
     )
     N.check(rc, "ltv_hm_scan_forward_ws")
+    N.chain_done(cw)
 
 
 @torch.library.impl(
@@ -185,8 +186,8 @@ def backward_kernel(
     lib = N.lib()
     ws_bytes = lib.ltv_hm_scan_backward_workspace_size(dt, B, T, NH, NKVH, da, r)
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=combined.device)
-    cws, cws_bytes = N.chain_workspace_for(combined.dtype, combined.device, B, T, NH, NKVH, da, r,
-                                           backward=True)
+    cw = N.chain_workspace_for(combined.dtype, combined.device, B, T, NH, NKVH, da, r,
+                               backward=True)
     rc = lib.ltv_hm_scan_backward_ws(
         dt,
         combined.data_ptr(), N.strides(combined, 3),
@@ -198,11 +199,12 @@ def backward_kernel(
         grad_combined.data_ptr(), N.strides(grad_combined, 3),
         grad_inits.data_ptr(), N.strides(grad_inits, 3),
         grad_logit_bias.data_ptr(),
-        ws.data_ptr(), ws_bytes, cws, cws_bytes,
+        ws.data_ptr(), ws_bytes, cw.ptr, cw.nbytes,
         B, T, NH, NKVH, da, r, int(bool(use_sigmoid)),
         N.stream_of(combined),
     )
     N.check(rc, "ltv_hm_scan_backward_ws")
+    N.chain_done(cw)
 
 
 def _setup(ctx, inputs, output):

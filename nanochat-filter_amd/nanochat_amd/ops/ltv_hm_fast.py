@@ -280,17 +280,18 @@ def scan_forward(values: torch.Tensor, logits: torch.Tensor, inits: torch.Tensor
     else:  # (B, T, >= H Da), column h Da + j
         sb, st_, sl = logits.stride()
         lgs = (sb, Da * sl, st_, sl)
-    ws, ws_bytes = (N.chain_workspace_for(values.dtype, values.device, B, T, NH, NKVH, Da, r)
-                    if P >= T else (None, 0))
+    cw = (N.chain_workspace_for(values.dtype, values.device, B, T, NH, NKVH, Da, r)
+          if P >= T else N._NO_CHAIN)
     with N.span("scan_fwd"):
         rc = N.lib().ltv_hm_look_back_scan_forward_split_ws(
             N.dtype_code(values.dtype),
             values.data_ptr(), N.strides(values, 4), logits.data_ptr(), _arr(lgs),
             inits.data_ptr(), _arr(ist), idt, logit_bias.data_ptr(),
             out[0].data_ptr(), N.strides(out[0], 4), out[1].data_ptr(), N.strides(out[1], 4),
-            out[2].data_ptr(), N.strides(out[2], 4), ws, ws_bytes,
+            out[2].data_ptr(), N.strides(out[2], 4), cw.ptr, cw.nbytes,
             B, T, NH, NKVH, Da, r, P, Q, K, int(bool(use_sigmoid)), N.stream_of(values))
     N.check(rc, "ltv_hm_look_back_scan_forward_split_ws")
+    N.chain_done(cw)
     return out[0], out[1], out[2]
 
 
@@ -322,9 +323,9 @@ def scan_backward(values, logits, inits, logit_bias, hq, hk, hv, gq, gk, gv, NH:
     glg_ptr = grad_combined.data_ptr() + H * D * gsc * grad_combined.element_size()
     F = H * (D + Da)
     pad = (-F) % 8 if zero_pad else 0
-    cws, cws_bytes = (N.chain_workspace_for(values.dtype, values.device, B, T, NH, NKVH, Da, r,
-                                            backward=True)
-                      if P >= T else (None, 0))
+    cw = (N.chain_workspace_for(values.dtype, values.device, B, T, NH, NKVH, Da, r,
+                                backward=True)
+          if P >= T else N._NO_CHAIN)
     with N.span("scan_bwd"):
         rc = lib.ltv_hm_look_back_scan_backward_split_ws(
             dt,
@@ -336,9 +337,10 @@ def scan_backward(values, logits, inits, logit_bias, hq, hk, hv, gq, gk, gv, NH:
             gv.data_ptr(), N.strides(gv, 4),
             grad_combined.data_ptr(), _arr(gvals), glg_ptr, _arr(glgs), pad,
             grad_inits.data_ptr(), _arr(gist), grad_bias.data_ptr(),
-            ws.data_ptr(), ws_bytes, cws, cws_bytes, B, T, NH, NKVH, Da, r, P, Q, K,
+            ws.data_ptr(), ws_bytes, cw.ptr, cw.nbytes, B, T, NH, NKVH, Da, r, P, Q, K,
             int(bool(use_sigmoid)), N.stream_of(values))
     N.check(rc, "ltv_hm_look_back_scan_backward_split_ws")
+    N.chain_done(cw)
     return grad_inits, grad_bias
 
 

@@ -4,6 +4,9 @@ import sys
 import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+# every chained scan call synchronises and checks the library's error mailbox
+# (outside tests a failure is reported by the next chained call)
+os.environ.setdefault("LTV_CHAIN_SYNC_CHECK", "1")
 for p in (os.path.join(ROOT, "nanochat-filter_amd"), os.path.join(ROOT, "oracle"), ROOT):
     if p not in sys.path:
         sys.path.insert(0, p)

@@ -69,7 +69,7 @@ def test_abi_version_and_host_only_queries():
     if not os.path.exists(N.LIB_PATH):
         pytest.skip("library not built")
     lib = N.load()
-    assert lib.ltv_abi_version() == 8
+    assert lib.ltv_abi_version() == 9
     # d12: 18 heads x (128 + 1) = 2322 -> padded to a multiple of 128; 18 logits -> 24
     assert lib.ltv_qkv_packed_width(18, 128, 1) == 2432
     assert lib.ltv_qkv_logit_width(18, 1) == 24
@@ -170,3 +170,18 @@ def test_product_path_refuses_cpu_tensors():
     bias = torch.zeros(6, 1)
     with pytest.raises(RuntimeError, match="GPU tensors"):
         torch.ops.nanochat_amd.qkv_filter(x, w, inits, bias, 2, 2, 1, 8)
+
+
+def test_chain_error_mailbox_and_controls_host_side():
+    """The chain error mailbox reads 0 before any chained launch (and never
+    allocates or touches the device for that), and the test controls refuse
+    a negative spin bound and accept the defaults back."""
+    from nanochat_amd import _native as N
+    if not os.path.exists(N.LIB_PATH):
+        pytest.skip("library not built")
+    lib = N.lib()
+    assert lib.ltv_chain_take_error() == 0
+    assert lib.ltv_chain_set_test_controls(-1, 0) == 1  # LTV_ERR_INVALID_ARG
+    assert "spin_max" in N.last_error()
+    assert lib.ltv_chain_set_test_controls(0, 0) == 0
+    assert lib.ltv_chain_take_error() == 0

@@ -601,3 +601,182 @@ def test_chain_backward_graph_replays_match_eager():
         gc2 = torch.zeros_like(gc_eager)
         gi2, gb2 = run(gc2)
         assert torch.equal(gc2[..., :F], gc_eager[..., :F]) and torch.equal(gi2, gi_eager)
+
+
+# ---------------------------------------------------------------------------
+# Failure handling.  The host forces the failure: ltv_chain_set_test_controls
+# bounds every carry wait at a few polls and makes the chained launches
+# publish no carry, so every wait of a chunk after a sequence's first runs out
+# and every kernel still exits normally.
+# ---------------------------------------------------------------------------
+@pytest.fixture
+def forced_chain_timeouts():
+    """Yields a switch for forced carry-wait timeouts: on = 16 polls per wait
+    and no carry published; off = the defaults; an int n = n polls per wait
+    with carries published.  Restores the default controls, drains the error
+    mailbox and drops the cached chain workspaces afterwards."""
+    N, lib = _lib()
+
+    def switch(on):
+        spin, nopub = (on, 0) if type(on) is int else ((16, 1) if on else (0, 0))
+        N.check(lib.ltv_chain_set_test_controls(spin, nopub), "ltv_chain_set_test_controls")
+
+    try:
+        yield switch
+    finally:
+        switch(False)
+        torch.cuda.synchronize()
+        lib.ltv_chain_take_error()
+        N._CHAIN_WS.clear()
+
+
+def _fast_inputs(B, T, NH, NKVH, D, seed):
+    H = NH + 2 * NKVH
+    g = torch.Generator().manual_seed(seed)
+    values = torch.randn(B, H, T, D, generator=g).to(torch.bfloat16).to(DEV)
+    logits = (-(2.0 + torch.randn(B, T, H, generator=g))).to(torch.bfloat16).to(DEV)
+    inits = torch.randn(B, H, D, generator=g).to(torch.bfloat16).to(DEV)
+    bias = torch.zeros(H, 1, device=DEV)
+    return values, logits, inits, bias
+
+
+def test_chain_failure_reported_through_the_abi(forced_chain_timeouts):
+    """A chained forward whose waits run out reports code 1 in the
+    workspace's error word and in the host mailbox (read once, then clear);
+    with the controls back to normal and the workspace re-zeroed (what the
+    header asks after an error), the next launch is bitwise the healthy
+    result."""
+    N, lib = _lib()
+    B, T, NH, NKVH, Da, r = 2, 4100, 1, 1, 1, 128
+    dtype = torch.bfloat16
+    nbytes = _ws_bytes(dtype, B, T, NH, NKVH, Da, r)
+    assert nbytes > 0
+    c, ini, bias = _random_case(B, T, NH, NKVH, Da, r, seed=11, io="bf16")
+    cd, idv, bd = to_torch(c, dtype, DEV), to_torch(ini, dtype, DEV), to_torch(bias, torch.float32, DEV)
+    ws = _zero_ws(nbytes)
+    assert lib.ltv_chain_take_error() == 0
+    good = _forward(cd, idv, bd, NH, NKVH, Da, r, True, ws)
+    torch.cuda.synchronize()
+    assert lib.ltv_chain_take_error() == 0
+    forced_chain_timeouts(True)
+    _forward(cd, idv, bd, NH, NKVH, Da, r, True, ws)
+    torch.cuda.synchronize()
+    assert int(ws.view(torch.int32)[1]) == 1, "error word"
+    assert lib.ltv_chain_take_error() == 1
+    assert lib.ltv_chain_take_error() == 0, "the mailbox is cleared by a read"
+    forced_chain_timeouts(False)
+    ws.zero_()
+    again = _forward(cd, idv, bd, NH, NKVH, Da, r, True, ws)
+    torch.cuda.synchronize()
+    assert lib.ltv_chain_take_error() == 0
+    for a, b in zip(again, good):
+        assert torch.equal(a, b)
+    _check_ws_clean(ws, "after recovery")
+
+
+@pytest.mark.parametrize("sync_check", [True, False], ids=["sync", "deferred"])
+def test_chain_forward_failure_raises_and_recovers(forced_chain_timeouts, monkeypatch, sync_check):
+    """Through the fast path's op: with LTV_CHAIN_SYNC_CHECK=1 the failing
+    call raises; without it the next chained call raises.  Either way the
+    cached workspace is dropped and the call after that is bitwise the
+    healthy result."""
+    from nanochat_amd.ops import ltv_hm_fast as F_
+    N, lib = _lib()
+    monkeypatch.setenv("LTV_CHAIN_SYNC_CHECK", "1" if sync_check else "0")
+    B, T, NH, NKVH, D = 2, 4100, 1, 1, 128
+    values, logits, inits, bias = _fast_inputs(B, T, NH, NKVH, D, seed=12)
+    assert N.chain_workspace_for(values.dtype, values.device, B, T, NH, NKVH, 1, D).nbytes > 0
+
+    def run():
+        return F_.scan_forward(values, logits, inits, bias, NH, NKVH, 1, D, True)
+
+    good = run()
+    forced_chain_timeouts(True)
+    if sync_check:
+        with pytest.raises(RuntimeError, match=r"chained LTV scan failed \(code 1"):
+            run()
+        forced_chain_timeouts(False)
+    else:
+        run()  # fails on the device, reported later
+        torch.cuda.synchronize()
+        forced_chain_timeouts(False)
+        with pytest.raises(RuntimeError, match=r"chained LTV scan failed \(code 1"):
+            run()
+    assert not N._CHAIN_WS, "the chain workspaces are dropped after an error"
+    again = run()
+    torch.cuda.synchronize()
+    for a, b in zip(again, good):
+        assert torch.equal(a, b)
+    for buf in N._CHAIN_WS.values():
+        assert int(torch.count_nonzero(buf)) == 0
+
+
+def test_chain_backward_failure_raises_and_recovers(forced_chain_timeouts, monkeypatch):
+    """The chained backward under forced timeouts: the op raises (sync
+    check), and the next backward is bitwise the healthy one."""
+    from nanochat_amd.ops import ltv_hm_fast as F_
+    N, lib = _lib()
+    monkeypatch.setenv("LTV_CHAIN_SYNC_CHECK", "1")
+    B, T, NH, NKVH, D = 2, 3000, 2, 1, 128
+    H = NH + 2 * NKVH
+    values, logits, inits, bias = _fast_inputs(B, T, NH, NKVH, D, seed=13)
+    assert N.chain_workspace_for(values.dtype, values.device, B, T, NH, NKVH, 1, D,
+                                 backward=True).nbytes > 0
+    g = torch.Generator().manual_seed(14)
+    gys = [torch.randn(B, nh, T, D, generator=g).to(torch.bfloat16).to(DEV) for nh in (NH, NKVH, NKVH)]
+    hq, hk, hv = F_.scan_forward(values, logits, inits, bias, NH, NKVH, 1, D, True)
+    Fp = F_.packed_width(H, D, 1)
+    F = H * (D + 1)
+
+    def run():
+        gc = torch.zeros(B, T, Fp, dtype=torch.bfloat16, device=DEV)
+        gi, gb = F_.scan_backward(values, logits, inits, bias, hq, hk, hv, *gys, NH, NKVH, 1, D,
+                                  True, gc)
+        return gc[..., :F], gi, gb
+
+    good = run()
+    forced_chain_timeouts(True)
+    with pytest.raises(RuntimeError, match=r"chained LTV scan failed \(code 1"):
+        run()
+    forced_chain_timeouts(False)
+    again = run()
+    torch.cuda.synchronize()
+    for a, b in zip(again, good):
+        assert torch.equal(a, b)
+    for buf in N._CHAIN_WS.values():
+        assert int(torch.count_nonzero(buf)) == 0
+
+
+def test_chain_late_carries_leave_no_stale_words(forced_chain_timeouts):
+    """Waits bounded at one poll while every chunk still publishes: readers
+    that give up before their carry lands mark the word abandoned, and the
+    late publisher clears it, so the workspace is all zero after every call
+    whether or not a wait ran out; a call whose waits all succeeded is
+    bitwise the healthy result, one with a timeout reports code 1."""
+    N, lib = _lib()
+    B, T, NH, NKVH, Da, r = 1, 8200, 1, 1, 1, 128
+    dtype = torch.bfloat16
+    nbytes = _ws_bytes(dtype, B, T, NH, NKVH, Da, r)
+    assert nbytes > 0
+    c, ini, bias = _random_case(B, T, NH, NKVH, Da, r, seed=15, io="bf16")
+    cd, idv, bd = to_torch(c, dtype, DEV), to_torch(ini, dtype, DEV), to_torch(bias, torch.float32, DEV)
+    ws = _zero_ws(nbytes)
+    good = _forward(cd, idv, bd, NH, NKVH, Da, r, True, ws)
+    torch.cuda.synchronize()
+    assert lib.ltv_chain_take_error() == 0
+    forced_chain_timeouts(1)
+    codes = []
+    for i in range(6):
+        out = _forward(cd, idv, bd, NH, NKVH, Da, r, True, ws)
+        torch.cuda.synchronize()
+        code = lib.ltv_chain_take_error()
+        codes.append(code)
+        assert code in (0, 1), code
+        nz = int(torch.count_nonzero(ws[256:]))
+        assert nz == 0, f"call {i}: {nz} nonzero carry-word bytes (code {code})"
+        assert int(ws.view(torch.int32)[0]) == 0, f"call {i}: ticket counter"
+        if code == 0:
+            for a, b in zip(out, good):
+                assert torch.equal(a, b)
+        ws.zero_()  # the error word (header) after a reported error
+    print(f"error codes with 1-poll waits: {codes}")
