@@ -67,15 +67,19 @@ __device__ __forceinline__ i32x4_t make_buffer_rsrc(const void* p, uint32_t byte
 
 // One wavefront-wide 16-byte-per-lane load into LDS at lds_base (wave-uniform
 // byte address): lane l's chunk goes to lds_base + 16 l.
+// lds_base is bound to M0 as an input operand ("{m0}"), so the compiler
+// writes M0 itself and knows it is read here; nothing clobbers the register
+// it reserves.  The load stays inline asm rather than the
+// buffer-load-to-LDS builtin: with the builtin the compiler cannot tell that
+// a k-step's loads fill the other LDS stage, and waits for all of them
+// (vmcnt(0)) before the first fragment read of the row-contiguous kernels'
+// every k-step.  The nop covers the M0 write -> LDS-DMA hazard.
 __device__ __forceinline__ void dma16(uint32_t lds_base, i32x4_t rsrc, uint32_t voffset,
                                       uint32_t soffset) {
-  asm volatile(
-      "s_mov_b32 m0, %0\n\t"
-      "s_nop 4\n\t"
-      "buffer_load_dwordx4 %1, %2, %3 offen lds"
-      :
-      : "s"(lds_base), "v"(voffset), "s"(rsrc), "s"(soffset)
-      : "memory", "m0");
+  asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
+               :
+               : "v"(voffset), "s"(rsrc), "s"(soffset), "{m0}"(lds_base)
+               : "memory");
 }
 
 template <int N>
