@@ -101,6 +101,26 @@ def profiled_traffic(span: str, summary: str = "d12_traffic.json"):
         return None, None
 
 
+def emit(out: dict) -> None:
+    """Print the result line, after checking that no chained scan of the run
+    reported a failure (the library's error mailbox; raises if one did)."""
+    from nanochat_amd import _native as N
+    N.check_chain_errors()
+    print(json.dumps(out), flush=True)
+
+
+def cpu_model() -> str:
+    """The host CPU's model name (from /proc/cpuinfo), or "unknown"."""
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(seconds_target: float = 10.0, pqk=None):
     """Time the oracle's forward+backward on a sample of the workload (with
     ``pqk``, the look-back scan in place of the full recurrence)."""
@@ -144,6 +164,7 @@ def cpu_baseline(seconds_target: float = 10.0, pqk=None):
         "value": round(Bs * T * reps / el, 1),
         "unit": "tokens/s",
         "cores": cores,
+        "cpu": cpu_model(),
         "kind": "port",
         "sample": f"{reps} x fwd+bwd of {Bs} sequence(s) of the workload "
                   f"(T={T}, C={C}, F={F}{'' if pqk is None else f', look-back {pqk}'}), "
@@ -325,7 +346,7 @@ def main():
         out["config"]["look_back_pqk"] = list(LOOK_BACK_PQK)
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(args.cpu_seconds, LOOK_BACK_PQK if look_back else None)
-    print(json.dumps(out), flush=True)
+    emit(out)
 
 
 # the standalone scan forward, per-element decay
@@ -366,7 +387,7 @@ def scan_fwd_cpu_baseline(seconds_target: float):
                 break
     per_row = scan_fwd_bytes() / SF_B
     return {"value": round(per_row * reps / el / 1e9, 3), "unit": "GB/s", "cores": cores,
-            "kind": "port",
+            "cpu": cpu_model(), "kind": "port",
             "sample": f"{reps} x the scan forward of 1 of the {SF_B} batch rows "
                       f"(18 heads, T={SF_T}, D={SF_D}, r=1), fp32 numpy, {el:.1f} s"}
 
@@ -437,7 +458,7 @@ def scan_fwd_main(args):
     }
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = scan_fwd_cpu_baseline(args.cpu_seconds)
-    print(json.dumps(out), flush=True)
+    emit(out)
 
 
 # long-sequence prefill
@@ -531,7 +552,7 @@ def prefill_main(args):
                      "traffic": traffic, "traffic_source": traffic_src},
         "kernels": kernels,
     }
-    print(json.dumps(out), flush=True)
+    emit(out)
 
 
 # decode
@@ -654,7 +675,7 @@ def decode_main(args):
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4),
                      "traffic": None, "avg_us": round(avg_us, 2), "work_per_launch": nbytes},
     }
-    print(json.dumps(out), flush=True)
+    emit(out)
 
 
 def gpt_main(args):
@@ -721,7 +742,7 @@ def gpt_main(args):
         "filter_share": round(filter_ms / ms_per_step, 4),
         "filter_kernels_us": {k: round(sum(v) / len(v) * 1e3, 2) for k, v in durs.items()},
     }
-    print(json.dumps(out), flush=True)
+    emit(out)
 
 
 if __name__ == "__main__":

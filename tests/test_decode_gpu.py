@@ -205,6 +205,50 @@ def test_decode_config5_vs_full_recompute():
     assert float(err.mean()) <= 0.25 * bound
 
 
+def test_decode_config5_data_dependent_gates_vs_full_recompute():
+    """Config 5's decode with data-dependent gates (gate rows at full scale,
+    bias in [-3.5, -2.5]): B = 64, 256 steps after a 16-token prefill, against
+    the full sequence in one call.  Per step the decode path can differ from
+    the full scan by
+      * the bf16 rounding of the carried state, <= 2^-8 max|h|;
+      * its own projection of the new token, summed in another order than the
+        GEMM's: a value or a logit can round to the neighbouring bf16 (<= 2^-7
+        of it), which moves the step by <= alpha 2^-7 max|u|, and alpha by <=
+        alpha (1 - alpha) 2^-7 |logit| <= 2^-9 |logit| (times |u - h|).
+    Each perturbation then decays by (1 - alpha) per step, so the difference is
+    bounded by the largest perturbation over the smallest alpha seen (the
+    largest decay), plus one bf16 rounding of the output."""
+    from nanochat_amd.ltv.ltv_filter import LtvInitValues
+    from nanochat_amd.ltv_combined_qkv_computer_module import LtvCombinedQkvComputerModule
+    from nanochat_amd.ops import ltv_hm_fast as F_
+    NH, NKVH, D = 6, 6, 128
+    H = NH + 2 * NKVH
+    f = _make_filter(NH, NKVH, D, D, seed=3, gate_scale=1.0, bias=(-3.5, -2.5))
+    m = LtvCombinedQkvComputerModule(0, f)
+    B, T0, N = 64, 16, 256
+    g = torch.Generator().manual_seed(6)
+    xs = torch.randn(B, T0 + N, NH * D, generator=g).to(torch.bfloat16).to(DEV)
+    cache = _Cache()
+    with torch.no_grad():
+        m(xs[:, :T0], cache)
+    dec = _chain(m, xs[:, T0:], cache, fused=True)
+    with torch.no_grad():
+        full = torch.cat(f(xs, LtvInitValues()), dim=2)[:, T0:]
+        vals, logits, _ = F_.project(xs, f.c.weight.detach(), H, D, 1)
+    lg = logits[:, T0:, :H].float()
+    alpha = torch.sigmoid(lg + f.logit_bias.detach().float().view(1, 1, H))
+    a_min, a_max = float(alpha.min()), float(alpha.max())
+    assert a_max - a_min > 0.05, "the gates should vary with the data"
+    umax = float(vals[:, :, T0:].float().abs().max())
+    lmax = float(lg.abs().max())
+    hmax = float(full.float().abs().max())
+    delta = 2.0 ** -8 * hmax + a_max * 2.0 ** -7 * umax + 2.0 ** -9 * lmax * (umax + hmax)
+    bound = delta / a_min + 2.0 ** -8 * hmax
+    err = (dec.float() - full.float()).abs()
+    assert float(err.max()) <= bound, (float(err.max()), bound, a_min)
+    assert float(err.mean()) <= 0.25 * bound, (float(err.mean()), bound)
+
+
 def test_decode_writes_cache_rows_in_place():
     """Through LtvCombinedQkvComputerModule and a KVCache, the fused decode step
     stores the new last rows into the cache's row buffers itself
