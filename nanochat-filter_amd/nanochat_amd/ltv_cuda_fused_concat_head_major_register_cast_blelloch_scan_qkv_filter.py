@@ -93,10 +93,16 @@ class LtvCudaFusedConcatHeadMajorRegisterCastBlellochScanQkvFilter(
         the KV cache's last-row buffers, which may be the previous rows
         themselves) in the same launch.  Returns (q, k, v) as ``forward`` does,
         or None where ``forward`` would not take that path (then nothing is
-        written)."""
+        written).  Also None unless every row buffer is a bf16 tensor on x's
+        device with contiguous channels (stride(-1) == 1), as the kernel
+        stores them: a cache filled by an fp32 prefill, say, then takes the
+        general path and the module's own row update."""
         if (x.size(1) != 1 or torch.is_grad_enabled() or previous_values.q is None
                 or any(t is None for t in rows)
                 or self._compute_dtype(x) != torch.bfloat16):
+            return None
+        if any(t.dtype != torch.bfloat16 or t.device != x.device or t.stride(-1) != 1
+               for t in rows):
             return None
         return self._decode_bf16(x, previous_values, rows)
 

@@ -11,7 +11,9 @@ The fused ``ltv_qkv_decode_step`` is pinned three ways:
   recompute of the whole sequence.  The cache holds bf16 rows, so every decode
   step re-quantises the state that the full scan keeps in fp32; with a constant
   decay a = 1 - alpha the difference is bounded by 2^-9 max|h| / alpha (the
-  bound of the reference's own decode), which the test asserts.
+  bound of the reference's own decode), which the test asserts; with
+  data-dependent gates, by the largest per-step perturbation over the smallest
+  alpha seen.
 """
 
 import numpy as np
@@ -291,3 +293,41 @@ def test_decode_writes_cache_rows_in_place():
     for x, y in zip(rows_a, rows_b):
         assert torch.equal(x, y)
     assert torch.equal(rows_a[0], a[:, -1, :6])
+
+
+def test_decode_into_rows_declines_rows_it_cannot_store():
+    """decode_into_rows takes the fused in-place step only when every row
+    buffer is bf16 on x's device with contiguous channels; for fp32 rows (a
+    cache filled by an fp32 prefill) or channel-strided rows it returns None
+    and writes nothing, so the module runs the general step and its own row
+    update."""
+    from nanochat_amd.ltv.ltv_filter import LtvInitValues
+    NH, NKVH, D = 2, 1, 64
+    f = _make_filter(NH, NKVH, D, D, seed=4)
+    B = 3
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(B, 1, NH * D, generator=g).to(torch.bfloat16).to(DEV)
+
+    def rows(dtype, strided=False):
+        out = []
+        for nh in (NH, NKVH, NKVH):
+            if strided:
+                t = torch.randn(B, nh, 2 * D, generator=g).to(dtype).to(DEV)[..., ::2]
+            else:
+                t = torch.randn(B, nh, D, generator=g).to(dtype).to(DEV)
+            out.append(t)
+        return out
+
+    with torch.no_grad():
+        for bad in (rows(torch.float32), rows(torch.bfloat16, strided=True)):
+            before = [t.clone() for t in bad]
+            prev = LtvInitValues(q=bad[0], k=bad[1], v=bad[2])
+            assert f.decode_into_rows(x, prev, tuple(bad)) is None
+            for t, t0 in zip(bad, before):
+                assert torch.equal(t, t0), "declined call wrote the rows"
+        good = rows(torch.bfloat16)
+        prev = LtvInitValues(q=good[0].clone(), k=good[1].clone(), v=good[2].clone())
+        out = f.decode_into_rows(x, prev, tuple(good))
+        assert out is not None
+        torch.cuda.synchronize()
+        assert torch.equal(out[0][:, 0], good[0])
