@@ -101,6 +101,22 @@ def profiled_traffic(span: str, summary: str = "d12_traffic.json"):
         return None, None
 
 
+def measured_peak(name: str, bound: str):
+    """The box-measured ceiling for a kernel (profiles/peaks.json, written from
+    ``bench.py --workload peaks``): the bf16 MFMA loop with random operands
+    for the GEMMs, the HBM stream of the kernel's read/write mix in the scan's
+    access shape for the scans, the grid-stride copy otherwise; None when the
+    file is absent."""
+    try:
+        with open(os.path.join(ROOT, "profiles", "peaks.json")) as fh:
+            p = json.load(fh)
+    except (OSError, ValueError):
+        return None
+    if bound == "mfma":
+        return p.get("bf16_mfma_tflops")
+    return p.get("stream_gbs", {}).get(name, p.get("hbm_copy_gbs"))
+
+
 def emit(out: dict) -> None:
     """Print the result line, after checking that no chained scan of the run
     reported a failure (the library's error mailbox; raises if one did)."""
@@ -180,7 +196,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--workload",
-                    choices=("filter", "look_back", "gpt", "scan_fwd", "prefill", "decode"),
+                    choices=("filter", "look_back", "gpt", "scan_fwd", "prefill", "decode",
+                             "peaks"),
                     default="filter",
                     help="filter: BASELINE.json configs[2] (the default, the metric's workload); "
                          "look_back: the same shapes through the look-back filter with the d12 "
@@ -189,7 +206,9 @@ def main():
                          "filter in every layer (tokens/s and the filter's share of the step); "
                          "scan_fwd: configs[1], the standalone per-element-decay scan forward "
                          "(GB/s); prefill: configs[4]'s prefill, the filter forward at B=8, "
-                         "T=8192 with decay sigmoid(N(3, 1.5)) (tokens/s)")
+                         "T=8192 with decay sigmoid(N(3, 1.5)) (tokens/s); "
+                         "peaks: the measured roofline peaks (MFMA loop, HBM streams in the "
+                         "scan's access shape, the library GEMM on the projection's shapes)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="after the timed region, run a plain device copy of 256 MiB five times "
                          "(the known-size reference for rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -211,6 +230,9 @@ def main():
         return
     if args.workload == "decode":
         decode_main(args)
+        return
+    if args.workload == "peaks":
+        peaks_main(args)
         return
 
     import torch
@@ -299,16 +321,21 @@ def main():
             ach, peak, unit = amount / (avg * 1e-3) / 1e9, HBM_PEAK_GBS, "GB/s"
         else:
             ach, peak, unit = amount / (avg * 1e-3) / 1e12, BF16_PEAK_TFLOPS, "TFLOP/s"
+        mp = measured_peak(name, bound)
         kernels[name] = {"bound": bound, "avg_us": round(avg * 1e3, 2), "launches": len(ms),
                          "achieved": round(ach, 1), "peak": peak, "unit": unit,
-                         "frac": round(ach / peak, 4), "work_per_launch": amount}
+                         "frac": round(ach / peak, 4), "work_per_launch": amount,
+                         "peak_measured": mp,
+                         "frac_measured": round(ach / mp, 4) if mp else None}
     dominant = max(kernels, key=lambda k: kernels[k]["avg_us"] * kernels[k]["launches"])
     dk_ = kernels[dominant]
     traffic, traffic_src = profiled_traffic(
         dominant, "d12_look_back_traffic.json" if look_back else "d12_traffic.json")
     roofline = {"kernel": dominant, "bound": dk_["bound"], "achieved": dk_["achieved"],
                 "peak": dk_["peak"], "unit": dk_["unit"], "frac": dk_["frac"], "traffic": traffic,
-                "traffic_source": traffic_src}
+                "traffic_source": traffic_src, "peak_measured": dk_["peak_measured"],
+                "frac_measured": dk_["frac_measured"],
+                "peak_measured_source": "profiles/peaks.json"}
     scan_time = kernels.get("scan_fwd", {}).get("avg_us", 0) + kernels.get("scan_bwd", {}).get("avg_us", 0)
     scan_bytes = work["scan_fwd"][1] + work["scan_bwd"][1]
     scan_gbs = scan_bytes / (scan_time * 1e-6) / 1e9 if scan_time else None
@@ -351,6 +378,108 @@ def main():
 
 # the standalone scan forward, per-element decay
 SF_B, SF_H, SF_T, SF_D = 32, 18, 1024, 128
+
+
+# configs[1]'s and the d12 scan's arrays: 1,152 (b, head, 64-channel slab)
+# sequences of T = 1024 steps x 128 bytes, 151 MB per array
+PEAK_SLICES = 1152
+PEAK_SLICE_BYTES = 1024 * 128
+
+
+def peaks_main(args):
+    """Measured peaks on this box, printed as one JSON line (no CPU baseline):
+      * bf16 MFMA: v_mfma_f32_32x32x16_bf16 loop, two wavefronts per SIMD,
+        random operand bits (and all-zero operands: higher clock);
+      * HBM: 16-byte streams over 151 MB arrays -- grid-stride copy, read and
+        write, and the scan's access shape (one contiguous 128 KB slice per
+        workgroup, 1,152 workgroups) with 1, 2 and 3 arrays read and one
+        written;
+      * the library GEMM (torch.matmul, hipBLASLt) on the projection's three
+        shapes, for comparison with this library's kernels.
+    Each figure is the median of ``--steps`` timed launches (HIP events)."""
+    import ctypes
+    import torch
+    from nanochat_amd import _native as N
+
+    lib = ctypes.CDLL(os.path.join(ROOT, "nanochat-filter_amd", "nanochat_amd", "libltv_peaks.so"))
+    lib.ltv_peak_mfma.restype = ctypes.c_int
+    lib.ltv_peak_mfma.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                  ctypes.c_void_p]
+    lib.ltv_peak_stream.restype = ctypes.c_int
+    lib.ltv_peak_stream.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_int,
+                                    ctypes.c_int, ctypes.c_int64, ctypes.c_int64, ctypes.c_int,
+                                    ctypes.c_uint32, ctypes.c_void_p]
+    dev = torch.device("cuda:0")
+    st = N.stream_of(torch.empty(1, device=dev))
+    n_cu = torch.cuda.get_device_properties(dev).multi_processor_count
+    steps = max(3, args.steps)
+
+    def timed(fn):
+        for _ in range(2):
+            fn()
+        ts = []
+        for _ in range(steps):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            fn()
+            b.record()
+            b.synchronize()
+            ts.append(a.elapsed_time(b) * 1e-3)
+        ts.sort()
+        return ts[len(ts) // 2]
+
+    out = {"metric": "measured roofline peaks (bf16 MFMA, HBM streams) on one MI355X",
+           "n_gpus": 1, "steps": steps, "cus": n_cu, "published": {"bf16_mfma_tflops": 2500.0,
+                                                                    "hbm_gbs": 8000.0}}
+    # MFMA
+    blocks, iters = 2 * n_cu, 4096
+    res = torch.empty(blocks * 256, dtype=torch.float32, device=dev)
+    flop = blocks * 4 * iters * 8 * 32768
+    for name, zero in (("bf16_mfma_random", 0), ("bf16_mfma_zero", 1)):
+        t = timed(lambda: N.check(lib.ltv_peak_mfma(res.data_ptr(), blocks, iters, zero, st),
+                                  "ltv_peak_mfma"))
+        out[name] = {"tflops": round(flop / t / 1e12, 1), "us": round(t * 1e6, 1)}
+    # HBM streams
+    nbytes = PEAK_SLICES * PEAK_SLICE_BYTES
+    n16 = nbytes // 16
+    arrs = [torch.empty(nbytes, dtype=torch.uint8, device=dev) for _ in range(4)]
+    for a_ in arrs:
+        a_.random_(0, 256)
+    srcs = (ctypes.c_void_p * 3)(*[a_.data_ptr() for a_ in arrs[:3]])
+    dst = arrs[3].data_ptr()
+
+    def stream(nr, write, nt, slice16, nblocks):
+        t = timed(lambda: N.check(lib.ltv_peak_stream(srcs, nr, dst, write, nt, n16, slice16,
+                                                      nblocks, 0x9e3779b9, st),
+                                  "ltv_peak_stream"))
+        moved = (nr + (1 if write else 0)) * nbytes
+        return {"gbs": round(moved / t / 1e9, 1), "us": round(t * 1e6, 1), "bytes": moved}
+
+    gs = 64 * n_cu  # grid-stride workgroups
+    out["copy_grid_nt"] = stream(1, 1, 1, 0, gs)
+    out["copy_grid"] = stream(1, 1, 0, 0, gs)
+    out["read_grid"] = stream(1, 0, 0, 0, gs)
+    out["write_grid_nt"] = stream(0, 1, 1, 0, gs)
+    sl = PEAK_SLICE_BYTES // 16
+    for nr in (1, 2, 3):
+        out[f"slices_{nr}r1w"] = stream(nr, 1, 0, sl, PEAK_SLICES)
+        out[f"slices_{nr}r1w_nt"] = stream(nr, 1, 1, sl, PEAK_SLICES)
+    del arrs
+    torch.cuda.synchronize()
+    # library GEMM on the projection's shapes (bf16 in, bf16 out)
+    M, Kc, Fp = B * T, C, 2432
+    g = torch.Generator(device=dev).manual_seed(0)
+    shapes = {"gemm_lib_forward": ((M, Kc), (Kc, Fp)),   # x (M, C) . Wp^T (C, Fp)
+              "gemm_lib_grad_x": ((M, Fp), (Fp, Kc)),    # dC (M, Fp) . Wp (Fp, C)
+              "gemm_lib_grad_weight": ((Fp, M), (M, Kc))}  # dC^T (Fp, M) . x (M, C)
+    for name, (sa, sb) in shapes.items():
+        a_ = torch.randn(sa, generator=g, device=dev).to(torch.bfloat16).contiguous()
+        b_ = torch.randn(sb, generator=g, device=dev).to(torch.bfloat16).contiguous()
+        t = timed(lambda: torch.matmul(a_, b_))
+        out[name] = {"tflops": round(2 * M * Kc * F / t / 1e12, 1), "us": round(t * 1e6, 1),
+                     "shape": [list(sa), list(sb)]}
+        del a_, b_
+    emit(out)
 
 
 def scan_fwd_bytes():
@@ -454,7 +583,11 @@ def scan_fwd_main(args):
         "roofline": {"kernel": "scan_fwd", "bound": "hbm", "achieved": round(ach, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4),
                      "traffic": traffic, "traffic_source": traffic_src,
-                     "avg_us": round(avg_us, 2), "work_per_launch": nbytes},
+                     "avg_us": round(avg_us, 2), "work_per_launch": nbytes,
+                     "peak_measured": measured_peak("scan_fwd_r1", "hbm"),
+                     "frac_measured": (round(ach / measured_peak("scan_fwd_r1", "hbm"), 4)
+                                       if measured_peak("scan_fwd_r1", "hbm") else None),
+                     "peak_measured_source": "profiles/peaks.json"},
     }
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = scan_fwd_cpu_baseline(args.cpu_seconds)
@@ -525,9 +658,12 @@ def prefill_main(args):
             ach, peak, unit = amount / (avg * 1e-3) / 1e9, HBM_PEAK_GBS, "GB/s"
         else:
             ach, peak, unit = amount / (avg * 1e-3) / 1e12, BF16_PEAK_TFLOPS, "TFLOP/s"
+        mp = measured_peak(name, bound)
         kernels[name] = {"bound": bound, "avg_us": round(avg * 1e3, 2), "launches": len(ms),
                          "achieved": round(ach, 1), "peak": peak, "unit": unit,
-                         "frac": round(ach / peak, 4), "work_per_launch": amount}
+                         "frac": round(ach / peak, 4), "work_per_launch": amount,
+                         "peak_measured": mp,
+                         "frac_measured": round(ach / mp, 4) if mp else None}
     dominant = max(kernels, key=lambda k: kernels[k]["avg_us"] * kernels[k]["launches"])
     dk_ = kernels[dominant]
     traffic, traffic_src = profiled_traffic(dominant, "prefill_traffic.json")

@@ -3,7 +3,9 @@
     python nanochat-filter_amd/build_lib.py [--jobs N]
 
 Compiles each source under ``csrc/`` with hipcc for gfx950 (in parallel) and
-links them into ``nanochat_amd/libnanochat_filter_amd.so``.  Always rebuilds.
+links them into ``nanochat_amd/libnanochat_filter_amd.so``; the roofline
+microbenchmarks of ``csrc/bench/`` go into ``nanochat_amd/libltv_peaks.so``.
+Always rebuilds.
 """
 
 from __future__ import annotations
@@ -23,6 +25,9 @@ SOURCES = ["ltv_scan_fwd_bf16.hip", "ltv_scan_fwd_f32.hip", "ltv_scan_bwd_bf16.h
            "ltv_scan_bwd_f32.hip", "ltv_scan_abi.hip", "ltv_scan_lb.hip", "ltv_gemm.hip", "ltv_decode.hip",
            "ltv_abi.cpp"]
 ARCH = "gfx950"
+# roofline microbenchmarks for bench.py --workload peaks: a library of their own
+PEAKS_SOURCES = ["bench/ltv_peaks.hip"]
+PEAKS_OUT = os.path.join(HERE, "nanochat_amd", "libltv_peaks.so")
 
 
 def hipcc() -> str:
@@ -54,16 +59,19 @@ def _compile(src: str, obj: str) -> tuple[str, int, str]:
 
 
 def build(jobs: int | None = None, verbose: bool = True) -> str:
+    """Compile and link both libraries; returns the filter library's path."""
     tmp = tempfile.mkdtemp(prefix="ltv_build_")
     try:
-        objs = []
-        jobs = jobs or min(len(SOURCES), os.cpu_count() or 1)
+        targets = [(SOURCES, OUT), (PEAKS_SOURCES, PEAKS_OUT)]
+        objs = {out: [] for _, out in targets}
+        jobs = jobs or min(len(SOURCES) + len(PEAKS_SOURCES), os.cpu_count() or 1)
         with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
             futs = []
-            for src in SOURCES:
-                obj = os.path.join(tmp, os.path.splitext(src)[0] + ".o")
-                objs.append(obj)
-                futs.append(ex.submit(_compile, src, obj))
+            for srcs, out in targets:
+                for src in srcs:
+                    obj = os.path.join(tmp, os.path.splitext(os.path.basename(src))[0] + ".o")
+                    objs[out].append(obj)
+                    futs.append(ex.submit(_compile, src, obj))
             failed = []
             for f in futs:
                 src, rc, err = f.result()
@@ -73,14 +81,16 @@ def build(jobs: int | None = None, verbose: bool = True) -> str:
                     failed.append(src)
             if failed:
                 raise RuntimeError(f"hipcc failed for {failed}")
-        tmp_out = OUT + ".tmp"
-        cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp_out]
-        p = subprocess.run(cmd, capture_output=True, text=True)
-        if p.returncode != 0:
-            raise RuntimeError(f"link failed:\n{p.stdout}\n{p.stderr}")
-        os.replace(tmp_out, OUT)
-        if verbose:
-            print(f"[build] wrote {OUT} ({os.path.getsize(OUT)} bytes)")
+        for _, out in targets:
+            tmp_out = out + ".tmp"
+            cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs[out], "-o",
+                   tmp_out]
+            p = subprocess.run(cmd, capture_output=True, text=True)
+            if p.returncode != 0:
+                raise RuntimeError(f"link failed:\n{p.stdout}\n{p.stderr}")
+            os.replace(tmp_out, out)
+            if verbose:
+                print(f"[build] wrote {out} ({os.path.getsize(out)} bytes)")
         return OUT
     finally:
         shutil.rmtree(tmp, ignore_errors=True)

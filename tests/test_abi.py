@@ -185,3 +185,18 @@ def test_chain_error_mailbox_and_controls_host_side():
     assert "spin_max" in N.last_error()
     assert lib.ltv_chain_set_test_controls(0, 0) == 0
     assert lib.ltv_chain_take_error() == 0
+
+
+def test_peaks_library_exports_its_header():
+    """libltv_peaks.so (bench.py --workload peaks) exports every function
+    include/ltv_peaks.h declares."""
+    from nanochat_amd import _native as N
+    path = os.path.join(os.path.dirname(N.LIB_PATH), "libltv_peaks.so")
+    if not os.path.exists(path):
+        pytest.skip("peaks library not built")
+    src = re.sub(r"/\*.*?\*/", "", open(os.path.join(ROOT, "include", "ltv_peaks.h")).read(),
+                 flags=re.S)
+    names = re.findall(r"^\s*int\s+(ltv_[a-z0-9_]+)\s*\(", src, flags=re.M)
+    assert sorted(names) == ["ltv_peak_mfma", "ltv_peak_stream"]
+    lib = ctypes.CDLL(path)
+    assert all(hasattr(lib, n) for n in names)
