@@ -17,15 +17,23 @@
 // step equals the corresponding step of a full recompute up to fp32
 // summation order in the projection.
 //
-// Work split: one workgroup per (head h, 32-channel block cb).  Its features
-// are the 32 value rows of the block and the 32 packed rows starting at the
-// block's first gate row (every gate the block's channels use; r >= 1 means at
-// most 32).  Sixteen wavefronts: wave w computes, over k slice w / 4 of the
-// reduction, the 32 x 32 MFMA block of feature block (w & 1) and token block
-// ((w >> 1) & 1) + 2 i, i = 0, 1, ..., with operand fragments loaded straight
-// from global memory (the weight slice is read once per workgroup; tokens come
-// from L2).  The partial blocks go through LDS, are summed in a fixed order and
-// feed the recurrence step, which writes 32 consecutive channels per token.
+// Work split: one workgroup per (head h, 16-channel block cb, 32-token block
+// tb).  Its 32 MFMA rows are the block's 16 value rows and, from row 16, the
+// gate rows its channels use (channels c0 .. c0 + 15 use gates c0 / r ..
+// (c0 + 15) / r: at most 16), so one 32 x 32 block covers values and gates.
+// Six wavefronts, each a sixth of the reduction (8 k16 steps at C = 768: 256
+// contiguous bytes of every row), load all their operand fragments straight
+// from global memory in one batch, then run their MFMAs; the partial blocks
+// are summed through LDS in a fixed order and feed the recurrence step, one
+// thread per (token, channel).  The step is latency-bound (7,000 MFMAs and
+// 4 MB of weight at d12, B = 64).  Measured on MI355X (d12, B = 64, kernel
+// durations): the earlier (head, 32 channels) split with 72 workgroups 13.2
+// us; this split with 16 wavefronts of 3 k16 steps 9.8 us, with 12 of 4 8.6
+// us, with 6 of 8 7.9 us -- a fragment load touches one 32-byte piece of 32
+// rows, and the longer a wavefront's stretch of each row, the more of those
+// pieces the L1 merges into one L2 request.  The same kernel with no operand
+// loads or MFMAs takes 5.1 us (an empty launch 1.4 us): the floor of a launch
+// that loads, reduces and stores.
 #include "ltv_abi_internal.hpp"
 #include "ltv_device.hpp"
 #include "ltv_gemm_mfma.hpp"
@@ -44,8 +52,8 @@ struct DecodeArgs {
   // optional second copy of the new rows of q, k, v: (B, H_g, D), strides
   // (b, h), d = 1 (null: none).  May be the previous rows themselves: every
   // element of prev is read, before it is written, by the thread that writes
-  // it (one workgroup per (head, 32 channels), and in it one thread per
-  // (token, channel) for the read and the store alike).
+  // it (one workgroup per (head, 16 channels, 32 tokens), and in it one thread
+  // per (token, channel) for the read and the store alike).
   bf16_t* rows[3];
   int64_t rows_s[3][2];
   int B, C, NH, NKVH, D, Da, r, Fp, use_sigmoid;
@@ -60,28 +68,27 @@ __device__ __forceinline__ bf16x8_t load_frag(const bf16_t* row, bool ok) {
   return __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(row));
 }
 
-constexpr int kDecKSlices = 4;  // the reduction split across wavefronts
-constexpr int kDecThreads = 2 * 2 * kDecKSlices * 64;
-constexpr int kDecBatch = 8;
+constexpr int kDecCh = 16;       // channels per workgroup
+constexpr int kDecKSlices = 6;   // wavefronts: slices of the reduction
+constexpr int kDecThreads = kDecKSlices * 64;
+constexpr int kDecBatch = 8;     // k16 steps whose loads are in flight together
 
 __global__ void __launch_bounds__(kDecThreads) qkv_decode_kernel(const DecodeArgs a) {
-  // [k slice][token block slot][feature block][feature][token]
-  __shared__ float lds_p[kDecKSlices][2][2][32][33];
+  // [k slice][row: 16 values, then 16 gates][token]
+  __shared__ float lds_p[kDecKSlices][32][33];
 
   const int H = a.NH + 2 * a.NKVH;
-  const int nblk = (a.D + 31) / 32;
-  const int h = blockIdx.x / nblk, cb = blockIdx.x % nblk;
+  const int nblk = (a.D + kDecCh - 1) / kDecCh;
+  const int ntb = (a.B + 31) / 32;
+  const int tb = blockIdx.x % ntb;
+  const int hc = blockIdx.x / ntb;
+  const int h = hc / nblk, cb = hc % nblk;
   const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int fb = wave & 1;    // 0: value rows, 1: gate rows
-  const int tslot = (wave >> 1) & 1;
-  const int ks = wave >> 2;   // k slice
+  const int ks = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // k slice
 
-  const int c0 = cb * 32;
+  const int c0 = cb * kDecCh;
   const int j0 = c0 / a.r;
-  const int nrow0 = fb == 0 ? h * a.D + c0 : H * a.D + h * a.Da + j0;
-  // valid feature rows of this wave's block
-  const int nrows = fb == 0 ? min(32, a.D - c0) : min(32, a.Da - j0);
+  const int ngate = (min(c0 + kDecCh, a.D) - 1) / a.r - j0 + 1;  // <= 16
 
   int g, hl;
   if (h < a.NH) {
@@ -102,87 +109,78 @@ __global__ void __launch_bounds__(kDecThreads) qkv_decode_kernel(const DecodeArg
   const int64_t rsb = a.rows_s[g][0];
   if (rowsp != nullptr) rowsp += (int64_t)hl * a.rows_s[g][1];
 
+  // the recurrence step's inputs other than the projection, loaded first so
+  // their latency overlaps the MFMA phase: item it -> (token it / 16, channel
+  // it % 16), kDecItems items per thread
+  constexpr int kDecItems = (32 * kDecCh + kDecThreads - 1) / kDecThreads;
+  float hp[kDecItems], bias[kDecItems];
+#pragma unroll
+  for (int q = 0; q < kDecItems; ++q) {
+    const int it = threadIdx.x + q * kDecThreads;
+    const int it_m = it / kDecCh, m_out = tb * 32 + it_m, ch_out = c0 + it % kDecCh;
+    const bool out_ok = it_m < 32 && m_out < a.B && ch_out < a.D;
+    hp[q] = out_ok ? bf16_to_f32(prevp[(int64_t)m_out * psb + ch_out]) : 0.0f;
+    bias[q] = out_ok ? a.bias[h * a.Da + ch_out / a.r] : 0.0f;
+  }
+
+  // MFMA phase: row ri of the block, k offset kh within each k16 step
+  const int ri = lane & 31, kh = 8 * (lane >> 5);
+  const bool vrow = ri < kDecCh;
+  const bool row_ok = vrow ? c0 + ri < a.D : ri - kDecCh < ngate;
+  const int64_t nrow = vrow ? (int64_t)h * a.D + c0 + ri
+                            : (int64_t)H * a.D + (int64_t)h * a.Da + j0 + (ri - kDecCh);
+  const bf16_t* wrow = a.wp + (row_ok ? nrow : 0) * a.C + kh;
+  const int m = tb * 32 + ri;
+  const bool tok_ok = m < a.B;
+  const bf16_t* xrow = a.x + (int64_t)(tok_ok ? m : 0) * a.xs + kh;
   const int nk = a.C / 16;
   const int per = (nk + kDecKSlices - 1) / kDecKSlices;
   const int kb = ks * per, ke = min(nk, kb + per);
-  const int ntb = (a.B + 31) / 32;
-  const int ri = lane & 31, kh = 8 * (lane >> 5);
-  const bool row_ok = ri < nrows;
-  const bf16_t* wrow = a.wp + (int64_t)(nrow0 + ri) * a.C + kh;
+  f32x16_t acc;
+#pragma unroll
+  for (int v = 0; v < 16; ++v) acc[v] = 0.0f;
+  for (int k0 = kb; k0 < ke; k0 += kDecBatch) {
+    bf16x8_t wf[kDecBatch], xf[kDecBatch];
+#pragma unroll
+    for (int i = 0; i < kDecBatch; ++i) {
+      const bool kok = k0 + i < ke;
+      wf[i] = load_frag(wrow + 16 * (k0 + i), row_ok && kok);
+      xf[i] = load_frag(xrow + 16 * (k0 + i), tok_ok && kok);
+    }
+#pragma unroll
+    for (int i = 0; i < kDecBatch; ++i)
+      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[i], xf[i], acc, 0, 0, 0);
+  }
+  // acc[4 q + e] = partial comb(row 8 q + 4 (lane / 32) + e, token lane % 32)
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) lds_p[ks][8 * q + 4 * (lane >> 5) + e][ri] = acc[4 * q + e];
+  __syncthreads();
 
-  const float* bias_h = a.bias + h * a.Da;
-  for (int tb0 = 0; tb0 < ntb; tb0 += 2) {
-    // the recurrence step's inputs other than the projection, loaded first so
-    // their latency overlaps the MFMA phase: thread -> (slot, token, channel)
-    constexpr int kItems = 2 * 32 * 32 / kDecThreads;
-    float hp_pre[kItems], bias_pre[kItems];
+  // recurrence step: the k slices summed in a fixed order, then rounded to
+  // bf16 as the projection stores the values and logits
 #pragma unroll
-    for (int q = 0; q < kItems; ++q) {
-      const int it = threadIdx.x + q * kDecThreads;
-      const int c = it & 31, mi = (it >> 5) & 31, s = it >> 10;
-      const int m = (tb0 + s) * 32 + mi, ch = c0 + c;
-      const bool ok = tb0 + s < ntb && m < a.B && ch < a.D;
-      hp_pre[q] = ok ? bf16_to_f32(prevp[(int64_t)m * psb + ch]) : 0.0f;
-      bias_pre[q] = ok ? bias_h[min(ch, a.D - 1) / a.r] : 0.0f;
-    }
-    const int tb = tb0 + tslot;
-    if (tb < ntb) {
-      const int m = tb * 32 + ri;
-      const bool tok_ok = m < a.B;
-      const bf16_t* xrow = a.x + (int64_t)m * a.xs + kh;
-      f32x16_t acc;
+  for (int q = 0; q < kDecItems; ++q) {
+    const int it = threadIdx.x + q * kDecThreads;
+    const int it_c = it % kDecCh, it_m = it / kDecCh;
+    const int m_out = tb * 32 + it_m, ch_out = c0 + it_c;
+    if (it_m < 32 && m_out < a.B && ch_out < a.D) {
+      const int jl = ch_out / a.r - j0;
+      float u = 0.0f, z = 0.0f;
 #pragma unroll
-      for (int v = 0; v < 16; ++v) acc[v] = 0.0f;
-      // batches of kDecBatch k16 steps: all of a batch's fragment loads are
-      // issued before its MFMAs
-      for (int k0 = kb; k0 < ke; k0 += kDecBatch) {
-        bf16x8_t wf[kDecBatch], xf[kDecBatch];
-#pragma unroll
-        for (int i = 0; i < kDecBatch; ++i) {
-          const bool kok = k0 + i < ke;
-          wf[i] = load_frag(wrow + 16 * (k0 + i), row_ok && kok);
-          xf[i] = load_frag(xrow + 16 * (k0 + i), tok_ok && kok);
-        }
-#pragma unroll
-        for (int i = 0; i < kDecBatch; ++i)
-          acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[i], xf[i], acc, 0, 0, 0);
+      for (int s = 0; s < kDecKSlices; ++s) {
+        u += lds_p[s][it_c][it_m];
+        z += lds_p[s][kDecCh + jl][it_m];
       }
-      // acc[4 q + e] = partial comb(feature 8 q + 4 (lane / 32) + e, token lane % 32)
-#pragma unroll
-      for (int q = 0; q < 4; ++q)
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          lds_p[ks][tslot][fb][8 * q + 4 * (lane >> 5) + e][ri] = acc[4 * q + e];
+      u = bf16_round_f32(u);
+      z = bf16_round_f32(z) + bias[q];
+      const float alpha = gate_alpha(z, a.use_sigmoid != 0);
+      const float hn = fmaf(alpha, u - hp[q], hp[q]);
+      const bf16_t hb = (bf16_t)f32_to_bf16_bits(hn);
+      a.out[((int64_t)m_out * H + h) * a.D + ch_out] = hb;
+      if (rowsp != nullptr) rowsp[(int64_t)m_out * rsb + ch_out] = hb;
     }
-    __syncthreads();
-    // recurrence step: thread -> (token block slot, token, channel), channels
-    // fastest; the k slices are summed in a fixed order, then rounded to bf16
-    // as the projection stores the values and logits
-#pragma unroll
-    for (int q = 0; q < kItems; ++q) {
-      const int it = threadIdx.x + q * kDecThreads;
-      const int c = it & 31, mi = (it >> 5) & 31, s = it >> 10;
-      const int tbs = tb0 + s;
-      const int m = tbs * 32 + mi, ch = c0 + c;
-      if (tbs < ntb && m < a.B && ch < a.D) {
-        const int jl = ch / a.r - j0;
-        float u = 0.0f, z = 0.0f;
-#pragma unroll
-        for (int q = 0; q < kDecKSlices; ++q) {
-          u += lds_p[q][s][0][c][mi];
-          z += lds_p[q][s][1][jl][mi];
-        }
-        u = bf16_round_f32(u);
-        z = bf16_round_f32(z) + bias_pre[q];
-        const float alpha = gate_alpha(z, a.use_sigmoid != 0);
-        const float hp = hp_pre[q];
-        const float hn = fmaf(alpha, u - hp, hp);
-        const bf16_t hb = (bf16_t)f32_to_bf16_bits(hn);
-        a.out[((int64_t)m * H + h) * a.D + ch] = hb;
-        if (rowsp != nullptr) rowsp[(int64_t)m * rsb + ch] = hb;
-      }
-    }
-    __syncthreads();
   }
 }
 
@@ -244,7 +242,9 @@ int decode_step_impl(const void* x, int64_t x_row_stride, const void* wpack, con
   a.r = D / Da;
   a.Fp = Fp;
   a.use_sigmoid = use_sigmoid;
-  const int grid = H * ((D + 31) / 32);
+  const int64_t grid64 = (int64_t)H * ((D + kDecCh - 1) / kDecCh) * ((B + 31) / 32);
+  LTV_REQUIRE(grid64 < (1ll << 31), LTV_ERR_UNSUPPORTED, "decode grid too large");
+  const int grid = (int)grid64;
   hipLaunchKernelGGL(qkv_decode_kernel, dim3(grid), dim3(kDecThreads), 0, (hipStream_t)stream, a);
   LTV_LAUNCH_CHECK();
   return LTV_OK;
