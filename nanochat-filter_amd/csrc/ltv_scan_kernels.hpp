@@ -1104,7 +1104,8 @@ scan_fwd_chain_kernel(const FwdArgs args, const ChainArgs ch) {
 
   // the chain step: wavefront 0, lane j = slab channel j, takes the entering
   // state, publishes the leaving one and hands the entering one to the others
-  unsigned long long* pub_word = nullptr;
+  // the published word's previous value (wavefront 0, chunks before the
+  // last); its address is recomputed at the end, so only the value stays live
   unsigned long long pub_prev = 0ull;
   if (w == 0 && lane < NCH) {
     const int j = lane;
@@ -1121,8 +1122,8 @@ scan_fwd_chain_kernel(const FwdArgs args, const ChainArgs ch) {
 #pragma unroll
       for (int ww = 0; ww < NW; ++ww)
         p = fmaf(lds_a[ww][j / V][GL ? 0 : j % V], p, xa[ww * NCH + j]);
-      pub_word = ch.words + ((int64_t)seq * (ch.nchunk - 1) + chunk) * NCH + j;
-      pub_prev = chain_publish(pub_word, p, ch.ctl);
+      pub_prev =
+          chain_publish(ch.words + ((int64_t)seq * (ch.nchunk - 1) + chunk) * NCH + j, p, ch.ctl);
     }
     lds_c[j] = cin;
   }
@@ -1166,7 +1167,9 @@ scan_fwd_chain_kernel(const FwdArgs args, const ChainArgs ch) {
     bst_vec<TIO, VEC, GM == GATE_CHANVEC ? kStStream : kStNormal>(
         orr, ooff + s * ostb, oscb, nvalid, active && (t0 + s) < T, hv);
   }
-  if (pub_word != nullptr) chain_clear_abandoned(pub_word, pub_prev);
+  if (w == 0 && lane < NCH && chunk + 1 < ch.nchunk)
+    chain_clear_abandoned(ch.words + ((int64_t)seq * (ch.nchunk - 1) + chunk) * NCH + lane,
+                          pub_prev);
 }
 
 // ---------------------------------------------------------------------------
@@ -1421,9 +1424,8 @@ scan_bwd_kernel(const BwdArgs args) {
 #pragma unroll
   for (int v = 0; v < V; ++v) dinit_v[v] = 0.0f;
 
-  // the chained mode's published word and its previous value (cleared at the
-  // end if the reader gave up)
-  unsigned long long* pub_word = nullptr;
+  // the chained mode's published word's previous value (the word is cleared at
+  // the end if its reader gave up; its address is recomputed there)
   unsigned long long pub_prev = 0ull;
   auto process_tile = [&](int it, auto bufc) {
     constexpr int buf = decltype(bufc)::value;
@@ -1530,8 +1532,8 @@ scan_bwd_kernel(const BwdArgs args) {
 #pragma unroll
               for (int ww = NW - 1; ww >= 0; --ww)
                 p = fmaf(lds_ba[par][ww][jl][GL ? 0 : jv], p, xb[(ww * CL + jl) * V + jv]);
-              pub_word = args.ch_words + (row + chunk - 1) * NCH + j;
-              pub_prev = chain_publish(pub_word, p, args.ch_ctl);
+              pub_prev = chain_publish(args.ch_words + (row + chunk - 1) * NCH + j, p,
+                                       args.ch_ctl);
             }
           }
           lds_cin[j] = cin;
@@ -1746,7 +1748,10 @@ scan_bwd_kernel(const BwdArgs args) {
     args.dbias_partial[((int64_t)bh * args.nchunk + chunk) * S.Da + j] = acc;
   }
   if constexpr (CHAIN) {
-    if (pub_word != nullptr) chain_clear_abandoned(pub_word, pub_prev);
+    if (threadIdx.x < NCH && (int)threadIdx.x < S.D && chunk > 0)
+      chain_clear_abandoned(
+          args.ch_words + ((int64_t)bh * (args.nchunk - 1) + chunk - 1) * NCH + threadIdx.x,
+          pub_prev);
   }
 }
 
