@@ -427,8 +427,10 @@ constexpr int kFwdChainMinChunks = 8;
 // Error mailbox of the chained kernels: one mapped, pinned host word that a
 // failing launch stores its code into (ChainCtl::host_err), read and cleared
 // by ltv_chain_take_error without synchronising the device.  Allocated once,
-// on the first chained launch; if the allocation fails the kernels report
-// into the workspace header only.
+// on the first chained launch made outside stream capture (an allocation
+// during capture could invalidate the capture; such launches report into the
+// workspace header only); if the allocation fails the kernels report into the
+// workspace header only.
 struct ChainHost {
   std::mutex mu;
   bool tried = false;
@@ -442,9 +444,15 @@ ChainHost& chain_host() {
   return h;
 }
 
-ChainCtl chain_ctl() {
+ChainCtl chain_ctl(hipStream_t st) {
   ChainHost& h = chain_host();
   std::lock_guard<std::mutex> lk(h.mu);
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (!h.tried && (hipStreamIsCapturing(st, &cs) != hipSuccess ||
+                   cs != hipStreamCaptureStatusNone)) {
+    (void)hipGetLastError();
+    return ChainCtl{nullptr, h.spin_max, h.no_publish};
+  }
   if (!h.tried) {
     h.tried = true;
     void* p = nullptr;
@@ -638,7 +646,7 @@ int scan_forward_impl(int dtype, const HostView4& u, const HostView4& lg, const 
       LTV_REQUIRE(pl.nseq * pl.nchunk < (1ll << 31), LTV_ERR_UNSUPPORTED, "grid too large");
       ch.nseq = (int)pl.nseq;
       ch.nchunk = pl.nchunk;
-      ch.ctl = chain_ctl();
+      ch.ctl = chain_ctl(st);
       return scan_launch_fwd_chain(dtype == LTV_DTYPE_BF16, a, ch, pl.cfg, pl.gm, st);
     }
   }
@@ -1008,7 +1016,7 @@ int scan_backward_impl(int dtype, const HostView4& u, const HostView4& lg, const
       a.ch_err = reinterpret_cast<uint32_t*>(chain_ws) + 1;
       a.ch_words = reinterpret_cast<unsigned long long*>(reinterpret_cast<char*>(chain_ws) +
                                                          kChainHeader);
-      a.ch_ctl = chain_ctl();
+      a.ch_ctl = chain_ctl(st);
       rc = scan_launch_bwd_chain(dtype == LTV_DTYPE_BF16, a, pl.cfg, (int)grid, gm, st);
       if (rc) return rc;
       return scan_launch_dbias_reduce(a.dbias_partial, dbias, B, H, a.nchunk, Da, st, ds, pz);
