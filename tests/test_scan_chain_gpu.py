@@ -780,3 +780,68 @@ def test_chain_late_carries_leave_no_stale_words(forced_chain_timeouts):
                 assert torch.equal(a, b)
         ws.zero_()  # the error word (header) after a reported error
     print(f"error codes with 1-poll waits: {codes}")
+
+
+_CAPTURE_FIRST = r"""
+import sys
+import torch
+from nanochat_amd import _native as N
+from nanochat_amd.ops import ltv_hm_fast as F_
+
+B, T, NH, NKVH, D = 2, 4100, 1, 1, 128
+H = NH + 2 * NKVH
+g = torch.Generator().manual_seed(16)
+values = torch.randn(B, H, T, D, generator=g).to(torch.bfloat16).cuda()
+logits = (-(2.0 + torch.randn(B, T, H, generator=g))).to(torch.bfloat16).cuda()
+inits = torch.randn(B, H, D, generator=g).to(torch.bfloat16).cuda()
+bias = torch.zeros(H, 1, device="cuda")
+run = lambda: F_.scan_forward(values, logits, inits, bias, NH, NKVH, 1, D, True)
+assert N.chain_workspace_for(values.dtype, values.device, B, T, NH, NKVH, 1, D).nbytes > 0
+torch.cuda.synchronize()
+graph = torch.cuda.CUDAGraph()
+with torch.cuda.graph(graph):  # the process's first chained launch
+    outs = run()
+print("captured", flush=True)
+for o in outs:
+    o.fill_(0)
+graph.replay()
+torch.cuda.synchronize()
+eager = run()
+torch.cuda.synchronize()
+for a, b in zip(outs, eager):
+    assert torch.equal(a, b), "replay differs from eager"
+assert N.lib().ltv_chain_take_error() == 0
+# the eager launch allocated the mailbox: a forced failure now reaches it
+N.check(N.lib().ltv_chain_set_test_controls(16, 1), "controls")
+try:
+    run()
+except RuntimeError as e:
+    assert "code 1" in str(e), e
+else:
+    sys.exit("a forced chain failure after capture was not reported")
+N.check(N.lib().ltv_chain_set_test_controls(0, 0), "controls")
+again = run()
+torch.cuda.synchronize()
+for a, b in zip(again, eager):
+    assert torch.equal(a, b), "recovery differs from eager"
+print("capture-first ok", flush=True)
+"""
+
+
+def test_chain_first_launch_under_capture():
+    """In a fresh process whose first chained launch is made under HIP graph
+    capture (no eager warm-up): the capture succeeds (the library does not
+    allocate its error mailbox then), a replay equals the eager result, and
+    the first eager launch afterwards sets the mailbox up, so a forced
+    failure is reported through it."""
+    import os
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    env = dict(os.environ, LTV_CHAIN_SYNC_CHECK="1",
+               PYTHONPATH=os.pathsep.join([os.path.join(root, "nanochat-filter_amd"), root,
+                                           os.environ.get("PYTHONPATH", "")]))
+    p = subprocess.run([sys.executable, "-c", _CAPTURE_FIRST], env=env, capture_output=True,
+                       text=True, timeout=100)
+    assert p.returncode == 0, f"rc={p.returncode}\n{p.stdout}\n{p.stderr[-3000:]}"
+    assert "capture-first ok" in p.stdout
