@@ -45,7 +45,7 @@ extern "C" {
 #define LTV_ERR_HIP 3
 #define LTV_ERR_WORKSPACE 4
 
-/* Version of this ABI (bumped on any signature change or addition): 9. */
+/* Version of this ABI (bumped on any signature change or addition): 10. */
 int ltv_abi_version(void);
 
 /* Message of the last failing call on this host thread ("" if none). */
@@ -138,6 +138,19 @@ int ltv_chain_take_error(void);
  * normally.  Applies to launches made after the call.  No reference
  * counterpart. */
 int ltv_chain_set_test_controls(int spin_max, int no_publish);
+
+/* Windows per lane of the short-window look-back backward (the kernel behind
+ * ltv_hm_look_back_scan_backward[_split] for windows with a warm-up of at most
+ * 8 steps shorter than P and Q).  With wpl > 1 a lane walks wpl consecutive
+ * windows last to first and hands each one's chain value and warm-up to the
+ * window before it, so u and the upstream gradients are read once per step;
+ * the results are bitwise those of wpl = 1.  0 (the default) picks the
+ * smallest wpl whose wavefronts fit one round of the device.  A tuning and
+ * test control, applied to launches made after the call (overrides
+ * LTV_SCAN_LB_WPL); returns LTV_ERR_INVALID_ARG for wpl < 0.  No reference
+ * counterpart (the reference's look-back kernels take no such parameter:
+ * cpp_ewma/src/ltv_look_back_fused_concat_head_major_register_cast_blelloch_scan_cuda_backward.cu). */
+int ltv_lb_set_windows_per_lane(int wpl);
 
 /* Workspace bytes needed by ltv_hm_scan_backward / ltv_hm_scan_backward_split. */
 size_t ltv_hm_scan_backward_workspace_size(int dtype, int B, int T, int NH, int NKVH, int Da,

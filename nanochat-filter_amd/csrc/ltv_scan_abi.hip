@@ -4,6 +4,7 @@
 #include <stdlib.h>
 
 #include <algorithm>
+#include <atomic>
 #include <mutex>
 
 #include "ltv_scan_launch.hpp"
@@ -284,8 +285,11 @@ struct ScanTuning {
   int bwd_chain_l = 0, bwd_chain_nw = 0;
   bool bwd_chain = true;
   bool lb_short = true;  // LTV_SCAN_LB_SHORT=0: look-back windows through the tile kernels
+  // LTV_SCAN_LB_WPL=n: windows per lane of the short-window backward (0 = automatic)
+  int lb_wpl = 0;
   ScanTuning() {
     if (const char* e = getenv("LTV_SCAN_LB_SHORT")) lb_short = atoi(e) != 0;
+    if (const char* e = getenv("LTV_SCAN_LB_WPL")) lb_wpl = atoi(e) > 0 ? atoi(e) : 0;
     if (const char* e = getenv("LTV_SCAN_BWD_CHUNKS")) bwd_chunks = atoi(e) > 0 ? atoi(e) : 0;
     if (const char* e = getenv("LTV_SCAN_FWD_CFG")) {
       if (sscanf(e, "%d,%d,%d", &fwd_cl, &fwd_l, &fwd_nw) != 3) fwd_cl = fwd_l = fwd_nw = 0;
@@ -311,6 +315,24 @@ struct ScanTuning {
 const ScanTuning& tuning() {
   static const ScanTuning t;
   return t;
+}
+
+// ltv_lb_set_windows_per_lane: 0 = LTV_SCAN_LB_WPL or automatic
+std::atomic<int> g_lb_wpl{0};
+
+// Compute units of the current device (cached per device).
+int scan_cu_count() {
+  static int counts[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (counts[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        n <= 0)
+      n = 256;
+    counts[dev] = n;
+  }
+  return counts[dev];
 }
 
 int check_shape(int dtype, int B, int T, int NH, int NKVH, int Da, int r) {
@@ -843,6 +865,7 @@ int scan_backward_impl(int dtype, const HostView4& u, const HostView4& lg, const
   a.init_f32 = init_f32 ? 1 : 0;
   a.dinit_ws = nullptr;
   a.bias = bias;
+  a.wpl = 1;
   const int E = dtype == LTV_DTYPE_BF16 ? 2 : 4;
   if ((rc = check_tile_offsets("values", u.s, D, E)) || (rc = check_tile_offsets("logits", lg.s, D, E)) ||
       (rc = check_tile_offsets("grad values", du.s, D, E)) ||
@@ -939,6 +962,22 @@ int scan_backward_impl(int dtype, const HostView4& u, const HostView4& lg, const
       if ((i == 0 ? NH : NKVH) > 0)
         buf = buf && view_span_bytes(hs[i], 1, 1, T, D, E) <= kBufSpanMax &&
               view_span_bytes(gs[i], 1, 1, T, D, E) <= kBufSpanMax;
+    // Several consecutive windows per lane, each handing its chain value and
+    // warm-up to the window before it (u and gy then read once per step), as
+    // long as about 1.5 rounds of resident wavefronts remain (two workgroups
+    // of four per CU: the kernel's 64 KB of LDS).  The kernel is bound by its
+    // load latency more than by its bytes: measured at the d12 look-back shape
+    // (B = 32, 9,216 wavefronts with one window each), 1 / 3 / 5 windows per
+    // lane read 680 / 555 / 519 MB, and the backward with its two reduction
+    // launches takes 178 / 171 / 194 us.
+    if (buf && K - 1 <= 8 && K - 1 < Q && K - 1 < P) {
+      const int64_t waves1 = (int64_t)B * H * (((int64_t)nwin * a.lanes + 63) / 64);
+      const int64_t slots = (int64_t)scan_cu_count() * 8;
+      int64_t w = waves1 * 2 / (3 * slots);
+      if (tuning().lb_wpl > 0) w = tuning().lb_wpl;
+      if (g_lb_wpl.load(std::memory_order_relaxed) > 0) w = g_lb_wpl.load(std::memory_order_relaxed);
+      a.wpl = (int)std::max<int64_t>(1, std::min<int64_t>(w, nwin));
+    }
     rc = scan_launch_lb_short_bwd(bf16, a, vec, sgm, K - 1, buf, st);
     if (rc) return rc;
     rc = scan_launch_lb_dinit(bf16, a, st);
@@ -1282,6 +1321,12 @@ extern "C" int ltv_chain_take_error(void) {
   std::lock_guard<std::mutex> lk(h.mu);
   if (h.host == nullptr) return 0;
   return (int)__atomic_exchange_n(h.host, 0u, __ATOMIC_SEQ_CST);
+}
+
+extern "C" int ltv_lb_set_windows_per_lane(int wpl) {
+  LTV_REQUIRE(wpl >= 0, LTV_ERR_INVALID_ARG, "wpl must be >= 0 (got %d)", wpl);
+  ltv::g_lb_wpl.store(wpl, std::memory_order_relaxed);
+  return LTV_OK;
 }
 
 extern "C" int ltv_chain_set_test_controls(int spin_max, int no_publish) {

@@ -176,6 +176,7 @@ struct BwdArgs {
   float* wdl;
   float* wdi;
   int lanes;  // short-window kernel: lanes per window (a power of two >= D / V)
+  int wpl;    // short-window backward: consecutive windows per lane (1: one each)
   // Chained mode of the tile kernel (one tile per chunk, chunks of a sequence
   // handed their gradient carry through tagged words): the ticket counter, the
   // error word and the words, (B H, nchunk - 1, CL V) -- the same zeroed

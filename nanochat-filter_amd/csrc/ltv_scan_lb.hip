@@ -944,6 +944,442 @@ __global__ void __launch_bounds__(256) scan_lb_buf_bwd_kernel(const BwdArgs args
   }
 }
 
+// Several consecutive windows per lane (args.wpl), walked last to first.  The
+// window a lane processes before window o is o + 1, so what o needs from its
+// successor is already in the lane instead of being recomputed from memory:
+//   G, a_hi -- o + 1's own chain at its first step and 1 - alpha there: o + 1's
+//              g1 and an when its walk ends;
+//   HN, u   -- o + 1's warm-up states and inputs on [lo', st') = o's tail,
+//              formed by o + 1's own warm-up pass and kept in this lane's LDS
+//              slot until o's tail pass reads them.
+// So u and gy are read once per step; only a lane's first window (the last of
+// its group) recomputes its successor's G and warm-up from memory, as the
+// one-window kernel does for every window.  Per window:
+//   (B1) the tail [lo', st') in reverse, u and HN from the slot;
+//   (A)  the own warm-up [lo, st): the state entering st, prod (1 - alpha), and
+//        the states and u the next window in the lane needs (into the slot);
+//   (B2) [st, lo') in reverse.
+// The outputs are those of scan_lb_buf_bwd_kernel, element for element (the
+// same operations in the same order).  Requires K - 1 < min(P, Q), so a tail
+// never holds st, and KW <= 8 (the slot).
+template <typename TIO, int GM, bool VEC, int KW>
+__global__ void __launch_bounds__(256, 2) scan_lb_buf_bwd_multi_kernel(const BwdArgs args) {
+  constexpr int V = Pack<TIO>::V;
+  constexpr int NA = GM == GATE_LANE ? 1 : V;
+  constexpr bool GL = GM == GATE_LANE;
+  constexpr int NB = bwd_batch<GM>();
+  constexpr int NBW = KW / NB;
+  constexpr int E = sizeof(TIO);
+  static_assert(KW % NB == 0 && KW <= 8, "warm-up rows in whole batches, at most 8");
+  using B0 = std::integral_constant<int, 0>;
+  using B1 = std::integral_constant<int, 1>;
+  const ScanShape& S = args.sh;
+  const int nwin = args.nchunk;
+  const int wpl = args.wpl;
+  const int ngrp = (nwin + wpl - 1) / wpl;
+  const LaneMap m = lane_map_bh(args.lanes, ngrp);  // m.win: the lane's group of windows
+  const int bhu = __builtin_amdgcn_readfirstlane(
+      (int)(m.bh < (int64_t)S.B * S.H ? m.bh : (int64_t)S.B * S.H));
+  const bool in_grid = bhu < S.B * S.H;
+  const int bhc = in_grid ? bhu : 0;
+  const int h = bhc % S.H, b = bhc / S.H;
+  const int c0 = m.cv * V;
+  const int nvalid = min(V, S.D - c0);
+  const bool lane_ok = in_grid && m.win < ngrp && nvalid > 0;
+  const int gl = GL ? S.r / V : 1;  // lanes per gate group (GATE_LANE)
+  const int g_lo = m.win * wpl;                    // the group's first window
+  const int o_top = min(nwin, g_lo + wpl) - 1;     // its last: processed first
+
+  int which, hl;
+  head_select(h, S.NH, S.NKVH, which, hl);
+  const HeadView hvw = head_view(args.h, which), gvw = head_view(args.gy, which);
+  const Rsrc ur = slice_rsrc(args.u, b, h, E), lr = slice_rsrc(args.lg, b, h, E),
+             hr = slice_rsrc(hvw, b, hl, E), gr = slice_rsrc(gvw, b, hl, E),
+             dur = slice_rsrc(args.du, b, h, E), dlr = slice_rsrc(args.dlg, b, h, E);
+  const uint32_t ustb = (uint32_t)(args.u.s[2] * E), uscb = (uint32_t)(args.u.s[3] * E);
+  const uint32_t lstb = (uint32_t)(args.lg.s[2] * E);
+  const uint32_t hstb = (uint32_t)(hvw.s[2] * E), hscb = (uint32_t)(hvw.s[3] * E);
+  const uint32_t gstb = (uint32_t)(gvw.s[2] * E), gscb = (uint32_t)(gvw.s[3] * E);
+  const uint32_t dustb = (uint32_t)(args.du.s[2] * E), duscb = (uint32_t)(args.du.s[3] * E);
+  const uint32_t dlstb = (uint32_t)(args.dlg.s[2] * E), dlscb = (uint32_t)(args.dlg.s[3] * E);
+  const uint32_t ub = chan_off(args.u, c0, E);
+  const uint32_t lb = GM == GATE_CHANVEC ? chan_off(args.lg, c0, E) : 0u;
+  const uint32_t hb = chan_off(hvw, c0, E), gb = chan_off(gvw, c0, E);
+  const uint32_t dub = chan_off(args.du, c0, E);
+  const uint32_t dlb = 0u;
+  GateIdx<GM, V> gi;
+  gi.init(args.bias + h * S.Da, c0, nvalid, S.D, S.r, args.lg.s[3]);
+  const bool use_sig = S.use_sigmoid != 0;
+  const int gjl = GL ? c0 / S.r : 0;  // gate group of this lane (GATE_LANE)
+  const bool glead0 = GL && (m.cv % gl) == 0;
+
+  // the inits, read again by every window's warm-up pass (registers are short)
+  const Rsrc irs = slice_rsrc(args.init, b, h, E);
+  const uint32_t ioff = chan_off(args.init, c0, E), iscb = (uint32_t)(args.init.s[3] * E);
+
+  // this lane's slot: row s holds the state entering step lo' + s of the
+  // successor's warm-up and the input u there (one 16-byte vector each)
+  __shared__ uint4 slot_h[KW][256], slot_u[KW][256];
+  const int tid = threadIdx.x;
+
+  // ---- the successor of the lane's first window: its warm-up over that
+  // window's tail (states and u into the slot), and its own chain's G
+  float G[V], a_hi[NA];
+#pragma unroll
+  for (int v = 0; v < V; ++v) G[v] = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NA; ++i) a_hi[i] = 0.0f;
+  {
+    const Window wd = look_back_window(o_top, S.T, args.P, args.Q, args.K);
+    const bool has_next = o_top + 1 < nwin;
+    Window wn;
+    {
+      const Window wr = look_back_window(o_top + 1, S.T, args.P, args.Q, args.K);
+      wn.lo = (int)opaque((uint32_t)(has_next ? wr.lo : wd.hi));
+      wn.st = (int)opaque((uint32_t)(has_next ? wr.st : wd.hi));
+      wn.hi = (int)opaque((uint32_t)(has_next ? wr.hi : wd.hi));
+    }
+    const int nb_g = (wave_max(lane_ok ? wn.hi - wn.st : 0) + NB - 1) / NB;
+    {
+      float hn[V];
+      {
+        const uint4 q = bld_vec<TIO, VEC>(irs, ioff, iscb, nvalid, lane_ok);
+#pragma unroll
+        for (int v = 0; v < V; ++v) hn[v] = Pack<TIO>::get(q, v);
+      }
+      uint4 wu[2][NB];
+      LogitRaw<TIO, GM, NB> wl[2];
+      auto wload = [&](int k, auto bufc) __attribute__((always_inline)) {
+        constexpr int buf = decltype(bufc)::value;
+        const int t0 = wn.lo + k * NB;
+#pragma unroll
+        for (int s = 0; s < NB; ++s)
+          wu[buf][s] = bld_vec<TIO, VEC>(ur, ub + (uint32_t)(t0 + s) * ustb, uscb, nvalid,
+                                         lane_ok && k < NBW && t0 + s < wn.st);
+        wl[buf].template load<true>(lr, lb + (uint32_t)t0 * lstb, lstb, gi, t0, wn.st,
+                                    lane_ok && k < NBW, nvalid);
+      };
+      auto wstep = [&](auto kc) __attribute__((always_inline)) {
+        constexpr int k = decltype(kc)::value;
+        constexpr int buf = k & 1;
+        const int t0 = wn.lo + k * NB;
+        uint4 uq[NB];
+#pragma unroll
+        for (int s = 0; s < NB; ++s) uq[s] = wu[buf][s];
+        float al[NB][NA];
+        wl[buf].gates(gi, t0, wn.st, lane_ok, use_sig, al);
+        wload(k + 1, std::integral_constant<int, 1 - buf>{});
+#pragma unroll
+        for (int s = 0; s < NB; ++s) {
+          slot_h[k * NB + s][tid] = Pack<TIO>::pack(hn);
+          slot_u[k * NB + s][tid] = uq[s];
+#pragma unroll
+          for (int v = 0; v < V; ++v)
+            hn[v] = fmaf(al[s][GL ? 0 : v], Pack<TIO>::get(uq[s], v) - hn[v], hn[v]);
+        }
+      };
+      wload(0, B0{});
+      static_loop<0, NBW>(wstep);
+    }
+    {
+      uint4 ng[2][NB];
+      LogitRaw<TIO, GM, NB> nl[2];
+      auto gload = [&](int k, auto bufc) __attribute__((always_inline)) {
+        constexpr int buf = decltype(bufc)::value;
+        const int tl = wn.hi - (k + 1) * NB;
+#pragma unroll
+        for (int s = 0; s < NB; ++s)
+          ng[buf][s] = bld_vec<TIO, VEC>(gr, gb + (uint32_t)(tl + s) * gstb, gscb, nvalid,
+                                         lane_ok && k < nb_g && tl + s >= wn.st);
+        nl[buf].template load<true>(lr, lb + (uint32_t)tl * lstb, lstb, gi, tl, wn.hi,
+                                    lane_ok && k < nb_g, nvalid, wn.st);
+      };
+      auto gstep = [&](int k, auto bufc) __attribute__((always_inline)) {
+        constexpr int buf = decltype(bufc)::value;
+        const int tl = wn.hi - (k + 1) * NB;
+        uint4 gq[NB];
+#pragma unroll
+        for (int s = 0; s < NB; ++s) gq[s] = ng[buf][s];
+        float al[NB][NA];
+        nl[buf].gates(gi, tl, wn.hi, lane_ok, use_sig, al);
+        gload(k + 1, std::integral_constant<int, 1 - buf>{});
+#pragma unroll
+        for (int s = NB - 1; s >= 0; --s) {
+          const bool ok = lane_ok && tl + s >= wn.st;
+#pragma unroll
+          for (int v = 0; v < V; ++v) {
+            const float gn = fmaf(a_hi[GL ? 0 : v], G[v], Pack<TIO>::get(gq[s], v));
+            G[v] = ok ? gn : G[v];
+          }
+#pragma unroll
+          for (int i = 0; i < NA; ++i) a_hi[i] = ok ? 1.0f - al[s][i] : a_hi[i];
+        }
+      };
+      gload(0, B0{});
+      for (int k = 0; k < nb_g; k += 2) {
+        gstep(k, B0{});
+        if (k + 1 < nb_g) gstep(k + 1, B1{});
+      }
+    }
+  }
+
+  for (int it = 0; it < wpl; ++it) {
+    const int o = o_top - it;
+    const bool active = lane_ok && o >= g_lo;
+    const Window wd = look_back_window(active ? o : 0, S.T, args.P, args.Q, args.K);
+    const bool has_next = o + 1 < nwin;
+    Window wn;
+    {
+      const Window wr = look_back_window(o + 1, S.T, args.P, args.Q, args.K);
+      wn.lo = (int)opaque((uint32_t)(has_next ? wr.lo : wd.hi));
+      wn.st = (int)opaque((uint32_t)(has_next ? wr.st : wd.hi));
+      wn.hi = (int)opaque((uint32_t)(has_next ? wr.hi : wd.hi));
+    }
+    const int nt = wn.st - wn.lo;  // tail steps of this window (<= KW)
+    const int b2_hi = has_next ? wn.lo : wd.hi;
+    const int nb_b2 = (wave_max(active ? b2_hi - wd.st : 0) + NB - 1) / NB;
+    const bool glead = glead0 && active;
+
+    float g1[V], g2[V], an[NA];
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      g1[v] = 0.0f;
+      g2[v] = G[v];
+    }
+#pragma unroll
+    for (int i = 0; i < NA; ++i) an[i] = a_hi[i];
+    float dacc[GL ? 1 : V];
+#pragma unroll
+    for (int k = 0; k < (GL ? 1 : V); ++k) dacc[k] = 0.0f;
+
+    // one reverse step at t (branch-free; a masked step changes nothing); with_g2:
+    // t lies in the next window's warm-up, hn its state
+    auto step = [&](int t, bool ok, const uint4& gq, const uint4& uq, const uint4& hq,
+                    const float (&a)[NA], bool with_g2, const uint4& hn) {
+      float duv[V], dav[V];
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        const int ia = GL ? 0 : v;
+        const float g1n = fmaf(an[ia], g1[v], Pack<TIO>::get(gq, v));
+        const float g2n = with_g2 ? an[ia] * g2[v] : 0.0f;
+        g1[v] = ok ? g1n : g1[v];
+        g2[v] = ok ? g2n : g2[v];
+        const float u = Pack<TIO>::get(uq, v);
+        duv[v] = a[ia] * (g1n + g2n);
+        dav[v] = (u - Pack<TIO>::get(hq, v)) * g1n;
+        if (with_g2) dav[v] = fmaf(u - Pack<TIO>::get(hn, v), g2n, dav[v]);
+      }
+#pragma unroll
+      for (int i = 0; i < NA; ++i) an[i] = ok ? 1.0f - a[i] : an[i];
+      bst_vec<TIO, VEC>(dur, dub + (uint32_t)t * dustb, duscb, nvalid, ok, duv);
+      if (GL) {
+        float p = 0.0f;
+#pragma unroll
+        for (int v = 0; v < V; ++v) p += v < nvalid ? dav[v] : 0.0f;
+        p = group_sum_fixed(ok ? p : 0.0f, gl);
+        const float d = use_sig ? p * (a[0] * (1.0f - a[0])) : p;
+        const bool stl = ok && glead;
+        dacc[0] += stl ? d : 0.0f;
+        bst1<TIO>(dlr, stl ? dlb + (uint32_t)t * dlstb + (uint32_t)gjl * dlscb : kOob, d);
+      } else {
+#pragma unroll
+        for (int mm = 1; mm < V; mm <<= 1) {
+          if (mm < S.r) {
+            float tsum[V];
+#pragma unroll
+            for (int v = 0; v < V; ++v) tsum[v] = dav[v] + dav[v ^ mm];
+#pragma unroll
+            for (int v = 0; v < V; ++v) dav[v] = tsum[v];
+          }
+        }
+        float dl[V];
+#pragma unroll
+        for (int v = 0; v < V; ++v) dl[v] = use_sig ? dav[v] * (a[v] * (1.0f - a[v])) : dav[v];
+        if (GM == GATE_CHANVEC) {
+          bst_vec<TIO, true>(dlr, dlb + (uint32_t)t * dlstb + (uint32_t)c0 * E, E, V, ok, dl);
+#pragma unroll
+          for (int v = 0; v < V; ++v) dacc[v] += ok ? dl[v] : 0.0f;
+        } else {
+#pragma unroll
+          for (int v = 0; v < V; ++v) {
+            const bool lead = ok && (v & (S.r - 1)) == 0 && v < nvalid;
+            dacc[v] += lead ? dl[v] : 0.0f;
+            bst1<TIO>(dlr, lead ? dlb + (uint32_t)t * dlstb + (uint32_t)((c0 + v) / S.r) * dlscb
+                                : kOob,
+                      dl[v]);
+          }
+        }
+      }
+    };
+
+    // The three passes' loads are chained: the last batch of (B1) issues the
+    // first of (A), the last of (A) the first of (B2), so only the first batch
+    // of a window waits for a full load round trip.
+    float h1[V], prodw[NA];
+    {
+      const uint4 q = bld_vec<TIO, VEC>(irs, ioff, iscb, nvalid, lane_ok);
+#pragma unroll
+      for (int v = 0; v < V; ++v) h1[v] = Pack<TIO>::get(q, v);
+    }
+#pragma unroll
+    for (int i = 0; i < NA; ++i) prodw[i] = 1.0f;
+    uint4 wu[2][NB];
+    LogitRaw<TIO, GM, NB> wl[2];
+    auto wload = [&](int kk, auto bufc) __attribute__((always_inline)) {
+      constexpr int buf = decltype(bufc)::value;
+      const int t0 = wd.lo + kk * NB;
+#pragma unroll
+      for (int s = 0; s < NB; ++s)
+        wu[buf][s] = bld_vec<TIO, VEC>(ur, ub + (uint32_t)(t0 + s) * ustb, uscb, nvalid,
+                                       active && kk < NBW && t0 + s < wd.st);
+      wl[buf].template load<true>(lr, lb + (uint32_t)t0 * lstb, lstb, gi, t0, wd.st,
+                                  active && kk < NBW, nvalid);
+    };
+    uint4 cg[2][NB], cu[2][NB], ch[2][NB];
+    LogitRaw<TIO, GM, NB> cl[2];
+    auto bload = [&](int tlow, bool any, auto bufc) __attribute__((always_inline)) {
+      constexpr int buf = decltype(bufc)::value;
+#pragma unroll
+      for (int s = 0; s < NB; ++s) {
+        const int t = tlow + s;
+        const bool ok = active && any && t >= wd.st && t < b2_hi;
+        cg[buf][s] = bld_vec<TIO, VEC>(gr, gb + (uint32_t)t * gstb, gscb, nvalid, ok);
+        cu[buf][s] = bld_vec<TIO, VEC>(ur, ub + (uint32_t)t * ustb, uscb, nvalid, ok);
+        ch[buf][s] = bld_vec<TIO, VEC>(hr, hb + (uint32_t)(t - 1) * hstb, hscb, nvalid,
+                                       ok && t != wd.st);
+      }
+      cl[buf].template load<true>(lr, lb + (uint32_t)tlow * lstb, lstb, gi, tlow, b2_hi,
+                                  active && any, nvalid, wd.st);
+    };
+
+    // (B1) the tail [wn.lo, wn.st) in reverse: gy, the saved states and the
+    // logits from memory, u and the successor's warm-up states from the slot
+    {
+      uint4 bg[2][NB], bh[2][NB];
+      LogitRaw<TIO, GM, NB> bl[2];
+      auto tload = [&](int q, auto bufc) __attribute__((always_inline)) {
+        constexpr int buf = decltype(bufc)::value;
+        const int tlow = wn.lo + KW - (q + 1) * NB;
+#pragma unroll
+        for (int s = 0; s < NB; ++s) {
+          const int t = tlow + s;
+          const bool ok = active && q < NBW && t >= wn.lo && t < wn.st;
+          bg[buf][s] = bld_vec<TIO, VEC>(gr, gb + (uint32_t)t * gstb, gscb, nvalid, ok);
+          bh[buf][s] = bld_vec<TIO, VEC>(hr, hb + (uint32_t)(t - 1) * hstb, hscb, nvalid, ok);
+        }
+        bl[buf].template load<true>(lr, lb + (uint32_t)tlow * lstb, lstb, gi, tlow, wn.st,
+                                    active && q < NBW, nvalid, wn.lo);
+      };
+      auto tstep = [&](auto qc) __attribute__((always_inline)) {
+        constexpr int q = decltype(qc)::value;
+        constexpr int buf = q & 1;
+        const int s0 = KW - (q + 1) * NB;
+        const int tlow = wn.lo + s0;
+        uint4 gq[NB], hq[NB];
+#pragma unroll
+        for (int s = 0; s < NB; ++s) {
+          gq[s] = bg[buf][s];
+          hq[s] = bh[buf][s];
+        }
+        float al[NB][NA];
+        bl[buf].gates(gi, tlow, wn.st, active, use_sig, al);
+        if constexpr (q + 1 < NBW)
+          tload(q + 1, std::integral_constant<int, 1 - buf>{});
+        else
+          wload(0, B0{});  // the first batch of (A)
+#pragma unroll
+        for (int s = NB - 1; s >= 0; --s) {
+          const int t = tlow + s;
+          step(t, active && s0 + s < nt, gq[s], slot_u[s0 + s][tid], hq[s], al[s], true,
+               slot_h[s0 + s][tid]);
+        }
+      };
+      tload(0, B0{});
+      static_loop<0, NBW>(tstep);
+    }
+
+    // (A) the own warm-up [lo, st): the state entering st and prod (1 - alpha);
+    // its states and u are the slot of the next window in the lane (o - 1,
+    // whose tail this is), written after (B1) has read this window's
+    {
+      auto wstep = [&](auto kc) __attribute__((always_inline)) {
+        constexpr int kk = decltype(kc)::value;
+        constexpr int buf = kk & 1;
+        const int t0 = wd.lo + kk * NB;
+        uint4 uq[NB];
+#pragma unroll
+        for (int s = 0; s < NB; ++s) uq[s] = wu[buf][s];
+        float al[NB][NA];
+        wl[buf].gates(gi, t0, wd.st, active, use_sig, al);  // 0 when masked: the identity step
+        if constexpr (kk + 1 < NBW)
+          wload(kk + 1, std::integral_constant<int, 1 - buf>{});
+        else
+          bload(b2_hi - NB, nb_b2 > 0, B0{});  // the first batch of (B2)
+#pragma unroll
+        for (int s = 0; s < NB; ++s) {
+          slot_h[kk * NB + s][tid] = Pack<TIO>::pack(h1);
+          slot_u[kk * NB + s][tid] = uq[s];
+#pragma unroll
+          for (int v = 0; v < V; ++v)
+            h1[v] = fmaf(al[s][GL ? 0 : v], Pack<TIO>::get(uq[s], v) - h1[v], h1[v]);
+#pragma unroll
+          for (int i = 0; i < NA; ++i) prodw[i] *= 1.0f - al[s][i];
+        }
+      };
+      static_loop<0, NBW>(wstep);
+    }
+    const uint4 h_st = Pack<TIO>::pack(h1);  // I/O-rounded, as the saved outputs
+
+    // (B2) [st, b2_hi) in reverse (its first batch was issued by (A))
+    {
+      auto b2step = [&](int kk, auto bufc) __attribute__((always_inline)) {
+        constexpr int buf = decltype(bufc)::value;
+        const int tlow = b2_hi - (kk + 1) * NB;
+        uint4 gq[NB], uq[NB], hq[NB];
+#pragma unroll
+        for (int s = 0; s < NB; ++s) {
+          gq[s] = cg[buf][s];
+          uq[s] = cu[buf][s];
+          hq[s] = tlow + s == wd.st ? h_st : ch[buf][s];
+        }
+        float al[NB][NA];
+        cl[buf].gates(gi, tlow, b2_hi, active, use_sig, al);
+        bload(tlow - NB, kk + 1 < nb_b2, std::integral_constant<int, 1 - buf>{});
+#pragma unroll
+        for (int s = NB - 1; s >= 0; --s) {
+          const int t = tlow + s;
+          step(t, active && t >= wd.st && t < b2_hi, gq[s], uq[s], hq[s], al[s], false, h_st);
+        }
+      };
+      for (int kk = 0; kk < nb_b2; kk += 2) {
+        b2step(kk, B0{});
+        if (kk + 1 < nb_b2) b2step(kk + 1, B1{});
+      }
+    }
+
+    // ---- this window's share of grad_inits and its dbias partial
+    if (active) {
+      float di[V];
+#pragma unroll
+      for (int v = 0; v < V; ++v) di[v] = prodw[GL ? 0 : v] * an[GL ? 0 : v] * g1[v];
+      st_f32<VEC, V>(args.wdi + ((int64_t)bhc * nwin + o) * S.D + c0, nvalid, di);
+      float* pp = args.dbias_partial + ((int64_t)bhc * nwin + o) * S.Da;
+      if (GL) {
+        if (glead) pp[gjl] = dacc[0];
+      } else {
+#pragma unroll
+        for (int v = 0; v < V; ++v)
+          if ((GM == GATE_CHANVEC || (v & (S.r - 1)) == 0) && v < nvalid) pp[(c0 + v) / S.r] = dacc[v];
+      }
+    }
+    // the window before this one in the lane starts from this one's chain
+#pragma unroll
+    for (int v = 0; v < V; ++v) G[v] = g1[v];
+#pragma unroll
+    for (int i = 0; i < NA; ++i) a_hi[i] = an[i];
+  }
+}
+
 template <typename TIO, int GM, bool VEC>
 void launch_fwd(const FwdArgs& a, int grid, bool buf, hipStream_t st) {
   if (buf)
@@ -953,7 +1389,24 @@ void launch_fwd(const FwdArgs& a, int grid, bool buf, hipStream_t st) {
 }
 
 template <typename TIO, int GM, bool VEC>
-void launch_bwd(const BwdArgs& a, int grid, int kw_max, bool buf, hipStream_t st) {
+constexpr bool lb_multi_ok() {
+  return sizeof(TIO) == 4 || (GM == GATE_LANE && VEC);
+}
+inline bool lb_multi_ok_rt(bool f32, int gm, bool vec) {
+  return f32 || (gm == GATE_LANE && vec);
+}
+
+template <typename TIO, int GM, bool VEC>
+void launch_bwd(const BwdArgs& a, int grid, int kw_max, bool buf, bool multi, hipStream_t st) {
+  // the several-windows kernel is built where it fits two wavefronts per SIMD
+  // without spilling in its loops
+  if constexpr (lb_multi_ok<TIO, GM, VEC>()) {
+    if (multi) {
+      hipLaunchKernelGGL((scan_lb_buf_bwd_multi_kernel<TIO, GM, VEC, 8>), dim3(grid), dim3(256),
+                         0, st, a);
+      return;
+    }
+  }
   if (buf) {
     if (kw_max <= 8)
       hipLaunchKernelGGL((scan_lb_buf_bwd_kernel<TIO, GM, VEC, 8>), dim3(grid), dim3(256), 0, st, a);
@@ -986,18 +1439,22 @@ int fwd_t(const FwdArgs& a, bool vec, int gm, bool buf, hipStream_t st) {
 
 template <typename TIO>
 int bwd_t(const BwdArgs& a, bool vec, int gm, int kw_max, bool buf, hipStream_t st) {
+  // several windows per lane (a.wpl) only with buffer addressing, a warm-up of
+  // at most 8 steps and an instantiation that has the kernel
+  const bool multi = buf && a.wpl > 1 && kw_max <= 8 && lb_multi_ok_rt(sizeof(TIO) == 4, gm, vec);
+  const int ngrp = multi ? (a.nchunk + a.wpl - 1) / a.wpl : a.nchunk;
   const int64_t lanes = (int64_t)a.sh.B * a.sh.H *
-                        (buf ? lanes_per_bh(a.lanes, a.nchunk) : (int64_t)a.nchunk * a.lanes);
+                        (buf ? lanes_per_bh(a.lanes, ngrp) : (int64_t)a.nchunk * a.lanes);
   const int64_t grid = (lanes + 255) / 256;
   LTV_REQUIRE(grid < (1ll << 31), LTV_ERR_UNSUPPORTED, "grid too large");
   LTV_REQUIRE(kw_max <= 16, LTV_ERR_UNSUPPORTED, "warm-up of %d steps too long", kw_max);
   if (vec) {
-    if (gm == GATE_LANE) launch_bwd<TIO, GATE_LANE, true>(a, (int)grid, kw_max, buf, st);
-    else if (gm == GATE_CHANVEC) launch_bwd<TIO, GATE_CHANVEC, true>(a, (int)grid, kw_max, buf, st);
-    else launch_bwd<TIO, GATE_CHAN, true>(a, (int)grid, kw_max, buf, st);
+    if (gm == GATE_LANE) launch_bwd<TIO, GATE_LANE, true>(a, (int)grid, kw_max, buf, multi, st);
+    else if (gm == GATE_CHANVEC) launch_bwd<TIO, GATE_CHANVEC, true>(a, (int)grid, kw_max, buf, multi, st);
+    else launch_bwd<TIO, GATE_CHAN, true>(a, (int)grid, kw_max, buf, multi, st);
   } else {
-    if (gm == GATE_LANE) launch_bwd<TIO, GATE_LANE, false>(a, (int)grid, kw_max, buf, st);
-    else launch_bwd<TIO, GATE_CHAN, false>(a, (int)grid, kw_max, buf, st);
+    if (gm == GATE_LANE) launch_bwd<TIO, GATE_LANE, false>(a, (int)grid, kw_max, buf, multi, st);
+    else launch_bwd<TIO, GATE_CHAN, false>(a, (int)grid, kw_max, buf, multi, st);
   }
   LTV_LAUNCH_CHECK();
   return LTV_OK;

@@ -178,6 +178,7 @@ SIGNATURES = {
     ),
     "ltv_chain_take_error": (_c_int, []),
     "ltv_chain_set_test_controls": (_c_int, [_c_int, _c_int]),
+    "ltv_lb_set_windows_per_lane": (_c_int, [_c_int]),
     "ltv_hm_scan_backward_noalloc_max_workspace": (_c_sz, []),
     "ltv_hm_scan_backward_noalloc": (
         _c_int,

@@ -69,7 +69,7 @@ def test_abi_version_and_host_only_queries():
     if not os.path.exists(N.LIB_PATH):
         pytest.skip("library not built")
     lib = N.load()
-    assert lib.ltv_abi_version() == 9
+    assert lib.ltv_abi_version() == 10
     # d12: 18 heads x (128 + 1) = 2322 -> padded to a multiple of 128; 18 logits -> 24
     assert lib.ltv_qkv_packed_width(18, 128, 1) == 2432
     assert lib.ltv_qkv_logit_width(18, 1) == 24
@@ -185,6 +185,19 @@ def test_chain_error_mailbox_and_controls_host_side():
     assert "spin_max" in N.last_error()
     assert lib.ltv_chain_set_test_controls(0, 0) == 0
     assert lib.ltv_chain_take_error() == 0
+
+
+def test_look_back_windows_per_lane_control_host_side():
+    """The short-window backward's windows-per-lane control refuses a negative
+    value and accepts any positive one and 0 (automatic) back."""
+    from nanochat_amd import _native as N
+    if not os.path.exists(N.LIB_PATH):
+        pytest.skip("library not built")
+    lib = N.lib()
+    assert lib.ltv_lb_set_windows_per_lane(-1) == 1  # LTV_ERR_INVALID_ARG
+    assert "wpl" in N.last_error()
+    assert lib.ltv_lb_set_windows_per_lane(3) == 0
+    assert lib.ltv_lb_set_windows_per_lane(0) == 0
 
 
 def test_peaks_library_exports_its_header():
