@@ -82,6 +82,8 @@ def algorithmic_work():
         "qkv_project_fwd": ("mfma", gemm),
         "qkv_project_bwd_input": ("mfma", gemm),
         "qkv_project_bwd_weight": ("mfma", gemm),
+        # grad_x and grad_weight through one library call (one fused launch at d12)
+        "qkv_project_bwd": ("mfma", 2 * gemm),
         "pack_weight": ("hbm", F * C * 4 + FP * C * 2),
     }
 

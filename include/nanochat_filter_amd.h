@@ -45,7 +45,7 @@ extern "C" {
 #define LTV_ERR_HIP 3
 #define LTV_ERR_WORKSPACE 4
 
-/* Version of this ABI (bumped on any signature change or addition): 10. */
+/* Version of this ABI (bumped on any signature change or addition): 11. */
 int ltv_abi_version(void);
 
 /* Message of the last failing call on this host thread ("" if none). */
@@ -457,6 +457,23 @@ int ltv_qkv_project_backward(const void* x, const void* wpack, void* grad_combin
                              void* grad_x, float* grad_weight, void* workspace,
                              size_t workspace_bytes, int M, int C, int H, int D, int Da,
                              void* stream);
+/* ltv_qkv_project_backward for a grad_combined whose columns
+ * F .. round_up(F, 8) - 1 are zero already (as for
+ * ltv_qkv_project_backward_input_zero_padded): grad_combined is only read.
+ * Both combined calls run grad_x and grad_weight's GEMM in one launch where
+ * grad_x's 256 x 256 tiles take more than one and less than two rounds of the
+ * device's compute units (d12: 384 tiles on 256): the compute units that run
+ * one grad_x tile take longer pieces of grad_weight's split reduction than
+ * those that run two (LTV_GEMM_BWD_FUSED=0 runs the two GEMMs one after the
+ * other).  grad_x is bitwise that of ltv_qkv_project_backward_input;
+ * grad_weight sums the same products in fp32 over other split boundaries.
+ * Counterpart in the reference: fused_linear_transpose_backward.cu:22-132
+ * (both gradients of one call). */
+int ltv_qkv_project_backward_zero_padded(const void* x, const void* wpack,
+                                         const void* grad_combined, void* grad_x,
+                                         float* grad_weight, void* workspace,
+                                         size_t workspace_bytes, int M, int C, int H, int D,
+                                         int Da, void* stream);
 /* The two halves of ltv_qkv_project_backward, as separate calls: grad_x
  * (one GEMM launch) and grad_weight (split-K GEMM plus a fixed-order reduction;
  * needs the workspace).  They mirror the grad_x and grad_weight loops of

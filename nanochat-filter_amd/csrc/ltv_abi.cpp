@@ -17,6 +17,6 @@ void set_error(const char* fmt, ...) {
 
 }  // namespace ltv
 
-extern "C" int ltv_abi_version(void) { return 10; }
+extern "C" int ltv_abi_version(void) { return 11; }
 
 extern "C" const char* ltv_last_error(void) { return ltv::g_last_error; }

@@ -679,6 +679,28 @@ inline int dw_split_rows(int M, int C, int Fp) {
   // per-item overhead and partial sums than they gain in parallelism
   return std::max(1024, round_up((M + S - 1) / S, 64));
 }
+// Sum of the S fp32 partials of grad_weight (S slots of Fr x C) into the
+// parameter's interleaved row order.
+int dw_reduce_launch(void* workspace, float* grad_weight, int S, int Fr, int H, int D, int Da,
+                     int C, hipStream_t st) {
+  const int Fvalid = H * (D + Da);
+  const int64_t total = (int64_t)Fvalid * C;
+  if (C % 4 == 0 && total < (1ll << 31) && ((uintptr_t)workspace & 15) == 0 &&
+      ((uintptr_t)grad_weight & 15) == 0) {
+    const int blocks = (int)std::min<int64_t>((total / 4 + 255) / 256, 8192);
+    hipLaunchKernelGGL(dw_reduce4_kernel, dim3(blocks), dim3(256), 0, st,
+                       reinterpret_cast<const float4*>(workspace),
+                       reinterpret_cast<float4*>(grad_weight), S, (int64_t)Fr * C / 4, H, D, Da,
+                       C / 4);
+  } else {
+    const int blocks = (int)std::min<int64_t>((total + 255) / 256, 8192);
+    hipLaunchKernelGGL(dw_reduce_kernel, dim3(blocks), dim3(256), 0, st,
+                       reinterpret_cast<const float*>(workspace), grad_weight, S,
+                       (int64_t)Fr * C, H, D, Da, C);
+  }
+  LTV_LAUNCH_CHECK();
+  return LTV_OK;
+}
 }  // namespace
 
 extern "C" size_t ltv_qkv_project_backward_workspace_size(int M, int C, int H, int D, int Da) {
@@ -823,32 +845,133 @@ extern "C" int ltv_qkv_project_backward_weight(const void* x, const void* grad_c
     rc = launch_gemm<128, 256, 2, 2, OP_RC, OP_RC>(a, e, S, st);
   }
   if (rc) return rc;
-  const int64_t total = (int64_t)Fvalid * C;
-  if (C % 4 == 0 && total < (1ll << 31) && ((uintptr_t)workspace & 15) == 0 &&
-      ((uintptr_t)grad_weight & 15) == 0) {
-    const int blocks = (int)std::min<int64_t>((total / 4 + 255) / 256, 8192);
-    hipLaunchKernelGGL(dw_reduce4_kernel, dim3(blocks), dim3(256), 0, st,
-                       reinterpret_cast<const float4*>(workspace),
-                       reinterpret_cast<float4*>(grad_weight), S, (int64_t)Fr * C / 4, H, D, Da,
-                       C / 4);
-  } else {
-    const int blocks = (int)std::min<int64_t>((total + 255) / 256, 8192);
-    hipLaunchKernelGGL(dw_reduce_kernel, dim3(blocks), dim3(256), 0, st,
-                       reinterpret_cast<const float*>(workspace), grad_weight, S,
-                       (int64_t)Fr * C, H, D, Da, C);
-  }
-  LTV_LAUNCH_CHECK();
-  return LTV_OK;
+  return dw_reduce_launch(workspace, grad_weight, S, Fr, H, D, Da, C, st);
 }
+
+namespace {
+// grad_x and grad_weight in one launch of gemm_dma_bwd_fused_kernel, where
+// grad_x's 256 x 256 tiles take more than one round of the persistent grid and
+// less than two: the workgroups that run one grad_x tile take the longer
+// pieces of grad_weight's reduction.  Returns LTV_OK when launched (with the
+// zeroing and reduction launches around it), 1 when the shapes or tunables
+// leave it out (nothing launched), or an error code.
+int project_backward_fused(const void* x, const void* wpack, void* grad_combined, void* grad_x,
+                           float* grad_weight, void* workspace, int M, int C, int H, int D,
+                           int Da, bool pad_zeroed, hipStream_t st) {
+  static const bool enabled = [] {
+    const char* e = getenv("LTV_GEMM_BWD_FUSED");
+    return e == nullptr || atoi(e) != 0;
+  }();
+  const GemmTuning& tu = gemm_tuning();
+  if (!enabled || !tu.dma || tu.dx == 3 || M == 0) return 1;
+  const int Fp = ltv_qkv_packed_width(H, D, Da);
+  const int Fvalid = H * (D + Da);
+  const int Fv8 = round_up(Fvalid, 8);
+  // grad_x: as project_backward_input_impl's direct-to-LDS path
+  GemmArgs ax;
+  ax.P = GemmOperand{reinterpret_cast<const bf16_t*>(wpack), C, C, Fvalid};
+  ax.Q = GemmOperand{reinterpret_cast<const bf16_t*>(grad_combined), Fp, M, Fv8};
+  ax.K = Fv8;
+  ax.k_split = Fv8;
+  ax.splits = 1;
+  ax.tiles_i = (C + 255) / 256;
+  ax.tiles_j = (M + 255) / 256;
+  EpiRowBF16 ex{reinterpret_cast<bf16_t*>(grad_x), C, C, M};
+  // grad_weight: as ltv_qkv_project_backward_weight's direct-to-LDS path
+  const int split_rows = dw_split_rows(M, C, Fp);
+  const int S = dw_splits(M, split_rows);
+  const int Fr = dw_rows(Fp, tu.dw);
+  GemmArgs aw;
+  aw.P = GemmOperand{reinterpret_cast<const bf16_t*>(x), C, C, M};
+  aw.Q = GemmOperand{reinterpret_cast<const bf16_t*>(grad_combined), Fp, Fp, M};
+  aw.K = M;
+  aw.k_split = split_rows;
+  aw.splits = S;
+  aw.tiles_i = (C + 255) / 256;
+  aw.tiles_j = (Fr + 255) / 256;
+  EpiRowF32Split ew{reinterpret_cast<float*>(workspace), C, (int64_t)Fr * C, C, Fr};
+  if (!dma_usable(ax, OP_RC, OP_KC, ex, 1) || !dma_usable(aw, OP_RC, OP_RC, ew, S)) return 1;
+  // the plan
+  const int G = device_cu_count();
+  const int total_x = ax.tiles_i * ax.tiles_j;
+  if (total_x <= G || total_x >= 2 * G) return 1;
+  DwPlan p;
+  p.n_late = total_x - G;
+  const int n_early = G - p.n_late;
+  p.nt = aw.tiles_i * aw.tiles_j;
+  p.S = S;
+  p.e2 = n_early / p.nt;
+  p.e1 = p.e2 + 1;
+  p.x = n_early - p.nt * p.e2;
+  if (p.e2 < 1 || p.S - p.e1 < 1) return 1;
+  if (p.x * (p.S - p.e1) + (p.nt - p.x) * (p.S - p.e2) > p.n_late) return 1;
+  p.ksteps = (M + kDmaBK - 1) / kDmaBK;
+  // an early workgroup starts its piece one grad_x tile (kx k-steps) before a
+  // late one; a grad_weight k-step (two row-contiguous operands) takes about
+  // 8/7 of a grad_x one (measured at d12: 1.89 against 1.65 us)
+  const int kx = (Fv8 + kDmaBK - 1) / kDmaBK;
+  static const int delta_pct = [] {
+    const char* e = getenv("LTV_GEMM_BWD_DELTA_PCT");
+    return e != nullptr && atoi(e) > 0 ? atoi(e) : 87;
+  }();
+  int delta = (kx * delta_pct + 50) / 100;
+  auto lengths = [&](int e, int& a, int& b) {
+    for (int d = delta; d >= 0; --d) {
+      a = (p.ksteps + (p.S - e) * d) / p.S;
+      b = a - d;
+      if (b >= 1 && e * a + (p.S - e - 1) * b < p.ksteps) return true;
+    }
+    return false;
+  };
+  if (!lengths(p.e1, p.a1, p.b1) || !lengths(p.e2, p.a2, p.b2)) return 1;
+  if (Fv8 > Fvalid && !pad_zeroed) {
+    hipLaunchKernelGGL(zero_cols_kernel, dim3((M + 255) / 256), dim3(256), 0, st,
+                       reinterpret_cast<bf16_t*>(grad_combined), M, (int64_t)Fp, Fvalid, Fv8);
+    LTV_LAUNCH_CHECK();
+  }
+  hipLaunchKernelGGL((gemm_dma_bwd_fused_kernel<EpiRowBF16, EpiRowF32Split>), dim3(G), dim3(512),
+                     0, st, ax, ex, aw, ew, p);
+  LTV_LAUNCH_CHECK();
+  return dw_reduce_launch(workspace, grad_weight, S, Fr, H, D, Da, C, st);
+}
+
+int project_backward_impl(const void* x, const void* wpack, void* grad_combined, void* grad_x,
+                          float* grad_weight, void* workspace, size_t workspace_bytes, int M,
+                          int C, int H, int D, int Da, bool pad_zeroed, void* stream) {
+  int rc = project_backward_check(x, wpack, grad_combined, M, C, H, D, Da);
+  if (rc) return rc;
+  LTV_REQUIRE(grad_x && aligned16(grad_x), LTV_ERR_INVALID_ARG, "grad_x null or misaligned");
+  LTV_REQUIRE(grad_weight, LTV_ERR_INVALID_ARG, "null grad_weight");
+  if (M > 0) {
+    const size_t need = ltv_qkv_project_backward_workspace_size(M, C, H, D, Da);
+    LTV_REQUIRE(workspace && workspace_bytes >= need, LTV_ERR_WORKSPACE,
+                "workspace too small: need %zu bytes, got %zu", need, workspace_bytes);
+    rc = project_backward_fused(x, wpack, grad_combined, grad_x, grad_weight, workspace, M, C, H,
+                                D, Da, pad_zeroed, (hipStream_t)stream);
+    if (rc != 1) return rc;
+  }
+  rc = project_backward_input_impl(x, wpack, grad_combined, grad_x, M, C, H, D, Da, pad_zeroed,
+                                   stream);
+  if (rc) return rc;
+  return ltv_qkv_project_backward_weight(x, grad_combined, grad_weight, workspace,
+                                         workspace_bytes, M, C, H, D, Da, stream);
+}
+}  // namespace
 
 extern "C" int ltv_qkv_project_backward(const void* x, const void* wpack,
                                         void* grad_combined, void* grad_x,
                                         float* grad_weight, void* workspace,
                                         size_t workspace_bytes, int M, int C, int H, int D,
                                         int Da, void* stream) {
-  int rc = ltv_qkv_project_backward_input(x, wpack, grad_combined, grad_x, M, C, H, D, Da,
-                                          stream);
-  if (rc) return rc;
-  return ltv_qkv_project_backward_weight(x, grad_combined, grad_weight, workspace,
-                                         workspace_bytes, M, C, H, D, Da, stream);
+  return project_backward_impl(x, wpack, grad_combined, grad_x, grad_weight, workspace,
+                               workspace_bytes, M, C, H, D, Da, false, stream);
+}
+
+extern "C" int ltv_qkv_project_backward_zero_padded(const void* x, const void* wpack,
+                                                    const void* grad_combined, void* grad_x,
+                                                    float* grad_weight, void* workspace,
+                                                    size_t workspace_bytes, int M, int C, int H,
+                                                    int D, int Da, void* stream) {
+  return project_backward_impl(x, wpack, const_cast<void*>(grad_combined), grad_x, grad_weight,
+                               workspace, workspace_bytes, M, C, H, D, Da, true, stream);
 }

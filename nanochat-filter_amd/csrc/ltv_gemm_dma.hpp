@@ -519,11 +519,32 @@ __device__ __forceinline__ bf16x8_t dma_read_frag(const bf16_t* stage, int row_b
   }
 }
 
+// Work items of a persistent launch: item k of this workgroup is
+// blockIdx.x + k gridDim.x of the (tile, split) items, XCD-contiguous.
+template <int BI, int BJ>
+struct GridItems {
+  __device__ __forceinline__ void decode(const GemmArgs& g, GemmCursor& c) const {
+    gemm_decode<BI, BJ>(g, c);
+  }
+};
+
+// LDS of one direct-to-LDS GEMM workgroup: NST stages of each operand tile and
+// a per-wavefront epilogue staging area (the launches declare it once and may
+// run several GEMMs through it one after another).
+template <int BI, int BJ, int NW>
+struct DmaLds {
+  static constexpr int kPB = BI * kDmaBK * 2, kQB = BJ * kDmaBK * 2;  // stage bytes per operand
+  __attribute__((aligned(1024))) bf16_t p[kDmaStages][kPB / 2];
+  __attribute__((aligned(1024))) bf16_t q[kDmaStages][kQB / 2];
+  __attribute__((aligned(16))) char epi[NW][kEpiStageBytes];
+};
+
 // Persistent over (tile, split) work items like gemm_bf16_kernel, stepping the
-// reduction in kDmaBK slices through two LDS stages.
-template <int BI, int BJ, int WGI, int WGJ, int PL, int QL, class Epi>
-__global__ void __launch_bounds__(WGI * WGJ * 64)
-gemm_dma_kernel(const GemmArgs g, const Epi epi) {
+// reduction in kDmaBK slices through two LDS stages; the items are those
+// Items::decode gives this workgroup, in order.
+template <int BI, int BJ, int WGI, int WGJ, int PL, int QL, class Epi, class Items>
+__device__ __forceinline__ void gemm_dma_run(const GemmArgs& g, const Epi& epi, const Items& items,
+                                             DmaLds<BI, BJ, WGI * WGJ>& lds) {
   constexpr int NW = WGI * WGJ;
   constexpr int WI = BI / WGI, WJ = BJ / WGJ;
   constexpr int MI = WI / 32, MJ = WJ / 32;
@@ -542,9 +563,10 @@ gemm_dma_kernel(const GemmArgs g, const Epi epi) {
 
   constexpr int NST = kDmaStages;
   constexpr int kLoads = OpP::kPerWave + OpQ::kPerWave;  // vm instructions per k-step
-  __shared__ __attribute__((aligned(1024))) bf16_t lds_p[NST][PB / 2];
-  __shared__ __attribute__((aligned(1024))) bf16_t lds_q[NST][QB / 2];
-  __shared__ __attribute__((aligned(16))) char lds_epi[NW][kEpiStageBytes];
+  static_assert(PB == DmaLds<BI, BJ, NW>::kPB && QB == DmaLds<BI, BJ, NW>::kQB, "stage sizes");
+  auto& lds_p = lds.p;
+  auto& lds_q = lds.q;
+  auto& lds_epi = lds.epi;
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -565,7 +587,7 @@ gemm_dma_kernel(const GemmArgs g, const Epi epi) {
 
   // cursors count k-steps of kDmaBK; reuse GemmCursor with nk in those units
   auto decode = [&](GemmCursor& c) {
-    gemm_decode<BI, BJ>(g, c);
+    items.decode(g, c);
     if (c.valid) c.nk = (c.ke - c.kb + kDmaBK - 1) / kDmaBK;
   };
   auto advance = [&](GemmCursor& c) {
@@ -773,6 +795,101 @@ gemm_dma_kernel(const GemmArgs g, const Epi epi) {
     if (!cc.valid) break;
   }
   wait_vmcnt<0>();
+}
+
+template <int BI, int BJ, int WGI, int WGJ, int PL, int QL, class Epi>
+__global__ void __launch_bounds__(WGI * WGJ * 64)
+gemm_dma_kernel(const GemmArgs g, const Epi epi) {
+  __shared__ DmaLds<BI, BJ, WGI * WGJ> lds;
+  gemm_dma_run<BI, BJ, WGI, WGJ, PL, QL>(g, epi, GridItems<BI, BJ>{}, lds);
+}
+
+// ---------------------------------------------------------------------------
+// The projection backward's two GEMMs in one persistent launch.  grad_x has
+// more tiles than the grid has workgroups but fewer than twice as many (384
+// on 256 CUs at d12), so one round of tiles leaves workgroups [n_late, G)
+// idle while [0, n_late) run their second tile.  Here every workgroup runs its
+// grad_x tiles and then one piece of grad_weight's split reduction, the
+// workgroups that finished grad_x a tile earlier taking the longer pieces:
+// each of grad_weight's nt output tiles keeps S partial slots (the layout
+// dw_reduce4_kernel sums), filled by e "early" pieces of a k-steps followed by
+// S - e "late" pieces of b = a - delta k-steps, the last of which ends the
+// reduction.  Tiles [0, x) have e1 early pieces, tiles [x, nt) e2 = e1 - 1, so
+// that the early pieces number exactly the early workgroups.
+// ---------------------------------------------------------------------------
+struct DwPlan {
+  int n_late;      // workgroups running two grad_x tiles (the rest run one)
+  int nt, S, x;    // grad_weight output tiles, slots per tile, tiles with e1 early pieces
+  int e1, a1, b1;  // tiles [0, x): early pieces, their k-steps, late pieces' k-steps
+  int e2, a2, b2;  // tiles [x, nt)
+  int ksteps;      // k-steps of the whole reduction
+};
+
+template <int BI, int BJ>
+struct DwPlanItems {
+  DwPlan p;
+  __device__ __forceinline__ void decode(const GemmArgs& g, GemmCursor& c) const {
+    c.valid = false;
+    if (c.k != 0) return;  // one piece per workgroup
+    const int b = blockIdx.x;
+    int t, slot, k0, k1;
+    if (b >= p.n_late) {  // early: one grad_x tile before this piece
+      const int w = b - p.n_late;
+      if (w < p.x * p.e1) {
+        t = w / p.e1;
+        slot = w % p.e1;
+        k0 = slot * p.a1;
+        k1 = k0 + p.a1;
+      } else {
+        const int w2 = w - p.x * p.e1;
+        if (w2 >= (p.nt - p.x) * p.e2) return;
+        t = p.x + w2 / p.e2;
+        slot = w2 % p.e2;
+        k0 = slot * p.a2;
+        k1 = k0 + p.a2;
+      }
+    } else {  // late: two grad_x tiles before this piece
+      const int l1 = p.S - p.e1, l2 = p.S - p.e2;
+      int j, e, a, lb, nl;
+      if (b < p.x * l1) {
+        t = b / l1;
+        j = b % l1;
+        e = p.e1;
+        a = p.a1;
+        lb = p.b1;
+        nl = l1;
+      } else {
+        const int w2 = b - p.x * l1;
+        if (w2 >= (p.nt - p.x) * l2) return;
+        t = p.x + w2 / l2;
+        j = w2 % l2;
+        e = p.e2;
+        a = p.a2;
+        lb = p.b2;
+        nl = l2;
+      }
+      slot = e + j;
+      k0 = e * a + j * lb;
+      k1 = j == nl - 1 ? p.ksteps : k0 + lb;
+    }
+    c.valid = true;
+    c.i0 = (t % g.tiles_i) * BI;
+    c.j0 = (t / g.tiles_i) * BJ;
+    c.split = slot;
+    c.kb = k0 * kDmaBK;
+    c.ke = min(k1 * kDmaBK, g.K);
+    c.kt = 0;
+  }
+};
+
+template <class EpiX, class EpiW>
+__global__ void __launch_bounds__(512)
+gemm_dma_bwd_fused_kernel(const GemmArgs gx, const EpiX ex, const GemmArgs gw, const EpiW ew,
+                          const DwPlan plan) {
+  __shared__ DmaLds<256, 256, 8> lds;
+  gemm_dma_run<256, 256, 2, 4, OP_RC, OP_KC>(gx, ex, GridItems<256, 256>{}, lds);
+  __syncthreads();  // the LDS stages and staging areas are reused
+  gemm_dma_run<256, 256, 2, 4, OP_RC, OP_RC>(gw, ew, DwPlanItems<256, 256>{plan}, lds);
 }
 
 }  // namespace ltv

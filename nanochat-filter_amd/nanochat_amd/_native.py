@@ -157,6 +157,11 @@ SIGNATURES = {
         [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_sz, _c_int, _c_int, _c_int, _c_int,
          _c_int, _c_vp],
     ),
+    "ltv_qkv_project_backward_zero_padded": (
+        _c_int,
+        [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_sz, _c_int, _c_int, _c_int, _c_int,
+         _c_int, _c_vp],
+    ),
     "ltv_qkv_project_backward_input": (
         _c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_int, _c_int, _c_int, _c_int, _c_int, _c_vp]),
     "ltv_qkv_project_backward_input_zero_padded": (

@@ -215,17 +215,14 @@ def project_backward(x: torch.Tensor, wpack: torch.Tensor, grad_combined: torch.
     grad_w = torch.empty((H * (D + Da), C), dtype=torch.float32, device=x.device)
     ws_bytes = lib.ltv_qkv_project_backward_workspace_size(M, C, H, D, Da)
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=x.device)
-    fn = (lib.ltv_qkv_project_backward_input_zero_padded if pad_zeroed
-          else lib.ltv_qkv_project_backward_input)
-    with N.span("qkv_project_bwd_input"):
+    # both gradients in one call: the library runs the two GEMMs in one launch
+    # where grad_x's tiles leave part of the device idle in their last round
+    fn = (lib.ltv_qkv_project_backward_zero_padded if pad_zeroed
+          else lib.ltv_qkv_project_backward)
+    with N.span("qkv_project_bwd"):
         rc = fn(x.data_ptr(), wpack.data_ptr(), grad_combined.data_ptr(), grad_x.data_ptr(),
-                M, C, H, D, Da, st)
-    N.check(rc, "ltv_qkv_project_backward_input")
-    with N.span("qkv_project_bwd_weight"):
-        rc = lib.ltv_qkv_project_backward_weight(x.data_ptr(), grad_combined.data_ptr(),
-                                                 grad_w.data_ptr(), ws.data_ptr(), ws_bytes,
-                                                 M, C, H, D, Da, st)
-    N.check(rc, "ltv_qkv_project_backward_weight")
+                grad_w.data_ptr(), ws.data_ptr(), ws_bytes, M, C, H, D, Da, st)
+    N.check(rc, "ltv_qkv_project_backward")
     return grad_x, grad_w
 
 

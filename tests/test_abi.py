@@ -69,7 +69,7 @@ def test_abi_version_and_host_only_queries():
     if not os.path.exists(N.LIB_PATH):
         pytest.skip("library not built")
     lib = N.load()
-    assert lib.ltv_abi_version() == 10
+    assert lib.ltv_abi_version() == 11
     # d12: 18 heads x (128 + 1) = 2322 -> padded to a multiple of 128; 18 logits -> 24
     assert lib.ltv_qkv_packed_width(18, 128, 1) == 2432
     assert lib.ltv_qkv_logit_width(18, 1) == 24
