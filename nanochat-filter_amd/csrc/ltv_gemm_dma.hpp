@@ -825,6 +825,14 @@ struct DwPlan {
   int ksteps;      // k-steps of the whole reduction
 };
 
+// Which piece a workgroup takes: the early pieces in (slot, tile) order, and
+// likewise the late ones, are dealt to the early (late) workgroups XCD by XCD
+// (workgroup b runs on XCD b % 8), so the pieces an XCD holds mostly share
+// their k-range and read the same rows of both operands through its L2.
+// Measured at d12: 567 MB read from HBM against 808 MB when consecutive
+// workgroups take consecutive pieces of one tile (about the same time, 214
+// against 213 us), and 238 us when the (slot, tile) order is dealt round the
+// XCDs instead.
 template <int BI, int BJ>
 struct DwPlanItems {
   DwPlan p;
@@ -832,45 +840,42 @@ struct DwPlanItems {
     c.valid = false;
     if (c.k != 0) return;  // one piece per workgroup
     const int b = blockIdx.x;
+    const int G = gridDim.x;
+    const bool xcd = G % 8 == 0 && p.n_late % 8 == 0;
     int t, slot, k0, k1;
     if (b >= p.n_late) {  // early: one grad_x tile before this piece
-      const int w = b - p.n_late;
-      if (w < p.x * p.e1) {
-        t = w / p.e1;
-        slot = w % p.e1;
-        k0 = slot * p.a1;
-        k1 = k0 + p.a1;
+      const int w = b - p.n_late, n = G - p.n_late;
+      const int i = xcd ? (w % 8) * (n / 8) + w / 8 : w;
+      int s;
+      if (i < p.e2 * p.nt) {
+        s = i / p.nt;
+        t = i % p.nt;
       } else {
-        const int w2 = w - p.x * p.e1;
-        if (w2 >= (p.nt - p.x) * p.e2) return;
-        t = p.x + w2 / p.e2;
-        slot = w2 % p.e2;
-        k0 = slot * p.a2;
-        k1 = k0 + p.a2;
+        s = p.e2;
+        t = i - p.e2 * p.nt;
+        if (t >= p.x) return;
       }
+      const int a = t < p.x ? p.a1 : p.a2;
+      slot = s;
+      k0 = s * a;
+      k1 = k0 + a;
     } else {  // late: two grad_x tiles before this piece
-      const int l1 = p.S - p.e1, l2 = p.S - p.e2;
-      int j, e, a, lb, nl;
-      if (b < p.x * l1) {
-        t = b / l1;
-        j = b % l1;
-        e = p.e1;
-        a = p.a1;
-        lb = p.b1;
-        nl = l1;
+      const int i = xcd ? (b % 8) * (p.n_late / 8) + b / 8 : b;
+      const int l1 = p.S - p.e1;  // late pieces of a tile with e1 early ones (one fewer than e2's)
+      int j;
+      if (i < l1 * p.nt) {
+        j = i / p.nt;
+        t = i % p.nt;
       } else {
-        const int w2 = b - p.x * l1;
-        if (w2 >= (p.nt - p.x) * l2) return;
-        t = p.x + w2 / l2;
-        j = w2 % l2;
-        e = p.e2;
-        a = p.a2;
-        lb = p.b2;
-        nl = l2;
+        j = l1;
+        t = p.x + (i - l1 * p.nt);
+        if (t >= p.nt) return;
       }
+      const bool c1 = t < p.x;
+      const int e = c1 ? p.e1 : p.e2, a = c1 ? p.a1 : p.a2, lb = c1 ? p.b1 : p.b2;
       slot = e + j;
       k0 = e * a + j * lb;
-      k1 = j == nl - 1 ? p.ksteps : k0 + lb;
+      k1 = j == p.S - e - 1 ? p.ksteps : k0 + lb;
     }
     c.valid = true;
     c.i0 = (t % g.tiles_i) * BI;
