@@ -618,8 +618,10 @@ int scan_forward_impl(int dtype, const HostView4& u, const HostView4& lg, const 
   a.nwin = look_back_nwin(T, P, Q);
   a.wst = nullptr;
   a.kw = 0;
-  LTV_REQUIRE(!init_f32 || a.nwin == 1, LTV_ERR_UNSUPPORTED,
-              "fp32 inits with bf16 values need the full recurrence (P >= T)");
+  LTV_REQUIRE(!init_f32 || a.nwin == 1 || (tuning().lb_short && lb_short_ok(V, r, Q, K)),
+              LTV_ERR_UNSUPPORTED,
+              "fp32 inits with bf16 values need the full recurrence (P >= T) or look-back "
+              "windows the short-window kernels take");
   const int E = dtype == LTV_DTYPE_BF16 ? 2 : 4;
   if ((rc = check_tile_offsets("values", u.s, D, E)) || (rc = check_tile_offsets("logits", lg.s, D, E)) ||
       (rc = check_tile_offsets("inits", init.s, D, init_f32 ? 4 : E)))
@@ -648,6 +650,9 @@ int scan_forward_impl(int dtype, const HostView4& u, const HostView4& lg, const 
     for (int i = 0; i < 3; ++i)
       if ((i == 0 ? NH : NKVH) > 0)
         buf = buf && view_span_bytes(outs[i], 1, 1, T, D, E) <= kBufSpanMax;
+    LTV_REQUIRE(!init_f32 || buf, LTV_ERR_UNSUPPORTED,
+                "fp32 inits with look-back windows need views whose (b, h) slices span less "
+                "than 2 GiB");
     return scan_launch_lb_short_fwd(dtype == LTV_DTYPE_BF16, a, vec, gm, buf, st);
   }
   if (a.nwin == 1 && chain_ws != nullptr) {
@@ -916,10 +921,13 @@ int scan_backward_impl(int dtype, const HostView4& u, const HostView4& lg, const
   if (gm == GATE_CHAN && vec && chanvec_ok(r, D, V, lg) && chanvec_ok(r, D, V, dlg))
     gm = GATE_CHANVEC;
   const int nwin = look_back_nwin(T, P, Q);
-  LTV_REQUIRE(!(init_f32 || dinit_sum) || (nwin == 1 && gm >= 0), LTV_ERR_UNSUPPORTED,
+  const bool lb_short = nwin > 1 && tuning().lb_short && lb_short_ok(V, r, Q, K);
+  LTV_REQUIRE(!(init_f32 || dinit_sum) || (nwin == 1 && gm >= 0) || (lb_short && !dinit_sum),
+              LTV_ERR_UNSUPPORTED,
               "fp32 inits with bf16 values, or grad_inits summed over the batch (batch stride "
               "0), need the full recurrence (P >= T) and gate groups of r channels with r a "
-              "multiple of %d and Da <= %d, or r dividing %d (r=%d Da=%d)",
+              "multiple of %d and Da <= %d, or r dividing %d (r=%d Da=%d); fp32 inits also go "
+              "with look-back windows the short-window kernels take",
               V, kMaxLaneGroups, V, r, Da);
   PadZero pz;
   if (dlg_pad > 0) {
@@ -978,6 +986,9 @@ int scan_backward_impl(int dtype, const HostView4& u, const HostView4& lg, const
       if (g_lb_wpl.load(std::memory_order_relaxed) > 0) w = g_lb_wpl.load(std::memory_order_relaxed);
       a.wpl = (int)std::max<int64_t>(1, std::min<int64_t>(w, nwin));
     }
+    LTV_REQUIRE(!init_f32 || buf, LTV_ERR_UNSUPPORTED,
+                "fp32 inits with look-back windows need views whose (b, h) slices span less "
+                "than 2 GiB");
     rc = scan_launch_lb_short_bwd(bf16, a, vec, sgm, K - 1, buf, st);
     if (rc) return rc;
     rc = scan_launch_lb_dinit(bf16, a, st);

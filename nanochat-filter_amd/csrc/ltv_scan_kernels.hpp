@@ -1945,10 +1945,15 @@ __global__ void __launch_bounds__(256) scan_lb_dinit_kernel(const BwdArgs args) 
 #pragma unroll
     for (int k = 0; k < KB; ++k) acc += x[k];
   }
-  TIO* dip = reinterpret_cast<TIO*>(const_cast<void*>(args.dinit.p)) +
-             (int64_t)b * args.dinit.s[0] + (int64_t)h * args.dinit.s[1] +
-             (int64_t)d * args.dinit.s[3];
-  Pack<TIO>::store1(dip, acc);
+  const int64_t o = (int64_t)b * args.dinit.s[0] + (int64_t)h * args.dinit.s[1] +
+                    (int64_t)d * args.dinit.s[3];
+  if (args.init_f32) {
+    // fp32 inits read as bf16: the gradient of the bf16 tensor, widened
+    reinterpret_cast<float*>(const_cast<void*>(args.dinit.p))[o] =
+        __uint_as_float(cvt_pk_bf16(acc, 0.0f) << 16);
+  } else {
+    Pack<TIO>::store1(reinterpret_cast<TIO*>(const_cast<void*>(args.dinit.p)) + o, acc);
+  }
 }
 
 // ---------------------------------------------------------------------------

@@ -541,8 +541,11 @@ __global__ void __launch_bounds__(256) scan_lb_buf_fwd_kernel(const FwdArgs args
 
   float hv[V];
   {
-    const uint4 q = bld_vec<TIO, VEC>(slice_rsrc(args.init, b, h, E), chan_off(args.init, c0, E),
-                                      (uint32_t)(args.init.s[3] * E), nvalid, active);
+    // fp32 inits (with bf16 values) are rounded to bf16 as they are read
+    const int EI = args.init_f32 ? 4 : E;
+    const uint4 q = bld_init<TIO, VEC>(slice_rsrc(args.init, b, h, EI), chan_off(args.init, c0, EI),
+                                       (uint32_t)(args.init.s[3] * EI), nvalid, active,
+                                       args.init_f32 != 0);
 #pragma unroll
     for (int v = 0; v < V; ++v) hv[v] = Pack<TIO>::get(q, v);
   }
@@ -648,8 +651,11 @@ __global__ void __launch_bounds__(256) scan_lb_buf_bwd_kernel(const BwdArgs args
 
   float ini[V];
   {
-    const uint4 q = bld_vec<TIO, VEC>(slice_rsrc(args.init, b, h, E), chan_off(args.init, c0, E),
-                                      (uint32_t)(args.init.s[3] * E), nvalid, active);
+    // fp32 inits (with bf16 values) are rounded to bf16 as they are read
+    const int EI = args.init_f32 ? 4 : E;
+    const uint4 q = bld_init<TIO, VEC>(slice_rsrc(args.init, b, h, EI), chan_off(args.init, c0, EI),
+                                       (uint32_t)(args.init.s[3] * EI), nvalid, active,
+                                       args.init_f32 != 0);
 #pragma unroll
     for (int v = 0; v < V; ++v) ini[v] = Pack<TIO>::get(q, v);
   }
@@ -1014,8 +1020,9 @@ __global__ void __launch_bounds__(256, 2) scan_lb_buf_bwd_multi_kernel(const Bwd
   const bool glead0 = GL && (m.cv % gl) == 0;
 
   // the inits, read again by every window's warm-up pass (registers are short)
-  const Rsrc irs = slice_rsrc(args.init, b, h, E);
-  const uint32_t ioff = chan_off(args.init, c0, E), iscb = (uint32_t)(args.init.s[3] * E);
+  const int EI = args.init_f32 ? 4 : E;  // fp32 inits: rounded to bf16 as they are read
+  const Rsrc irs = slice_rsrc(args.init, b, h, EI);
+  const uint32_t ioff = chan_off(args.init, c0, EI), iscb = (uint32_t)(args.init.s[3] * EI);
 
   // this lane's slot: row s holds the state entering step lo' + s of the
   // successor's warm-up and the input u there (one 16-byte vector each)
@@ -1043,7 +1050,7 @@ __global__ void __launch_bounds__(256, 2) scan_lb_buf_bwd_multi_kernel(const Bwd
     {
       float hn[V];
       {
-        const uint4 q = bld_vec<TIO, VEC>(irs, ioff, iscb, nvalid, lane_ok);
+        const uint4 q = bld_init<TIO, VEC>(irs, ioff, iscb, nvalid, lane_ok, args.init_f32 != 0);
 #pragma unroll
         for (int v = 0; v < V; ++v) hn[v] = Pack<TIO>::get(q, v);
       }
@@ -1217,7 +1224,7 @@ __global__ void __launch_bounds__(256, 2) scan_lb_buf_bwd_multi_kernel(const Bwd
     // of a window waits for a full load round trip.
     float h1[V], prodw[NA];
     {
-      const uint4 q = bld_vec<TIO, VEC>(irs, ioff, iscb, nvalid, lane_ok);
+      const uint4 q = bld_init<TIO, VEC>(irs, ioff, iscb, nvalid, lane_ok, args.init_f32 != 0);
 #pragma unroll
       for (int v = 0; v < V; ++v) h1[v] = Pack<TIO>::get(q, v);
     }

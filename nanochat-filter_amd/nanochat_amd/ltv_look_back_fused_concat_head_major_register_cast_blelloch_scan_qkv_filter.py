@@ -85,8 +85,8 @@ def look_back_fused_forward(filt: LtvLookBackHeadMajorQkvFilter, x: torch.Tensor
     """bf16 fused path of a look-back filter: (q, k, v) as (B, T, H, D) views."""
     NH, NKVH, Da, D = filt.n_head, filt.n_kv_head, filt.num_alpha_groups, filt.head_dim
     H = NH + 2 * NKVH
-    inits = resolved_inits.to(torch.bfloat16)
     if full_recurrence and x.size(1) == 1 and not torch.is_grad_enabled():
+        inits = resolved_inits.to(torch.bfloat16)
         # one recurrence step from the cached rows: the fused decode kernel
         wpack = hm_fast.cached_packed_weight(filt, H, D, Da)
         out = hm_fast.decode_step(x, wpack, (inits[:, :NH], inits[:, NH:NH + NKVH],
@@ -96,7 +96,14 @@ def look_back_fused_forward(filt: LtvLookBackHeadMajorQkvFilter, x: torch.Tensor
         return (out[:, :NH].unsqueeze(1), out[:, NH:NH + NKVH].unsqueeze(1),
                 out[:, NH + NKVH:].unsqueeze(1))
     P, Q, K = filt.chunking(full_recurrence)
+    if resolved_inits.dtype == torch.float32 and hm_fast.fp32_inits_ok(x.size(1), D, filt.r, P, Q, K):
+        # the kernels round fp32 inits to bf16 as they read them and return
+        # their gradient as the widened bf16 one -- what .to(bfloat16) and its
+        # backward give, without the two conversion launches
+        inits = resolved_inits
+    else:
+        inits = resolved_inits.to(torch.bfloat16).contiguous()
     hq, hk, hv, _, _, _ = torch.ops.nanochat_amd.qkv_filter(
-        x.contiguous(), filt.c.weight, inits.contiguous(), filt.logit_bias.float().contiguous(),
+        x.contiguous(), filt.c.weight, inits, filt.logit_bias.float().contiguous(),
         NH, NKVH, Da, filt.r, P, Q, K)
     return hq.transpose(1, 2), hk.transpose(1, 2), hv.transpose(1, 2)

@@ -234,6 +234,18 @@ def shared_inits_ok(D: int, Da: int, r: int) -> bool:
     return D % 8 == 0 and ((r % 8 == 0 and Da <= 16) or 8 % r == 0)
 
 
+def fp32_inits_ok(T: int, D: int, r: int, P: int, Q: int, K: int) -> bool:
+    """Whether the bf16 scan takes (B, H, D) fp32 inits for this chunking: the
+    full recurrence (P >= T) with gate groups the tile kernels reduce, or
+    look-back windows the short-window kernels take (Q <= 64, a warm-up
+    K - 1 <= min(Q, 16), gate groups of 8 2^k channels or dividing 8)."""
+    if P >= T:  # the tile kernels' gate groups, as for shared inits
+        return D % 8 == 0 and ((r % 8 == 0 and D // r <= 16) or 8 % r == 0)
+    if Q > 64 or K - 1 > 16 or K - 1 > Q or D % 8:
+        return False
+    return (r % 8 == 0 and (r // 8) & (r // 8 - 1) == 0) or 8 % r == 0
+
+
 def _inits_view(inits: torch.Tensor, values: torch.Tensor):
     """(strides (b, h, d), dtype code) of the inits: (B, H, D) per sequence,
     or (H, D) shared by every sequence (batch stride 0); the values' dtype,

@@ -147,3 +147,34 @@ def test_kv_cache_groupings_match_chunked_scan(variant, pqk):
         assert_close(np_of(torch.cat([s[i] for s in steps], dim=1)), ref, tol, f"{name} steps")
         assert_close(np_of(torch.cat([s[i] for s in steps3], dim=1)), ref, tol,
                      f"{name} prefilled steps")
+
+
+@pytest.mark.parametrize("pqk", [(16, 16, 9), (64, 60, 5), (32, 8, 9)], ids=str)
+def test_fp32_inits_bitwise_equal_bf16_cast(pqk, monkeypatch):
+    """The bf16 look-back filter hands the fp32 inits (the expanded parameter)
+    to the kernels, which round them to bf16 as they read them and return the
+    widened bf16 gradient: outputs and every gradient bitwise those of casting
+    the inits to bf16 first (the reference's ``.to(dtype)``), with and without
+    the fp32 hand-over."""
+    from nanochat_amd.ops import ltv_hm_fast as F_
+    NH, NKVH, D, r = 2, 1, 128, 128
+    B, T = 4, 200
+    g = torch.Generator().manual_seed(7)
+    x = torch.randn(B, T, NH * D, generator=g).to(torch.bfloat16).to(DEV)
+    gy = [torch.randn(B, T, n, D, generator=g).to(torch.bfloat16).to(DEV) for n in (NH, NKVH, NKVH)]
+
+    def run():
+        f = _make("blelloch", NH, NKVH, D, r, pqk, seed=5)
+        xd = x.clone().requires_grad_(True)
+        inits = f.init_param.unsqueeze(0).expand(B, -1, -1)
+        q, k, v = f(xd, inits, full_recurrence=False)
+        torch.autograd.backward([q, k, v], gy)
+        return [q, k, v, xd.grad, f.c.weight.grad, f.init_param.grad, f.logit_bias.grad]
+
+    assert F_.fp32_inits_ok(T, D, r, *pqk)
+    fp32 = run()
+    monkeypatch.setattr(F_, "fp32_inits_ok", lambda *a: False)
+    cast = run()
+    for name, a, b in zip(("q", "k", "v", "grad_x", "grad_weight", "grad_init_param",
+                           "grad_logit_bias"), fp32, cast):
+        assert torch.equal(a, b), f"{name} differs with pqk={pqk}"

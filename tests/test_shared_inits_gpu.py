@@ -136,15 +136,21 @@ def test_shared_inits_oracle_rows():
 
 
 def test_unsupported_forms_are_refused():
-    """fp32 inits need the full recurrence; a batch-summed grad_inits needs
-    gate groups the tile kernels reduce; the values' dtype must be bf16 for
-    fp32 inits.  Each is an error before any launch."""
+    """A batch-summed grad_inits needs the full recurrence and gate groups the
+    tile kernels reduce (look-back windows read shared fp32 inits in the
+    forward, but their backward refuses the batch sum); the values' dtype must
+    be bf16 for fp32 inits.  Each is an error before any launch."""
     F = _F()
     B, T, NH, NKVH, Da, r = 2, 64, 1, 1, 1, 128
     H, D = NH + 2 * NKVH, Da * r
     values, logits, param, bias, gys = _case(B, T, NH, NKVH, Da, r, seed=1)
-    with pytest.raises(RuntimeError, match="full recurrence"):
-        F.scan_forward(values, logits, param, bias, NH, NKVH, Da, r, True, P=16, Q=16, K=4)
+    q, k, v = F.scan_forward(values, logits, param, bias, NH, NKVH, Da, r, True, P=16, Q=16, K=4)
+    gc = torch.zeros(B, T, F.packed_width(H, D, Da), dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(RuntimeError, match="batch"):
+        F.scan_backward(values, logits, param, bias, q, k, v, *gys, NH, NKVH, Da, r, True, gc,
+                        P=16, Q=16, K=4)
+    with pytest.raises(RuntimeError, match="full recurrence"):  # not a short-window spec
+        F.scan_forward(values, logits, param, bias, NH, NKVH, Da, r, True, P=16, Q=100, K=4)
     with pytest.raises(RuntimeError, match="float32 with bfloat16"):
         F.scan_forward(values.float(), logits.float(), param.to(torch.bfloat16), bias, NH, NKVH,
                        Da, r, True)
