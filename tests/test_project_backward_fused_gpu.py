@@ -38,12 +38,18 @@ def _separate(N, lib, x, wpack, gc, H, D, Da):
     return gx, gw
 
 
-@pytest.mark.parametrize("B", [32, 40, 16], ids=lambda b: f"B{b}")
-def test_combined_backward_matches_separate_calls(B):
+@pytest.mark.parametrize("B,T,C", [(32, 1024, 768), (40, 1024, 768), (16, 1024, 768),
+                                   (1, 33000, 768), (3, 11000, 640)],
+                         ids=lambda v: str(v))
+def test_combined_backward_matches_separate_calls(B, T, C):
+    """(32, 1024): d12's 384 grad_x tiles; (40, 1024): 480 tiles, other piece
+    lengths; (16, 1024): 192 tiles, the two GEMMs one after the other;
+    (1, 33000): ragged last token tile and reduction (516 k-steps);
+    (3, 11000, 640): partial channel tiles."""
     from nanochat_amd import _native as N
     from nanochat_amd.ops import ltv_hm_fast as F_
     lib = N.lib()
-    T, C, NH, NKVH, D, Da = 1024, 768, 6, 6, 128, 1
+    NH, NKVH, D, Da = 6, 6, 128, 1
     H = NH + 2 * NKVH
     F = H * (D + Da)
     Fp = F_.packed_width(H, D, Da)
