@@ -461,11 +461,10 @@ int ltv_qkv_project_backward(const void* x, const void* wpack, void* grad_combin
  * F .. round_up(F, 8) - 1 are zero already (as for
  * ltv_qkv_project_backward_input_zero_padded): grad_combined is only read.
  * Both combined calls run grad_x and grad_weight's GEMM in one launch where
- * grad_x's 256 x 256 tiles take more than one and less than two rounds of the
- * device's compute units (d12: 384 tiles on 256): the compute units that run
- * one grad_x tile take longer pieces of grad_weight's split reduction than
- * those that run two (LTV_GEMM_BWD_FUSED=0 runs the two GEMMs one after the
- * other).  grad_x is bitwise that of ltv_qkv_project_backward_input;
+ * grad_x's 256 x 256 tiles do not fill their last round of the device's
+ * compute units (d12: 384 tiles on 256; B = 16: 192): the compute units with
+ * one grad_x tile fewer take longer pieces of grad_weight's split reduction
+ * (LTV_GEMM_BWD_FUSED=0 runs the two GEMMs one after the other).  grad_x is bitwise that of ltv_qkv_project_backward_input;
  * grad_weight sums the same products in fp32 over other split boundaries.
  * Counterpart in the reference: fused_linear_transpose_backward.cu:22-132
  * (both gradients of one call). */

@@ -850,9 +850,9 @@ extern "C" int ltv_qkv_project_backward_weight(const void* x, const void* grad_c
 
 namespace {
 // grad_x and grad_weight in one launch of gemm_dma_bwd_fused_kernel, where
-// grad_x's 256 x 256 tiles take more than one round of the persistent grid and
-// less than two: the workgroups that run one grad_x tile take the longer
-// pieces of grad_weight's reduction.  Returns LTV_OK when launched (with the
+// grad_x's 256 x 256 tiles do not fill their last round of the persistent grid:
+// the workgroups that run one grad_x tile fewer take the longer pieces of
+// grad_weight's reduction.  Returns LTV_OK when launched (with the
 // zeroing and reduction launches around it), 1 when the shapes or tunables
 // leave it out (nothing launched), or an error code.
 int project_backward_fused(const void* x, const void* wpack, void* grad_combined, void* grad_x,
@@ -894,9 +894,10 @@ int project_backward_fused(const void* x, const void* wpack, void* grad_combined
   // the plan
   const int G = device_cu_count();
   const int total_x = ax.tiles_i * ax.tiles_j;
-  if (total_x <= G || total_x >= 2 * G) return 1;
+  // workgroups [0, total_x % G) run one grad_x tile more than the others
+  if (total_x % G == 0) return 1;
   DwPlan p;
-  p.n_late = total_x - G;
+  p.n_late = total_x % G;
   const int n_early = G - p.n_late;
   p.nt = aw.tiles_i * aw.tiles_j;
   p.S = S;

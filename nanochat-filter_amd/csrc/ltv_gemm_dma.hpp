@@ -805,12 +805,12 @@ gemm_dma_kernel(const GemmArgs g, const Epi epi) {
 }
 
 // ---------------------------------------------------------------------------
-// The projection backward's two GEMMs in one persistent launch.  grad_x has
-// more tiles than the grid has workgroups but fewer than twice as many (384
-// on 256 CUs at d12), so one round of tiles leaves workgroups [n_late, G)
-// idle while [0, n_late) run their second tile.  Here every workgroup runs its
-// grad_x tiles and then one piece of grad_weight's split reduction, the
-// workgroups that finished grad_x a tile earlier taking the longer pieces:
+// The projection backward's two GEMMs in one persistent launch.  When grad_x's
+// tiles do not fill their last round of the grid (384 tiles on 256 CUs at
+// d12, 192 at B = 16), workgroups [n_late, G) sit idle while [0, n_late) run
+// their last tile.  Here every workgroup runs its grad_x tiles and then one
+// piece of grad_weight's split reduction, the workgroups that finished grad_x
+// a tile earlier taking the longer pieces:
 // each of grad_weight's nt output tiles keeps S partial slots (the layout
 // dw_reduce4_kernel sums), filled by e "early" pieces of a k-steps followed by
 // S - e "late" pieces of b = a - delta k-steps, the last of which ends the
@@ -818,7 +818,7 @@ gemm_dma_kernel(const GemmArgs g, const Epi epi) {
 // that the early pieces number exactly the early workgroups.
 // ---------------------------------------------------------------------------
 struct DwPlan {
-  int n_late;      // workgroups running two grad_x tiles (the rest run one)
+  int n_late;      // workgroups running one grad_x tile more than the rest
   int nt, S, x;    // grad_weight output tiles, slots per tile, tiles with e1 early pieces
   int e1, a1, b1;  // tiles [0, x): early pieces, their k-steps, late pieces' k-steps
   int e2, a2, b2;  // tiles [x, nt)
@@ -843,7 +843,7 @@ struct DwPlanItems {
     const int G = gridDim.x;
     const bool xcd = G % 8 == 0 && p.n_late % 8 == 0;
     int t, slot, k0, k1;
-    if (b >= p.n_late) {  // early: one grad_x tile before this piece
+    if (b >= p.n_late) {  // early: one grad_x tile fewer before this piece
       const int w = b - p.n_late, n = G - p.n_late;
       const int i = xcd ? (w % 8) * (n / 8) + w / 8 : w;
       int s;
@@ -859,7 +859,7 @@ struct DwPlanItems {
       slot = s;
       k0 = s * a;
       k1 = k0 + a;
-    } else {  // late: two grad_x tiles before this piece
+    } else {  // late
       const int i = xcd ? (b % 8) * (p.n_late / 8) + b / 8 : b;
       const int l1 = p.S - p.e1;  // late pieces of a tile with e1 early ones (one fewer than e2's)
       int j;

@@ -6,7 +6,8 @@ same kernel body and work items); grad_weight sums the same products over
 other split boundaries, so it is checked against the separate grad_weight
 call to fp32 summation accuracy and against a float64 product of the same
 bf16 operands.  Token counts where the fused launch applies with different
-plans (d12's 384 grad_x tiles, 480 tiles) and where it does not (192 tiles).
+plans (d12's 384 grad_x tiles, 480, 192) and where it does not (768: whole
+rounds).
 """
 
 from __future__ import annotations
@@ -39,11 +40,12 @@ def _separate(N, lib, x, wpack, gc, H, D, Da):
 
 
 @pytest.mark.parametrize("B,T,C", [(32, 1024, 768), (40, 1024, 768), (16, 1024, 768),
-                                   (1, 33000, 768), (3, 11000, 640)],
+                                   (64, 1024, 768), (1, 33000, 768), (3, 11000, 640)],
                          ids=lambda v: str(v))
 def test_combined_backward_matches_separate_calls(B, T, C):
     """(32, 1024): d12's 384 grad_x tiles; (40, 1024): 480 tiles, other piece
-    lengths; (16, 1024): 192 tiles, the two GEMMs one after the other;
+    lengths; (16, 1024): 192 tiles, a quarter of the CUs with no grad_x tile;
+    (64, 1024): 768 tiles, whole rounds, the two GEMMs one after the other;
     (1, 33000): ragged last token tile and reduction (516 k-steps);
     (3, 11000, 640): partial channel tiles."""
     from nanochat_amd import _native as N
