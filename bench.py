@@ -687,7 +687,9 @@ def prefill_main(args):
                    "head_dim": D, "r": R, "parallelism": "single GPU"},
         "roofline": {"kernel": dominant, "bound": dk_["bound"], "achieved": dk_["achieved"],
                      "peak": dk_["peak"], "unit": dk_["unit"], "frac": dk_["frac"],
-                     "traffic": traffic, "traffic_source": traffic_src},
+                     "traffic": traffic, "traffic_source": traffic_src,
+                     "peak_measured": dk_["peak_measured"], "frac_measured": dk_["frac_measured"],
+                     "peak_measured_source": "profiles/peaks.json"},
         "kernels": kernels,
     }
     emit(out)
@@ -811,7 +813,11 @@ def decode_main(args):
                   "us_per_step": round(graph_s * 1e6 / (args.steps * DC_N), 2)},
         "roofline": {"kernel": "qkv_decode", "bound": "hbm", "achieved": round(ach, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4),
-                     "traffic": None, "avg_us": round(avg_us, 2), "work_per_launch": nbytes},
+                     "traffic": None, "avg_us": round(avg_us, 2), "work_per_launch": nbytes,
+                     "peak_measured": measured_peak("qkv_decode", "hbm"),
+                     "frac_measured": (round(ach / measured_peak("qkv_decode", "hbm"), 4)
+                                       if measured_peak("qkv_decode", "hbm") else None),
+                     "peak_measured_source": "profiles/peaks.json"},
     }
     emit(out)
 
