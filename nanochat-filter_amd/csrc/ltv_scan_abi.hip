@@ -401,6 +401,18 @@ int check_tile_offsets(const char* what, const int64_t* s, int64_t chan_extent, 
 inline ScanCfg bwd_default_cfg(int cl, bool vec) {
   return vec && cl == 16 ? ScanCfg{16, 4, 2} : ScanCfg{cl, 4, 4};
 }
+// The whole-head tile backward at 16 vector lanes: 2 wavefronts per workgroup
+// where that keeps the grid to one round of resident workgroups (four per CU
+// at two wavefronts per SIMD) and 4 wavefronts would need two; 4 otherwise.
+// Measured on MI355X (heads of 128, bf16, T = 1024; sequences = B H): B = 16
+// (288 sequences) 85.3 -> 75.1 us with 4 wavefronts, B = 32 (576) 113.8 ->
+// 117.5 us, B = 48 (864) 151.3 -> 153.4 us, B = 64 (1152) 232.7 -> 214.1 us.
+inline ScanCfg bwd_tile_cfg(int cl, bool vec, int64_t nseq) {
+  ScanCfg c = bwd_default_cfg(cl, vec);
+  const int64_t slots = (int64_t)scan_cu_count() * 2;  // 4-wavefront workgroups per round
+  if (c.CL == 16 && c.NW == 2 && (nseq <= slots || nseq > 2 * slots)) c.NW = 4;
+  return c;
+}
 
 // Bytes from a view's first to its last element, (B, NX, T, X) elements
 // (non-negative strides, checked by check_tile_offsets).
@@ -1074,7 +1086,7 @@ int scan_backward_impl(int dtype, const HostView4& u, const HostView4& lg, const
   }
   if (gm >= 0) {
     // whole head per workgroup
-    ScanCfg cfg = bwd_default_cfg(next_pow2((D + V - 1) / V), vec);
+    ScanCfg cfg = bwd_tile_cfg(next_pow2((D + V - 1) / V), vec, (int64_t)B * H);
     const ScanTuning& tu = tuning();
     if (vec && tu.bwd_l > 0) {
       cfg.L = tu.bwd_l;
