@@ -1,7 +1,7 @@
 """Benchmark of the LTV combined-QKV filter path on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
-                    [--workload filter|look_back|gpt|scan_fwd|prefill|decode]
+                    [--workload filter|look_back|gpt|scan_fwd|prefill|decode|peaks|lt_f32]
 
 Workload (the d12 training shape): x bf16
 [32, 1024, 768] ~ N(0, 1); c.weight [2322, 768] fp32 ~ N(0, 1/768) (value rows
@@ -25,7 +25,9 @@ prefill`` is configs[4]'s prefill: one forward of the filter at B = 8,
 T = 8192 with long-memory decays (tokens / s).  ``--workload decode`` is
 configs[4]'s decode: 256 single-token steps at B = 64 through the KV-cache
 protocol after a 16-token prefill (tokens / s through the module), and the same
-256 steps replayed from a captured HIP graph.
+256 steps replayed from a captured HIP graph.  ``--workload lt_f32`` is the
+filter's fp32 path's projection (the reference-layout ``fused_linear_transpose``,
+forward and both gradients) at configs[2]'s shapes, in TFLOP/s.
 
 Printed as one JSON line, with
   roofline     -- the dominant kernel's algorithmic bytes (or FLOPs) per launch
@@ -56,6 +58,7 @@ COPY_CAL_BYTES = 256 << 20
 # published MI355X peaks
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
+F32_MFMA_PEAK_TFLOPS = 157.3
 
 B, T, C = 32, 1024, 768
 NH = NKVH = 6
@@ -199,7 +202,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--workload",
                     choices=("filter", "look_back", "gpt", "scan_fwd", "prefill", "decode",
-                             "peaks"),
+                             "peaks", "lt_f32"),
                     default="filter",
                     help="filter: BASELINE.json configs[2] (the default, the metric's workload); "
                          "look_back: the same shapes through the look-back filter with the d12 "
@@ -210,7 +213,9 @@ def main():
                          "(GB/s); prefill: configs[4]'s prefill, the filter forward at B=8, "
                          "T=8192 with decay sigmoid(N(3, 1.5)) (tokens/s); "
                          "peaks: the measured roofline peaks (MFMA loop, HBM streams in the "
-                         "scan's access shape, the library GEMM on the projection's shapes)")
+                         "scan's access shape, the library GEMM on the projection's shapes); "
+                         "lt_f32: the filter's fp32 path's projection, fused_linear_transpose "
+                         "forward + backward at configs[2]'s shapes (TFLOP/s)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="after the timed region, run a plain device copy of 256 MiB five times "
                          "(the known-size reference for rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -235,6 +240,9 @@ def main():
         return
     if args.workload == "peaks":
         peaks_main(args)
+        return
+    if args.workload == "lt_f32":
+        lt_f32_main(args)
         return
 
     import torch
@@ -482,6 +490,131 @@ def peaks_main(args):
                      "shape": [list(sa), list(sb)]}
         del a_, b_
     emit(out)
+
+
+def lt_f32_main(args):
+    """The filter's fp32 path projects through the reference-layout op
+    ``fused_linear_transpose`` (x (B, T, C) . W (F, C)^T -> (B, F, T)).  One
+    step at configs[2]'s shapes is its forward and both gradients from a
+    (B, F, T) grad_out, through the ops the fp32 filter's autograd calls (the
+    backward with its split workspace); value is the step's TFLOP/s (3 GEMMs
+    of 2 B T C F FLOP), the roofline the forward GEMM against the fp32 MFMA
+    peak, with the library GEMM (torch.matmul, hipBLASLt) on the forward's
+    shape beside it."""
+    import torch
+    from nanochat_amd import _native as N
+    import nanochat_amd.ops  # noqa: F401
+
+    ops = torch.ops.nanochat_cuda
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(0)
+    x = torch.randn((B, T, C), generator=g, device=dev)
+    w = torch.randn((F, C), generator=g, device=dev) / C ** 0.5
+    go = torch.randn((B, F, T), generator=g, device=dev)
+    gx, gw = torch.empty_like(x), torch.empty_like(w)
+
+    def step():
+        ops.fused_linear_transpose_cuda_op(x, w)
+        ops.fused_linear_transpose_backward_kernel(x, w, go, gx, gw)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    with N.KernelRecorder() as rec:
+        for _ in range(args.steps):
+            step()
+        torch.cuda.synchronize()
+    flop = 2.0 * B * T * C * F
+    durs = rec.durations_ms()
+    spans = {}
+    for name, n_gemm in (("linear_transpose_fwd", 1), ("linear_transpose_bwd", 2)):
+        ms = durs[name]
+        avg = sum(ms) / len(ms)
+        ach = n_gemm * flop / (avg * 1e-3) / 1e12
+        spans[name] = {"avg_us": round(avg * 1e3, 2), "launches": len(ms),
+                       "achieved": round(ach, 1), "peak": F32_MFMA_PEAK_TFLOPS,
+                       "unit": "TFLOP/s", "frac": round(ach / F32_MFMA_PEAK_TFLOPS, 4),
+                       "work_per_launch": n_gemm * flop}
+    # the library GEMM on the forward's shape (same operands, fp32)
+    lib_ms = []
+    for _ in range(args.steps + 2):
+        a_, b_ = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a_.record()
+        torch.matmul(w, x.transpose(1, 2))
+        b_.record()
+        b_.synchronize()
+        lib_ms.append(a_.elapsed_time(b_))
+    lib_ms = sorted(lib_ms[2:])
+    lib_t = lib_ms[len(lib_ms) // 2] * 1e-3
+    fw = spans["linear_transpose_fwd"]
+    out = {
+        "metric": "fp32 reference-layout projection (fused_linear_transpose fwd + bwd) TFLOP/s, "
+                  "configs[2] shapes x (32, 1024, 768) . W (2322, 768)^T",
+        "value": round(3 * flop * args.steps / elapsed / 1e12, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(elapsed * 1e3 / args.steps, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": "fp32 path projection at configs[2] shapes (B=32, T=1024, "
+                               "C=768, F=2322)",
+                   "B": B, "T": T, "K": C, "F": F, "parallelism": "single GPU"},
+        "roofline": {"kernel": "linear_transpose_fwd (gemm_f32m_kernel)", "bound": "mfma",
+                     "achieved": fw["achieved"], "peak": F32_MFMA_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": fw["frac"], "traffic": None,
+                     "avg_us": fw["avg_us"], "work_per_launch": flop},
+        "spans": spans,
+        "library_gemm_fwd": {"tflops": round(flop / lib_t / 1e12, 1), "us": round(lib_t * 1e6, 1),
+                             "what": "torch.matmul(W, x^T), fp32 (hipBLASLt)"},
+    }
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = lt_f32_cpu_baseline(args.cpu_seconds)
+    emit(out)
+
+
+def lt_f32_cpu_baseline(seconds_target: float):
+    """The oracle's projection forward + backward (numpy, float64 accumulation)
+    on one of the 32 sequences, repeated for about ``seconds_target``."""
+    import numpy as np
+    from threadpoolctl import threadpool_limits
+
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import ltv_oracle as O
+
+    cores = len(os.sched_getaffinity(0))
+    rng = np.random.default_rng(0)
+    x = rng.standard_normal((1, T, C), dtype=np.float32)
+    w = (rng.standard_normal((F, C)) / np.sqrt(C)).astype(np.float32)
+    go = rng.standard_normal((1, F, T), dtype=np.float32)
+    reps = 0
+    t0 = time.perf_counter()
+    with threadpool_limits(limits=cores):
+        while True:
+            O.linear_transpose_forward(x, w, "f32")
+            O.linear_transpose_backward(x, w, go, "f32")
+            reps += 1
+            el = time.perf_counter() - t0
+            if el >= seconds_target:
+                break
+    return {
+        "value": round(3 * 2.0 * T * C * F * reps / el / 1e12, 4),
+        "unit": "TFLOP/s",
+        "cores": cores,
+        "cpu": cpu_model(),
+        "kind": "port",
+        "sample": f"{reps} x fwd+bwd of 1 sequence (T={T}, C={C}, F={F}), numpy float64 "
+                  f"accumulation, {el:.1f} s",
+    }
 
 
 def scan_fwd_bytes():

@@ -383,8 +383,10 @@ int ltv_hm_look_back_scan_backward_split_ws(
  *
  * x (B, T, K), weight (F, K), out (B, F, T): all contiguous, all `dtype`.
  * bf16 with T a multiple of 256 and K of 8 (16-byte aligned buffers) runs on
- * bf16 MFMA (fp32 accumulation) and writes the (B, F, T) layout directly; other
- * shapes and fp32 run a SIMT fp32-accumulation kernel.
+ * bf16 MFMA (fp32 accumulation) and writes the (B, F, T) layout directly; fp32
+ * and the other bf16 shapes run on fp32 MFMA (v_mfma_f32_32x32x2_f32, fp32
+ * accumulation, any sizes and alignment).  x and weight may be NULL when
+ * K = 0 (out is then zeros).
  * Replaces fused_linear_transpose (cpp_ewma/src/fused_linear_transpose_forward.cu:23-58,
  * called from nanochat/ops/fused_linear_transpose.py:20-40).
  * ---------------------------------------------------------------------- */
@@ -396,19 +398,22 @@ int ltv_linear_transpose_forward(int dtype, const void* x, const void* weight, v
  * `dtype`, fp32 accumulation).
  * grad_out is (B, F, T) contiguous, or its (B, T, F)-contiguous transpose
  * when grad_out_is_btf != 0 (the two layouts the reference accepts,
- * nanochat/ops/fused_linear_transpose.py:76-84).
+ * nanochat/ops/fused_linear_transpose.py:76-84).  Runs on fp32 MFMA, the
+ * weight gradient in one pass per output tile.  Pointers of tensors with no
+ * elements may be NULL.
  * Replaces fused_linear_transpose_backward
  * (cpp_ewma/src/fused_linear_transpose_backward.cu:22-132). */
 int ltv_linear_transpose_backward(int dtype, const void* x, const void* weight,
                                   const void* grad_out, int grad_out_is_btf, void* grad_x,
                                   void* grad_weight, int B, int T, int K, int F, void* stream);
 
-/* The same backward with a workspace: bf16 with grad_out (B, F, T) contiguous,
- * T a multiple of 256 and K of 8 (16-byte aligned buffers) runs both GEMMs on
- * bf16 MFMA -- grad_x directly, grad_weight as fp32 split partials in the
- * workspace summed in a fixed order (deterministic) -- and needs
- * ltv_linear_transpose_backward_workspace_size bytes; every other case runs
- * ltv_linear_transpose_backward (workspace size 0, workspace may be NULL).
+/* The same backward with a workspace for grad_weight's reduction over B T,
+ * split into fp32 partials summed in a fixed order (deterministic): bf16 with
+ * grad_out (B, F, T) contiguous, T a multiple of 256 and K of 8 (16-byte
+ * aligned buffers) runs both GEMMs on bf16 MFMA; every other case on fp32
+ * MFMA, its weight gradient split when the workspace holds
+ * ltv_linear_transpose_backward_workspace_size bytes (0: no split, and the
+ * workspace may be NULL).
  * Same contract and counterpart as ltv_linear_transpose_backward. */
 size_t ltv_linear_transpose_backward_workspace_size(int dtype, int B, int T, int K, int F,
                                                     int grad_out_is_btf);

@@ -1,6 +1,7 @@
 // Fused QKV projection for gfx950: bf16 MFMA GEMMs (fp32 accumulate) for the
-// filter module's fast path, and a strided SIMT GEMM for the reference-layout
-// fused_linear_transpose op (fp32 or bf16 I/O).
+// filter module's fast path, and the reference-layout fused_linear_transpose
+// op (fp32 or bf16 I/O) on the bf16 direct-to-LDS kernels where its layout
+// allows, else on the strided fp32-MFMA GEMM of ltv_gemm_f32.hpp.
 //
 // Reference: cpp_ewma/src/fused_linear_transpose_forward.cu:23-58 (one
 // strided-batched GEMM, out[b] = W x[b]^T written (B, F, T)) and
@@ -17,6 +18,7 @@
 #include "ltv_device.hpp"
 #include "ltv_abi_internal.hpp"
 #include "ltv_gemm_dma.hpp"
+#include "ltv_gemm_f32.hpp"
 
 #include <stdio.h>
 #include <stdlib.h>
@@ -190,81 +192,6 @@ dw_reduce4_kernel(const float4* __restrict__ part, float4* __restrict__ gw, int 
   }
 }
 
-// ---------------------------------------------------------------------------
-// Strided SIMT GEMM (any layout, fp32 or bf16 in, fp32 accumulate):
-//   C(m, n) = sum_kk A(m, kk) B(n, kk)
-// where the reduction index kk = ko * kin + ki addresses
-//   A + m*sam + ko*sako + ki*saki,  B + n*sbn + ko*sbko + ki*sbki,
-// and blockIdx.z selects a batch (a/b/c batch strides).  64 x 64 tiles,
-// 256 threads with 4 x 4 outputs each.
-// ---------------------------------------------------------------------------
-struct SimtArgs {
-  const void* A;
-  int64_t sam, sako, saki, sab;
-  const void* B;
-  int64_t sbn, sbko, sbki, sbb;
-  void* C;
-  int64_t scm, scn, scb;
-  int M, N, K, kin;
-};
-
-template <typename TI, typename TO>
-__global__ void __launch_bounds__(256) gemm_simt_kernel(const SimtArgs g) {
-  constexpr int BM = 64, BN = 64, BK = 16;
-  __shared__ float sa[BK][BM + 1];
-  __shared__ float sb[BK][BN + 1];
-  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
-  const int z = blockIdx.z;
-  const TI* A = reinterpret_cast<const TI*>(g.A) + (int64_t)z * g.sab;
-  const TI* B = reinterpret_cast<const TI*>(g.B) + (int64_t)z * g.sbb;
-  const int tx = threadIdx.x % 16, ty = threadIdx.x / 16;
-  float acc[4][4] = {};
-  for (int k0 = 0; k0 < g.K; k0 += BK) {
-    for (int e = threadIdx.x; e < BK * BM; e += 256) {
-      const int kk = e / BM, mm = e % BM;
-      const int m = m0 + mm, k = k0 + kk;
-      float v = 0.0f;
-      if (m < g.M && k < g.K) {
-        const int ko = k / g.kin, ki = k % g.kin;
-        v = io_traits<TI>::load(A + (int64_t)m * g.sam + (int64_t)ko * g.sako + (int64_t)ki * g.saki);
-      }
-      sa[kk][mm] = v;
-    }
-    for (int e = threadIdx.x; e < BK * BN; e += 256) {
-      const int kk = e / BN, nn = e % BN;
-      const int n = n0 + nn, k = k0 + kk;
-      float v = 0.0f;
-      if (n < g.N && k < g.K) {
-        const int ko = k / g.kin, ki = k % g.kin;
-        v = io_traits<TI>::load(B + (int64_t)n * g.sbn + (int64_t)ko * g.sbko + (int64_t)ki * g.sbki);
-      }
-      sb[kk][nn] = v;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int kk = 0; kk < BK; ++kk) {
-      float av[4], bv[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) av[i] = sa[kk][ty + 16 * i];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) bv[j] = sb[kk][tx + 16 * j];
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(av[i], bv[j], acc[i][j]);
-    }
-    __syncthreads();
-  }
-  TO* C = reinterpret_cast<TO*>(g.C) + (int64_t)z * g.scb;
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int m = m0 + ty + 16 * i, n = n0 + tx + 16 * j;
-      if (m < g.M && n < g.N) io_traits<TO>::store(C + (int64_t)m * g.scm + (int64_t)n * g.scn, acc[i][j]);
-    }
-}
-
 }  // namespace ltv
 
 // ===========================================================================
@@ -274,17 +201,72 @@ using namespace ltv;
 
 namespace {
 
-int launch_simt(int dtype_in, int dtype_out, const SimtArgs& a, int batches, hipStream_t st) {
-  if (a.M == 0 || a.N == 0 || batches == 0) return LTV_OK;
-  dim3 grid((a.N + 63) / 64, (a.M + 63) / 64, batches);
-  if (dtype_in == LTV_DTYPE_F32 && dtype_out == LTV_DTYPE_F32)
-    hipLaunchKernelGGL((gemm_simt_kernel<float, float>), grid, dim3(256), 0, st, a);
-  else if (dtype_in == LTV_DTYPE_BF16 && dtype_out == LTV_DTYPE_BF16)
-    hipLaunchKernelGGL((gemm_simt_kernel<bf16_t, bf16_t>), grid, dim3(256), 0, st, a);
-  else if (dtype_in == LTV_DTYPE_BF16 && dtype_out == LTV_DTYPE_F32)
-    hipLaunchKernelGGL((gemm_simt_kernel<bf16_t, float>), grid, dim3(256), 0, st, a);
+// Staging form of one operand of the fp32-MFMA GEMM (row stride sr, reduction
+// strides sko / ski, batch stride sbatch): quads need 4-element-aligned
+// starts, and a KQ quad must not straddle two outer reduction indices.
+int f32m_stage(const void* p, int64_t sr, int64_t sko, int64_t ski, int64_t sbatch, int batches,
+               int kin, int K, int esize) {
+  const bool aligned =
+      (reinterpret_cast<uintptr_t>(p) % (uintptr_t)(4 * esize)) == 0 &&
+      (batches <= 1 || sbatch % 4 == 0);
+  const bool outer = kin < K;
+  if (aligned && ski == 1 && sr % 4 == 0 && (!outer || (kin % 4 == 0 && sko % 4 == 0)))
+    return kF32KQ;
+  if (aligned && sr == 1 && ski % 4 == 0 && (!outer || sko % 4 == 0)) return kF32MQ;
+  return kF32SC;
+}
+
+template <typename TI, typename TO, int LA>
+void f32m_launch_b(int lb, const F32mArgs& a, dim3 grid, hipStream_t st) {
+  if (lb == kF32KQ)
+    hipLaunchKernelGGL((gemm_f32m_kernel<TI, TO, LA, kF32KQ>), grid, dim3(256), 0, st, a);
+  else if (lb == kF32MQ)
+    hipLaunchKernelGGL((gemm_f32m_kernel<TI, TO, LA, kF32MQ>), grid, dim3(256), 0, st, a);
   else
-    hipLaunchKernelGGL((gemm_simt_kernel<float, bf16_t>), grid, dim3(256), 0, st, a);
+    hipLaunchKernelGGL((gemm_f32m_kernel<TI, TO, LA, kF32SC>), grid, dim3(256), 0, st, a);
+}
+
+template <typename TI, typename TO>
+void f32m_launch_ab(int la, int lb, const F32mArgs& a, dim3 grid, hipStream_t st) {
+  if (la == kF32KQ)
+    f32m_launch_b<TI, TO, kF32KQ>(lb, a, grid, st);
+  else if (la == kF32MQ)
+    f32m_launch_b<TI, TO, kF32MQ>(lb, a, grid, st);
+  else
+    f32m_launch_b<TI, TO, kF32SC>(lb, a, grid, st);
+}
+
+// C (dtype_out; fp32 for split partials) = A . B^T over `batches` batches and
+// `splits` reduction splits of k_split indices each (splits = 1: k_split is
+// ignored), on the fp32-MFMA GEMM.
+int launch_f32m(int dtype_in, int dtype_out, F32mArgs a, int batches, int splits, int k_split,
+                hipStream_t st) {
+  if (a.M == 0 || a.N == 0 || batches == 0) return LTV_OK;
+  LTV_REQUIRE((dtype_in == LTV_DTYPE_F32 && dtype_out == LTV_DTYPE_F32) ||
+                  (dtype_in == LTV_DTYPE_BF16 &&
+                   (dtype_out == LTV_DTYPE_BF16 || dtype_out == LTV_DTYPE_F32)),
+              LTV_ERR_UNSUPPORTED, "fp32-MFMA GEMM: unsupported dtypes %d -> %d", dtype_in,
+              dtype_out);
+  a.splits = std::max(1, splits);
+  a.k_split = a.splits == 1 ? a.K : k_split;
+  LTV_REQUIRE(a.splits == 1 || (a.k_split > 0 && a.k_split % kF32BK == 0 &&
+                                (int64_t)a.k_split * a.splits >= a.K),
+              LTV_ERR_INVALID_ARG, "bad reduction split (%d x %d for K = %d)", a.splits,
+              a.k_split, a.K);
+  const int64_t gy = (a.M + kF32B - 1) / kF32B, gz = (int64_t)batches * a.splits;
+  LTV_REQUIRE(gy <= 65535 && gz <= 65535, LTV_ERR_UNSUPPORTED,
+              "fp32-MFMA GEMM grid too large (%lld row tiles, %lld batches x splits)",
+              (long long)gy, (long long)gz);
+  const dim3 grid((a.N + kF32B - 1) / kF32B, (unsigned)gy, (unsigned)gz);
+  const int es = dtype_in == LTV_DTYPE_BF16 ? 2 : 4;
+  const int la = f32m_stage(a.A, a.sam, a.sako, a.saki, a.sab, batches, a.kin, a.K, es);
+  const int lb = f32m_stage(a.B, a.sbn, a.sbko, a.sbki, a.sbb, batches, a.kin, a.K, es);
+  if (dtype_in == LTV_DTYPE_F32)
+    f32m_launch_ab<float, float>(la, lb, a, grid, st);
+  else if (dtype_out == LTV_DTYPE_BF16)
+    f32m_launch_ab<bf16_t, bf16_t>(la, lb, a, grid, st);
+  else
+    f32m_launch_ab<bf16_t, float>(la, lb, a, grid, st);
   LTV_LAUNCH_CHECK();
   return LTV_OK;
 }
@@ -395,8 +377,6 @@ const GemmTuning& gemm_tuning() {
 
 inline int round_up(int x, int m) { return (x + m - 1) / m * m; }
 
-inline int dsize(int dtype) { return dtype == LTV_DTYPE_BF16 ? 2 : 4; }
-
 }  // namespace
 
 extern "C" int ltv_linear_transpose_forward(int dtype, const void* x, const void* weight,
@@ -406,7 +386,8 @@ extern "C" int ltv_linear_transpose_forward(int dtype, const void* x, const void
               "dtype must be LTV_DTYPE_F32 or LTV_DTYPE_BF16, got %d", dtype);
   LTV_REQUIRE(B >= 0 && T >= 0 && K >= 0 && F >= 0, LTV_ERR_INVALID_ARG, "negative size");
   if ((int64_t)B * T * F == 0) return LTV_OK;
-  LTV_REQUIRE(x && weight && out, LTV_ERR_INVALID_ARG, "null tensor pointer");
+  // an empty reduction (K = 0) reads neither operand and writes zeros
+  LTV_REQUIRE(out && (K == 0 || (x && weight)), LTV_ERR_INVALID_ARG, "null tensor pointer");
   hipStream_t st = (hipStream_t)stream;
   if (dtype == LTV_DTYPE_BF16 && gemm_tuning().dma && T % 256 == 0 && K % 8 == 0 && K > 0 &&
       aligned16(x) && aligned16(weight) && aligned16(out) && (int64_t)B * T < (1ll << 31)) {
@@ -428,51 +409,17 @@ extern "C" int ltv_linear_transpose_forward(int dtype, const void* x, const void
     }
   }
   // per batch: out_b (F x T) = W (F x K) . x_b^T
-  SimtArgs a;
+  F32mArgs a{};
   a.A = weight; a.sam = K; a.sako = 0; a.saki = 1; a.sab = 0;
   a.B = x; a.sbn = K; a.sbko = 0; a.sbki = 1; a.sbb = (int64_t)T * K;
   a.C = out; a.scm = T; a.scn = 1; a.scb = (int64_t)F * T;
   a.M = F; a.N = T; a.K = K; a.kin = K > 0 ? K : 1;
-  return launch_simt(dtype, dtype, a, B, st);
-}
-
-extern "C" int ltv_linear_transpose_backward(int dtype, const void* x, const void* weight,
-                                             const void* grad_out, int grad_out_is_btf,
-                                             void* grad_x, void* grad_weight, int B, int T,
-                                             int K, int F, void* stream) {
-  LTV_REQUIRE(dtype == LTV_DTYPE_F32 || dtype == LTV_DTYPE_BF16, LTV_ERR_INVALID_ARG,
-              "dtype must be LTV_DTYPE_F32 or LTV_DTYPE_BF16, got %d", dtype);
-  LTV_REQUIRE(B >= 0 && T >= 0 && K >= 0 && F >= 0, LTV_ERR_INVALID_ARG, "negative size");
-  LTV_REQUIRE(x && weight && grad_out && grad_x && grad_weight, LTV_ERR_INVALID_ARG,
-              "null tensor pointer");
-  hipStream_t st = (hipStream_t)stream;
-  // grad_out element (b, f, t): (B,F,T) -> b*F*T + f*T + t ; (B,T,F) -> b*T*F + t*F + f
-  const int64_t go_f = grad_out_is_btf ? 1 : T;
-  const int64_t go_t = grad_out_is_btf ? F : 1;
-  // grad_x_b (T x K) = sum_f go_b(f, t) W(f, k)
-  SimtArgs a;
-  a.A = grad_out; a.sam = go_t; a.sako = 0; a.saki = go_f; a.sab = (int64_t)F * T;
-  a.B = weight; a.sbn = 1; a.sbko = 0; a.sbki = K; a.sbb = 0;
-  a.C = grad_x; a.scm = K; a.scn = 1; a.scb = (int64_t)T * K;
-  a.M = T; a.N = K; a.K = F; a.kin = F > 0 ? F : 1;
-  int rc = launch_simt(dtype, dtype, a, B, st);
-  if (rc) return rc;
-  // grad_W (F x K) = sum_{b,t} go(b, f, t) x(b, t, k); reduction index kk = b*T + t
-  SimtArgs w;
-  w.A = grad_out; w.sam = go_f; w.sako = (int64_t)F * T; w.saki = go_t; w.sab = 0;
-  w.B = x; w.sbn = 1; w.sbko = (int64_t)T * K; w.sbki = K; w.sbb = 0;
-  w.C = grad_weight; w.scm = K; w.scn = 1; w.scb = 0;
-  w.M = F; w.N = K; w.K = B * T; w.kin = T > 0 ? T : 1;
-  if (w.K == 0) {
-    LTV_HIP_CHECK(hipMemsetAsync(grad_weight, 0, (size_t)F * K * dsize(dtype), st));
-    return LTV_OK;
-  }
-  return launch_simt(dtype, dtype, w, 1, st);
+  return launch_f32m(dtype, dtype, a, B, 1, 0, st);
 }
 
 namespace {
-// The bf16 MFMA path of the reference-layout backward: grad_out (B, F, T)
-// contiguous, T a multiple of the 256-token tile, K a multiple of 8.
+// The bf16 direct-to-LDS path of the reference-layout backward: grad_out
+// (B, F, T) contiguous, T a multiple of the 256-token tile, K a multiple of 8.
 bool lt_backward_mfma(int dtype, int is_btf, int B, int T, int K, int F) {
   return dtype == LTV_DTYPE_BF16 && !is_btf && gemm_tuning().dma && T % 256 == 0 && K % 8 == 0 &&
          K > 0 && F > 0 && (int64_t)B * T < (1ll << 31) && (int64_t)B * F * T < kDmaMaxSpan &&
@@ -493,12 +440,112 @@ LtSplits lt_splits(int M, int K, int F) {
   p.S = std::max(1, (M + p.rows - 1) / p.rows);
   return p;
 }
+
+// grad_weight's split over the B T reduction on the fp32-MFMA GEMM.  With
+// `slots` workgroups resident at once (two per CU) and `tiles` 128 x 128
+// output tiles, S splits take ceil(tiles S / slots) rounds of M / S
+// reduction indices each: S minimises rounds / S (the smallest S within 4%
+// of the best, up to 32 splits of at least 256 indices).  At d12 (114 tiles,
+// 512 slots) S = 13: 1,482 items in 3 rounds (S = 5 leaves 58 items for a
+// second round, S = 4 a quarter of the slots idle).  S = 1 needs no workspace.
+LtSplits lt_f32m_splits(int M, int K, int F) {
+  LtSplits p;
+  p.Fr = F;
+  const int tiles = std::max(1, ((K + kF32B - 1) / kF32B) * ((F + kF32B - 1) / kF32B));
+  const int slots = 2 * device_cu_count();
+  auto cost = [&](int s) { return (double)((tiles * s + slots - 1) / slots) / s; };
+  double best = cost(1);
+  int smax = 1;
+  for (int s = 2; s <= 32 && (M + s - 1) / s >= 256; ++s) {
+    best = std::min(best, cost(s));
+    smax = s;
+  }
+  int S = 1;
+  while (S < smax && cost(S) > 1.04 * best) ++S;
+  p.rows = std::max(kF32BK, round_up((M + S - 1) / S, kF32BK));
+  p.S = std::max(1, (M + p.rows - 1) / p.rows);
+  return p;
+}
+
+// Only tensors with no elements may be null (PyTorch hands those over as 0).
+bool lt_backward_pointers_ok(const void* x, const void* weight, const void* grad_out,
+                             const void* grad_x, const void* grad_weight, int B, int T, int K,
+                             int F) {
+  const int64_t nx = (int64_t)B * T * K, nw = (int64_t)F * K, ng = (int64_t)B * F * T;
+  return (x || nx == 0) && (grad_x || nx == 0) && (weight || nw == 0) &&
+         (grad_weight || nw == 0) && (grad_out || ng == 0);
+}
+
+size_t lt_f32m_workspace(int B, int T, int K, int F) {
+  const LtSplits p = lt_f32m_splits(B * T, K, F);
+  return p.S > 1 ? (size_t)p.S * F * K * sizeof(float) : 0;
+}
+
+// Both gradients on the fp32-MFMA GEMM.  grad_weight is split over the B T
+// reduction into fp32 partials in `workspace` when it holds
+// lt_f32m_workspace() bytes (then summed in a fixed order), else computed in
+// one pass per output tile.
+int lt_backward_f32m(int dtype, const void* x, const void* weight, const void* grad_out,
+                     int grad_out_is_btf, void* grad_x, void* grad_weight, void* workspace,
+                     size_t workspace_bytes, int B, int T, int K, int F, hipStream_t st) {
+  // grad_out element (b, f, t): (B,F,T) -> b*F*T + f*T + t ; (B,T,F) -> b*T*F + t*F + f
+  const int64_t go_f = grad_out_is_btf ? 1 : T;
+  const int64_t go_t = grad_out_is_btf ? F : 1;
+  // grad_x_b (T x K) = sum_f go_b(f, t) W(f, k)
+  F32mArgs a{};
+  a.A = grad_out; a.sam = go_t; a.sako = 0; a.saki = go_f; a.sab = (int64_t)F * T;
+  a.B = weight; a.sbn = 1; a.sbko = 0; a.sbki = K; a.sbb = 0;
+  a.C = grad_x; a.scm = K; a.scn = 1; a.scb = (int64_t)T * K;
+  a.M = T; a.N = K; a.K = F; a.kin = F > 0 ? F : 1;
+  int rc = launch_f32m(dtype, dtype, a, B, 1, 0, st);
+  if (rc) return rc;
+  // grad_W (F x K) = sum_{b,t} go(b, f, t) x(b, t, k); reduction index kk = b*T + t
+  // (an empty reduction, B T = 0, stores zeros)
+  F32mArgs w{};
+  w.A = grad_out; w.sam = go_f; w.sako = (int64_t)F * T; w.saki = go_t; w.sab = 0;
+  w.B = x; w.sbn = 1; w.sbko = (int64_t)T * K; w.sbki = K; w.sbb = 0;
+  w.C = grad_weight; w.scm = K; w.scn = 1; w.scb = 0;
+  w.M = F; w.N = K; w.K = B * T; w.kin = T > 0 ? T : 1;
+  const LtSplits sp = lt_f32m_splits(w.K, K, F);
+  const size_t need = lt_f32m_workspace(B, T, K, F);
+  if (need == 0 || workspace == nullptr || workspace_bytes < need)
+    return launch_f32m(dtype, dtype, w, 1, 1, 0, st);
+  w.C = workspace;
+  w.scs = (int64_t)F * K;
+  rc = launch_f32m(dtype, LTV_DTYPE_F32, w, 1, sp.S, sp.rows, st);
+  if (rc) return rc;
+  const int64_t n = (int64_t)F * K;
+  const int blocks = (int)std::min<int64_t>((n + 255) / 256, 8192);
+  if (dtype == LTV_DTYPE_F32)
+    hipLaunchKernelGGL(reduce_splits_kernel<float>, dim3(blocks), dim3(256), 0, st,
+                       reinterpret_cast<const float*>(workspace),
+                       reinterpret_cast<float*>(grad_weight), sp.S, n, n);
+  else
+    hipLaunchKernelGGL(reduce_splits_kernel<bf16_t>, dim3(blocks), dim3(256), 0, st,
+                       reinterpret_cast<const float*>(workspace),
+                       reinterpret_cast<bf16_t*>(grad_weight), sp.S, n, n);
+  LTV_LAUNCH_CHECK();
+  return LTV_OK;
+}
 }  // namespace
+
+extern "C" int ltv_linear_transpose_backward(int dtype, const void* x, const void* weight,
+                                             const void* grad_out, int grad_out_is_btf,
+                                             void* grad_x, void* grad_weight, int B, int T,
+                                             int K, int F, void* stream) {
+  LTV_REQUIRE(dtype == LTV_DTYPE_F32 || dtype == LTV_DTYPE_BF16, LTV_ERR_INVALID_ARG,
+              "dtype must be LTV_DTYPE_F32 or LTV_DTYPE_BF16, got %d", dtype);
+  LTV_REQUIRE(B >= 0 && T >= 0 && K >= 0 && F >= 0, LTV_ERR_INVALID_ARG, "negative size");
+  LTV_REQUIRE(lt_backward_pointers_ok(x, weight, grad_out, grad_x, grad_weight, B, T, K, F),
+              LTV_ERR_INVALID_ARG, "null tensor pointer");
+  return lt_backward_f32m(dtype, x, weight, grad_out, grad_out_is_btf, grad_x, grad_weight,
+                          nullptr, 0, B, T, K, F, (hipStream_t)stream);
+}
 
 extern "C" size_t ltv_linear_transpose_backward_workspace_size(int dtype, int B, int T, int K,
                                                                 int F, int grad_out_is_btf) {
   if (B <= 0 || T <= 0 || K <= 0 || F <= 0) return 0;
-  if (!lt_backward_mfma(dtype, grad_out_is_btf, B, T, K, F)) return 0;
+  if (!lt_backward_mfma(dtype, grad_out_is_btf, B, T, K, F)) return lt_f32m_workspace(B, T, K, F);
   const LtSplits p = lt_splits(B * T, K, F);
   return (size_t)p.S * p.Fr * K * sizeof(float);
 }
@@ -511,14 +558,14 @@ extern "C" int ltv_linear_transpose_backward_ws(int dtype, const void* x, const 
   LTV_REQUIRE(dtype == LTV_DTYPE_F32 || dtype == LTV_DTYPE_BF16, LTV_ERR_INVALID_ARG,
               "dtype must be LTV_DTYPE_F32 or LTV_DTYPE_BF16, got %d", dtype);
   LTV_REQUIRE(B >= 0 && T >= 0 && K >= 0 && F >= 0, LTV_ERR_INVALID_ARG, "negative size");
+  LTV_REQUIRE(lt_backward_pointers_ok(x, weight, grad_out, grad_x, grad_weight, B, T, K, F),
+              LTV_ERR_INVALID_ARG, "null tensor pointer");
+  hipStream_t st = (hipStream_t)stream;
   if (!lt_backward_mfma(dtype, grad_out_is_btf, B, T, K, F) ||
       !(aligned16(x) && aligned16(weight) && aligned16(grad_out) && aligned16(grad_x) &&
         aligned16(grad_weight)))
-    return ltv_linear_transpose_backward(dtype, x, weight, grad_out, grad_out_is_btf, grad_x,
-                                         grad_weight, B, T, K, F, stream);
-  LTV_REQUIRE(x && weight && grad_out && grad_x && grad_weight, LTV_ERR_INVALID_ARG,
-              "null tensor pointer");
-  hipStream_t st = (hipStream_t)stream;
+    return lt_backward_f32m(dtype, x, weight, grad_out, grad_out_is_btf, grad_x, grad_weight,
+                            workspace, workspace_bytes, B, T, K, F, st);
   const int M = B * T;
   const LtSplits sp = lt_splits(M, K, F);
   const size_t need = (size_t)sp.S * sp.Fr * K * sizeof(float);

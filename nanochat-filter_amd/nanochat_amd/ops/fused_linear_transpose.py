@@ -5,7 +5,8 @@ Behavioural mirror of the reference's ``nanochat/ops/fused_linear_transpose.py``
 inputs, a zero-initialised (B, F, T) output from the functional op, and a
 backward that accepts grad_out either contiguous or as the transposed view of a
 (B, T, F)-contiguous tensor.  The work runs in the gfx950 library
-(``ltv_linear_transpose_forward`` / ``ltv_linear_transpose_backward``).
+(``ltv_linear_transpose_forward`` / ``ltv_linear_transpose_backward_ws``): bf16
+MFMA kernels where the layout allows, else the strided fp32-MFMA GEMM.
 """
 
 import torch
@@ -30,9 +31,10 @@ def fused_linear_transpose(x, weight, out):
         raise RuntimeError(
             f"shape mismatch: x {tuple(x.shape)}, weight {tuple(weight.shape)}, "
             f"out {tuple(out.shape)}")
-    rc = N.lib().ltv_linear_transpose_forward(
-        N.dtype_code(x.dtype), x.data_ptr(), weight.data_ptr(), out.data_ptr(),
-        B, T, K, F, N.stream_of(x))
+    with N.span("linear_transpose_fwd"):
+        rc = N.lib().ltv_linear_transpose_forward(
+            N.dtype_code(x.dtype), x.data_ptr(), weight.data_ptr(), out.data_ptr(),
+            B, T, K, F, N.stream_of(x))
     N.check(rc, "ltv_linear_transpose_forward")
     return None
 
@@ -79,14 +81,15 @@ def fused_linear_transpose_backward_kernel(x, weight, grad_out, grad_x, grad_wei
     F = weight.size(0)
     is_btf = 1 if (not grad_out.is_contiguous()) else 0
     lib = N.lib()
-    # bf16 (B, F, T) gradients run on MFMA; the weight gradient's split
-    # partials need a workspace (0 bytes where the SIMT kernel runs)
+    # the weight gradient's reduction over B T is split into fp32 partials,
+    # which need a workspace (0 bytes: no split)
     ws_bytes = lib.ltv_linear_transpose_backward_workspace_size(N.dtype_code(dt), B, T, K, F, is_btf)
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=x.device)
-    rc = lib.ltv_linear_transpose_backward_ws(
-        N.dtype_code(dt), x.data_ptr(), weight.data_ptr(), grad_out.data_ptr(), is_btf,
-        grad_x.data_ptr(), grad_weight.data_ptr(), ws.data_ptr(), ws_bytes, B, T, K, F,
-        N.stream_of(x))
+    with N.span("linear_transpose_bwd"):
+        rc = lib.ltv_linear_transpose_backward_ws(
+            N.dtype_code(dt), x.data_ptr(), weight.data_ptr(), grad_out.data_ptr(), is_btf,
+            grad_x.data_ptr(), grad_weight.data_ptr(), ws.data_ptr(), ws_bytes, B, T, K, F,
+            N.stream_of(x))
     N.check(rc, "ltv_linear_transpose_backward_ws")
     return None
 

@@ -75,6 +75,12 @@ def test_abi_version_and_host_only_queries():
     assert lib.ltv_qkv_logit_width(18, 1) == 24
     assert lib.ltv_hm_scan_backward_workspace_size(1, 32, 1024, 6, 6, 1, 128) >= 32 * 18 * 4
     assert lib.ltv_qkv_project_backward_workspace_size(32768, 768, 18, 128, 1) > 0
+    # reference-layout backward, fp32 at d12: grad_weight's 19 x 6 tiles of
+    # 128 x 128 split over B T into S fp32 partials of F x K; a single tile
+    # row and column with B T = 256 (one split): none
+    ws = lib.ltv_linear_transpose_backward_workspace_size(N.DTYPE_F32, 32, 1024, 768, 2322, 0)
+    assert ws > 0 and ws % (2322 * 768 * 4) == 0 and ws // (2322 * 768 * 4) >= 2
+    assert lib.ltv_linear_transpose_backward_workspace_size(N.DTYPE_F32, 1, 256, 64, 100, 0) == 0
     # chained scan forward: 256-byte header + one 8-byte word per channel of
     # every chunk but a sequence's last.  configs[4] prefill (8 x 18 heads x 2
     # slabs of 64 channels): 16 chunks of 512 steps; fp32: slabs of 32

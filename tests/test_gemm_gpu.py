@@ -132,7 +132,7 @@ def test_projection_ragged_token_counts(M):
 def test_fused_linear_transpose_bf16_mfma(B, T, K, F):
     """bf16 reference-layout projection on the MFMA kernels (T a multiple of
     256, K of 8): out (B, F, T), grad_x and grad_weight against an fp32 torch
-    product of the same bf16 operands, and against the SIMT kernel
+    product of the same bf16 operands, and against the fp32-MFMA kernel
     (ltv_linear_transpose_backward) -- both fp32-accumulated, so within
     accumulation-order rounding; the weight gradient twice bitwise equal
     (fixed-order split sum)."""
@@ -161,11 +161,11 @@ def test_fused_linear_transpose_bf16_mfma(B, T, K, F):
                            xf.reshape(B * T, K))                          # (F, K)
     assert_close(np_of(gx), np_of(want_gx), 2e-2, "grad_x")
     assert_close(np_of(gw), np_of(want_gw), 2e-2, "grad_weight")
-    # the SIMT kernel on the same operands
+    # the fp32-MFMA kernel on the same operands
     sx, sw = torch.empty_like(x), torch.empty_like(w)
     N.check(lib.ltv_linear_transpose_backward(N.DTYPE_BF16, x.data_ptr(), w.data_ptr(),
                                               go.data_ptr(), 0, sx.data_ptr(), sw.data_ptr(),
-                                              B, T, K, F, N.stream_of(x)), "simt backward")
+                                              B, T, K, F, N.stream_of(x)), "fp32-MFMA backward")
     torch.cuda.synchronize()
-    assert_close(np_of(gx), np_of(sx), 2e-2, "grad_x vs SIMT")
-    assert_close(np_of(gw), np_of(sw), 2e-2, "grad_weight vs SIMT")
+    assert_close(np_of(gx), np_of(sx), 2e-2, "grad_x vs fp32-MFMA")
+    assert_close(np_of(gw), np_of(sw), 2e-2, "grad_weight vs fp32-MFMA")
