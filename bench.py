@@ -281,8 +281,9 @@ def main():
     dv = torch.randn(B, T, NKVH, D, generator=g, device=dev).to(torch.bfloat16)
     if look_back:
         def forward():
-            inits = f.init_param.unsqueeze(0).expand(B, -1, -1)
-            return f(x, inits, full_recurrence=False)
+            # the (H, D) parameter, as LtvLookBackQkvComputerModule hands it over
+            # without a KV cache (its gradient summed over the batch in the library)
+            return f(x, f.init_param, full_recurrence=False)
     else:
         none = LtvInitValues()
 

@@ -323,7 +323,9 @@ int ltv_hm_look_back_scan_forward_split(
  *   values: fp32 inits (the parameter itself, e.g. (H, D) with batch stride 0)
  *   rounded to bf16 when read, exactly the reference's
  *   `init_param.expand(B, H, D).to(bfloat16)` before its kernel, without the
- *   cast's copy.  The fp32 form needs the full recurrence (P >= T). */
+ *   cast's copy.  The fp32 form needs the full recurrence (P >= T), or
+ *   look-back windows the short-window kernels take (Q <= 64, warm-up
+ *   K - 1 <= min(Q, 16), gate groups of 8 x 2^k channels or dividing 8). */
 int ltv_hm_look_back_scan_forward_split_ws(
     int dtype, const void* values, const int64_t values_strides[4], const void* logits,
     const int64_t logits_strides[4], const void* inits, const int64_t inits_strides[3],
@@ -357,7 +359,8 @@ int ltv_hm_look_back_scan_backward_split(
  *   which is what the broadcast's backward computes (the reference sums the
  *   expanded inits' gradient over B).  Needs the full recurrence and gate
  *   groups the tile kernels take (r a multiple of 8 bf16 / 4 fp32 channels
- *   with Da <= 16, or r dividing it); the sum is formed by the launch that
+ *   with Da <= 16, or r dividing it), or look-back windows the short-window
+ *   kernels take (as for fp32 inits); the sum is formed by the launch that
  *   reduces grad_logit_bias, in `workspace`.
  * grad_logits_pad: 0 .. 64 logit slots past the last head's last gate that
  *   are set to zero in every (b, t) row, slot q = H Da + p at

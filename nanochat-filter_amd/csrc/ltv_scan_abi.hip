@@ -780,11 +780,14 @@ BwdWorkspace bwd_workspace_plan(int dtype, int B, int T, int NH, int NKVH, int D
   BwdWorkspace w;
   const int nwin = look_back_nwin(T, P, Q);
   if (nwin > 1 && (tuning().lb_short && lb_short_ok(V, r, Q, K))) {
-    // short windows: dbias partials and per-window grad_inits shares only
+    // short windows: dbias partials, per-window grad_inits shares and the
+    // per-(b, h) inits gradients of the batch sum
     const size_t rows = (size_t)B * H * nwin;
     size_t off = al(rows * Da * sizeof(float));
     w.wdi = off;
     off += al(rows * D * sizeof(float));
+    w.dinit = off;
+    off += al((size_t)B * H * D * sizeof(float));
     w.total = off;
     return w;
   }
@@ -934,12 +937,12 @@ int scan_backward_impl(int dtype, const HostView4& u, const HostView4& lg, const
     gm = GATE_CHANVEC;
   const int nwin = look_back_nwin(T, P, Q);
   const bool lb_short = nwin > 1 && tuning().lb_short && lb_short_ok(V, r, Q, K);
-  LTV_REQUIRE(!(init_f32 || dinit_sum) || (nwin == 1 && gm >= 0) || (lb_short && !dinit_sum),
+  LTV_REQUIRE(!(init_f32 || dinit_sum) || (nwin == 1 && gm >= 0) || lb_short,
               LTV_ERR_UNSUPPORTED,
               "fp32 inits with bf16 values, or grad_inits summed over the batch (batch stride "
               "0), need the full recurrence (P >= T) and gate groups of r channels with r a "
-              "multiple of %d and Da <= %d, or r dividing %d (r=%d Da=%d); fp32 inits also go "
-              "with look-back windows the short-window kernels take",
+              "multiple of %d and Da <= %d, or r dividing %d (r=%d Da=%d), or look-back "
+              "windows the short-window kernels take",
               V, kMaxLaneGroups, V, r, Da);
   PadZero pz;
   if (dlg_pad > 0) {

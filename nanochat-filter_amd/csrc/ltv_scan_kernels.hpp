@@ -1922,7 +1922,10 @@ __global__ void __launch_bounds__(256) scan_lb_fold_kernel(const BwdArgs args) {
 }
 
 // grad_inits[b, h, d] = sum over the non-empty windows of their fp32
-// contributions, in window order.
+// contributions, in window order.  With grad_inits summed over the batch
+// (args.dinit_ws set), the per-sequence gradient goes there instead, rounded to
+// the I/O dtype as a per-sequence gradient tensor would be, for the batch sum
+// of the dbias reduction launch.
 template <typename TIO>
 __global__ void __launch_bounds__(256) scan_lb_dinit_kernel(const BwdArgs args) {
   const ScanShape& S = args.sh;
@@ -1944,6 +1947,10 @@ __global__ void __launch_bounds__(256) scan_lb_dinit_kernel(const BwdArgs args) 
     for (int k = 0; k < KB; ++k) x[k] = c0 + k < nw ? wp[(int64_t)(c0 + k) * S.D] : 0.0f;
 #pragma unroll
     for (int k = 0; k < KB; ++k) acc += x[k];
+  }
+  if (args.dinit_ws != nullptr) {
+    args.dinit_ws[bh * S.D + d] = round_io<TIO>(acc);
+    return;
   }
   const int64_t o = (int64_t)b * args.dinit.s[0] + (int64_t)h * args.dinit.s[1] +
                     (int64_t)d * args.dinit.s[3];

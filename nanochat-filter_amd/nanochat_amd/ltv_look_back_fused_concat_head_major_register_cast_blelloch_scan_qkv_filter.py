@@ -57,10 +57,26 @@ class LtvLookBackFusedConcatHeadMajorRegisterCastBlellochScanQkvFilter(
                 ltv_cuda_look_back_fused_concat_head_major_register_cast_blelloch_scan)
 
     def forward(self, x: torch.Tensor, resolved_inits: torch.Tensor, full_recurrence: bool):
-        if (self._uses_library_ops() and x.is_cuda and x.dtype == torch.bfloat16
-                and not should_run_ltv_in_fp32(x.device.type)):
+        """resolved_inits: (B, H, D), or (H, D) shared by every sequence (the
+        init parameter itself, as the computer module passes it without a KV
+        cache): the library then sums its gradient over the batch where the
+        kernels can, else it is expanded to (B, H, D) here."""
+        fused = (self._uses_library_ops() and x.is_cuda and x.dtype == torch.bfloat16
+                 and not should_run_ltv_in_fp32(x.device.type))
+        if resolved_inits.dim() == 2 and not (fused and self.takes_shared_inits(x, full_recurrence)):
+            resolved_inits = resolved_inits.unsqueeze(0).expand(x.size(0), -1, -1)
+        if fused:
             return look_back_fused_forward(self, x, resolved_inits, full_recurrence)
         return super().forward(x, resolved_inits, full_recurrence)
+
+    def takes_shared_inits(self, x: torch.Tensor, full_recurrence: bool) -> bool:
+        """Whether the fused path takes (H, D) inits for this input and sums
+        their gradient over the batch in the library (not the one-step decode,
+        which reads per-sequence cache rows)."""
+        if full_recurrence and x.size(1) == 1:
+            return False
+        P, Q, K = self.chunking(full_recurrence)
+        return hm_fast.fp32_inits_ok(x.size(1), self.head_dim, self.r, P, Q, K)
 
     def _project(self, x: torch.Tensor) -> torch.Tensor:
         fp32 = x.dtype == torch.float32

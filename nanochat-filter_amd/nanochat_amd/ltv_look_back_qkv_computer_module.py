@@ -130,6 +130,11 @@ class LtvLookBackQkvComputerModule(nn.Module):
 
     def forward(self, x, kv_cache: Optional[KVCache]):
         B = x.size(0)
+        if kv_cache is None and hasattr(self.ltv_filter, "takes_shared_inits"):
+            # the (H, D) parameter itself: the filter broadcasts it to every
+            # sequence and its gradient comes back summed over the batch
+            # (the reference expands it to (B, H, D) here; same values)
+            return self.ltv_filter(x, self.ltv_filter.init_param, full_recurrence=False)
         resolved_inits = self.ltv_filter.init_param.unsqueeze(0).expand(B, -1, -1)
         if kv_cache is not None:
             return self.advance_last_qkv(kv_cache, resolved_inits, x)

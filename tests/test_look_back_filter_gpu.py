@@ -178,3 +178,50 @@ def test_fp32_inits_bitwise_equal_bf16_cast(pqk, monkeypatch):
     for name, a, b in zip(("q", "k", "v", "grad_x", "grad_weight", "grad_init_param",
                            "grad_logit_bias"), fp32, cast):
         assert torch.equal(a, b), f"{name} differs with pqk={pqk}"
+
+
+@pytest.mark.parametrize("pqk", [(16, 16, 9), (64, 60, 5), (32, 8, 9), (128, 100, 5)], ids=str)
+def test_shared_inits_match_expanded(pqk):
+    """The (H, D) init parameter handed to the bf16 look-back filter directly
+    (what the computer module does without a KV cache): q, k, v and the
+    gradients of x, the weight and the logit bias bitwise those of the
+    expanded (B, H, D) inits; the parameter's gradient bitwise the batch-order
+    fp32 sum of the per-sequence gradients (which the library forms itself
+    where the kernels take shared inits -- (128, 100, 5) does not, and is
+    expanded by the filter)."""
+    from nanochat_amd.ltv_look_back_qkv_computer_module import LtvLookBackQkvComputerModule
+    NH, NKVH, D, r = 2, 1, 128, 128
+    B, T = 5, 200
+    g = torch.Generator().manual_seed(11)
+    x = torch.randn(B, T, NH * D, generator=g).to(torch.bfloat16).to(DEV)
+    gy = [torch.randn(B, T, n, D, generator=g).to(torch.bfloat16).to(DEV) for n in (NH, NKVH, NKVH)]
+
+    def run(mode):
+        f = _make("blelloch", NH, NKVH, D, r, pqk, seed=3)
+        xd = x.clone().requires_grad_(True)
+        per_seq = None
+        if mode == "shared":
+            q, k, v = f(xd, f.init_param, full_recurrence=False)
+        elif mode == "module":
+            q, k, v = LtvLookBackQkvComputerModule(0, f)(xd, None)
+        else:  # per-sequence leaf inits: their (B, H, D) gradient
+            per_seq = f.init_param.detach().unsqueeze(0).repeat(B, 1, 1).requires_grad_(True)
+            q, k, v = f(xd, per_seq, full_recurrence=False)
+        torch.autograd.backward([q, k, v], gy)
+        gi = per_seq.grad if per_seq is not None else f.init_param.grad
+        return [q, k, v, xd.grad, f.c.weight.grad, f.logit_bias.grad], gi
+
+    ref, gi_seq = run("per_sequence")
+    want = np.zeros(gi_seq.shape[1:], np.float32)
+    for b in range(B):  # batch order, fp32
+        want = (want + gi_seq[b].cpu().numpy()).astype(np.float32)
+    for mode in ("shared", "module"):
+        outs, gi = run(mode)
+        for name, a, b in zip(("q", "k", "v", "grad_x", "grad_weight", "grad_logit_bias"),
+                              outs, ref):
+            assert torch.equal(a, b), f"{name} differs ({mode}, pqk={pqk})"
+        got = gi.cpu().numpy()
+        if pqk == (128, 100, 5):  # expanded by the filter: torch's batch reduction
+            assert_close(got, want, 1e-6, f"grad_init_param ({mode})")
+        else:
+            assert np.array_equal(got, want), f"grad_init_param ({mode}, pqk={pqk})"

@@ -12,7 +12,8 @@ with ``inits_dtype`` and a batch-stride-0 ``grad_inits``):
   dtype;
 * the filter module's forward and backward with the parameter passed as it is
   equal those of the cast-and-broadcast path (outputs and x / weight / bias
-  gradients bitwise, init_param's gradient to fp32 summation order).
+  gradients bitwise, init_param's gradient to fp32 summation order);
+* the same batch sum on look-back windows the short-window kernels take.
 """
 
 from __future__ import annotations
@@ -135,20 +136,73 @@ def test_shared_inits_oracle_rows():
     assert np.abs(got - want).max() <= 2e-2 * scale
 
 
+# (B, T, NH, NKVH, Da, r, (P, Q, K)): look-back windows the short-window kernels
+# take -- one window per lane, several per lane (the d12 spec), 16-channel gate
+# groups, per-channel gates
+LB_SHAPES = [(2, 64, 1, 1, 1, 128, (16, 16, 4)), (5, 300, 2, 1, 1, 128, (16, 16, 9)),
+             (3, 300, 1, 1, 8, 16, (32, 8, 9)), (2, 129, 1, 1, 64, 1, (16, 16, 9))]
+
+
+@pytest.fixture
+def windows_per_lane():
+    from nanochat_amd import _native as N
+    lib = N.lib()
+
+    def set_(n):
+        N.check(lib.ltv_lb_set_windows_per_lane(n), "ltv_lb_set_windows_per_lane")
+
+    try:
+        yield set_
+    finally:
+        set_(0)
+
+
+@pytest.mark.parametrize("wpl", [0, 3], ids=["auto", "wpl3"])
+@pytest.mark.parametrize("B,T,NH,NKVH,Da,r,pqk", LB_SHAPES, ids=str)
+@pytest.mark.parametrize("init_dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+def test_shared_inits_look_back_batch_sum(B, T, NH, NKVH, Da, r, pqk, init_dtype, wpl,
+                                          windows_per_lane):
+    """Look-back windows with (H, D) inits: outputs bitwise those of the
+    bf16-cast (B, H, D) inits, grad_combined and grad_logit_bias bitwise, and
+    grad_inits bitwise the float32 batch-order sum of the per-sequence bf16
+    gradients (the per-window shares summed per sequence, then over the batch
+    by the reduction launch); with the automatic windows per lane and with
+    three (the several-window kernel where the spec allows it)."""
+    windows_per_lane(wpl)
+    F = _F()
+    H, D = NH + 2 * NKVH, Da * r
+    Fp = F.packed_width(H, D, Da)
+    values, logits, param, bias, gys = _case(B, T, NH, NKVH, Da, r, seed=B + T + r,
+                                             init_dtype=init_dtype)
+    expanded = param.to(torch.bfloat16).unsqueeze(0).expand(B, H, D).contiguous()
+    shared = F.scan_forward(values, logits, param, bias, NH, NKVH, Da, r, True, *pqk)
+    ref = F.scan_forward(values, logits, expanded, bias, NH, NKVH, Da, r, True, *pqk)
+    for a, b in zip(shared, ref):
+        assert torch.equal(a, b)
+    gc_s = torch.zeros(B, T, Fp, dtype=torch.bfloat16, device=DEV)
+    gi_s, gb_s = F.scan_backward(values, logits, param, bias, *ref, *gys, NH, NKVH, Da, r, True,
+                                 gc_s, *pqk)
+    gc_r = torch.zeros_like(gc_s)
+    gi_r, gb_r = F.scan_backward(values, logits, expanded, bias, *ref, *gys, NH, NKVH, Da, r,
+                                 True, gc_r, *pqk)
+    assert gi_s.shape == (H, D) and gi_s.dtype == init_dtype
+    assert torch.equal(gc_s, gc_r) and torch.equal(gb_s, gb_r)
+    per_seq = gi_r.float().cpu().numpy()
+    want = np.zeros((H, D), np.float32)
+    for b in range(B):
+        want = (want + per_seq[b]).astype(np.float32)
+    assert torch.equal(gi_s.cpu(), torch.from_numpy(want).to(init_dtype))
+
+
 def test_unsupported_forms_are_refused():
-    """A batch-summed grad_inits needs the full recurrence and gate groups the
-    tile kernels reduce (look-back windows read shared fp32 inits in the
-    forward, but their backward refuses the batch sum); the values' dtype must
-    be bf16 for fp32 inits.  Each is an error before any launch."""
+    """A batch-summed grad_inits needs the full recurrence with gate groups
+    the tile kernels reduce, or look-back windows the short-window kernels
+    take; the values' dtype must be bf16 for fp32 inits.  Each is an error
+    before any launch."""
     F = _F()
     B, T, NH, NKVH, Da, r = 2, 64, 1, 1, 1, 128
     H, D = NH + 2 * NKVH, Da * r
     values, logits, param, bias, gys = _case(B, T, NH, NKVH, Da, r, seed=1)
-    q, k, v = F.scan_forward(values, logits, param, bias, NH, NKVH, Da, r, True, P=16, Q=16, K=4)
-    gc = torch.zeros(B, T, F.packed_width(H, D, Da), dtype=torch.bfloat16, device=DEV)
-    with pytest.raises(RuntimeError, match="batch"):
-        F.scan_backward(values, logits, param, bias, q, k, v, *gys, NH, NKVH, Da, r, True, gc,
-                        P=16, Q=16, K=4)
     with pytest.raises(RuntimeError, match="full recurrence"):  # not a short-window spec
         F.scan_forward(values, logits, param, bias, NH, NKVH, Da, r, True, P=16, Q=100, K=4)
     with pytest.raises(RuntimeError, match="float32 with bfloat16"):
