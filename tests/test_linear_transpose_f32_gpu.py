@@ -186,3 +186,57 @@ def test_f32_empty_reductions_give_zeros():
                                               B, T, K, F, N.stream_of(xs)), "backward")
     torch.cuda.synchronize()
     assert np.array_equal(gw.cpu().numpy(), np.zeros((F, K), np.float32))
+
+
+def test_random_shapes_layouts_and_offsets():
+    """24 seeded random cases: B, T, K, F from 1 to a few hundred, fp32 and
+    bf16, grad_out (B, F, T) or (B, T, F), tensors 0-3 elements past a
+    16-byte boundary (every staging form, tails in every dimension), through
+    the forward and both backward entry points (workspace split and none)."""
+    N, lib = _lib()
+    rng = np.random.default_rng(2024)
+    for case in range(24):
+        B = int(rng.integers(1, 5))
+        T, K, F = (int(v) for v in rng.integers(1, 300, size=3))
+        dtype = torch.float32 if case % 3 else torch.bfloat16
+        btf = bool(case % 2)
+        off = int(rng.integers(0, 4))
+        es = 4 if dtype == torch.float32 else 2
+        g = torch.Generator().manual_seed(case)
+
+        def place(shape, scale):
+            n = int(np.prod(shape))
+            buf = torch.empty(n + off, dtype=dtype, device=DEV)
+            t = buf[off:].view(*shape)
+            t.copy_((torch.randn(*shape, generator=g) * scale).to(dtype))
+            return t
+
+        x = place((B, T, K), K ** -0.5)
+        w = place((F, K), K ** -0.5)
+        go_store = place((B, T, F) if btf else (B, F, T), 1.0)
+        go = go_store.transpose(1, 2) if btf else go_store
+        out = torch.empty(B, F, T, dtype=dtype, device=DEV)
+        gx, gw = torch.empty(B, T, K, dtype=dtype, device=DEV), torch.empty(F, K, dtype=dtype, device=DEV)
+        hx, hw = torch.empty_like(gx), torch.empty_like(gw)
+        st = N.stream_of(x)
+        code = N.dtype_code(dtype)
+        label = f"case {case}: B={B} T={T} K={K} F={F} {dtype} btf={btf} off={off * es}B"
+        N.check(lib.ltv_linear_transpose_forward(code, x.data_ptr(), w.data_ptr(), out.data_ptr(),
+                                                 B, T, K, F, st), label)
+        ws_bytes = lib.ltv_linear_transpose_backward_workspace_size(code, B, T, K, F, int(btf))
+        ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=DEV)
+        N.check(lib.ltv_linear_transpose_backward_ws(
+            code, x.data_ptr(), w.data_ptr(), go_store.data_ptr(), int(btf), gx.data_ptr(),
+            gw.data_ptr(), ws.data_ptr(), ws_bytes, B, T, K, F, st), label)
+        N.check(lib.ltv_linear_transpose_backward(
+            code, x.data_ptr(), w.data_ptr(), go_store.data_ptr(), int(btf), hx.data_ptr(),
+            hw.data_ptr(), B, T, K, F, st), label)
+        torch.cuda.synchronize()
+        bf = dtype == torch.bfloat16
+        splits = ws_bytes // (F * K * 4) if ws_bytes else 1
+        _check(out, w.unsqueeze(0).expand(B, F, K), x.transpose(1, 2), K, f"out, {label}", bf)
+        _check(gx, go.transpose(1, 2), w.unsqueeze(0).expand(B, F, K), F, f"grad_x, {label}", bf)
+        _check(hx, go.transpose(1, 2), w.unsqueeze(0).expand(B, F, K), F, f"grad_x nows, {label}", bf)
+        gof = go.permute(1, 0, 2).reshape(F, B * T)
+        _check(gw, gof, x.reshape(B * T, K), B * T + splits, f"grad_weight, {label}", bf)
+        _check(hw, gof, x.reshape(B * T, K), B * T, f"grad_weight nows, {label}", bf)
