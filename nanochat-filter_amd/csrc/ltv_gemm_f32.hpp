@@ -309,12 +309,8 @@ __global__ void __launch_bounds__(256, 2) gemm_f32m_kernel(const F32mArgs g) {
       sb.store(lds_b[cur ^ 1]);
     }
     __syncthreads();
-    if (more) {
-      read_group(S0{}, cur ^ 1, 0);
-      mfma_group(S1{});
-      } else {
-      mfma_group(S1{});
-    }
+    if (more) read_group(S0{}, cur ^ 1, 0);
+    mfma_group(S1{});
   }
 
   // lane l of block (a, b) holds column n = 32 b + l % 32 and rows
