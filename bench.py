@@ -530,6 +530,12 @@ def lt_f32_main(args):
         for _ in range(args.steps):
             step()
         torch.cuda.synchronize()
+    if args.calibrate_copy:
+        src = torch.empty(COPY_CAL_BYTES, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
     flop = 2.0 * B * T * C * F
     durs = rec.durations_ms()
     spans = {}
@@ -553,6 +559,7 @@ def lt_f32_main(args):
     lib_ms = sorted(lib_ms[2:])
     lib_t = lib_ms[len(lib_ms) // 2] * 1e-3
     fw = spans["linear_transpose_fwd"]
+    traffic, traffic_src = profiled_traffic("linear_transpose_fwd", "lt_f32_traffic.json")
     out = {
         "metric": "fp32 reference-layout projection (fused_linear_transpose fwd + bwd) TFLOP/s, "
                   "configs[2] shapes x (32, 1024, 768) . W (2322, 768)^T",
@@ -572,8 +579,9 @@ def lt_f32_main(args):
                    "B": B, "T": T, "K": C, "F": F, "parallelism": "single GPU"},
         "roofline": {"kernel": "linear_transpose_fwd (gemm_f32m_kernel)", "bound": "mfma",
                      "achieved": fw["achieved"], "peak": F32_MFMA_PEAK_TFLOPS,
-                     "unit": "TFLOP/s", "frac": fw["frac"], "traffic": None,
-                     "avg_us": fw["avg_us"], "work_per_launch": flop},
+                     "unit": "TFLOP/s", "frac": fw["frac"], "traffic": traffic,
+                     "traffic_source": traffic_src, "avg_us": fw["avg_us"],
+                     "work_per_launch": flop},
         "spans": spans,
         "library_gemm_fwd": {"tflops": round(flop / lib_t / 1e12, 1), "us": round(lib_t * 1e6, 1),
                              "what": "torch.matmul(W, x^T), fp32 (hipBLASLt)"},

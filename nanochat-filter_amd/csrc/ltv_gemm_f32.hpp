@@ -219,11 +219,20 @@ __global__ void __launch_bounds__(256, 2) gemm_f32m_kernel(const F32mArgs g) {
   __shared__ __attribute__((aligned(16))) float lds_a[2][F32LdsTile<LA>::kFloats];
   __shared__ __attribute__((aligned(16))) float lds_b[2][F32LdsTile<LB>::kFloats];
 
-  const int z = blockIdx.z;
+  // workgroup w (dispatch order) runs on XCD w % 8: deal the tiles to the XCDs
+  // in contiguous ranges (n-tiles fastest), so tiles sharing an operand tile
+  // share that XCD's L2.  XCD x holds the workgroups x, x + 8, ... < total:
+  // q + (x < r) of them (q, r = total / 8, total % 8), tiles from x q + min(x, r).
+  const int gx = gridDim.x, gy = gridDim.y;
+  const int64_t total = (int64_t)gx * gy * gridDim.z;
+  const int64_t w = blockIdx.x + (int64_t)gx * (blockIdx.y + (int64_t)gy * blockIdx.z);
+  const int64_t xcd = w % 8, q = total / 8, r = total % 8;
+  const int64_t u = xcd * q + (xcd < r ? xcd : r) + w / 8;
+  const int tx = (int)(u % gx), ty = (int)((u / gx) % gy), z = (int)(u / ((int64_t)gx * gy));
   const int batch = z / g.splits, split = z - batch * g.splits;
   const int kb = split * g.k_split;
   const int ke = min(g.K, kb + g.k_split);
-  const int m0 = blockIdx.y * kF32B, n0 = blockIdx.x * kF32B;
+  const int m0 = ty * kF32B, n0 = tx * kF32B;
   const bool outer = g.kin < g.K;
 
   F32Operand<TI> oa{reinterpret_cast<const TI*>(g.A) + (int64_t)batch * g.sab, g.sam, g.sako,
