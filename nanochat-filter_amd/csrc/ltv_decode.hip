@@ -80,8 +80,13 @@ __global__ void __launch_bounds__(kDecThreads) qkv_decode_kernel(const DecodeArg
   const int H = a.NH + 2 * a.NKVH;
   const int nblk = (a.D + kDecCh - 1) / kDecCh;
   const int ntb = (a.B + 31) / 32;
-  const int tb = blockIdx.x % ntb;
-  const int hc = blockIdx.x / ntb;
+  // workgroup w runs on XCD w % 8: the workgroups are dealt to the XCDs in
+  // contiguous ranges of (head, channel block, token block), so the token
+  // blocks that read the same weight rows share one L2
+  const int nb = (int)gridDim.x, xcd = (int)blockIdx.x % 8, q = nb / 8, rr = nb % 8;
+  const int u = xcd * q + (xcd < rr ? xcd : rr) + (int)blockIdx.x / 8;
+  const int tb = u % ntb;
+  const int hc = u / ntb;
   const int h = hc / nblk, cb = hc % nblk;
   const int lane = threadIdx.x & 63;
   const int ks = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // k slice
