@@ -219,11 +219,11 @@ int f32m_stage(const void* p, int64_t sr, int64_t sko, int64_t ski, int64_t sbat
 template <typename TI, typename TO, int LA>
 void f32m_launch_b(int lb, const F32mArgs& a, dim3 grid, hipStream_t st) {
   if (lb == kF32KQ)
-    hipLaunchKernelGGL((gemm_f32m_kernel<TI, TO, LA, kF32KQ>), grid, dim3(256), 0, st, a);
+    hipLaunchKernelGGL((gemm_f32m_kernel<TI, TO, LA, kF32KQ>), grid, dim3(kF32Threads), 0, st, a);
   else if (lb == kF32MQ)
-    hipLaunchKernelGGL((gemm_f32m_kernel<TI, TO, LA, kF32MQ>), grid, dim3(256), 0, st, a);
+    hipLaunchKernelGGL((gemm_f32m_kernel<TI, TO, LA, kF32MQ>), grid, dim3(kF32Threads), 0, st, a);
   else
-    hipLaunchKernelGGL((gemm_f32m_kernel<TI, TO, LA, kF32SC>), grid, dim3(256), 0, st, a);
+    hipLaunchKernelGGL((gemm_f32m_kernel<TI, TO, LA, kF32SC>), grid, dim3(kF32Threads), 0, st, a);
 }
 
 template <typename TI, typename TO>

@@ -9,10 +9,10 @@
 // The products are exact in fp32 for bf16 operands and rounded once for fp32
 // ones, as in an fp32 FMA; the sums run in fp32.
 //
-// 128 x 128 output tiles, 4 wavefronts of 64 x 64 (2 x 2 blocks of 32 x 32),
+// 128 x 128 output tiles, 8 wavefronts of 64 x 32 (2 blocks of 32 x 32),
 // 32-wide k-steps through two LDS stages: the global loads of step s + 1 sit
 // in registers while step s runs its MFMAs, then go to the other stage; one
-// barrier per step.  Two workgroups share a CU (2 x 36 KB of LDS at most).
+// barrier per step.  Two workgroups share a CU (at most 72 KB of LDS each).
 // Each operand is staged in one of three ways, chosen per launch from its
 // strides:
 //   kF32KQ  k-contiguous quads (saki = 1): 4 consecutive k of one row per
@@ -43,6 +43,12 @@ constexpr int kF32B = 128;  // tile rows of A and of B
 constexpr int kF32BK = 32;  // reduction indices per k-step
 constexpr int kF32RowKQ = kF32BK + 4;  // floats per LDS row, KQ staging
 constexpr int kF32RowMQ = kF32B + 8;   // floats per LDS k-row, MQ / SC staging
+// 8 wavefronts (2 along the rows x 4 along the columns) of 64 x 32: four per
+// SIMD with two workgroups per CU, so one wavefront's barrier or load wait
+// leaves three to feed the SIMD's matrix core
+constexpr int kF32Threads = 512;
+constexpr int kF32Quads = kF32B * kF32BK / 4 / kF32Threads;  // quads per thread per operand
+constexpr int kF32BlocksN = 1;  // 32-column blocks per wavefront
 
 template <int L>
 struct F32LdsTile {
@@ -94,8 +100,8 @@ __device__ __forceinline__ float4 ld_quad(const bf16_t* p) {
 // takes the general load).  Other steps check every element.
 template <typename TI, int L>
 struct F32Stager {
-  float4 r[4];  // KQ / MQ: 4 quads per thread; SC: 16 elements
-  const TI* rp[4];  // KQ / MQ: quad c at the tile's rows and this thread's k, k0 = 0
+  float4 r[kF32Quads];  // KQ / MQ: kF32Quads quads per thread; SC: 4 kF32Quads elements
+  const TI* rp[kF32Quads];  // KQ / MQ: quad c at the tile's rows and this thread's k, k0 = 0
   uint32_t ok;      // bit c: quad c lies inside the operand's rows
   uint32_t keep;    // bit c: quad c of the last load is stored as loaded (else zeros)
   bool fast_ok;     // the fast load applies to this tile (uniform)
@@ -106,8 +112,8 @@ struct F32Stager {
     fast_ok = L != kF32SC && (!op.outer || op.kin % kF32BK == 0) &&
               !(L == kF32MQ && op.rows % 4 != 0 && op.row0 + kF32B > op.rows);
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const int q = t + 256 * c;
+    for (int c = 0; c < kF32Quads; ++c) {
+      const int q = t + kF32Threads * c;
       if (L == kF32KQ) {
         const int row = op.row0 + (q >> 3);
         rp[c] = op.p + (int64_t)(row < op.rows ? row : 0) * op.sr + 4 * (q & 7);
@@ -133,16 +139,16 @@ struct F32Stager {
     const int64_t ks = op.outer ? (int64_t)(k0 / op.kin) * op.sko + (int64_t)(k0 % op.kin) * op.ski
                                 : (int64_t)k0 * op.ski;
 #pragma unroll
-    for (int c = 0; c < 4; ++c) r[c] = ld_quad(rp[c] + ks);
+    for (int c = 0; c < kF32Quads; ++c) r[c] = ld_quad(rp[c] + ks);
     keep = ok;
   }
 
   __device__ __forceinline__ void load_checked(const F32Operand<TI>& op, int k0) {
     const int t = threadIdx.x;
-    keep = 0xfu;
+    keep = (1u << kF32Quads) - 1;
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const int q = t + 256 * c;
+    for (int c = 0; c < kF32Quads; ++c) {
+      const int q = t + kF32Threads * c;
       float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
       if (L == kF32KQ) {
         const int row = op.row0 + (q >> 3), kk = k0 + 4 * (q & 7);
@@ -171,10 +177,10 @@ struct F32Stager {
           }
         }
       } else {
-        // element e of this thread: row (t & 127), k-row (t >> 7) + 2 (4 c + e)
+        // element e of this thread: row (t & 127), k-row (t >> 7) + 4 (4 c + e)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const int row = op.row0 + (t & 127), kk = k0 + (t >> 7) + 2 * (4 * c + e);
+          const int row = op.row0 + (t & 127), kk = k0 + (t >> 7) + (kF32Threads / kF32B) * (4 * c + e);
           if (row < op.rows && kk < op.ke)
             v[e] = io_traits<TI>::load(op.p + (int64_t)row * op.sr + op.koff(kk));
         }
@@ -186,8 +192,8 @@ struct F32Stager {
   __device__ __forceinline__ void store(float* lds) const {
     const int t = threadIdx.x;
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const int q = t + 256 * c;
+    for (int c = 0; c < kF32Quads; ++c) {
+      const int q = t + kF32Threads * c;
       const bool in = (keep >> c) & 1u;
       const float4 v = in ? r[c] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
       if (L == kF32KQ) {
@@ -198,7 +204,7 @@ struct F32Stager {
         const float v[4] = {r[c].x, r[c].y, r[c].z, r[c].w};
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-          lds[((t >> 7) + 2 * (4 * c + e)) * kF32RowMQ + (t & 127)] = v[e];
+          lds[((t >> 7) + (kF32Threads / kF32B) * (4 * c + e)) * kF32RowMQ + (t & 127)] = v[e];
       }
     }
   }
@@ -215,7 +221,7 @@ __device__ __forceinline__ float4 f32_frag(const float* lds, int rb, int g, int 
 }
 
 template <typename TI, typename TO, int LA, int LB>
-__global__ void __launch_bounds__(256, 2) gemm_f32m_kernel(const F32mArgs g) {
+__global__ void __launch_bounds__(kF32Threads, 2) gemm_f32m_kernel(const F32mArgs g) {
   __shared__ __attribute__((aligned(16))) float lds_a[2][F32LdsTile<LA>::kFloats];
   __shared__ __attribute__((aligned(16))) float lds_b[2][F32LdsTile<LB>::kFloats];
 
@@ -242,13 +248,13 @@ __global__ void __launch_bounds__(256, 2) gemm_f32m_kernel(const F32mArgs g) {
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int wm = (wave & 1) * 64, wn = (wave >> 1) * 64;
+  const int wm = (wave & 1) * 64, wn = (wave >> 1) * (32 * kF32BlocksN);
 
-  f32x16_t acc[2][2];
+  f32x16_t acc[2][kF32BlocksN];
 #pragma unroll
   for (int a = 0; a < 2; ++a)
 #pragma unroll
-    for (int b = 0; b < 2; ++b)
+    for (int b = 0; b < kF32BlocksN; ++b)
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[a][b][v] = 0.0f;
 
@@ -275,13 +281,13 @@ __global__ void __launch_bounds__(256, 2) gemm_f32m_kernel(const F32mArgs g) {
   // Fragments of 8-k group g go to register set g & 1, read one group ahead
   // of their MFMAs.  The last group's MFMAs of a step run after the barrier
   // that ends it, covering the first reads of the next step.
-  float4 fa[2][2], fb[2][2];
+  float4 fa[2][2], fb[2][kF32BlocksN];
   auto read_group = [&](auto setc, int stage, int gi) {
     constexpr int set = decltype(setc)::value;
 #pragma unroll
     for (int a = 0; a < 2; ++a) fa[set][a] = f32_frag<LA>(lds_a[stage], wm + 32 * a, gi, lane);
 #pragma unroll
-    for (int b = 0; b < 2; ++b) fb[set][b] = f32_frag<LB>(lds_b[stage], wn + 32 * b, gi, lane);
+    for (int b = 0; b < kF32BlocksN; ++b) fb[set][b] = f32_frag<LB>(lds_b[stage], wn + 32 * b, gi, lane);
   };
   auto mfma_group = [&](auto setc) {
     constexpr int set = decltype(setc)::value;
@@ -290,7 +296,7 @@ __global__ void __launch_bounds__(256, 2) gemm_f32m_kernel(const F32mArgs g) {
 #pragma unroll
       for (int a = 0; a < 2; ++a)
 #pragma unroll
-        for (int b = 0; b < 2; ++b) {
+        for (int b = 0; b < kF32BlocksN; ++b) {
           const float4& A = fa[set][a];
           const float4& Bf = fb[set][b];
           const float av = p == 0 ? A.x : p == 1 ? A.y : p == 2 ? A.z : A.w;
@@ -328,7 +334,7 @@ __global__ void __launch_bounds__(256, 2) gemm_f32m_kernel(const F32mArgs g) {
 #pragma unroll
   for (int a = 0; a < 2; ++a)
 #pragma unroll
-    for (int b = 0; b < 2; ++b) {
+    for (int b = 0; b < kF32BlocksN; ++b) {
       const int n = n0 + wn + 32 * b + (lane & 31);
       if (n >= g.N) continue;
 #pragma unroll
