@@ -15,7 +15,7 @@ import pytest
 import torch
 
 import ltv_oracle as O
-from ltv_test_utils import TOL, assert_close, np_of
+from ltv_test_utils import TOL, assert_close, io_name, np_of
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -99,3 +99,52 @@ def test_filter_state_continuity(dtype):
     for i in range(3):
         got = torch.cat([a[i], b[i]], dim=1)
         assert_close(np_of(got), np_of(full[i]), tol, f"output {i}")
+
+
+def _random_cases(n=16, seed=7):
+    """Seeded filter shapes: heads, head widths, gate group sizes (r = D: one
+    gate per head; r = 1: one gate per channel), batch and sequence lengths
+    off the kernels' tile sizes (T = 1 included), both I/O dtypes."""
+    rng = np.random.default_rng(seed)
+    cases = []
+    for i in range(n):
+        NH = int(rng.integers(1, 5))
+        NKVH = int(rng.integers(1, NH + 1))
+        D = int(rng.choice([32, 64, 128]))
+        r = int(rng.choice([D, D // 2, D // 4, 8, 1]))
+        B = int(rng.integers(1, 4))
+        T = 1 if i == 0 else int(rng.integers(2, 301))
+        dtype = torch.bfloat16 if i % 2 else torch.float32
+        cases.append(pytest.param(NH, NKVH, D, r, B, T, dtype,
+                                  id=f"{i}-{io_name(dtype)}-h{NH}.{NKVH}-D{D}-r{r}-B{B}-T{T}"))
+    return cases
+
+
+@pytest.mark.parametrize("NH, NKVH, D, r, B, T, dtype", _random_cases())
+def test_filter_random_shapes(NH, NKVH, D, r, B, T, dtype):
+    """Forward and every gradient of the module at seeded random shapes against
+    the oracle (fp32: the reference dataflow; bf16: the MFMA fast path)."""
+    from nanochat_amd.ltv.ltv_filter import LtvInitValues
+    io = io_name(dtype)
+    f = _make_filter(NH=NH, NKVH=NKVH, D=D, r=r, seed=T)
+    C = NH * D
+    g = torch.Generator().manual_seed(B * 1000 + T)
+    x = torch.randn(B, T, C, generator=g).to(dtype)
+    dq = torch.randn(B, T, NH, D, generator=g).to(dtype)
+    dk = torch.randn(B, T, NKVH, D, generator=g).to(dtype)
+    dv = torch.randn(B, T, NKVH, D, generator=g).to(dtype)
+
+    xd = x.to(DEV).requires_grad_(True)
+    q, k, v = f(xd, LtvInitValues())
+    torch.autograd.backward([q, k, v], [dq.to(DEV), dk.to(DEV), dv.to(DEV)])
+
+    (eq, ek, ev), egx, egw, egi, egb = _oracle(
+        f, x.float().numpy(), dq.float().numpy(), dk.float().numpy(), dv.float().numpy(), io)
+    tol = TOL[dtype]
+    assert_close(np_of(q), eq, tol, "q")
+    assert_close(np_of(k), ek, tol, "k")
+    assert_close(np_of(v), ev, tol, "v")
+    assert_close(np_of(xd.grad), egx, tol, "grad_x")
+    assert_close(np_of(f.c.weight.grad), egw, tol, "grad_weight")
+    assert_close(np_of(f.init_param.grad), egi, tol, "grad_init_param")
+    assert_close(np_of(f.logit_bias.grad), egb, tol, "grad_logit_bias")

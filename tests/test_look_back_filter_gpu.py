@@ -225,3 +225,55 @@ def test_shared_inits_match_expanded(pqk):
             assert_close(got, want, 1e-6, f"grad_init_param ({mode})")
         else:
             assert np.array_equal(got, want), f"grad_init_param ({mode}, pqk={pqk})"
+
+
+def _random_cases(n=12, seed=11):
+    """Seeded look-back filter cases: chunk specs (P, Q, K) with short and long
+    warm-ups, P = 0 and unbounded P, heads, head widths and gate group sizes,
+    batch and sequence lengths off the kernels' tile sizes, both variants and
+    both I/O dtypes; odd Blelloch cases hand over the (H, D) inits parameter."""
+    rng = np.random.default_rng(seed)
+    cases = []
+    for i in range(n):
+        NH = int(rng.integers(1, 4))
+        NKVH = int(rng.integers(1, NH + 1))
+        D = int(rng.choice([32, 64, 128]))
+        r = int(rng.choice([D, D // 2, 8, 1]))
+        Q = int(rng.integers(1, 131))
+        K = int(rng.integers(1, 40))
+        P = O.UNBOUNDED_P if i % 5 == 4 else int(rng.choice([0, int(rng.integers(1, 200))]))
+        B = int(rng.integers(1, 4))
+        T = int(rng.integers(1, 301))
+        variant = "blelloch" if i % 4 < 2 else "sequential"
+        dtype = torch.bfloat16 if i % 2 else torch.float32
+        shared = variant == "blelloch" and i % 2 == 1
+        cases.append(pytest.param(variant, NH, NKVH, D, r, (P, Q, K), B, T, dtype, shared,
+                                  id=f"{i}-{variant}-{'bf16' if i % 2 else 'f32'}-h{NH}.{NKVH}"
+                                     f"-D{D}-r{r}-pqk{P}.{Q}.{K}-B{B}-T{T}"))
+    return cases
+
+
+@pytest.mark.parametrize("variant, NH, NKVH, D, r, pqk, B, T, dtype, shared", _random_cases())
+def test_look_back_filter_random(variant, NH, NKVH, D, r, pqk, B, T, dtype, shared):
+    io = "bf16" if dtype == torch.bfloat16 else "f32"
+    f = _make(variant, NH, NKVH, D, r, pqk, seed=T)
+    C = NH * D
+    g = torch.Generator().manual_seed(B * 1000 + T)
+    x = torch.randn(B, T, C, generator=g).to(dtype)
+    gq = torch.randn(B, T, NH, D, generator=g).to(dtype)
+    gk = torch.randn(B, T, NKVH, D, generator=g).to(dtype)
+    gv = torch.randn(B, T, NKVH, D, generator=g).to(dtype)
+    xd = x.to(DEV).requires_grad_(True)
+    inits = f.init_param if shared else f.init_param.unsqueeze(0).expand(B, -1, -1)
+    q, k, v = f(xd, inits, full_recurrence=False)
+    torch.autograd.backward([q, k, v], [gq.to(DEV), gk.to(DEV), gv.to(DEV)])
+    (eq, ek, ev), egx, egw, egi, egb = _oracle(f, x.float().numpy(), gq.float().numpy(),
+                                              gk.float().numpy(), gv.float().numpy(), pqk, io)
+    tol = TOL[dtype]
+    assert_close(np_of(q), eq, tol, "q")
+    assert_close(np_of(k), ek, tol, "k")
+    assert_close(np_of(v), ev, tol, "v")
+    assert_close(np_of(xd.grad), egx, tol, "grad_x")
+    assert_close(np_of(f.c.weight.grad), egw, tol, "grad_weight")
+    assert_close(np_of(f.init_param.grad), egi, tol, "grad_init_param")
+    assert_close(np_of(f.logit_bias.grad), egb, tol, "grad_logit_bias")
