@@ -13,6 +13,13 @@ forward (bf16 MFMA projection into the head-major layout, gated EWMA scan) and
 backward (reverse scan, projection dX and dW) via autograd.  Inputs are resident
 in HBM before the timed region.  ``value`` = tokens / s = B*T*K / elapsed.
 
+Before the W warm-up steps, untimed steps of the same workload run for
+``--settle-s`` seconds (0.1 by default; reported as ``settle``): after an idle
+period the GPU's clock ramps up over the first 15-20 ms of load (measured on
+MI355X at configs[2]: per-step times fall from 590-630 us to about 520 us over
+the first ~30 steps of a process), and the metric is the steady-state rate of a
+training loop.  The timed region is still exactly K full steps.
+
 ``--workload look_back`` runs the same shapes through the look-back filter
 with the d12 layer spec (P, Q, K) = (16, 16, 9): chunks of 16 steps, each
 restarted from the inits over an 8-step warm-up (the reference's production
@@ -193,11 +200,34 @@ def cpu_baseline(seconds_target: float = 10.0, pqk=None):
     }
 
 
+def settle(step, seconds: float) -> int:
+    """Untimed steps for ``seconds`` of wall time (the GPU clock's ramp from
+    idle), counted from the end of a first step that takes the one-time costs
+    (library load, first allocations); the queue is drained every 8 steps so
+    it stays short.  Returns the number of steps run."""
+    import torch
+    if seconds <= 0:
+        return 0
+    step()
+    torch.cuda.synchronize()
+    n = 1
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end:
+        for _ in range(8):
+            step()
+        n += 8
+        torch.cuda.synchronize()
+    return n
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--settle-s", type=float, default=0.1,
+                    help="untimed steps for this many seconds before the warm-up steps (the "
+                         "GPU clock's ramp from idle); 0: none")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--workload",
@@ -296,6 +326,7 @@ def main():
         q, k, v = forward()
         torch.autograd.backward([q, k, v], [dq, dk, dv])
 
+    settled = settle(step, args.settle_s)
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -366,6 +397,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "settle": {"seconds": args.settle_s, "steps": settled},
         "ms_per_step": round(ms_per_step, 4),
         "higher_is_better": True,
         "scaling": "weak",
@@ -518,6 +550,7 @@ def lt_f32_main(args):
         ops.fused_linear_transpose_cuda_op(x, w)
         ops.fused_linear_transpose_backward_kernel(x, w, go, gx, gw)
 
+    settled = settle(step, args.settle_s)
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -568,6 +601,7 @@ def lt_f32_main(args):
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "settle": {"seconds": args.settle_s, "steps": settled},
         "ms_per_step": round(elapsed * 1e3 / args.steps, 4),
         "higher_is_better": True,
         "scaling": "weak",
@@ -683,6 +717,7 @@ def scan_fwd_main(args):
     def step():
         return hm.scan_forward(u, logits, inits, bias, 6, 6, SF_D, 1, True)
 
+    settled = settle(step, args.settle_s)
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -715,6 +750,7 @@ def scan_fwd_main(args):
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "settle": {"seconds": args.settle_s, "steps": settled},
         "ms_per_step": round(ms_per_step, 4),
         "higher_is_better": True,
         "scaling": "weak",
@@ -772,6 +808,7 @@ def prefill_main(args):
         with torch.no_grad():
             return f(x, none)
 
+    settled = settle(step, args.settle_s)
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -818,6 +855,7 @@ def prefill_main(args):
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "settle": {"seconds": args.settle_s, "steps": settled},
         "ms_per_step": round(elapsed * 1e3 / args.steps, 4),
         "higher_is_better": True,
         "scaling": "weak",
@@ -885,6 +923,7 @@ def decode_main(args):
             for t in range(DC_T0, DC_T0 + DC_N):
                 m(xs[:, t:t + 1], cache)
 
+    settled = settle(lambda: decode_pass(new_cache()), args.settle_s)
     for _ in range(max(args.warmup, 1)):
         decode_pass(new_cache())
     caches = [new_cache() for _ in range(args.steps)]
@@ -941,6 +980,7 @@ def decode_main(args):
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "settle": {"seconds": args.settle_s, "steps": settled},
         "ms_per_step": round(elapsed * 1e3 / (args.steps * DC_N), 4),
         "higher_is_better": True,
         "scaling": "weak",
@@ -990,6 +1030,7 @@ def gpt_main(args):
             loss = model(idx, tgt)
         loss.backward()
 
+    settled = settle(step, args.settle_s)
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -1014,6 +1055,7 @@ def gpt_main(args):
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "settle": {"seconds": args.settle_s, "steps": settled},
         "ms_per_step": round(ms_per_step, 4),
         "higher_is_better": True,
         "scaling": "weak",
