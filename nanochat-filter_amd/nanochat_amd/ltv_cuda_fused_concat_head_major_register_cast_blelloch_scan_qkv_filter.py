@@ -135,7 +135,7 @@ class LtvCudaFusedConcatHeadMajorRegisterCastBlellochScanQkvFilter(
     def _forward_bf16(self, x, inits):
         """inits: (B, H, D) bf16, contiguous or the batch-shared view, or the
         (H, D) parameter (fp32 or bf16) shared by every sequence."""
-        hq, hk, hv, _, _, _ = torch.ops.nanochat_amd.qkv_filter(
+        hq, hk, hv, _, _, _ = hm_fast.qkv_filter_call(
             x.to(torch.bfloat16).contiguous(),
             self.c.weight,
             inits,

@@ -119,7 +119,7 @@ def look_back_fused_forward(filt: LtvLookBackHeadMajorQkvFilter, x: torch.Tensor
         inits = resolved_inits
     else:
         inits = resolved_inits.to(torch.bfloat16).contiguous()
-    hq, hk, hv, _, _, _ = torch.ops.nanochat_amd.qkv_filter(
+    hq, hk, hv, _, _, _ = hm_fast.qkv_filter_call(
         x.contiguous(), filt.c.weight, inits, filt.logit_bias.float().contiguous(),
         NH, NKVH, Da, filt.r, P, Q, K)
     return hq.transpose(1, 2), hk.transpose(1, 2), hv.transpose(1, 2)

@@ -356,17 +356,21 @@ def scan_backward(values, logits, inits, logit_bias, hq, hk, hv, gq, gk, gv, NH:
 # ---------------------------------------------------------------------------
 # the fused op
 # ---------------------------------------------------------------------------
+def _qkv_filter_impl(x, weight, inits, logit_bias, NH, NKVH, Da, r, P, Q, K):
+    H = NH + 2 * NKVH
+    D = Da * r
+    values, logits, wpack = project(x, weight, H, D, Da)
+    q, k, v = scan_forward(values, logits, inits, logit_bias, NH, NKVH, Da, r, True, P, Q, K)
+    return q, k, v, values, logits, wpack
+
+
 @torch.library.custom_op("nanochat_amd::qkv_filter", mutates_args=())
 def qkv_filter(x: torch.Tensor, weight: torch.Tensor, inits: torch.Tensor,
                logit_bias: torch.Tensor, NH: int, NKVH: int, Da: int, r: int,
                P: int = UNBOUNDED_P, Q: int = 1,
                K: int = 1) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor,
                                     torch.Tensor, torch.Tensor]:
-    H = NH + 2 * NKVH
-    D = Da * r
-    values, logits, wpack = project(x, weight, H, D, Da)
-    q, k, v = scan_forward(values, logits, inits, logit_bias, NH, NKVH, Da, r, True, P, Q, K)
-    return q, k, v, values, logits, wpack
+    return _qkv_filter_impl(x, weight, inits, logit_bias, NH, NKVH, Da, r, P, Q, K)
 
 
 @qkv_filter.register_fake
@@ -381,14 +385,8 @@ def _(x, weight, inits, logit_bias, NH, NKVH, Da, r, P=UNBOUNDED_P, Q=1, K=1):
             x.new_empty((packed_width(H, D, Da), C), dtype=bf))
 
 
-@torch.library.custom_op("nanochat_amd::qkv_filter_backward", mutates_args=())
-def qkv_filter_backward(x: torch.Tensor, wpack: torch.Tensor, values: torch.Tensor,
-                        logits: torch.Tensor, inits: torch.Tensor, logit_bias: torch.Tensor,
-                        hq: torch.Tensor, hk: torch.Tensor, hv: torch.Tensor, gq: torch.Tensor,
-                        gk: torch.Tensor, gv: torch.Tensor, NH: int, NKVH: int, Da: int,
-                        r: int, P: int = UNBOUNDED_P, Q: int = 1,
-                        K: int = 1) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor,
-                                             torch.Tensor]:
+def _qkv_filter_backward_impl(x, wpack, values, logits, inits, logit_bias, hq, hk, hv, gq, gk,
+                              gv, NH, NKVH, Da, r, P, Q, K):
     B, T, C = x.shape
     H = NH + 2 * NKVH
     D = Da * r
@@ -400,6 +398,18 @@ def qkv_filter_backward(x: torch.Tensor, wpack: torch.Tensor, values: torch.Tens
                                           zero_pad=True)
     grad_x, grad_w = project_backward(x, wpack, grad_combined, H, D, Da, pad_zeroed=True)
     return grad_x, grad_w, grad_inits, grad_bias
+
+
+@torch.library.custom_op("nanochat_amd::qkv_filter_backward", mutates_args=())
+def qkv_filter_backward(x: torch.Tensor, wpack: torch.Tensor, values: torch.Tensor,
+                        logits: torch.Tensor, inits: torch.Tensor, logit_bias: torch.Tensor,
+                        hq: torch.Tensor, hk: torch.Tensor, hv: torch.Tensor, gq: torch.Tensor,
+                        gk: torch.Tensor, gv: torch.Tensor, NH: int, NKVH: int, Da: int,
+                        r: int, P: int = UNBOUNDED_P, Q: int = 1,
+                        K: int = 1) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor,
+                                             torch.Tensor]:
+    return _qkv_filter_backward_impl(x, wpack, values, logits, inits, logit_bias, hq, hk, hv,
+                                     gq, gk, gv, NH, NKVH, Da, r, P, Q, K)
 
 
 @qkv_filter_backward.register_fake
@@ -438,3 +448,45 @@ def _filter_backward(ctx, gq, gk, gv, g_values, g_logits, g_wpack):
 
 
 qkv_filter.register_autograd(_filter_backward, setup_context=_filter_setup)
+
+
+class _QkvFilterEager(torch.autograd.Function):
+    """The op's forward and backward implementations under a plain autograd
+    function: the same launches, without the library op's dispatch (default
+    filling, the compiler guards, the registered-autograd wrapper), which took
+    about as much host time per step as the launches themselves."""
+
+    @staticmethod
+    def forward(ctx, x, weight, inits, logit_bias, NH, NKVH, Da, r, P, Q, K):
+        out = _qkv_filter_impl(x, weight, inits, logit_bias, NH, NKVH, Da, r, P, Q, K)
+        q, k, v, values, logits, wpack = out
+        ctx.save_for_backward(x, wpack, values, logits, inits, logit_bias, q, k, v)
+        ctx.args = (NH, NKVH, Da, r, P, Q, K)
+        ctx.weight_dtype = weight.dtype
+        ctx.mark_non_differentiable(values, logits, wpack)
+        ctx.set_materialize_grads(False)
+        return out
+
+    @staticmethod
+    def backward(ctx, gq, gk, gv, g_values, g_logits, g_wpack):
+        x, wpack, values, logits, inits, logit_bias, q, k, v = ctx.saved_tensors
+        gq = torch.zeros_like(q) if gq is None else gq
+        gk = torch.zeros_like(k) if gk is None else gk
+        gv = torch.zeros_like(v) if gv is None else gv
+        gx, gw, gi, gb = _qkv_filter_backward_impl(x, wpack, values, logits, inits, logit_bias,
+                                                   q, k, v, gq, gk, gv, *ctx.args)
+        if ctx.weight_dtype != torch.float32:
+            gw = gw.to(ctx.weight_dtype)
+        return (gx, gw, gi, gb.view_as(logit_bias)) + (None,) * len(ctx.args)
+
+
+def qkv_filter_call(x: torch.Tensor, weight: torch.Tensor, inits: torch.Tensor,
+                    logit_bias: torch.Tensor, NH: int, NKVH: int, Da: int, r: int,
+                    P: int = UNBOUNDED_P, Q: int = 1, K: int = 1):
+    """``nanochat_amd::qkv_filter`` as the filter modules call it: the library
+    op under ``torch.compile`` (its schema, fake impl and registered autograd),
+    the same implementation through ``_QkvFilterEager`` in eager mode."""
+    if torch.compiler.is_compiling():
+        return torch.ops.nanochat_amd.qkv_filter(x, weight, inits, logit_bias, NH, NKVH, Da, r,
+                                                 P, Q, K)
+    return _QkvFilterEager.apply(x, weight, inits, logit_bias, NH, NKVH, Da, r, P, Q, K)
