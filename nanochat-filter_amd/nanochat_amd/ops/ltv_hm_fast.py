@@ -433,18 +433,24 @@ def _filter_setup(ctx, inputs, output):
     ctx.set_materialize_grads(False)
 
 
-def _filter_backward(ctx, gq, gk, gv, g_values, g_logits, g_wpack):
+def _filter_grads(ctx, gq, gk, gv, backward_fn):
+    """Input gradients from the saved tensors, through ``backward_fn`` (the
+    library op or its implementation)."""
     x, wpack, values, logits, inits, logit_bias, q, k, v = ctx.saved_tensors
     # upstream grads keep their strides (typically the transposed (B, T, H, D)
     # views): the scan backward reads any layout, 16-byte vectors along D
     gq = torch.zeros_like(q) if gq is None else gq
     gk = torch.zeros_like(k) if gk is None else gk
     gv = torch.zeros_like(v) if gv is None else gv
-    gx, gw, gi, gb = torch.ops.nanochat_amd.qkv_filter_backward(
-        x, wpack, values, logits, inits, logit_bias, q, k, v, gq, gk, gv, *ctx.args)
+    gx, gw, gi, gb = backward_fn(x, wpack, values, logits, inits, logit_bias, q, k, v, gq, gk, gv,
+                                 *ctx.args)
     if ctx.weight_dtype != torch.float32:
         gw = gw.to(ctx.weight_dtype)
     return (gx, gw, gi, gb.view_as(logit_bias)) + (None,) * len(ctx.args)
+
+
+def _filter_backward(ctx, gq, gk, gv, g_values, g_logits, g_wpack):
+    return _filter_grads(ctx, gq, gk, gv, torch.ops.nanochat_amd.qkv_filter_backward)
 
 
 qkv_filter.register_autograd(_filter_backward, setup_context=_filter_setup)
@@ -459,25 +465,13 @@ class _QkvFilterEager(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, weight, inits, logit_bias, NH, NKVH, Da, r, P, Q, K):
         out = _qkv_filter_impl(x, weight, inits, logit_bias, NH, NKVH, Da, r, P, Q, K)
-        q, k, v, values, logits, wpack = out
-        ctx.save_for_backward(x, wpack, values, logits, inits, logit_bias, q, k, v)
-        ctx.args = (NH, NKVH, Da, r, P, Q, K)
-        ctx.weight_dtype = weight.dtype
-        ctx.mark_non_differentiable(values, logits, wpack)
-        ctx.set_materialize_grads(False)
+        _filter_setup(ctx, (x, weight, inits, logit_bias, NH, NKVH, Da, r, P, Q, K), out)
+        ctx.mark_non_differentiable(*out[3:])
         return out
 
     @staticmethod
     def backward(ctx, gq, gk, gv, g_values, g_logits, g_wpack):
-        x, wpack, values, logits, inits, logit_bias, q, k, v = ctx.saved_tensors
-        gq = torch.zeros_like(q) if gq is None else gq
-        gk = torch.zeros_like(k) if gk is None else gk
-        gv = torch.zeros_like(v) if gv is None else gv
-        gx, gw, gi, gb = _qkv_filter_backward_impl(x, wpack, values, logits, inits, logit_bias,
-                                                   q, k, v, gq, gk, gv, *ctx.args)
-        if ctx.weight_dtype != torch.float32:
-            gw = gw.to(ctx.weight_dtype)
-        return (gx, gw, gi, gb.view_as(logit_bias)) + (None,) * len(ctx.args)
+        return _filter_grads(ctx, gq, gk, gv, _qkv_filter_backward_impl)
 
 
 def qkv_filter_call(x: torch.Tensor, weight: torch.Tensor, inits: torch.Tensor,
