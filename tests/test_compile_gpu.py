@@ -11,7 +11,10 @@ ops for that (nanochat/ops/ltv_cuda_meta.py:155-252, 341-377).  Here:
     the eager loss and filter gradients (the other ops may fuse, so within
     bf16 tolerance);
   * ``torch.library.opcheck`` passes for the ops (schema, fake tensors,
-    autograd registration, AOT dispatch).
+    autograd registration, AOT dispatch);
+  * in eager mode the modules run the fused op's implementations through a
+    plain autograd function: its outputs and every gradient equal the library
+    op's bitwise (shared and per-sequence inits, one upstream gradient absent).
 """
 
 from __future__ import annotations
@@ -135,3 +138,31 @@ def test_opcheck_reference_namespace_ops():
     x = torch.randn(B, T, 64, generator=g).to(DEV).requires_grad_(True)
     w = torch.randn(96, 64, generator=g).to(DEV).requires_grad_(True)
     _opcheck(torch.ops.nanochat_cuda.fused_linear_transpose_cuda_op.default, (x, w))
+
+
+@pytest.mark.parametrize("shared", [False, True], ids=["batch_inits", "shared_inits"])
+def test_eager_function_matches_library_op(shared):
+    from nanochat_amd.ops import ltv_hm_fast as hm
+    NH, NKVH, D, r, B, T = 2, 1, 64, 16, 3, 150
+    H, Da, C = NH + 2 * NKVH, D // r, NH * D
+    g = torch.Generator().manual_seed(5)
+    x0 = torch.randn(B, T, C, generator=g).to(torch.bfloat16).to(DEV)
+    w0 = (torch.randn(H * (D + Da), C, generator=g) / C ** 0.5).to(DEV)
+    i0 = torch.randn(H, D, generator=g) if shared else torch.randn(B, H, D, generator=g)
+    i0 = i0.to(torch.bfloat16).to(DEV)
+    b0 = (torch.rand(H, Da, generator=g) - 0.5).to(DEV)
+    gq = torch.randn(B, NH, T, D, generator=g).to(torch.bfloat16).to(DEV)
+    gv = torch.randn(B, NKVH, T, D, generator=g).to(torch.bfloat16).to(DEV)
+
+    def run(fn):
+        x, w, i, b = (t.detach().clone().requires_grad_(True) for t in (x0, w0, i0, b0))
+        q, k, v, *_ = fn(x, w, i, b, NH, NKVH, Da, r)
+        torch.autograd.backward([q, v], [gq, gv])  # k's gradient absent
+        torch.cuda.synchronize()
+        return [q, k, v, x.grad, w.grad, i.grad, b.grad]
+
+    want = run(torch.ops.nanochat_amd.qkv_filter)
+    got = run(hm.qkv_filter_call)
+    names = ["q", "k", "v", "grad_x", "grad_weight", "grad_inits", "grad_logit_bias"]
+    for name, a, e in zip(names, got, want):
+        assert torch.equal(a, e), f"{name}: eager function differs from the library op"
