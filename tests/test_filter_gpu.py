@@ -15,7 +15,7 @@ import pytest
 import torch
 
 import ltv_oracle as O
-from ltv_test_utils import TOL, assert_close, io_name, np_of
+from ltv_test_utils import TOL, assert_close, assert_norm_rel, io_name, np_of
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -141,10 +141,9 @@ def test_filter_random_shapes(NH, NKVH, D, r, B, T, dtype):
     (eq, ek, ev), egx, egw, egi, egb = _oracle(
         f, x.float().numpy(), dq.float().numpy(), dk.float().numpy(), dv.float().numpy(), io)
     tol = TOL[dtype]
-    assert_close(np_of(q), eq, tol, "q")
-    assert_close(np_of(k), ek, tol, "k")
-    assert_close(np_of(v), ev, tol, "v")
-    assert_close(np_of(xd.grad), egx, tol, "grad_x")
-    assert_close(np_of(f.c.weight.grad), egw, tol, "grad_weight")
-    assert_close(np_of(f.init_param.grad), egi, tol, "grad_init_param")
-    assert_close(np_of(f.logit_bias.grad), egb, tol, "grad_logit_bias")
+    for name, got, want in (("q", q, eq), ("k", k, ek), ("v", v, ev), ("grad_x", xd.grad, egx),
+                            ("grad_weight", f.c.weight.grad, egw),
+                            ("grad_init_param", f.init_param.grad, egi),
+                            ("grad_logit_bias", f.logit_bias.grad, egb)):
+        assert_close(np_of(got), want, tol, name)
+        assert_norm_rel(np_of(got), want, tol, name)
