@@ -1653,21 +1653,17 @@ scan_bwd_kernel(const BwdArgs args) {
       // whose own gate gives the slope
       // (compile-time levels with masked adds: a loop or a branch around the
       // shuffles makes the compiler drain every outstanding memory operation
-      // at the top of the tile loop).  Shifts inside a 16-lane row are DPP
-      // moves: the lead lane ends a row (or a group within one), and so does
-      // every lane whose partial sum reaches it, so at each level these lanes
-      // read a source in their own row -- the same sums, in the same order,
-      // as the cross-lane shuffle, without the round trip through the LDS.
+      // at the top of the tile loop).  Every level is a cross-lane shuffle:
+      // a group of a non-power-of-two number of lanes (r / V = 3, 5, 6, ...)
+      // straddles 16-lane rows, and a lane on the path to its lead can then
+      // need a source in the row before, which a DPP row shift cannot reach
+      // (it reads 0 there).
       static_loop<0, ilog2(CL)>([&](auto lc) __attribute__((always_inline)) {
         constexpr int d = 1 << decltype(lc)::value;
         const bool take = d < gl_lanes && cl - d >= seg0;
 #pragma unroll
         for (int s = 0; s < L; ++s) {
-          float q;
-          if constexpr (d * TG < 16)
-            q = shift_up<16, d * TG>(pl[s]);
-          else
-            q = __shfl_up(pl[s], d * TG, 64);
+          const float q = __shfl_up(pl[s], d * TG, 64);
           pl[s] += take ? q : 0.0f;
         }
       });

@@ -114,7 +114,8 @@ def test_exact_all_strides(dtype, pqk, T):
 
 
 @pytest.mark.parametrize("dtype", DTYPES, ids=io_name)
-@pytest.mark.parametrize("D,r", [(128, 128), (128, 16), (128, 8), (128, 1), (64, 4), (32, 32)])
+@pytest.mark.parametrize("D,r", [(128, 128), (128, 16), (128, 8), (128, 1), (64, 4), (32, 32),
+                                 (48, 24), (40, 40), (120, 24)])
 @pytest.mark.parametrize("pqk", [(64, 60, 5), (224, 100, 125), (16, 16, 9), (0, 48, 80)],
                          ids=str)
 def test_exact_wide_heads_many_windows(dtype, D, r, pqk):

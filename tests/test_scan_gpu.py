@@ -112,6 +112,9 @@ def test_backward_exact_all_strides(dtype, T):
 # per-channel fallback; contiguous (B, T, F) and the projection's (B, F, T) view
 WIDE_CASES = [(128, r) for r in (1, 2, 4, 8, 16, 32, 64, 128)] + [(12, 3), (12, 12), (24, 24),
                                                                   (40, 5)]
+# gate groups of a non-power-of-two number of channel lanes (r / V = 3, 5, 6, 10, 12 with 8 bf16
+# or 4 fp32 channels per lane), which straddle the wavefront's 16-lane rows
+WIDE_CASES += [(48, 24), (40, 40), (120, 24), (96, 12), (96, 48)]
 
 
 @pytest.mark.parametrize("dtype", DTYPES, ids=io_name)
