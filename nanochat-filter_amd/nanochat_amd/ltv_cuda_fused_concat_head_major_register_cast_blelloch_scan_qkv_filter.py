@@ -99,7 +99,8 @@ class LtvCudaFusedConcatHeadMajorRegisterCastBlellochScanQkvFilter(
         general path and the module's own row update."""
         if (x.size(1) != 1 or torch.is_grad_enabled() or previous_values.q is None
                 or any(t is None for t in rows)
-                or self._compute_dtype(x) != torch.bfloat16):
+                or self._compute_dtype(x) != torch.bfloat16
+                or not hm_fast.decode_ok(x.size(2), self.head_dim)):
             return None
         if any(t.dtype != torch.bfloat16 or t.device != x.device or t.stride(-1) != 1
                for t in rows):
@@ -107,9 +108,12 @@ class LtvCudaFusedConcatHeadMajorRegisterCastBlellochScanQkvFilter(
         return self._decode_bf16(x, previous_values, rows)
 
     def forward(self, x, previous_values: LtvInitValues):
-        B, _, _ = x.size()
+        B, _, C = x.size()
         compute_dtype = self._compute_dtype(x)
-        if compute_dtype == torch.bfloat16 and x.size(1) == 1 and not torch.is_grad_enabled():
+        if compute_dtype == torch.bfloat16 and not hm_fast.fast_path_ok(C, self.head_dim):
+            return self._forward_bf16_dataflow(x, previous_values)
+        if (compute_dtype == torch.bfloat16 and x.size(1) == 1 and not torch.is_grad_enabled()
+                and hm_fast.decode_ok(C, self.head_dim)):
             return self._decode_bf16(x, previous_values)
         if compute_dtype == torch.bfloat16:
             if previous_values.q is None and self._shared_inits_in_kernel():
@@ -172,6 +176,25 @@ class LtvCudaFusedConcatHeadMajorRegisterCastBlellochScanQkvFilter(
                                   self.num_alpha_groups, self.r, rows=rows)
         # (B, 1, nh, D) views of the new rows, in one split
         return out.unsqueeze(1).split((NH, NKVH, NKVH), dim=2)
+
+    def _forward_bf16_dataflow(self, x, previous_values):
+        """bf16 for the shapes the fused path does not take (C not a multiple
+        of 8, D not of 4): the reference's dataflow in bf16 -- the projection
+        into a (B, F, T) buffer with the weight rounded to bf16, then the scan
+        through the transposed view."""
+        bf = torch.bfloat16
+        out_buf = fused_linear_transpose(x.to(bf).contiguous(), self.c.weight.to(bf).contiguous())
+        kernel_combined = out_buf.transpose(1, 2)
+        inits = resolve_inits_original_dtype(x.size(0), self.init_param, previous_values).to(
+            dtype=bf).contiguous()
+        hq, hk, hv = ltv_cuda_fused_concat_head_major_register_cast_blelloch_scan(
+            kernel_combined, inits, self.logit_bias.float().contiguous(), self.n_head,
+            self.n_kv_head, self.num_alpha_groups, self.r,
+            _SCAN_THREADS_FORWARD, _R_THREADS_FORWARD, _R_ITEMS_FORWARD,
+            _SCAN_THREADS_BACKWARD, _R_THREADS_BACKWARD, _R_ITEMS_BACKWARD,
+            True,  # use_sigmoid
+        )
+        return hq.transpose(1, 2), hk.transpose(1, 2), hv.transpose(1, 2)
 
     def _forward_fp32(self, x, inits):
         out_buf = fused_linear_transpose(x.float().contiguous(), self.c.weight.float().contiguous())

@@ -62,7 +62,8 @@ class LtvLookBackFusedConcatHeadMajorRegisterCastBlellochScanQkvFilter(
         cache): the library then sums its gradient over the batch where the
         kernels can, else it is expanded to (B, H, D) here."""
         fused = (self._uses_library_ops() and x.is_cuda and x.dtype == torch.bfloat16
-                 and not should_run_ltv_in_fp32(x.device.type))
+                 and not should_run_ltv_in_fp32(x.device.type)
+                 and hm_fast.fast_path_ok(x.size(2), self.head_dim))
         if resolved_inits.dim() == 2 and not (fused and self.takes_shared_inits(x, full_recurrence)):
             resolved_inits = resolved_inits.unsqueeze(0).expand(x.size(0), -1, -1)
         if fused:
@@ -79,9 +80,8 @@ class LtvLookBackFusedConcatHeadMajorRegisterCastBlellochScanQkvFilter(
         return hm_fast.fp32_inits_ok(x.size(1), self.head_dim, self.r, P, Q, K)
 
     def _project(self, x: torch.Tensor) -> torch.Tensor:
-        fp32 = x.dtype == torch.float32
-        out_buf = self.transpose_op(x.float() if fp32 else x,
-                                    self.c.weight.float() if fp32 else self.c.weight)
+        # the projection runs in x's dtype (the weight rounded to it)
+        out_buf = self.transpose_op(x, self.c.weight.to(x.dtype))
         return out_buf.transpose(1, 2)  # (B, T, F) view of the (B, F, T) buffer
 
     def _look_back_op(self, combined, inits, logit_bias, full_recurrence: bool):
@@ -101,7 +101,8 @@ def look_back_fused_forward(filt: LtvLookBackHeadMajorQkvFilter, x: torch.Tensor
     """bf16 fused path of a look-back filter: (q, k, v) as (B, T, H, D) views."""
     NH, NKVH, Da, D = filt.n_head, filt.n_kv_head, filt.num_alpha_groups, filt.head_dim
     H = NH + 2 * NKVH
-    if full_recurrence and x.size(1) == 1 and not torch.is_grad_enabled():
+    if (full_recurrence and x.size(1) == 1 and not torch.is_grad_enabled()
+            and hm_fast.decode_ok(x.size(2), D)):
         inits = resolved_inits.to(torch.bfloat16)
         # one recurrence step from the cached rows: the fused decode kernel
         wpack = hm_fast.cached_packed_weight(filt, H, D, Da)

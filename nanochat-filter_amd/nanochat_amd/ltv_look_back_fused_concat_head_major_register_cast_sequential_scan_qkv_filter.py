@@ -24,6 +24,7 @@ from nanochat_amd.ltv_look_back_fused_concat_head_major_register_cast_blelloch_s
     look_back_fused_forward,
 )
 from nanochat_amd.ltv_look_back_head_major_qkv_filter_base import LtvLookBackHeadMajorQkvFilter
+from nanochat_amd.ops import ltv_hm_fast as hm_fast
 from nanochat_amd.ops.ltv_cuda_ops import (
     ltv_cuda_look_back_fused_concat_head_major_register_cast_sequential_scan,
 )
@@ -45,12 +46,14 @@ class LtvLookBackFusedConcatHeadMajorRegisterCastSequentialScanQkvFilter(
         if (self.sequential_look_back_op is
                 ltv_cuda_look_back_fused_concat_head_major_register_cast_sequential_scan
                 and x.is_cuda and x.dtype == torch.bfloat16
-                and not should_run_ltv_in_fp32(x.device.type)):
+                and not should_run_ltv_in_fp32(x.device.type)
+                and hm_fast.fast_path_ok(x.size(2), self.head_dim)):
             return look_back_fused_forward(self, x, resolved_inits, full_recurrence)
         return super().forward(x, resolved_inits, full_recurrence)
 
     def _project(self, x: torch.Tensor) -> torch.Tensor:
-        return self.c(x).contiguous()
+        # in x's dtype, the weight rounded to it
+        return torch.nn.functional.linear(x, self.c.weight.to(x.dtype)).contiguous()
 
     def _look_back_op(self, combined, inits, logit_bias, full_recurrence: bool):
         P, Q, K = self.chunking(full_recurrence)

@@ -226,6 +226,21 @@ def project_backward(x: torch.Tensor, wpack: torch.Tensor, grad_combined: torch.
     return grad_x, grad_w
 
 
+def fast_path_ok(C: int, D: int) -> bool:
+    """Whether the fused bf16 path (the head-major MFMA projection and its
+    backward) takes this width and head size: C a multiple of 8 (16-byte rows
+    of x and of the packed weight), D of 4.  The filters run other shapes
+    through the reference dataflow (``fused_linear_transpose`` in bf16, then
+    the scan op)."""
+    return C % 8 == 0 and D % 4 == 0
+
+
+def decode_ok(C: int, D: int) -> bool:
+    """Whether the fused decode step takes this shape: the fused path's, with
+    C a multiple of 16 (the step's k16 MFMA slices)."""
+    return fast_path_ok(C, D) and C % 16 == 0
+
+
 def shared_inits_ok(D: int, Da: int, r: int) -> bool:
     """Whether the bf16 scan takes one (H, D) set of inits for every sequence,
     fp32 or bf16, with the inits gradient summed over the batch by the

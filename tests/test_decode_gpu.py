@@ -82,7 +82,11 @@ def _general_step(f, x, prev):
 
 
 @pytest.mark.parametrize("NH,NKVH,D,r,B", [(6, 6, 128, 128, 64), (4, 2, 128, 32, 37),
-                                            (2, 1, 64, 1, 5), (3, 0, 64, 16, 33)])
+                                            (2, 1, 64, 1, 5), (3, 0, 64, 16, 33),
+                                            # C = 24: not the fused step's multiple of 16, the
+                                            # fused path at T = 1; C = 12, D = 6: the reference
+                                            # dataflow in bf16
+                                            (1, 1, 24, 24, 9), (1, 1, 12, 12, 5), (2, 1, 6, 2, 3)])
 def test_decode_step_matches_oracle_and_general_path(NH, NKVH, D, r, B):
     from nanochat_amd.ltv.ltv_filter import LtvInitValues
     f = _make_filter(NH, NKVH, D, r, seed=NH + r)

@@ -147,3 +147,34 @@ def test_filter_random_shapes(NH, NKVH, D, r, B, T, dtype):
                             ("grad_logit_bias", f.logit_bias.grad, egb)):
         assert_close(np_of(got), want, tol, name)
         assert_norm_rel(np_of(got), want, tol, name)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("NH,NKVH,D,r", [(1, 1, 12, 12), (3, 2, 4, 4), (3, 1, 12, 3), (2, 1, 6, 2)])
+def test_filter_shapes_outside_the_fused_path(dtype, NH, NKVH, D, r):
+    """C not a multiple of 8 or D not of 4: bf16 runs the reference dataflow
+    (the projection into (B, F, T) with the weight rounded to bf16, then the
+    scan op) instead of the fused path; forward and every gradient against the
+    oracle."""
+    from nanochat_amd.ltv.ltv_filter import LtvInitValues
+    io = io_name(dtype)
+    f = _make_filter(NH=NH, NKVH=NKVH, D=D, r=r, seed=D + r)
+    B, T, C = 2, 75, NH * D
+    g = torch.Generator().manual_seed(C)
+    x = torch.randn(B, T, C, generator=g).to(dtype)
+    dq = torch.randn(B, T, NH, D, generator=g).to(dtype)
+    dk = torch.randn(B, T, NKVH, D, generator=g).to(dtype)
+    dv = torch.randn(B, T, NKVH, D, generator=g).to(dtype)
+    xd = x.to(DEV).requires_grad_(True)
+    q, k, v = f(xd, LtvInitValues())
+    assert q.dtype == dtype
+    torch.autograd.backward([q, k, v], [dq.to(DEV), dk.to(DEV), dv.to(DEV)])
+    (eq, ek, ev), egx, egw, egi, egb = _oracle(
+        f, x.float().numpy(), dq.float().numpy(), dk.float().numpy(), dv.float().numpy(), io)
+    tol = TOL[dtype]
+    for name, got, want in (("q", q, eq), ("k", k, ek), ("v", v, ev), ("grad_x", xd.grad, egx),
+                            ("grad_weight", f.c.weight.grad, egw),
+                            ("grad_init_param", f.init_param.grad, egi),
+                            ("grad_logit_bias", f.logit_bias.grad, egb)):
+        assert_close(np_of(got), want, tol, name)
+        assert_norm_rel(np_of(got), want, tol, name)

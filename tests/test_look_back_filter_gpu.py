@@ -276,3 +276,32 @@ def test_look_back_filter_random(variant, NH, NKVH, D, r, pqk, B, T, dtype, shar
                             ("grad_logit_bias", f.logit_bias.grad, egb)):
         assert_close(np_of(got), want, tol, name)
         assert_norm_rel(np_of(got), want, tol, name)
+
+
+@pytest.mark.parametrize("variant", ["blelloch", "sequential"])
+@pytest.mark.parametrize("NH,NKVH,D,r", [(1, 1, 12, 4), (2, 1, 6, 2)])
+def test_look_back_filter_shapes_outside_the_fused_path(variant, NH, NKVH, D, r):
+    """bf16 with C not a multiple of 8 or D not of 4: the generic dataflow
+    (projection in bf16 with the weight rounded to it, then the look-back op),
+    forward and every gradient against the oracle."""
+    pqk = (16, 16, 9)
+    f = _make(variant, NH, NKVH, D, r, pqk, seed=D)
+    B, T, C = 2, 70, NH * D
+    g = torch.Generator().manual_seed(C)
+    dtype = torch.bfloat16
+    x = torch.randn(B, T, C, generator=g).to(dtype)
+    gq = torch.randn(B, T, NH, D, generator=g).to(dtype)
+    gk = torch.randn(B, T, NKVH, D, generator=g).to(dtype)
+    gv = torch.randn(B, T, NKVH, D, generator=g).to(dtype)
+    xd = x.to(DEV).requires_grad_(True)
+    q, k, v = f(xd, f.init_param.unsqueeze(0).expand(B, -1, -1), full_recurrence=False)
+    torch.autograd.backward([q, k, v], [gq.to(DEV), gk.to(DEV), gv.to(DEV)])
+    (eq, ek, ev), egx, egw, egi, egb = _oracle(f, x.float().numpy(), gq.float().numpy(),
+                                              gk.float().numpy(), gv.float().numpy(), pqk, "bf16")
+    tol = TOL[dtype]
+    for name, got, want in (("q", q, eq), ("k", k, ek), ("v", v, ev), ("grad_x", xd.grad, egx),
+                            ("grad_weight", f.c.weight.grad, egw),
+                            ("grad_init_param", f.init_param.grad, egi),
+                            ("grad_logit_bias", f.logit_bias.grad, egb)):
+        assert_close(np_of(got), want, tol, name)
+        assert_norm_rel(np_of(got), want, tol, name)
