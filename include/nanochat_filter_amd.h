@@ -273,8 +273,10 @@ int ltv_hm_scan_backward_split(
  * step inside later chunks' warm-ups receives one contribution per chunk that
  * reads it, and every chunk adds to grad_inits.  Same buffer contracts as
  * ltv_hm_scan_backward; the workspace size depends on P, Q, K.  With several
- * chunk windows the backward needs gate groups of r channels with r a multiple
- * of V (8 for bf16, 4 for fp32) and Da <= 16, or r dividing V.
+ * chunk windows and gate groups outside the tile kernel's patterns (r neither a
+ * multiple of V -- 8 for bf16, 4 for fp32 -- with Da <= 16, nor dividing V),
+ * one thread per channel walks the windows, with two fp32 (B, H, T, D)
+ * workspaces more.
  *
  * Replace ltv_look_back_fused_concat_head_major_register_cast_{blelloch,sequential}_scan_cuda_{forward,backward}
  * (cpp_ewma/src/ltv_look_back_fused_concat_head_major_register_cast_blelloch_scan_cuda_forward.cu:466-509,

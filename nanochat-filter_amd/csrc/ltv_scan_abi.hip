@@ -161,13 +161,38 @@ int scan_launch_bwd_channel(bool bf16, const BwdArgs& a, float* dalpha, hipStrea
                        dalpha);
     LTV_LAUNCH_CHECK();
     hipLaunchKernelGGL(scan_bwd_group_reduce_kernel<bf16_t>, dim3(gblocks), dim3(threads), 0,
-                       st, a, dalpha);
+                       st, a, dalpha, nullptr);
   } else {
     hipLaunchKernelGGL(scan_bwd_channel_kernel<float>, dim3(blocks), dim3(threads), 0, st, a,
                        dalpha);
     LTV_LAUNCH_CHECK();
     hipLaunchKernelGGL(scan_bwd_group_reduce_kernel<float>, dim3(gblocks), dim3(threads), 0, st,
-                       a, dalpha);
+                       a, dalpha, nullptr);
+  }
+  LTV_LAUNCH_CHECK();
+  return LTV_OK;
+}
+
+int scan_launch_lb_channel(bool bf16, const BwdArgs& a, float* dalpha, float* du_ws,
+                           hipStream_t st) {
+  const ScanShape& S = a.sh;
+  const int64_t n = (int64_t)S.B * S.H * S.D;
+  const int threads = 256;
+  const int blocks = (int)((n + threads - 1) / threads);
+  const int64_t ng = (int64_t)S.B * S.H * S.Da;
+  const int gblocks = (int)((ng + threads - 1) / threads);
+  if (bf16) {
+    hipLaunchKernelGGL(scan_lb_channel_kernel<bf16_t>, dim3(blocks), dim3(threads), 0, st, a,
+                       dalpha, du_ws);
+    LTV_LAUNCH_CHECK();
+    hipLaunchKernelGGL(scan_bwd_group_reduce_kernel<bf16_t>, dim3(gblocks), dim3(threads), 0,
+                       st, a, dalpha, du_ws);
+  } else {
+    hipLaunchKernelGGL(scan_lb_channel_kernel<float>, dim3(blocks), dim3(threads), 0, st, a,
+                       dalpha, du_ws);
+    LTV_LAUNCH_CHECK();
+    hipLaunchKernelGGL(scan_bwd_group_reduce_kernel<float>, dim3(gblocks), dim3(threads), 0, st,
+                       a, dalpha, du_ws);
   }
   LTV_LAUNCH_CHECK();
   return LTV_OK;
@@ -765,6 +790,7 @@ struct BwdWorkspace {
   size_t partial = 0, agg = 0, carry = 0, dalpha = 0;
   size_t dinit = 0;  // per-(b, h) inits gradients for their batch sum
   size_t wst = 0, wdu = 0, wdl = 0, wdi = 0;  // look-back windows
+  size_t du = 0;  // look-back windows, per-channel kernel: value-gradient sums
   size_t total = 0;
 };
 
@@ -804,6 +830,13 @@ BwdWorkspace bwd_workspace_plan(int dtype, int B, int T, int NH, int NKVH, int D
     off += al(rows * kw * Da * sizeof(float));
     w.wdi = off;
     off += al(rows * D * sizeof(float));
+    if (bwd_gate_mode(r, Da, V) < 0) {
+      // the per-channel kernel's dalpha and value-gradient sums
+      w.dalpha = off;
+      off += al((size_t)B * H * T * D * sizeof(float));
+      w.du = off;
+      off += al((size_t)B * H * T * D * sizeof(float));
+    }
     w.total = off;
     return w;
   }
@@ -1013,11 +1046,8 @@ int scan_backward_impl(int dtype, const HostView4& u, const HostView4& lg, const
   if (nwin > 1) {
     // Look-back windows: recompute each window's warm-up states, run every
     // window's reverse chain, then fold the warm-up contributions into the
-    // owning windows' steps and sum the inits gradients.
-    LTV_REQUIRE(gm >= 0, LTV_ERR_UNSUPPORTED,
-                "look-back backward with several chunk windows needs gate groups of r "
-                "channels with r a multiple of %d and Da <= %d, or r dividing %d (r=%d Da=%d)",
-                V, kMaxLaneGroups, V, r, Da);
+    // owning windows' steps and sum the inits gradients (gate groups outside
+    // the tile kernel's patterns: one thread per channel walks the windows).
     const int64_t grid = (int64_t)B * H * nwin;
     LTV_REQUIRE(grid < (1ll << 31), LTV_ERR_UNSUPPORTED, "grid too large");
     a.nchunk = nwin;
@@ -1047,6 +1077,13 @@ int scan_backward_impl(int dtype, const HostView4& u, const HostView4& lg, const
       const bool fvec = (D % V == 0) && vec_ok(u.p, u.s, 3, V) && vec_ok(init.p, init.s, 3, V);
       rc = launch_forward(dtype, f, fvec, lg, B, T, NH, NKVH, Da, r, use_sigmoid, st);
       if (rc) return rc;
+    }
+    if (gm < 0) {
+      LTV_REQUIRE((int64_t)B * H * D < (1ll << 31), LTV_ERR_UNSUPPORTED, "grid too large");
+      rc = scan_launch_lb_channel(bf16, a, reinterpret_cast<float*>(wsb + wp.dalpha),
+                                  reinterpret_cast<float*>(wsb + wp.du), st);
+      if (rc) return rc;
+      return scan_launch_dbias_reduce(a.dbias_partial, dbias, B, H, 1, Da, st, ds, pz);
     }
     ScanCfg cfg = bwd_default_cfg(next_pow2((D + V - 1) / V), vec);
     const ScanTuning& tu = tuning();

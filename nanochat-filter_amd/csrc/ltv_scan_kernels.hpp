@@ -2013,11 +2013,14 @@ __global__ void scan_bwd_channel_kernel(const BwdArgs args, float* __restrict__ 
   }
 }
 
+// One thread per (b, h, gate group j) over all t, so the dbias partial needs
+// no extra pass.  du_ws (look-back windows): the group's value gradients,
+// summed over windows in fp32, rounded to the I/O dtype here.
 template <typename TIO>
 __global__ void scan_bwd_group_reduce_kernel(const BwdArgs args,
-                                             const float* __restrict__ dalpha_ws) {
+                                             const float* __restrict__ dalpha_ws,
+                                             const float* __restrict__ du_ws) {
   const ScanShape& S = args.sh;
-  // one thread per (b, h, j) over all t, so the dbias partial needs no extra pass
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= (int64_t)S.B * S.H * S.Da) return;
   const int j = (int)(idx % S.Da);
@@ -2029,17 +2032,103 @@ __global__ void scan_bwd_group_reduce_kernel(const BwdArgs args,
              (int64_t)h * args.dlg.s[1] + (int64_t)j * args.dlg.s[3];
   const float bias = args.bias[h * S.Da + j];
   const bool use_sig = S.use_sigmoid != 0;
+  TIO* dup = reinterpret_cast<TIO*>(const_cast<void*>(args.du.p)) + (int64_t)b * args.du.s[0] +
+             (int64_t)h * args.du.s[1] + (int64_t)j * S.r * args.du.s[3];
   float acc_b = 0.0f;
   for (int t = 0; t < S.T; ++t) {
-    const float* row = dalpha_ws + (((int64_t)b * S.H + h) * S.T + t) * S.D + (int64_t)j * S.r;
+    const int64_t ro = (((int64_t)b * S.H + h) * S.T + t) * S.D + (int64_t)j * S.r;
+    const float* row = dalpha_ws + ro;
     float p = 0.0f;
     for (int q = 0; q < S.r; ++q) p += row[q];
+    if (du_ws != nullptr)
+      for (int q = 0; q < S.r; ++q)
+        Pack<TIO>::store1(dup + (int64_t)t * args.du.s[2] + (int64_t)q * args.du.s[3],
+                          du_ws[ro + q]);
     const float alpha = gate_alpha(Pack<TIO>::load1(lp + (int64_t)t * args.lg.s[2]) + bias, use_sig);
     const float d = use_sig ? p * (alpha * (1.0f - alpha)) : p;
     Pack<TIO>::store1(dlp + (int64_t)t * args.dlg.s[2], d);
     acc_b += d;
   }
   args.dbias_partial[idx] = acc_b;
+}
+
+// Look-back windows with such gate groups: the same walk per (b, h, channel),
+// window by window from the last.  Each window runs its reverse chain over
+// [lo, hi), with upstream gradients on its own steps [st, hi) only; the state
+// before step t is the saved output (t - 1 >= st), the warm-up state in wst
+// (lo <= t - 1 < st: row t - 1 - lo of the window's rows) or the inits
+// (t = lo).  A step lies in its own window and in the warm-ups of later ones:
+// its du and dalpha terms are summed in fp32 workspaces (B, H, T, D), where
+// the first window to reach it writes -- the latest that covers it, as the
+// windows run latest first, so the step lies below the next window's lo --
+// and the others add; the group reduction then rounds du once.  The inits
+// gradient sums every window's term at its first step.
+template <typename TIO>
+__global__ void scan_lb_channel_kernel(const BwdArgs args, float* __restrict__ dalpha_ws,
+                                       float* __restrict__ du_ws) {
+  const ScanShape& S = args.sh;
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (int64_t)S.B * S.H * S.D) return;
+  const int c = (int)(idx % S.D);
+  const int h = (int)((idx / S.D) % S.H);
+  const int b = (int)(idx / ((int64_t)S.D * S.H));
+  int which, hl;
+  head_select(h, S.NH, S.NKVH, which, hl);
+  const HeadView hvw = head_view(args.h, which), gvw = head_view(args.gy, which);
+  const TIO* hp = reinterpret_cast<const TIO*>(hvw.p) + (int64_t)b * hvw.s[0] +
+                  (int64_t)hl * hvw.s[1] + (int64_t)c * hvw.s[3];
+  const TIO* gp = reinterpret_cast<const TIO*>(gvw.p) + (int64_t)b * gvw.s[0] +
+                  (int64_t)hl * gvw.s[1] + (int64_t)c * gvw.s[3];
+  const TIO* up = reinterpret_cast<const TIO*>(args.u.p) + (int64_t)b * args.u.s[0] +
+                  (int64_t)h * args.u.s[1] + (int64_t)c * args.u.s[3];
+  const int j = c / S.r;
+  const TIO* lp = reinterpret_cast<const TIO*>(args.lg.p) + (int64_t)b * args.lg.s[0] +
+                  (int64_t)h * args.lg.s[1] + (int64_t)j * args.lg.s[3];
+  const float bias = args.bias[h * S.Da + j];
+  const bool use_sig = S.use_sigmoid != 0;
+  const float init = Pack<TIO>::load1(reinterpret_cast<const TIO*>(args.init.p) +
+                                      (int64_t)b * args.init.s[0] + (int64_t)h * args.init.s[1] +
+                                      (int64_t)c * args.init.s[3]);
+  const int nwin = args.nchunk;
+  const TIO* wsp = reinterpret_cast<const TIO*>(args.wst) +
+                   ((int64_t)b * S.H + h) * nwin * args.kw * S.D + c;
+  const int64_t base = ((int64_t)b * S.H + h) * S.T * S.D + c;
+  float dinit = 0.0f;
+  int lo_next = S.T;  // lo of the window after the current one (T: none)
+  for (int w = nwin - 1; w >= 0; --w) {
+    const Window wd = look_back_window(w, S.T, args.P, args.Q, args.K);
+    float g = 0.0f, a_next = 0.0f;
+    for (int t = wd.hi - 1; t >= wd.lo; --t) {
+      const float alpha =
+          gate_alpha(Pack<TIO>::load1(lp + (int64_t)t * args.lg.s[2]) + bias, use_sig);
+      const float gy = t >= wd.st ? Pack<TIO>::load1(gp + (int64_t)t * gvw.s[2]) : 0.0f;
+      g = fmaf(a_next, g, gy);
+      float hprev;
+      if (t == wd.lo)
+        hprev = init;
+      else if (t - 1 >= wd.st)
+        hprev = Pack<TIO>::load1(hp + (int64_t)(t - 1) * hvw.s[2]);
+      else
+        hprev = Pack<TIO>::load1(wsp + ((int64_t)w * args.kw + (t - 1 - wd.lo)) * S.D);
+      const float du = alpha * g;
+      const float da = (Pack<TIO>::load1(up + (int64_t)t * args.u.s[2]) - hprev) * g;
+      const int64_t o = base + (int64_t)t * S.D;
+      if (t < lo_next) {
+        du_ws[o] = du;
+        dalpha_ws[o] = da;
+      } else {
+        du_ws[o] += du;
+        dalpha_ws[o] += da;
+      }
+      a_next = 1.0f - alpha;
+    }
+    dinit += a_next * g;  // the window's first step reads the inits
+    lo_next = wd.lo;
+  }
+  Pack<TIO>::store1(reinterpret_cast<TIO*>(const_cast<void*>(args.dinit.p)) +
+                        (int64_t)b * args.dinit.s[0] + (int64_t)h * args.dinit.s[1] +
+                        (int64_t)c * args.dinit.s[3],
+                    dinit);
 }
 
 // ---------------------------------------------------------------------------
@@ -2076,6 +2165,11 @@ int scan_launch_lb_short_bwd(bool bf16, const BwdArgs& a, bool vec, int gm, int 
                              hipStream_t st);
 // Backward for gate groups outside the main kernel's reduction patterns.
 int scan_launch_bwd_channel(bool bf16, const BwdArgs& a, float* dalpha_ws, hipStream_t st);
+// The same for look-back windows (a.nchunk windows, warm-up states in a.wst):
+// value and dalpha terms summed over windows in fp32 workspaces of
+// (B, H, T, D) each.
+int scan_launch_lb_channel(bool bf16, const BwdArgs& a, float* dalpha_ws, float* du_ws,
+                           hipStream_t st);
 // The batch sum of the inits gradient, done by the dbias reduction's launch:
 // out[h, d] (strides sh, sd elements; fp32, or bf16 with out_bf16) = the sum
 // over b, in batch order, of ws[(b H + h) D + d].

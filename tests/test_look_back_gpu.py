@@ -139,24 +139,28 @@ def test_exact_wide_heads_many_windows(dtype, D, r, pqk):
         _check(got, want, 0, f"D={D} r={r} pqk={pqk} {layout}")
 
 
-def test_unsupported_gate_groups_raise():
+@pytest.mark.parametrize("dtype", DTYPES, ids=io_name)
+@pytest.mark.parametrize("D,r", [(12, 3), (24, 6), (40, 5), (96, 4), (36, 12)])
+@pytest.mark.parametrize("pqk", [(8, 6, 4), (0, 5, 9), (64, 60, 5)], ids=str)
+def test_exact_gate_groups_outside_the_tile_patterns(dtype, D, r, pqk):
     """Several windows with gate groups neither filling whole lanes nor fitting
-    in one (r = 3 with bf16) are refused with a clear error, not computed wrong."""
-    B, T, NH, NKVH, Da, r = 1, 20, 1, 1, 4, 3
+    in one (r = 3, 5, 6, 12 against 8 bf16 / 4 fp32 channels per lane) or more
+    than 16 per head (D = 96, r = 4): the per-channel look-back backward
+    (warm-ups in fp32 sums across windows), exact on the integer inputs, with
+    the full-recurrence kernels for one window."""
+    B, T, NH, NKVH = 2, 70, 1, 1
+    Da = D // r
     c = int_combined(B, T, NH, NKVH, Da, r)
     ini = int_inits(B, NH, NKVH, Da, r)
     bias = int_logit_bias(NH, NKVH, Da, False)
-    gy = np.ones((B, NH + 2 * NKVH, T, Da * r), np.float32)
-    with pytest.raises(RuntimeError, match="gate groups"):
-        _run("blelloch", to_torch(c, torch.bfloat16, DEV), to_torch(ini, torch.bfloat16, DEV),
-             to_torch(bias, torch.float32, DEV), NH, NKVH, Da, r, (8, 6, 4), False,
-             _grads(gy, NH, NKVH, torch.bfloat16))
-    # one window (P >= T) uses the full-recurrence kernels, which handle it
-    got = _run("blelloch", to_torch(c, torch.bfloat16, DEV), to_torch(ini, torch.bfloat16, DEV),
-               to_torch(bias, torch.float32, DEV), NH, NKVH, Da, r, (64, 6, 4), False,
-               _grads(gy, NH, NKVH, torch.bfloat16))
-    want = _expected(c, ini, bias, NH, NKVH, Da, r, (64, 6, 4), False, "bf16", gy)
-    _check(got, want, 0, "r=3 one window")
+    rng = np.random.default_rng(D + r)
+    gy = rng.integers(-2, 3, size=(B, NH + 2 * NKVH, T, D)).astype(np.float32)
+    for spec in (pqk, (T, 6, 4)):
+        got = _run("blelloch", to_torch(c, dtype, DEV), to_torch(ini, dtype, DEV),
+                   to_torch(bias, torch.float32, DEV), NH, NKVH, Da, r, spec, False,
+                   _grads(gy, NH, NKVH, dtype))
+        want = _expected(c, ini, bias, NH, NKVH, Da, r, spec, False, io_name(dtype), gy)
+        _check(got, want, 0, f"D={D} r={r} pqk={spec}")
 
 
 # ---------------------------------------------------------------------------
