@@ -102,16 +102,18 @@ def test_filter_state_continuity(dtype):
 
 
 def _random_cases(n=16, seed=7):
-    """Seeded filter shapes: heads, head widths, gate group sizes (r = D: one
-    gate per head; r = 1: one gate per channel), batch and sequence lengths
-    off the kernels' tile sizes (T = 1 included), both I/O dtypes."""
+    """Seeded filter shapes: heads, head widths (12 to 128: C off the fused
+    path's multiple of 8 included), any gate group size r | D (one gate per
+    head to one per channel; groups of a non-power-of-two number of lanes
+    included), batch and sequence lengths off the kernels' tile sizes (T = 1
+    included), both I/O dtypes."""
     rng = np.random.default_rng(seed)
     cases = []
     for i in range(n):
         NH = int(rng.integers(1, 5))
         NKVH = int(rng.integers(1, NH + 1))
-        D = int(rng.choice([32, 64, 128]))
-        r = int(rng.choice([D, D // 2, D // 4, 8, 1]))
+        D = int(rng.choice([12, 24, 32, 48, 64, 96, 128]))
+        r = int(rng.choice([d for d in range(1, D + 1) if D % d == 0]))
         B = int(rng.integers(1, 4))
         T = 1 if i == 0 else int(rng.integers(2, 301))
         dtype = torch.bfloat16 if i % 2 else torch.float32

@@ -237,8 +237,8 @@ def _random_cases(n=12, seed=11):
     for i in range(n):
         NH = int(rng.integers(1, 4))
         NKVH = int(rng.integers(1, NH + 1))
-        D = int(rng.choice([32, 64, 128]))
-        r = int(rng.choice([D, D // 2, 8, 1]))
+        D = int(rng.choice([12, 24, 32, 48, 64, 96, 128]))
+        r = int(rng.choice([d for d in range(1, D + 1) if D % d == 0]))
         Q = int(rng.integers(1, 131))
         K = int(rng.integers(1, 40))
         P = O.UNBOUNDED_P if i % 5 == 4 else int(rng.choice([0, int(rng.integers(1, 200))]))
