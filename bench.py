@@ -438,7 +438,11 @@ def peaks_main(args):
         workgroup, 1,152 workgroups) with 1, 2 and 3 arrays read and one
         written;
       * the library GEMM (torch.matmul, hipBLASLt) on the projection's three
-        shapes, for comparison with this library's kernels.
+        shapes, for comparison with this library's kernels;
+      * the projection GEMM's k-step without its epilogue on every CU (64 KB
+        of direct-to-LDS loads, 256 bf16 MFMAs on random bits, fragment
+        reads, one barrier per step): each part alone and together, in us
+        per step.
     Each figure is the median of ``--steps`` timed launches (HIP events)."""
     import ctypes
     import torch
@@ -452,6 +456,9 @@ def peaks_main(args):
     lib.ltv_peak_stream.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_int,
                                     ctypes.c_int, ctypes.c_int64, ctypes.c_int64, ctypes.c_int,
                                     ctypes.c_uint32, ctypes.c_void_p]
+    lib.ltv_peak_overlap.restype = ctypes.c_int
+    lib.ltv_peak_overlap.argtypes = [ctypes.c_void_p, ctypes.c_uint32, ctypes.c_void_p,
+                                     ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
     dev = torch.device("cuda:0")
     st = N.stream_of(torch.empty(1, device=dev))
     n_cu = torch.cuda.get_device_properties(dev).multi_processor_count
@@ -508,6 +515,24 @@ def peaks_main(args):
         out[f"slices_{nr}r1w"] = stream(nr, 1, 0, sl, PEAK_SLICES)
         out[f"slices_{nr}r1w_nt"] = stream(nr, 1, 1, sl, PEAK_SLICES)
     del arrs
+    torch.cuda.synchronize()
+    # the GEMM k-step's parts beside each other (one workgroup of 8 wavefronts per CU)
+    src_bytes = 64 << 20
+    src = torch.empty(src_bytes, dtype=torch.uint8, device=dev)
+    src.random_(0, 256)
+    ov_out = torch.empty(n_cu * 512, dtype=torch.float32, device=dev)
+    ov_steps = 600
+    ov = {}
+    for name, mode in (("loads", 5), ("mfma", 6), ("loads_mfma", 7), ("mfma_reads", 30),
+                       ("loads_mfma_reads", 31), ("mfma_reads_sink", 58),
+                       ("loads_mfma_reads_sink", 59), ("mfma_reads_2ahead", 94),
+                       ("loads_mfma_reads_2ahead", 95)):
+        t = timed(lambda: N.check(lib.ltv_peak_overlap(src.data_ptr(), src_bytes, ov_out.data_ptr(),
+                                                       n_cu, ov_steps, mode, st),
+                                  "ltv_peak_overlap"))
+        ov[name] = round(t * 1e6 / ov_steps, 3)
+    out["gemm_step_parts_us"] = ov
+    del src, ov_out
     torch.cuda.synchronize()
     # library GEMM on the projection's shapes (bf16 in, bf16 out)
     M, Kc, Fp = B * T, C, 2432

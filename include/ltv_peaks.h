@@ -34,6 +34,19 @@ int ltv_peak_mfma(float* out, int blocks, int iters, int zero_operands, void* st
 int ltv_peak_stream(const void* const* srcs, int nr, void* dst, int write, int nontemporal,
                     int64_t n16, int64_t slice16, int blocks, uint32_t never, void* stream);
 
+/* The projection GEMM's k-step without its epilogue, `steps` steps on each of
+ * `blocks` workgroups of 8 wavefronts (one per CU at 256): 64 KB of
+ * direct-to-LDS loads per step from `src` (src_bytes a power of two, at least
+ * 1 MiB; row offsets wrap inside it) issued one step ahead by 4 wavefronts,
+ * 256 v_mfma_f32_32x32x16_bf16 on random bits, fragment reads from LDS, one
+ * barrier per step.  mode: 5 loads only, 6 MFMAs only, 7 loads + MFMAs,
+ * 30 MFMAs + 3 fragment reads per 4 MFMAs (read one group ahead and XORed
+ * into the operands), 31 all three, 58 / 59 as 30 / 31 with the reads going
+ * to a sink (no MFMA waits on them), 94 / 95 as 30 / 31 with the reads two
+ * groups ahead.  out: blocks * 512 floats. */
+int ltv_peak_overlap(const void* src, uint32_t src_bytes, float* out, int blocks, int steps,
+                     int mode, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -216,6 +216,6 @@ def test_peaks_library_exports_its_header():
     src = re.sub(r"/\*.*?\*/", "", open(os.path.join(ROOT, "include", "ltv_peaks.h")).read(),
                  flags=re.S)
     names = re.findall(r"^\s*int\s+(ltv_[a-z0-9_]+)\s*\(", src, flags=re.M)
-    assert sorted(names) == ["ltv_peak_mfma", "ltv_peak_stream"]
+    assert sorted(names) == ["ltv_peak_mfma", "ltv_peak_overlap", "ltv_peak_stream"]
     lib = ctypes.CDLL(path)
     assert all(hasattr(lib, n) for n in names)
