@@ -151,15 +151,20 @@ def decode_step(x: torch.Tensor, wpack: torch.Tensor, prev, logit_bias: torch.Te
     if x.dim() == 3:
         if x.shape[1] != 1:
             raise RuntimeError(f"decode_step takes one token per sequence, got x {tuple(x.shape)}")
-        x = x[:, 0]
+        # (B, 1, C): token b's row starts b * stride(0) elements in, as in (B, C)
+        B, _, C = x.shape
+        x_rs, x_cs = x.stride(0), x.stride(2)
+    else:
+        B, C = x.shape
+        x_rs, x_cs = x.stride(0), x.stride(1)
     N.require_device(x, wpack, logit_bias, *prev)
     if x.dtype != torch.bfloat16 or wpack.dtype != torch.bfloat16:
         raise RuntimeError("decode_step computes in bf16")
-    B, C = x.shape
     D = Da * r
     H = NH + 2 * NKVH
-    if x.stride(1) != 1 or x.stride(0) % 8 != 0:
-        x = x.contiguous()
+    if x_cs != 1 or x_rs % 8 != 0:
+        x = x.reshape(B, C).contiguous()
+        x_rs = C
     prevs = []
     for t, nh in zip(prev, (NH, NKVH, NKVH)):
         if t.dtype != torch.bfloat16:
@@ -175,21 +180,24 @@ def decode_step(x: torch.Tensor, wpack: torch.Tensor, prev, logit_bias: torch.Te
     strides = _arr([s for t in prevs for s in t.stride()[:2]])
     if rows is None:
         with N.span("qkv_decode"):
-            rc = N.lib().ltv_qkv_decode_step(x.data_ptr(), x.stride(0), wpack.data_ptr(),
+            rc = N.lib().ltv_qkv_decode_step(x.data_ptr(), x_rs, wpack.data_ptr(),
                                              prevs[0].data_ptr(), prevs[1].data_ptr(),
                                              prevs[2].data_ptr(), strides, logit_bias.data_ptr(),
                                              out.data_ptr(), B, C, NH, NKVH, D, Da,
                                              int(use_sigmoid), N.stream_of(x))
         N.check(rc, "ltv_qkv_decode_step")
         return out
-    for t, nh in zip(rows, (NH, NKVH, NKVH)):
-        if (t.dtype != torch.bfloat16 or tuple(t.shape) != (B, nh, D) or t.stride(2) != 1
-                or t.device != x.device):
-            raise RuntimeError(f"rows must be ({B}, {nh}, {D}) bf16 with channel stride 1 on "
-                               f"{x.device}, got {tuple(t.shape)} {t.dtype} {t.device}")
-    rstrides = _arr([s for t in rows for s in t.stride()[:2]])
+    if all(a is b for a, b in zip(rows, prevs)):
+        rstrides = strides  # the rows are the previous rows, checked above (the cache in place)
+    else:
+        for t, nh in zip(rows, (NH, NKVH, NKVH)):
+            if (t.dtype != torch.bfloat16 or tuple(t.shape) != (B, nh, D) or t.stride(2) != 1
+                    or t.device != x.device):
+                raise RuntimeError(f"rows must be ({B}, {nh}, {D}) bf16 with channel stride 1 on "
+                                   f"{x.device}, got {tuple(t.shape)} {t.dtype} {t.device}")
+        rstrides = _arr([s for t in rows for s in t.stride()[:2]])
     with N.span("qkv_decode"):
-        rc = N.lib().ltv_qkv_decode_step_rows(x.data_ptr(), x.stride(0), wpack.data_ptr(),
+        rc = N.lib().ltv_qkv_decode_step_rows(x.data_ptr(), x_rs, wpack.data_ptr(),
                                               prevs[0].data_ptr(), prevs[1].data_ptr(),
                                               prevs[2].data_ptr(), strides, logit_bias.data_ptr(),
                                               out.data_ptr(), rows[0].data_ptr(),
